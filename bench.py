@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark of the compressed-weight inference hot path on one MI355X.
+
+Headline (BASELINE.json metric "fused decode-GEMV HBM GB/s"): configs[1] at M = 1, i.e.
+one step = Y_a = W_a . x_a and Y_b = W_b . x_b for the two dictionary-coded matrices
+W_a 4096 x 11008 and W_b 11008 x 4096 (1 x 64 blocks, shared-format dictionary of
+1024 unit-norm fp32 atoms, 8 nonzeros per block, fp16 coefficients, x fp16, fp32
+accumulation). value = algorithmic bytes of a step / step time, where algorithmic bytes
+= compressed codes + dictionary + x + y of both matrices, each counted once.
+
+Inputs are resident in HBM before timing. Each step uses a different copy of the coded
+matrices (a rotation over > 3 x 256 MiB) so the Infinity Cache cannot serve them.
+
+The JSON line carries:
+  roofline      dominant kernel (the gather), timed with HIP events on its own stream
+  cpu_baseline  the CPU restatement of the reference algorithm (oracle/, OpenMP) on a
+                bounded sample of the same workload, on this host's cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2"])
+    return ap.parse_args()
+
+
+def workloads(cfg: str):
+    if cfg == "cfg1":
+        return [dict(name="W 4096x4096", R=4096, C=4096, K=512, s=4, xdtype=np.float32)]
+    return [
+        dict(name="W 4096x11008", R=4096, C=11008, K=1024, s=8, xdtype=np.float16),
+        dict(name="W 11008x4096", R=11008, C=4096, K=1024, s=8, xdtype=np.float16),
+    ]
+
+
+def alg_bytes(w, M=1):
+    NB = w["C"] // 64
+    codes = w["R"] * NB * w["s"] * 4
+    dict_b = w["K"] * 64 * 4
+    xb = w["C"] * M * np.dtype(w["xdtype"]).itemsize
+    yb = w["R"] * M * 4
+    P = NB * w["K"] * M * 4
+    return dict(op=codes + dict_b + xb + yb, gather=codes + P + yb, codes=codes)
+
+
+def cpu_baseline(streams, xs, seconds):
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    xs32 = [x.astype(np.float32) for x in xs]
+    for s, x in zip(streams, xs32):  # warm-up
+        oracle.hsdb_matmul(s, x)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for s, x in zip(streams, xs32):
+            oracle.hsdb_matmul(s, x)
+        n += 1
+        if time.perf_counter() - t0 >= seconds and n >= 2:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return dt, n, threads
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by output rows across GPUs, which is not built here)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    from cortexsdr_amd import synth
+    from cortexsdr_amd.hsdr import HsdbSegment
+
+    wl = workloads(args.config)
+    t_gen = time.time()
+    streams = [synth.hsdb_layer(w["R"], w["C"], w["K"], w["s"], seed_dict=1, seed_codes=2 + i)
+               for i, w in enumerate(wl)]
+    xs = [synth.activations(w["C"], 1, seed=3 + i, dtype=w["xdtype"]) for i, w in enumerate(wl)]
+    print(f"# generated {len(wl)} coded matrices in {time.time() - t_gen:.1f}s", flush=True)
+
+    step_codes = sum(alg_bytes(w)["codes"] for w in wl)
+    copies = max(2, math.ceil(3 * MALL_BYTES / step_codes) + 1)
+    segs = [[HsdbSegment(s) for s in streams] for _ in range(copies)]
+    xd = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in xs]
+    yd = [torch.empty((w["R"], 1), dtype=torch.float32, device="cuda") for w in wl]
+    ws = [segs[0][i].workspace(1) for i in range(len(wl))]
+    print(f"# {copies} rotating copies, {copies * step_codes / 2**20:.0f} MiB of codes resident",
+          flush=True)
+
+    from cortexsdr_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream()
+    sp = int(stream.cuda_stream)
+    xt = [1 if w["xdtype"] == np.float16 else 0 for w in wl]
+
+    def step(it, ev=None):
+        c = it % copies
+        for i in range(len(wl)):
+            h = segs[c][i]._h
+            _lib.check(lib.csdr_hsdb_dx(h, xd[i].data_ptr(), xt[i], 1, ws[i].data_ptr(),
+                                        ws[i].numel(), sp))
+            if ev is not None:
+                ev[i][0].record(stream)
+            _lib.check(lib.csdr_hsdb_gather(h, xd[i].data_ptr(), xt[i], 1, yd[i].data_ptr(),
+                                            ws[i].data_ptr(), ws[i].numel(), sp))
+            if ev is not None:
+                ev[i][1].record(stream)
+
+    for it in range(args.warmup):
+        step(it)
+    torch.cuda.synchronize()
+
+    # Timed region: the K steps are captured once into a HIP graph (the launches are
+    # host-bound through ctypes otherwise) and replayed, bracketed by synchronize.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gs = torch.cuda.current_stream()
+        sp_cap = int(gs.cuda_stream)
+        for it in range(args.steps):
+            c = it % copies
+            for i in range(len(wl)):
+                _lib.check(lib.csdr_hsdb_matmul(segs[c][i]._h, xd[i].data_ptr(), xt[i], 1,
+                                                yd[i].data_ptr(), ws[i].data_ptr(),
+                                                ws[i].numel(), sp_cap))
+    graph.replay()  # untimed first replay
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = start.elapsed_time(end)
+    ms_step = ms_total / args.steps
+
+    # Dominant-kernel duration: HIP events around every gather launch on the launch stream.
+    # A few large GEMMs are queued first so the host is far ahead of the device and the
+    # events bracket kernel execution, not host launch gaps.
+    a = torch.randn(8192, 8192, device="cuda")
+    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            for _ in wl] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        a = a @ a.T * 1e-4
+    for it in range(args.steps):
+        step(it, evs[it])
+    torch.cuda.synchronize()
+    del a
+    gather_ms = [float(np.mean([evs[k][i][0].elapsed_time(evs[k][i][1])
+                                for k in range(args.steps)])) for i in range(len(wl))]
+
+    op_bytes = sum(alg_bytes(w)["op"] for w in wl)
+    value = op_bytes / (ms_step * 1e-3) / 1e9
+    # dominant kernel: the gather (largest share of the step); roofline over both shapes
+    g_bytes = sum(alg_bytes(w)["gather"] for w in wl)
+    g_ms = sum(gather_ms)
+    achieved = g_bytes / (g_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": "fused decode-GEMV HBM GB/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64/Box-Muller; BASELINE.json configs[1])",
+        "config": {
+            "workload": ("cfg2 M=1: Y=W.x for W 4096x11008 and W 11008x4096, 1x64 blocks, "
+                         "K=1024 unit-norm fp32 atoms, 8 nnz/block, fp16 coef, x fp16, "
+                         "fp32 accumulate") if args.config == "cfg2" else
+                        "cfg1 M=1: W 4096x4096, K=512, 4 nnz/block, x fp32",
+            "M": 1,
+            "algorithmic_bytes_per_step": op_bytes,
+            "rotating_copies": copies,
+            "percent_hbm_roofline": round(100.0 * value / HBM_PEAK_GBS, 2),
+            "wall_s_timed": round(wall, 4),
+            "gather_ms": [round(v, 6) for v in gather_ms],
+        },
+        "roofline": {
+            "kernel": "gather_kernel (csdr_hsdb_gather)",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": [alg_bytes(w)["gather"] for w in wl],
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        dt, n, threads = cpu_baseline(streams, xs, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": round(op_bytes / dt / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"{n} full steps of the same workload (both matrices, M=1) through "
+                       f"oracle/csdr_oracle.c orc_hsdb_matmul with OpenMP, "
+                       f"{dt * 1e3:.1f} ms/step"),
+        }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,164 @@
+"""Host-side mirror of the reference's HSDR operator interface, on the MI355X kernels.
+
+Reference interface (cortexSDR tree):
+  HierarchicalSDRStrategy::matmulRowMajor(const vector<byte>&, const float* x, size_t batch)
+      -> vector<float>                     strategies/HierarchicalSDRStrategy.hpp:179-181
+  HierarchicalSDRStrategy::decompress(const vector<byte>&, SegmentType, size_t originalSize)
+      -> vector<byte>                      strategies/HierarchicalSDRStrategy.hpp:170-172
+Errors: the reference throws CompressionError (CompressionStrategy.hpp:33-36); here the
+C-ABI status is raised as CompressionError (a RuntimeError subclass) with the same cases:
+bad magic/version, geometry mismatch, truncation.
+
+HsdbSegment keeps a stream resident on the device (what SDRModelLoader's per-call file read
+and parse, SparseInferenceEngine.cpp:1055-1091, becomes here): load once, matmul many times
+on device tensors with inputs already in HBM.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+
+CSDR_F32 = 0
+CSDR_F16 = 1
+
+
+class CompressionError(_lib.CsdrError):
+    """Status of a rejected stream (the reference's CompressionError cases)."""
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = _lib.load().csdr_last_error()
+        raise CompressionError(rc, msg.decode() if msg else "")
+
+
+def _torch():
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("cortexsdr_amd needs a HIP device (no CPU fallback)")
+    return torch
+
+
+def _stream_ptr(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class HsdbSegment:
+    """A device-resident HSDR (binary) or HSDB (block-coded) weight segment."""
+
+    def __init__(self, stream: bytes, hip_stream=None):
+        lib = _lib.load()
+        _torch()
+        self._buf = C.create_string_buffer(bytes(stream), len(stream))
+        h = C.c_void_p()
+        _check(lib.csdr_hsdb_load(C.cast(self._buf, C.c_void_p), len(stream),
+                                  _stream_ptr(hip_stream), C.byref(h)))
+        self._h = h
+        self._buf = None
+        info = _lib.HsdbInfo()
+        _check(lib.csdr_hsdb_get_info(self._h, C.byref(info)))
+        self.info = {name: getattr(info, name) for name, _ in info._fields_}
+        self.rows = info.rows
+        self.cols = info.cols
+        self._ws = {}
+
+    # ------------------------------------------------------------------ lifetime
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().csdr_hsdb_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ compute
+    def workspace_bytes(self, M: int) -> int:
+        return int(_lib.load().csdr_hsdb_workspace_bytes(self._h, M))
+
+    def workspace(self, M: int):
+        """A zero-filled device workspace for batch M (cached per M)."""
+        torch = _torch()
+        n = self.workspace_bytes(M)
+        ws = self._ws.get(M)
+        if ws is None or ws.numel() < n:
+            ws = torch.zeros(n, dtype=torch.uint8, device="cuda")
+            self._ws[M] = ws
+        return ws
+
+    def matmul(self, x, out=None, workspace=None, stream=None):
+        """Y (R, M) fp32 = W . X for a device X (C, M) or (C,) in fp32/fp16."""
+        torch = _torch()
+        if x.dim() == 1:
+            x = x.reshape(-1, 1)
+        if x.shape[0] != self.cols:
+            raise ValueError(f"x has {x.shape[0]} rows, segment expects {self.cols}")
+        if not x.is_cuda or not x.is_contiguous():
+            raise ValueError("x must be a contiguous device tensor")
+        if x.dtype == torch.float32:
+            dt = CSDR_F32
+        elif x.dtype == torch.float16:
+            dt = CSDR_F16
+        else:
+            raise ValueError("x must be float32 or float16")
+        M = x.shape[1]
+        if out is None:
+            out = torch.empty((self.rows, M), dtype=torch.float32, device=x.device)
+        ws = workspace if workspace is not None else self.workspace(M)
+        _check(_lib.load().csdr_hsdb_matmul(self._h, x.data_ptr(), dt, M, out.data_ptr(),
+                                            ws.data_ptr(), ws.numel(), _stream_ptr(stream)))
+        return out
+
+    def decompress(self, stream=None):
+        """Dense W (R, C) fp32 on the device."""
+        torch = _torch()
+        w = torch.empty((self.rows, self.cols), dtype=torch.float32, device="cuda")
+        _check(_lib.load().csdr_hsdb_decompress(self._h, w.data_ptr(), _stream_ptr(stream)))
+        return w
+
+    def export_codes(self, stream=None):
+        """(packed, |c| fp16 bits) as numpy uint16 arrays in stream order."""
+        torch = _torch()
+        n = self.info["slots"] * (self.info["n_block_cols"] * self.rows
+                                  if self.info["tile_rows"] == 1 else 0)
+        if self.info["tile_rows"] != 1:
+            tr, tc = self.info["tile_rows"], self.info["tile_cols"]
+            n = self.info["slots"] * (self.rows // tr) * (self.cols // tc)
+        packed = torch.empty(max(n, 1), dtype=torch.int16, device="cuda")
+        coef = torch.empty(max(n, 1), dtype=torch.int16, device="cuda")
+        _check(_lib.load().csdr_hsdb_export_codes(self._h, packed.data_ptr(), coef.data_ptr(),
+                                                  _stream_ptr(stream)))
+        torch.cuda.current_stream().synchronize()
+        return (packed.cpu().numpy().view(np.uint16)[:n],
+                coef.cpu().numpy().view(np.uint16)[:n])
+
+
+def matmul_row_major(stream: bytes, x: np.ndarray, batch: int) -> np.ndarray:
+    """Drop-in for HierarchicalSDRStrategy::matmulRowMajor: host x (C x batch) row-major
+    fp32 in, host Y (R x batch) fp32 out. Loads the stream per call like the reference;
+    use HsdbSegment to keep it resident."""
+    torch = _torch()
+    seg = HsdbSegment(stream)
+    try:
+        xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(seg.cols, batch)).cuda()
+        y = seg.matmul(xd)
+        return y.cpu().numpy()
+    finally:
+        seg.free()
+
+
+def decompress(stream: bytes) -> np.ndarray:
+    """Drop-in for HierarchicalSDRStrategy::decompress (fp32 R x C)."""
+    seg = HsdbSegment(stream)
+    try:
+        return seg.decompress().cpu().numpy()
+    finally:
+        seg.free()

@@ -1,0 +1,586 @@
+/*
+ * csdr_oracle.c — CPU restatement of cortexSDR's compressed-weight inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see csdr_oracle.h): the checker for tests/, smoke() and
+ * bench.py's cpu_baseline leg. Never linked into the product.
+ *
+ * Arithmetic: built with -ffp-contract=off; every multiply-add that the reference
+ * performs as `acc += a * b` inside a loop is written here as fmaf(a, b, acc) in the
+ * reference's loop order, so that dense decodes can be compared bit-exactly with the
+ * reference built by oracle/Makefile (its -O3 -mfma build contracts the same
+ * expressions into FMAs).
+ */
+#include "csdr_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ fp16 */
+
+float orc_f16_to_f32(uint16_t h) {
+    /* utils/fp16_convert.hpp:33-60 (bit-level decode incl. subnormals, inf, nan) */
+    uint32_t sign = (uint32_t)(h >> 15) & 1u;
+    uint32_t e = (uint32_t)(h >> 10) & 0x1Fu;
+    uint32_t m = (uint32_t)h & 0x3FFu;
+    uint32_t f;
+    if (e == 0) {
+        if (m == 0) {
+            f = sign << 31;
+        } else {
+            int ex = 1;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                ex--;
+            }
+            m &= 0x3FFu;
+            f = (sign << 31) | ((uint32_t)(ex + 112) << 23) | (m << 13);
+        }
+    } else if (e == 0x1F) {
+        f = (sign << 31) | 0x7F800000u | (m << 13);
+    } else {
+        f = (sign << 31) | ((e + 112u) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &f, 4);
+    return out;
+}
+
+uint16_t orc_f32_to_f16(float fv) {
+    /* IEEE-754 binary16, round to nearest, ties to even (the F16C path of
+     * utils/fp16_convert.hpp:68-71). Subnormals are produced, not flushed. */
+    uint32_t x;
+    memcpy(&x, &fv, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t absx = x & 0x7FFFFFFFu;
+    if (absx >= 0x7F800000u) { /* inf or nan */
+        if (absx > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((absx >> 13) & 0x3FFu));
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    if (absx >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to >= 65520 -> inf */
+    if (absx < 0x38800000u) {                                   /* below 2^-14: subnormal */
+        if (absx < 0x33000000u) return (uint16_t)sign;          /* < 2^-25 rounds to 0 */
+        uint32_t e = absx >> 23;
+        uint32_t m = (absx & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126u - e; /* value = m * 2^(e-150); unit = 2^-24 */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t e = (absx >> 23) - 112u;
+    uint32_t m = absx & 0x7FFFFFu;
+    uint32_t q = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+void orc_f16_to_f32_array(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f16_to_f32(src[i]);
+}
+
+void orc_f32_to_f16_array(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16(src[i]);
+}
+
+/* ---------------------------------------------------------- stream parse */
+
+static uint32_t rd32(const uint8_t* p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+static uint16_t rd16(const uint8_t* p) {
+    uint16_t v;
+    memcpy(&v, p, 2);
+    return v;
+}
+
+int orc_hsdr_parse(const uint8_t* buf, size_t n, orc_hsdr_view* v) {
+    /* Header layout: HierarchicalSDRStrategy.cpp:49-66 (packed, 36 bytes). */
+    if (!buf || !v) return ORC_E_ARG;
+    memset(v, 0, sizeof(*v));
+    if (n < 36) return ORC_E_TRUNCATED;
+    if (memcmp(buf, "HSDR", 4) == 0) {
+        v->is_hsdb = 0;
+    } else if (memcmp(buf, "HSDB", 4) == 0) {
+        v->is_hsdb = 1;
+    } else {
+        return ORC_E_MAGIC; /* :1266-1268 */
+    }
+    v->version = rd32(buf + 4);
+    if ((!v->is_hsdb && v->version != 2) || (v->is_hsdb && v->version != 1))
+        return ORC_E_VERSION; /* :1269-1271 */
+    v->rows = rd32(buf + 8);
+    v->cols = rd32(buf + 12);
+    v->n_tiles = rd32(buf + 16);
+    v->tile_rows = rd16(buf + 20);
+    v->tile_cols = rd16(buf + 22);
+    v->n_atoms = rd16(buf + 24);
+    v->n_stages = buf[26];
+    v->k_per_stage = buf[27];
+    memcpy(&v->stage_decay, buf + 28, 4);
+    v->edge_bytes = rd32(buf + 32);
+    if (v->tile_rows == 0 || v->tile_cols == 0) return ORC_E_GEOMETRY;
+    if (v->is_hsdb && v->tile_rows != 1) return ORC_E_GEOMETRY;
+    {
+        uint64_t rf = (uint64_t)(v->rows / v->tile_rows) * v->tile_rows;
+        uint64_t cf = (uint64_t)(v->cols / v->tile_cols) * v->tile_cols;
+        uint64_t expect_tiles = (rf / v->tile_rows) * (cf / v->tile_cols);
+        if (expect_tiles != v->n_tiles) return ORC_E_GEOMETRY;
+        uint64_t expect_edge = (rf * (v->cols - cf) + (v->rows - rf) * (uint64_t)v->cols) * 4u;
+        if (expect_edge != v->edge_bytes) return ORC_E_GEOMETRY;
+    }
+    v->slots_per_tile = (size_t)v->n_stages * v->k_per_stage;
+    v->n_codes = (size_t)v->n_tiles * v->slots_per_tile;
+    size_t tile_dim = (size_t)v->tile_rows * v->tile_cols;
+    size_t off = 36;
+    v->off_gamma = off;
+    off += 4u * v->n_stages;
+    v->off_dict = off;
+    off += 4u * (size_t)v->n_atoms * tile_dim;
+    v->off_packed = off;
+    off += 2u * v->n_codes;
+    v->off_coef = off;
+    if (v->is_hsdb) off += 2u * v->n_codes;
+    v->off_edge = off;
+    off += v->edge_bytes;
+    v->end = off;
+    if (off > n) return ORC_E_TRUNCATED; /* readBuffer, :218-225 */
+    return ORC_OK;
+}
+
+int orc_hsdr_unpack(const uint8_t* buf, size_t n, uint16_t* idx, int8_t* sign, float* coef) {
+    orc_hsdr_view v;
+    int rc = orc_hsdr_parse(buf, n, &v);
+    if (rc) return rc;
+    for (size_t i = 0; i < v.n_codes; ++i) {
+        uint16_t p = rd16(buf + v.off_packed + 2 * i);
+        size_t slot = i % v.slots_per_tile;
+        size_t l = slot / v.k_per_stage;
+        float g;
+        memcpy(&g, buf + v.off_gamma + 4 * l, 4);
+        int8_t s = (p & 0x8000u) ? -1 : 1; /* :81-84 */
+        if (idx) idx[i] = (uint16_t)(p & 0x7FFFu);
+        if (sign) sign[i] = s;
+        if (coef) {
+            float mag = v.is_hsdb ? orc_f16_to_f32(rd16(buf + v.off_coef + 2 * i)) : 1.0f;
+            coef[i] = g * ((float)s * mag); /* scale = gamma * sign, :627 */
+        }
+    }
+    return ORC_OK;
+}
+
+/* Copies the dictionary (n_atoms x tile_dim fp32) out of the stream. */
+static float* copy_dict(const uint8_t* buf, const orc_hsdr_view* v) {
+    size_t nf = (size_t)v->n_atoms * v->tile_rows * v->tile_cols;
+    float* D = (float*)malloc(nf * 4 + 4);
+    if (D) memcpy(D, buf + v->off_dict, nf * 4);
+    return D;
+}
+
+int orc_hsdr_decompress(const uint8_t* buf, size_t n, float* out, size_t out_floats) {
+    orc_hsdr_view v;
+    int rc = orc_hsdr_parse(buf, n, &v);
+    if (rc) return rc;
+    const size_t R = v.rows, C = v.cols;
+    if (out_floats < R * C) return ORC_E_ARG; /* originalSize check, :1371-1374 */
+    const size_t tr = v.tile_rows, tc = v.tile_cols, tile_dim = tr * tc;
+    const size_t R_full = (R / tr) * tr, C_full = (C / tc) * tc;
+    const size_t n_col_tiles = C_full / tc;
+    float* D = copy_dict(buf, &v);
+    float* coef = (float*)malloc(v.n_codes * 4 + 4);
+    uint16_t* idx = (uint16_t*)malloc(v.n_codes * 2 + 2);
+    float* tile = (float*)malloc(tile_dim * 4);
+    if (!D || !coef || !idx || !tile) {
+        free(D), free(coef), free(idx), free(tile);
+        return ORC_E_ARG;
+    }
+    orc_hsdr_unpack(buf, n, idx, NULL, coef);
+    for (size_t t = 0; t < v.n_tiles; ++t) {
+        /* decodeAllTiles, :612-634: zero tile, then stage-major slot accumulation */
+        for (size_t c = 0; c < tile_dim; ++c) tile[c] = 0.0f;
+        for (size_t s = 0; s < v.slots_per_tile; ++s) {
+            size_t slot = t * v.slots_per_tile + s;
+            const float scale = coef[slot];
+            /* the reference's sign-0 skip (:626) never fires: unpacked signs are +-1 */
+            if (idx[slot] >= v.n_atoms) continue; /* out of range: reference reads past D */
+            const float* atom = D + (size_t)idx[slot] * tile_dim;
+            for (size_t c = 0; c < tile_dim; ++c) tile[c] = fmaf(scale, atom[c], tile[c]);
+        }
+        /* reassembleTiles, :119-135: tile (br, bc) -> rows br*tr.., cols bc*tc.. */
+        size_t br = t / n_col_tiles, bc = t % n_col_tiles;
+        for (size_t r = 0; r < tr; ++r)
+            memcpy(out + (br * tr + r) * C + bc * tc, tile + r * tc, tc * 4);
+    }
+    /* edge splice: top-right strip then bottom strip, :1401-1438 */
+    size_t e = 0;
+    const uint8_t* eb = buf + v.off_edge;
+    for (size_t r = 0; r < R_full; ++r)
+        for (size_t c = C_full; c < C; ++c, ++e) memcpy(out + r * C + c, eb + 4 * e, 4);
+    for (size_t r = R_full; r < R; ++r)
+        for (size_t c = 0; c < C; ++c, ++e) memcpy(out + r * C + c, eb + 4 * e, 4);
+    free(D), free(coef), free(idx), free(tile);
+    return ORC_OK;
+}
+
+int orc_hsdr_matmul_row_major(const uint8_t* buf, size_t n, const float* x, size_t batch,
+                              float* y) {
+    orc_hsdr_view v;
+    int rc = orc_hsdr_parse(buf, n, &v);
+    if (rc) return rc;
+    if (v.is_hsdb) return ORC_E_MAGIC;
+    /* :1273-1289 geometry checks */
+    if (v.tile_rows != 1 || v.tile_cols != v.cols || v.n_tiles != v.rows) return ORC_E_GEOMETRY;
+    const size_t R = v.rows, C = v.cols, K = v.n_atoms;
+    float* D = copy_dict(buf, &v);
+    float* Dx = (float*)calloc(K * batch + 1, 4);
+    float* coef = (float*)malloc(v.n_codes * 4 + 4);
+    uint16_t* idx = (uint16_t*)malloc(v.n_codes * 2 + 2);
+    if (!D || !Dx || !coef || !idx) {
+        free(D), free(Dx), free(coef), free(idx);
+        return ORC_E_ARG;
+    }
+    orc_hsdr_unpack(buf, n, idx, NULL, coef);
+    /* hot loop 1, :1304-1315: Dx[a, b] = sum_c D[a, c] * x[c, b] */
+    for (size_t a = 0; a < K; ++a)
+        for (size_t c = 0; c < C; ++c) {
+            const float av = D[a * C + c];
+            for (size_t b = 0; b < batch; ++b)
+                Dx[a * batch + b] = fmaf(av, x[c * batch + b], Dx[a * batch + b]);
+        }
+    /* hot loop 2, :1318-1336: per-row signed gather */
+    for (size_t r = 0; r < R; ++r) {
+        float* yr = y + r * batch;
+        for (size_t b = 0; b < batch; ++b) yr[b] = 0.0f;
+        for (size_t s = 0; s < v.slots_per_tile; ++s) {
+            size_t slot = r * v.slots_per_tile + s;
+            if (idx[slot] >= K) continue;
+            const float scale = coef[slot];
+            const float* dx = Dx + (size_t)idx[slot] * batch;
+            for (size_t b = 0; b < batch; ++b) yr[b] = fmaf(scale, dx[b], yr[b]);
+        }
+    }
+    free(D), free(Dx), free(coef), free(idx);
+    return ORC_OK;
+}
+
+int orc_hsdb_matmul(const uint8_t* buf, size_t n, const float* x, size_t M, float* y) {
+    orc_hsdr_view v;
+    int rc = orc_hsdr_parse(buf, n, &v);
+    if (rc) return rc;
+    if (v.tile_rows != 1) return ORC_E_GEOMETRY;
+    const size_t R = v.rows, C = v.cols, K = v.n_atoms, B = v.tile_cols;
+    const size_t NB = C / B, C_full = NB * B, S = v.slots_per_tile;
+    float* D = copy_dict(buf, &v);
+    float* coef = (float*)malloc(v.n_codes * 4 + 4);
+    uint16_t* idx = (uint16_t*)malloc(v.n_codes * 2 + 2);
+    float* Dx = (float*)malloc(NB * K * M * 4 + 4);
+    if (!D || !coef || !idx || !Dx) {
+        free(D), free(coef), free(idx), free(Dx);
+        return ORC_E_ARG;
+    }
+    orc_hsdr_unpack(buf, n, idx, NULL, coef);
+    /* impl_fused_real, benchmark.py:117-118: Dx_b = D @ x_block, per block column b */
+#pragma omp parallel for schedule(static)
+    for (long long ba = 0; ba < (long long)(NB * K); ++ba) {
+        size_t b = (size_t)ba / K, a = (size_t)ba % K;
+        float* o = Dx + (b * K + a) * M;
+        for (size_t m = 0; m < M; ++m) o[m] = 0.0f;
+        for (size_t t = 0; t < B; ++t) {
+            const float dv = D[a * B + t];
+            const float* xr = x + (b * B + t) * M;
+            for (size_t m = 0; m < M; ++m) o[m] = fmaf(dv, xr[m], o[m]);
+        }
+    }
+    /* benchmark.py:122-127: tile (r, b) contributes its code row times Dx_b to row r;
+     * tile (r, b) sits at index r*NB + b (HierarchicalSDRStrategy.cpp:101-104). */
+#pragma omp parallel for schedule(static)
+    for (long long rr = 0; rr < (long long)R; ++rr) {
+        size_t r = (size_t)rr;
+        float* yr = y + r * M;
+        for (size_t m = 0; m < M; ++m) yr[m] = 0.0f;
+        for (size_t b = 0; b < NB; ++b) {
+            const size_t t = r * NB + b;
+            for (size_t s = 0; s < S; ++s) {
+                const size_t slot = t * S + s;
+                if (idx[slot] >= K) continue;
+                const float cf = coef[slot];
+                const float* dx = Dx + (b * K + idx[slot]) * M;
+                for (size_t m = 0; m < M; ++m) yr[m] = fmaf(cf, dx[m], yr[m]);
+            }
+        }
+        /* edge strip (cols C_full..C of row r), fp32 verbatim */
+        const size_t ce = C - C_full;
+        for (size_t c = 0; c < ce; ++c) {
+            float ev;
+            memcpy(&ev, buf + v.off_edge + 4 * (r * ce + c), 4);
+            const float* xr = x + (C_full + c) * M;
+            for (size_t m = 0; m < M; ++m) yr[m] = fmaf(ev, xr[m], yr[m]);
+        }
+    }
+    free(D), free(coef), free(idx), free(Dx);
+    return ORC_OK;
+}
+
+/* --------------------------------------------------------------- K-quants */
+
+/* ggufGetScaleMinQ4K, SparseInferenceEngine.cpp:266-274 (identical bit layout to
+ * unpack_k_scales_mins, HierarchicalSDRStrategy.cpp:802-814). */
+static void q4k_scale_min(const uint8_t* sc12, int j, uint8_t* sc, uint8_t* mn) {
+    if (j < 4) {
+        *sc = sc12[j] & 0x3Fu;
+        *mn = sc12[j + 4] & 0x3Fu;
+    } else {
+        *sc = (uint8_t)((sc12[j + 4] & 0x0Fu) | ((sc12[j - 4] >> 6) << 4));
+        *mn = (uint8_t)((sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4));
+    }
+}
+
+void orc_q4k_dequant(const uint8_t* blocks, size_t n_blocks, int order, float* out) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* p = blocks + b * 144;
+        const float d = orc_f16_to_f32(rd16(p));
+        const float dmin = orc_f16_to_f32(rd16(p + 2));
+        const uint8_t* sc12 = p + 4;
+        const uint8_t* qs = p + 16;
+        float* o = out + b * 256;
+        for (int is = 0; is < 8; ++is) {
+            uint8_t sc, mn;
+            q4k_scale_min(sc12, is, &sc, &mn);
+            const float ds = d * (float)sc;
+            const float dm = dmin * (float)mn;
+            for (int j = 0; j < 32; ++j) {
+                uint8_t q;
+                if (order == ORC_Q4K_GGML) {
+                    /* SparseInferenceEngine.cpp:375-382: group g = is/2 holds 32 bytes;
+                     * even sub-block = low nibbles, odd = high nibbles */
+                    const uint8_t byte = qs[(is / 2) * 32 + j];
+                    q = (is & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0x0Fu);
+                } else {
+                    /* HierarchicalSDRStrategy.cpp:840-845 */
+                    const int idx = is * 32 + j;
+                    const uint8_t byte = qs[idx / 2];
+                    q = (idx & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0x0Fu);
+                }
+                o[is * 32 + j] = (float)q * ds - dm;
+            }
+        }
+    }
+}
+
+void orc_q5k_dequant(const uint8_t* blocks, size_t n_blocks, float* out) {
+    /* HierarchicalSDRStrategy.cpp:851-885 */
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* p = blocks + b * 176;
+        const float d = orc_f16_to_f32(rd16(p));
+        const float dmin = orc_f16_to_f32(rd16(p + 2));
+        const uint8_t* sc12 = p + 4;
+        const uint8_t* qh = p + 16;
+        const uint8_t* qs = qh + 32;
+        for (int is = 0; is < 8; ++is) {
+            uint8_t sc, mn;
+            q4k_scale_min(sc12, is, &sc, &mn);
+            const float ds = d * (float)sc, dm = dmin * (float)mn;
+            for (int j = 0; j < 32; ++j) {
+                const int idx = is * 32 + j;
+                const uint8_t byte = qs[idx / 2];
+                const uint8_t lo = (idx & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0x0Fu);
+                const uint8_t hi = (uint8_t)((qh[idx / 8] >> (idx % 8)) & 1u);
+                out[b * 256 + idx] = (float)((hi << 4) | lo) * ds - dm;
+            }
+        }
+    }
+}
+
+void orc_q6k_dequant(const uint8_t* blocks, size_t n_blocks, float* out) {
+    /* HierarchicalSDRStrategy.cpp:888-933 (interleaved nibble / 2-bit order) */
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* p = blocks + b * 210;
+        const uint8_t* ql = p;
+        const uint8_t* qh = p + 128;
+        const int8_t* scales = (const int8_t*)(p + 192);
+        const float d = orc_f16_to_f32(rd16(p + 208));
+        for (int half = 0; half < 2; ++half) {
+            for (int sub = 0; sub < 8; ++sub) {
+                const float ds = d * (float)scales[half * 8 + sub];
+                for (int j = 0; j < 16; ++j) {
+                    const int e = sub * 16 + j;
+                    const uint8_t qb = ql[half * 64 + e / 2];
+                    const uint8_t lo = (e & 1) ? (uint8_t)(qb >> 4) : (uint8_t)(qb & 0x0Fu);
+                    const uint8_t hi = (uint8_t)((qh[half * 32 + e / 4] >> ((e % 4) * 2)) & 3u);
+                    out[b * 256 + half * 128 + e] = (float)(((hi << 4) | lo) - 32) * ds;
+                }
+            }
+        }
+    }
+}
+
+int orc_q4k_linear(const uint8_t* w, size_t R, size_t C, int order, const float* x, size_t M,
+                   float* y) {
+    if (C % 256) return ORC_E_GEOMETRY;
+    const size_t nb = C / 256;
+    /* decode (SparseInferenceEngine.cpp:362-384), then out[m, r] = sum_c in[m, c] * W[r, c]
+     * (blas_kernels.cpp:264-293 / BLAS-less row loop :101-143) */
+#pragma omp parallel
+    {
+        float* row = (float*)malloc(C * 4);
+#pragma omp for schedule(static)
+        for (long long rr = 0; rr < (long long)R; ++rr) {
+            size_t r = (size_t)rr;
+            orc_q4k_dequant(w + r * nb * 144, nb, order, row);
+            for (size_t m = 0; m < M; ++m) {
+                float acc = 0.0f;
+                const float* xm = x + m * C;
+                for (size_t c = 0; c < C; ++c) acc = fmaf(xm[c], row[c], acc);
+                y[m * R + r] = acc;
+            }
+        }
+        free(row);
+    }
+    return ORC_OK;
+}
+
+/* --------------------------------------------------------------- attention */
+
+static void softmax_row(float* s, size_t n) {
+    /* simd_kernels.cpp softmax: subtract max, exp, normalise */
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; ++i)
+        if (s[i] > mx) mx = s[i];
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        s[i] = expf(s[i] - mx);
+        sum += s[i];
+    }
+    for (size_t i = 0; i < n; ++i) s[i] /= sum;
+}
+
+void orc_mha_causal(const float* q, const float* k, const float* v, float* out, size_t B,
+                    size_t T, size_t hidden, size_t heads) {
+    /* attention_kernels.cpp:26-113 */
+    const size_t d = hidden / heads;
+    const float scale = 1.0f / sqrtf((float)d);
+    float* sc = (float*)malloc(T * 4 + 4);
+    for (size_t b = 0; b < B; ++b)
+        for (size_t h = 0; h < heads; ++h)
+            for (size_t i = 0; i < T; ++i) {
+                const float* qi = q + (b * T + i) * hidden + h * d;
+                for (size_t j = 0; j < T; ++j) {
+                    const float* kj = k + (b * T + j) * hidden + h * d;
+                    float acc = 0.0f;
+                    for (size_t t = 0; t < d; ++t) acc = fmaf(qi[t], kj[t], acc);
+                    sc[j] = (j > i) ? -INFINITY : acc * scale; /* apply_causal_mask */
+                }
+                softmax_row(sc, T);
+                float* o = out + (b * T + i) * hidden + h * d;
+                for (size_t t = 0; t < d; ++t) {
+                    float acc = 0.0f;
+                    for (size_t j = 0; j < T; ++j)
+                        acc = fmaf(sc[j], v[(b * T + j) * hidden + h * d + t], acc);
+                    o[t] = acc;
+                }
+            }
+    free(sc);
+}
+
+void orc_attn_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                     const int32_t* lens, size_t B, size_t T, size_t Hq, size_t Hkv, size_t d,
+                     float scale, float* out) {
+    const size_t rep = Hq / Hkv;
+    float* sc = (float*)malloc(T * 4 + 4);
+    for (size_t b = 0; b < B; ++b) {
+        const size_t L = lens ? (size_t)lens[b] : T;
+        for (size_t h = 0; h < Hq; ++h) {
+            const size_t kvh = h / rep;
+            const float* qh = q + (b * Hq + h) * d;
+            for (size_t j = 0; j < L; ++j) {
+                const uint16_t* kj = kcache + ((b * T + j) * Hkv + kvh) * d;
+                float acc = 0.0f;
+                for (size_t t = 0; t < d; ++t) acc = fmaf(qh[t], orc_f16_to_f32(kj[t]), acc);
+                sc[j] = acc * scale;
+            }
+            float* o = out + (b * Hq + h) * d;
+            if (L == 0) {
+                for (size_t t = 0; t < d; ++t) o[t] = 0.0f;
+                continue;
+            }
+            softmax_row(sc, L);
+            for (size_t t = 0; t < d; ++t) {
+                float acc = 0.0f;
+                for (size_t j = 0; j < L; ++j)
+                    acc = fmaf(sc[j], orc_f16_to_f32(vcache[((b * T + j) * Hkv + kvh) * d + t]),
+                               acc);
+                o[t] = acc;
+            }
+        }
+    }
+    free(sc);
+}
+
+/* ---------------------------------------------------------- decoder ops */
+
+void orc_rms_norm(const float* x, const float* w, size_t ntok, size_t n, float eps, float* y) {
+    /* cortex_sdk.cpp:1208-1232 */
+    for (size_t t = 0; t < ntok; ++t) {
+        const float* s = x + t * n;
+        float ms = 0.0f;
+        for (size_t i = 0; i < n; ++i) ms += s[i] * s[i];
+        ms /= (float)n;
+        const float inv = 1.0f / sqrtf(ms + eps);
+        for (size_t i = 0; i < n; ++i) y[t * n + i] = s[i] * inv * w[i];
+    }
+}
+
+void orc_silu_mul(const float* gate, const float* up, size_t n, float* y) {
+    /* cortex_sdk.cpp:1245-1256 */
+    for (size_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        const float sig = 1.0f / (1.0f + expf(-g));
+        y[i] = (g * sig) * up[i];
+    }
+}
+
+void orc_rope(float* x, size_t ntok, size_t heads, size_t head_dim, float theta, size_t pos0) {
+    /* get_rope_cache / apply_rope_inplace, cortex_sdk.cpp:1363-1423: freq for pair
+     * (i, i+1) = theta^(-i/head_dim), angle = pos * freq, adjacent-pair rotation. */
+    const size_t rot = head_dim - (head_dim % 2);
+    for (size_t t = 0; t < ntok; ++t) {
+        const float pos = (float)(pos0 + t);
+        for (size_t h = 0; h < heads; ++h) {
+            float* base = x + (t * heads + h) * head_dim;
+            for (size_t i = 0; i < rot; i += 2) {
+                const float freq = powf(theta, -((float)i / (float)head_dim));
+                const float ang = pos * freq;
+                const float c = cosf(ang), s = sinf(ang);
+                const float x0 = base[i], x1 = base[i + 1];
+                base[i] = x0 * c - x1 * s;
+                base[i + 1] = x0 * s + x1 * c;
+            }
+        }
+    }
+}
+
+int orc_select_best(const float* logits, size_t n, const uint8_t* repeated, float temperature,
+                    float penalty) {
+    /* cortex_sdk.cpp:1005-1030 */
+    const float ts = temperature > 0.0f ? 1.0f / temperature : 1.0f;
+    float best = -INFINITY;
+    int tok = -1;
+    for (size_t i = 0; i < n; ++i) {
+        float s = logits[i] * ts;
+        if (!isfinite(s)) continue;
+        if (repeated && repeated[i]) s -= penalty;
+        if (s > best) {
+            best = s;
+            tok = (int)i;
+        }
+    }
+    return tok;
+}

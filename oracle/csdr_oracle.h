@@ -1,0 +1,136 @@
+/*
+ * csdr_oracle.h — CPU restatement of cortexSDR's compressed-weight inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker. The product
+ * (cortexsdr_amd/) never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to the
+ * cortexSDR source tree). Pinning: each function is checked in tests/ against
+ * reference golden vectors (known-answer tests, fixtures emitted by the compiled
+ * reference in oracle/_ref) or against closed forms / brute force. Functions with
+ * no such check are marked "parity unpinned" below (none at present).
+ *
+ * Conventions
+ *   - status codes: 0 ok, negative = error (ORC_E_*).
+ *   - HSDR weight W is R x C row-major fp32 (segment dims {R, C}).
+ *   - matmul_row_major x is (C x batch) row-major, Y is (R x batch) row-major
+ *     (HierarchicalSDRStrategy.hpp:179-181 convention).
+ *   - linear x is (M x C) row-major, y is (M x R) row-major
+ *     (kernels/blas_kernels.cpp:264-293 linear_forward convention).
+ */
+#ifndef CSDR_ORACLE_H
+#define CSDR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_OK 0
+#define ORC_E_MAGIC (-1)
+#define ORC_E_VERSION (-2)
+#define ORC_E_TRUNCATED (-3)
+#define ORC_E_GEOMETRY (-4)
+#define ORC_E_ARG (-5)
+
+/* ---- fp16 (utils/fp16_convert.hpp:26-62 decode; encode = IEEE round-to-nearest-even,
+ *      the F16C branch at :68-71, not the truncating scalar branch at :73-93) ---- */
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+void orc_f16_to_f32_array(const uint16_t* src, float* dst, size_t n);
+void orc_f32_to_f16_array(const float* src, uint16_t* dst, size_t n);
+
+/* ---- HSDR-family stream view (HierarchicalSDRStrategy.cpp:46-66 header, :1197-1237 order).
+ * Magic "HSDR" (version 2): binary codes, coefficient = gamma_l * sign.
+ * Magic "HSDB" (version 1): block-coded extension, tile 1 x B; after the packed
+ * u16 codes it carries one fp16 |c| per slot; coefficient = gamma_l * sign * |c|.
+ * Arrays are copied out (the stream gives no alignment guarantee). */
+typedef struct {
+    int is_hsdb;
+    uint32_t version, rows, cols, n_tiles;
+    uint32_t tile_rows, tile_cols, n_atoms, n_stages, k_per_stage;
+    float stage_decay;
+    uint32_t edge_bytes;
+    size_t slots_per_tile;  /* n_stages * k_per_stage */
+    size_t n_codes;         /* n_tiles * slots_per_tile */
+    size_t off_gamma, off_dict, off_packed, off_coef, off_edge, end;
+} orc_hsdr_view;
+
+int orc_hsdr_parse(const uint8_t* buf, size_t n, orc_hsdr_view* v);
+
+/* Unpacked codes in stream (tile-major, stage-major slot) order:
+ * idx = packed & 0x7FFF, sign = +1/-1 from bit 15 (HierarchicalSDRStrategy.cpp:81-84).
+ * coef = gamma_l * sign (HSDR) or gamma_l * sign * f16(|c|) (HSDB), fp32. */
+int orc_hsdr_unpack(const uint8_t* buf, size_t n, uint16_t* idx, int8_t* sign, float* coef);
+
+/* Dense decode, A2: decodeAllTiles + reassembleTiles + edge splice
+ * (HierarchicalSDRStrategy.cpp:612-634, 119-135, 1340-1440). out: R*C fp32. */
+int orc_hsdr_decompress(const uint8_t* buf, size_t n, float* out, size_t out_floats);
+
+/* Fused 1D-row matmul, A3 (HierarchicalSDRStrategy.cpp:1257-1338). HSDR only;
+ * requires tile_rows == 1, tile_cols == C, n_tiles == R (same checks as :1273-1289). */
+int orc_hsdr_matmul_row_major(const uint8_t* buf, size_t n, const float* x, size_t batch,
+                              float* y);
+
+/* Block-coded fused matmul, A0 (research exp_c_kernel/benchmark.py:106-130 impl_fused_real,
+ * with the 1 x B tile order of HierarchicalSDRStrategy.cpp:95-116): per block column b,
+ * Dx_b = D . x_b (K x M), then Y[r] += sum_j coef_j * Dx_b[idx_j]; plus the fp32 edge strip
+ * times x[C_full:]. x is (C x M) row-major, y (R x M). Accepts HSDR streams with
+ * tile_rows == 1 as well (binary codes). */
+int orc_hsdb_matmul(const uint8_t* buf, size_t n, const float* x, size_t M, float* y);
+
+/* ---- GGUF K-quant dequant ----
+ * ggml order (engine path, A7): SparseInferenceEngine.cpp:266-274 (scale/min unpack),
+ * :362-384 (per 32-byte group g: 32 low nibbles -> sub-block 2g, 32 high -> 2g+1).
+ * interleaved order (HSDR compress side, A6): HierarchicalSDRStrategy.cpp:802-849
+ * (element i of the super-block reads byte i/2, low nibble when i is even).
+ * value = (d*sc) * q - (dmin*m). One super-block = 144 bytes = 256 values. */
+#define ORC_Q4K_GGML 0
+#define ORC_Q4K_INTERLEAVED 1
+void orc_q4k_dequant(const uint8_t* blocks, size_t n_blocks, int order, float* out);
+/* Q5_K (176 B) and Q6_K (210 B) dequant as HierarchicalSDRStrategy.cpp:851-989. */
+void orc_q5k_dequant(const uint8_t* blocks, size_t n_blocks, float* out);
+void orc_q6k_dequant(const uint8_t* blocks, size_t n_blocks, float* out);
+
+/* Q4_K linear: y (M x R) = x (M x C) . dequant(W)^T, W = R rows of C/256 super-blocks
+ * (GGUF row-major). Dequant then linear_forward semantics (blas_kernels.cpp:264-293,
+ * BLAS-less row loop :101-143), fp32 accumulation in column order. */
+int orc_q4k_linear(const uint8_t* w, size_t R, size_t C, int order, const float* x,
+                   size_t M, float* y);
+
+/* ---- Attention ----
+ * Causal multi-head attention as kernels/attention_kernels.cpp:26-113: per head,
+ * scores = Q K^T / sqrt(d), causal mask, row softmax, times V. q,k,v,out: (B, T, H*d). */
+void orc_mha_causal(const float* q, const float* k, const float* v, float* out, size_t B,
+                    size_t T, size_t hidden, size_t heads);
+
+/* Decode attention against a cache (the behaviour flash_attention_with_kv_cache,
+ * kernels/flash_attention.cpp:165-247, intends, with GQA as repeat_kv_heads,
+ * api/cortex_sdk.cpp:1453-1478: q head h reads kv head h / (Hq/Hkv)).
+ * q: (B, Hq, d) fp32; kcache/vcache: (B, T, Hkv, d) fp16 bits; out (B, Hq, d).
+ * Attends to positions [0, len_b) where len_b = lens[b] (or T when lens == NULL). */
+void orc_attn_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                     const int32_t* lens, size_t B, size_t T, size_t Hq, size_t Hkv, size_t d,
+                     float scale, float* out);
+
+/* ---- Decoder elementwise (api/cortex_sdk.cpp) ---- */
+/* rms_norm :1208-1232 (eps default 1e-5) over ntok rows of width n. */
+void orc_rms_norm(const float* x, const float* w, size_t ntok, size_t n, float eps, float* y);
+/* silu_mul :1245-1256 */
+void orc_silu_mul(const float* gate, const float* up, size_t n, float* y);
+/* RoPE on adjacent pairs, get_rope_cache/apply_rope_inplace :1363-1423, positions
+ * pos0..pos0+ntok-1; x is (ntok, heads, head_dim) in place. */
+void orc_rope(float* x, size_t ntok, size_t heads, size_t head_dim, float theta, size_t pos0);
+/* select_best_from_logits :1005-1030: score = logit * (1/temperature when > 0), minus
+ * penalty when the token was generated before; strict '>' keeps the first maximum;
+ * non-finite scores skipped. Returns -1 when nothing is finite. */
+int orc_select_best(const float* logits, size_t n, const uint8_t* repeated, float temperature,
+                    float penalty);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

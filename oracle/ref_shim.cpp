@@ -1,0 +1,131 @@
+// ref_shim.cpp — C-ABI driver over the cortexSDR reference sources, compiled from where
+// they lie under the reference tree by oracle/Makefile into oracle/_ref/libcsdr_ref.so.
+//
+// TEST INFRASTRUCTURE ONLY: used by tests/ (and tests/golden/make_fixtures.py) to check the
+// oracle restatement against the reference's own code. No reference source is copied here;
+// this file only calls the reference's public entry points:
+//   HierarchicalSDRStrategy::{compress, decompress, matmulRowMajor, dequantizeToFP32}
+//     (strategies/HierarchicalSDRStrategy.hpp:170-181, :333)
+//   Kernels::multi_head_attention (kernels/attention_kernels.hpp:26)
+//   Kernels::flash_attention_forward (kernels/flash_attention.hpp:43)
+#include "strategies/HierarchicalSDRStrategy.hpp"
+#include "kernels/attention_kernels.hpp"
+#include "kernels/flash_attention.hpp"
+
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+#include <string>
+#include <vector>
+
+using namespace CortexAICompression;
+
+namespace {
+thread_local std::string g_err;
+
+int fail(const std::exception& e, int code) {
+    g_err = e.what();
+    return code;
+}
+
+std::vector<std::byte> as_bytes(const void* p, size_t n) {
+    std::vector<std::byte> v(n);
+    if (n) std::memcpy(v.data(), p, n);
+    return v;
+}
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error() { return g_err.c_str(); }
+
+void ref_free(void* p) { std::free(p); }
+
+// Compress an R x C fp32 matrix with the reference V4b fit. The same config is installed
+// for the attention and MLP roles, so configFor() picks it regardless of the name (it still
+// widens tile_cols to C when tile_rows == 1, HierarchicalSDRStrategy.cpp:1024-1046).
+int ref_hsdr_compress(const float* w, uint32_t R, uint32_t C, uint16_t tile_rows,
+                      uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages, uint8_t k_per_stage,
+                      uint8_t ksvd_iters, float stage_decay, uint8_t** out, size_t* out_n) {
+    try {
+        HierarchicalSDRConfig cfg;
+        cfg.tile_rows = tile_rows;
+        cfg.tile_cols = tile_cols;
+        cfg.n_atoms = n_atoms;
+        cfg.n_stages = n_stages;
+        cfg.active_bits_per_stage = k_per_stage;
+        cfg.ksvd_iters = ksvd_iters;
+        cfg.stage_decay = stage_decay;
+        HierarchicalSDRStrategy strat(cfg, cfg);
+        ModelSegment seg(SegmentType::WEIGHTS_FP32, "ref.weight",
+                         as_bytes(w, sizeof(float) * size_t(R) * C));
+        TensorMetadata meta;
+        meta.dimensions = {R, C};
+        seg.tensor_metadata = meta;
+        seg.data_format = "f32";
+        std::vector<std::byte> bytes = strat.compress(seg);
+        *out_n = bytes.size();
+        *out = static_cast<uint8_t*>(std::malloc(bytes.size() ? bytes.size() : 1));
+        std::memcpy(*out, bytes.data(), bytes.size());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+int ref_hsdr_decompress(const uint8_t* stream, size_t n, float* out, size_t out_floats) {
+    try {
+        HierarchicalSDRStrategy strat;
+        std::vector<std::byte> bytes =
+            strat.decompress(as_bytes(stream, n), SegmentType::WEIGHTS_FP32, out_floats * 4);
+        std::memcpy(out, bytes.data(), bytes.size());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+int ref_hsdr_matmul_row_major(const uint8_t* stream, size_t n, const float* x, size_t batch,
+                              float* y, size_t y_floats) {
+    try {
+        HierarchicalSDRStrategy strat;
+        std::vector<float> Y = strat.matmulRowMajor(as_bytes(stream, n), x, batch);
+        if (Y.size() > y_floats) return -2;
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+// dequantizeToFP32 on a one-segment byte stream tagged with `fmt` ("q4_k", "q5_k", ...).
+int ref_dequant(const uint8_t* data, size_t n, const char* fmt, uint32_t R, uint32_t C,
+                float* out, size_t out_floats) {
+    try {
+        ModelSegment seg(SegmentType::WEIGHTS_INT8, "ref.kquant", as_bytes(data, n));
+        seg.data_format = fmt;
+        TensorMetadata meta;
+        meta.dimensions = {R, C};
+        seg.tensor_metadata = meta;
+        std::vector<float> v = HierarchicalSDRStrategy::dequantizeToFP32(seg);
+        if (v.size() > out_floats) return -2;
+        std::memcpy(out, v.data(), v.size() * sizeof(float));
+        return static_cast<int>(v.size());
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+void ref_mha(const float* q, const float* k, const float* v, float* out, size_t B, size_t T,
+             size_t hidden, size_t heads, int causal) {
+    Kernels::multi_head_attention(q, k, v, out, B, T, hidden, heads, causal != 0);
+}
+
+void ref_flash_attention(const float* q, const float* k, const float* v, float* out, size_t B,
+                         size_t T, size_t hidden, size_t heads, int causal) {
+    Kernels::FlashAttentionConfig cfg;
+    cfg.use_causal_mask = causal != 0;
+    Kernels::flash_attention_forward(q, k, v, out, B, T, hidden, heads, cfg);
+}
+
+}  // extern "C"

@@ -1,0 +1,92 @@
+"""Writes tests/golden/ref_fixtures.npz from the reference's own code.
+
+Runs in the build container only (it needs oracle/_ref/libcsdr_ref.so, compiled by
+`make -C oracle ref` from the reference sources). The .npz holds data only: the inputs
+this script generates and the outputs the reference computed for them.
+
+  hsdr1d_*   HierarchicalSDRStrategy::compress on a 64 x 256 fp32 matrix with 1-row tiles
+             (K=32, 3 stages x 4), then decompress and matmulRowMajor (x: 256 x 4)
+  hsdr1de_*  same with C = 200 (1-row tiles cover the whole row, no edge)
+  hsdr2d_*   compress with 8 x 16 tiles on a 40 x 100 matrix (edge strip of 4 columns),
+             then decompress
+  hsdr2db_*  compress with 8 x 16 tiles on a 45 x 96 matrix (bottom edge of 5 rows)
+  q4k/q5k/q6k_*  random super-blocks through dequantizeToFP32 (interleaved orders)
+  mha_*      Kernels::multi_head_attention / flash_attention_forward, causal, B=2, T=9,
+             hidden=32, heads=4
+
+Usage: python tests/golden/make_fixtures.py
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+
+
+def main() -> None:
+    oracle.build(ref=True)
+    if oracle.ref() is None:
+        raise SystemExit("oracle/_ref/libcsdr_ref.so is not built")
+    rng = np.random.default_rng(20261201)
+    out = {}
+
+    w = rng.normal(0, 0.05, (64, 256)).astype(np.float32)
+    s = oracle.ref_hsdr_compress(w, 1, 256, 32, 3, 4, ksvd_iters=4)
+    x = rng.normal(0, 1, (256, 4)).astype(np.float32)
+    out["hsdr1d_stream"] = np.frombuffer(s, np.uint8)
+    out["hsdr1d_x"] = x
+    out["hsdr1d_w"] = oracle.ref_hsdr_decompress(s, 64, 256)
+    out["hsdr1d_y"] = oracle.ref_hsdr_matmul_row_major(s, x, 64)
+
+    w = rng.normal(0, 0.05, (48, 200)).astype(np.float32)
+    s = oracle.ref_hsdr_compress(w, 1, 200, 16, 2, 3, ksvd_iters=3)
+    x = rng.normal(0, 1, (200, 3)).astype(np.float32)
+    out["hsdr1de_stream"] = np.frombuffer(s, np.uint8)
+    out["hsdr1de_x"] = x
+    out["hsdr1de_w"] = oracle.ref_hsdr_decompress(s, 48, 200)
+    out["hsdr1de_y"] = oracle.ref_hsdr_matmul_row_major(s, x, 48)
+
+    w = rng.normal(0, 0.05, (40, 100)).astype(np.float32)
+    s = oracle.ref_hsdr_compress(w, 8, 16, 16, 3, 2, ksvd_iters=3)
+    out["hsdr2d_stream"] = np.frombuffer(s, np.uint8)
+    out["hsdr2d_w"] = oracle.ref_hsdr_decompress(s, 40, 100)
+
+    w = rng.normal(0, 0.05, (45, 96)).astype(np.float32)
+    s = oracle.ref_hsdr_compress(w, 8, 16, 16, 2, 3, ksvd_iters=3)
+    out["hsdr2db_stream"] = np.frombuffer(s, np.uint8)
+    out["hsdr2db_w"] = oracle.ref_hsdr_decompress(s, 45, 96)
+
+    for name, nbytes in (("q4_k", 144), ("q5_k", 176), ("q6_k", 210)):
+        blocks = rng.integers(0, 256, (6, nbytes), dtype=np.uint8)
+        # keep the fp16 scales finite and modest: d (and dmin) from U(0.001, 0.05)
+        d_off = 208 if name == "q6_k" else 0
+        for i in range(6):
+            for off in ((d_off,) if name == "q6_k" else (0, 2)):
+                v = np.float16(rng.uniform(0.001, 0.05)).view(np.uint16)
+                blocks[i, off:off + 2] = np.array([v], "<u2").view(np.uint8)
+        key = name.replace("_", "")
+        out[f"{key}_blocks"] = blocks
+        out[f"{key}_ref"] = oracle.ref_dequant(blocks.ravel(), name, 6, 256)
+
+    B, T, H, heads = 2, 9, 32, 4
+    q = rng.normal(0, 1, (B, T, H)).astype(np.float32)
+    k = rng.normal(0, 1, (B, T, H)).astype(np.float32)
+    v = rng.normal(0, 1, (B, T, H)).astype(np.float32)
+    out["mha_q"], out["mha_k"], out["mha_v"] = q, k, v
+    out["mha_out"] = oracle.ref_mha(q, k, v, heads, causal=True)
+    out["mha_flash_out"] = oracle.ref_mha(q, k, v, heads, causal=True, flash=True)
+
+    path = os.path.join(HERE, "ref_fixtures.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
+if __name__ == "__main__":
+    main()
