@@ -48,8 +48,13 @@ SIGNATURES = {
     "csdr_hsdb_get_info": (C.c_int, [_vp, C.POINTER(HsdbInfo)]),
     "csdr_hsdb_workspace_bytes": (_sz, [_vp, C.c_int]),
     "csdr_hsdb_matmul": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, _sz, _vp]),
-    "csdr_hsdb_dx": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _sz, _vp]),
-    "csdr_hsdb_gather": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, _sz, _vp]),
+    "csdr_hsdb_group_workspace_bytes": (_sz, [C.c_int, C.POINTER(_vp), C.c_int]),
+    "csdr_hsdb_matmul_group": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
+                                         C.c_int, C.POINTER(_vp), _vp, _sz, _vp]),
+    "csdr_hsdb_dx_group": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
+                                     C.c_int, C.POINTER(_vp), _vp, _sz, _vp]),
+    "csdr_hsdb_gather_group": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
+                                         C.c_int, C.POINTER(_vp), _vp, _sz, _vp]),
     "csdr_hsdb_decompress": (C.c_int, [_vp, _vp, _vp]),
     "csdr_hsdb_export_codes": (C.c_int, [_vp, _vp, _vp, _vp]),
 }

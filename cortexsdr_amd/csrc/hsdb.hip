@@ -6,27 +6,29 @@
 //
 // Math. W is R x C; tile (r, b) covers W[r, b*B : b*B+B] (1-row tiles, B = tile_cols) and
 // is sum_j c_j * D[idx_j] over its S*k coded slots, c_j = gamma_{j/k} * signed fp16 |c|
-// (binary HSDR: |c| = 1). Y = W.X is computed without W:
-//   kernel 1 (dx):     P[b][a][m] = D[a] . X[b*B : b*B+B, m]          (the reference's Dx)
-//   kernel 2 (gather): Y[r][m] = sum_b sum_j c_j * P[b][idx_j][m] + edge strip . X
+// (binary HSDR: |c| = 1). Y = W.X is computed without W, for a group of up to 8 matrices
+// per call, in two launches:
+//   dx:     P[b][a][m] = D[a] . X[b*B : b*B+B, m] (the reference's Dx precompute), Y = 0
+//   gather: Y[r][m] += sum_b sum_j c_j * P[b][idx_j][m] (+ fp32 edge strip . X)
 //
 // Device code layout (built at load time; 4 bytes per slot, the stream's own byte count):
 //   word = (signed fp16 coefficient bits << 16) | atom index (15 bits)
 // ordered chunk-major: block columns are grouped in chunks of NBc; chunk c holds, for
-// every row r, the NBc tiles (r, c*NBc .. c*NBc+NBc-1) back to back, so a workgroup that
-// owns (chunk, row tile) streams one contiguous range. 2-D tiles (tile_rows > 1, decode
-// only) keep the stream's tile-major order.
+// every row r, the NBc tiles (r, c*NBc .. c*NBc+NBc-1) back to back, so the rows of one
+// chunk are one contiguous run. 2-D tiles (tile_rows > 1, decode only) keep the stream's
+// tile-major order.
 //
-// Gather workgroup = (chunk, row tile). It stages the chunk's P slice (NBc*K floats per
-// column) in LDS, streams its code words once (non-temporal vector loads), gathers from
-// LDS, reduces per row, writes a per-chunk partial, and the last workgroup to finish a row
-// tile (device-scope counter, self-resetting by wrap-around) sums the partials in chunk
-// order and adds the fp32 edge strip. Workgroups are numbered so that all row tiles of a
-// chunk land on one XCD (dispatch is round-robin over the 8 XCDs), which keeps that
-// chunk's P slice in a single L2.
+// The M == 1 gather is persistent: a workgroup owns (chunk, row range), stages the chunk's
+// P slice in LDS once and streams its run with three units of 16-byte loads in flight
+// (each wave instruction reads 1 KiB contiguous), gathers from LDS and adds each row's
+// total into Y with device-scope float atomics (other chunks of the row run on other
+// workgroups), so the summation order over chunks is not fixed: results agree to fp32
+// rounding, not bit for bit. Workgroups of one chunk are numbered to share an XCD
+// (dispatch is round-robin over the 8 XCDs), which keeps the P slice in one L2.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -44,6 +46,7 @@ struct csdr_hsdb {
     uint32_t* d_codes = nullptr;    // n_tiles * slots words
     float* d_slot_gamma = nullptr;  // slots floats: gamma[j / k]
     float* d_edge = nullptr;        // top-right strip (R_full x Ce) then bottom strip
+    float h_slot_gamma[32] = {};    // host copy of the first 32 slot gammas (kernel args)
     size_t edge_floats = 0;
     size_t device_bytes = 0;
 };
@@ -54,266 +57,405 @@ using csdr::set_error;
 
 constexpr int kThreads = 256;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kDxBlocksPerWG = 16;
+
 constexpr uint32_t kMaxChunkBlocks = 8;
 
-// Row-tile height of the gather for a given column group width.
-inline int gather_rows_per_wg(int MV) { return MV == 1 ? 256 : 64; }
 
-// ------------------------------------------------------------------ dx kernels
+// ------------------------------------------------------------------ matmul kernels
 
-// P[b][a][m] for block length 64: one thread per atom, D row held in registers, the
-// x blocks of this workgroup staged in LDS. Summation order over t matches the CPU
-// restatement (t ascending, fused multiply-add).
-template <typename XT>
-__global__ __launch_bounds__(kThreads) void dx_b64_kernel(const float* __restrict__ D,
-                                                          const XT* __restrict__ x, int K,
-                                                          int NB, int M,
-                                                          float* __restrict__ P) {
-    __shared__ float xs[kDxBlocksPerWG][64];
-    const int a = blockIdx.x * kThreads + threadIdx.x;
-    const int b0 = blockIdx.y * kDxBlocksPerWG;
-    const int m = blockIdx.z;
-    const int nb = min(kDxBlocksPerWG, NB - b0);
-    for (int i = threadIdx.x; i < nb * 64; i += kThreads)
-        xs[i >> 6][i & 63] = csdr::to_f32(x[(size_t)(b0 * 64 + i) * M + m]);
-    __syncthreads();
-    if (a >= K) return;
-    float drow[64];
-    const float4* dp = reinterpret_cast<const float4*>(D + (size_t)a * 64);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float4 v = dp[i];
-        drow[4 * i + 0] = v.x;
-        drow[4 * i + 1] = v.y;
-        drow[4 * i + 2] = v.z;
-        drow[4 * i + 3] = v.w;
-    }
-    for (int bb = 0; bb < nb; ++bb) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 64; ++t) acc = fmaf(drow[t], xs[bb][t], acc);
-        P[((size_t)(b0 + bb) * K + a) * M + m] = acc;
-    }
-}
+constexpr int kMaxGroup = 8;
+constexpr int kMaxSlotsArg = 32;
+constexpr int kStageBatch = 8;  // global loads in flight per thread while staging to LDS
+constexpr int kDepth = 3;       // code units in flight per gather workgroup (M == 1)
+constexpr int kGatherWGsPerCU = 8;
 
-// P[b][a][m] for any block length (1-row HSDR streams have B = C): one wave per
-// (b, a, group of up to 8 columns); lanes stride over the block, then a wave reduction.
-template <typename XT>
-__global__ __launch_bounds__(kThreads) void dx_generic_kernel(const float* __restrict__ D,
-                                                              const XT* __restrict__ x, int K,
-                                                              int NB, int blen, int M,
-                                                              float* __restrict__ P) {
-    const int lane = threadIdx.x & 63;
-    const long long wave = ((long long)blockIdx.x * kThreads + threadIdx.x) >> 6;
-    const int mg = (M + 7) / 8;
-    if (wave >= (long long)NB * K * mg) return;
-    const int g = (int)(wave % mg);
-    const long long ba = wave / mg;
-    const int b = (int)(ba / K), a = (int)(ba % K);
-    const int m0 = g * 8, nm = min(8, M - m0);
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    const float* drow = D + (size_t)a * blen;
-    const XT* xb = x + (size_t)b * blen * M + m0;
-    for (int t = lane; t < blen; t += 64) {
-        const float dv = drow[t];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (j < nm) acc[j] = fmaf(dv, csdr::to_f32(xb[(size_t)t * M + j]), acc[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = csdr::wave_sum(acc[j]);
-    if (lane == 0)
-        for (int j = 0; j < nm; ++j) P[((size_t)b * K + a) * M + m0 + j] = acc[j];
-}
-
-// ------------------------------------------------------------------ gather kernel
-
-struct GatherParams {
+// One coded matrix of a grouped launch.
+struct MatDesc {
     const uint32_t* codes;
-    const float* P;
+    const float* dict;
     const float* slot_gamma;
     const float* edge;
     const void* x;
     float* y;
-    float* ypart;
-    unsigned int* counters;
-    int x_f16;
-    int R, K, NB, NBc, nchunks, slots, Rt, nrt, M, MVz, Ce, C_full;
+    float* P;  // NB * K * M floats of workspace
+    int R, K, NB, NBc, nchunks, slots, blen, Ce, C_full;
+    int PB;                   // dx: block columns per workgroup (block length 64)
+    int dx_base, dx_count;    // dx workgroup ids [base, base + count)
+    int g_base, g_count;      // gather workgroup ids, base a multiple of 8
+    int splits;               // gather workgroups per chunk
+    int rows_per_wg;          // rows of a chunk handled by one gather workgroup
+    int Rt;                   // M > 1 gather: rows per workgroup
+    float sgam[kMaxSlotsArg]; // gamma of each slot (slots <= kMaxSlotsArg; scalar loads)
 };
 
-template <typename XT>
-__device__ __forceinline__ float edge_dot(const GatherParams& p, int r, int m) {
-    const XT* x = static_cast<const XT*>(p.x);
-    const float* e = p.edge + (size_t)r * p.Ce;
-    float s = 0.0f;
-    for (int c = 0; c < p.Ce; ++c)
-        s = fmaf(e[c], csdr::to_f32(x[(size_t)(p.C_full + c) * p.M + m]), s);
-    return s;
+struct Params {
+    MatDesc m[kMaxGroup];
+    int G, M, MVz, x_f16;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each row of 16 lanes, result in every lane of the row: pair swap, quad swap,
+// half-row mirror, row mirror (DPP moves, no LDS round trip).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x141>(v);  // row_half_mirror
+    v += dpp_move<0x140>(v);  // row_mirror
+    return v;
 }
 
-// MV: output columns per pass (1 or 4); MAXIT: (row, block) pairs per thread;
-// SLOTS: coded slots per tile when it is a multiple of 4 (vector loads), 0 = any.
-template <int MV, int MAXIT, int SLOTS>
-__global__ __launch_bounds__(kThreads) void gather_kernel(GatherParams p) {
-    extern __shared__ float smem[];
-    // ---- workgroup -> (chunk, row tile), all row tiles of a chunk on one XCD
-    const int wg = blockIdx.x;
-    const int xcd = wg & 7;
-    const int j = wg >> 3;
-    const int cl = j / p.nrt;
-    const int rt = j - cl * p.nrt;
-    const int c = cl * 8 + xcd;
-    if (c >= p.nchunks) return;
+template <typename XT>
+__device__ __forceinline__ float xval(const void* x, size_t i) {
+    return csdr::to_f32(static_cast<const XT*>(x)[i]);
+}
+__device__ __forceinline__ float xload(const void* x, int f16, size_t i) {
+    return f16 ? xval<_Float16>(x, i) : xval<float>(x, i);
+}
 
+// xs[i] = float(src[i]) for i < n by the whole workgroup, kStageBatch independent loads
+// per thread in flight at a time (branch-free: out-of-range lanes reload the last element).
+template <typename T>
+__device__ __forceinline__ void stage_to_lds(const T* __restrict__ src, int n, float* xs) {
     const int tid = threadIdx.x;
-    const int b0 = c * p.NBc;
-    const int nbc = min(p.NBc, p.NB - b0);
-    const int r0 = rt * p.Rt;
-    const int nr = min(p.Rt, p.R - r0);
-    const int npairs = nr * nbc;
-    const int slots = SLOTS > 0 ? SLOTS : p.slots;
-    const uint32_t* cb =
-        p.codes + (size_t)c * p.NBc * p.R * slots + (size_t)r0 * nbc * slots;
-
-    float* Ps = smem;                                      // nbc * K * MV
-    float* part = smem + (size_t)p.NBc * p.K * MV;         // Rt * NBc * MV
-
-    // ---- 1. stream this workgroup's code words into registers (issued first)
-    constexpr int NV = SLOTS > 0 ? SLOTS / 4 : 1;
-    u32x4 wv[MAXIT][NV];
-    if constexpr (SLOTS > 0) {
+    for (int i0 = 0; i0 < n; i0 += kThreads * kStageBatch) {
+        float v[kStageBatch];
 #pragma unroll
-        for (int i = 0; i < MAXIT; ++i) {
-            const int pi = tid + i * kThreads;
-            if (pi < npairs) {
-                const u32x4* src = reinterpret_cast<const u32x4*>(cb + (size_t)pi * SLOTS);
+        for (int j = 0; j < kStageBatch; ++j)
+            v[j] = csdr::to_f32(src[min(i0 + j * kThreads + tid, n - 1)]);
 #pragma unroll
-                for (int q = 0; q < NV; ++q) wv[i][q] = __builtin_nontemporal_load(src + q);
-            }
+        for (int j = 0; j < kStageBatch; ++j) {
+            const int i = i0 + j * kThreads + tid;
+            if (i < n) xs[i] = v[j];
         }
     }
-    float sg[SLOTS > 0 ? SLOTS : 1];
-    if constexpr (SLOTS > 0) {
-#pragma unroll
-        for (int q = 0; q < SLOTS; ++q) sg[q] = p.slot_gamma[q];
-    }
+}
 
-    const bool direct = (p.nchunks == 1);
-    for (int z = 0; z < p.MVz; ++z) {
-        const int m0 = z * MV;
-        // ---- 2. stage the chunk's P slice (columns m0 .. m0+MV) in LDS
-        if (z > 0) __syncthreads();
-        const int nP = nbc * p.K;
-        const float* Pg = p.P + (size_t)b0 * p.K * p.M;
-        if (MV == 1 && p.M == 1 && (p.K & 3) == 0) {
-            const int n4 = nP >> 2;
-            const float4* s4 = reinterpret_cast<const float4*>(Pg);
-            float4* d4 = reinterpret_cast<float4*>(Ps);
-            for (int i = tid; i < n4; i += kThreads) d4[i] = s4[i];
-            for (int i = (n4 << 2) + tid; i < nP; i += kThreads) Ps[i] = Pg[i];
-        } else {
-            for (int i = tid; i < nP * MV; i += kThreads) {
-                const int e = i / MV, mm = i - e * MV;
-                const int m = m0 + mm;
-                Ps[i] = (m < p.M) ? Pg[(size_t)e * p.M + m] : 0.0f;
-            }
+// Copies n floats (n % 4 == 0, 16-byte aligned) global -> LDS, batched like stage_to_lds.
+__device__ __forceinline__ void copy_to_lds4(const float* __restrict__ src, int n, float* dst) {
+    const int tid = threadIdx.x;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    const int n4 = n >> 2;
+    for (int i0 = 0; i0 < n4; i0 += kThreads * kStageBatch) {
+        float4 v[kStageBatch];
+#pragma unroll
+        for (int j = 0; j < kStageBatch; ++j) v[j] = s4[min(i0 + j * kThreads + tid, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < kStageBatch; ++j) {
+            const int i = i0 + j * kThreads + tid;
+            if (i < n4) d4[i] = v[j];
         }
+    }
+}
+
+// ---- kernel 1 (dx): P[b][a][m] = D[a] . X[b*B : b*B+B, m] (the reference's Dx precompute)
+// and Y = 0 (the gathers accumulate into Y). Visibility to the gather kernel comes from the
+// dispatch boundary.
+__global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
+    extern __shared__ float smem[];
+    const int wg = blockIdx.x;
+    int g = 0;
+    while (g + 1 < p.G && wg >= p.m[g + 1].dx_base) ++g;
+    const MatDesc& d = p.m[g];
+    const int u = wg - d.dx_base;
+    const int tid = threadIdx.x;
+    const int M = p.M;
+    {
+        const size_t ytot = (size_t)d.R * M;
+        const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
+        const size_t ye = min(ytot, (size_t)(u + 1) * yper);
+        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) d.y[i] = 0.0f;
+    }
+    if (d.blen == 64) {
+        // 16 lanes per atom: lane l holds D[a][4l .. 4l+3] (one coalesced 16-byte load; a
+        // wave reads 4 whole rows). The x range of this workgroup is staged in LDS in one
+        // coalesced pass; per (block, column) each lane does 4 FMAs against its 4 x values
+        // and a 4-step DPP butterfly sums the 16 lanes.
+        const int l16 = tid & 15;
+        const int na16 = (d.K + 15) / 16;
+        const int ag = u % na16, bg = u / na16;
+        const int a = ag * 16 + (tid >> 4);
+        const int b0 = bg * d.PB;
+        const int nb = min(d.PB, d.NB - b0);
+        const bool live = a < d.K;
+        float* xs = smem;  // [bb][t][m], nb * 64 * M floats (x rows are contiguous)
+        const size_t xbase = (size_t)b0 * 64 * M;
+        const int nx = nb * 64 * M;
+        if (p.x_f16)
+            stage_to_lds(static_cast<const _Float16*>(d.x) + xbase, nx, xs);
+        else
+            stage_to_lds(static_cast<const float*>(d.x) + xbase, nx, xs);
+        float4 dv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) dv = reinterpret_cast<const float4*>(d.dict + (size_t)a * 64)[l16];
+        float* const Pout = d.P + (size_t)b0 * d.K * M + (size_t)a * M;  // + bb*K*M + m
+        const size_t pstride = (size_t)d.K * M;
         __syncthreads();
-
-        // ---- 3. gather from LDS
-        float acc[MAXIT][MV];
+        int bb = 0;
+        if (M == 1) {
+            // four independent (block) dot products per step so the DPP chains interleave
+            for (; bb + 4 <= nb; bb += 4) {
+                float sum[4];
 #pragma unroll
-        for (int i = 0; i < MAXIT; ++i)
+                for (int q = 0; q < 4; ++q) {
+                    const float4 xv =
+                        *reinterpret_cast<const float4*>(xs + (bb + q) * 64 + 4 * l16);
+                    float t = dv.x * xv.x;
+                    t = fmaf(dv.y, xv.y, t);
+                    t = fmaf(dv.z, xv.z, t);
+                    sum[q] = fmaf(dv.w, xv.w, t);
+                }
 #pragma unroll
-            for (int mm = 0; mm < MV; ++mm) acc[i][mm] = 0.0f;
+                for (int q = 0; q < 4; ++q) sum[q] = row16_sum(sum[q]);
+                if (live && l16 == 0) {
 #pragma unroll
-        for (int i = 0; i < MAXIT; ++i) {
-            const int pi = tid + i * kThreads;
-            if (pi < npairs) {
-                const int bb = pi % nbc;
-                const float* Pb = Ps + (size_t)bb * p.K * MV;
-                if constexpr (SLOTS > 0) {
-#pragma unroll
-                    for (int q = 0; q < NV; ++q) {
-                        const uint32_t w4[4] = {wv[i][q].x, wv[i][q].y, wv[i][q].z, wv[i][q].w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const uint32_t w = w4[e];
-                            const float cf = sg[q * 4 + e] * csdr::h2f(w >> 16);
-                            const float* pv = Pb + (size_t)(w & 0x7FFFu) * MV;
-                            if constexpr (MV == 1) {
-                                acc[i][0] = fmaf(cf, pv[0], acc[i][0]);
-                            } else {
-                                const float4 v = *reinterpret_cast<const float4*>(pv);
-                                acc[i][0] = fmaf(cf, v.x, acc[i][0]);
-                                acc[i][1] = fmaf(cf, v.y, acc[i][1]);
-                                acc[i][2] = fmaf(cf, v.z, acc[i][2]);
-                                acc[i][3] = fmaf(cf, v.w, acc[i][3]);
-                            }
-                        }
-                    }
-                } else {
-                    const uint32_t* src = cb + (size_t)pi * slots;
-                    for (int s = 0; s < slots; ++s) {
-                        const uint32_t w = src[s];
-                        const float cf = p.slot_gamma[s] * csdr::h2f(w >> 16);
-                        const float* pv = Pb + (size_t)(w & 0x7FFFu) * MV;
-#pragma unroll
-                        for (int mm = 0; mm < MV; ++mm) acc[i][mm] = fmaf(cf, pv[mm], acc[i][mm]);
-                    }
+                    for (int q = 0; q < 4; ++q) Pout[(bb + q) * pstride] = sum[q];
                 }
             }
         }
+        for (; bb < nb; ++bb) {
+            for (int m = 0; m < M; ++m) {
+                float4 xv;
+                if (M == 1) {
+                    xv = *reinterpret_cast<const float4*>(xs + bb * 64 + 4 * l16);
+                } else {
+                    const float* xp = xs + ((size_t)bb * 64 + 4 * l16) * M + m;
+                    xv = make_float4(xp[0], xp[M], xp[2 * M], xp[3 * M]);
+                }
+                float sum = dv.x * xv.x;
+                sum = fmaf(dv.y, xv.y, sum);
+                sum = fmaf(dv.z, xv.z, sum);
+                sum = fmaf(dv.w, xv.w, sum);
+                sum = row16_sum(sum);
+                if (live && l16 == 0) Pout[bb * pstride + m] = sum;
+            }
+        }
+    } else {
+        // any block length: one wave per (b, a, group of 8 columns), lane-strided dot
+        const int lane = tid & 63;
+        const int mg = (M + 7) / 8;
+        const long long item = (long long)u * (kThreads / 64) + (tid >> 6);
+        if (item < (long long)d.NB * d.K * mg) {
+            const int gi = (int)(item % mg);
+            const long long ba = item / mg;
+            const int b = (int)(ba / d.K), a = (int)(ba % d.K);
+            const int m0 = gi * 8, nm = min(8, M - m0);
+            float acc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+            const float* drow = d.dict + (size_t)a * d.blen;
+            for (int t = lane; t < d.blen; t += 64) {
+                const float dv = drow[t];
+                const size_t xo = ((size_t)b * d.blen + t) * M + m0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j < nm) acc[j] = fmaf(dv, xload(d.x, p.x_f16, xo + j), acc[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = csdr::wave_sum(acc[j]);
+            if (lane == 0)
+                for (int j = 0; j < nm; ++j) d.P[((size_t)b * d.K + a) * M + m0 + j] = acc[j];
+        }
+    }
+}
 
-        // ---- 4. per-row reduction over the chunk's blocks (block order)
+// Finds this gather workgroup's matrix and (chunk, split); false for padding slots.
+// Workgroups of one chunk are numbered to share an XCD (dispatch is round-robin over the
+// 8 XCDs), so that chunk's P slice is fetched into one L2 only.
+__device__ __forceinline__ bool gather_slot(const Params& p, int& g, int& c, int& sidx) {
+    const int wg = blockIdx.x;
+    g = -1;
+    for (int i = 0; i < p.G; ++i)
+        if (wg >= p.m[i].g_base && wg < p.m[i].g_base + p.m[i].g_count) g = i;
+    if (g < 0) return false;
+    const MatDesc& d = p.m[g];
+    const int u = wg - d.g_base;
+    const int j = u >> 3;
+    const int cl = j / d.splits;
+    sidx = j - cl * d.splits;
+    c = cl * 8 + (u & 7);
+    return c < d.nchunks;
+}
+
+__device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, int r, int m) {
+    float s = 0.0f;
+    const float* e = d.edge + (size_t)r * d.Ce;
+    for (int cc = 0; cc < d.Ce; ++cc)
+        s = fmaf(e[cc], xload(d.x, p.x_f16, (size_t)(d.C_full + cc) * p.M + m), s);
+    return s;
+}
+
+// ---- kernel 2, M == 1: persistent gather. Workgroup = (chunk, row range). It stages the
+// chunk's P slice (nbc * K floats) in LDS once, then walks its rows in units of
+// 256 * PPT "pieces" (4 code words = 16 bytes each; every load instruction of a wave reads
+// 1 KiB contiguous) with kDepth units of loads in flight, gathers P from LDS, sums each
+// row's pieces and adds the row total into Y (device-scope float atomics: other chunks of
+// the row run elsewhere).
+template <int SLOTS, int PPT>
+__device__ __forceinline__ void load_unit(u32x4 (&buf)[PPT], const uint32_t* base, int npieces) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(base);
 #pragma unroll
-        for (int i = 0; i < MAXIT; ++i) {
-            const int pi = tid + i * kThreads;
-            if (pi < npairs)
+    for (int j = 0; j < PPT; ++j) {
+        const int q = threadIdx.x + j * kThreads;
+        buf[j] = __builtin_nontemporal_load(src + min(q, npieces - 1));
+    }
+}
+
+template <int SLOTS, int PPT>
+__device__ __forceinline__ void process_unit(const Params& p, const MatDesc& d,
+                                             const u32x4 (&buf)[PPT], const float* Ps,
+                                             float* part, int nbc, int row0, int nrows,
+                                             bool last_chunk) {
+    constexpr int PPP = SLOTS / 4;  // pieces per (row, block) pair
+    const int ppr = nbc * PPP;       // pieces per row
+    const int npieces = nrows * ppr;
+    const int tid = threadIdx.x;
 #pragma unroll
-                for (int mm = 0; mm < MV; ++mm) part[pi * MV + mm] = acc[i][mm];
+    for (int j = 0; j < PPT; ++j) {
+        const int q = tid + j * kThreads;
+        if (q < npieces) {
+            const int pr = q % ppr;
+            const int bb = pr / PPP;
+            const int h = pr - bb * PPP;  // which 4 slots of the pair
+            const float* Pb = Ps + (size_t)bb * d.K;
+            const uint32_t w4[4] = {buf[j].x, buf[j].y, buf[j].z, buf[j].w};
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float gm = d.sgam[e];
+#pragma unroll
+                for (int hh = 1; hh < PPP; ++hh)
+                    if (h == hh) gm = d.sgam[hh * 4 + e];
+                const float cf = gm * csdr::h2f(w4[e] >> 16);
+                acc = fmaf(cf, Pb[w4[e] & 0x7FFFu], acc);
+            }
+            part[q] = acc;
+        }
+    }
+    __syncthreads();
+    for (int rr = tid; rr < nrows; rr += kThreads) {
+        float sum = 0.0f;
+        for (int k = 0; k < ppr; ++k) sum += part[rr * ppr + k];
+        const int r = row0 + rr;
+        if (last_chunk && d.Ce > 0) sum += edge_term(p, d, r, 0);
+        __hip_atomic_fetch_add(d.y + r, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+}
+
+template <int SLOTS, int PPT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void gather1_kernel(Params p) {
+    extern __shared__ float smem[];
+    int g, c, sidx;
+    if (!gather_slot(p, g, c, sidx)) return;
+    const MatDesc& d = p.m[g];
+    const int b0 = c * d.NBc;
+    const int nbc = min(d.NBc, d.NB - b0);
+    const int rbeg = sidx * d.rows_per_wg;
+    const int rend = min(d.R, rbeg + d.rows_per_wg);
+    if (rbeg >= rend) return;
+    constexpr int PPP = SLOTS / 4;
+    const int ppr = nbc * PPP;
+    const int rows_unit = max(1, (kThreads * PPT) / ppr);
+    const int nunits = (rend - rbeg + rows_unit - 1) / rows_unit;
+    // codes of rows [rbeg, rend) of chunk c are one contiguous run
+    const uint32_t* run = d.codes + (size_t)c * d.NBc * d.R * SLOTS + (size_t)rbeg * nbc * SLOTS;
+    auto unit_base = [&](int k) { return run + (size_t)k * rows_unit * ppr * 4; };
+    auto unit_rows = [&](int k) { return min(rows_unit, rend - rbeg - k * rows_unit); };
+    const bool last_chunk = (c == d.nchunks - 1);
+
+    u32x4 b0v[PPT], b1v[PPT], b2v[PPT];
+    load_unit<SLOTS, PPT>(b0v, unit_base(0), unit_rows(0) * ppr);
+    if (nunits > 1) load_unit<SLOTS, PPT>(b1v, unit_base(1), unit_rows(1) * ppr);
+
+    float* Ps = smem;                         // nbc * K floats
+    float* part = smem + (size_t)d.NBc * d.K; // kThreads * PPT floats
+    const float* Pg = d.P + (size_t)b0 * d.K;
+    if ((d.K & 3) == 0)
+        copy_to_lds4(Pg, nbc * d.K, Ps);
+    else
+        stage_to_lds(Pg, nbc * d.K, Ps);
+    __syncthreads();
+
+    for (int k = 0; k < nunits; k += kDepth) {
+        if (k + 2 < nunits) load_unit<SLOTS, PPT>(b2v, unit_base(k + 2), unit_rows(k + 2) * ppr);
+        process_unit<SLOTS, PPT>(p, d, b0v, Ps, part, nbc, rbeg + k * rows_unit, unit_rows(k),
+                                 last_chunk);
+        if (k + 1 >= nunits) break;
+        if (k + 3 < nunits) load_unit<SLOTS, PPT>(b0v, unit_base(k + 3), unit_rows(k + 3) * ppr);
+        process_unit<SLOTS, PPT>(p, d, b1v, Ps, part, nbc, rbeg + (k + 1) * rows_unit,
+                                 unit_rows(k + 1), last_chunk);
+        if (k + 2 >= nunits) break;
+        if (k + 4 < nunits) load_unit<SLOTS, PPT>(b1v, unit_base(k + 4), unit_rows(k + 4) * ppr);
+        process_unit<SLOTS, PPT>(p, d, b2v, Ps, part, nbc, rbeg + (k + 2) * rows_unit,
+                                 unit_rows(k + 2), last_chunk);
+    }
+}
+
+// ---- kernel 2, any M / any slot count: workgroup = (chunk, row tile of Rt rows); the
+// chunk's P slice is staged MV columns at a time, code words are read per pair.
+template <int MV>
+__global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
+    extern __shared__ float smem[];
+    int g, c, sidx;
+    if (!gather_slot(p, g, c, sidx)) return;
+    const MatDesc& d = p.m[g];
+    const int tid = threadIdx.x;
+    const int M = p.M;
+    const int b0 = c * d.NBc;
+    const int nbc = min(d.NBc, d.NB - b0);
+    const int r0 = sidx * d.Rt;
+    const int nr = min(d.Rt, d.R - r0);
+    if (nr <= 0) return;
+    const int npairs = nr * nbc;
+    const uint32_t* cb =
+        d.codes + (size_t)c * d.NBc * d.R * d.slots + (size_t)r0 * nbc * d.slots;
+    float* Ps = smem;                              // nbc * K * MV
+    float* part = smem + (size_t)d.NBc * d.K * MV; // Rt * NBc * MV
+    const bool last_chunk = (c == d.nchunks - 1);
+    for (int z = 0; z < p.MVz; ++z) {
+        const int m0 = z * MV;
+        if (z > 0) __syncthreads();
+        const float* Pg = d.P + (size_t)b0 * d.K * M;
+        for (int i = tid; i < nbc * d.K * MV; i += kThreads) {
+            const int e = i / MV, mm = i - e * MV;
+            const int m = m0 + mm;
+            Ps[i] = (m < M) ? Pg[(size_t)e * M + m] : 0.0f;
+        }
+        __syncthreads();
+        for (int pi = tid; pi < npairs; pi += kThreads) {
+            const int bb = pi % nbc;
+            const float* Pb = Ps + (size_t)bb * d.K * MV;
+            const uint32_t* src = cb + (size_t)pi * d.slots;
+            float acc[MV];
+#pragma unroll
+            for (int mm = 0; mm < MV; ++mm) acc[mm] = 0.0f;
+            for (int sl = 0; sl < d.slots; ++sl) {
+                const uint32_t w = src[sl];
+                const float cf = d.slot_gamma[sl] * csdr::h2f(w >> 16);
+                const float* pv = Pb + (size_t)(w & 0x7FFFu) * MV;
+#pragma unroll
+                for (int mm = 0; mm < MV; ++mm) acc[mm] = fmaf(cf, pv[mm], acc[mm]);
+            }
+#pragma unroll
+            for (int mm = 0; mm < MV; ++mm) part[pi * MV + mm] = acc[mm];
         }
         __syncthreads();
         for (int t = tid; t < nr * MV; t += kThreads) {
             const int rr = t / MV, mm = t - rr * MV;
             const int m = m0 + mm;
-            if (m >= p.M) continue;
-            float s = 0.0f;
-            for (int bb = 0; bb < nbc; ++bb) s += part[(rr * nbc + bb) * MV + mm];
+            if (m >= M) continue;
+            float sum = 0.0f;
+            for (int bb = 0; bb < nbc; ++bb) sum += part[(rr * nbc + bb) * MV + mm];
             const int r = r0 + rr;
-            if (direct) {
-                if (p.Ce > 0)
-                    s += p.x_f16 ? edge_dot<_Float16>(p, r, m) : edge_dot<float>(p, r, m);
-                p.y[(size_t)r * p.M + m] = s;
-            } else {
-                p.ypart[((size_t)c * p.R + r) * p.M + m] = s;
-            }
+            if (last_chunk && d.Ce > 0) sum += edge_term(p, d, r, m);
+            __hip_atomic_fetch_add(d.y + (size_t)r * M + m, sum, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
-    }
-    if (direct) return;
-
-    // ---- 5. last workgroup of this row tile sums the chunk partials in chunk order
-    __shared__ int s_last;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned int old = atomicInc(&p.counters[rt], (unsigned int)(p.nchunks - 1));
-        s_last = (old == (unsigned int)(p.nchunks - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int t = tid; t < nr * p.M; t += kThreads) {
-        const int rr = t / p.M, m = t - rr * p.M;
-        const int r = r0 + rr;
-        float s = 0.0f;
-        for (int cc = 0; cc < p.nchunks; ++cc)
-            s += __builtin_nontemporal_load(&p.ypart[((size_t)cc * p.R + r) * p.M + m]);
-        if (p.Ce > 0) s += p.x_f16 ? edge_dot<_Float16>(p, r, m) : edge_dot<float>(p, r, m);
-        p.y[(size_t)r * p.M + m] = s;
     }
 }
 
@@ -486,6 +628,7 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     std::vector<float> slot_gamma(std::max<uint32_t>(s->slots, 1), 0.0f);
     for (uint32_t j = 0; j < s->slots; ++j)
         std::memcpy(&slot_gamma[j], buf + off_gamma + 4u * (j / s->k), 4);
+    for (uint32_t j = 0; j < s->slots && j < 32; ++j) s->h_slot_gamma[j] = slot_gamma[j];
 
     const size_t b_dict = (size_t)s->K * tile_dim * 4;
     const size_t b_codes = n_codes * 4;
@@ -518,56 +661,184 @@ void release(csdr_hsdb* s) {
     delete s;
 }
 
-struct WsLayout {
-    size_t counters, P, ypart, total;
-};
+constexpr size_t kWsHeader = 256;  // reserved
 
-WsLayout ws_layout(const csdr_hsdb* s, int M) {
-    WsLayout w{};
-    const size_t max_row_tiles = (s->R + 63) / 64;
-    w.counters = 0;
-    w.P = csdr::align_up(max_row_tiles * 4, 256);
-    w.ypart = w.P + csdr::align_up((size_t)s->NB * s->K * M * 4, 256);
-    w.total = w.ypart + csdr::align_up((size_t)s->nchunks * s->R * M * 4, 256);
-    return w;
+// Launch-shape defaults, overridable for tuning sweeps through the environment
+// (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_GATHER_UNITS_PER_WG).
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    const int x = std::atoi(v);
+    return x > 0 ? x : dflt;
 }
 
-template <int MV, int MAXIT>
-hipError_t launch_gather_mv(const GatherParams& p, int slots, int grid, size_t lds,
-                            hipStream_t st) {
+// Block columns per dx workgroup (block length 64): about `work` (block, column) dot
+// products per 16-lane group.
+inline int producer_blocks(int M) {
+    const int work = env_int("CSDR_DX_WORK", 16);
+    return M >= work ? 1 : work / M;
+}
+
+size_t p_bytes(const csdr_hsdb* s, int M) {
+    return csdr::align_up((size_t)s->NB * s->K * M * 4, 256);
+}
+
+size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
+    size_t t = kWsHeader;
+    for (int i = 0; i < n; ++i) t += p_bytes(segs[i], M);
+    return t;
+}
+
+template <int PPT>
+void launch_gather1(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
     switch (slots) {
         case 4:
-            gather_kernel<MV, MAXIT, 4><<<grid, kThreads, lds, st>>>(p);
+            gather1_kernel<4, PPT><<<grid, kThreads, lds, st>>>(p);
             break;
         case 8:
-            gather_kernel<MV, MAXIT, 8><<<grid, kThreads, lds, st>>>(p);
-            break;
-        case 16:
-            gather_kernel<MV, MAXIT, 16><<<grid, kThreads, lds, st>>>(p);
-            break;
-        case 24:
-            gather_kernel<MV, MAXIT, 24><<<grid, kThreads, lds, st>>>(p);
+            gather1_kernel<8, PPT><<<grid, kThreads, lds, st>>>(p);
             break;
         default:
-            gather_kernel<MV, MAXIT, 0><<<grid, kThreads, lds, st>>>(p);
+            gather1_kernel<16, PPT><<<grid, kThreads, lds, st>>>(p);
             break;
     }
-    return hipGetLastError();
 }
 
-template <int MV>
-hipError_t launch_gather(const GatherParams& p, int maxit, int slots, int grid, size_t lds,
-                         hipStream_t st) {
-    switch (maxit) {
-        case 1:
-            return launch_gather_mv<MV, 1>(p, slots, grid, lds, st);
-        case 2:
-            return launch_gather_mv<MV, 2>(p, slots, grid, lds, st);
-        case 4:
-            return launch_gather_mv<MV, 4>(p, slots, grid, lds, st);
-        default:
-            return launch_gather_mv<MV, 8>(p, slots, grid, lds, st);
+constexpr int kPhaseDx = 1;
+constexpr int kPhaseGather = 2;
+
+int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
+                 float* const* ys, void* workspace, size_t workspace_bytes, hipStream_t st,
+                 int phases = kPhaseDx | kPhaseGather) {
+    if (n <= 0 || n > kMaxGroup || !segs || !xs || !ys || M <= 0)
+        return set_error(CSDR_E_INVALID, "hsdb_matmul: bad argument (group of 1.." +
+                                             std::to_string(kMaxGroup) + ")");
+    if (x_dtype != CSDR_F32 && x_dtype != CSDR_F16)
+        return set_error(CSDR_E_INVALID, "hsdb_matmul: x_dtype must be CSDR_F32 or CSDR_F16");
+    const size_t need = group_ws_bytes(n, segs, M);
+    if (!workspace || workspace_bytes < need)
+        return set_error(CSDR_E_WORKSPACE,
+                         "hsdb_matmul: workspace needs " + std::to_string(need) + " bytes");
+    Params p{};
+    p.G = n;
+    p.M = M;
+    const int MV = (M == 1) ? 1 : 4;
+    p.MVz = (M + MV - 1) / MV;
+    p.x_f16 = (x_dtype == CSDR_F16);
+    char* ws = static_cast<char*>(workspace);
+    size_t off = kWsHeader;
+    // the register-resident M == 1 gather needs every matrix at 4, 8 or 16 slots (16-byte
+    // pieces) and the same count across the group; anything else takes the generic gather
+    int slots = -1;
+    bool fast = (M == 1);
+    int ndx = 0;
+    size_t lds_dx = 0, lds_g = 0;
+    long long total_units = 0;
+    for (int i = 0; i < n; ++i) {
+        const csdr_hsdb* s = segs[i];
+        if (!s || !xs[i] || !ys[i]) return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
+        if (s->tile_rows != 1)
+            return set_error(CSDR_E_FORMAT,
+                             "hsdb_matmul: fused matmul requires tile_rows == 1; use "
+                             "csdr_hsdb_decompress + a dense matmul for 2-D tiles");
+        if (s->NB == 0)
+            return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: matrix narrower than one block");
+        if (!(s->slots == 4 || s->slots == 8 || s->slots == 16)) fast = false;
+        if (slots >= 0 && (int)s->slots != slots) fast = false;
+        slots = (int)s->slots;
+        MatDesc& d = p.m[i];
+        d.codes = s->d_codes;
+        d.dict = s->d_dict;
+        d.slot_gamma = s->d_slot_gamma;
+        for (uint32_t q = 0; q < s->slots && q < (uint32_t)kMaxSlotsArg; ++q)
+            d.sgam[q] = s->h_slot_gamma[q];
+        d.edge = s->d_edge;
+        d.x = xs[i];
+        d.y = ys[i];
+        d.P = reinterpret_cast<float*>(ws + off);
+        off += p_bytes(s, M);
+        d.R = (int)s->R;
+        d.K = (int)s->K;
+        d.NB = (int)s->NB;
+        d.NBc = (int)s->NBc;
+        d.nchunks = (int)s->nchunks;
+        d.slots = (int)s->slots;
+        d.blen = (int)s->tile_cols;
+        d.Ce = (int)s->Ce;
+        d.C_full = (int)s->C_full;
+        d.PB = producer_blocks(M);
+        if (d.blen == 64) {
+            d.dx_count = ((d.K + 15) / 16) * ((d.NB + d.PB - 1) / d.PB);
+            lds_dx = std::max(lds_dx, (size_t)d.PB * 64 * M * 4);
+        } else {
+            const long long items = (long long)d.NB * d.K * ((M + 7) / 8);
+            d.dx_count = (int)((items + kThreads / 64 - 1) / (kThreads / 64));
+        }
+        d.dx_base = ndx;
+        ndx += d.dx_count;
     }
+    if (fast) {
+        // M == 1: pieces of 16 bytes; PPT pieces per thread per unit
+        for (int i = 0; i < n; ++i) {
+            const MatDesc& d = p.m[i];
+            const long long pieces = (long long)d.R * d.NB * (slots / 4);
+            total_units += (pieces + kThreads * 2 - 1) / (kThreads * 2);
+        }
+    }
+    int dev = 0, ncu = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            v > 0)
+            ncu = v;
+    }
+    const int PPT = 2;
+    int base = 0;
+    for (int i = 0; i < n; ++i) {
+        MatDesc& d = p.m[i];
+        const int nchunks8 = (d.nchunks + 7) / 8 * 8;
+        if (fast) {
+            // enough workgroups to fill every CU kGatherWGsPerCU deep, and >= 2 units each
+            const long long target =
+                (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGatherWGsPerCU);
+            const int ppr_full = d.NBc * (slots / 4);
+            const int rows_unit = std::max(1, (kThreads * PPT) / ppr_full);
+            const long long units_chunk = (d.R + rows_unit - 1) / rows_unit;
+            const long long units = units_chunk * d.nchunks;
+            long long wgs_i = std::max<long long>(1, target * units / std::max(1LL, total_units));
+            long long per_wg = std::max<long long>(env_int("CSDR_GATHER_UNITS_PER_WG", 4),
+                                                   (units + wgs_i - 1) / wgs_i);
+            d.splits = (int)((units_chunk + per_wg - 1) / per_wg);
+            d.rows_per_wg = (int)(((long long)d.R + d.splits - 1) / d.splits);
+            d.rows_per_wg = (d.rows_per_wg + rows_unit - 1) / rows_unit * rows_unit;
+            d.splits = (d.R + d.rows_per_wg - 1) / d.rows_per_wg;
+            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + (size_t)kThreads * PPT) * 4);
+        } else {
+            d.Rt = MV == 1 ? 256 : 64;
+            while (d.Rt > 16 && (size_t)d.Rt * d.NBc > 2048) d.Rt /= 2;
+            d.splits = (d.R + d.Rt - 1) / d.Rt;
+            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K * MV + (size_t)d.Rt * d.NBc * MV) * 4);
+        }
+        d.g_base = base;
+        d.g_count = nchunks8 * d.splits;
+        base += d.g_count;
+    }
+    if (lds_g > 160 * 1024 || lds_dx > 160 * 1024)
+        return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: dictionary too large for LDS");
+    if (phases & kPhaseDx) {
+        dx_kernel<<<ndx, kThreads, lds_dx, st>>>(p);
+        CSDR_LAUNCH_CHECK("hsdb dx");
+    }
+    if (phases & kPhaseGather) {
+        if (fast)
+            launch_gather1<PPT>(p, slots, base, lds_g, st);
+        else if (MV == 1)
+            gatherm_kernel<1><<<base, kThreads, lds_g, st>>>(p);
+        else
+            gatherm_kernel<4><<<base, kThreads, lds_g, st>>>(p);
+        CSDR_LAUNCH_CHECK("hsdb gather");
+    }
+    return CSDR_OK;
 }
 
 }  // namespace
@@ -625,120 +896,41 @@ CSDR_API int csdr_hsdb_get_info(const csdr_hsdb* s, csdr_hsdb_info* info) {
 
 CSDR_API size_t csdr_hsdb_workspace_bytes(const csdr_hsdb* s, int M) {
     if (!s || M <= 0) return 0;
-    return ws_layout(s, M).total;
+    return group_ws_bytes(1, &s, M);
 }
 
-namespace {
-
-int check_matmul_args(const csdr_hsdb* s, const void* x, int x_dtype, int M, void* workspace,
-                      size_t workspace_bytes, const char* who) {
-    if (!s || !x || M <= 0) return set_error(CSDR_E_INVALID, std::string(who) + ": bad argument");
-    if (s->tile_rows != 1)
-        return set_error(CSDR_E_FORMAT,
-                         std::string(who) + ": fused matmul requires tile_rows == 1; use "
-                                            "csdr_hsdb_decompress + a dense matmul for 2-D tiles");
-    if (x_dtype != CSDR_F32 && x_dtype != CSDR_F16)
-        return set_error(CSDR_E_INVALID, std::string(who) + ": x_dtype must be CSDR_F32 or CSDR_F16");
-    if (s->NB == 0)
-        return set_error(CSDR_E_UNSUPPORTED, std::string(who) + ": matrix narrower than one block");
-    const WsLayout wl = ws_layout(s, M);
-    if (!workspace || workspace_bytes < wl.total)
-        return set_error(CSDR_E_WORKSPACE, std::string(who) + ": workspace needs " +
-                                               std::to_string(wl.total) + " bytes");
-    return CSDR_OK;
-}
-
-}  // namespace
-
-CSDR_API int csdr_hsdb_dx(const csdr_hsdb* s, const void* x, int x_dtype, int M, void* workspace,
-                          size_t workspace_bytes, void* hip_stream) {
-    int rc = check_matmul_args(s, x, x_dtype, M, workspace, workspace_bytes, "hsdb_dx");
-    if (rc) return rc;
-    const WsLayout wl = ws_layout(s, M);
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    float* P = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.P);
-    if (s->tile_cols == 64) {
-        dim3 grid((s->K + kThreads - 1) / kThreads, (s->NB + kDxBlocksPerWG - 1) / kDxBlocksPerWG,
-                  M);
-        if (x_dtype == CSDR_F16)
-            dx_b64_kernel<_Float16><<<grid, kThreads, 0, st>>>(
-                s->d_dict, static_cast<const _Float16*>(x), s->K, s->NB, M, P);
-        else
-            dx_b64_kernel<float><<<grid, kThreads, 0, st>>>(
-                s->d_dict, static_cast<const float*>(x), s->K, s->NB, M, P);
-    } else {
-        const long long waves = (long long)s->NB * s->K * ((M + 7) / 8);
-        const int grid = (int)((waves * 64 + kThreads - 1) / kThreads);
-        if (x_dtype == CSDR_F16)
-            dx_generic_kernel<_Float16><<<grid, kThreads, 0, st>>>(
-                s->d_dict, static_cast<const _Float16*>(x), s->K, s->NB, s->tile_cols, M, P);
-        else
-            dx_generic_kernel<float><<<grid, kThreads, 0, st>>>(
-                s->d_dict, static_cast<const float*>(x), s->K, s->NB, s->tile_cols, M, P);
-    }
-    CSDR_LAUNCH_CHECK("hsdb dx");
-    return CSDR_OK;
-}
-
-CSDR_API int csdr_hsdb_gather(const csdr_hsdb* s, const void* x, int x_dtype, int M, float* y,
-                              void* workspace, size_t workspace_bytes, void* hip_stream) {
-    int rc = check_matmul_args(s, x, x_dtype, M, workspace, workspace_bytes, "hsdb_gather");
-    if (rc) return rc;
-    if (!y) return set_error(CSDR_E_INVALID, "hsdb_gather: null y");
-    const WsLayout wl = ws_layout(s, M);
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    char* ws = static_cast<char*>(workspace);
-    GatherParams p{};
-    p.codes = s->d_codes;
-    p.P = reinterpret_cast<float*>(ws + wl.P);
-    p.slot_gamma = s->d_slot_gamma;
-    p.edge = s->d_edge;
-    p.x = x;
-    p.y = y;
-    p.ypart = reinterpret_cast<float*>(ws + wl.ypart);
-    p.counters = reinterpret_cast<unsigned int*>(ws + wl.counters);
-    p.x_f16 = (x_dtype == CSDR_F16);
-    p.R = (int)s->R;
-    p.K = (int)s->K;
-    p.NB = (int)s->NB;
-    p.NBc = (int)s->NBc;
-    p.nchunks = (int)s->nchunks;
-    p.slots = (int)s->slots;
-    p.M = M;
-    p.Ce = (int)s->Ce;
-    p.C_full = (int)s->C_full;
-    const int MV = (M == 1) ? 1 : 4;
-    p.MVz = (M + MV - 1) / MV;
-    int Rt = gather_rows_per_wg(MV);
-    int maxit = (Rt * (int)s->NBc + kThreads - 1) / kThreads;
-    while (maxit > 8) {
-        Rt /= 2;
-        maxit = (Rt * (int)s->NBc + kThreads - 1) / kThreads;
-    }
-    int mi = 1;
-    while (mi < maxit) mi <<= 1;
-    p.Rt = Rt;
-    p.nrt = ((int)s->R + Rt - 1) / Rt;
-    const size_t lds = ((size_t)s->NBc * s->K * MV + (size_t)Rt * s->NBc * MV) * 4;
-    if (lds > 160 * 1024)
-        return set_error(CSDR_E_UNSUPPORTED, "hsdb_gather: dictionary too large for LDS");
-    const int grid = 8 * ((p.nchunks + 7) / 8) * p.nrt;
-    const int slots_t = (s->slots == 4 || s->slots == 8 || s->slots == 16 || s->slots == 24)
-                            ? (int)s->slots
-                            : 0;
-    hipError_t e = (MV == 1) ? launch_gather<1>(p, mi, slots_t, grid, lds, st)
-                             : launch_gather<4>(p, mi, slots_t, grid, lds, st);
-    if (e != hipSuccess)
-        return set_error(CSDR_E_HIP, std::string("hsdb gather launch failed: ") +
-                                         hipGetErrorString(e));
-    return CSDR_OK;
+CSDR_API size_t csdr_hsdb_group_workspace_bytes(int n, const csdr_hsdb* const* segs, int M) {
+    if (n <= 0 || !segs || M <= 0) return 0;
+    for (int i = 0; i < n; ++i)
+        if (!segs[i]) return 0;
+    return group_ws_bytes(n, segs, M);
 }
 
 CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* s, const void* x, int x_dtype, int M, float* y,
                               void* workspace, size_t workspace_bytes, void* hip_stream) {
-    int rc = csdr_hsdb_dx(s, x, x_dtype, M, workspace, workspace_bytes, hip_stream);
-    if (rc) return rc;
-    return csdr_hsdb_gather(s, x, x_dtype, M, y, workspace, workspace_bytes, hip_stream);
+    return matmul_group(1, &s, &x, x_dtype, M, &y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream));
+}
+
+CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                    int x_dtype, int M, float* const* y, void* workspace,
+                                    size_t workspace_bytes, void* hip_stream) {
+    return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream));
+}
+
+CSDR_API int csdr_hsdb_dx_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                int x_dtype, int M, float* const* y, void* workspace,
+                                size_t workspace_bytes, void* hip_stream) {
+    return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream), kPhaseDx);
+}
+
+CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                    int x_dtype, int M, float* const* y, void* workspace,
+                                    size_t workspace_bytes, void* hip_stream) {
+    return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream), kPhaseGather);
 }
 
 CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* s, float* w, void* hip_stream) {

@@ -141,6 +141,36 @@ class HsdbSegment:
                 coef.cpu().numpy().view(np.uint16)[:n])
 
 
+def group_workspace(segs, M: int):
+    """Zero-filled device workspace for matmul_group over `segs` at batch M."""
+    torch = _torch()
+    arr = (C.c_void_p * len(segs))(*[s._h.value for s in segs])
+    n = int(_lib.load().csdr_hsdb_group_workspace_bytes(len(segs), arr, M))
+    return torch.zeros(n, dtype=torch.uint8, device="cuda")
+
+
+def matmul_group(segs, xs, ys=None, workspace=None, stream=None):
+    """Y_i = W_i . X_i for up to 8 segments in one launch (same M and dtype for all)."""
+    torch = _torch()
+    n = len(segs)
+    M = xs[0].shape[1] if xs[0].dim() == 2 else 1
+    dt = CSDR_F16 if xs[0].dtype == torch.float16 else CSDR_F32
+    for s, x in zip(segs, xs):
+        if x.shape[0] != s.cols or not x.is_contiguous() or not x.is_cuda:
+            raise ValueError("each x must be a contiguous device tensor with C rows")
+        if (x.shape[1] if x.dim() == 2 else 1) != M or x.dtype != xs[0].dtype:
+            raise ValueError("all x must share M and dtype")
+    if ys is None:
+        ys = [torch.empty((s.rows, M), dtype=torch.float32, device="cuda") for s in segs]
+    ws = workspace if workspace is not None else group_workspace(segs, M)
+    hs = (C.c_void_p * n)(*[s._h.value for s in segs])
+    xp = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
+    yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+    _check(_lib.load().csdr_hsdb_matmul_group(n, hs, xp, dt, M, yp, ws.data_ptr(), ws.numel(),
+                                              _stream_ptr(stream)))
+    return ys
+
+
 def matmul_row_major(stream: bytes, x: np.ndarray, batch: int) -> np.ndarray:
     """Drop-in for HierarchicalSDRStrategy::matmulRowMajor: host x (C x batch) row-major
     fp32 in, host Y (R x batch) fp32 out. Loads the stream per call like the reference;

@@ -95,8 +95,8 @@ CSDR_API int csdr_hsdb_load(const void* stream, size_t nbytes, void* hip_stream,
 CSDR_API int csdr_hsdb_free(csdr_hsdb* seg);
 CSDR_API int csdr_hsdb_get_info(const csdr_hsdb* seg, csdr_hsdb_info* info);
 
-/* Device workspace bytes csdr_hsdb_matmul needs for batch M. The workspace must be
- * zero-filled once before its first use; every completed call leaves it reusable. */
+/* Device workspace bytes csdr_hsdb_matmul needs for batch M (it holds P = D . X). Calls
+ * that share a workspace must be ordered (same stream); concurrent calls need their own. */
 CSDR_API size_t csdr_hsdb_workspace_bytes(const csdr_hsdb* seg, int M);
 
 /* Y = W . X with W never materialised. X: device, (C x M) row-major (feature-major, the
@@ -106,13 +106,25 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
                               float* y, void* workspace, size_t workspace_bytes,
                               void* hip_stream);
 
-/* The two phases of csdr_hsdb_matmul, callable separately with the same arguments and
- * workspace (the first writes P = D . X per block column into the workspace, the second
- * gathers it); csdr_hsdb_matmul is exactly dx followed by gather on the stream. */
-CSDR_API int csdr_hsdb_dx(const csdr_hsdb* seg, const void* x, int x_dtype, int M,
-                          void* workspace, size_t workspace_bytes, void* hip_stream);
-CSDR_API int csdr_hsdb_gather(const csdr_hsdb* seg, const void* x, int x_dtype, int M, float* y,
-                              void* workspace, size_t workspace_bytes, void* hip_stream);
+/* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
+ * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches:
+ * a dx launch (P = D . X per block column into the workspace, Y = 0) and a gather launch
+ * (Y += the coded rows gathered from P). The workspace is
+ * csdr_hsdb_group_workspace_bytes(n, segs, M) bytes. csdr_hsdb_matmul is the n = 1 case.
+ * Y rows are accumulated over block-column chunks with device-scope float atomics, so
+ * repeated calls agree to fp32 rounding, not bit for bit. */
+CSDR_API size_t csdr_hsdb_group_workspace_bytes(int n, const csdr_hsdb* const* segs, int M);
+CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                    int x_dtype, int M, float* const* y, void* workspace,
+                                    size_t workspace_bytes, void* hip_stream);
+/* The two launches of csdr_hsdb_matmul_group, separately (same arguments; dx must precede
+ * gather on the stream, with the same workspace and X). */
+CSDR_API int csdr_hsdb_dx_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                int x_dtype, int M, float* const* y, void* workspace,
+                                size_t workspace_bytes, void* hip_stream);
+CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                    int x_dtype, int M, float* const* y, void* workspace,
+                                    size_t workspace_bytes, void* hip_stream);
 
 /* Dense decode to device W (R x C fp32 row-major), bit-identical to the reference decode
  * order (stage-major slot accumulation with fused multiply-adds, then the edge strips). */
