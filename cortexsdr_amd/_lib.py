@@ -57,6 +57,23 @@ SIGNATURES = {
                                          C.c_int, C.POINTER(_vp), _vp, _sz, _vp]),
     "csdr_hsdb_decompress": (C.c_int, [_vp, _vp, _vp]),
     "csdr_hsdb_export_codes": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "csdr_q4k_linear": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
+                                  _vp]),
+    "csdr_q4k_dequant": (C.c_int, [_vp, _sz, C.c_int, _vp, _vp]),
+    "csdr_hsdb_matmul_group_ex": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
+                                            C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
+                                            _vp, _sz, _vp]),
+    "csdr_hsdb_decode_row": (C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+    "csdr_rms_norm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "csdr_silu_mul": (C.c_int, [_vp, _vp, _sz, _vp, _vp]),
+    "csdr_rope_kv": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
+                               C.c_float, _vp, _vp, C.c_int, _vp]),
+    "csdr_attn_decode_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    "csdr_attn_decode": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                   C.c_int, C.c_int, C.c_float, _vp, _vp, _sz, _vp]),
+    "csdr_select_workspace_bytes": (_sz, []),
+    "csdr_select_best": (C.c_int, [_vp, C.c_int, _vp, C.c_float, C.c_float, _vp, _vp, _vp,
+                                   _vp, _sz, _vp]),
 }
 
 

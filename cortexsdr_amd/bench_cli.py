@@ -1,0 +1,149 @@
+"""Bench CLI for the compressed-weight path: every BASELINE.json configuration on one GPU.
+
+    python -m cortexsdr_amd.bench_cli [--configs cfg1,cfg2,cfg3] [--steps 50] [--out f.json]
+
+The role of the reference's `cortexsdr_bench` suite runner (src/cortexsdr_bench.cpp:52-79,
+160-181: run each workload, collect times, write a summary JSON), for the device path:
+each workload is timed as `steps` calls captured in a HIP graph and replayed between two HIP
+events, inputs resident in HBM, over rotating weight copies larger than the 256 MiB
+Infinity Cache. Reported per workload: microseconds per call, algorithmic GB/s (compressed
+weights + dictionary + x + y, each once), the fraction of the 8 TB/s HBM peak and, for the
+batched cases, dense-equivalent TFLOP/s (2*R*C*M per call).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK = 8.0e12
+MALL = 256 * 1024 * 1024
+
+
+def _copies(nbytes: int, cap: int = 24) -> int:
+    return max(2, min(cap, math.ceil(3 * MALL / max(1, nbytes)) + 1))
+
+
+def time_graph(torch, fn, n_copies: int, steps: int) -> float:
+    """Microseconds per call of fn(i) (i = copy index), `steps` calls in one graph replay."""
+    for i in range(3):
+        fn(i % n_copies)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i % n_copies)
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(3):
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / steps)
+    return best
+
+
+def bench_hsdb(torch, R, Cc, K, s, M, xdtype, steps, seed=2):
+    from . import _lib, synth
+    from .hsdr import HsdbSegment, group_workspace
+
+    stream = synth.hsdb_layer(R, Cc, K, s, seed_dict=1, seed_codes=seed)
+    codes = R * (Cc // 64) * s * 4
+    ncp = _copies(codes)
+    segs = [HsdbSegment(stream) for _ in range(ncp)]
+    x = torch.from_numpy(synth.activations(Cc, M, seed=3, dtype=xdtype)).cuda()
+    y = torch.empty((R, M), dtype=torch.float32, device="cuda")
+    ws = group_workspace([segs[0]], M)
+    lib = _lib.load()
+    xt = 1 if xdtype == np.float16 else 0
+    xp = (C.c_void_p * 1)(x.data_ptr())
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    hs = [(C.c_void_p * 1)(sg._h.value) for sg in segs]
+
+    def fn(i):
+        sp = int(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.csdr_hsdb_matmul_group(1, hs[i], xp, xt, M, yp, ws.data_ptr(),
+                                              ws.numel(), sp))
+
+    us = time_graph(torch, fn, ncp, steps)
+    alg = codes + K * 64 * 4 + Cc * M * np.dtype(xdtype).itemsize + R * M * 4
+    for sg in segs:
+        sg.free()
+    return {"R": R, "C": Cc, "K": K, "nnz": s, "M": M, "us": round(us, 3),
+            "GBps": round(alg / us / 1e3, 1), "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4),
+            "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
+
+
+def bench_q4k(torch, R, Cc, M, steps, order=0):
+    from . import _lib, q4k, synth
+
+    blob = synth.q4k_matrix(R, Cc, seed=7)
+    ncp = _copies(len(blob))
+    ws = [q4k.upload(blob) for _ in range(ncp)]
+    x = torch.from_numpy(synth.activations(Cc, M, seed=11).T.copy().astype(np.float16)).cuda()
+    y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    lib = _lib.load()
+
+    def fn(i):
+        sp = int(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.csdr_q4k_linear(ws[i].data_ptr(), R, Cc, order, x.data_ptr(), 1, M,
+                                       y.data_ptr(), sp))
+
+    us = time_graph(torch, fn, ncp, steps)
+    alg = len(blob) + Cc * M * 2 + R * M * 4
+    return {"R": R, "C": Cc, "M": M, "us": round(us, 3), "GBps": round(alg / us / 1e3, 1),
+            "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4),
+            "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--configs", default="cfg1,cfg2,cfg3")
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--out", default=None)
+    args = ap.parse_args(argv)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench_cli: no HIP device", file=sys.stderr)
+        return 1
+    cfgs = set(args.configs.split(","))
+    res = {"device": torch.cuda.get_device_name(0), "steps": args.steps, "results": {}}
+    t0 = time.time()
+    if "cfg1" in cfgs:
+        res["results"]["cfg1"] = [bench_hsdb(torch, 4096, 4096, 512, 4, 1, np.float32,
+                                             args.steps)]
+    if "cfg2" in cfgs:
+        out = []
+        for (R, Cc) in ((4096, 11008), (11008, 4096)):
+            for M in (1, 16, 64, 256):
+                out.append(bench_hsdb(torch, R, Cc, 1024, 8, M, np.float16, args.steps))
+                print(json.dumps(out[-1]), flush=True)
+        res["results"]["cfg2"] = out
+    if "cfg3" in cfgs:
+        out = []
+        for (R, Cc) in ((4096, 4096), (4096, 14336)):
+            for M in (1, 32):
+                out.append(bench_q4k(torch, R, Cc, M, args.steps))
+                print(json.dumps(out[-1]), flush=True)
+        res["results"]["cfg3"] = out
+    res["wall_s"] = round(time.time() - t0, 1)
+    text = json.dumps(res)
+    print(text, flush=True)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

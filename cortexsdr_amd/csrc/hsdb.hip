@@ -77,6 +77,7 @@ struct MatDesc {
     const float* edge;
     const void* x;
     float* y;
+    const float* bias;  // per output row, added once (nullable)
     float* P;  // NB * K * M floats of workspace
     int R, K, NB, NBc, nchunks, slots, blen, Ce, C_full;
     int PB;                   // dx: block columns per workgroup (block length 64)
@@ -91,6 +92,7 @@ struct MatDesc {
 struct Params {
     MatDesc m[kMaxGroup];
     int G, M, MVz, x_f16;
+    int accumulate;  // 1: Y += W.X (+ bias); 0: Y = W.X (+ bias)
 };
 
 template <int CTRL>
@@ -165,10 +167,14 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     const int tid = threadIdx.x;
     const int M = p.M;
     {
+        // Y initialisation for the gathers' accumulation: 0 or bias, or left as it is (+ bias)
         const size_t ytot = (size_t)d.R * M;
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
         const size_t ye = min(ytot, (size_t)(u + 1) * yper);
-        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) d.y[i] = 0.0f;
+        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
+            const float bv = d.bias ? d.bias[i / M] : 0.0f;
+            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        }
     }
     if (d.blen == 64) {
         // 16 lanes per atom: lane l holds D[a][4l .. 4l+3] (one coalesced 16-byte load; a
@@ -493,6 +499,31 @@ __global__ __launch_bounds__(kThreads) void decode_dense_kernel(csdr_hsdb s,
     }
 }
 
+// One row of W (1-row tiles) into out[C]: the row's tiles decoded as decode_dense_kernel
+// does, then its edge columns. The row index is read from device memory (a token id).
+__global__ __launch_bounds__(kThreads) void decode_row_kernel(csdr_hsdb s,
+                                                              const int* __restrict__ row_dev,
+                                                              int row_host, float* __restrict__ out) {
+    const int r = row_dev ? *row_dev : row_host;
+    if (r < 0 || r >= (int)s.R) return;
+    const uint32_t B = s.tile_cols;
+    for (uint32_t g = blockIdx.x * kThreads + threadIdx.x; g < s.C; g += gridDim.x * kThreads) {
+        if (g >= s.C_full) {
+            out[g] = s.d_edge[(size_t)r * s.Ce + (g - s.C_full)];
+            continue;
+        }
+        const uint32_t b = g / B, e = g - b * B;
+        const uint32_t* w = s.d_codes + code_offset(s, (uint32_t)r * s.NB + b);
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < s.slots; ++j) {
+            const uint32_t wd = w[j];
+            const float cf = s.d_slot_gamma[j] * csdr::h2f(wd >> 16);
+            acc = fmaf(cf, s.d_dict[(size_t)(wd & 0x7FFFu) * B + e], acc);
+        }
+        out[g] = acc;
+    }
+}
+
 // Edge strips back into W: top-right (rows < R_full, cols >= C_full), then bottom rows.
 __global__ __launch_bounds__(kThreads) void decode_edge_kernel(csdr_hsdb s,
                                                                float* __restrict__ W) {
@@ -709,7 +740,8 @@ constexpr int kPhaseGather = 2;
 
 int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
                  float* const* ys, void* workspace, size_t workspace_bytes, hipStream_t st,
-                 int phases = kPhaseDx | kPhaseGather) {
+                 int phases = kPhaseDx | kPhaseGather, const float* const* bias = nullptr,
+                 int flags = 0) {
     if (n <= 0 || n > kMaxGroup || !segs || !xs || !ys || M <= 0)
         return set_error(CSDR_E_INVALID, "hsdb_matmul: bad argument (group of 1.." +
                                              std::to_string(kMaxGroup) + ")");
@@ -725,6 +757,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     const int MV = (M == 1) ? 1 : 4;
     p.MVz = (M + MV - 1) / MV;
     p.x_f16 = (x_dtype == CSDR_F16);
+    p.accumulate = (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0;
     char* ws = static_cast<char*>(workspace);
     size_t off = kWsHeader;
     // the register-resident M == 1 gather needs every matrix at 4, 8 or 16 slots (16-byte
@@ -755,6 +788,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.edge = s->d_edge;
         d.x = xs[i];
         d.y = ys[i];
+        d.bias = bias ? bias[i] : nullptr;
         d.P = reinterpret_cast<float*>(ws + off);
         off += p_bytes(s, M);
         d.R = (int)s->R;
@@ -917,6 +951,28 @@ CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const v
                                     size_t workspace_bytes, void* hip_stream) {
     return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
                         static_cast<hipStream_t>(hip_stream));
+}
+
+CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                       int x_dtype, int M, float* const* y,
+                                       const float* const* bias, int flags, void* workspace,
+                                       size_t workspace_bytes, void* hip_stream) {
+    return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream), kPhaseDx | kPhaseGather, bias,
+                        flags);
+}
+
+CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* s, const int* row_dev, int row_host, float* out,
+                                  void* hip_stream) {
+    if (!s || !out) return set_error(CSDR_E_INVALID, "hsdb_decode_row: bad argument");
+    if (s->tile_rows != 1)
+        return set_error(CSDR_E_FORMAT, "hsdb_decode_row: needs 1-row tiles");
+    if (!row_dev && (row_host < 0 || (uint32_t)row_host >= s->R))
+        return set_error(CSDR_E_INVALID, "hsdb_decode_row: row out of range");
+    decode_row_kernel<<<grid_for(s->C), kThreads, 0, static_cast<hipStream_t>(hip_stream)>>>(
+        *s, row_dev, row_host, out);
+    CSDR_LAUNCH_CHECK("hsdb decode_row");
+    return CSDR_OK;
 }
 
 CSDR_API int csdr_hsdb_dx_group(int n, const csdr_hsdb* const* segs, const void* const* x,

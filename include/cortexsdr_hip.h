@@ -27,6 +27,9 @@
  *   csdr_hsdb_export_codes
  *       the unpacked (index, sign) view of decodeAllTiles' inputs
  *       (HierarchicalSDRStrategy.cpp:81-84, 612-634), for bit-exact layout checks.
+ *   csdr_q4k_linear / csdr_q4k_dequant
+ *       decodeSupportedGGUFQuantized q4_k (SparseInferenceEngine.cpp:266-274, 362-384) followed
+ *       by Kernels::linear_forward (kernels/blas_kernels.cpp:264-293).
  */
 #ifndef CORTEXSDR_HIP_H
 #define CORTEXSDR_HIP_H
@@ -126,6 +129,23 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
                                     int x_dtype, int M, float* const* y, void* workspace,
                                     size_t workspace_bytes, void* hip_stream);
 
+/* As csdr_hsdb_matmul_group with per-matrix bias (bias[i] = NULL or R_i floats added to every
+ * column; bias itself may be NULL) and flags: CSDR_HSDB_ACCUMULATE makes Y += W.X (+ bias)
+ * instead of Y = W.X (+ bias), which folds a residual add into the product. */
+#define CSDR_HSDB_ACCUMULATE 1
+CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, const void* const* x,
+                                       int x_dtype, int M, float* const* y,
+                                       const float* const* bias, int flags, void* workspace,
+                                       size_t workspace_bytes, void* hip_stream);
+
+/* Row `row` of W (1-row tiles) decoded into out[C] (device), bit-identical to the same row
+ * of csdr_hsdb_decompress. The row is *row_dev when row_dev is not NULL (a token id produced
+ * on the device, e.g. a tied embedding lookup inside a captured decode step), else row_host.
+ * The CLI's lazy embedding-row decode (cortexsdr_cli.cpp:536-554) with the canonical code
+ * unpacking of HierarchicalSDRStrategy.cpp:81-84. */
+CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* seg, const int* row_dev, int row_host,
+                                  float* out, void* hip_stream);
+
 /* Dense decode to device W (R x C fp32 row-major), bit-identical to the reference decode
  * order (stage-major slot accumulation with fused multiply-adds, then the edge strips). */
 CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* seg, float* w, void* hip_stream);
@@ -135,6 +155,69 @@ CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* seg, float* w, void* hip_stre
  * Both are device buffers of n_tiles * slots uint16 (coef_abs may be NULL). */
 CSDR_API int csdr_hsdb_export_codes(const csdr_hsdb* seg, uint16_t* packed, uint16_t* coef_abs,
                                     void* hip_stream);
+
+/* ======================================================================
+ * GGUF Q4_K dequant-matmul (engine path, no fp32 W materialised)
+ * ==================================================================== */
+
+/* Element order inside a 144-byte super-block:
+ *   CSDR_Q4K_GGML        32-byte group g: low nibbles = sub-block 2g, high = 2g+1 (the engine
+ *                        and SDK decoders, SparseInferenceEngine.cpp:362-384,
+ *                        api/cortex_sdk.cpp:352-372)
+ *   CSDR_Q4K_INTERLEAVED element i = byte i/2, low nibble when i is even (HSDR compress side,
+ *                        HierarchicalSDRStrategy.cpp:836-845) */
+#define CSDR_Q4K_GGML 0
+#define CSDR_Q4K_INTERLEAVED 1
+
+/* y (M x R, fp32) = x (M x C) . dequant(W)^T, W = R rows of C/256 super-blocks (GGUF
+ * row-major, 16-byte aligned device memory); the linear_forward convention of
+ * kernels/blas_kernels.cpp:264-293 applied to the tensor decodeSupportedGGUFQuantized
+ * (SparseInferenceEngine.cpp:276-469) would produce. M == 1 takes fp32 or fp16 x; M > 1 takes
+ * fp16 x (MFMA path). C must be a multiple of 256. No workspace. */
+CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void* x, int x_dtype,
+                             int M, float* y, void* hip_stream);
+
+/* Dequantise n_blocks super-blocks to fp32 (256 values each), same arithmetic as the
+ * reference: (d*sc)*q - dmin*m. */
+CSDR_API int csdr_q4k_dequant(const void* w, size_t n_blocks, int order, float* out,
+                              void* hip_stream);
+
+/* ======================================================================
+ * Decoder ops (api/cortex_sdk.cpp run_transformer_decode building blocks)
+ * ==================================================================== */
+
+/* y = x / sqrt(mean(x^2) + eps) * w per row of n (rms_norm, cortex_sdk.cpp:1208-1232). */
+CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, float eps, float* y,
+                           void* hip_stream);
+/* y = silu(g) * u (silu_mul, cortex_sdk.cpp:1245-1256). */
+CSDR_API int csdr_silu_mul(const float* g, const float* u, size_t n, float* y, void* hip_stream);
+/* RoPE on adjacent pairs (get_rope_cache/apply_rope_inplace, cortex_sdk.cpp:1363-1423) of
+ * q (ntok x Hq x hd) and k (ntok x Hkv x hd) in place at positions *pos_dev + t, then k and v
+ * appended to the fp16 caches [position][kv head][hd] (capacity max_ctx positions). */
+CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, int Hkv, int hd,
+                          const int* pos_dev, float theta, uint16_t* kcache, uint16_t* vcache,
+                          int max_ctx, void* hip_stream);
+/* Decode attention: out (B x Hq x hd) = softmax(q.K^T * scale) V over cached positions
+ * [0, len_b) (len_b = lens_dev[b], or len_host when lens_dev is NULL); caches (B x T x Hkv x
+ * hd) fp16; GQA as repeat_kv_heads (cortex_sdk.cpp:1453-1478); scale 0 = 1/sqrt(hd).
+ * Split over 256-position chunks (workspace csdr_attn_decode_workspace_bytes) then combined.
+ * head_dim 64 or 128. Replaces Kernels::multi_head_attention's full-context recompute
+ * (attention_kernels.cpp:26-113) with the cached form flash_attention.cpp:165-247 intends. */
+CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T);
+CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                              const int* lens_dev, int len_host, int B, int T, int Hq, int Hkv,
+                              int hd, float scale, float* out, void* workspace,
+                              size_t workspace_bytes, void* hip_stream);
+/* Next token as select_best_from_logits (cortex_sdk.cpp:1005-1030): score = logit /
+ * temperature (temperature <= 0: 1) minus penalty where repeated[i] != 0 (repeated may be
+ * NULL); best finite score, lowest index on ties; -1 when none is finite. Writes the token to
+ * *out_token (device); when pos_dev is not NULL increments *pos_dev, and when repeated_update
+ * is not NULL sets repeated_update[token] = 1 (both for captured decode loops). */
+CSDR_API size_t csdr_select_workspace_bytes(void);
+CSDR_API int csdr_select_best(const float* logits, int n, const uint8_t* repeated,
+                              float temperature, float penalty, int* out_token, int* pos_dev,
+                              uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
+                              void* hip_stream);
 
 #ifdef __cplusplus
 }

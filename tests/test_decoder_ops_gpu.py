@@ -1,0 +1,161 @@
+"""GPU parity of the decoder ops (HK6 attention, HK7 elementwise, HK8 token selection, tied
+embedding row decode, bias/residual-folded HSDB products) against the CPU oracle, through
+the C-ABI."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_l2
+from cortexsdr_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def lib():
+    from cortexsdr_amd import _lib
+
+    return _lib.load()
+
+
+def sp(gpu):
+    return int(gpu.cuda.current_stream().cuda_stream)
+
+
+def chk(rc):
+    from cortexsdr_amd import _lib
+
+    _lib.check(rc)
+
+
+def dev(gpu, a):
+    return gpu.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("ntok,n", [(1, 896), (3, 4096), (2, 77)])
+def test_rms_norm(gpu, ntok, n):
+    rng = np.random.default_rng(1)
+    x = rng.normal(size=(ntok, n)).astype(np.float32)
+    w = rng.normal(size=n).astype(np.float32)
+    xd, wd = dev(gpu, x), dev(gpu, w)
+    y = gpu.empty_like(xd)
+    chk(lib().csdr_rms_norm(xd.data_ptr(), wd.data_ptr(), ntok, n, 1e-5, y.data_ptr(), sp(gpu)))
+    assert rel_l2(y.cpu().numpy(), oracle.rms_norm(x, w)) < 1e-6
+
+
+def test_silu_mul(gpu):
+    rng = np.random.default_rng(2)
+    g = rng.normal(size=4864).astype(np.float32) * 4
+    u = rng.normal(size=4864).astype(np.float32)
+    gd, ud = dev(gpu, g), dev(gpu, u)
+    y = gpu.empty_like(gd)
+    chk(lib().csdr_silu_mul(gd.data_ptr(), ud.data_ptr(), g.size, y.data_ptr(), sp(gpu)))
+    assert rel_l2(y.cpu().numpy(), oracle.silu_mul(g, u)) < 1e-6
+
+
+@pytest.mark.parametrize("pos", [0, 5, 511, 639])
+def test_rope_kv(gpu, pos):
+    rng = np.random.default_rng(3 + pos)
+    Hq, Hkv, hd, T = 14, 2, 64, 640
+    q = rng.normal(size=(Hq, hd)).astype(np.float32)
+    k = rng.normal(size=(Hkv, hd)).astype(np.float32)
+    v = rng.normal(size=(Hkv, hd)).astype(np.float32)
+    qd, kd, vd = dev(gpu, q), dev(gpu, k), dev(gpu, v)
+    kc = gpu.zeros((T, Hkv, hd), dtype=gpu.float16, device="cuda")
+    vc = gpu.zeros((T, Hkv, hd), dtype=gpu.float16, device="cuda")
+    pd = gpu.tensor([pos], dtype=gpu.int32, device="cuda")
+    chk(lib().csdr_rope_kv(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), 1, Hq, Hkv, hd,
+                           pd.data_ptr(), 1e6, kc.data_ptr(), vc.data_ptr(), T, sp(gpu)))
+    qr = oracle.rope(q[None], Hq, hd, 1e6, pos)[0]
+    kr = oracle.rope(k[None], Hkv, hd, 1e6, pos)[0]
+    # the angle pos * theta^(-i/hd) is an fp32 product: a 1-ulp difference between host and
+    # device powf moves it by up to pos * 6e-8 rad, so the bound grows with the position
+    tol = 1e-6 + pos * 1.2e-7
+    assert rel_l2(qd.cpu().numpy(), qr) < tol
+    assert rel_l2(kd.cpu().numpy(), kr) < tol
+    assert np.array_equal(kc[pos].cpu().numpy(), kd.cpu().numpy().astype(np.float16))
+    assert np.array_equal(vc[pos].cpu().numpy(), v.astype(np.float16))
+    assert not kc[:pos].cpu().numpy().any()
+
+
+@pytest.mark.parametrize("B,T,L,Hq,Hkv,hd", [
+    (1, 640, 577, 14, 2, 64),     # config 4 shape
+    (1, 640, 1, 14, 2, 64),
+    (1, 4096, 4096, 32, 32, 128), # config 5 shape, batch 1
+    (2, 300, None, 8, 2, 128),    # per-batch lengths
+    (1, 256, 256, 4, 1, 64),      # exactly one split
+])
+def test_attn_decode(gpu, B, T, L, Hq, Hkv, hd):
+    rng = np.random.default_rng(4)
+    q = rng.normal(size=(B, Hq, hd)).astype(np.float32)
+    kc = rng.normal(size=(B, T, Hkv, hd)).astype(np.float16)
+    vc = rng.normal(size=(B, T, Hkv, hd)).astype(np.float16)
+    lens = np.array([T - 17 * b for b in range(B)], np.int32) if L is None else \
+        np.full(B, L, np.int32)
+    qd, kd, vd = dev(gpu, q), dev(gpu, kc), dev(gpu, vc)
+    out = gpu.empty_like(qd)
+    wsb = lib().csdr_attn_decode_workspace_bytes(B, Hq, hd, T)
+    ws = gpu.zeros(max(wsb, 4), dtype=gpu.uint8, device="cuda")
+    ld = dev(gpu, lens) if L is None else None
+    chk(lib().csdr_attn_decode(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                               ld.data_ptr() if ld is not None else None, int(lens[0]), B, T, Hq,
+                               Hkv, hd, 0.0, out.data_ptr(), ws.data_ptr(), ws.numel(), sp(gpu)))
+    ref = oracle.attn_decode(q, kc.view(np.uint16), vc.view(np.uint16), lens, Hq, Hkv, hd)
+    assert rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("n", [151936, 1000, 7])
+def test_select_best(gpu, n):
+    rng = np.random.default_rng(5)
+    lg = rng.normal(size=n).astype(np.float32)
+    lg[n // 3] = lg[n // 2] = lg.max() + 1.0  # tie: the first index wins
+    if n > 10:
+        lg[3] = np.nan
+        lg[4] = np.inf
+    rep = (rng.random(n) < 0.1).astype(np.uint8)
+    ld, rd = dev(gpu, lg), dev(gpu, rep)
+    out = gpu.zeros(1, dtype=gpu.int32, device="cuda")
+    pos = gpu.zeros(1, dtype=gpu.int32, device="cuda")
+    upd = gpu.zeros(n, dtype=gpu.uint8, device="cuda")
+    ws = gpu.zeros(lib().csdr_select_workspace_bytes(), dtype=gpu.uint8, device="cuda")
+    for temp, pen, use_rep in ((0.0, 0.0, False), (0.8, 1.5, True)):
+        chk(lib().csdr_select_best(ld.data_ptr(), n, rd.data_ptr() if use_rep else None, temp, pen,
+                                   out.data_ptr(), pos.data_ptr(), upd.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), sp(gpu)))
+        ref = oracle.select_best(lg, rep if use_rep else None, temp, pen)
+        assert int(out.item()) == ref
+    assert int(pos.item()) == 2
+    assert upd.cpu().numpy().sum() >= 1
+
+
+def test_decode_row_and_bias_accumulate(gpu):
+    from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
+
+    R, Cc = 300, 200  # edge strip of 8 columns
+    stream = synth.hsdb_layer(R, Cc, 64, 8, seed_dict=3, seed_codes=4)
+    seg = HsdbSegment(stream)
+    w = oracle.hsdr_decompress(stream)
+    out = gpu.zeros(Cc, dtype=gpu.float32, device="cuda")
+    row = gpu.tensor([123], dtype=gpu.int32, device="cuda")
+    chk(lib().csdr_hsdb_decode_row(seg._h, row.data_ptr(), 0, out.data_ptr(), sp(gpu)))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), w[123].view(np.uint32))
+    chk(lib().csdr_hsdb_decode_row(seg._h, None, 299, out.data_ptr(), sp(gpu)))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), w[299].view(np.uint32))
+    # y = W x + bias, then y += W x (residual folding)
+    x = synth.activations(Cc, 1, seed=5)
+    bias = np.random.default_rng(6).normal(size=R).astype(np.float32)
+    xd, bd = dev(gpu, x), dev(gpu, bias)
+    y = gpu.zeros((R, 1), dtype=gpu.float32, device="cuda")
+    ws = group_workspace([seg], 1)
+    hs = (C.c_void_p * 1)(seg._h.value)
+    xp = (C.c_void_p * 1)(xd.data_ptr())
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    bp = (C.c_void_p * 1)(bd.data_ptr())
+    chk(lib().csdr_hsdb_matmul_group_ex(1, hs, xp, 0, 1, yp, bp, 0, ws.data_ptr(), ws.numel(),
+                                        sp(gpu)))
+    wx = oracle.hsdb_matmul(stream, x)[:, 0]
+    assert rel_l2(y.cpu().numpy()[:, 0], wx + bias) < 1e-5
+    chk(lib().csdr_hsdb_matmul_group_ex(1, hs, xp, 0, 1, yp, None, 1, ws.data_ptr(), ws.numel(),
+                                        sp(gpu)))
+    assert rel_l2(y.cpu().numpy()[:, 0], 2 * wx + bias) < 1e-5
