@@ -74,7 +74,26 @@ SIGNATURES = {
     "csdr_select_workspace_bytes": (_sz, []),
     "csdr_select_best": (C.c_int, [_vp, C.c_int, _vp, C.c_float, C.c_float, _vp, _vp, _vp,
                                    _vp, _sz, _vp]),
+    "csdr_decoder_create": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "csdr_decoder_free": (C.c_int, [_vp]),
+    "csdr_decoder_set_layer": (C.c_int, [_vp, C.c_int] + [_vp] * 7 + [_vp] * 5),
+    "csdr_decoder_set_output": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "csdr_decoder_prefill": (C.c_int, [_vp, _vp, C.c_int, C.c_float, C.c_float]),
+    "csdr_decoder_decode": (C.c_int, [_vp, C.c_int, C.c_float, C.c_float]),
+    "csdr_decoder_tokens": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
+    "csdr_decoder_generate": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, C.c_float,
+                                        C.c_int, _vp, C.POINTER(C.c_int)]),
+    "csdr_decoder_logits": (C.c_int, [_vp, _vp]),
+    "csdr_decoder_position": (C.c_int, [_vp]),
 }
+
+
+class DecoderConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int),
+        ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
+        ("max_ctx", C.c_int), ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+    ]
 
 
 def _hip_runtimes_mapped() -> set[str]:

@@ -21,6 +21,8 @@ import time
 
 import numpy as np
 
+from . import synth
+
 HBM_PEAK = 8.0e12
 MALL = 256 * 1024 * 1024
 
@@ -53,7 +55,7 @@ def time_graph(torch, fn, n_copies: int, steps: int) -> float:
 
 
 def bench_hsdb(torch, R, Cc, K, s, M, xdtype, steps, seed=2):
-    from . import _lib, synth
+    from . import _lib
     from .hsdr import HsdbSegment, group_workspace
 
     stream = synth.hsdb_layer(R, Cc, K, s, seed_dict=1, seed_codes=seed)
@@ -84,7 +86,7 @@ def bench_hsdb(torch, R, Cc, K, s, M, xdtype, steps, seed=2):
 
 
 def bench_q4k(torch, R, Cc, M, steps, order=0):
-    from . import _lib, q4k, synth
+    from . import _lib, q4k
 
     blob = synth.q4k_matrix(R, Cc, seed=7)
     ncp = _copies(len(blob))
@@ -105,9 +107,46 @@ def bench_q4k(torch, R, Cc, M, steps, order=0):
             "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
 
 
+def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
+    """Config 4: Qwen2-0.5B-shaped decoder, all linears HSDB-coded (1024 x 64 shared
+    dictionary, 8 nnz per block), prompt of uniform random ids, greedy (plain argmax)."""
+    from .decoder import QWEN2_0_5B, Decoder, synthetic_weights
+
+    t0 = time.time()
+    w = synthetic_weights(QWEN2_0_5B, seed=seed)
+    t_build = time.time() - t0
+    prompt = (synth.uniform(seed + 77, n_prompt, stream=61) * QWEN2_0_5B.vocab).astype(np.int32)
+    dec = Decoder(w)
+    try:
+        dec.prefill(prompt[:8], 0.0, 0.0)          # capture both graphs, warm up
+        dec.decode(8, 0.0, 0.0)
+        t0 = time.perf_counter()
+        dec.prefill(prompt, 0.0, 0.0)
+        t_prefill = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        dec.decode(n_new - 1, 0.0, 0.0)
+        t_decode = time.perf_counter() - t0
+        toks = dec.tokens(n_prompt, n_new)
+        per_tok = t_decode / (n_new - 1)
+        code = w.code_bytes()
+        kv = 2 * QWEN2_0_5B.n_layers * QWEN2_0_5B.n_kv_heads * QWEN2_0_5B.head_dim * 2
+        alg = code + kv * (n_prompt + n_new // 2)
+        return {"n_prompt": n_prompt, "n_new": n_new,
+                "decode_tokens_per_s": round(1.0 / per_tok, 1),
+                "ms_per_token": round(per_tok * 1e3, 4),
+                "prefill_tokens_per_s": round(n_prompt / t_prefill, 1),
+                "code_MB_per_token": round(code / 1e6, 2),
+                "alg_GBps": round(alg / per_tok / 1e9, 1),
+                "hbm_frac": round(alg / per_tok / HBM_PEAK, 4),
+                "device_MB": round(dec.device_bytes() / 1e6, 1),
+                "host_build_s": round(t_build, 1), "first_tokens": toks[:8].tolist()}
+    finally:
+        dec.close()
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--configs", default="cfg1,cfg2,cfg3")
+    ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4")
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--out", default=None)
     args = ap.parse_args(argv)
@@ -136,6 +175,9 @@ def main(argv=None) -> int:
                 out.append(bench_q4k(torch, R, Cc, M, args.steps))
                 print(json.dumps(out[-1]), flush=True)
         res["results"]["cfg3"] = out
+    if "cfg4" in cfgs:
+        res["results"]["cfg4"] = bench_decoder(torch)
+        print(json.dumps(res["results"]["cfg4"]), flush=True)
     res["wall_s"] = round(time.time() - t0, 1)
     text = json.dumps(res)
     print(text, flush=True)

@@ -1,0 +1,490 @@
+// decoder.hip — a Llama/Qwen-style decoder over device-resident HSDB-coded weights.
+//
+// Reference: the SDK's native decoder run_transformer_decode (api/cortex_sdk.cpp:1543-1696),
+// its token choice select_next_token_from_embedding_transpose (:1032-1206, with
+// sanitize_hidden_for_sampling :959-976 and select_best_from_logits :1005-1030) and the
+// generate_text loop (:1951-2054). Per block: RMSNorm -> q/k/v projections -> RoPE -> GQA
+// attention -> o projection + residual -> RMSNorm -> gate/up -> SiLU*up -> down + residual;
+// then the output RMSNorm, the lm_head scores of the sanitized hidden state and the
+// penalised argmax. The reference recomputes the whole context for every token over dense
+// fp32 weights; here the weights stay coded in HBM, K/V live in an fp16 cache, and one step
+// is a fixed kernel sequence captured once in a HIP graph and replayed per token: the token,
+// position and context length are device integers that each step reads and advances.
+//
+// Device token ring: ring[p] holds the token at position p (prompt tokens, then the tokens
+// the steps select). A step at position p reads ring[p], appends K/V at p and, when it has the
+// output head, selects the token for p + 1 and writes it to ring[p + 1]. Prompt positions
+// before the last run the body-only step (no head; the reference's generate_text samples only
+// after the whole prompt).
+//
+// Biases fold into the projections' output initialisation and the residual adds into the
+// o/down projections (CSDR_HSDB_ACCUMULATE); the embedding is the lm_head row of the token
+// (tied embeddings, decoded on the device) unless a separate coded embedding is set.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace {
+
+using csdr::set_error;
+
+constexpr int kSanThreads = 256;
+
+__global__ void step_begin_kernel(const int* __restrict__ pos, const int* __restrict__ ring,
+                                  int cap, int* __restrict__ tok, int* __restrict__ len) {
+    if (threadIdx.x == 0) {
+        const int p = *pos;
+        *len = p + 1;
+        *tok = (p >= 0 && p < cap) ? ring[p] : -1;
+    }
+}
+
+// Body-only step end: advance the position.
+__global__ void advance_kernel(int* __restrict__ pos) {
+    if (threadIdx.x == 0) *pos += 1;
+}
+
+// Head step end (after select_best advanced the position): ring[pos] = selected token.
+__global__ void record_kernel(const int* __restrict__ tok, const int* __restrict__ pos,
+                              int* __restrict__ ring, int cap) {
+    if (threadIdx.x == 0) {
+        const int p = *pos;
+        if (p >= 0 && p < cap) ring[p] = *tok;
+    }
+}
+
+// sanitize_hidden_for_sampling (cortex_sdk.cpp:959-976) in place: non-finite -> 0, then a
+// uniform scale to max |h| = 1000 when the largest finite magnitude exceeds 1000.
+__global__ __launch_bounds__(kSanThreads) void sanitize_kernel(float* __restrict__ h, int n) {
+    __shared__ float red[kSanThreads];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kSanThreads) {
+        float v = h[i];
+        if (!isfinite(v)) {
+            v = 0.0f;
+            h[i] = 0.0f;
+        }
+        m = fmaxf(m, fabsf(v));
+    }
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int off = kSanThreads / 2; off > 0; off >>= 1) {
+        if (threadIdx.x < off) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + off]);
+        __syncthreads();
+    }
+    const float mx = red[0];
+    if (mx > 1000.0f) {
+        const float scale = 1000.0f / mx;
+        for (int i = threadIdx.x; i < n; i += kSanThreads) h[i] *= scale;
+    }
+}
+
+struct Layer {
+    const csdr_hsdb *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    const csdr_hsdb *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace
+
+struct csdr_decoder {
+    csdr_decoder_config cfg{};
+    std::vector<Layer> layers;
+    const csdr_hsdb* lm = nullptr;
+    const csdr_hsdb* emb = nullptr;
+    float* final_norm = nullptr;
+    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *a = nullptr;
+    float *g = nullptr, *u = nullptr, *logits = nullptr;
+    int *tok = nullptr, *pos = nullptr, *len = nullptr, *ring = nullptr;
+    uint8_t* repeated = nullptr;
+    void* ws_hsdb = nullptr;
+    size_t ws_hsdb_bytes = 0, ws_hsdb_alloc = 0;
+    void* ws_attn = nullptr;
+    size_t ws_attn_bytes = 0;
+    void* ws_sel = nullptr;
+    size_t ws_sel_bytes = 0;
+    hipStream_t stream = nullptr;
+    hipGraph_t graph[2] = {nullptr, nullptr};  // [0] body-only step, [1] step with head
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    float g_temp = 0.0f, g_pen = 0.0f;  // sampling parameters graph[1] was captured with
+    int host_pos = 0;                   // positions processed (host mirror of *pos)
+    int n_prompt = 0;
+    std::vector<void*> allocs;
+};
+
+namespace {
+
+template <typename T>
+int dalloc(csdr_decoder* d, T** p, size_t count) {
+    void* ptr = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 4);
+    CSDR_HIP_CHECK(hipMalloc(&ptr, bytes));
+    d->allocs.push_back(ptr);
+    CSDR_HIP_CHECK(hipMemset(ptr, 0, bytes));
+    *p = static_cast<T*>(ptr);
+    return CSDR_OK;
+}
+
+int upload_vec(csdr_decoder* d, float** dst, const float* host, size_t n) {
+    if (!host) {
+        *dst = nullptr;
+        return CSDR_OK;
+    }
+    if (!*dst) {
+        int rc = dalloc(d, dst, n);
+        if (rc) return rc;
+    }
+    CSDR_HIP_CHECK(hipMemcpy(*dst, host, n * 4, hipMemcpyHostToDevice));
+    return CSDR_OK;
+}
+
+int check_shape(const csdr_hsdb* s, uint32_t R, uint32_t C, const char* what) {
+    csdr_hsdb_info info;
+    if (!s || csdr_hsdb_get_info(s, &info) != CSDR_OK)
+        return set_error(CSDR_E_INVALID, std::string("decoder: missing ") + what);
+    if (info.rows != R || info.cols != C || info.tile_rows != 1)
+        return set_error(CSDR_E_INVALID, std::string("decoder: ") + what + " is " +
+                                             std::to_string(info.rows) + "x" +
+                                             std::to_string(info.cols) + ", expected " +
+                                             std::to_string(R) + "x" + std::to_string(C));
+    return CSDR_OK;
+}
+
+#define RC(expr)                        \
+    do {                                \
+        int rc_ = (expr);               \
+        if (rc_ != CSDR_OK) return rc_; \
+    } while (0)
+
+int mm(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x, float* const* ys,
+       const float* const* bias, int flags, hipStream_t st) {
+    const void* xs[4];
+    for (int i = 0; i < n; ++i) xs[i] = x;
+    return csdr_hsdb_matmul_group_ex(n, segs, xs, CSDR_F32, 1, ys, bias, flags, d->ws_hsdb,
+                                     d->ws_hsdb_bytes, st);
+}
+
+// One step at device position *pos for the token ring[*pos]; with_head adds the output norm,
+// the lm_head scores and the token selection.
+int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, float penalty) {
+    const csdr_decoder_config& c = d->cfg;
+    const int H = c.hidden, Hq = c.n_heads, Hkv = c.n_kv_heads, hd = c.head_dim;
+    const int cap = c.max_ctx + 1;
+    step_begin_kernel<<<1, 64, 0, st>>>(d->pos, d->ring, cap, d->tok, d->len);
+    CSDR_LAUNCH_CHECK("decoder step_begin");
+    RC(csdr_hsdb_decode_row(d->emb, d->tok, 0, d->x, st));
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = d->layers[l];
+        RC(csdr_rms_norm(d->x, L.attn_norm, 1, H, c.rms_eps, d->h, st));
+        {
+            const csdr_hsdb* segs[3] = {L.q, L.k, L.v};
+            float* ys[3] = {d->q, d->k, d->v};
+            const float* bias[3] = {L.bq, L.bk, L.bv};
+            RC(mm(d, 3, segs, d->h, ys, bias, 0, st));
+        }
+        RC(csdr_rope_kv(d->q, d->k, d->v, 1, Hq, Hkv, hd, d->pos, c.rope_theta, L.kc, L.vc,
+                        c.max_ctx, st));
+        RC(csdr_attn_decode(d->q, L.kc, L.vc, d->len, 0, 1, c.max_ctx, Hq, Hkv, hd, 0.0f, d->a,
+                            d->ws_attn, d->ws_attn_bytes, st));
+        {
+            const csdr_hsdb* segs[1] = {L.o};
+            float* ys[1] = {d->x};
+            RC(mm(d, 1, segs, d->a, ys, nullptr, CSDR_HSDB_ACCUMULATE, st));  // x += o(a)
+        }
+        RC(csdr_rms_norm(d->x, L.ffn_norm, 1, H, c.rms_eps, d->h, st));
+        {
+            const csdr_hsdb* segs[2] = {L.gate, L.up};
+            float* ys[2] = {d->g, d->u};
+            RC(mm(d, 2, segs, d->h, ys, nullptr, 0, st));
+        }
+        RC(csdr_silu_mul(d->g, d->u, (size_t)c.ffn, d->a, st));
+        {
+            const csdr_hsdb* segs[1] = {L.down};
+            float* ys[1] = {d->x};
+            RC(mm(d, 1, segs, d->a, ys, nullptr, CSDR_HSDB_ACCUMULATE, st));  // x += down(a)
+        }
+    }
+    if (!with_head) {
+        advance_kernel<<<1, 64, 0, st>>>(d->pos);
+        CSDR_LAUNCH_CHECK("decoder advance");
+        return CSDR_OK;
+    }
+    if (d->final_norm) RC(csdr_rms_norm(d->x, d->final_norm, 1, H, c.rms_eps, d->h, st));
+    else CSDR_HIP_CHECK(hipMemcpyAsync(d->h, d->x, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    sanitize_kernel<<<1, kSanThreads, 0, st>>>(d->h, H);
+    CSDR_LAUNCH_CHECK("decoder sanitize");
+    {
+        const csdr_hsdb* segs[1] = {d->lm};
+        float* ys[1] = {d->logits};
+        RC(mm(d, 1, segs, d->h, ys, nullptr, 0, st));
+    }
+    RC(csdr_select_best(d->logits, c.vocab, d->repeated, temperature, penalty, d->tok, d->pos,
+                        d->repeated, d->ws_sel, d->ws_sel_bytes, st));
+    record_kernel<<<1, 64, 0, st>>>(d->tok, d->pos, d->ring, cap);
+    CSDR_LAUNCH_CHECK("decoder record");
+    return CSDR_OK;
+}
+
+void destroy_graphs(csdr_decoder* d) {
+    for (int i = 0; i < 2; ++i) {
+        if (d->exec[i]) (void)hipGraphExecDestroy(d->exec[i]);
+        if (d->graph[i]) (void)hipGraphDestroy(d->graph[i]);
+        d->exec[i] = nullptr;
+        d->graph[i] = nullptr;
+    }
+}
+
+int ready(csdr_decoder* d) {
+    if (!d) return set_error(CSDR_E_INVALID, "decoder: null handle");
+    for (size_t l = 0; l < d->layers.size(); ++l)
+        if (!d->layers[l].q)
+            return set_error(CSDR_E_INVALID, "decoder: layer " + std::to_string(l) + " not set");
+    if (!d->lm || !d->emb) return set_error(CSDR_E_INVALID, "decoder: output head not set");
+    if (d->ws_hsdb_alloc < d->ws_hsdb_bytes) {
+        unsigned char* p = nullptr;
+        RC(dalloc(d, &p, d->ws_hsdb_bytes));
+        d->ws_hsdb = p;
+        d->ws_hsdb_alloc = d->ws_hsdb_bytes;
+        destroy_graphs(d);
+    }
+    return CSDR_OK;
+}
+
+// Captures graph[i] (i = with_head) if it is missing or was captured with other parameters.
+int ensure_graph(csdr_decoder* d, int i, float temperature, float penalty) {
+    if (d->exec[i] && (i == 0 || (d->g_temp == temperature && d->g_pen == penalty)))
+        return CSDR_OK;
+    if (d->exec[i]) (void)hipGraphExecDestroy(d->exec[i]);
+    if (d->graph[i]) (void)hipGraphDestroy(d->graph[i]);
+    d->exec[i] = nullptr;
+    d->graph[i] = nullptr;
+    CSDR_HIP_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = step(d, d->stream, i == 1, temperature, penalty);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(d->stream, &g);
+    if (rc != CSDR_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess || !g)
+        return set_error(CSDR_E_HIP, std::string("decoder: graph capture failed: ") +
+                                         hipGetErrorString(e));
+    d->graph[i] = g;
+    CSDR_HIP_CHECK(hipGraphInstantiate(&d->exec[i], g, nullptr, nullptr, 0));
+    if (i == 1) {
+        d->g_temp = temperature;
+        d->g_pen = penalty;
+    }
+    return CSDR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** out) {
+    if (!cfg || !out) return set_error(CSDR_E_INVALID, "decoder_create: null argument");
+    *out = nullptr;
+    const csdr_decoder_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+        c.n_heads % c.n_kv_heads || c.head_dim * c.n_heads != c.hidden || c.ffn <= 0 ||
+        c.vocab <= 0 || c.max_ctx <= 0 || (c.head_dim != 64 && c.head_dim != 128) ||
+        !(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f))
+        return set_error(CSDR_E_INVALID, "decoder_create: inconsistent config");
+    csdr_decoder* d = new (std::nothrow) csdr_decoder();
+    if (!d) return set_error(CSDR_E_INVALID, "decoder_create: out of host memory");
+    d->cfg = c;
+    d->layers.resize(c.n_layers);
+    int rc = CSDR_OK;
+    const size_t kvn = (size_t)c.max_ctx * c.n_kv_heads * c.head_dim;
+    for (auto& L : d->layers)
+        if ((rc = dalloc(d, &L.kc, kvn)) || (rc = dalloc(d, &L.vc, kvn))) break;
+    const int kvw = c.n_kv_heads * c.head_dim;
+    const int wide = std::max(c.hidden, c.ffn);
+    if (!rc) rc = dalloc(d, &d->x, c.hidden);
+    if (!rc) rc = dalloc(d, &d->h, c.hidden);
+    if (!rc) rc = dalloc(d, &d->q, c.hidden);
+    if (!rc) rc = dalloc(d, &d->k, kvw);
+    if (!rc) rc = dalloc(d, &d->v, kvw);
+    if (!rc) rc = dalloc(d, &d->a, wide);
+    if (!rc) rc = dalloc(d, &d->g, c.ffn);
+    if (!rc) rc = dalloc(d, &d->u, c.ffn);
+    if (!rc) rc = dalloc(d, &d->logits, c.vocab);
+    if (!rc) rc = dalloc(d, &d->tok, 1);
+    if (!rc) rc = dalloc(d, &d->pos, 1);
+    if (!rc) rc = dalloc(d, &d->len, 1);
+    if (!rc) rc = dalloc(d, &d->ring, (size_t)c.max_ctx + 1);
+    if (!rc) rc = dalloc(d, &d->repeated, c.vocab);
+    if (!rc) {
+        d->ws_attn_bytes = csdr_attn_decode_workspace_bytes(1, c.n_heads, c.head_dim, c.max_ctx);
+        unsigned char* p = nullptr;
+        rc = dalloc(d, &p, d->ws_attn_bytes);
+        d->ws_attn = p;
+    }
+    if (!rc) {
+        d->ws_sel_bytes = csdr_select_workspace_bytes();
+        unsigned char* p = nullptr;
+        rc = dalloc(d, &p, d->ws_sel_bytes);
+        d->ws_sel = p;
+    }
+    if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
+        rc = set_error(CSDR_E_HIP, "decoder_create: stream creation failed");
+    if (rc) {
+        csdr_decoder_free(d);
+        return rc;
+    }
+    *out = d;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_free(csdr_decoder* d) {
+    if (!d) return CSDR_OK;
+    if (d->stream) (void)hipStreamSynchronize(d->stream);
+    destroy_graphs(d);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
+    for (void* p : d->allocs) (void)hipFree(p);
+    delete d;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_set_layer(csdr_decoder* d, int layer, const csdr_hsdb* wq,
+                                    const csdr_hsdb* wk, const csdr_hsdb* wv, const csdr_hsdb* wo,
+                                    const csdr_hsdb* wgate, const csdr_hsdb* wup,
+                                    const csdr_hsdb* wdown, const float* attn_norm,
+                                    const float* ffn_norm, const float* bq, const float* bk,
+                                    const float* bv) {
+    if (!d || layer < 0 || layer >= d->cfg.n_layers || !attn_norm || !ffn_norm)
+        return set_error(CSDR_E_INVALID, "decoder_set_layer: bad argument");
+    const csdr_decoder_config& c = d->cfg;
+    const uint32_t H = c.hidden, kvw = c.n_kv_heads * c.head_dim, F = c.ffn;
+    RC(check_shape(wq, H, H, "q"));
+    RC(check_shape(wk, kvw, H, "k"));
+    RC(check_shape(wv, kvw, H, "v"));
+    RC(check_shape(wo, H, H, "o"));
+    RC(check_shape(wgate, F, H, "gate"));
+    RC(check_shape(wup, F, H, "up"));
+    RC(check_shape(wdown, H, F, "down"));
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    destroy_graphs(d);
+    Layer& L = d->layers[layer];
+    L.q = wq, L.k = wk, L.v = wv, L.o = wo, L.gate = wgate, L.up = wup, L.down = wdown;
+    RC(upload_vec(d, &L.attn_norm, attn_norm, H));
+    RC(upload_vec(d, &L.ffn_norm, ffn_norm, H));
+    RC(upload_vec(d, &L.bq, bq, H));
+    RC(upload_vec(d, &L.bk, bk, kvw));
+    RC(upload_vec(d, &L.bv, bv, kvw));
+    const csdr_hsdb* qkv[3] = {wq, wk, wv};
+    const csdr_hsdb* gu[2] = {wgate, wup};
+    d->ws_hsdb_bytes = std::max({d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(3, qkv, 1),
+                                 csdr_hsdb_group_workspace_bytes(1, &wo, 1),
+                                 csdr_hsdb_group_workspace_bytes(2, gu, 1),
+                                 csdr_hsdb_group_workspace_bytes(1, &wdown, 1)});
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_set_output(csdr_decoder* d, const csdr_hsdb* lm_head,
+                                     const float* final_norm, const csdr_hsdb* embedding) {
+    if (!d) return set_error(CSDR_E_INVALID, "decoder_set_output: null handle");
+    const csdr_decoder_config& c = d->cfg;
+    RC(check_shape(lm_head, c.vocab, c.hidden, "lm_head"));
+    if (embedding) RC(check_shape(embedding, c.vocab, c.hidden, "embedding"));
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    destroy_graphs(d);
+    d->lm = lm_head;
+    d->emb = embedding ? embedding : lm_head;
+    RC(upload_vec(d, &d->final_norm, final_norm, c.hidden));
+    d->ws_hsdb_bytes =
+        std::max(d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(1, &lm_head, 1));
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_prompt,
+                                  float temperature, float penalty) {
+    RC(ready(d));
+    const csdr_decoder_config& c = d->cfg;
+    if (!prompt || n_prompt <= 0)
+        return set_error(CSDR_E_INVALID, "decoder_prefill: empty prompt");
+    if (n_prompt > c.max_ctx)
+        return set_error(CSDR_E_INVALID, "decoder_prefill: prompt longer than the context");
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab)
+            return set_error(CSDR_E_INVALID, "decoder_prefill: token id out of range");
+    RC(ensure_graph(d, 0, temperature, penalty));
+    RC(ensure_graph(d, 1, temperature, penalty));
+    hipStream_t st = d->stream;
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
+    CSDR_HIP_CHECK(hipMemset(d->pos, 0, 4));
+    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, c.vocab));
+    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)(c.max_ctx + 1) * 4));
+    CSDR_HIP_CHECK(hipMemcpy(d->ring, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    for (int i = 0; i + 1 < n_prompt; ++i) CSDR_HIP_CHECK(hipGraphLaunch(d->exec[0], st));
+    CSDR_HIP_CHECK(hipGraphLaunch(d->exec[1], st));
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
+    d->host_pos = n_prompt;
+    d->n_prompt = n_prompt;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_decode(csdr_decoder* d, int n_steps, float temperature, float penalty) {
+    RC(ready(d));
+    if (n_steps < 0) return set_error(CSDR_E_INVALID, "decoder_decode: negative step count");
+    if (d->n_prompt == 0) return set_error(CSDR_E_INVALID, "decoder_decode: prefill first");
+    if (d->host_pos + n_steps > d->cfg.max_ctx)
+        return set_error(CSDR_E_INVALID, "decoder_decode: context capacity exceeded");
+    RC(ensure_graph(d, 1, temperature, penalty));
+    for (int i = 0; i < n_steps; ++i) CSDR_HIP_CHECK(hipGraphLaunch(d->exec[1], d->stream));
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->host_pos += n_steps;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_tokens(const csdr_decoder* d, int first, int count, int32_t* out) {
+    if (!d || !out || first < 0 || count < 0 || first + count > d->cfg.max_ctx + 1)
+        return set_error(CSDR_E_INVALID, "decoder_tokens: bad argument");
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    if (count)
+        CSDR_HIP_CHECK(hipMemcpy(out, d->ring + first, (size_t)count * 4, hipMemcpyDeviceToHost));
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_generate(csdr_decoder* d, const int32_t* prompt, int n_prompt,
+                                   int max_new_tokens, float temperature, float penalty,
+                                   int eos_id, int32_t* out_tokens, int* n_generated) {
+    if (!d || !out_tokens || !n_generated)
+        return set_error(CSDR_E_INVALID, "decoder_generate: null argument");
+    *n_generated = 0;
+    const int steps = std::max(1, max_new_tokens);
+    if ((long long)n_prompt + steps > d->cfg.max_ctx + 1LL)
+        return set_error(CSDR_E_INVALID, "decoder_generate: context capacity exceeded");
+    RC(csdr_decoder_prefill(d, prompt, n_prompt, temperature, penalty));
+    RC(csdr_decoder_decode(d, steps - 1, temperature, penalty));
+    RC(csdr_decoder_tokens(d, n_prompt, steps, out_tokens));
+    int n = 0;
+    while (n < steps) {
+        if (out_tokens[n] < 0) break;  // no finite score: the reference fails the step
+        ++n;
+        if (eos_id >= 0 && out_tokens[n - 1] == eos_id) break;
+    }
+    *n_generated = n;
+    if (n == 0) return set_error(CSDR_E_UNSUPPORTED, "decoder_generate: no finite logit");
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_logits(const csdr_decoder* d, float* out) {
+    if (!d || !out) return set_error(CSDR_E_INVALID, "decoder_logits: bad argument");
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    CSDR_HIP_CHECK(hipMemcpy(out, d->logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_position(const csdr_decoder* d) { return d ? d->host_pos : -1; }
+
+}  // extern "C"

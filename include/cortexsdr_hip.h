@@ -219,6 +219,60 @@ CSDR_API int csdr_select_best(const float* logits, int n, const uint8_t* repeate
                               uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
                               void* hip_stream);
 
+/* ======================================================================
+ * Decoder engine (api/cortex_sdk.cpp run_transformer_decode :1543-1696 and
+ * cortex_inference_engine_generate_text :1951-2054, batch 1)
+ *
+ * A Llama/Qwen-style decoder whose linears are loaded csdr_hsdb segments (the decoder keeps
+ * the pointers; the caller keeps the segments alive). K/V are kept in a per-layer fp16 cache
+ * (max_ctx positions) instead of the reference's whole-context recompute; each step is one
+ * replay of a captured HIP graph. Token choice as select_next_token_from_embedding_transpose
+ * (cortex_sdk.cpp:1032-1206): output RMSNorm, sanitize_hidden_for_sampling (:959-976), lm_head
+ * scores, select_best_from_logits with `temperature` and `penalty` for tokens generated so far
+ * (the reference's generate_text uses 0.8 and 1.5). Not reentrant: one thread per decoder.
+ * ==================================================================== */
+typedef struct csdr_decoder csdr_decoder;
+typedef struct csdr_decoder_config {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
+    float rope_theta; /* RoPE base (get_rope_cache, cortex_sdk.cpp:1363; 1e6 there) */
+    float rms_eps;    /* RMSNorm epsilon (rms_norm, cortex_sdk.cpp:1212; 1e-5 there) */
+} csdr_decoder_config;
+
+CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** out);
+CSDR_API int csdr_decoder_free(csdr_decoder* dec);
+/* Block `layer`'s weights (transformer_blocks names attn_q/k/v/output, ffn_gate/up/down,
+ * attn_norm, ffn_norm; cortex_sdk.cpp:1570-1660). Shapes: q,o H x H; k,v (Hkv*hd) x H;
+ * gate,up F x H; down H x F; all 1-row-tile HSDB. Norm weights (H floats, host) required;
+ * q/k/v biases optional (NULL = none; the reference applies none). */
+CSDR_API int csdr_decoder_set_layer(csdr_decoder* dec, int layer, const csdr_hsdb* wq,
+                                    const csdr_hsdb* wk, const csdr_hsdb* wv, const csdr_hsdb* wo,
+                                    const csdr_hsdb* wgate, const csdr_hsdb* wup,
+                                    const csdr_hsdb* wdown, const float* attn_norm,
+                                    const float* ffn_norm, const float* bq, const float* bk,
+                                    const float* bv);
+/* Output projection (vocab x H) and output norm (NULL = none, as when output_norm_layer_name
+ * is empty, cortex_sdk.cpp:1682-1688); embedding NULL = tied (rows of lm_head). */
+CSDR_API int csdr_decoder_set_output(csdr_decoder* dec, const csdr_hsdb* lm_head,
+                                     const float* final_norm, const csdr_hsdb* embedding);
+/* Runs the prompt from position 0 (resetting the cache and the generated-token set) and
+ * selects the first new token (it lands at position n_prompt). */
+CSDR_API int csdr_decoder_prefill(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
+                                  float temperature, float penalty);
+/* n_steps further tokens, one graph replay each; synchronises at the end. */
+CSDR_API int csdr_decoder_decode(csdr_decoder* dec, int n_steps, float temperature,
+                                 float penalty);
+/* Host copy of the tokens at positions [first, first + count) (prompt, then generated). */
+CSDR_API int csdr_decoder_tokens(const csdr_decoder* dec, int first, int count, int32_t* out);
+/* generate_text's loop: prefill, then max_new_tokens - 1 decode steps; out_tokens receives
+ * up to max_new_tokens ids, *n_generated stops after eos_id (eos_id < 0: none). */
+CSDR_API int csdr_decoder_generate(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
+                                   int max_new_tokens, float temperature, float penalty,
+                                   int eos_id, int32_t* out_tokens, int* n_generated);
+/* Host copy of the last head step's lm_head scores (vocab floats, before temperature). */
+CSDR_API int csdr_decoder_logits(const csdr_decoder* dec, float* out);
+/* Number of positions processed so far (-1 for NULL). */
+CSDR_API int csdr_decoder_position(const csdr_decoder* dec);
+
 #ifdef __cplusplus
 }
 #endif

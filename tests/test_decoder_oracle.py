@@ -1,0 +1,103 @@
+"""Pins the oracle decoder (oracle/decoder.py) on tiny models against an independent float64
+dense restatement of the reference's block (api/cortex_sdk.cpp:1543-1696): dense W from the
+(reference-pinned) decompress, float64 RMSNorm, RoPE angles, grouped attention, SwiGLU and
+residuals written from the textbook definitions. A wrong residual, GQA mapping, RoPE pairing
+or norm placement in the oracle fails these."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import decoder as odec
+from cortexsdr_amd.decoder import DecoderSpec, synthetic_weights
+from conftest import rel_l2
+
+
+def dense_forward(w, tokens):
+    s = w.spec
+    T, hd, Hq, Hkv = len(tokens), s.head_dim, s.n_heads, s.n_kv_heads
+    dense = {}
+
+    def W(stream):
+        key = id(stream)
+        if key not in dense:
+            dense[key] = oracle.hsdr_decompress(stream).astype(np.float64)
+        return dense[key]
+
+    def norm(x, g):
+        return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + s.rms_eps) * g
+
+    def rot(x, heads):
+        x = x.reshape(T, heads, hd).copy()
+        i = np.arange(0, hd, 2)
+        ang = np.arange(T)[:, None] * (float(s.rope_theta) ** (-i / hd))[None, :]
+        c, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        a, b = x[..., 0::2].copy(), x[..., 1::2].copy()
+        x[..., 0::2] = a * c - b * sn
+        x[..., 1::2] = a * sn + b * c
+        return x
+
+    x = W(w.lm_head)[np.asarray(tokens)]
+    for L in w.layers:
+        h = norm(x, L["attn_norm"])
+        q = h @ W(L["q"]).T + L.get("bq", 0.0)
+        k = h @ W(L["k"]).T + L.get("bk", 0.0)
+        v = h @ W(L["v"]).T + L.get("bv", 0.0)
+        q, k = rot(q, Hq), rot(k, Hkv)
+        v = v.reshape(T, Hkv, hd)
+        a = np.zeros((T, Hq, hd))
+        for hh in range(Hq):
+            g = hh // (Hq // Hkv)
+            sc = q[:, hh] @ k[:, g].T / np.sqrt(hd)
+            sc[np.triu_indices(T, 1)] = -np.inf
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            a[:, hh] = p @ v[:, g]
+        x = x + a.reshape(T, -1) @ W(L["o"]).T
+        h = norm(x, L["ffn_norm"])
+        gt, up = h @ W(L["gate"]).T, h @ W(L["up"]).T
+        x = x + (gt / (1 + np.exp(-gt)) * up) @ W(L["down"]).T
+    return norm(x, w.final_norm)[-1], W(w.lm_head)
+
+
+SPECS = [
+    DecoderSpec(2, 128, 2, 1, 64, 200, 150, 32),   # GQA 2:1, FFN with an edge strip
+    DecoderSpec(1, 256, 2, 2, 128, 128, 97, 32),   # head_dim 128, MHA
+]
+
+
+@pytest.mark.parametrize("spec", SPECS)
+def test_oracle_decoder_matches_dense_float64(spec):
+    w = synthetic_weights(spec, n_atoms=64, nnz=4, seed=5, sigma=0.1, norm_jitter=0.1,
+                          bias_sigma=0.1)
+    tokens = [3, 17, 42, 8, 99 % spec.vocab, 1, 0, 64]
+    h32 = odec.hidden_last(w, tokens)
+    h64, lm = dense_forward(w, tokens)
+    assert rel_l2(h32, h64) < 1e-5
+    lg = odec.step_scores(w, tokens)
+    assert rel_l2(lg, lm @ h64) < 1e-5
+
+
+def test_oracle_sanitize():
+    h = np.array([1.0, np.nan, -3000.0, np.inf, 10.0], np.float32)
+    out = odec.sanitize(h)
+    np.testing.assert_allclose(out, [1 / 3, 0, -1000, 0, 10 / 3], rtol=1e-6)
+    small = np.array([5.0, -999.0], np.float32)
+    assert np.array_equal(odec.sanitize(small), small)
+
+
+def test_oracle_generate_forced_matches_free():
+    # the forced form equals the free run when forced with the free run's own tokens
+    spec = SPECS[0]
+    w = synthetic_weights(spec, n_atoms=64, nnz=4, seed=6, sigma=0.1)
+    toks, sc = odec.generate(w, [5, 6, 7], 4)
+    toks2, sc2 = odec.generate(w, [5, 6, 7], 4, forced=toks)
+    assert np.array_equal(toks, toks2)
+    assert all(np.array_equal(a, b) for a, b in zip(sc, sc2))
+    # the repeat penalty is applied to generated tokens: a repeated token only wins when its
+    # lead exceeds penalty * temperature-scaled margin
+    for i in range(1, 4):
+        ts = sc[i] / 0.8
+        rep = np.zeros(spec.vocab, bool)
+        rep[toks[:i]] = True
+        ts = np.where(rep, ts - 1.5, ts)
+        assert toks[i] == int(np.argmax(ts))
