@@ -16,6 +16,11 @@ The JSON line carries:
                 HIP events around K back-to-back gather launches on its stream
   cpu_baseline  the CPU restatement of the reference algorithm (oracle/, OpenMP) on a
                 bounded sample of the same workload, on this host's cores
+  decode        the metric's second half, configs[3]: Qwen2-0.5B-shaped decoder (24 layers,
+                hidden 896, 14/2 heads of 64, FFN 4864, vocab 151936, every linear
+                HSDB-coded against one shared 1024 x 64 dictionary), 512-token prompt of
+                uniform random ids, then greedy decode of 128 tokens; tokens/s of the decode
+                phase next to a KV-cached CPU decode step of the same model (oracle/)
 """
 from __future__ import annotations
 
@@ -40,6 +45,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2"])
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
+    ap.add_argument("--decode-cpu-seconds", type=float, default=5.0)
     return ap.parse_args()
 
 
@@ -79,6 +86,91 @@ def cpu_baseline(streams, xs, seconds):
             break
     dt = (time.perf_counter() - t0) / n
     return dt, n, threads
+
+
+def cpu_decode_step(w, ctx: int, seconds: float):
+    """Seconds per KV-cached decode step of the same model on the CPU restatement (oracle/):
+    per layer RMSNorm, the seven HSDB linears (orc_hsdb_matmul, OpenMP), RoPE, GQA attention
+    over `ctx` fp16 cached positions, SwiGLU; then output norm, lm_head scores, argmax."""
+    import oracle
+
+    s = w.spec
+    rng = np.random.default_rng(0)
+    kc = rng.standard_normal((1, ctx, s.n_kv_heads, s.head_dim)).astype(np.float16)
+    vc = rng.standard_normal((1, ctx, s.n_kv_heads, s.head_dim)).astype(np.float16)
+    kc, vc = kc.view(np.uint16), vc.view(np.uint16)
+    lens = np.array([ctx], np.int32)
+    x0 = rng.standard_normal(s.hidden).astype(np.float32)
+
+    def one():
+        x = x0.copy()
+        for L in w.layers:
+            h = oracle.rms_norm(x, L["attn_norm"]).reshape(-1, 1)
+            q = oracle.hsdb_matmul(L["q"], h)[:, 0]
+            k = oracle.hsdb_matmul(L["k"], h)[:, 0]
+            oracle.hsdb_matmul(L["v"], h)
+            q = oracle.rope(q, s.n_heads, s.head_dim, s.rope_theta, ctx - 1)
+            oracle.rope(k, s.n_kv_heads, s.head_dim, s.rope_theta, ctx - 1)
+            a = oracle.attn_decode(q.reshape(1, s.n_heads, s.head_dim), kc, vc, lens,
+                                   s.n_heads, s.n_kv_heads, s.head_dim)
+            x = x + oracle.hsdb_matmul(L["o"], a.reshape(-1, 1))[:, 0]
+            h = oracle.rms_norm(x, L["ffn_norm"]).reshape(-1, 1)
+            f = oracle.silu_mul(oracle.hsdb_matmul(L["gate"], h), oracle.hsdb_matmul(L["up"], h))
+            x = x + oracle.hsdb_matmul(L["down"], f)[:, 0]
+        h = oracle.rms_norm(x, w.final_norm).reshape(-1, 1)
+        oracle.select_best(oracle.hsdb_matmul(w.lm_head, h)[:, 0], None, 0.0, 0.0)
+
+    one()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        n += 1
+        if time.perf_counter() - t0 >= seconds and n >= 2:
+            break
+    return (time.perf_counter() - t0) / n, n
+
+
+def decode_leg(args):
+    """tokens/s of graph-replayed decode steps after a 512-token prefill."""
+    from cortexsdr_amd import synth
+    from cortexsdr_amd.decoder import QWEN2_0_5B, Decoder, synthetic_weights
+
+    spec, n_prompt, n_new = QWEN2_0_5B, 512, 128
+    w = synthetic_weights(spec, seed=0)
+    prompt = (synth.uniform(77, n_prompt, stream=61) * spec.vocab).astype(np.int32)
+    dec = Decoder(w)
+    try:
+        dec.prefill(prompt[:8], 0.0, 0.0)   # captures the step graphs; untimed
+        dec.decode(8, 0.0, 0.0)
+        t0 = time.perf_counter()
+        dec.prefill(prompt, 0.0, 0.0)       # greedy: temperature 0 (scale 1), no penalty
+        t_pre = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        dec.decode(n_new - 1, 0.0, 0.0)     # token 1 came from the prefill's last step
+        t_dec = time.perf_counter() - t0
+        toks = dec.tokens(n_prompt, n_new)
+    finally:
+        dec.close()
+    per_tok = t_dec / (n_new - 1)
+    out = {
+        "metric": "Qwen2-0.5B-shape decode tokens/sec",
+        "value": round(1.0 / per_tok, 1),
+        "unit": "tokens/s",
+        "ms_per_token": round(per_tok * 1e3, 4),
+        "prefill_tokens_per_s": round(n_prompt / t_pre, 1),
+        "workload": "cfg4: 512-token prompt, greedy decode of 128 tokens, batch 1",
+        "code_bytes_per_token": w.code_bytes(),
+        "first_tokens": toks[:4].tolist(),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        dt, n = cpu_decode_step(w, n_prompt + n_new // 2, args.decode_cpu_seconds)
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+        out["cpu_baseline"] = {
+            "value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"{n} KV-cached decode steps at context {n_prompt + n_new // 2} through "
+                       f"oracle/ (orc_hsdb_matmul OpenMP linears), {dt * 1e3:.0f} ms/token")}
+    return out
 
 
 def main():
@@ -233,6 +325,8 @@ def main():
                        f"oracle/csdr_oracle.c orc_hsdb_matmul with OpenMP, "
                        f"{dt * 1e3:.1f} ms/step"),
         }
+    if not args.no_decode:
+        out["decode"] = decode_leg(args)
     print(json.dumps(out), flush=True)
 
 

@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <new>
 #include <string>
@@ -116,6 +117,7 @@ struct csdr_decoder {
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     float g_temp = 0.0f, g_pen = 0.0f;  // sampling parameters graph[1] was captured with
     int host_pos = 0;                   // positions processed (host mirror of *pos)
+    bool use_graph = true;              // CSDR_DECODER_GRAPH=0: issue each step's kernels directly
     int n_prompt = 0;
     std::vector<void*> allocs;
 };
@@ -286,6 +288,13 @@ int ensure_graph(csdr_decoder* d, int i, float temperature, float penalty) {
     return CSDR_OK;
 }
 
+// One step: a replay of the captured graph, or the kernels issued directly on the stream.
+int run_step(csdr_decoder* d, int i, float temperature, float penalty) {
+    if (!d->use_graph) return step(d, d->stream, i == 1, temperature, penalty);
+    CSDR_HIP_CHECK(hipGraphLaunch(d->exec[i], d->stream));
+    return CSDR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -303,6 +312,7 @@ CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** 
     if (!d) return set_error(CSDR_E_INVALID, "decoder_create: out of host memory");
     d->cfg = c;
     d->layers.resize(c.n_layers);
+    if (const char* e = getenv("CSDR_DECODER_GRAPH")) d->use_graph = atoi(e) != 0;
     int rc = CSDR_OK;
     const size_t kvn = (size_t)c.max_ctx * c.n_kv_heads * c.head_dim;
     for (auto& L : d->layers)
@@ -417,16 +427,18 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
     for (int i = 0; i < n_prompt; ++i)
         if (prompt[i] < 0 || prompt[i] >= c.vocab)
             return set_error(CSDR_E_INVALID, "decoder_prefill: token id out of range");
-    RC(ensure_graph(d, 0, temperature, penalty));
-    RC(ensure_graph(d, 1, temperature, penalty));
+    if (d->use_graph) {
+        RC(ensure_graph(d, 0, temperature, penalty));
+        RC(ensure_graph(d, 1, temperature, penalty));
+    }
     hipStream_t st = d->stream;
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
     CSDR_HIP_CHECK(hipMemset(d->pos, 0, 4));
     CSDR_HIP_CHECK(hipMemset(d->repeated, 0, c.vocab));
     CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)(c.max_ctx + 1) * 4));
     CSDR_HIP_CHECK(hipMemcpy(d->ring, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
-    for (int i = 0; i + 1 < n_prompt; ++i) CSDR_HIP_CHECK(hipGraphLaunch(d->exec[0], st));
-    CSDR_HIP_CHECK(hipGraphLaunch(d->exec[1], st));
+    for (int i = 0; i + 1 < n_prompt; ++i) RC(run_step(d, 0, temperature, penalty));
+    RC(run_step(d, 1, temperature, penalty));
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
     d->host_pos = n_prompt;
     d->n_prompt = n_prompt;
@@ -439,8 +451,8 @@ CSDR_API int csdr_decoder_decode(csdr_decoder* d, int n_steps, float temperature
     if (d->n_prompt == 0) return set_error(CSDR_E_INVALID, "decoder_decode: prefill first");
     if (d->host_pos + n_steps > d->cfg.max_ctx)
         return set_error(CSDR_E_INVALID, "decoder_decode: context capacity exceeded");
-    RC(ensure_graph(d, 1, temperature, penalty));
-    for (int i = 0; i < n_steps; ++i) CSDR_HIP_CHECK(hipGraphLaunch(d->exec[1], d->stream));
+    if (d->use_graph) RC(ensure_graph(d, 1, temperature, penalty));
+    for (int i = 0; i < n_steps; ++i) RC(run_step(d, 1, temperature, penalty));
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
     d->host_pos += n_steps;
     return CSDR_OK;
