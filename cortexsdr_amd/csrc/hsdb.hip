@@ -35,21 +35,7 @@
 #include <vector>
 
 #include "common.hpp"
-
-struct csdr_hsdb {
-    uint32_t R = 0, C = 0, tile_rows = 1, tile_cols = 0, K = 0, S = 0, k = 0, slots = 0;
-    uint32_t n_row_tiles = 0, NB = 0, n_tiles = 0, R_full = 0, C_full = 0, Ce = 0;
-    uint32_t NBc = 1, nchunks = 1;
-    int is_hsdb = 0;
-    int device = 0;
-    float* d_dict = nullptr;        // K x tile_dim fp32
-    uint32_t* d_codes = nullptr;    // n_tiles * slots words
-    float* d_slot_gamma = nullptr;  // slots floats: gamma[j / k]
-    float* d_edge = nullptr;        // top-right strip (R_full x Ce) then bottom strip
-    float h_slot_gamma[32] = {};    // host copy of the first 32 slot gammas (kernel args)
-    size_t edge_floats = 0;
-    size_t device_bytes = 0;
-};
+#include "hsdb_impl.hpp"
 
 namespace {
 
@@ -671,6 +657,21 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     CSDR_HIP_CHECK(hipMalloc(&s->d_edge, std::max<size_t>(b_edge, 4)));
     s->device_bytes = b_dict + b_codes + b_gamma + b_edge;
     CSDR_HIP_CHECK(hipMemcpyAsync(s->d_dict, buf + off_dict, b_dict, hipMemcpyHostToDevice, st));
+    // 64-wide blocks: the dictionary also as fp16 (round to nearest even), each 64-row in
+    // the matrix-core k order (csdr::kperm64), for the batched product
+    std::vector<_Float16> dict16;
+    if (s->tile_rows == 1 && s->tile_cols == 64) {
+        const size_t n = (size_t)s->K * 64;
+        dict16.resize(n);
+        std::vector<float> d32(n);
+        std::memcpy(d32.data(), buf + off_dict, n * 4);
+        for (size_t i = 0; i < n; ++i)
+            dict16[(i & ~(size_t)63) + csdr::kperm64((int)(i & 63))] = (_Float16)d32[i];
+        CSDR_HIP_CHECK(hipMalloc(&s->d_dict16p, n * 2));
+        s->device_bytes += n * 2;
+        CSDR_HIP_CHECK(
+            hipMemcpyAsync(s->d_dict16p, dict16.data(), n * 2, hipMemcpyHostToDevice, st));
+    }
     if (b_codes)
         CSDR_HIP_CHECK(
             hipMemcpyAsync(s->d_codes, words.data(), b_codes, hipMemcpyHostToDevice, st));
@@ -686,6 +687,7 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
 void release(csdr_hsdb* s) {
     if (!s) return;
     if (s->d_dict) (void)hipFree(s->d_dict);
+    if (s->d_dict16p) (void)hipFree(s->d_dict16p);
     if (s->d_codes) (void)hipFree(s->d_codes);
     if (s->d_slot_gamma) (void)hipFree(s->d_slot_gamma);
     if (s->d_edge) (void)hipFree(s->d_edge);
@@ -714,10 +716,19 @@ size_t p_bytes(const csdr_hsdb* s, int M) {
     return csdr::align_up((size_t)s->NB * s->K * M * 4, 256);
 }
 
-size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
+// Workspace of the P path (dx + gather launches).
+size_t p_path_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
     size_t t = kWsHeader;
     for (int i = 0; i < n; ++i) t += p_bytes(segs[i], M);
     return t;
+}
+
+// Workspace of a full product at batch M, large enough for every batch <= M as well (the
+// MFMA path at M >= 16 needs less than the P path at M = 15).
+size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
+    if (csdr::mfma_eligible(n, segs, M))
+        return std::max(csdr::mfma_workspace_bytes(n, segs, M), p_path_ws_bytes(n, segs, 15));
+    return p_path_ws_bytes(n, segs, M);
 }
 
 template <int PPT>
@@ -747,7 +758,14 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
                                              std::to_string(kMaxGroup) + ")");
     if (x_dtype != CSDR_F32 && x_dtype != CSDR_F16)
         return set_error(CSDR_E_INVALID, "hsdb_matmul: x_dtype must be CSDR_F32 or CSDR_F16");
-    const size_t need = group_ws_bytes(n, segs, M);
+    for (int i = 0; i < n; ++i)
+        if (!segs[i] || !xs[i] || !ys[i])
+            return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
+    if (phases == (kPhaseDx | kPhaseGather) && csdr::mfma_eligible(n, segs, M))
+        return csdr::mfma_matmul(n, segs, xs, x_dtype, M, ys, bias,
+                                 (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0, workspace,
+                                 workspace_bytes, st);
+    const size_t need = p_path_ws_bytes(n, segs, M);
     if (!workspace || workspace_bytes < need)
         return set_error(CSDR_E_WORKSPACE,
                          "hsdb_matmul: workspace needs " + std::to_string(need) + " bytes");

@@ -1,0 +1,468 @@
+// hsdb_mfma.hip — batched (M >= 16) block-coded product Y = W.X on gfx950 matrix cores.
+//
+// Path (cortexSDR tree): HierarchicalSDRStrategy::matmulRowMajor with batch > 1
+// (strategies/HierarchicalSDRStrategy.cpp:1257-1338), block-coded as in research
+// exp_c_kernel/benchmark.py:106-130. W is never stored: each 64-column tile of a 128-row
+// strip is decoded into registers straight in the MFMA A-operand layout and multiplied
+// against the matching 64 x M slice of X.
+//
+// Decode: W[r][k] = sum_j c_j * D[idx_j][k] in fp32 over the row's slots, with the dictionary
+// held in LDS as fp16 (K <= 1024 atoms: 128 KiB), then rounded to fp16 for the MFMA
+// (v_mfma_f32_16x16x16f16, fp32 accumulation). X is fp16 as given, or split into fp16
+// hi + lo parts for fp32 input (two MFMAs). The two fp16 roundings (D, decoded W) keep the
+// product within ~2e-4 relative L2 of the fp32 decode.
+//
+// Layout. MFMA 16x16x16: lane l holds A[l%16][4(l/16)+i], B[4(l/16)+i][l%16] and the
+// result D[4(l/16)+i][l%16] (i = 0..3). Every 64-long k range (one block column) is stored
+// permuted, k = 16s + 4q + i at position 16q + 4s + i, in both the LDS dictionary and the
+// transposed X, so lane l (q = l/16) reads its 16 k values for the four 16-deep MFMA steps
+// as one contiguous 32-byte run.
+//
+// Launches: an init kernel (Y = bias (+ Y when accumulating) + the fp32 edge strip times X,
+// and X transposed to fp16 [m][k] with the permutation, in the workspace), then one
+// persistent kernel: workgroup = 4 waves x 32 rows; the (row strip, block column) units of
+// all matrices are split in contiguous ranges over the workgroups, and each strip's
+// partial sums are added into Y with device-scope float atomics.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <string>
+
+#include "common.hpp"
+#include "hsdb_impl.hpp"
+
+namespace {
+
+using csdr::set_error;
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kMaxAtoms = 1024;
+constexpr int kMaxMTile = 256;
+constexpr int kGroup = 8;
+constexpr size_t kWsHeader = 256;
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+struct MDesc {
+    const uint32_t* codes;
+    const _Float16* dict16p;  // K x 64 fp16, rows in kperm64 order
+    const float* edge;
+    const void* x;
+    float* y;
+    const float* bias;
+    _Float16* xt;  // Mpad x C_full fp16 (hi), then Mpad x C_full (lo) for fp32 X
+    int R, K, NB, NBc, slots, Ce, C_full;
+    int u_base, u_count;  // units (row strip x block column) [u_base, u_base + u_count)
+    float sgam[16];
+};
+
+struct MParams {
+    MDesc m[kGroup];
+    int G, M, Mpad, x_f16, accumulate, total_units;
+    int m0;  // first column of this launch (the launch covers 16 * NT columns)
+};
+
+__device__ __forceinline__ float xget(const MParams& p, const MDesc& d, size_t i) {
+    return p.x_f16 ? (float)static_cast<const _Float16*>(d.x)[i]
+                   : static_cast<const float*>(d.x)[i];
+}
+
+// ---- init: Y start values, and X transposed to [m][k] fp16 in 16-byte granules of the
+// permuted k order (threads run along m, so the X reads coalesce).
+__global__ __launch_bounds__(kThreads) void mfma_init_kernel(MParams p) {
+    const MDesc& d = p.m[blockIdx.y];
+    const int M = p.M;
+    const size_t ny = (size_t)d.R * M;
+    const size_t ngr = (size_t)p.Mpad * d.NB * 8;
+    const size_t nx = (size_t)p.Mpad * d.C_full;
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < ny + ngr; t += stride) {
+        if (t < ny) {
+            const int r = (int)(t / M), m = (int)(t - (size_t)r * M);
+            float v = p.accumulate ? d.y[t] : 0.0f;
+            if (d.bias) v += d.bias[r];
+            if (d.Ce > 0) {
+                const float* e = d.edge + (size_t)r * d.Ce;
+                float s = 0.0f;
+                for (int cc = 0; cc < d.Ce; ++cc)
+                    s = fmaf(e[cc], xget(p, d, (size_t)(d.C_full + cc) * M + m), s);
+                v += s;
+            }
+            d.y[t] = v;
+        } else {
+            const size_t u = t - ny;
+            const int m = (int)(u % p.Mpad);
+            const size_t bg = u / p.Mpad;
+            const int b = (int)(bg >> 3), g = (int)(bg & 7);
+            _Float16 hi[8], lo[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int k = b * 64 + csdr::kperm64(g * 8 + j);
+                const float xv = (m < M) ? xget(p, d, (size_t)k * M + m) : 0.0f;
+                hi[j] = (_Float16)xv;
+                lo[j] = (_Float16)(xv - (float)hi[j]);
+            }
+            const size_t o = (size_t)m * d.C_full + (size_t)b * 64 + g * 8;
+            *reinterpret_cast<u32x4*>(d.xt + o) = __builtin_bit_cast(u32x4, hi);
+            if (!p.x_f16)
+                *reinterpret_cast<u32x4*>(d.xt + nx + o) = __builtin_bit_cast(u32x4, lo);
+        }
+    }
+}
+
+__device__ __forceinline__ int find_matrix(const MParams& p, int u, int g) {
+    if (g >= 0 && u >= p.m[g].u_base && u < p.m[g].u_base + p.m[g].u_count) return g;
+    g = 0;
+    while (g + 1 < p.G && u >= p.m[g + 1].u_base) ++g;
+    return g;
+}
+
+// ---- main: persistent; NT = 16-column tiles of this launch, XS = fp32-X split, W waves of
+// 32 rows (strip = 32 W rows). The codes and X slice of unit u + 1 are loaded into registers
+// while unit u is decoded and multiplied. One workgroup per CU (the dictionary fills most of
+// the LDS), so latency is hidden by the W waves of that workgroup.
+template <int NT, bool XS, int W>
+__global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
+    constexpr int kThreads = W * 64;
+    constexpr int kStripRows = W * 32;
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem16[];
+    constexpr int MT = NT * 16;
+    constexpr int NGR = MT * 8 * (XS ? 2 : 1);  // 16-byte X granules per unit
+    constexpr int GPT = (NGR + kThreads - 1) / kThreads;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int q = lane >> 4, rl = lane & 15;
+    const int U = p.total_units;
+    const int u0 = (int)((long long)U * blockIdx.x / gridDim.x);
+    const int u1 = (int)((long long)U * (blockIdx.x + 1) / gridDim.x);
+    if (u0 >= u1) return;
+    // K x 64; 16-byte granule g of atom a at g ^ ((a >> 1) & 7): rows are 128 bytes, so
+    // without it the 16 lanes of one k segment would meet in two bank groups
+    _Float16* Ds = smem16;
+    _Float16* Xs = smem16 + (size_t)kMaxAtoms * 64;  // MT x 64 (hi), then MT x 64 (lo)
+    const int M = p.M;
+
+    floatx4 acc[2][NT];
+    u32x4 xr[GPT];   // prefetched X granules of the next unit
+    u32x4 cr[2][4];  // prefetched code words of the next unit (2 row tiles, <= 16 slots)
+    int ng = -1, nstrip = 0, nb = 0;  // the prefetched unit
+
+    auto prefetch = [&](int u) {
+        ng = find_matrix(p, u, ng);
+        const MDesc& d = p.m[ng];
+        const int lu = u - d.u_base;
+        nstrip = lu / d.NB;
+        nb = lu - nstrip * d.NB;
+        const size_t nxt = (size_t)p.Mpad * d.C_full;
+#pragma unroll
+        for (int i = 0; i < GPT; ++i) {
+            const int gi = min(tid + i * kThreads, NGR - 1);
+            const int part = XS ? gi / (MT * 8) : 0;
+            const int gg = gi - part * MT * 8;
+            const int mrow = gg >> 3, gr = gg & 7;
+            xr[i] = *reinterpret_cast<const u32x4*>(
+                d.xt + part * nxt + (size_t)(p.m0 + mrow) * d.C_full + (size_t)nb * 64 + gr * 8);
+        }
+        const int c = nb / d.NBc, bb = nb - c * d.NBc;
+        const int nbc = min(d.NBc, d.NB - c * d.NBc);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int r = min(nstrip * kStripRows + wave * 32 + rt * 16 + rl, d.R - 1);
+            const uint32_t* cw =
+                d.codes + ((size_t)c * d.NBc * d.R + (size_t)r * nbc + bb) * d.slots;
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4)
+                cr[rt][j4] = *reinterpret_cast<const u32x4*>(cw + min(j4 * 4, d.slots - 4));
+        }
+    };
+
+    auto flush = [&](int g, int strip) {
+        const MDesc& d = p.m[g];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int rbase = strip * kStripRows + wave * 32 + rt * 16 + q * 4;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int m = p.m0 + nt * 16 + rl;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = rbase + i;
+                    if (r < d.R && m < M)
+                        __hip_atomic_fetch_add(d.y + (size_t)r * M + m, acc[rt][nt][i],
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+    };
+
+    int cur_g = -1, cur_strip = -1;
+    prefetch(u0);
+    for (int u = u0; u < u1; ++u) {
+        const int g = ng, strip = nstrip, b = nb;
+        (void)b;
+        const MDesc& d = p.m[g];
+        if (g != cur_g || strip != cur_strip) {
+            if (cur_strip >= 0) flush(cur_g, cur_strip);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (g != cur_g) {
+                // the matrix's fp16 dictionary -> LDS (16-byte granules, 8 loads in flight)
+                __syncthreads();
+                const int n = d.K * 8;
+                for (int i0 = 0; i0 < n; i0 += kThreads * 8) {
+                    u32x4 v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        v[j] = *reinterpret_cast<const u32x4*>(
+                            d.dict16p + (size_t)min(i0 + j * kThreads + tid, n - 1) * 8);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int i = i0 + j * kThreads + tid;
+                        const int a = i >> 3, gr = i & 7;
+                        if (i < n)
+                            *reinterpret_cast<u32x4*>(Ds + (size_t)a * 64 +
+                                                      ((gr ^ ((a >> 1) & 7)) * 8)) = v[j];
+                    }
+                }
+            }
+            cur_g = g;
+            cur_strip = strip;
+        }
+        // X slice -> LDS; granule index XOR (row & 7) against bank conflicts
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < GPT; ++i) {
+            const int gi = min(tid + i * kThreads, NGR - 1);
+            const int part = XS ? gi / (MT * 8) : 0;
+            const int gg = gi - part * MT * 8;
+            const int mrow = gg >> 3, gr = gg & 7;
+            *reinterpret_cast<u32x4*>(Xs + (size_t)part * MT * 64 + mrow * 64 +
+                                      ((gr ^ (mrow & 7)) * 8)) = xr[i];
+        }
+        u32x4 cc[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4) cc[rt][j4] = cr[rt][j4];
+        const int slots = d.slots;
+        float sg[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sg[j] = d.sgam[j];
+        __syncthreads();
+        if (u + 1 < u1) prefetch(u + 1);
+        // decode this lane's 16 k values of its two rows (fp32 sums of fp16 atoms)
+        half4 a[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            float w[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) w[t] = 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4) {
+                if (j4 * 4 < slots) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const uint32_t word = cc[rt][j4][jj];
+                        const float cf = sg[j4 * 4 + jj] * csdr::h2f(word >> 16);
+                        const uint32_t a = word & 0x7FFFu;
+                        const uint32_t sw = (a >> 1) & 7;
+                        const _Float16* drow = Ds + a * 64;
+                        const u32x4 lo =
+                            *reinterpret_cast<const u32x4*>(drow + (((2 * q) ^ sw) * 8));
+                        const u32x4 hi =
+                            *reinterpret_cast<const u32x4*>(drow + (((2 * q + 1) ^ sw) * 8));
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            w[2 * t] = fmaf(cf, csdr::h2f(lo[t] & 0xFFFFu), w[2 * t]);
+                            w[2 * t + 1] = fmaf(cf, csdr::h2f(lo[t] >> 16), w[2 * t + 1]);
+                            w[8 + 2 * t] = fmaf(cf, csdr::h2f(hi[t] & 0xFFFFu), w[8 + 2 * t]);
+                            w[9 + 2 * t] = fmaf(cf, csdr::h2f(hi[t] >> 16), w[9 + 2 * t]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                a[rt][s] = half4{(_Float16)w[4 * s], (_Float16)w[4 * s + 1],
+                                 (_Float16)w[4 * s + 2], (_Float16)w[4 * s + 3]};
+        }
+        // MFMA over the four 16-deep steps of the block column
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = nt * 16 + rl;
+            const int g0 = (2 * q) ^ (n & 7), g1 = (2 * q + 1) ^ (n & 7);
+#pragma unroll
+            for (int part = 0; part < (XS ? 2 : 1); ++part) {
+                const _Float16* xrow = Xs + (size_t)part * MT * 64 + n * 64;
+                const u32x4 b0 = *reinterpret_cast<const u32x4*>(xrow + g0 * 8);
+                const u32x4 b1 = *reinterpret_cast<const u32x4*>(xrow + g1 * 8);
+                half4 bs[4];
+                bs[0] = __builtin_bit_cast(half4, u32x2{b0[0], b0[1]});
+                bs[1] = __builtin_bit_cast(half4, u32x2{b0[2], b0[3]});
+                bs[2] = __builtin_bit_cast(half4, u32x2{b1[0], b1[1]});
+                bs[3] = __builtin_bit_cast(half4, u32x2{b1[2], b1[3]});
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                            a[rt][s], bs[s], acc[rt][nt], 0, 0, 0);
+            }
+        }
+    }
+    if (cur_strip >= 0) flush(cur_g, cur_strip);
+}
+
+// Columns of X the kernels see: M rounded up to a power of two >= 16 (<= 256), beyond 256 to
+// a multiple of 256, so every launch covers a power-of-two tile of 16 NT columns.
+int padded_m(int M) {
+    if (M > kMaxMTile) return (M + kMaxMTile - 1) / kMaxMTile * kMaxMTile;
+    int p = 16;
+    while (p < M) p *= 2;
+    return p;
+}
+
+size_t xt_bytes(const csdr_hsdb* s, int M) {
+    const size_t mpad = (size_t)padded_m(M);
+    return csdr::align_up(2 * mpad * s->C_full * sizeof(_Float16), 256);
+}
+
+// Waves per workgroup for a column tile of 16 NT: more waves hide more load latency; the
+// register budget (accumulators grow with NT) caps it.
+constexpr int waves_for(int nt) { return nt <= 1 ? 16 : (nt <= 4 ? 8 : 4); }
+
+template <int NT, bool XS>
+int launch_one(const MParams& p, int grid, size_t lds, hipStream_t st) {
+    constexpr int W = waves_for(NT);
+    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W>);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    mfma_kernel<NT, XS, W><<<grid, W * 64, lds, st>>>(p);
+    CSDR_LAUNCH_CHECK("hsdb mfma");
+    return CSDR_OK;
+}
+
+template <int NT>
+int launch_main(const MParams& p, bool xs, int grid, size_t lds, hipStream_t st) {
+    return xs ? launch_one<NT, true>(p, grid, lds, st) : launch_one<NT, false>(p, grid, lds, st);
+}
+
+}  // namespace
+
+namespace csdr {
+
+bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M) {
+    if (M < 16) return false;
+    const char* e = std::getenv("CSDR_HSDB_MFMA");
+    if (e && *e && std::atoi(e) == 0) return false;
+    for (int i = 0; i < n; ++i) {
+        const csdr_hsdb* s = segs[i];
+        if (!s || s->tile_rows != 1 || s->tile_cols != 64 || s->K > (uint32_t)kMaxAtoms ||
+            !s->d_dict16p ||
+            s->NB == 0 || !(s->slots == 4 || s->slots == 8 || s->slots == 16))
+            return false;
+    }
+    return true;
+}
+
+size_t mfma_workspace_bytes(int n, const csdr_hsdb* const* segs, int M) {
+    size_t t = kWsHeader;
+    for (int i = 0; i < n; ++i) t += xt_bytes(segs[i], M);
+    return t;
+}
+
+int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
+                float* const* ys, const float* const* bias, int accumulate, void* workspace,
+                size_t workspace_bytes, hipStream_t st) {
+    const size_t need = mfma_workspace_bytes(n, segs, M);
+    if (!workspace || workspace_bytes < need)
+        return set_error(CSDR_E_WORKSPACE,
+                         "hsdb_matmul: workspace needs " + std::to_string(need) + " bytes");
+    MParams p{};
+    p.G = n;
+    p.M = M;
+    p.Mpad = padded_m(M);
+    p.x_f16 = (x_dtype == CSDR_F16);
+    p.accumulate = accumulate;
+    char* ws = static_cast<char*>(workspace);
+    size_t off = kWsHeader;
+    size_t max_elems = 0;
+    for (int i = 0; i < n; ++i) {
+        const csdr_hsdb* s = segs[i];
+        MDesc& d = p.m[i];
+        d.codes = s->d_codes;
+        d.dict16p = s->d_dict16p;
+        d.edge = s->d_edge;
+        d.x = xs[i];
+        d.y = ys[i];
+        d.bias = bias ? bias[i] : nullptr;
+        d.xt = reinterpret_cast<_Float16*>(ws + off);
+        off += xt_bytes(s, M);
+        d.R = (int)s->R;
+        d.K = (int)s->K;
+        d.NB = (int)s->NB;
+        d.NBc = (int)s->NBc;
+        d.slots = (int)s->slots;
+        d.Ce = (int)s->Ce;
+        d.C_full = (int)s->C_full;
+        for (uint32_t j = 0; j < s->slots && j < 16; ++j) d.sgam[j] = s->h_slot_gamma[j];
+        max_elems = std::max(max_elems, (size_t)d.R * M + (size_t)p.Mpad * d.NB * 8);
+    }
+    int dev = 0, ncu = 256, lds_max = 65536;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            v > 0)
+            ncu = v;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                hipSuccess &&
+            v > 0)
+            lds_max = v;
+    }
+    {
+        const int gx = (int)std::min<size_t>(2048, (max_elems + kThreads - 1) / kThreads);
+        mfma_init_kernel<<<dim3(std::max(gx, 1), n), kThreads, 0, st>>>(p);
+        CSDR_LAUNCH_CHECK("hsdb mfma init");
+    }
+    const bool xsplit = !p.x_f16;
+    const size_t dict_lds = (size_t)kMaxAtoms * 64 * sizeof(_Float16);
+    // widest power-of-two column tile whose X slice fits next to the dictionary
+    int mt = std::min(p.Mpad, kMaxMTile);
+    while (mt > 16 && dict_lds + (size_t)mt * 64 * 2 * (xsplit ? 2 : 1) > (size_t)lds_max)
+        mt /= 2;
+    const size_t lds = dict_lds + (size_t)mt * 64 * 2 * (xsplit ? 2 : 1);
+    if (lds > (size_t)lds_max)
+        return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: LDS too small for the MFMA path");
+    const int nt = mt / 16;
+    const int strip_rows = 32 * waves_for(nt);
+    int units = 0;
+    for (int i = 0; i < n; ++i) {
+        MDesc& d = p.m[i];
+        d.u_base = units;
+        d.u_count = (d.R + strip_rows - 1) / strip_rows * d.NB;
+        units += d.u_count;
+    }
+    p.total_units = units;
+    const int grid = std::max(1, std::min(units, ncu));
+    for (int m0 = 0; m0 < p.Mpad; m0 += mt) {
+        MParams q = p;
+        q.m0 = m0;
+        int rc;
+        switch (nt) {
+            case 16: rc = launch_main<16>(q, xsplit, grid, lds, st); break;
+            case 8: rc = launch_main<8>(q, xsplit, grid, lds, st); break;
+            case 4: rc = launch_main<4>(q, xsplit, grid, lds, st); break;
+            case 2: rc = launch_main<2>(q, xsplit, grid, lds, st); break;
+            default: rc = launch_main<1>(q, xsplit, grid, lds, st); break;
+        }
+        if (rc != CSDR_OK) return rc;
+    }
+    return CSDR_OK;
+}
+
+}  // namespace csdr

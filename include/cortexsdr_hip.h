@@ -98,8 +98,10 @@ CSDR_API int csdr_hsdb_load(const void* stream, size_t nbytes, void* hip_stream,
 CSDR_API int csdr_hsdb_free(csdr_hsdb* seg);
 CSDR_API int csdr_hsdb_get_info(const csdr_hsdb* seg, csdr_hsdb_info* info);
 
-/* Device workspace bytes csdr_hsdb_matmul needs for batch M (it holds P = D . X). Calls
- * that share a workspace must be ordered (same stream); concurrent calls need their own. */
+/* Device workspace bytes csdr_hsdb_matmul needs for batch M (P = D . X for M < 16, the
+ * transposed fp16 X for the matrix-core path at M >= 16); enough for every batch <= M too.
+ * Calls that share a workspace must be ordered (same stream); concurrent calls need their
+ * own. */
 CSDR_API size_t csdr_hsdb_workspace_bytes(const csdr_hsdb* seg, int M);
 
 /* Y = W . X with W never materialised. X: device, (C x M) row-major (feature-major, the
@@ -110,18 +112,23 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
                               void* hip_stream);
 
 /* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
- * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches:
- * a dx launch (P = D . X per block column into the workspace, Y = 0) and a gather launch
- * (Y += the coded rows gathered from P). The workspace is
- * csdr_hsdb_group_workspace_bytes(n, segs, M) bytes. csdr_hsdb_matmul is the n = 1 case.
- * Y rows are accumulated over block-column chunks with device-scope float atomics, so
+ * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
+ * M < 16: a dx launch (P = D . X per block column into the workspace, Y = 0) and a gather
+ * launch (Y += the coded rows gathered from P), all fp32. M >= 16 (64-column blocks, K <=
+ * 1024 atoms, 4/8/16 slots): an init launch and a matrix-core launch that decodes 64-column
+ * tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
+ * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
+ * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace
+ * is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes. csdr_hsdb_matmul is the n = 1 case.
+ * Y rows are accumulated over block-column ranges with device-scope float atomics, so
  * repeated calls agree to fp32 rounding, not bit for bit. */
 CSDR_API size_t csdr_hsdb_group_workspace_bytes(int n, const csdr_hsdb* const* segs, int M);
 CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const void* const* x,
                                     int x_dtype, int M, float* const* y, void* workspace,
                                     size_t workspace_bytes, void* hip_stream);
-/* The two launches of csdr_hsdb_matmul_group, separately (same arguments; dx must precede
- * gather on the stream, with the same workspace and X). */
+/* The two launches of the P path of csdr_hsdb_matmul_group, separately, at any M (same
+ * arguments; dx must precede gather on the stream, with the same workspace and X; the
+ * workspace must hold P: NB * K * M floats per matrix plus 256 bytes, rounded up to 256). */
 CSDR_API int csdr_hsdb_dx_group(int n, const csdr_hsdb* const* segs, const void* const* x,
                                 int x_dtype, int M, float* const* y, void* workspace,
                                 size_t workspace_bytes, void* hip_stream);
