@@ -88,6 +88,72 @@ SIGNATURES = {
 }
 
 
+class SegmentInfo(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p), ("data_format", C.c_char_p), ("layer_type", C.c_char_p),
+        ("layer_name", C.c_char_p), ("original_type", C.c_uint32), ("strategy_id", C.c_uint32),
+        ("original_size", C.c_uint64), ("compressed_size", C.c_uint64),
+        ("data_offset", C.c_uint64), ("layer_index", C.c_uint32), ("has_metadata", C.c_uint32),
+        ("n_dims", C.c_uint32), ("dims", C.c_uint32 * 8), ("sparsity_ratio", C.c_float),
+        ("n_input_dims", C.c_uint32), ("input_shape", C.c_uint32 * 8),
+        ("n_output_dims", C.c_uint32), ("output_shape", C.c_uint32 * 8),
+    ]
+
+
+class Dictionary(C.Structure):
+    _fields_ = [
+        ("tile_rows", C.c_uint32), ("tile_cols", C.c_uint32), ("n_atoms", C.c_uint32),
+        ("n_stages", C.c_uint32), ("k_per_stage", C.c_uint32), ("stage_decay", C.c_float),
+        ("stage_scales", C.c_void_p), ("n_stage_scales", C.c_uint32), ("atoms", C.c_void_p),
+        ("n_atom_floats", C.c_size_t),
+    ]
+
+
+class CortexError(C.Structure):
+    _fields_ = [("message", C.c_char_p), ("code", C.c_int)]
+
+
+_ce = CortexError
+SIGNATURES.update({
+    "csdr_archive_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "csdr_archive_close": (C.c_int, [_vp]),
+    "csdr_archive_count": (_sz, [_vp]),
+    "csdr_archive_info": (C.c_int, [_vp, _sz, C.POINTER(SegmentInfo)]),
+    "csdr_archive_find": (C.c_int, [_vp, C.c_char_p, C.POINTER(_sz)]),
+    "csdr_archive_read": (C.c_int, [_vp, _sz, _vp, _sz, C.POINTER(_sz)]),
+    "csdr_hsdb_load_codes": (C.c_int, [_vp, _sz, C.POINTER(Dictionary), _vp, C.POINTER(_vp)]),
+    "csdr_hsda_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "csdr_hsda_open_memory": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
+    "csdr_hsda_close": (C.c_int, [_vp]),
+    "csdr_hsda_count": (_sz, [_vp]),
+    "csdr_hsda_dictionary_count": (_sz, [_vp]),
+    "csdr_hsda_segment": (C.c_int, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint64)]),
+    "csdr_hsda_load": (C.c_int, [_vp, C.c_char_p, _vp, C.POINTER(_vp)]),
+    "csdr_dense_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
+    "cortex_inference_engine_create": (_ce, [C.c_char_p, C.POINTER(_vp)]),
+    "cortex_inference_engine_free": (_ce, [_vp]),
+    "cortex_inference_engine_set_batch_size": (_ce, [_vp, _sz]),
+    "cortex_inference_engine_enable_dropout": (_ce, [_vp, C.c_int]),
+    "cortex_inference_engine_set_mode": (_ce, [_vp, C.c_int]),
+    "cortex_inference_engine_init_memory_pool": (_ce, [_vp, _sz]),
+    "cortex_inference_engine_enable_aggressive_memory": (_ce, [_vp, C.c_int]),
+    "cortex_inference_engine_get_memory_usage": (_ce, [_vp, C.POINTER(_sz)]),
+    "cortex_inference_engine_enable_layer_prefetch": (_ce, [_vp, C.c_int]),
+    "cortex_inference_engine_get_last_run_stats_json": (_ce, [_vp, C.POINTER(C.c_void_p)]),
+    "cortex_free_string": (None, [C.c_void_p]),
+    "cortex_error_free": (None, [C.POINTER(CortexError)]),
+    "cortex_inference_engine_run": (_ce, [_vp, _vp, _sz, _vp, _sz, C.POINTER(_sz)]),
+    "cortex_inference_engine_run_layer": (_ce, [_vp, C.c_char_p, _vp, _sz, _vp, _sz,
+                                                C.POINTER(_sz)]),
+    "cortex_inference_engine_generate_text": (_ce, [_vp, C.c_char_p, C.c_int,
+                                                    C.POINTER(C.c_void_p)]),
+    "cortex_sdk_version": (C.c_char_p, []),
+    "cortex_inference_engine_matmul_device": (_ce, [_vp, C.c_char_p, _vp, C.c_int, C.c_int,
+                                                    _vp, _vp]),
+})
+
+
 class DecoderConfig(C.Structure):
     _fields_ = [
         ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int),

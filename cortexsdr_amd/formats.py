@@ -183,3 +183,108 @@ def pack_q4k(d16: np.ndarray, dmin16: np.ndarray, sc: np.ndarray, mn: np.ndarray
     blk[:, 4:16] = pack_q4k_scales(sc, mn)
     blk[:, 16:144] = qs
     return blk.tobytes()
+
+
+# ------------------------------------------------------------------ .sdr archive writer
+
+# SegmentType (core/ModelSegment.hpp:35-55), stored as u8 in the archive index.
+SEGMENT_TYPES = {
+    "UNKNOWN": 0, "WEIGHTS_FP32": 1, "WEIGHTS_FP16": 2, "WEIGHTS_INT8": 3, "WEIGHTS_INT4": 4,
+    "SPARSE_INDICES": 5, "METADATA_JSON": 6, "METADATA_TOML": 7, "TOKENIZER_VOCAB": 8,
+    "TOKENIZER_MODEL": 9, "CONFIG": 10, "ATTENTION_WEIGHTS": 11, "FEED_FORWARD_WEIGHTS": 12,
+    "EMBEDDING_WEIGHTS": 13, "LAYER_NORM_WEIGHTS": 14, "MODEL_INPUT": 15, "MODEL_OUTPUT": 16,
+    "GRAPH_STRUCTURE_PROTO": 17,
+}
+
+HSDR_STRATEGY_ID = 5
+
+
+@dataclass
+class SdrEntry:
+    """One segment of a .sdr archive (CompressedSegmentHeader, core/AICompressor.hpp:51-65)."""
+    name: str
+    payload: bytes
+    strategy_id: int = 0
+    data_format: str = "f32"
+    layer_type: str = ""
+    original_type: int = 1
+    original_size: int | None = None
+    layer_name: str = ""
+    layer_index: int = 0
+    dims: tuple | None = None
+    sparsity: float = 0.0
+    input_shape: tuple = ()
+    output_shape: tuple = ()
+
+
+def _str(s: str) -> bytes:
+    b = s.encode()
+    return struct.pack("<I", len(b)) + b
+
+
+def write_sdr(path: str, entries, version: int = 2) -> None:
+    """A .sdr archive as AICompressor::compressModel writes it (AICompressor.cpp:233-309):
+    magic "CORTEXSR", u32 version, u64 segment count, u64 index offset, the payloads, then
+    the index (strings u32-length-prefixed, bools one byte)."""
+    out = bytearray(b"CORTEXSR" + struct.pack("<IQQ", version, len(entries), 0))
+    offsets = []
+    for e in entries:
+        offsets.append(len(out))
+        out += bytes(e.payload)
+    index_off = len(out)
+    for e, off in zip(entries, offsets):
+        out += _str(e.name)
+        if version >= 2:
+            out += _str(e.data_format)
+        out += _str(e.layer_type)
+        orig = e.original_size if e.original_size is not None else len(e.payload)
+        out += struct.pack("<BBQQQ", e.original_type, e.strategy_id, orig, len(e.payload), off)
+        out += _str(e.layer_name)
+        out += struct.pack("<I", e.layer_index)
+        if e.dims is not None:
+            out += struct.pack("<BB", 1, len(e.dims))
+            out += struct.pack(f"<{len(e.dims)}I", *e.dims)
+            out += struct.pack("<fBBB", e.sparsity, 0, 0, 0)  # sparsity, sorted, no scale/zp
+        else:
+            out += b"\x00"
+        for shape in (e.input_shape, e.output_shape):
+            if shape:
+                out += struct.pack("<BB", 1, len(shape)) + struct.pack(f"<{len(shape)}I", *shape)
+            else:
+                out += b"\x00"
+    struct.pack_into("<Q", out, 20, index_off)
+    with open(path, "wb") as f:
+        f.write(out)
+
+
+def hsdb_entry(name: str, stream: bytes, **kw) -> SdrEntry:
+    """A strategy-5 entry for an HSDR/HSDB stream (dims from its header)."""
+    h = parse_header(stream)
+    return SdrEntry(name=name, payload=stream, strategy_id=HSDR_STRATEGY_ID, data_format="f32",
+                    original_size=h.rows * h.cols * 4, dims=(h.rows, h.cols), **kw)
+
+
+def vector_entry(name: str, v: np.ndarray, original_type: int = 14) -> SdrEntry:
+    v = np.ascontiguousarray(v, np.float32)
+    return SdrEntry(name=name, payload=v.tobytes(), original_type=original_type, dims=(v.size,))
+
+
+def decoder_entries(weights) -> list:
+    """The segments of a DecoderWeights under GGUF tensor names (token_embd, output_norm,
+    blk.N.attn_q ... ffn_down), the names discover_native_llm_paths keys on
+    (api/cortex_sdk.cpp:477-545). Tied embeddings: token_embd holds the lm_head codes."""
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
+             "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}
+    ents = [hsdb_entry("token_embd.weight", weights.lm_head, original_type=13)]
+    if weights.final_norm is not None:
+        ents.append(vector_entry("output_norm.weight", weights.final_norm))
+    for l, L in enumerate(weights.layers):
+        ents.append(vector_entry(f"blk.{l}.attn_norm.weight", L["attn_norm"]))
+        for key in ("q", "k", "v", "o"):
+            ents.append(hsdb_entry(f"blk.{l}.{names[key]}.weight", L[key], original_type=11,
+                                   layer_index=l))
+        ents.append(vector_entry(f"blk.{l}.ffn_norm.weight", L["ffn_norm"]))
+        for key in ("gate", "up", "down"):
+            ents.append(hsdb_entry(f"blk.{l}.{names[key]}.weight", L[key], original_type=12,
+                                   layer_index=l))
+    return ents

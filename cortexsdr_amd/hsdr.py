@@ -68,6 +68,21 @@ class HsdbSegment:
         self.cols = info.cols
         self._ws = {}
 
+    @classmethod
+    def from_handle(cls, h):
+        """Wrap a csdr_hsdb* that another loader (HSDC/HSDA/archive) produced."""
+        self = cls.__new__(cls)
+        lib = _lib.load()
+        self._buf = None
+        self._h = h
+        info = _lib.HsdbInfo()
+        _check(lib.csdr_hsdb_get_info(self._h, C.byref(info)))
+        self.info = {name: getattr(info, name) for name, _ in info._fields_}
+        self.rows = info.rows
+        self.cols = info.cols
+        self._ws = {}
+        return self
+
     # ------------------------------------------------------------------ lifetime
     def free(self) -> None:
         if getattr(self, "_h", None):

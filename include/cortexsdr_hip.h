@@ -196,6 +196,11 @@ CSDR_API int csdr_q4k_dequant(const void* w, size_t n_blocks, int order, float* 
 /* y = x / sqrt(mean(x^2) + eps) * w per row of n (rms_norm, cortex_sdk.cpp:1208-1232). */
 CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, float eps, float* y,
                            void* hip_stream);
+/* y (M x R) = x (M x C) . W^T for an uncoded fp32 W (R x C): Kernels::linear_forward's
+ * layout (blas_kernels.cpp:264-293), the dense fallback of matmulForLayer for strategy-0
+ * segments (SparseInferenceEngine.cpp:1290-1311). */
+CSDR_API int csdr_dense_linear(const float* w, int R, int C, const float* x, int M, float* y,
+                               void* hip_stream);
 /* y = silu(g) * u (silu_mul, cortex_sdk.cpp:1245-1256). */
 CSDR_API int csdr_silu_mul(const float* g, const float* u, size_t n, float* y, void* hip_stream);
 /* RoPE on adjacent pairs (get_rope_cache/apply_rope_inplace, cortex_sdk.cpp:1363-1423) of
@@ -225,6 +230,75 @@ CSDR_API int csdr_select_best(const float* logits, int n, const uint8_t* repeate
                               float temperature, float penalty, int* out_token, int* pos_dev,
                               uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
                               void* hip_stream);
+
+/* ======================================================================
+ * Containers: the .sdr archive, HSDC codes-only streams, the HSDA shared-dictionary archive
+ * (host parsing; loads go to the current device)
+ * ==================================================================== */
+
+/* Open .sdr archive: the index is read once (AIDecompressor::readArchiveIndex,
+ * core/AIDecompressor.cpp:78-262, magic "CORTEXSR", versions 1-2) and one file handle is kept
+ * for payload reads (the reference re-opens the file per read, :418-435). */
+typedef struct csdr_archive csdr_archive;
+/* One index entry (CompressedSegmentHeader, core/AICompressor.hpp:51-65). The strings stay
+ * valid until csdr_archive_close. At most 8 dims / shape entries are reported. */
+typedef struct csdr_segment_info {
+    const char* name;
+    const char* data_format;
+    const char* layer_type;
+    const char* layer_name;
+    uint32_t original_type; /* SegmentType (core/ModelSegment.hpp:35-55) */
+    uint32_t strategy_id;   /* 0 raw, 5 HSDR (SparseInferenceEngine.cpp:725-751) */
+    uint64_t original_size, compressed_size, data_offset;
+    uint32_t layer_index;
+    uint32_t has_metadata, n_dims, dims[8];
+    float sparsity_ratio;
+    uint32_t n_input_dims, input_shape[8], n_output_dims, output_shape[8];
+} csdr_segment_info;
+
+CSDR_API int csdr_archive_open(const char* path, csdr_archive** out);
+CSDR_API int csdr_archive_close(csdr_archive* archive);
+CSDR_API size_t csdr_archive_count(const csdr_archive* archive);
+CSDR_API int csdr_archive_info(const csdr_archive* archive, size_t index, csdr_segment_info* info);
+/* Index of the first entry named `name` (SDRModelLoader::findSegmentHeader,
+ * SparseInferenceEngine.cpp:1066-1072). */
+CSDR_API int csdr_archive_find(const csdr_archive* archive, const char* name, size_t* index);
+/* The stored (compressed) payload bytes of entry `index` (readCompressedBytes). With
+ * buf == NULL only *nbytes is set; otherwise cap must be >= the payload size. */
+CSDR_API int csdr_archive_read(const csdr_archive* archive, size_t index, void* buf, size_t cap,
+                               size_t* nbytes);
+
+/* External dictionary of a codes-only stream (HierarchicalSDRStrategy::SharedDictionary:
+ * config + stage scales + atoms, n_atoms * tile_rows * tile_cols floats). */
+typedef struct csdr_dictionary {
+    uint32_t tile_rows, tile_cols, n_atoms, n_stages, k_per_stage;
+    float stage_decay;
+    const float* stage_scales;
+    uint32_t n_stage_scales;
+    const float* atoms;
+    size_t n_atom_floats;
+} csdr_dictionary;
+/* Load an HSDC codes-only stream (HSDRCodesHeader, HierarchicalSDRStrategy.cpp:675-691) with
+ * its external dictionary as a device segment; the geometry checks of parseCodesStream
+ * (:1766-1801). The segment then serves csdr_hsdb_matmul (matmulWithExternalDictionary,
+ * :1830-1883) and csdr_hsdb_decompress (decompressWithExternalDictionary, :1804-1828). */
+CSDR_API int csdr_hsdb_load_codes(const void* codes, size_t nbytes, const csdr_dictionary* dict,
+                                  void* hip_stream, csdr_hsdb** out);
+
+/* HSDA shared-dictionary archive (SharedDictArchive::readFromStream,
+ * HierarchicalSDRStrategy.cpp:1937-2081) with HSDAReader's by-name access (:2506-2550):
+ * csdr_hsda_load builds the named segment's device form, which then serves matmul and
+ * decompress. */
+typedef struct csdr_hsda csdr_hsda;
+CSDR_API int csdr_hsda_open(const char* path, csdr_hsda** out);
+CSDR_API int csdr_hsda_open_memory(const void* data, size_t nbytes, csdr_hsda** out);
+CSDR_API int csdr_hsda_close(csdr_hsda* hsda);
+CSDR_API size_t csdr_hsda_count(const csdr_hsda* hsda);
+CSDR_API size_t csdr_hsda_dictionary_count(const csdr_hsda* hsda);
+CSDR_API int csdr_hsda_segment(const csdr_hsda* hsda, size_t index, const char** name,
+                               uint32_t* dict_index, uint64_t* original_size);
+CSDR_API int csdr_hsda_load(const csdr_hsda* hsda, const char* name, void* hip_stream,
+                            csdr_hsdb** out);
 
 /* ======================================================================
  * Decoder engine (api/cortex_sdk.cpp run_transformer_decode :1543-1696 and

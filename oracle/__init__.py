@@ -110,6 +110,12 @@ def ref():
         L.ref_mha.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, C.c_int]
         L.ref_flash_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz,
                                           C.c_int]
+        L.ref_hsda_build.argtypes = [C.c_uint32, C.POINTER(C.c_char_p), C.POINTER(C.c_void_p),
+                                     C.POINTER(C.c_uint32), C.c_uint32, C.c_uint16, C.c_uint8,
+                                     C.c_uint8, C.c_uint8, C.c_float,
+                                     C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]
+        L.ref_hsda_matmul.argtypes = [_u8p, _sz, C.c_char_p, _f32p, _sz, _f32p, _sz]
+        L.ref_hsda_decompress.argtypes = [_u8p, _sz, C.c_char_p, _f32p, _sz]
         _ref = L
     return _ref
 
@@ -284,7 +290,115 @@ def select_best(logits, repeated=None, temperature=0.0, penalty=1.5) -> int:
     return orc().orc_select_best(lg, lg.size, rp, temperature, penalty)
 
 
+# ------------------------------------------------------------- shared-dictionary containers
+
+HSDC_HEADER = "<4sIIIIHHHBBf"   # HSDRCodesHeader, HierarchicalSDRStrategy.cpp:680-691
+
+
+def hsda_parse(data):
+    """SharedDictArchive::readFromStream (HierarchicalSDRStrategy.cpp:2016-2063): returns
+    (dictionaries, segments); a dictionary is a dict of its 20-byte HierarchicalSDRConfig
+    fields (u16 tile_rows, tile_cols, n_atoms; u8 n_stages, k, ksvd_iters, pad; 2 padding
+    bytes; f32 stage_decay; u32 max_tiles_for_fit), stage_scales and atoms; a segment is
+    (name, dict_index, original_size, original_type, codes bytes)."""
+    import struct
+
+    b = bytes(data)
+    if b[:4] != b"HSDA":
+        raise ValueError("HSDA read: bad magic")
+    version, nd, ns = struct.unpack_from("<III", b, 4)
+    if version != 1:
+        raise ValueError("HSDA read: unsupported version")
+    off = 16
+    dicts = []
+    for _ in range(nd):
+        tr, tc, K, S, k, iters, _pad = struct.unpack_from("<HHHBBBB", b, off)
+        decay, _cap = struct.unpack_from("<fI", b, off + 12)
+        off += 20
+        (nsc,) = struct.unpack_from("<I", b, off)
+        scales = np.frombuffer(b, np.float32, nsc, off + 4).copy()
+        off += 4 + 4 * nsc
+        (na,) = struct.unpack_from("<I", b, off)
+        atoms = np.frombuffer(b, np.float32, na, off + 4).copy()
+        off += 4 + 4 * na
+        dicts.append(dict(tile_rows=tr, tile_cols=tc, n_atoms=K, n_stages=S, k=k,
+                          stage_decay=decay, stage_scales=scales, atoms=atoms))
+    segs = []
+    for _ in range(ns):
+        (nl,) = struct.unpack_from("<I", b, off)
+        name = b[off + 4:off + 4 + nl].decode()
+        off += 4 + nl
+        di, orig, typ, cl = struct.unpack_from("<IQBI", b, off)
+        off += 17
+        segs.append((name, di, orig, typ, b[off:off + cl]))
+        off += cl
+    return dicts, segs
+
+
+def hsdc_to_hsdr(codes, d) -> bytes:
+    """An HSDC codes-only stream + its dictionary as the equivalent HSDR v2 stream: the
+    dictionary's stage scales as gamma, its atoms as D, the packed codes unchanged, zero edge
+    strips (decompressWithExternalDictionary leaves them zero, :1804-1828)."""
+    import struct
+
+    b = bytes(codes)
+    mg, ver, R, Cc, nt, tr, tc, K, S, k, decay = struct.unpack_from(HSDC_HEADER, b, 0)
+    if mg != b"HSDC" or ver != 1:
+        raise ValueError("HSDR shared: bad codes-stream magic/version")
+    if (tr, tc, K, S, k) != (d["tile_rows"], d["tile_cols"], d["n_atoms"], d["n_stages"], d["k"]):
+        raise ValueError("HSDR shared: stream geometry doesn't match dictionary config")
+    n_codes = nt * S * k
+    hdr_n = struct.calcsize(HSDC_HEADER)
+    Rf, Cf = R // tr * tr, Cc // tc * tc
+    edge = (Rf * (Cc - Cf) + (R - Rf) * Cc) * 4
+    head = struct.pack("<4sIIIIHHHBBfI", b"HSDR", 2, R, Cc, nt, tr, tc, K, S, k, decay, edge)
+    return b"".join([head, np.asarray(d["stage_scales"][:S], np.float32).tobytes(),
+                     np.asarray(d["atoms"], np.float32).tobytes(),
+                     b[hdr_n:hdr_n + 2 * n_codes], bytes(edge)])
+
+
 # ------------------------------------------------------------- reference build
+
+def ref_hsda_build(mats: dict, n_atoms, n_stages, k_per_stage, ksvd_iters=4,
+                   stage_decay=0.5) -> bytes:
+    """{name: (R_i x C) fp32} -> HSDA bytes from the reference's compressGroupedSegments."""
+    L = ref()
+    names = list(mats)
+    arrs = [np.ascontiguousarray(mats[n], np.float32) for n in names]
+    Cc = arrs[0].shape[1]
+    nm = (C.c_char_p * len(names))(*[n.encode() for n in names])
+    ws = (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    rows = (C.c_uint32 * len(arrs))(*[a.shape[0] for a in arrs])
+    out = C.POINTER(C.c_uint8)()
+    n = _sz()
+    rc = L.ref_hsda_build(len(names), nm, ws, rows, Cc, n_atoms, n_stages, k_per_stage,
+                          ksvd_iters, stage_decay, C.byref(out), C.byref(n))
+    if rc:
+        raise RuntimeError(L.ref_last_error().decode())
+    data = bytes(C.string_at(out, n.value))
+    L.ref_free(out)
+    return data
+
+
+def ref_hsda_matmul(data, name: str, x, R: int) -> np.ndarray:
+    L = ref()
+    b = _u8(data)
+    x = np.ascontiguousarray(x, np.float32)
+    batch = x.shape[1] if x.ndim == 2 else 1
+    y = np.zeros(R * batch, np.float32)
+    if L.ref_hsda_matmul(b, b.size, name.encode(), x.ravel(), batch, y, y.size):
+        raise RuntimeError(L.ref_last_error().decode())
+    return y.reshape(R, batch)
+
+
+def ref_hsda_decompress(data, name: str, R: int, Cc: int) -> np.ndarray:
+    L = ref()
+    b = _u8(data)
+    w = np.zeros(R * Cc, np.float32)
+    if L.ref_hsda_decompress(b, b.size, name.encode(), w, w.size):
+        raise RuntimeError(L.ref_last_error().decode())
+    return w.reshape(R, Cc)
+
 
 def ref_hsdr_compress(w: np.ndarray, tile_rows, tile_cols, n_atoms, n_stages, k_per_stage,
                       ksvd_iters=4, stage_decay=0.5) -> bytes:

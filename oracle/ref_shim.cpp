@@ -6,6 +6,8 @@
 // this file only calls the reference's public entry points:
 //   HierarchicalSDRStrategy::{compress, decompress, matmulRowMajor, dequantizeToFP32}
 //     (strategies/HierarchicalSDRStrategy.hpp:170-181, :333)
+//   HierarchicalSDRStrategy::compressGroupedSegments + SharedDictArchive::writeToStream
+//     and HSDAReader::{matmul, decompress} (HierarchicalSDRStrategy.hpp:289-346, 368-405)
 //   Kernels::multi_head_attention (kernels/attention_kernels.hpp:26)
 //   Kernels::flash_attention_forward (kernels/flash_attention.hpp:43)
 #include "strategies/HierarchicalSDRStrategy.hpp"
@@ -14,6 +16,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <sstream>
 #include <exception>
 #include <string>
 #include <vector>
@@ -111,6 +114,78 @@ int ref_dequant(const uint8_t* data, size_t n, const char* fmt, uint32_t R, uint
         if (v.size() > out_floats) return -2;
         std::memcpy(out, v.data(), v.size() * sizeof(float));
         return static_cast<int>(v.size());
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+// n row-major fp32 matrices (R_i x C, names[i]) -> HSDA bytes through the reference's
+// shared-dictionary pipeline with 1-row tiles (one dictionary for the group).
+int ref_hsda_build(uint32_t n, const char* const* names, const float* const* ws,
+                   const uint32_t* rows, uint32_t C, uint16_t n_atoms, uint8_t n_stages,
+                   uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay, uint8_t** out,
+                   size_t* out_n) {
+    try {
+        HierarchicalSDRConfig cfg;
+        cfg.tile_rows = 1;
+        cfg.tile_cols = static_cast<uint16_t>(C);
+        cfg.n_atoms = n_atoms;
+        cfg.n_stages = n_stages;
+        cfg.active_bits_per_stage = k_per_stage;
+        cfg.ksvd_iters = ksvd_iters;
+        cfg.stage_decay = stage_decay;
+        HierarchicalSDRStrategy strat(cfg, cfg);
+        std::vector<ModelSegment> segs;
+        for (uint32_t i = 0; i < n; ++i) {
+            ModelSegment seg(SegmentType::WEIGHTS_FP32, names[i],
+                             as_bytes(ws[i], sizeof(float) * size_t(rows[i]) * C));
+            TensorMetadata meta;
+            meta.dimensions = {rows[i], C};
+            seg.tensor_metadata = meta;
+            seg.data_format = "f32";
+            segs.push_back(std::move(seg));
+        }
+        std::vector<std::string> skipped;
+        auto archive = strat.compressGroupedSegments(segs, &skipped);
+        if (!skipped.empty()) {
+            g_err = "segment skipped by the reference pipeline: " + skipped[0];
+            return -3;
+        }
+        std::ostringstream os;
+        archive.writeToStream(os);
+        const std::string b = os.str();
+        *out_n = b.size();
+        *out = static_cast<uint8_t*>(std::malloc(b.size() ? b.size() : 1));
+        std::memcpy(*out, b.data(), b.size());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+int ref_hsda_matmul(const uint8_t* data, size_t n, const char* name, const float* x,
+                    size_t batch, float* y, size_t y_floats) {
+    try {
+        std::istringstream is(std::string(reinterpret_cast<const char*>(data), n));
+        HSDAReader reader(HierarchicalSDRStrategy::SharedDictArchive::readFromStream(is));
+        std::vector<float> Y = reader.matmul(name, x, batch);
+        if (Y.size() > y_floats) return -2;
+        std::memcpy(y, Y.data(), Y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
+int ref_hsda_decompress(const uint8_t* data, size_t n, const char* name, float* w,
+                        size_t w_floats) {
+    try {
+        std::istringstream is(std::string(reinterpret_cast<const char*>(data), n));
+        HSDAReader reader(HierarchicalSDRStrategy::SharedDictArchive::readFromStream(is));
+        std::vector<std::byte> b = reader.decompress(name);
+        if (b.size() > w_floats * 4) return -2;
+        std::memcpy(w, b.data(), b.size());
+        return 0;
     } catch (const std::exception& e) {
         return fail(e, -1);
     }

@@ -14,7 +14,14 @@ this script generates and the outputs the reference computed for them.
   mha_*      Kernels::multi_head_attention / flash_attention_forward, causal, B=2, T=9,
              hidden=32, heads=4
 
-Usage: python tests/golden/make_fixtures.py
+and tests/golden/hsda_fixtures.npz (`hsda` argument):
+
+  hsda_bytes     SharedDictArchive::writeToStream of compressGroupedSegments over three
+                 matrices (32/20/45 x 64, 1-row tiles, K=16, 2 stages x 2) named like GGUF
+                 block tensors; hsda_x (64 x 3); per segment i: hsda_name_i, hsda_w_i
+                 (HSDAReader::decompress), hsda_y_i (HSDAReader::matmul)
+
+Usage: python tests/golden/make_fixtures.py [hsda]
 """
 from __future__ import annotations
 
@@ -88,5 +95,29 @@ def main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def hsda_main() -> None:
+    oracle.build(ref=True)
+    if oracle.ref() is None:
+        raise SystemExit("oracle/_ref/libcsdr_ref.so is not built")
+    rng = np.random.default_rng(20261202)
+    names = ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.1.ffn_up.weight"]
+    mats = {n: rng.normal(0, 0.05, (R, 64)).astype(np.float32)
+            for n, R in zip(names, (32, 20, 45))}
+    data = oracle.ref_hsda_build(mats, 16, 2, 2, ksvd_iters=3)
+    x = rng.normal(0, 1, (64, 3)).astype(np.float32)
+    out = {"hsda_bytes": np.frombuffer(data, np.uint8), "hsda_x": x}
+    for i, n in enumerate(names):
+        R = mats[n].shape[0]
+        out[f"hsda_name_{i}"] = np.frombuffer(n.encode(), np.uint8)
+        out[f"hsda_w_{i}"] = oracle.ref_hsda_decompress(data, n, R, 64)
+        out[f"hsda_y_{i}"] = oracle.ref_hsda_matmul(data, n, x, R)
+    path = os.path.join(HERE, "hsda_fixtures.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["hsda"]:
+        hsda_main()
+    else:
+        main()

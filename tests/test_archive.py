@@ -1,0 +1,112 @@
+"""Containers on the host (no device): the .sdr archive index read by the C-ABI reader
+(csdr_archive_*, AIDecompressor::readArchiveIndex, core/AIDecompressor.cpp:78-262), the HSDA
+shared-dictionary archive (csdr_hsda_*, SharedDictArchive::readFromStream,
+HierarchicalSDRStrategy.cpp:1937-2081) against the reference's own HSDA bytes, and the
+oracle's HSDA/HSDC restatement against the reference's HSDAReader outputs (bit-exact)."""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import GOLDEN
+from cortexsdr_amd import formats, synth
+from cortexsdr_amd._lib import CsdrError
+from cortexsdr_amd.archive import HsdaArchive, SdrArchive
+
+
+@pytest.fixture(scope="module")
+def hsda():
+    return np.load(os.path.join(GOLDEN, "hsda_fixtures.npz"), allow_pickle=False)
+
+
+def test_oracle_hsda_matches_reference_reader_bitexact(hsda):
+    data = hsda["hsda_bytes"].tobytes()
+    dicts, segs = oracle.hsda_parse(data)
+    assert len(dicts) == 1 and len(segs) == 3
+    for i, (name, di, orig, typ, codes) in enumerate(segs):
+        assert name == hsda[f"hsda_name_{i}"].tobytes().decode()
+        stream = oracle.hsdc_to_hsdr(codes, dicts[di])
+        w = oracle.hsdr_decompress(stream)
+        y = oracle.hsdr_matmul_row_major(stream, hsda["hsda_x"])
+        assert orig == w.size * 4
+        assert np.array_equal(w.view(np.uint32), hsda[f"hsda_w_{i}"].view(np.uint32))
+        assert np.array_equal(y.view(np.uint32), hsda[f"hsda_y_{i}"].view(np.uint32))
+
+
+def test_hsda_index_through_c_abi(hsda):
+    data = hsda["hsda_bytes"].tobytes()
+    a = HsdaArchive(data=data)
+    assert len(a) == 3 and a.num_dictionaries() == 1
+    names = [a.segment(i)[0] for i in range(3)]
+    assert names == [hsda[f"hsda_name_{i}"].tobytes().decode() for i in range(3)]
+    assert all(a.segment(i)[1] == 0 for i in range(3))
+    assert a.segment(0)[2] == 32 * 64 * 4
+
+
+@pytest.mark.parametrize("cut", [3, 15, 40, 200])
+def test_hsda_truncation_and_magic_rejected(hsda, cut):
+    data = hsda["hsda_bytes"].tobytes()
+    with pytest.raises(CsdrError):
+        HsdaArchive(data=data[:cut])
+    with pytest.raises(CsdrError):
+        HsdaArchive(data=b"HSDX" + data[4:])
+
+
+def _entries():
+    s1 = synth.hsdb_layer(64, 256, 32, 4, seed_dict=1, seed_codes=2)
+    w = np.arange(12, dtype=np.float32).reshape(3, 4)
+    return [
+        formats.hsdb_entry("blk.0.attn_q.weight", s1, layer_name="blk.0.attn_q", layer_index=0,
+                           input_shape=(1, 256), output_shape=(1, 64)),
+        formats.SdrEntry(name="dense.weight", payload=w.tobytes(), dims=(3, 4)),
+        formats.vector_entry("output_norm.weight", np.ones(8, np.float32)),
+        formats.SdrEntry(name="meta", payload=b'{"a": 1}', data_format="json", original_type=6),
+    ]
+
+
+@pytest.mark.parametrize("version", [1, 2])
+def test_sdr_index_round_trip(tmp_path, version):
+    path = str(tmp_path / "m.sdr")
+    ents = _entries()
+    formats.write_sdr(path, ents, version=version)
+    a = SdrArchive(path)
+    assert len(a) == len(ents)
+    for i, e in enumerate(ents):
+        info = a.info(i)
+        assert info["name"] == e.name
+        assert info["data_format"] == (e.data_format if version >= 2 else "")
+        assert info["strategy_id"] == e.strategy_id
+        assert info["original_type"] == e.original_type
+        assert info["compressed_size"] == len(e.payload)
+        assert info["layer_name"] == e.layer_name and info["layer_index"] == e.layer_index
+        assert info["dims"] == (tuple(e.dims) if e.dims is not None else None)
+        assert info["input_shape"] == tuple(e.input_shape)
+        assert info["output_shape"] == tuple(e.output_shape)
+        assert a.read(i) == bytes(e.payload)
+        assert a.find(e.name) == i
+    assert a.read("dense.weight") == ents[1].payload
+    with pytest.raises(CsdrError):
+        a.find("missing")
+
+
+def test_sdr_bad_archives_rejected(tmp_path):
+    path = str(tmp_path / "m.sdr")
+    formats.write_sdr(path, _entries())
+    raw = open(path, "rb").read()
+    cases = {
+        "magic": b"CORTEXSX" + raw[8:],
+        "version0": raw[:8] + struct.pack("<I", 0) + raw[12:],
+        "version3": raw[:8] + struct.pack("<I", 3) + raw[12:],
+        "index_past_end": raw[:20] + struct.pack("<Q", len(raw) + 10) + raw[28:],
+        "truncated_index": raw[:-5],
+        "short": raw[:10],
+    }
+    for name, b in cases.items():
+        p = str(tmp_path / f"{name}.sdr")
+        open(p, "wb").write(b)
+        with pytest.raises(CsdrError):
+            SdrArchive(p)
+    with pytest.raises(CsdrError):
+        SdrArchive(str(tmp_path / "does_not_exist.sdr"))

@@ -8,7 +8,7 @@ import pytest
 
 from conftest import ROOT
 
-HEADER_DECL = re.compile(r"CSDR_API\s+[^;(]*?\b(csdr_\w+)\s*\(", re.S)
+HEADER_DECL = re.compile(r"CSDR_API\s+[^;(]*?\b((?:csdr|cortex)_\w+)\s*\(", re.S)
 
 
 def declared_symbols() -> set[str]:
@@ -20,7 +20,9 @@ def declared_symbols() -> set[str]:
 
 def test_header_declares_entry_points():
     names = declared_symbols()
-    assert {"csdr_hsdb_load", "csdr_hsdb_matmul", "csdr_hsdb_decompress"} <= names
+    assert {"csdr_hsdb_load", "csdr_hsdb_matmul", "csdr_hsdb_decompress",
+            "cortex_inference_engine_create", "cortex_inference_engine_run_layer",
+            "csdr_archive_open", "csdr_hsda_load", "csdr_decoder_generate"} <= names
 
 
 def test_library_exports_every_declared_symbol():
