@@ -1,6 +1,7 @@
 """Bench CLI for the compressed-weight path: every BASELINE.json configuration on one GPU.
 
     python -m cortexsdr_amd.bench_cli [--configs cfg1,cfg2,cfg3] [--steps 50] [--out f.json]
+    python -m cortexsdr_amd.bench_cli --suite suite.json [--out summary.json]
 
 The role of the reference's `cortexsdr_bench` suite runner (src/cortexsdr_bench.cpp:52-79,
 160-181: run each workload, collect times, write a summary JSON), for the device path:
@@ -144,12 +145,90 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
         dec.close()
 
 
+def _percentile(v, q):
+    """Linear-interpolated percentile of the sorted samples (cortexsdr_bench.cpp:160-181)."""
+    v = sorted(v)
+    if not v:
+        return None
+    pos = (len(v) - 1) * q / 100.0
+    lo = int(pos)
+    hi = min(lo + 1, len(v) - 1)
+    return v[lo] + (v[hi] - v[lo]) * (pos - lo)
+
+
+def run_suite(path: str) -> dict:
+    """The reference bench suite runner's inference leg (cortexsdr_bench.cpp:52-79,
+    435-462) over a suite JSON of the reference's shape: "repeats", "warmup_runs",
+    "binaries.text_cli" (default: this package's cortexsdr_text_cli) and "tests" entries
+    with "sdr_path", "prompt" (token ids here), "max_length", "run_inference". Each run
+    spawns the text CLI with --profile and records wall time and the profile."""
+    import os
+    import subprocess
+    import tempfile
+
+    with open(path) as f:
+        suite = json.load(f)
+    root = suite.get("project_root", ".")
+    here = os.path.dirname(os.path.abspath(__file__))
+    cli = suite.get("binaries", {}).get("text_cli") or os.path.join(here, "bin",
+                                                                      "cortexsdr_text_cli")
+    if not os.path.isabs(cli) and not os.path.exists(cli):
+        cli = os.path.join(root, cli)
+    repeats = int(suite.get("repeats", 1))
+    warm = int(suite.get("warmup_runs", 0))
+    out = {"suite": path, "text_cli": cli, "tests": []}
+    for t in suite.get("tests", []):
+        if not t.get("run_inference", True):
+            continue
+        sdr = t["sdr_path"] if os.path.isabs(t["sdr_path"]) else os.path.join(root, t["sdr_path"])
+        runs = []
+        for i in range(warm + repeats):
+            with tempfile.TemporaryDirectory() as td:
+                prof = os.path.join(td, "profile.json")
+                cmd = [cli, "-p", str(t["prompt"]), "-m", str(t.get("max_length", 64)),
+                       "--profile", prof, sdr]
+                t0 = time.perf_counter()
+                r = subprocess.run(cmd, capture_output=True, text=True)
+                ms = (time.perf_counter() - t0) * 1e3
+                rec = {"exit_code": r.returncode, "elapsed_ms_wall": round(ms, 3),
+                       "command": " ".join(cmd)}
+                if os.path.exists(prof):
+                    with open(prof) as pf:
+                        rec["profile"] = json.load(pf)
+                    tps = rec["profile"].get("tokens_per_sec")
+                    if tps is not None:
+                        rec["tokens_per_min"] = tps * 60.0
+                elif r.returncode:
+                    rec["stderr"] = r.stderr[-2000:]
+            if i >= warm:
+                runs.append(rec)
+        walls = [r["elapsed_ms_wall"] for r in runs if r["exit_code"] == 0]
+        tps = [r["profile"]["tokens_per_sec"] for r in runs
+               if r["exit_code"] == 0 and "profile" in r]
+        out["tests"].append({
+            "name": t.get("name", sdr), "runs": runs,
+            "wall_ms_p50": _percentile(walls, 50), "wall_ms_p95": _percentile(walls, 95),
+            "tokens_per_sec_p50": _percentile(tps, 50), "tokens_per_sec_p95": _percentile(tps, 95),
+            "ok": all(r["exit_code"] == 0 for r in runs),
+        })
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4")
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--out", default=None)
+    ap.add_argument("--suite", default=None, help="run a bench suite JSON through the text CLI")
     args = ap.parse_args(argv)
+    if args.suite:
+        res = run_suite(args.suite)
+        text = json.dumps(res)
+        print(text, flush=True)
+        if args.out:
+            with open(args.out, "w") as f:
+                f.write(text + "\n")
+        return 0 if all(t["ok"] for t in res["tests"]) else 1
     import torch
 
     if not torch.cuda.is_available():

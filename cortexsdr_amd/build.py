@@ -19,6 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcortexsdr_amd.so")
+BIN = os.path.join(HERE, "bin")
+TOOLS = os.path.join(CSRC, "tools")
 ROOT = os.path.dirname(HERE)
 
 ARCH = os.environ.get("CSDR_OFFLOAD_ARCH", "gfx950")
@@ -62,6 +64,7 @@ def compile_one(src: str) -> str:
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
+    # (tools/ holds executables, built after the library)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(compile_one, srcs))
     tmp = LIB + ".tmp"
@@ -70,6 +73,16 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # host tools linked against the library (rpath to the package directory)
+    os.makedirs(BIN, exist_ok=True)
+    for src in sorted(glob.glob(os.path.join(TOOLS, "*.cpp"))):
+        exe = os.path.join(BIN, "cortexsdr_" + os.path.splitext(os.path.basename(src))[0])
+        cmd = [hipcc(), *common_flags(), src, "-L" + HERE, "-lcortexsdr_amd",
+               "-Wl,-rpath,$ORIGIN/..", "-o", exe + ".tmp"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"tool build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        os.replace(exe + ".tmp", exe)
     if verbose:
         print(f"built {LIB}")
     return LIB
