@@ -219,6 +219,7 @@ def main(argv=None) -> int:
     ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4")
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--out", default=None)
+    ap.add_argument("--cfg2-batches", default="1,16,64,256")
     ap.add_argument("--suite", default=None, help="run a bench suite JSON through the text CLI")
     args = ap.parse_args(argv)
     if args.suite:
@@ -241,9 +242,10 @@ def main(argv=None) -> int:
         res["results"]["cfg1"] = [bench_hsdb(torch, 4096, 4096, 512, 4, 1, np.float32,
                                              args.steps)]
     if "cfg2" in cfgs:
+        ms = [int(v) for v in args.cfg2_batches.split(",")]
         out = []
         for (R, Cc) in ((4096, 11008), (11008, 4096)):
-            for M in (1, 16, 64, 256):
+            for M in ms:
                 out.append(bench_hsdb(torch, R, Cc, 1024, 8, M, np.float16, args.steps))
                 print(json.dumps(out[-1]), flush=True)
         res["results"]["cfg2"] = out

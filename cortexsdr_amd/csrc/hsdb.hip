@@ -724,7 +724,7 @@ size_t p_path_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
 }
 
 // Workspace of a full product at batch M, large enough for every batch <= M as well (the
-// MFMA path at M >= 16 needs less than the P path at M = 15).
+// matrix-core path can need less than the P path at a smaller M).
 size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
     if (csdr::mfma_eligible(n, segs, M))
         return std::max(csdr::mfma_workspace_bytes(n, segs, M), p_path_ws_bytes(n, segs, 15));

@@ -34,7 +34,7 @@ __host__ __device__ __forceinline__ int kperm64(int k) {
     return (k & 3) | ((k >> 2) & 3) << 4 | ((k >> 4) & 3) << 2;
 }
 
-// Batched (M >= 16) product on matrix cores: decoded 64-column tiles times X (fp16 MFMA,
+// Batched (M >= 2) product on matrix cores: decoded 64-column tiles times X (fp16 MFMA,
 // fp32 accumulation). eligible(): every matrix has 1-row tiles of 64, at most 1024 atoms
 // and 4, 8 or 16 slots, and CSDR_HSDB_MFMA is not 0.
 bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M);

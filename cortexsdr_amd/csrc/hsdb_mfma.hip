@@ -1,4 +1,4 @@
-// hsdb_mfma.hip — batched (M >= 16) block-coded product Y = W.X on gfx950 matrix cores.
+// hsdb_mfma.hip — batched (M >= 2) block-coded product Y = W.X on gfx950 matrix cores.
 //
 // Path (cortexSDR tree): HierarchicalSDRStrategy::matmulRowMajor with batch > 1
 // (strategies/HierarchicalSDRStrategy.cpp:1257-1338), block-coded as in research
@@ -41,6 +41,7 @@ constexpr int kMaxAtoms = 1024;
 constexpr int kMaxMTile = 256;
 constexpr int kGroup = 8;
 constexpr size_t kWsHeader = 256;
+constexpr int kMfmaMinM = 2;  // smallest batch routed to this path (M = 1: the P-path GEMV)
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -357,9 +358,11 @@ int launch_main(const MParams& p, bool xs, int grid, size_t lds, hipStream_t st)
 namespace csdr {
 
 bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M) {
-    if (M < 16) return false;
     const char* e = std::getenv("CSDR_HSDB_MFMA");
     if (e && *e && std::atoi(e) == 0) return false;
+    const char* mm = std::getenv("CSDR_HSDB_MFMA_MIN_M");
+    const int min_m = (mm && std::atoi(mm) > 1) ? std::atoi(mm) : kMfmaMinM;
+    if (M < min_m) return false;
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
         if (!s || s->tile_rows != 1 || s->tile_cols != 64 || s->K > (uint32_t)kMaxAtoms ||

@@ -98,8 +98,8 @@ CSDR_API int csdr_hsdb_load(const void* stream, size_t nbytes, void* hip_stream,
 CSDR_API int csdr_hsdb_free(csdr_hsdb* seg);
 CSDR_API int csdr_hsdb_get_info(const csdr_hsdb* seg, csdr_hsdb_info* info);
 
-/* Device workspace bytes csdr_hsdb_matmul needs for batch M (P = D . X for M < 16, the
- * transposed fp16 X for the matrix-core path at M >= 16); enough for every batch <= M too.
+/* Device workspace bytes csdr_hsdb_matmul needs for batch M (P = D . X on the P path, the
+ * transposed fp16 X on the matrix-core path); enough for every batch <= M too.
  * Calls that share a workspace must be ordered (same stream); concurrent calls need their
  * own. */
 CSDR_API size_t csdr_hsdb_workspace_bytes(const csdr_hsdb* seg, int M);
@@ -113,9 +113,10 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
 
 /* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
  * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
- * M < 16: a dx launch (P = D . X per block column into the workspace, Y = 0) and a gather
- * launch (Y += the coded rows gathered from P), all fp32. M >= 16 (64-column blocks, K <=
- * 1024 atoms, 4/8/16 slots): an init launch and a matrix-core launch that decodes 64-column
+ * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
+ * column into the workspace, Y = 0) and a gather launch (Y += the coded rows gathered from
+ * P), all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots (the threshold
+ * is CSDR_HSDB_MFMA_MIN_M, default 2): an init launch and a matrix-core launch that decodes 64-column
  * tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
  * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
  * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace

@@ -1,4 +1,4 @@
-"""GPU parity of the batched (M >= 16) HSDB product on matrix cores (HK2: decoded 64-column
+"""GPU parity of the batched (M >= 2) HSDB product on matrix cores (HK2: decoded 64-column
 tiles x X with v_mfma_f32_16x16x16f16, fp32 accumulation) against the CPU oracle's fp32
 fused product, through the C-ABI.
 
