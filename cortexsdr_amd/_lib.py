@@ -85,6 +85,8 @@ SIGNATURES = {
                                         C.c_int, _vp, C.POINTER(C.c_int)]),
     "csdr_decoder_logits": (C.c_int, [_vp, _vp]),
     "csdr_decoder_position": (C.c_int, [_vp]),
+    "csdr_decoder_load_kv": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int]),
+    "csdr_decoder_set_position": (C.c_int, [_vp, C.c_int, C.c_int32]),
 }
 
 

@@ -145,6 +145,49 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
         dec.close()
 
 
+def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5):
+    """Config 5: Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads of 128, SwiGLU
+    11008, vocab 32000, all linears HSDB-coded: 1024 x 64 dictionary, 8 nnz per block) at
+    context `ctx` with the fp16 KV cache filled with N(0,1), batch 1, weights resident.
+    Two distinct coded layers are generated and loaded 16 times each: every layer has its own
+    device copy, so HBM traffic per step is that of 32 distinct layers."""
+    import dataclasses
+
+    from .decoder import Decoder, DecoderSpec, DecoderWeights, synthetic_weights
+
+    spec = DecoderSpec(32, 4096, 32, 32, 128, 11008, 32000, ctx + steps + 8)
+    t0 = time.time()
+    w2 = synthetic_weights(dataclasses.replace(spec, n_layers=2), seed=seed)
+    w = DecoderWeights(spec, [w2.layers[l % 2] for l in range(32)], w2.lm_head, w2.final_norm)
+    t_build = time.time() - t0
+    dec = Decoder(w)
+    try:
+        for l in range(spec.n_layers):
+            k = torch.randn((ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
+            v = torch.randn((ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
+            dec.load_kv(l, k, v, ctx)
+            del k, v
+        torch.cuda.synchronize()
+        dec.set_position(ctx, 1)
+        dec.decode(3, 0.0, 0.0)                      # captures the step graph
+        dec.set_position(ctx, 1)
+        t0 = time.perf_counter()
+        dec.decode(steps, 0.0, 0.0)
+        dt = (time.perf_counter() - t0) / steps
+        code = w.code_bytes()
+        kv = 2 * spec.n_layers * (ctx + steps // 2) * spec.n_kv_heads * spec.head_dim * 2
+        return {"layers": 32, "hidden": 4096, "heads": 32, "head_dim": 128, "ffn": 11008,
+                "vocab": 32000, "context": ctx, "batch": 1, "steps": steps,
+                "ms_per_step": round(dt * 1e3, 3), "tokens_per_s": round(1.0 / dt, 1),
+                "code_GB_per_step": round(code / 1e9, 3), "kv_GB_per_step": round(kv / 1e9, 3),
+                "alg_GBps": round((code + kv) / dt / 1e9, 1),
+                "hbm_frac": round((code + kv) / dt / HBM_PEAK, 4),
+                "device_GB": round(dec.device_bytes() / 1e9, 2),
+                "host_build_s": round(t_build, 1)}
+    finally:
+        dec.close()
+
+
 def _percentile(v, q):
     """Linear-interpolated percentile of the sorted samples (cortexsdr_bench.cpp:160-181)."""
     v = sorted(v)
@@ -256,6 +299,9 @@ def main(argv=None) -> int:
                 out.append(bench_q4k(torch, R, Cc, M, args.steps))
                 print(json.dumps(out[-1]), flush=True)
         res["results"]["cfg3"] = out
+    if "cfg5" in cfgs:
+        res["results"]["cfg5"] = bench_decoder_7b(torch)
+        print(json.dumps(res["results"]["cfg5"]), flush=True)
     if "cfg4" in cfgs:
         res["results"]["cfg4"] = bench_decoder(torch)
         print(json.dumps(res["results"]["cfg4"]), flush=True)

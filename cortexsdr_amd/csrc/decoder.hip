@@ -499,4 +499,35 @@ CSDR_API int csdr_decoder_logits(const csdr_decoder* d, float* out) {
 
 CSDR_API int csdr_decoder_position(const csdr_decoder* d) { return d ? d->host_pos : -1; }
 
+// Imports a precomputed context: K and V of positions [0, n) for `layer` (fp16
+// [position][kv head][head_dim], host or device memory).
+CSDR_API int csdr_decoder_load_kv(csdr_decoder* d, int layer, const uint16_t* k, const uint16_t* v,
+                                  int n) {
+    if (!d || layer < 0 || layer >= d->cfg.n_layers || !k || !v || n < 0 || n > d->cfg.max_ctx)
+        return set_error(CSDR_E_INVALID, "decoder_load_kv: bad argument");
+    const size_t bytes = (size_t)n * d->cfg.n_kv_heads * d->cfg.head_dim * 2;
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    if (bytes) {
+        CSDR_HIP_CHECK(hipMemcpy(d->layers[layer].kc, k, bytes, hipMemcpyDefault));
+        CSDR_HIP_CHECK(hipMemcpy(d->layers[layer].vc, v, bytes, hipMemcpyDefault));
+    }
+    return CSDR_OK;
+}
+
+// Continues from an imported context: positions [0, position) count as processed and
+// `token` is the token at `position` (the next decode step consumes it). The
+// generated-token set starts empty.
+CSDR_API int csdr_decoder_set_position(csdr_decoder* d, int position, int32_t token) {
+    if (!d || position < 0 || position >= d->cfg.max_ctx || token < 0 || token >= d->cfg.vocab)
+        return set_error(CSDR_E_INVALID, "decoder_set_position: bad argument");
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    CSDR_HIP_CHECK(hipMemcpy(d->pos, &position, 4, hipMemcpyHostToDevice));
+    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, d->cfg.vocab));
+    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)(d->cfg.max_ctx + 1) * 4));
+    CSDR_HIP_CHECK(hipMemcpy(d->ring + position, &token, 4, hipMemcpyHostToDevice));
+    d->host_pos = position;
+    d->n_prompt = std::max(1, position);
+    return CSDR_OK;
+}
+
 }  // extern "C"

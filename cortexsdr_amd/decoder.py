@@ -183,6 +183,15 @@ class Decoder:
         _lib.check(self._lib.csdr_decoder_logits(self._h, _fptr(out)))
         return out
 
+    def load_kv(self, layer: int, k, v, n: int) -> None:
+        """Import fp16 K/V of positions [0, n) (device torch tensors or host numpy arrays)."""
+        kp = k.data_ptr() if hasattr(k, "data_ptr") else k.ctypes.data
+        vp = v.data_ptr() if hasattr(v, "data_ptr") else v.ctypes.data
+        _lib.check(self._lib.csdr_decoder_load_kv(self._h, layer, kp, vp, n))
+
+    def set_position(self, position: int, token: int) -> None:
+        _lib.check(self._lib.csdr_decoder_set_position(self._h, position, token))
+
     def position(self) -> int:
         return int(self._lib.csdr_decoder_position(self._h))
 

@@ -354,6 +354,13 @@ CSDR_API int csdr_decoder_generate(csdr_decoder* dec, const int32_t* prompt, int
 CSDR_API int csdr_decoder_logits(const csdr_decoder* dec, float* out);
 /* Number of positions processed so far (-1 for NULL). */
 CSDR_API int csdr_decoder_position(const csdr_decoder* dec);
+/* Import a precomputed context (a cached prompt prefix): fp16 K and V of positions [0, n) for
+ * one layer, [position][kv head][head_dim], from host or device memory. */
+CSDR_API int csdr_decoder_load_kv(csdr_decoder* dec, int layer, const uint16_t* k,
+                                  const uint16_t* v, int n);
+/* Continue from an imported context: positions [0, position) count as processed and `token`
+ * is the token at `position`, consumed by the next csdr_decoder_decode step. */
+CSDR_API int csdr_decoder_set_position(csdr_decoder* dec, int position, int32_t token);
 
 #ifdef __cplusplus
 }
