@@ -54,17 +54,32 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 
 // ---------------------------------------------------------------- RMSNorm
 
-__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* __restrict__ x,
-                                                            const float* __restrict__ w, int n,
-                                                            float eps, float* __restrict__ y) {
-    __shared__ float red[kThreads / 64];
+// One workgroup per row (blockDim 256 or 1024); each thread keeps its elements in registers
+// between the sum of squares and the scaling (at most 8 per thread, else re-read).
+__global__ __launch_bounds__(1024) void rms_norm_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w, int n,
+                                                        float eps, float* __restrict__ y) {
+    __shared__ float red[1024 / 64];
     const float* xr = x + (size_t)blockIdx.x * n;
     float* yr = y + (size_t)blockIdx.x * n;
+    const int nt = blockDim.x;
+    float xv[8];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kThreads) ss = fmaf(xr[i], xr[i], ss);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = threadIdx.x + j * nt;
+        xv[j] = i < n ? xr[i] : 0.f;
+        ss = fmaf(xv[j], xv[j], ss);
+    }
+    for (int i = threadIdx.x + 8 * nt; i < n; i += nt) ss = fmaf(xr[i], xr[i], ss);
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += kThreads) yr[i] = xr[i] * inv * w[i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = threadIdx.x + j * nt;
+        if (i < n) yr[i] = xv[j] * inv * w[i];
+    }
+    for (int i = threadIdx.x + 8 * nt; i < n; i += nt) yr[i] = xr[i] * inv * w[i];
 }
 
 // ---------------------------------------------------------------- SiLU(g) * u
@@ -102,112 +117,175 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
 
 // q: ntok x Hq x hd, k: ntok x Hkv x hd (rotated in place); v: ntok x Hkv x hd.
 // Token t sits at position pos0 + t (pos0 = *pos_dev). K and V go to the fp16 caches laid
-// out [position][kv head][hd] with row capacity max_ctx.
-__global__ __launch_bounds__(kThreads) void rope_kv_kernel(float* __restrict__ q,
-                                                           float* __restrict__ k,
-                                                           const float* __restrict__ v, int ntok,
-                                                           int Hq, int Hkv, int hd,
-                                                           const int* __restrict__ pos_dev,
-                                                           float theta, _Float16* kcache,
-                                                           _Float16* vcache, int max_ctx) {
-    const int t = blockIdx.x;
+// out [position][kv head][hd] with row capacity max_ctx. One workgroup per (token, head):
+// blocks [0, Hq) rotate query heads, [Hq, Hq + Hkv) rotate a key head and append it (and the
+// value head) to the caches.
+__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q,
+                                                     float* __restrict__ k,
+                                                     const float* __restrict__ v, int ntok,
+                                                     int Hq, int Hkv, int hd,
+                                                     const int* __restrict__ pos_dev,
+                                                     float theta, _Float16* kcache,
+                                                     _Float16* vcache, int max_ctx) {
+    const int t = blockIdx.x / (Hq + Hkv);
+    const int head = blockIdx.x % (Hq + Hkv);
     const int pos = *pos_dev + t;
     const int half = hd / 2;
     const int rot = hd - (hd % 2);
-    // pairs (2i, 2i+1) of every head: Hq heads of q, then Hkv heads of k
-    for (int e = threadIdx.x; e < (Hq + Hkv) * half; e += kThreads) {
-        const int head = e / half, i2 = 2 * (e % half);
+    float* base = head < Hq ? q + ((size_t)t * Hq + head) * hd
+                            : k + ((size_t)t * Hkv + (head - Hq)) * hd;
+    for (int e = threadIdx.x; e < half; e += 64) {
+        const int i2 = 2 * e;
         if (i2 >= rot) continue;
-        float* base = head < Hq ? q + ((size_t)t * Hq + head) * hd
-                                : k + ((size_t)t * Hkv + (head - Hq)) * hd;
         const float freq = powf(theta, -((float)i2 / (float)hd));
         const float ang = (float)pos * freq;
-        const float c = cosf(ang), s = sinf(ang);
+        const float c = cosf(ang), sn = sinf(ang);
         const float x0 = base[i2], x1 = base[i2 + 1];
-        base[i2] = x0 * c - x1 * s;
-        base[i2 + 1] = x0 * s + x1 * c;
+        base[i2] = x0 * c - x1 * sn;
+        base[i2 + 1] = x0 * sn + x1 * c;
     }
+    if (head < Hq || pos >= max_ctx) return;
     __syncthreads();
-    if (pos >= max_ctx) return;
-    for (int e = threadIdx.x; e < Hkv * hd; e += kThreads) {
-        const size_t src = (size_t)t * Hkv * hd + e;
-        const size_t dst = (size_t)pos * Hkv * hd + e;
-        kcache[dst] = (_Float16)k[src];
-        vcache[dst] = (_Float16)v[src];
+    const int kh = head - Hq;
+    const size_t src = ((size_t)t * Hkv + kh) * hd;
+    const size_t dst = ((size_t)pos * Hkv + kh) * hd;
+    for (int e = threadIdx.x; e < hd; e += 64) {
+        kcache[dst + e] = (_Float16)base[e];
+        vcache[dst + e] = (_Float16)v[src + e];
     }
 }
 
 // ---------------------------------------------------------------- flash-decode attention
 
-// Partial softmax-attention of one query head over positions [s*S, min(L, (s+1)*S)):
-// part = (max score m, sum of exp l, o[hd] = sum exp * v). One thread per position for the
-// scores; for P.V, thread t owns dimension t % hd and a 1/(256/hd) share of the positions.
-template <int HD>
+// Partial softmax-attention over positions [s*S, min(L, (s+1)*S)) for the GW query heads
+// (of one batch entry) that share KV head kvh: part = (max score m, sum of exp l,
+// o[hd] = sum exp * v) per head. LPP = HD/8 lanes hold one position's 16-byte K/V pieces
+// (one coalesced HD*2-byte row per position), so each K/V byte is read once for all the
+// query heads of its group; scores go through LDS for the softmax.
+template <int HD, int GW>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
     const int* __restrict__ lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
     float* __restrict__ part, float* __restrict__ out, int nsplit) {
-    __shared__ float qs[HD];
-    __shared__ float ps[kThreads];
-    __shared__ float red[kThreads / 64];
-    __shared__ float acc_s[kThreads];
-    const int bh = blockIdx.x;  // batch * Hq + head
-    const int b = bh / Hq, h = bh % Hq;
-    const int kvh = h / (Hq / Hkv);
+    constexpr int LPP = HD / 8;          // lanes per position
+    constexpr int NG = kThreads / LPP;   // positions in flight per pass
+    constexpr int GPW = 64 / LPP;        // position groups per wave
+    __shared__ float sc[GW][256];
+    __shared__ float stat[GW][2];
+    __shared__ float red[kThreads / 64][GW][HD];
+    const int G = Hq / Hkv;
+    const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
     const int s = blockIdx.y;
+    const int h0 = kvh * G + blockIdx.z * GW;
+    const int nh = min(GW, G - (int)blockIdx.z * GW);
     const int L = lens ? lens[b] : len_host;
     const int p0 = s * S, p1 = min(L, p0 + S);
-    for (int i = threadIdx.x; i < HD; i += kThreads) qs[i] = q[(size_t)bh * HD + i];
-    __syncthreads();
-    float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lg = tid / LPP, li = tid % LPP;
     if (p0 >= p1) {  // empty split (the length is below this split's range)
-        if (nsplit > 1 && threadIdx.x == 0) {
-            pp[0] = -INFINITY;
-            pp[1] = 0.f;
+        for (int g = 0; g < nh; ++g) {
+            const int bh = b * Hq + h0 + g;
+            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            if (nsplit > 1) {
+                if (tid == 0) {
+                    pp[0] = -INFINITY;
+                    pp[1] = 0.f;
+                }
+                for (int i = tid; i < HD; i += kThreads) pp[2 + i] = 0.f;
+            } else {
+                for (int i = tid; i < HD; i += kThreads) out[(size_t)bh * HD + i] = 0.f;
+            }
         }
-        if (nsplit > 1)
-            for (int i = threadIdx.x; i < HD; i += kThreads) pp[2 + i] = 0.f;
-        else
-            for (int i = threadIdx.x; i < HD; i += kThreads) out[(size_t)bh * HD + i] = 0.f;
         return;
     }
-    // scores: one position per thread (S <= kThreads)
-    const int pos = p0 + threadIdx.x;
-    float sc = -INFINITY;
-    if (pos < p1) {
-        // the key row: HD fp16 values as 16-byte vectors
-        const h8* kr = reinterpret_cast<const h8*>(kc + (((size_t)b * T + pos) * Hkv + kvh) * HD);
-        float d = 0.f;
+    float qv[GW][8];
 #pragma unroll
-        for (int j = 0; j < HD / 8; ++j) {
-            const h8 kv = kr[j];
+    for (int g = 0; g < GW; ++g)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = fmaf(qs[j * 8 + i], (float)kv[i], d);
+        for (int i = 0; i < 8; ++i)
+            qv[g][i] = (g < nh) ? q[((size_t)b * Hq + h0 + g) * HD + li * 8 + i] : 0.f;
+    const size_t rstride = (size_t)Hkv * HD;
+    const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    // scores
+    for (int p = p0 + lg; p < p1; p += NG) {
+        const h8 kv = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
+#pragma unroll
+        for (int g = 0; g < GW; ++g) {
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], (float)kv[i], d);
+#pragma unroll
+            for (int off = LPP / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+            if (li == 0 && g < nh) sc[g][p - p0] = d * scale;
         }
-        sc = d * scale;
     }
-    const float m = block_max(sc, red);
-    const float e = (pos < p1) ? expf(sc - m) : 0.f;
-    ps[threadIdx.x] = e;
-    const float l = block_sum(e, red);
-    // P.V: thread t -> dim t % HD, positions p0 + g, g = t / HD, t/HD + G, ...
-    constexpr int G = kThreads / HD;
-    const int dim = threadIdx.x % HD, grp = threadIdx.x / HD;
-    float o = 0.f;
-    for (int j = grp; j < p1 - p0; j += G)
-        o = fmaf(ps[j], (float)vc[(((size_t)b * T + p0 + j) * Hkv + kvh) * HD + dim], o);
-    acc_s[threadIdx.x] = o;
     __syncthreads();
-    if (threadIdx.x < HD) {
+    // softmax statistics per head (wave w handles heads w, w + 4, ...)
+    const int n = p1 - p0;
+    for (int g = wave; g < nh; g += kThreads / 64) {
+        float m = -INFINITY;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[g][j]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int j = lane; j < n; j += 64) {
+            const float e = expf(sc[g][j] - m);
+            sc[g][j] = e;
+            l += e;
+        }
+        l = csdr::wave_sum(l);
+        if (lane == 0) {
+            stat[g][0] = m;
+            stat[g][1] = l;
+        }
+    }
+    __syncthreads();
+    // P.V: this lane's 8 dims over its positions, then across position groups
+    float o[GW][8];
+#pragma unroll
+    for (int g = 0; g < GW; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+    for (int p = p0 + lg; p < p1; p += NG) {
+        const h8 vv = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+#pragma unroll
+        for (int g = 0; g < GW; ++g) {
+            const float e = sc[g][p - p0];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[g][i] = fmaf(e, (float)vv[i], o[g][i]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GW; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float v = o[g][i];
+#pragma unroll
+            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+            o[g][i] = v;
+        }
+    (void)GPW;
+    if (lane < LPP) {
+#pragma unroll
+        for (int g = 0; g < GW; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red[wave][g][li * 8 + i] = o[g][i];
+    }
+    __syncthreads();
+    for (int e = tid; e < nh * HD; e += kThreads) {
+        const int g = e / HD, d = e % HD;
         float sum = 0.f;
-        for (int g2 = 0; g2 < G; ++g2) sum += acc_s[g2 * HD + threadIdx.x];
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) sum += red[w][g][d];
+        const int bh = b * Hq + h0 + g;
         if (nsplit == 1) {
-            out[(size_t)bh * HD + threadIdx.x] = sum / l;
+            out[(size_t)bh * HD + d] = sum / stat[g][1];
         } else {
-            pp[2 + threadIdx.x] = sum;
-            if (threadIdx.x == 0) {
-                pp[0] = m;
-                pp[1] = l;
+            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            pp[2 + d] = sum;
+            if (d == 0) {
+                pp[0] = stat[g][0];
+                pp[1] = stat[g][1];
             }
         }
     }
@@ -322,6 +400,29 @@ __global__ __launch_bounds__(kThreads) void select2_kernel(const float* __restri
 
 constexpr int kSelectBlocks = 256;
 
+// Positions per split: the power of two in [32, 256] that gives about 512 workgroups.
+int attn_split_len(int B, int Hkv, int zsplit, int T) {
+    const long long want = (long long)T * B * Hkv * zsplit / 512;
+    int S = 32;
+    while (S < 256 && S < want) S *= 2;
+    return S;
+}
+
+template <int HD>
+void launch_attn(dim3 grid, int G, const float* q, const _Float16* k16, const _Float16* v16,
+                 const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
+                 float* part, float* out, int nsplit, hipStream_t st) {
+    if (G == 1)
+        attn_split_kernel<HD, 1><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
+                                                             Hkv, scale, S, part, out, nsplit);
+    else if (G <= 4)
+        attn_split_kernel<HD, 4><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
+                                                             Hkv, scale, S, part, out, nsplit);
+    else
+        attn_split_kernel<HD, 8><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
+                                                             Hkv, scale, S, part, out, nsplit);
+}
+
 }  // namespace
 
 extern "C" {
@@ -330,7 +431,8 @@ CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, floa
                            void* hip_stream) {
     if (!x || !w || !y || ntok <= 0 || n <= 0)
         return set_error(CSDR_E_INVALID, "rms_norm: bad argument");
-    rms_norm_kernel<<<ntok, kThreads, 0, static_cast<hipStream_t>(hip_stream)>>>(x, w, n, eps, y);
+    const int nt = n > 2048 ? 1024 : 256;
+    rms_norm_kernel<<<ntok, nt, 0, static_cast<hipStream_t>(hip_stream)>>>(x, w, n, eps, y);
     CSDR_LAUNCH_CHECK("rms_norm");
     return CSDR_OK;
 }
@@ -361,7 +463,7 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
     if (!q || !k || !v || !pos_dev || !kcache || !vcache || ntok <= 0 || Hq <= 0 || Hkv <= 0 ||
         hd < 2 || Hq % Hkv)
         return set_error(CSDR_E_INVALID, "rope_kv: bad argument");
-    rope_kv_kernel<<<ntok, kThreads, 0, static_cast<hipStream_t>(hip_stream)>>>(
+    rope_kv_kernel<<<ntok * (Hq + Hkv), 64, 0, static_cast<hipStream_t>(hip_stream)>>>(
         q, k, v, ntok, Hq, Hkv, hd, pos_dev, theta, reinterpret_cast<_Float16*>(kcache),
         reinterpret_cast<_Float16*>(vcache), max_ctx);
     CSDR_LAUNCH_CHECK("rope_kv");
@@ -369,7 +471,7 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
 }
 
 CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T) {
-    const int nsplit = (T + kThreads - 1) / kThreads;
+    const int nsplit = (T + 31) / 32;  // the shortest split bounds the count
     return (size_t)B * Hq * nsplit * (hd + 2) * 4;
 }
 
@@ -382,25 +484,29 @@ CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint
         return set_error(CSDR_E_INVALID, "attn_decode: bad argument");
     if (!lens_dev && (len_host < 0 || len_host > T))
         return set_error(CSDR_E_INVALID, "attn_decode: length out of range");
-    const int nsplit = (T + kThreads - 1) / kThreads;
+    if (hd != 64 && hd != 128)
+        return set_error(CSDR_E_UNSUPPORTED, "attn_decode: head_dim must be 64 or 128");
+    const int G = Hq / Hkv;
+    const int GW = G == 1 ? 1 : (G <= 4 ? 4 : 8);
+    const int zsplit = (G + GW - 1) / GW;
+    const int S = attn_split_len(B, Hkv, zsplit, T);
+    const int nsplit = (T + S - 1) / S;
     if (nsplit > 1 && (!workspace || workspace_bytes < csdr_attn_decode_workspace_bytes(B, Hq, hd, T)))
         return set_error(CSDR_E_WORKSPACE, "attn_decode: workspace too small");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)hd);
     float* part = static_cast<float*>(workspace);
-    dim3 grid(B * Hq, nsplit);
+    dim3 grid(B * Hkv, nsplit, zsplit);
     auto k16 = reinterpret_cast<const _Float16*>(kcache);
     auto v16 = reinterpret_cast<const _Float16*>(vcache);
     if (hd == 64) {
-        attn_split_kernel<64><<<grid, kThreads, 0, st>>>(q, k16, v16, lens_dev, len_host, T, Hq,
-                                                        Hkv, scale, kThreads, part, out, nsplit);
+        launch_attn<64>(grid, G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale, S, part, out,
+                        nsplit, st);
         if (nsplit > 1) attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, nsplit, out);
-    } else if (hd == 128) {
-        attn_split_kernel<128><<<grid, kThreads, 0, st>>>(q, k16, v16, lens_dev, len_host, T, Hq,
-                                                         Hkv, scale, kThreads, part, out, nsplit);
-        if (nsplit > 1) attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, nsplit, out);
     } else {
-        return set_error(CSDR_E_UNSUPPORTED, "attn_decode: head_dim must be 64 or 128");
+        launch_attn<128>(grid, G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale, S, part,
+                         out, nsplit, st);
+        if (nsplit > 1) attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, nsplit, out);
     }
     CSDR_LAUNCH_CHECK("attn_decode");
     return CSDR_OK;

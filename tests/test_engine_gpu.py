@@ -50,7 +50,8 @@ def test_run_layer_routes(gpu, model, golden):
         assert eng.stats()["path"] == "hsdb"
         X = synth.activations(200, 3, seed=6)                # (C, M) -> the API's (M, C)
         Y = eng.run_layer("edge.weight", X.T).reshape(3, 40)
-        assert rel_l2(Y.T, oracle.hsdb_matmul(model["hsdb_edge"], X)) < 1e-5
+        # batches of 2+ take the matrix-core path (fp16 dictionary/weights: ~3e-4)
+        assert rel_l2(Y.T, oracle.hsdb_matmul(model["hsdb_edge"], X)) < 1e-3
         xr = golden["hsdr1d_x"]                              # reference HSDR payload, batch 4
         Y = eng.run_layer("hsdr_ref", xr.T).reshape(4, 64)
         assert rel_l2(Y.T, golden["hsdr1d_y"]) < 1e-5
@@ -123,7 +124,7 @@ def test_matmul_device(gpu, model):
         yd = gpu.empty((64, 5), dtype=gpu.float32, device="cuda")
         eng.matmul_device("blk.0.attn_q.weight", xd, yd)
         gpu.cuda.synchronize()
-        assert rel_l2(yd.cpu().numpy(), oracle.hsdb_matmul(model["hsdb"], X.astype(np.float32))) < 1e-5
+        assert rel_l2(yd.cpu().numpy(), oracle.hsdb_matmul(model["hsdb"], X.astype(np.float32))) < 1e-3
         with pytest.raises(EngineError):
             eng.matmul_device("dense.weight", xd, yd)        # not strategy 5
     finally:
@@ -142,8 +143,14 @@ def test_hsda_and_hsdc_loads(gpu):
     for i in range(3):
         name = f[f"hsda_name_{i}"].tobytes().decode()
         seg = a.load(name)
-        y = seg.matmul(x).cpu().numpy()
-        assert rel_l2(y, f[f"hsda_y_{i}"]) < 1e-6
+        y = seg.matmul(x).cpu().numpy()         # batch 3: matrix-core path (fp16 operands)
+        assert rel_l2(y, f[f"hsda_y_{i}"]) < 1e-3
+        os.environ["CSDR_HSDB_MFMA"] = "0"      # the fp32 path agrees to rounding
+        try:
+            y32 = seg.matmul(x).cpu().numpy()
+        finally:
+            del os.environ["CSDR_HSDB_MFMA"]
+        assert rel_l2(y32, f[f"hsda_y_{i}"]) < 1e-6
         w = seg.decompress().cpu().numpy()
         assert np.array_equal(w.view(np.uint32), f[f"hsda_w_{i}"].view(np.uint32))
         seg.free()
