@@ -133,6 +133,14 @@ SIGNATURES.update({
                                     C.POINTER(C.c_uint64)]),
     "csdr_hsda_load": (C.c_int, [_vp, C.c_char_p, _vp, C.POINTER(_vp)]),
     "csdr_dense_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
+    "csdr_hsdb_matmul_group_xop": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp),
+                                             C.POINTER(_vp), C.c_int, C.POINTER(_vp),
+                                             C.POINTER(_vp), C.c_int, C.c_int, _vp, C.c_float,
+                                             C.c_int, C.c_int, _vp, _sz, _vp]),
+    "csdr_attn_decode_splits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "csdr_attn_decode_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_float, C.c_float, _vp, _vp, _sz,
+                                        _vp]),
     "cortex_inference_engine_create": (_ce, [C.c_char_p, C.POINTER(_vp)]),
     "cortex_inference_engine_free": (_ce, [_vp]),
     "cortex_inference_engine_set_batch_size": (_ce, [_vp, _sz]),

@@ -118,6 +118,8 @@ struct csdr_decoder {
     float g_temp = 0.0f, g_pen = 0.0f;  // sampling parameters graph[1] was captured with
     int host_pos = 0;                   // positions processed (host mirror of *pos)
     bool use_graph = true;              // CSDR_DECODER_GRAPH=0: issue each step's kernels directly
+    bool fused = true;                  // CSDR_DECODER_FUSED=0: one launch per op (reference order)
+    int attn_splits = 1;
     int n_prompt = 0;
     std::vector<void*> allocs;
 };
@@ -174,6 +176,21 @@ int mm(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x, flo
                                      d->ws_hsdb_bytes, st);
 }
 
+int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x, const float* x2,
+           float* const* ys, const float* const* bias, int flags, int xop, const float* nw,
+           hipStream_t st) {
+    const void* xs[4];
+    const void* x2s[4];
+    for (int i = 0; i < n; ++i) {
+        xs[i] = x;
+        x2s[i] = x2;
+    }
+    const csdr_decoder_config& c = d->cfg;
+    return csdr_hsdb_matmul_group_xop(n, segs, xs, x2s, 1, ys, bias, flags, xop, nw, c.rms_eps,
+                                      d->attn_splits, c.head_dim, d->ws_hsdb, d->ws_hsdb_bytes,
+                                      st);
+}
+
 // One step at device position *pos for the token ring[*pos]; with_head adds the output norm,
 // the lm_head scores and the token selection.
 int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, float penalty) {
@@ -183,7 +200,37 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
     step_begin_kernel<<<1, 64, 0, st>>>(d->pos, d->ring, cap, d->tok, d->len);
     CSDR_LAUNCH_CHECK("decoder step_begin");
     RC(csdr_hsdb_decode_row(d->emb, d->tok, 0, d->x, st));
-    for (int l = 0; l < c.n_layers; ++l) {
+    for (int l = 0; l < c.n_layers && d->fused; ++l) {
+        // fused form: 5 calls (9 launches) per block; the normed inputs, the rotated q/k, the
+        // attention output and silu(gate)*up are never written out
+        const Layer& L = d->layers[l];
+        {
+            const csdr_hsdb* segs[3] = {L.q, L.k, L.v};
+            float* ys[3] = {d->q, d->k, d->v};
+            const float* bias[3] = {L.bq, L.bk, L.bv};
+            RC(mm_xop(d, 3, segs, d->x, nullptr, ys, bias, 0, CSDR_XOP_RMSNORM, L.attn_norm, st));
+        }
+        RC(csdr_attn_decode_rope(d->q, d->k, d->v, L.kc, L.vc, d->len, 1, c.max_ctx, Hq, Hkv, hd,
+                                 c.rope_theta, 0.0f, nullptr, d->ws_attn, d->ws_attn_bytes, st));
+        {
+            const csdr_hsdb* segs[1] = {L.o};
+            float* ys[1] = {d->x};  // x += o(attention)
+            RC(mm_xop(d, 1, segs, static_cast<const float*>(d->ws_attn), nullptr, ys, nullptr,
+                      CSDR_HSDB_ACCUMULATE, CSDR_XOP_ATTN, nullptr, st));
+        }
+        {
+            const csdr_hsdb* segs[2] = {L.gate, L.up};
+            float* ys[2] = {d->g, d->u};
+            RC(mm_xop(d, 2, segs, d->x, nullptr, ys, nullptr, 0, CSDR_XOP_RMSNORM, L.ffn_norm, st));
+        }
+        {
+            const csdr_hsdb* segs[1] = {L.down};
+            float* ys[1] = {d->x};  // x += down(silu(gate) * up)
+            RC(mm_xop(d, 1, segs, d->g, d->u, ys, nullptr, CSDR_HSDB_ACCUMULATE,
+                      CSDR_XOP_SILU_MUL, nullptr, st));
+        }
+    }
+    for (int l = 0; l < c.n_layers && !d->fused; ++l) {
         const Layer& L = d->layers[l];
         RC(csdr_rms_norm(d->x, L.attn_norm, 1, H, c.rms_eps, d->h, st));
         {
@@ -313,6 +360,8 @@ CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** 
     d->cfg = c;
     d->layers.resize(c.n_layers);
     if (const char* e = getenv("CSDR_DECODER_GRAPH")) d->use_graph = atoi(e) != 0;
+    if (const char* e = getenv("CSDR_DECODER_FUSED")) d->fused = atoi(e) != 0;
+    d->attn_splits = csdr_attn_decode_splits(1, c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx);
     int rc = CSDR_OK;
     const size_t kvn = (size_t)c.max_ctx * c.n_kv_heads * c.head_dim;
     for (auto& L : d->layers)

@@ -141,8 +141,9 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q,
         const float ang = (float)pos * freq;
         const float c = cosf(ang), sn = sinf(ang);
         const float x0 = base[i2], x1 = base[i2 + 1];
-        base[i2] = x0 * c - x1 * sn;
-        base[i2 + 1] = x0 * sn + x1 * c;
+        // explicit fma forms, the same in the fused attention, so both paths round alike
+        base[i2] = fmaf(x0, c, -(x1 * sn));
+        base[i2 + 1] = fmaf(x0, sn, x1 * c);
     }
     if (head < Hq || pos >= max_ctx) return;
     __syncthreads();
@@ -162,11 +163,22 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q,
 // o[hd] = sum exp * v) per head. LPP = HD/8 lanes hold one position's 16-byte K/V pieces
 // (one coalesced HD*2-byte row per position), so each K/V byte is read once for all the
 // query heads of its group; scores go through LDS for the softmax.
-template <int HD, int GW>
+// Fused form (ROPE): the query is rotated in registers at position L - 1, position L - 1's key
+// and value come from the projections (k_new rotated, both rounded to fp16 as the cache holds
+// them), and the workgroup whose split holds L - 1 appends them to the caches.
+struct RopeArgs {
+    const float* knew;  // B x Hkv x HD (fp32, unrotated)
+    const float* vnew;
+    _Float16* kcw;
+    _Float16* vcw;
+    float theta;
+};
+
+template <int HD, int GW, bool ROPE>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
     const int* __restrict__ lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
-    float* __restrict__ part, float* __restrict__ out, int nsplit) {
+    float* __restrict__ part, float* __restrict__ out, int nsplit, RopeArgs ra) {
     constexpr int LPP = HD / 8;          // lanes per position
     constexpr int NG = kThreads / LPP;   // positions in flight per pass
     constexpr int GPW = 64 / LPP;        // position groups per wave
@@ -182,11 +194,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const int p0 = s * S, p1 = min(L, p0 + S);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lg = tid / LPP, li = tid % LPP;
+    const bool direct = (nsplit == 1 && out != nullptr);
     if (p0 >= p1) {  // empty split (the length is below this split's range)
         for (int g = 0; g < nh; ++g) {
             const int bh = b * Hq + h0 + g;
             float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
-            if (nsplit > 1) {
+            if (!direct) {
                 if (tid == 0) {
                     pp[0] = -INFINITY;
                     pp[1] = 0.f;
@@ -207,9 +220,44 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const size_t rstride = (size_t)Hkv * HD;
     const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
     const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    const int plast = L - 1;
+    h8 knew = {}, vnew = {};
+    if constexpr (ROPE) {
+        // rotate this lane's 8 query dims of every head, and the new key, at position L - 1
+        const float* kn = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+        const float* vn = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const int i2 = li * 8 + i;
+            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
+            const float ang = (float)plast * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+#pragma unroll
+            for (int g = 0; g < GW; ++g) {
+                const float x0 = qv[g][i], x1 = qv[g][i + 1];
+                qv[g][i] = fmaf(x0, c, -(x1 * sn));
+                qv[g][i + 1] = fmaf(x0, sn, x1 * c);
+            }
+            const float k0 = kn[i], k1 = kn[i + 1];
+            knew[i] = (_Float16)fmaf(k0, c, -(k1 * sn));
+            knew[i + 1] = (_Float16)fmaf(k0, sn, k1 * c);
+            vnew[i] = (_Float16)vn[i];
+            vnew[i + 1] = (_Float16)vn[i + 1];
+        }
+        if (blockIdx.z == 0 && plast >= p0 && plast < p1 && lg == (plast - p0) % NG) {
+            *reinterpret_cast<h8*>(ra.kcw + ((size_t)b * T + plast) * rstride + kvh * HD + li * 8) =
+                knew;
+            *reinterpret_cast<h8*>(ra.vcw + ((size_t)b * T + plast) * rstride + kvh * HD + li * 8) =
+                vnew;
+        }
+    }
     // scores
     for (int p = p0 + lg; p < p1; p += NG) {
-        const h8 kv = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
+        h8 kv;
+        if (ROPE && p == plast)
+            kv = knew;
+        else
+            kv = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             float d = 0.f;
@@ -247,7 +295,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
     for (int p = p0 + lg; p < p1; p += NG) {
-        const h8 vv = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+        h8 vv;
+        if (ROPE && p == plast)
+            vv = vnew;
+        else
+            vv = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             const float e = sc[g][p - p0];
@@ -278,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 #pragma unroll
         for (int w = 0; w < kThreads / 64; ++w) sum += red[w][g][d];
         const int bh = b * Hq + h0 + g;
-        if (nsplit == 1) {
+        if (direct) {
             out[(size_t)bh * HD + d] = sum / stat[g][1];
         } else {
             float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
@@ -400,27 +452,78 @@ __global__ __launch_bounds__(kThreads) void select2_kernel(const float* __restri
 
 constexpr int kSelectBlocks = 256;
 
-// Positions per split: the power of two in [32, 256] that gives about 512 workgroups.
+// Positions per split: the power of two in [64, 256] that gives about 512 workgroups (at
+// least 64 positions per split keeps the partial count small for short contexts).
 int attn_split_len(int B, int Hkv, int zsplit, int T) {
     const long long want = (long long)T * B * Hkv * zsplit / 512;
-    int S = 32;
+    int S = 64;
     while (S < 256 && S < want) S *= 2;
     return S;
 }
 
-template <int HD>
+template <int HD, bool ROPE>
 void launch_attn(dim3 grid, int G, const float* q, const _Float16* k16, const _Float16* v16,
                  const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
-                 float* part, float* out, int nsplit, hipStream_t st) {
+                 float* part, float* out, int nsplit, const RopeArgs& ra, hipStream_t st) {
     if (G == 1)
-        attn_split_kernel<HD, 1><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
-                                                             Hkv, scale, S, part, out, nsplit);
+        attn_split_kernel<HD, 1, ROPE><<<grid, kThreads, 0, st>>>(
+            q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
     else if (G <= 4)
-        attn_split_kernel<HD, 4><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
-                                                             Hkv, scale, S, part, out, nsplit);
+        attn_split_kernel<HD, 4, ROPE><<<grid, kThreads, 0, st>>>(
+            q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
     else
-        attn_split_kernel<HD, 8><<<grid, kThreads, 0, st>>>(q, k16, v16, lens, len_host, T, Hq,
-                                                             Hkv, scale, S, part, out, nsplit);
+        attn_split_kernel<HD, 8, ROPE><<<grid, kThreads, 0, st>>>(
+            q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
+}
+
+struct AttnShape {
+    int G, GW, zsplit, S, nsplit;
+};
+
+AttnShape attn_shape(int B, int Hq, int Hkv, int T) {
+    AttnShape a;
+    a.G = Hq / Hkv;
+    a.GW = a.G == 1 ? 1 : (a.G <= 4 ? 4 : 8);
+    a.zsplit = (a.G + a.GW - 1) / a.GW;
+    a.S = attn_split_len(B, Hkv, a.zsplit, T);
+    a.nsplit = (T + a.S - 1) / a.S;
+    return a;
+}
+
+int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* lens_dev,
+             int len_host, int B, int T, int Hq, int Hkv, int hd, float scale, float* out,
+             void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t st) {
+    const AttnShape sh = attn_shape(B, Hq, Hkv, T);
+    const bool partials = sh.nsplit > 1 || out == nullptr;
+    if (partials &&
+        (!workspace || workspace_bytes < csdr_attn_decode_workspace_bytes(B, Hq, hd, T)))
+        return set_error(CSDR_E_WORKSPACE, "attn_decode: workspace too small");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)hd);
+    float* part = static_cast<float*>(workspace);
+    dim3 grid(B * Hkv, sh.nsplit, sh.zsplit);
+    auto k16 = reinterpret_cast<const _Float16*>(kcache);
+    auto v16 = reinterpret_cast<const _Float16*>(vcache);
+    const RopeArgs none{};
+    if (hd == 64) {
+        if (ra)
+            launch_attn<64, true>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale,
+                                  sh.S, part, out, sh.nsplit, *ra, st);
+        else
+            launch_attn<64, false>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale,
+                                   sh.S, part, out, sh.nsplit, none, st);
+        if (out && sh.nsplit > 1) attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, sh.nsplit, out);
+    } else {
+        if (ra)
+            launch_attn<128, true>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv,
+                                   scale, sh.S, part, out, sh.nsplit, *ra, st);
+        else
+            launch_attn<128, false>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv,
+                                    scale, sh.S, part, out, sh.nsplit, none, st);
+        if (out && sh.nsplit > 1)
+            attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, sh.nsplit, out);
+    }
+    CSDR_LAUNCH_CHECK("attn_decode");
+    return CSDR_OK;
 }
 
 }  // namespace
@@ -471,7 +574,7 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
 }
 
 CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T) {
-    const int nsplit = (T + 31) / 32;  // the shortest split bounds the count
+    const int nsplit = (T + 63) / 64;  // the shortest split bounds the count
     return (size_t)B * Hq * nsplit * (hd + 2) * 4;
 }
 
@@ -486,30 +589,30 @@ CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint
         return set_error(CSDR_E_INVALID, "attn_decode: length out of range");
     if (hd != 64 && hd != 128)
         return set_error(CSDR_E_UNSUPPORTED, "attn_decode: head_dim must be 64 or 128");
-    const int G = Hq / Hkv;
-    const int GW = G == 1 ? 1 : (G <= 4 ? 4 : 8);
-    const int zsplit = (G + GW - 1) / GW;
-    const int S = attn_split_len(B, Hkv, zsplit, T);
-    const int nsplit = (T + S - 1) / S;
-    if (nsplit > 1 && (!workspace || workspace_bytes < csdr_attn_decode_workspace_bytes(B, Hq, hd, T)))
-        return set_error(CSDR_E_WORKSPACE, "attn_decode: workspace too small");
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    if (scale == 0.0f) scale = 1.0f / sqrtf((float)hd);
-    float* part = static_cast<float*>(workspace);
-    dim3 grid(B * Hkv, nsplit, zsplit);
-    auto k16 = reinterpret_cast<const _Float16*>(kcache);
-    auto v16 = reinterpret_cast<const _Float16*>(vcache);
-    if (hd == 64) {
-        launch_attn<64>(grid, G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale, S, part, out,
-                        nsplit, st);
-        if (nsplit > 1) attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, nsplit, out);
-    } else {
-        launch_attn<128>(grid, G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale, S, part,
-                         out, nsplit, st);
-        if (nsplit > 1) attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, nsplit, out);
-    }
-    CSDR_LAUNCH_CHECK("attn_decode");
-    return CSDR_OK;
+    return attn_run(q, kcache, vcache, lens_dev, len_host, B, T, Hq, Hkv, hd, scale, out,
+                    workspace, workspace_bytes, nullptr, static_cast<hipStream_t>(hip_stream));
+}
+
+CSDR_API int csdr_attn_decode_splits(int B, int Hq, int Hkv, int hd, int T) {
+    (void)hd;
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || Hq % Hkv) return -1;
+    return attn_shape(B, Hq, Hkv, T).nsplit;
+}
+
+CSDR_API int csdr_attn_decode_rope(const float* q, const float* k_new, const float* v_new,
+                                   uint16_t* kcache, uint16_t* vcache, const int* lens_dev, int B,
+                                   int T, int Hq, int Hkv, int hd, float theta, float scale,
+                                   float* out, void* workspace, size_t workspace_bytes,
+                                   void* hip_stream) {
+    if (!q || !k_new || !v_new || !kcache || !vcache || !lens_dev || B <= 0 || T <= 0 ||
+        Hq <= 0 || Hkv <= 0 || Hq % Hkv)
+        return set_error(CSDR_E_INVALID, "attn_decode_rope: bad argument");
+    if (hd != 64 && hd != 128)
+        return set_error(CSDR_E_UNSUPPORTED, "attn_decode_rope: head_dim must be 64 or 128");
+    RopeArgs ra{k_new, v_new, reinterpret_cast<_Float16*>(kcache),
+                reinterpret_cast<_Float16*>(vcache), theta};
+    return attn_run(q, kcache, vcache, lens_dev, 0, B, T, Hq, Hkv, hd, scale, out, workspace,
+                    workspace_bytes, &ra, static_cast<hipStream_t>(hip_stream));
 }
 
 CSDR_API size_t csdr_select_workspace_bytes(void) { return (size_t)kSelectBlocks * 8; }

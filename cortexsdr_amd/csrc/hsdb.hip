@@ -54,6 +54,7 @@ constexpr int kMaxSlotsArg = 32;
 constexpr int kStageBatch = 8;  // global loads in flight per thread while staging to LDS
 constexpr int kDepth = 3;       // code units in flight per gather workgroup (M == 1)
 constexpr int kGatherWGsPerCU = 8;
+constexpr int kMaxXopM = 16;  // columns an x op supports
 
 // One coded matrix of a grouped launch.
 struct MatDesc {
@@ -65,6 +66,8 @@ struct MatDesc {
     float* y;
     const float* bias;  // per output row, added once (nullable)
     float* P;  // NB * K * M floats of workspace
+    const void* x2;  // second input of the x op (SiLU: the up projection)
+    float* xe;       // x op: transformed edge-strip inputs, Ce x M (workspace), else null
     int R, K, NB, NBc, nchunks, slots, blen, Ce, C_full;
     int PB;                   // dx: block columns per workgroup (block length 64)
     int dx_base, dx_count;    // dx workgroup ids [base, base + count)
@@ -79,6 +82,11 @@ struct Params {
     MatDesc m[kMaxGroup];
     int G, M, MVz, x_f16;
     int accumulate;  // 1: Y += W.X (+ bias); 0: Y = W.X (+ bias)
+    // input transform applied while staging x (csdr_hsdb_matmul_group_xop)
+    int xop;          // CSDR_XOP_*
+    const float* nw;  // RMSNorm weights (C)
+    float eps;
+    int nsplit, hd;   // attention combine: splits and head size of the partials in x
 };
 
 template <int CTRL>
@@ -143,6 +151,49 @@ __device__ __forceinline__ void copy_to_lds4(const float* __restrict__ src, int 
 // ---- kernel 1 (dx): P[b][a][m] = D[a] . X[b*B : b*B+B, m] (the reference's Dx precompute)
 // and Y = 0 (the gathers accumulate into Y). Visibility to the gather kernel comes from the
 // dispatch boundary.
+// ---- input transforms fused into the dx staging (x op)
+
+// Workgroup sum of v (kThreads threads), result in every thread.
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+    v = csdr::wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kThreads / 64; ++i) t += red[i];
+    return t;
+}
+
+// Attention output feature k (head k / hd, dim k % hd) combined from the split partials
+// (m, l, o[hd]) of attn_decode's workspace layout.
+__device__ __forceinline__ float attn_feature(const Params& p, const float* part, int k) {
+    const int h = k / p.hd, dd = k - h * p.hd;
+    const float* pp = part + (size_t)h * p.nsplit * (p.hd + 2);
+    float Mx = -INFINITY;
+    for (int s = 0; s < p.nsplit; ++s) Mx = fmaxf(Mx, pp[(size_t)s * (p.hd + 2)]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < p.nsplit; ++s) {
+        const float ms = pp[(size_t)s * (p.hd + 2)];
+        if (ms == -INFINITY) continue;
+        const float w = expf(ms - Mx);
+        den = fmaf(w, pp[(size_t)s * (p.hd + 2) + 1], den);
+        num = fmaf(w, pp[(size_t)s * (p.hd + 2) + 2 + dd], num);
+    }
+    return den > 0.f ? num / den : 0.f;
+}
+
+// x op of element (feature k, column m) given the raw value v (and inv[m] for RMSNorm).
+__device__ __forceinline__ float xop_apply(const Params& p, const MatDesc& d, float v, int k,
+                                           int m, const float* inv) {
+    if (p.xop == CSDR_XOP_RMSNORM) return v * inv[m] * p.nw[k];
+    if (p.xop == CSDR_XOP_SILU_MUL) {
+        const float u = static_cast<const float*>(d.x2)[(size_t)k * p.M + m];
+        return (v * (1.0f / (1.0f + expf(-v)))) * u;
+    }
+    return v;
+}
+
 __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     extern __shared__ float smem[];
     const int wg = blockIdx.x;
@@ -177,10 +228,76 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
         float* xs = smem;  // [bb][t][m], nb * 64 * M floats (x rows are contiguous)
         const size_t xbase = (size_t)b0 * 64 * M;
         const int nx = nb * 64 * M;
-        if (p.x_f16)
+        __shared__ float inv[kMaxXopM];
+        __shared__ float red[kThreads / 64];
+        if (p.xop == CSDR_XOP_RMSNORM) {
+            // 1 / rms of every column over all C features (each workgroup recomputes it: x is
+            // a few KiB, L2-resident)
+            const float* xf = static_cast<const float*>(d.x);
+            const int C = d.C_full + d.Ce;
+            for (int m = 0; m < M; ++m) {
+                float ss = 0.f;
+                for (int k = tid; k < C; k += kThreads) {
+                    const float v = xf[(size_t)k * M + m];
+                    ss = fmaf(v, v, ss);
+                }
+                ss = wg_sum(ss, red);
+                if (tid == 0) inv[m] = 1.0f / sqrtf(ss / (float)C + p.eps);
+            }
+        }
+        if (p.xop == CSDR_XOP_ATTN) {
+            // per head of this range: split weights exp(m_s - max) and 1 / sum(w_s l_s) in
+            // LDS once, then every feature is one weighted sum over the splits
+            const float* part = static_cast<const float*>(d.x);
+            const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
+            const int h0 = (b0 * 64) / hd, h1 = (b0 * 64 + nx - 1) / hd + 1;
+            float* wts = xs + nx;  // (h1 - h0) x (ns + 1)
+            for (int h = h0 + tid; h < h1; h += kThreads) {
+                const float* pp = part + (size_t)h * ns * ps;
+                float Mx = -INFINITY;
+                for (int s2 = 0; s2 < ns; ++s2) Mx = fmaxf(Mx, pp[(size_t)s2 * ps]);
+                float den = 0.f;
+                float* wh = wts + (h - h0) * (ns + 1);
+                for (int s2 = 0; s2 < ns; ++s2) {
+                    const float ms = pp[(size_t)s2 * ps];
+                    const float w = ms == -INFINITY ? 0.f : expf(ms - Mx);
+                    wh[s2] = w;
+                    den = fmaf(w, pp[(size_t)s2 * ps + 1], den);
+                }
+                wh[ns] = den > 0.f ? 1.0f / den : 0.f;
+            }
+            __syncthreads();
+            for (int i = tid; i < nx; i += kThreads) {
+                const int k = b0 * 64 + i, h = k / hd, dd = k - h * hd;
+                const float* wh = wts + (h - h0) * (ns + 1);
+                const float* po = part + (size_t)h * ns * ps + 2 + dd;
+                float num = 0.f;
+                for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * ps], num);
+                xs[i] = num * wh[ns];
+            }
+        } else if (p.x_f16) {
             stage_to_lds(static_cast<const _Float16*>(d.x) + xbase, nx, xs);
-        else
+        } else {
             stage_to_lds(static_cast<const float*>(d.x) + xbase, nx, xs);
+        }
+        if (p.xop == CSDR_XOP_RMSNORM || p.xop == CSDR_XOP_SILU_MUL) {
+            __syncthreads();
+            for (int i = tid; i < nx; i += kThreads) {
+                const int k = b0 * 64 + i / M, m = i % M;
+                xs[i] = xop_apply(p, d, xs[i], k, m, inv);
+            }
+            if (u == 0 && d.xe) {
+                const float* xf = static_cast<const float*>(d.x);
+                for (int t = tid; t < d.Ce * M; t += kThreads) {
+                    const int cc = t / M, m = t % M;
+                    const int k = d.C_full + cc;
+                    d.xe[t] = xop_apply(p, d, xf[(size_t)k * M + m], k, m, inv);
+                }
+            }
+        } else if (p.xop == CSDR_XOP_ATTN && u == 0 && d.xe) {
+            const float* part = static_cast<const float*>(d.x);
+            for (int t = tid; t < d.Ce; t += kThreads) d.xe[t] = attn_feature(p, part, d.C_full + t);
+        }
         float4 dv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (live) dv = reinterpret_cast<const float4*>(d.dict + (size_t)a * 64)[l16];
         float* const Pout = d.P + (size_t)b0 * d.K * M + (size_t)a * M;  // + bb*K*M + m
@@ -275,10 +392,16 @@ __device__ __forceinline__ bool gather_slot(const Params& p, int& g, int& c, int
 __device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, int r, int m) {
     float s = 0.0f;
     const float* e = d.edge + (size_t)r * d.Ce;
+    if (d.xe) {
+        for (int cc = 0; cc < d.Ce; ++cc) s = fmaf(e[cc], d.xe[(size_t)cc * p.M + m], s);
+        return s;
+    }
     for (int cc = 0; cc < d.Ce; ++cc)
         s = fmaf(e[cc], xload(d.x, p.x_f16, (size_t)(d.C_full + cc) * p.M + m), s);
     return s;
 }
+
+
 
 // ---- kernel 2, M == 1: persistent gather. Workgroup = (chunk, row range). It stages the
 // chunk's P slice (nbc * K floats) in LDS once, then walks its rows in units of
@@ -713,7 +836,8 @@ inline int producer_blocks(int M) {
 }
 
 size_t p_bytes(const csdr_hsdb* s, int M) {
-    return csdr::align_up((size_t)s->NB * s->K * M * 4, 256);
+    return csdr::align_up((size_t)s->NB * s->K * M * 4, 256) +
+           csdr::align_up((size_t)s->Ce * M * 4, 256);  // x-op edge inputs
 }
 
 // Workspace of the P path (dx + gather launches).
@@ -749,10 +873,18 @@ void launch_gather1(const Params& p, int slots, int grid, size_t lds, hipStream_
 constexpr int kPhaseDx = 1;
 constexpr int kPhaseGather = 2;
 
+struct XopArgs {
+    int xop = CSDR_XOP_NONE;
+    const void* const* x2 = nullptr;
+    const float* nw = nullptr;
+    float eps = 0.f;
+    int nsplit = 0, hd = 0;
+};
+
 int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
                  float* const* ys, void* workspace, size_t workspace_bytes, hipStream_t st,
                  int phases = kPhaseDx | kPhaseGather, const float* const* bias = nullptr,
-                 int flags = 0) {
+                 int flags = 0, const XopArgs& xa = XopArgs()) {
     if (n <= 0 || n > kMaxGroup || !segs || !xs || !ys || M <= 0)
         return set_error(CSDR_E_INVALID, "hsdb_matmul: bad argument (group of 1.." +
                                              std::to_string(kMaxGroup) + ")");
@@ -761,7 +893,23 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     for (int i = 0; i < n; ++i)
         if (!segs[i] || !xs[i] || !ys[i])
             return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
-    if (phases == (kPhaseDx | kPhaseGather) && csdr::mfma_eligible(n, segs, M))
+    if (xa.xop != CSDR_XOP_NONE) {
+        if (x_dtype != CSDR_F32 || M > kMaxXopM)
+            return set_error(CSDR_E_INVALID, "hsdb_matmul: x ops take fp32 x and M <= " +
+                                                 std::to_string(kMaxXopM));
+        if (xa.xop == CSDR_XOP_RMSNORM && !xa.nw)
+            return set_error(CSDR_E_INVALID, "hsdb_matmul: RMSNorm x op needs weights");
+        if (xa.xop == CSDR_XOP_ATTN && (M != 1 || xa.nsplit <= 0 || xa.hd <= 0))
+            return set_error(CSDR_E_INVALID, "hsdb_matmul: attention x op needs M == 1, splits, hd");
+        for (int i = 0; i < n; ++i) {
+            if (segs[i]->tile_cols != 64)
+                return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: x ops need 64-column blocks");
+            if (xa.xop == CSDR_XOP_SILU_MUL && (!xa.x2 || !xa.x2[i]))
+                return set_error(CSDR_E_INVALID, "hsdb_matmul: SiLU x op needs x2");
+        }
+    }
+    if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE &&
+        csdr::mfma_eligible(n, segs, M))
         return csdr::mfma_matmul(n, segs, xs, x_dtype, M, ys, bias,
                                  (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0, workspace,
                                  workspace_bytes, st);
@@ -776,6 +924,11 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     p.MVz = (M + MV - 1) / MV;
     p.x_f16 = (x_dtype == CSDR_F16);
     p.accumulate = (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0;
+    p.xop = xa.xop;
+    p.nw = xa.nw;
+    p.eps = xa.eps;
+    p.nsplit = xa.nsplit;
+    p.hd = xa.hd;
     char* ws = static_cast<char*>(workspace);
     size_t off = kWsHeader;
     // the register-resident M == 1 gather needs every matrix at 4, 8 or 16 slots (16-byte
@@ -808,6 +961,11 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.y = ys[i];
         d.bias = bias ? bias[i] : nullptr;
         d.P = reinterpret_cast<float*>(ws + off);
+        d.x2 = (xa.xop == CSDR_XOP_SILU_MUL) ? xa.x2[i] : nullptr;
+        d.xe = (xa.xop != CSDR_XOP_NONE && s->Ce > 0)
+                   ? reinterpret_cast<float*>(ws + off +
+                                              csdr::align_up((size_t)s->NB * s->K * M * 4, 256))
+                   : nullptr;
         off += p_bytes(s, M);
         d.R = (int)s->R;
         d.K = (int)s->K;
@@ -821,7 +979,10 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.PB = producer_blocks(M);
         if (d.blen == 64) {
             d.dx_count = ((d.K + 15) / 16) * ((d.NB + d.PB - 1) / d.PB);
-            lds_dx = std::max(lds_dx, (size_t)d.PB * 64 * M * 4);
+            size_t extra = 0;
+            if (xa.xop == CSDR_XOP_ATTN)  // split weights of the heads a workgroup covers
+                extra = ((size_t)d.PB * 64 / std::max(1, xa.hd) + 2) * (xa.nsplit + 1) * 4;
+            lds_dx = std::max(lds_dx, (size_t)d.PB * 64 * M * 4 + extra);
         } else {
             const long long items = (long long)d.NB * d.K * ((M + 7) / 8);
             d.dx_count = (int)((items + kThreads / 64 - 1) / (kThreads / 64));
@@ -978,6 +1139,26 @@ CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, cons
     return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
                         static_cast<hipStream_t>(hip_stream), kPhaseDx | kPhaseGather, bias,
                         flags);
+}
+
+CSDR_API int csdr_hsdb_matmul_group_xop(int n, const csdr_hsdb* const* segs,
+                                        const void* const* x, const void* const* x2, int M,
+                                        float* const* y, const float* const* bias, int flags,
+                                        int xop, const float* norm_w, float eps, int attn_splits,
+                                        int attn_head_dim, void* workspace,
+                                        size_t workspace_bytes, void* hip_stream) {
+    if (xop < CSDR_XOP_NONE || xop > CSDR_XOP_ATTN)
+        return set_error(CSDR_E_INVALID, "hsdb_matmul_group_xop: unknown x op");
+    XopArgs xa;
+    xa.xop = xop;
+    xa.x2 = x2;
+    xa.nw = norm_w;
+    xa.eps = eps;
+    xa.nsplit = attn_splits;
+    xa.hd = attn_head_dim;
+    return matmul_group(n, segs, x, CSDR_F32, M, y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream), kPhaseDx | kPhaseGather, bias,
+                        flags, xa);
 }
 
 CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* s, const int* row_dev, int row_host, float* out,

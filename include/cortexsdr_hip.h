@@ -146,6 +146,25 @@ CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, cons
                                        const float* const* bias, int flags, void* workspace,
                                        size_t workspace_bytes, void* hip_stream);
 
+/* As csdr_hsdb_matmul_group_ex (fp32 x, P path) with an input transform applied while x is
+ * staged, so the transformed vector is never written out (decoder kernel fusion):
+ *   CSDR_XOP_RMSNORM   x := x / sqrt(mean(x^2) + eps) * norm_w, per column (rms_norm,
+ *                      cortex_sdk.cpp:1208-1232); M <= 16
+ *   CSDR_XOP_SILU_MUL  x := silu(x) * x2 (silu_mul, :1245-1256); M <= 16
+ *   CSDR_XOP_ATTN      x := the attention output combined from csdr_attn_decode's split
+ *                      partials (x = its workspace, attn_splits splits, attn_head_dim); M == 1
+ * Matrices need 64-column blocks. */
+#define CSDR_XOP_NONE 0
+#define CSDR_XOP_RMSNORM 1
+#define CSDR_XOP_SILU_MUL 2
+#define CSDR_XOP_ATTN 3
+CSDR_API int csdr_hsdb_matmul_group_xop(int n, const csdr_hsdb* const* segs,
+                                        const void* const* x, const void* const* x2, int M,
+                                        float* const* y, const float* const* bias, int flags,
+                                        int xop, const float* norm_w, float eps, int attn_splits,
+                                        int attn_head_dim, void* workspace,
+                                        size_t workspace_bytes, void* hip_stream);
+
 /* Row `row` of W (1-row tiles) decoded into out[C] (device), bit-identical to the same row
  * of csdr_hsdb_decompress. The row is *row_dev when row_dev is not NULL (a token id produced
  * on the device, e.g. a tied embedding lookup inside a captured decode step), else row_host.
@@ -221,6 +240,20 @@ CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint
                               const int* lens_dev, int len_host, int B, int T, int Hq, int Hkv,
                               int hd, float scale, float* out, void* workspace,
                               size_t workspace_bytes, void* hip_stream);
+/* Number of position splits csdr_attn_decode uses for this shape (the partial count the
+ * CSDR_XOP_ATTN x op combines). */
+CSDR_API int csdr_attn_decode_splits(int B, int Hq, int Hkv, int hd, int T);
+/* Decode attention fused with RoPE and the KV append, for one new token per batch entry at
+ * position lens_dev[b] - 1: q (B x Hq x hd) and k_new (B x Hkv x hd) are rotated in
+ * registers (apply_rope_inplace, cortex_sdk.cpp:1395-1423), k_new and v_new are rounded to
+ * fp16 and appended to the caches at that position, and the attention reads them from there.
+ * out = NULL leaves the split partials in the workspace for a consumer that combines them
+ * (csdr_hsdb_matmul_group_xop with CSDR_XOP_ATTN); otherwise as csdr_attn_decode. */
+CSDR_API int csdr_attn_decode_rope(const float* q, const float* k_new, const float* v_new,
+                                   uint16_t* kcache, uint16_t* vcache, const int* lens_dev, int B,
+                                   int T, int Hq, int Hkv, int hd, float theta, float scale,
+                                   float* out, void* workspace, size_t workspace_bytes,
+                                   void* hip_stream);
 /* Next token as select_best_from_logits (cortex_sdk.cpp:1005-1030): score = logit /
  * temperature (temperature <= 0: 1) minus penalty where repeated[i] != 0 (repeated may be
  * NULL); best finite score, lowest index on ties; -1 when none is finite. Writes the token to

@@ -99,3 +99,26 @@ def test_decoder_rejects_bad_use(gpu):
     w2 = synthetic_weights(DecoderSpec(1, 128, 2, 1, 64, 192, 100, 8), n_atoms=64, nnz=4)
     with pytest.raises(CsdrError):
         Decoder(type(w2)(bad, w2.layers, w2.lm_head, w2.final_norm))  # ffn shape mismatch
+
+
+def test_decoder_fused_equals_unfused(gpu):
+    import os
+
+    spec, opts, n_prompt, n_new = CASES[0]
+    w = synthetic_weights(spec, n_atoms=128, nnz=8, seed=11, sigma=0.1, **opts)
+    prompt = ((np.arange(n_prompt) * 7919) % spec.vocab).astype(np.int32)
+    runs = []
+    for fused in ("1", "0"):
+        os.environ["CSDR_DECODER_FUSED"] = fused
+        try:
+            dec = Decoder(w)
+        finally:
+            del os.environ["CSDR_DECODER_FUSED"]
+        try:
+            dec.prefill(prompt, 0.8, 1.5)
+            dec.decode(n_new - 1, 0.8, 1.5)
+            runs.append((dec.tokens(n_prompt, n_new), dec.logits()))
+        finally:
+            dec.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert rel_l2(runs[0][1], runs[1][1]) < 1e-5

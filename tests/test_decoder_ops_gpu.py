@@ -159,3 +159,89 @@ def test_decode_row_and_bias_accumulate(gpu):
     chk(lib().csdr_hsdb_matmul_group_ex(1, hs, xp, 0, 1, yp, None, 1, ws.data_ptr(), ws.numel(),
                                         sp(gpu)))
     assert rel_l2(y.cpu().numpy()[:, 0], 2 * wx + bias) < 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_matmul_xop_rmsnorm_and_silu(gpu, M):
+    from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
+
+    R, Cc = 300, 200  # 3 block columns + an 8-column edge strip (transformed too)
+    stream = synth.hsdb_layer(R, Cc, 64, 8, seed_dict=3, seed_codes=9)
+    seg = HsdbSegment(stream)
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(Cc, M)).astype(np.float32) * 3
+    x2 = rng.normal(size=(Cc, M)).astype(np.float32)
+    nw = rng.normal(size=Cc).astype(np.float32)
+    bias = rng.normal(size=R).astype(np.float32)
+    xd, x2d, nwd, bd = dev(gpu, x), dev(gpu, x2), dev(gpu, nw), dev(gpu, bias)
+    y = gpu.zeros((R, M), dtype=gpu.float32, device="cuda")
+    ws = group_workspace([seg], M)
+    hs = (C.c_void_p * 1)(seg._h.value)
+    xp = (C.c_void_p * 1)(xd.data_ptr())
+    x2p = (C.c_void_p * 1)(x2d.data_ptr())
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    bp = (C.c_void_p * 1)(bd.data_ptr())
+    chk(lib().csdr_hsdb_matmul_group_xop(1, hs, xp, None, M, yp, bp, 0, 1, nwd.data_ptr(), 1e-5,
+                                         0, 0, ws.data_ptr(), ws.numel(), sp(gpu)))
+    xn = oracle.rms_norm(np.ascontiguousarray(x.T), nw).T   # per column
+    ref = oracle.hsdb_matmul(stream, np.ascontiguousarray(xn)) + bias[:, None]
+    assert rel_l2(y.cpu().numpy(), ref) < 1e-5
+    chk(lib().csdr_hsdb_matmul_group_xop(1, hs, xp, x2p, M, yp, None, 1, 2, None, 0.0, 0, 0,
+                                         ws.data_ptr(), ws.numel(), sp(gpu)))
+    xs = oracle.silu_mul(x, x2)
+    ref2 = ref + oracle.hsdb_matmul(stream, xs)
+    assert rel_l2(y.cpu().numpy(), ref2) < 1e-5
+
+
+@pytest.mark.parametrize("Hq,Hkv,hd,L,T", [(14, 2, 64, 300, 640), (32, 32, 128, 1000, 4096),
+                                           (4, 4, 64, 1, 64)])
+def test_attn_rope_fused_matches_unfused(gpu, Hq, Hkv, hd, L, T):
+    from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
+
+    rng = np.random.default_rng(11)
+    q = rng.normal(size=(Hq, hd)).astype(np.float32)
+    k = rng.normal(size=(Hkv, hd)).astype(np.float32)
+    v = rng.normal(size=(Hkv, hd)).astype(np.float32)
+    kc = rng.normal(size=(T, Hkv, hd)).astype(np.float16)
+    vc = rng.normal(size=(T, Hkv, hd)).astype(np.float16)
+    pos = L - 1
+    # unfused: rope_kv then attention then the o projection
+    qd, kd, vd = dev(gpu, q), dev(gpu, k), dev(gpu, v)
+    kcd, vcd = dev(gpu, kc), dev(gpu, vc)
+    pd = gpu.tensor([pos], dtype=gpu.int32, device="cuda")
+    ld = gpu.tensor([L], dtype=gpu.int32, device="cuda")
+    chk(lib().csdr_rope_kv(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), 1, Hq, Hkv, hd,
+                           pd.data_ptr(), 1e6, kcd.data_ptr(), vcd.data_ptr(), T, sp(gpu)))
+    out = gpu.empty((Hq, hd), dtype=gpu.float32, device="cuda")
+    wsb = lib().csdr_attn_decode_workspace_bytes(1, Hq, hd, T)
+    ws = gpu.zeros(max(wsb, 4), dtype=gpu.uint8, device="cuda")
+    chk(lib().csdr_attn_decode(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), ld.data_ptr(), 0, 1,
+                               T, Hq, Hkv, hd, 0.0, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                               sp(gpu)))
+    # fused: rotation and append inside the attention, partials combined by the o projection
+    q2, k2, v2 = dev(gpu, q), dev(gpu, k), dev(gpu, v)
+    kc2, vc2 = dev(gpu, kc), dev(gpu, vc)
+    ws2 = gpu.zeros(max(wsb, 4), dtype=gpu.uint8, device="cuda")
+    out2 = gpu.empty((Hq, hd), dtype=gpu.float32, device="cuda")
+    chk(lib().csdr_attn_decode_rope(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), kc2.data_ptr(),
+                                    vc2.data_ptr(), ld.data_ptr(), 1, T, Hq, Hkv, hd, 1e6, 0.0,
+                                    out2.data_ptr(), ws2.data_ptr(), ws2.numel(), sp(gpu)))
+    assert rel_l2(out2.cpu().numpy(), out.cpu().numpy()) < 1e-6
+    assert np.array_equal(kc2.cpu().numpy()[pos], kcd.cpu().numpy()[pos])
+    assert np.array_equal(vc2.cpu().numpy()[pos], vcd.cpu().numpy()[pos])
+    H = Hq * hd
+    stream = synth.hsdb_layer(96, H, 64, 4, seed_dict=2, seed_codes=3)
+    seg = HsdbSegment(stream)
+    y = gpu.zeros((96, 1), dtype=gpu.float32, device="cuda")
+    wsm = group_workspace([seg], 1)
+    chk(lib().csdr_attn_decode_rope(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), kc2.data_ptr(),
+                                    vc2.data_ptr(), ld.data_ptr(), 1, T, Hq, Hkv, hd, 1e6, 0.0,
+                                    None, ws2.data_ptr(), ws2.numel(), sp(gpu)))
+    nsplit = lib().csdr_attn_decode_splits(1, Hq, Hkv, hd, T)
+    hs = (C.c_void_p * 1)(seg._h.value)
+    xp = (C.c_void_p * 1)(ws2.data_ptr())
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    chk(lib().csdr_hsdb_matmul_group_xop(1, hs, xp, None, 1, yp, None, 0, 3, None, 0.0, nsplit,
+                                         hd, wsm.data_ptr(), wsm.numel(), sp(gpu)))
+    ref = oracle.hsdb_matmul(stream, out.cpu().numpy().reshape(H, 1))
+    assert rel_l2(y.cpu().numpy(), ref) < 1e-5
