@@ -36,6 +36,13 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
 
+# HBM bytes per gather launch (cfg2, M = 1, both matrices) from two rocprofv3 --pmc runs of
+# this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
+# counter reads for a plain 256 MiB device copy in the same run (--calibrate-copy: FETCH_SIZE
+# reads 0.5x the bytes copied, WRITE_SIZE 1.0x): 22549.2 KiB / 0.5 + 1376.0 KiB / 1.0.
+# Summary and commands: profiles/hsdb_gather_cfg2_hbm_traffic.md. Update with the kernel.
+GATHER_TRAFFIC_BYTES = int((22549.2 / 0.5 + 1376.0 / 1.0) * 1024)
+
 
 def parse():
     ap = argparse.ArgumentParser()
@@ -47,6 +54,9 @@ def parse():
     ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2"])
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
     ap.add_argument("--decode-cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy 5 times (the reference dispatch "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -309,7 +319,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GATHER_TRAFFIC_BYTES if args.config == "cfg2" else None,
             "algorithmic_bytes_per_launch": g_bytes,
         },
         "cpu_baseline": None,
@@ -327,6 +337,13 @@ def main():
         }
     if not args.no_decode:
         out["decode"] = decode_leg(args)
+    if args.calibrate_copy:
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
     print(json.dumps(out), flush=True)
 
 
