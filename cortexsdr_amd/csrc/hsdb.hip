@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -44,7 +45,17 @@ using csdr::set_error;
 constexpr int kThreads = 256;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kMaxChunkBlocks = 8;
+// Launch-shape defaults, overridable for tuning sweeps through the environment
+// (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_CHUNK_BYTES).
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    const int x = std::atoi(v);
+    return x > 0 ? x : dflt;
+}
+
+constexpr uint32_t kMaxChunkBlocks = 16;
+constexpr uint32_t kChunkPBytes = 65536;  // P slice of one chunk (nbc * K fp32), at most
 
 
 // ------------------------------------------------------------------ matmul kernels
@@ -52,8 +63,6 @@ constexpr uint32_t kMaxChunkBlocks = 8;
 constexpr int kMaxGroup = 8;
 constexpr int kMaxSlotsArg = 32;
 constexpr int kStageBatch = 8;  // global loads in flight per thread while staging to LDS
-constexpr int kDepth = 3;       // code units in flight per gather workgroup (M == 1)
-constexpr int kGatherWGsPerCU = 8;
 constexpr int kMaxXopM = 16;  // columns an x op supports
 
 // One coded matrix of a grouped launch.
@@ -74,8 +83,10 @@ struct MatDesc {
     int g_base, g_count;      // gather workgroup ids, base a multiple of 8
     int splits;               // gather workgroups per chunk
     int rows_per_wg;          // rows of a chunk handled by one gather workgroup
+    int rsplit[4], rrpw[4];   // M == 1 gather: ranges and rows per range of the remainder chunks
     int Rt;                   // M > 1 gather: rows per workgroup
     float sgam[kMaxSlotsArg]; // gamma of each slot (slots <= kMaxSlotsArg; scalar loads)
+    int gunif;                // every slot has gamma sgam[0]
 };
 
 struct Params {
@@ -87,6 +98,7 @@ struct Params {
     const float* nw;  // RMSNorm weights (C)
     float eps;
     int nsplit, hd;   // attention combine: splits and head size of the partials in x
+    int gpre;         // M == 1 gather: code loads per wave issued before the P slice's
 };
 
 template <int CTRL>
@@ -114,17 +126,17 @@ __device__ __forceinline__ float xload(const void* x, int f16, size_t i) {
 
 // xs[i] = float(src[i]) for i < n by the whole workgroup, kStageBatch independent loads
 // per thread in flight at a time (branch-free: out-of-range lanes reload the last element).
-template <typename T>
+template <typename T, int NT = kThreads>
 __device__ __forceinline__ void stage_to_lds(const T* __restrict__ src, int n, float* xs) {
     const int tid = threadIdx.x;
-    for (int i0 = 0; i0 < n; i0 += kThreads * kStageBatch) {
+    for (int i0 = 0; i0 < n; i0 += NT * kStageBatch) {
         float v[kStageBatch];
 #pragma unroll
         for (int j = 0; j < kStageBatch; ++j)
-            v[j] = csdr::to_f32(src[min(i0 + j * kThreads + tid, n - 1)]);
+            v[j] = csdr::to_f32(src[min(i0 + j * NT + tid, n - 1)]);
 #pragma unroll
         for (int j = 0; j < kStageBatch; ++j) {
-            const int i = i0 + j * kThreads + tid;
+            const int i = i0 + j * NT + tid;
             if (i < n) xs[i] = v[j];
         }
     }
@@ -153,7 +165,8 @@ __device__ __forceinline__ void copy_to_lds4(const float* __restrict__ src, int 
 // dispatch boundary.
 // ---- input transforms fused into the dx staging (x op)
 
-// Workgroup sum of v (kThreads threads), result in every thread.
+// Workgroup sum of v (NT threads), result in every thread.
+template <int NT = kThreads>
 __device__ __forceinline__ float wg_sum(float v, float* red) {
     v = csdr::wave_sum(v);
     __syncthreads();
@@ -161,7 +174,7 @@ __device__ __forceinline__ float wg_sum(float v, float* red) {
     __syncthreads();
     float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < kThreads / 64; ++i) t += red[i];
+    for (int i = 0; i < NT / 64; ++i) t += red[i];
     return t;
 }
 
@@ -192,6 +205,91 @@ __device__ __forceinline__ float xop_apply(const Params& p, const MatDesc& d, fl
         return (v * (1.0f / (1.0f + expf(-v)))) * u;
     }
     return v;
+}
+
+// Stages x features [64 b0, 64 (b0 + nb)) x M columns into xs (fp32, [feature][column])
+// with the call's x op applied (RMSNorm, SiLU(x) * x2, attention combine); with do_xe also
+// writes the transformed edge-strip inputs to xe_out (d.xe, or an LDS vector). A workgroup
+// of NT threads; ends with a barrier.
+template <int NT = kThreads>
+__device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb, float* xs,
+                              bool do_xe, float* xe_out = nullptr) {
+    const int tid = threadIdx.x;
+    const int M = p.M;
+    float* const xe = xe_out ? xe_out : d.xe;
+    const size_t xbase = (size_t)b0 * 64 * M;
+    const int nx = nb * 64 * M;
+    __shared__ float inv[kMaxXopM];
+    __shared__ float red[NT / 64];
+    if (p.xop == CSDR_XOP_RMSNORM) {
+        // 1 / rms of every column over all C features (each workgroup recomputes it: x is
+        // a few KiB, L2-resident)
+        const float* xf = static_cast<const float*>(d.x);
+        const int C = d.C_full + d.Ce;
+        for (int m = 0; m < M; ++m) {
+            float ss = 0.f;
+            for (int k = tid; k < C; k += NT) {
+                const float v = xf[(size_t)k * M + m];
+                ss = fmaf(v, v, ss);
+            }
+            ss = wg_sum<NT>(ss, red);
+            if (tid == 0) inv[m] = 1.0f / sqrtf(ss / (float)C + p.eps);
+        }
+    }
+    if (p.xop == CSDR_XOP_ATTN) {
+        // per head of this range: split weights exp(m_s - max) and 1 / sum(w_s l_s) in
+        // LDS once, then every feature is one weighted sum over the splits
+        const float* part = static_cast<const float*>(d.x);
+        const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
+        const int h0 = (b0 * 64) / hd, h1 = (b0 * 64 + nx - 1) / hd + 1;
+        float* wts = xs + nx;  // (h1 - h0) x (ns + 1)
+        for (int h = h0 + tid; h < h1; h += NT) {
+            const float* pp = part + (size_t)h * ns * ps;
+            float Mx = -INFINITY;
+            for (int s2 = 0; s2 < ns; ++s2) Mx = fmaxf(Mx, pp[(size_t)s2 * ps]);
+            float den = 0.f;
+            float* wh = wts + (h - h0) * (ns + 1);
+            for (int s2 = 0; s2 < ns; ++s2) {
+                const float ms = pp[(size_t)s2 * ps];
+                const float w = ms == -INFINITY ? 0.f : expf(ms - Mx);
+                wh[s2] = w;
+                den = fmaf(w, pp[(size_t)s2 * ps + 1], den);
+            }
+            wh[ns] = den > 0.f ? 1.0f / den : 0.f;
+        }
+        __syncthreads();
+        for (int i = tid; i < nx; i += NT) {
+            const int k = b0 * 64 + i, h = k / hd, dd = k - h * hd;
+            const float* wh = wts + (h - h0) * (ns + 1);
+            const float* po = part + (size_t)h * ns * ps + 2 + dd;
+            float num = 0.f;
+            for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * ps], num);
+            xs[i] = num * wh[ns];
+        }
+    } else if (p.x_f16) {
+        stage_to_lds<_Float16, NT>(static_cast<const _Float16*>(d.x) + xbase, nx, xs);
+    } else {
+        stage_to_lds<float, NT>(static_cast<const float*>(d.x) + xbase, nx, xs);
+    }
+    if (p.xop == CSDR_XOP_RMSNORM || p.xop == CSDR_XOP_SILU_MUL) {
+        __syncthreads();
+        for (int i = tid; i < nx; i += NT) {
+            const int k = b0 * 64 + i / M, m = i % M;
+            xs[i] = xop_apply(p, d, xs[i], k, m, inv);
+        }
+        if (do_xe && xe) {
+            const float* xf = static_cast<const float*>(d.x);
+            for (int t = tid; t < d.Ce * M; t += NT) {
+                const int cc = t / M, m = t % M;
+                const int k = d.C_full + cc;
+                xe[t] = xop_apply(p, d, xf[(size_t)k * M + m], k, m, inv);
+            }
+        }
+    } else if (p.xop == CSDR_XOP_ATTN && do_xe && xe) {
+        const float* part = static_cast<const float*>(d.x);
+        for (int t = tid; t < d.Ce; t += NT) xe[t] = attn_feature(p, part, d.C_full + t);
+    }
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
@@ -225,84 +323,12 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
         const int b0 = bg * d.PB;
         const int nb = min(d.PB, d.NB - b0);
         const bool live = a < d.K;
-        float* xs = smem;  // [bb][t][m], nb * 64 * M floats (x rows are contiguous)
-        const size_t xbase = (size_t)b0 * 64 * M;
-        const int nx = nb * 64 * M;
-        __shared__ float inv[kMaxXopM];
-        __shared__ float red[kThreads / 64];
-        if (p.xop == CSDR_XOP_RMSNORM) {
-            // 1 / rms of every column over all C features (each workgroup recomputes it: x is
-            // a few KiB, L2-resident)
-            const float* xf = static_cast<const float*>(d.x);
-            const int C = d.C_full + d.Ce;
-            for (int m = 0; m < M; ++m) {
-                float ss = 0.f;
-                for (int k = tid; k < C; k += kThreads) {
-                    const float v = xf[(size_t)k * M + m];
-                    ss = fmaf(v, v, ss);
-                }
-                ss = wg_sum(ss, red);
-                if (tid == 0) inv[m] = 1.0f / sqrtf(ss / (float)C + p.eps);
-            }
-        }
-        if (p.xop == CSDR_XOP_ATTN) {
-            // per head of this range: split weights exp(m_s - max) and 1 / sum(w_s l_s) in
-            // LDS once, then every feature is one weighted sum over the splits
-            const float* part = static_cast<const float*>(d.x);
-            const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
-            const int h0 = (b0 * 64) / hd, h1 = (b0 * 64 + nx - 1) / hd + 1;
-            float* wts = xs + nx;  // (h1 - h0) x (ns + 1)
-            for (int h = h0 + tid; h < h1; h += kThreads) {
-                const float* pp = part + (size_t)h * ns * ps;
-                float Mx = -INFINITY;
-                for (int s2 = 0; s2 < ns; ++s2) Mx = fmaxf(Mx, pp[(size_t)s2 * ps]);
-                float den = 0.f;
-                float* wh = wts + (h - h0) * (ns + 1);
-                for (int s2 = 0; s2 < ns; ++s2) {
-                    const float ms = pp[(size_t)s2 * ps];
-                    const float w = ms == -INFINITY ? 0.f : expf(ms - Mx);
-                    wh[s2] = w;
-                    den = fmaf(w, pp[(size_t)s2 * ps + 1], den);
-                }
-                wh[ns] = den > 0.f ? 1.0f / den : 0.f;
-            }
-            __syncthreads();
-            for (int i = tid; i < nx; i += kThreads) {
-                const int k = b0 * 64 + i, h = k / hd, dd = k - h * hd;
-                const float* wh = wts + (h - h0) * (ns + 1);
-                const float* po = part + (size_t)h * ns * ps + 2 + dd;
-                float num = 0.f;
-                for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * ps], num);
-                xs[i] = num * wh[ns];
-            }
-        } else if (p.x_f16) {
-            stage_to_lds(static_cast<const _Float16*>(d.x) + xbase, nx, xs);
-        } else {
-            stage_to_lds(static_cast<const float*>(d.x) + xbase, nx, xs);
-        }
-        if (p.xop == CSDR_XOP_RMSNORM || p.xop == CSDR_XOP_SILU_MUL) {
-            __syncthreads();
-            for (int i = tid; i < nx; i += kThreads) {
-                const int k = b0 * 64 + i / M, m = i % M;
-                xs[i] = xop_apply(p, d, xs[i], k, m, inv);
-            }
-            if (u == 0 && d.xe) {
-                const float* xf = static_cast<const float*>(d.x);
-                for (int t = tid; t < d.Ce * M; t += kThreads) {
-                    const int cc = t / M, m = t % M;
-                    const int k = d.C_full + cc;
-                    d.xe[t] = xop_apply(p, d, xf[(size_t)k * M + m], k, m, inv);
-                }
-            }
-        } else if (p.xop == CSDR_XOP_ATTN && u == 0 && d.xe) {
-            const float* part = static_cast<const float*>(d.x);
-            for (int t = tid; t < d.Ce; t += kThreads) d.xe[t] = attn_feature(p, part, d.C_full + t);
-        }
         float4 dv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (live) dv = reinterpret_cast<const float4*>(d.dict + (size_t)a * 64)[l16];
+        float* xs = smem;  // [bb][t][m], nb * 64 * M floats (x rows are contiguous)
+        stage_x_chunk(p, d, b0, nb, xs, u == 0);
         float* const Pout = d.P + (size_t)b0 * d.K * M + (size_t)a * M;  // + bb*K*M + m
         const size_t pstride = (size_t)d.K * M;
-        __syncthreads();
         int bb = 0;
         if (M == 1) {
             // four independent (block) dot products per step so the DPP chains interleave
@@ -403,112 +429,190 @@ __device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, in
 
 
 
-// ---- kernel 2, M == 1: persistent gather. Workgroup = (chunk, row range). It stages the
-// chunk's P slice (nbc * K floats) in LDS once, then walks its rows in units of
-// 256 * PPT "pieces" (4 code words = 16 bytes each; every load instruction of a wave reads
-// 1 KiB contiguous) with kDepth units of loads in flight, gathers P from LDS, sums each
-// row's pieces and adds the row total into Y (device-scope float atomics: other chunks of
-// the row run elsewhere).
-template <int SLOTS, int PPT>
-__device__ __forceinline__ void load_unit(u32x4 (&buf)[PPT], const uint32_t* base, int npieces) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(base);
-#pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-        const int q = threadIdx.x + j * kThreads;
-        buf[j] = __builtin_nontemporal_load(src + min(q, npieces - 1));
-    }
-}
+// ---- kernel 2, M == 1: the gather, 1024-thread workgroups
+// Workgroup = (matrix, chunk c, row range s), about kGWgsPerCu per CU in all
+// (CSDR_GATHER_WGS_PER_CU to change), each streaming about the same code bytes (plan_gather_splits), numbered
+// chunk-fastest so that consecutive ids (which dispatch round-robin over the 8 XCDs) spread
+// every matrix over all XCDs. Each of its 16 waves takes a contiguous sixteenth of the
+// workgroup's code run and first issues DEPTH 1 KiB loads of it (kept in registers); the
+// workgroup then stages the chunk's P slice (nbc * K floats, written by the dx launch) in LDS
+// and the waves stream their parts: per lane a fixed tile and slot quarter (each row of a
+// chunk spans a power of two of 16-byte pieces, 64 % pieces == 0), row totals as DPP /
+// shuffle butterflies over the row's lanes and one device-scope float atomic per
+// (row, chunk) into Y (initialised by the dx launch).
+constexpr int kGThreads = 1024;
+constexpr int kGWaves = kGThreads / 64;
+constexpr int kGDepth = 4;  // code loads in flight per wave
+constexpr int kGPre = 4;    // of which issued before the P slice's loads
+constexpr int kGWgsPerCu = 2;  // gather workgroups per CU (measured: 2 ahead of 1 by ~6%)
+constexpr size_t kGMaxP = 4 * 4 * kGThreads;  // P slice floats: 4 float4 per thread
+constexpr size_t kCodePad = 1024;             // bytes after the codes (one wave load)
 
-template <int SLOTS, int PPT>
-__device__ __forceinline__ void process_unit(const Params& p, const MatDesc& d,
-                                             const u32x4 (&buf)[PPT], const float* Ps,
-                                             float* part, int nbc, int row0, int nrows,
-                                             bool last_chunk) {
-    constexpr int PPP = SLOTS / 4;  // pieces per (row, block) pair
-    const int ppr = nbc * PPP;       // pieces per row
-    const int npieces = nrows * ppr;
-    const int tid = threadIdx.x;
+// Optional per-workgroup timeline of the gather launch (built only with
+// -DCSDR_GATHER_TIMELINE, for measurement): stamps and the hardware ids per workgroup id.
+#ifdef CSDR_GATHER_TIMELINE
+constexpr int kTlWgs = 4096;
+constexpr int kTlSlots = 8;  // stamps 0..6, then (XCC id << 32 | HW_ID)
+__device__ unsigned long long g_timeline[kTlWgs * kTlSlots];
+#define CSDR_TL(slot)                                                                       \
+    do {                                                                                    \
+        if (threadIdx.x == 0 && blockIdx.x < (unsigned)kTlWgs) {                            \
+            g_timeline[blockIdx.x * kTlSlots + (slot)] = wall_clock64();                   \
+            if ((slot) == 0)                                                                \
+                g_timeline[blockIdx.x * kTlSlots + 7] =                                    \
+                    ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | \
+                    (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);                   \
+        }                                                                                   \
+    } while (0)
+#else
+#define CSDR_TL(slot) \
+    do {              \
+    } while (0)
+#endif
+
+template <int SLOTS, int DEPTH>
+__global__ __launch_bounds__(kGThreads) void gatherw_kernel(Params p) {
+    extern __shared__ float smem[];
+    const int wg = (int)blockIdx.x;
+    int g = 0;
+    while (g + 1 < p.G && wg >= p.m[g + 1].g_base) ++g;
+    const MatDesc& d = p.m[g];
+    // workgroup -> (chunk, row range): the full chunks' ranges first, chunk-fastest (so that
+    // consecutive ids, which dispatch round-robin over the XCDs, spread each chunk), then each
+    // remainder chunk's ranges
+    const int u = wg - d.g_base;
+    const int nfull = d.NB / d.NBc;
+    int c, sidx, rpw;
+    if (u < nfull * d.splits) {
+        c = u % nfull;
+        sidx = u / nfull;
+        rpw = d.rows_per_wg;
+    } else {
+        int v = u - nfull * d.splits, j = 0;
+        while (j < 4 && v >= d.rsplit[j]) v -= d.rsplit[j++];
+        if (j == 4) return;
+        c = nfull + j;
+        sidx = v;
+        rpw = d.rrpw[j];
+    }
+    uint32_t b0u, nbcu;
+    csdr::chunk_span((uint32_t)c, (uint32_t)d.NB, (uint32_t)d.NBc, b0u, nbcu);
+    const int b0 = (int)b0u, nbc = (int)nbcu;
+    const int rbeg = sidx * rpw;
+    const int rend = min(d.R, rbeg + rpw);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    CSDR_TL(0);
+
+    // Every wave first issues its first DEPTH code loads, then the workgroup stages the chunk's
+    // P slice (nbc * K <= kGMaxP floats, written by the dx launch) in LDS: measured, P loads
+    // issued first (all CUs at once on the same ~1 MB of P) land later than behind the codes.
+    constexpr int PPB = SLOTS / 4;  // 16-byte pieces per tile
+    const int ppr = nbc * PPB;      // pieces per row: a power of two <= 64
+    const int npieces = (rend - rbeg) * ppr;
+    const int nload = (npieces + 63) >> 6;
+    // wave w streams its own contiguous part of the run (wave loads [w per, (w + 1) per)), so
+    // the workgroup's concurrent row atomics fall on 16 different lines of Y
+    const int per = (nload + kGWaves - 1) / kGWaves;
+    const int nk = max(0, min(per, nload - wave * per));
+    // the run, then this lane: loads past the run's end stay inside the codes allocation
+    // (kCodePad) and their lanes are discarded
+    const u32x4* lrun = reinterpret_cast<const u32x4*>(d.codes + (size_t)b0 * d.R * SLOTS +
+                                                       (size_t)rbeg * nbc * SLOTS) +
+                        wave * per * 64 + lane;
+    constexpr int kStep = 64;  // pieces between a wave's consecutive loads
+    u32x4 buf[DEPTH];
+    const int pre = p.gpre;  // code loads issued before the P slice's loads
 #pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-        const int q = tid + j * kThreads;
-        if (q < npieces) {
-            const int pr = q % ppr;
-            const int bb = pr / PPP;
-            const int h = pr - bb * PPP;  // which 4 slots of the pair
-            const float* Pb = Ps + (size_t)bb * d.K;
-            const uint32_t w4[4] = {buf[j].x, buf[j].y, buf[j].z, buf[j].w};
+    for (int k = 0; k < DEPTH; ++k)
+        if (k < nk && k < pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
+
+    float* Ps = smem;               // nbc * K floats
+    float* xe = Ps + d.NBc * d.K;   // Ce (< 64) floats
+    const bool edge = (c == d.nchunks - 1) && d.Ce > 0;
+    {
+        const float* Pg = d.P + (size_t)b0 * d.K;
+        const int np = nbc * d.K;
+        if ((d.K & 3) == 0) {
+            const float4* s4 = reinterpret_cast<const float4*>(Pg);
+            float4* d4 = reinterpret_cast<float4*>(Ps);
+            const int np4 = np >> 2;
+            float4 pv[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) pv[jj] = s4[min(jj * kGThreads + tid, np4 - 1)];
+#pragma unroll
+            for (int k = 0; k < DEPTH; ++k)
+                if (k < nk && k >= pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                if (jj * kGThreads + tid < np4) d4[jj * kGThreads + tid] = pv[jj];
+        } else {
+#pragma unroll
+            for (int k = 0; k < DEPTH; ++k)
+                if (k < nk && k >= pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
+            stage_to_lds<float, kGThreads>(Pg, np, Ps);
+        }
+        if (edge && tid < d.Ce)
+            xe[tid] = d.xe ? d.xe[tid] : xload(d.x, p.x_f16, (size_t)d.C_full + tid);
+    }
+    __syncthreads();
+    CSDR_TL(1);
+
+    // per lane a fixed tile and slot quarter; word = (signed fp16 coefficient << 16) | index,
+    // the low half is the index itself (bit 15 is 0)
+    const int pl = lane & (ppr - 1);
+    const int lg_ppr = __builtin_ctz((unsigned)ppr);
+    const int bb = pl / PPB, h = pl - bb * PPB;
+    const float* Pb = Ps + bb * d.K;
+    float gm[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        gm[e] = d.sgam[e];
+#pragma unroll
+        for (int hh = 1; hh < PPB; ++hh)
+            if (h == hh) gm[e] = d.sgam[hh * 4 + e];
+    }
+    const bool gu = d.gunif != 0;
+    const float g0 = d.sgam[0];
+    const bool head = (pl == 0);
+    const int q0 = wave * per * 64 + lane;  // this lane's piece in the wave's first load
+    for (int k0 = 0; k0 < nk; k0 += DEPTH) {
+#pragma unroll
+        for (int jj = 0; jj < DEPTH; ++jj) {
+            const int k = k0 + jj;
+            if (k >= nk) break;
+            const int qp = q0 + k * kStep;
+            const u32x4 w = buf[jj];
+            if (k + DEPTH < nk) buf[jj] = __builtin_nontemporal_load(lrun + (k + DEPTH) * kStep);
+            const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
             float acc = 0.0f;
+            if (gu) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float gm = d.sgam[e];
+                for (int e = 0; e < 4; ++e)
+                    acc = fmaf(csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
+            } else {
 #pragma unroll
-                for (int hh = 1; hh < PPP; ++hh)
-                    if (h == hh) gm = d.sgam[hh * 4 + e];
-                const float cf = gm * csdr::h2f(w4[e] >> 16);
-                acc = fmaf(cf, Pb[w4[e] & 0x7FFFu], acc);
+                for (int e = 0; e < 4; ++e)
+                    acc = fmaf(gm[e] * csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
             }
-            part[q] = acc;
+            if (qp >= npieces) acc = 0.0f;
+            if (ppr > 1) acc += dpp_move<0xB1>(acc);   // quad_perm [1,0,3,2]
+            if (ppr > 2) acc += dpp_move<0x4E>(acc);   // quad_perm [2,3,0,1]
+            if (ppr > 4) acc += dpp_move<0x141>(acc);  // row_half_mirror
+            if (ppr > 8) acc += dpp_move<0x140>(acc);  // row_mirror
+            if (ppr > 16) acc += __shfl_xor(acc, 16, 64);
+            if (ppr > 32) acc += __shfl_xor(acc, 32, 64);
+            if (head && qp < npieces) {
+                const int r = rbeg + (qp >> lg_ppr);
+                if (gu) acc *= g0;
+                if (edge) {
+                    const float* er = d.edge + (size_t)r * d.Ce;
+                    for (int cc = 0; cc < d.Ce; ++cc) acc = fmaf(er[cc], xe[cc], acc);
+                }
+                __hip_atomic_fetch_add(d.y + r, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
-    __syncthreads();
-    for (int rr = tid; rr < nrows; rr += kThreads) {
-        float sum = 0.0f;
-        for (int k = 0; k < ppr; ++k) sum += part[rr * ppr + k];
-        const int r = row0 + rr;
-        if (last_chunk && d.Ce > 0) sum += edge_term(p, d, r, 0);
-        __hip_atomic_fetch_add(d.y + r, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-}
-
-template <int SLOTS, int PPT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
-void gather1_kernel(Params p) {
-    extern __shared__ float smem[];
-    int g, c, sidx;
-    if (!gather_slot(p, g, c, sidx)) return;
-    const MatDesc& d = p.m[g];
-    const int b0 = c * d.NBc;
-    const int nbc = min(d.NBc, d.NB - b0);
-    const int rbeg = sidx * d.rows_per_wg;
-    const int rend = min(d.R, rbeg + d.rows_per_wg);
-    if (rbeg >= rend) return;
-    constexpr int PPP = SLOTS / 4;
-    const int ppr = nbc * PPP;
-    const int rows_unit = max(1, (kThreads * PPT) / ppr);
-    const int nunits = (rend - rbeg + rows_unit - 1) / rows_unit;
-    // codes of rows [rbeg, rend) of chunk c are one contiguous run
-    const uint32_t* run = d.codes + (size_t)c * d.NBc * d.R * SLOTS + (size_t)rbeg * nbc * SLOTS;
-    auto unit_base = [&](int k) { return run + (size_t)k * rows_unit * ppr * 4; };
-    auto unit_rows = [&](int k) { return min(rows_unit, rend - rbeg - k * rows_unit); };
-    const bool last_chunk = (c == d.nchunks - 1);
-
-    u32x4 b0v[PPT], b1v[PPT], b2v[PPT];
-    load_unit<SLOTS, PPT>(b0v, unit_base(0), unit_rows(0) * ppr);
-    if (nunits > 1) load_unit<SLOTS, PPT>(b1v, unit_base(1), unit_rows(1) * ppr);
-
-    float* Ps = smem;                         // nbc * K floats
-    float* part = smem + (size_t)d.NBc * d.K; // kThreads * PPT floats
-    const float* Pg = d.P + (size_t)b0 * d.K;
-    if ((d.K & 3) == 0)
-        copy_to_lds4(Pg, nbc * d.K, Ps);
-    else
-        stage_to_lds(Pg, nbc * d.K, Ps);
-    __syncthreads();
-
-    for (int k = 0; k < nunits; k += kDepth) {
-        if (k + 2 < nunits) load_unit<SLOTS, PPT>(b2v, unit_base(k + 2), unit_rows(k + 2) * ppr);
-        process_unit<SLOTS, PPT>(p, d, b0v, Ps, part, nbc, rbeg + k * rows_unit, unit_rows(k),
-                                 last_chunk);
-        if (k + 1 >= nunits) break;
-        if (k + 3 < nunits) load_unit<SLOTS, PPT>(b0v, unit_base(k + 3), unit_rows(k + 3) * ppr);
-        process_unit<SLOTS, PPT>(p, d, b1v, Ps, part, nbc, rbeg + (k + 1) * rows_unit,
-                                 unit_rows(k + 1), last_chunk);
-        if (k + 2 >= nunits) break;
-        if (k + 4 < nunits) load_unit<SLOTS, PPT>(b1v, unit_base(k + 4), unit_rows(k + 4) * ppr);
-        process_unit<SLOTS, PPT>(p, d, b2v, Ps, part, nbc, rbeg + (k + 2) * rows_unit,
-                                 unit_rows(k + 2), last_chunk);
-    }
+    CSDR_TL(2);
 }
 
 // ---- kernel 2, any M / any slot count: workgroup = (chunk, row tile of Rt rows); the
@@ -521,14 +625,15 @@ __global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
     const MatDesc& d = p.m[g];
     const int tid = threadIdx.x;
     const int M = p.M;
-    const int b0 = c * d.NBc;
-    const int nbc = min(d.NBc, d.NB - b0);
+    uint32_t b0u, nbcu;
+    csdr::chunk_span((uint32_t)c, (uint32_t)d.NB, (uint32_t)d.NBc, b0u, nbcu);
+    const int b0 = (int)b0u, nbc = (int)nbcu;
     const int r0 = sidx * d.Rt;
     const int nr = min(d.Rt, d.R - r0);
     if (nr <= 0) return;
     const int npairs = nr * nbc;
     const uint32_t* cb =
-        d.codes + (size_t)c * d.NBc * d.R * d.slots + (size_t)r0 * nbc * d.slots;
+        d.codes + (size_t)b0 * d.R * d.slots + (size_t)r0 * nbc * d.slots;
     float* Ps = smem;                              // nbc * K * MV
     float* part = smem + (size_t)d.NBc * d.K * MV; // Rt * NBc * MV
     const bool last_chunk = (c == d.nchunks - 1);
@@ -579,9 +684,7 @@ __global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
 __device__ __forceinline__ size_t code_offset(const csdr_hsdb& s, uint32_t t) {
     if (s.tile_rows != 1) return (size_t)t * s.slots;
     const uint32_t r = t / s.NB, b = t - r * s.NB;
-    const uint32_t c = b / s.NBc, bb = b - c * s.NBc;
-    const uint32_t nbc = min(s.NBc, s.NB - c * s.NBc);
-    return ((size_t)c * s.NBc * s.R + (size_t)r * nbc + bb) * s.slots;
+    return csdr::tile_word_offset(r, b, s.R, s.NB, s.NBc, s.slots);
 }
 
 // Dense tiles: element e of tile t = sum over slots (stage-major) of coef * atom[e], one
@@ -736,17 +839,20 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     if (s->slots == 0 && s->n_tiles > 0)
         return set_error(CSDR_E_FORMAT, "hsdb_load: zero coded slots per tile");
 
-    // chunking of block columns (1-row tiles): P slice of a chunk <= 16 KiB per column
+    // chunking of block columns (1-row tiles): the P slice of a chunk (nbc * K fp32, staged
+    // in LDS by the M == 1 products) at most kChunkPBytes (CSDR_CHUNK_BYTES overrides)
     if (s->tile_rows == 1) {
+        const size_t cap = (size_t)env_int("CSDR_CHUNK_BYTES", (int)kChunkPBytes);
         uint32_t nbc = kMaxChunkBlocks;
-        while (nbc > 1 && (size_t)nbc * s->K * 4 > 16384) nbc >>= 1;
+        while (nbc > 1 && (size_t)nbc * s->K * 4 > cap) nbc >>= 1;
         while (nbc > 1 && nbc > s->NB) nbc >>= 1;
         s->NBc = nbc;
-        s->nchunks = s->NB ? (s->NB + nbc - 1) / nbc : 0;
+        s->nchunks = s->NB ? csdr::n_chunks(s->NB, nbc) : 0;
     }
 
     // build the device words
     std::vector<uint32_t> words(n_codes);
+    size_t tile_dst = 0;
     for (size_t i = 0; i < n_codes; ++i) {
         const uint16_t pk = rd16(buf + off_packed + 2 * i);
         const uint32_t idx = pk & 0x7FFFu;
@@ -758,10 +864,11 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
         size_t dst = i;
         if (s->tile_rows == 1) {
             const size_t t = i / s->slots, j = i - t * s->slots;
-            const uint32_t r = (uint32_t)(t / s->NB), b = (uint32_t)(t - (size_t)r * s->NB);
-            const uint32_t c = b / s->NBc, bb = b - c * s->NBc;
-            const uint32_t nbc = std::min(s->NBc, s->NB - c * s->NBc);
-            dst = ((size_t)c * s->NBc * s->R + (size_t)r * nbc + bb) * s->slots + j;
+            if (j == 0) {
+                const uint32_t r = (uint32_t)(t / s->NB), b = (uint32_t)(t - (size_t)r * s->NB);
+                tile_dst = csdr::tile_word_offset(r, b, s->R, s->NB, s->NBc, s->slots);
+            }
+            dst = tile_dst + j;
         }
         words[dst] = (h << 16) | idx;
     }
@@ -775,7 +882,10 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     const size_t b_gamma = slot_gamma.size() * 4;
     const size_t b_edge = edge_bytes;
     CSDR_HIP_CHECK(hipMalloc(&s->d_dict, std::max<size_t>(b_dict, 4)));
-    CSDR_HIP_CHECK(hipMalloc(&s->d_codes, std::max<size_t>(b_codes, 4)));
+    // + kCodePad zero bytes: a gather wave load may read up to 1 KiB past the end of the last
+    // row range's run (those lanes' results are discarded)
+    CSDR_HIP_CHECK(hipMalloc(&s->d_codes, b_codes + kCodePad));
+    CSDR_HIP_CHECK(hipMemsetAsync(reinterpret_cast<char*>(s->d_codes) + b_codes, 0, kCodePad, st));
     CSDR_HIP_CHECK(hipMalloc(&s->d_slot_gamma, b_gamma));
     CSDR_HIP_CHECK(hipMalloc(&s->d_edge, std::max<size_t>(b_edge, 4)));
     s->device_bytes = b_dict + b_codes + b_gamma + b_edge;
@@ -817,16 +927,7 @@ void release(csdr_hsdb* s) {
     delete s;
 }
 
-constexpr size_t kWsHeader = 256;  // reserved
 
-// Launch-shape defaults, overridable for tuning sweeps through the environment
-// (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_GATHER_UNITS_PER_WG).
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    if (!v || !*v) return dflt;
-    const int x = std::atoi(v);
-    return x > 0 ? x : dflt;
-}
 
 // Block columns per dx workgroup (block length 64): about `work` (block, column) dot
 // products per 16-lane group.
@@ -842,7 +943,7 @@ size_t p_bytes(const csdr_hsdb* s, int M) {
 
 // Workspace of the P path (dx + gather launches).
 size_t p_path_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
-    size_t t = kWsHeader;
+    size_t t = csdr::kWsHead;
     for (int i = 0; i < n; ++i) t += p_bytes(segs[i], M);
     return t;
 }
@@ -855,18 +956,103 @@ size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
     return p_path_ws_bytes(n, segs, M);
 }
 
-template <int PPT>
-void launch_gather1(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
+template <int DEPTH>
+void launch_gatherw_d(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
     switch (slots) {
         case 4:
-            gather1_kernel<4, PPT><<<grid, kThreads, lds, st>>>(p);
+            gatherw_kernel<4, DEPTH><<<grid, kGThreads, lds, st>>>(p);
             break;
         case 8:
-            gather1_kernel<8, PPT><<<grid, kThreads, lds, st>>>(p);
+            gatherw_kernel<8, DEPTH><<<grid, kGThreads, lds, st>>>(p);
             break;
         default:
-            gather1_kernel<16, PPT><<<grid, kThreads, lds, st>>>(p);
+            gatherw_kernel<16, DEPTH><<<grid, kGThreads, lds, st>>>(p);
             break;
+    }
+}
+
+void launch_gatherw(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
+    if (env_int("CSDR_GATHER_DEPTH", kGDepth) >= 8)
+        launch_gatherw_d<8>(p, slots, grid, lds, st);
+    else
+        launch_gatherw_d<kGDepth>(p, slots, grid, lds, st);
+}
+
+// Row ranges for the M == 1 gather, balanced by bytes: a workgroup of a chunk of nbc block
+// columns gets about U / nbc rows, U = all block-rows / target, so every workgroup streams
+// about the same code bytes whatever its chunk's width. Per matrix, the full chunks share one
+// split count (splits, rows_per_wg) and each remainder chunk (at most 4, widths NBc/2, ...,
+// largest first) has its own (rsplit[j], rrpw[j]). Starting from floor(rows * width / U)
+// ranges per chunk, ranges are added one class at a time (all full chunks of a matrix, or one
+// remainder chunk) to the class with the most block-rows per workgroup while the total stays
+// within the target.
+void plan_gather_splits(Params& p, int n, long long target) {
+    struct Cls {
+        int g, j;       // matrix, remainder index (-1: the full chunks)
+        int width, count, R;
+        int splits;
+    };
+    Cls cls[kMaxGroup * 5];
+    int ncls = 0;
+    long long total_br = 0;  // block-rows of all matrices
+    for (int i = 0; i < n; ++i) total_br += (long long)p.m[i].R * p.m[i].NB;
+    const double U = std::max(1.0, (double)total_br / (double)std::max(1LL, target));
+    long long used = 0;
+    for (int i = 0; i < n; ++i) {
+        const MatDesc& d = p.m[i];
+        const int nfull = d.NB / d.NBc;
+        auto add = [&](int j, int width, int count) {
+            Cls c{i, j, width, count, d.R, 1};
+            c.splits = (int)std::max(1.0, std::floor((double)d.R * width / U));
+            c.splits = std::min(c.splits, d.R);
+            used += (long long)c.splits * count;
+            cls[ncls++] = c;
+        };
+        if (nfull) add(-1, d.NBc, nfull);
+        int j = 0;
+        for (int bit = d.NBc >> 1; bit; bit >>= 1)
+            if ((d.NB % d.NBc) & bit) add(j++, bit, 1);
+    }
+    for (;;) {
+        int best = -1;
+        double best_b = 0.0;
+        for (int k = 0; k < ncls; ++k) {
+            const Cls& c = cls[k];
+            if (c.splits >= c.R || used + c.count > target) continue;
+            const double b = (double)c.R * c.width / c.splits;
+            if (b > best_b) {
+                best_b = b;
+                best = k;
+            }
+        }
+        if (best < 0) break;
+        ++cls[best].splits;
+        used += cls[best].count;
+    }
+    int base = 0;
+    for (int i = 0; i < n; ++i) {
+        MatDesc& d = p.m[i];
+        d.splits = 0;
+        d.rows_per_wg = 1;
+        for (int j = 0; j < 4; ++j) d.rsplit[j] = d.rrpw[j] = 0;
+        int count = 0;
+        for (int k = 0; k < ncls; ++k) {
+            const Cls& c = cls[k];
+            if (c.g != i) continue;
+            const int rpw = (c.R + c.splits - 1) / c.splits;
+            const int sp = (c.R + rpw - 1) / rpw;  // every range non-empty
+            if (c.j < 0) {
+                d.splits = sp;
+                d.rows_per_wg = rpw;
+            } else {
+                d.rsplit[c.j] = sp;
+                d.rrpw[c.j] = rpw;
+            }
+            count += sp * c.count;
+        }
+        d.g_base = base;
+        d.g_count = count;
+        base += count;
     }
 }
 
@@ -920,7 +1106,10 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     Params p{};
     p.G = n;
     p.M = M;
-    const int MV = (M == 1) ? 1 : 4;
+    // generic gather: P staged 4 columns at a time when that fits in LDS, else 1
+    size_t max_pk = 0;
+    for (int i = 0; i < n; ++i) max_pk = std::max(max_pk, (size_t)segs[i]->NBc * segs[i]->K);
+    const int MV = (M == 1 || max_pk * 4 * 4 > 96 * 1024) ? 1 : 4;
     p.MVz = (M + MV - 1) / MV;
     p.x_f16 = (x_dtype == CSDR_F16);
     p.accumulate = (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0;
@@ -930,14 +1119,13 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     p.nsplit = xa.nsplit;
     p.hd = xa.hd;
     char* ws = static_cast<char*>(workspace);
-    size_t off = kWsHeader;
+    size_t off = csdr::kWsHead;
     // the register-resident M == 1 gather needs every matrix at 4, 8 or 16 slots (16-byte
     // pieces) and the same count across the group; anything else takes the generic gather
     int slots = -1;
     bool fast = (M == 1);
     int ndx = 0;
     size_t lds_dx = 0, lds_g = 0;
-    long long total_units = 0;
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
         if (!s || !xs[i] || !ys[i]) return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
@@ -948,14 +1136,18 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         if (s->NB == 0)
             return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: matrix narrower than one block");
         if (!(s->slots == 4 || s->slots == 8 || s->slots == 16)) fast = false;
+        if ((size_t)s->NBc * s->K > kGMaxP) fast = false;  // the gather's P slice registers
         if (slots >= 0 && (int)s->slots != slots) fast = false;
         slots = (int)s->slots;
         MatDesc& d = p.m[i];
         d.codes = s->d_codes;
         d.dict = s->d_dict;
         d.slot_gamma = s->d_slot_gamma;
-        for (uint32_t q = 0; q < s->slots && q < (uint32_t)kMaxSlotsArg; ++q)
+        d.gunif = 1;
+        for (uint32_t q = 0; q < s->slots && q < (uint32_t)kMaxSlotsArg; ++q) {
             d.sgam[q] = s->h_slot_gamma[q];
+            if (d.sgam[q] != d.sgam[0]) d.gunif = 0;
+        }
         d.edge = s->d_edge;
         d.x = xs[i];
         d.y = ys[i];
@@ -990,14 +1182,6 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.dx_base = ndx;
         ndx += d.dx_count;
     }
-    if (fast) {
-        // M == 1: pieces of 16 bytes; PPT pieces per thread per unit
-        for (int i = 0; i < n; ++i) {
-            const MatDesc& d = p.m[i];
-            const long long pieces = (long long)d.R * d.NB * (slots / 4);
-            total_units += (pieces + kThreads * 2 - 1) / (kThreads * 2);
-        }
-    }
     int dev = 0, ncu = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
         int v = 0;
@@ -1005,36 +1189,26 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             v > 0)
             ncu = v;
     }
-    const int PPT = 2;
     int base = 0;
-    for (int i = 0; i < n; ++i) {
-        MatDesc& d = p.m[i];
-        const int nchunks8 = (d.nchunks + 7) / 8 * 8;
-        if (fast) {
-            // enough workgroups to fill every CU kGatherWGsPerCU deep, and >= 2 units each
-            const long long target =
-                (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGatherWGsPerCU);
-            const int ppr_full = d.NBc * (slots / 4);
-            const int rows_unit = std::max(1, (kThreads * PPT) / ppr_full);
-            const long long units_chunk = (d.R + rows_unit - 1) / rows_unit;
-            const long long units = units_chunk * d.nchunks;
-            long long wgs_i = std::max<long long>(1, target * units / std::max(1LL, total_units));
-            long long per_wg = std::max<long long>(env_int("CSDR_GATHER_UNITS_PER_WG", 4),
-                                                   (units + wgs_i - 1) / wgs_i);
-            d.splits = (int)((units_chunk + per_wg - 1) / per_wg);
-            d.rows_per_wg = (int)(((long long)d.R + d.splits - 1) / d.splits);
-            d.rows_per_wg = (d.rows_per_wg + rows_unit - 1) / rows_unit * rows_unit;
-            d.splits = (d.R + d.rows_per_wg - 1) / d.rows_per_wg;
-            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + (size_t)kThreads * PPT) * 4);
-        } else {
+    p.gpre = env_int("CSDR_GATHER_PRE", kGPre);
+    if (fast) {
+        plan_gather_splits(p, n, (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGWgsPerCu));
+        for (int i = 0; i < n; ++i) {
+            const MatDesc& d = p.m[i];
+            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64) * 4);
+            base += d.g_count;
+        }
+    } else {
+        for (int i = 0; i < n; ++i) {
+            MatDesc& d = p.m[i];
             d.Rt = MV == 1 ? 256 : 64;
             while (d.Rt > 16 && (size_t)d.Rt * d.NBc > 2048) d.Rt /= 2;
             d.splits = (d.R + d.Rt - 1) / d.Rt;
             lds_g = std::max(lds_g, ((size_t)d.NBc * d.K * MV + (size_t)d.Rt * d.NBc * MV) * 4);
+            d.g_base = base;
+            d.g_count = (d.nchunks + 7) / 8 * 8 * d.splits;
+            base += d.g_count;
         }
-        d.g_base = base;
-        d.g_count = nchunks8 * d.splits;
-        base += d.g_count;
     }
     if (lds_g > 160 * 1024 || lds_dx > 160 * 1024)
         return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: dictionary too large for LDS");
@@ -1044,7 +1218,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     if (phases & kPhaseGather) {
         if (fast)
-            launch_gather1<PPT>(p, slots, base, lds_g, st);
+            launch_gatherw(p, slots, base, lds_g, st);
         else if (MV == 1)
             gatherm_kernel<1><<<base, kThreads, lds_g, st>>>(p);
         else
@@ -1187,6 +1361,23 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
     return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
                         static_cast<hipStream_t>(hip_stream), kPhaseGather);
 }
+
+#ifdef CSDR_GATHER_TIMELINE
+// Copies the gather launch timeline (4 stamps per workgroup id, wall-clock ticks) to host and
+// clears it; *rate_hz gets the wall-clock rate.
+CSDR_API int csdr_debug_timeline(unsigned long long* host, size_t n, long long* rate_hz) {
+    n = std::min<size_t>(n, (size_t)kTlWgs * kTlSlots);
+    CSDR_HIP_CHECK(hipDeviceSynchronize());
+    CSDR_HIP_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), n * 8));
+    std::vector<unsigned long long> z((size_t)kTlWgs * kTlSlots, 0ull);
+    CSDR_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), z.data(), z.size() * 8));
+    int dev = 0, r = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev);
+    *rate_hz = (long long)r * 1000;
+    return CSDR_OK;
+}
+#endif
 
 CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* s, float* w, void* hip_stream) {
     if (!s || !w) return set_error(CSDR_E_INVALID, "hsdb_decompress: bad argument");

@@ -27,6 +27,78 @@ struct csdr_hsdb {
 
 namespace csdr {
 
+// ---- chunk-major code layout of 1-row tiles
+// Block columns are grouped in chunks: full chunks of NBc (a power of two) columns, then the
+// remainder NB % NBc split into power-of-two chunks, largest first (e.g. NB = 14, NBc = 8:
+// widths 8, 4, 2). Chunk c covering columns [b0, b0 + nbc) is stored at word b0 * R * slots,
+// each row's nbc tiles back to back, so every chunk's rows form one contiguous run and every
+// row of a chunk spans a power-of-two number of 16-byte pieces.
+__host__ __device__ __forceinline__ uint32_t n_chunks(uint32_t NB, uint32_t NBc) {
+    return NB / NBc + (uint32_t)__builtin_popcount(NB % NBc);
+}
+
+// First column b0 and width nbc of chunk c (nbc = 0 past the last chunk).
+__host__ __device__ __forceinline__ void chunk_span(uint32_t c, uint32_t NB, uint32_t NBc,
+                                                   uint32_t& b0, uint32_t& nbc) {
+    const uint32_t nfull = NB / NBc;
+    if (c < nfull) {
+        b0 = c * NBc;
+        nbc = NBc;
+        return;
+    }
+    const uint32_t rem = NB - nfull * NBc;
+    b0 = nfull * NBc;
+    c -= nfull;
+    nbc = 0;
+    for (uint32_t bit = NBc >> 1; bit; bit >>= 1) {
+        if (!(rem & bit)) continue;
+        if (c == 0) {
+            nbc = bit;
+            return;
+        }
+        --c;
+        b0 += bit;
+    }
+}
+
+// Chunk c, first column b0 and width nbc of the chunk holding block column b (b < NB).
+__host__ __device__ __forceinline__ void chunk_of(uint32_t b, uint32_t NB, uint32_t NBc,
+                                                 uint32_t& c, uint32_t& b0, uint32_t& nbc) {
+    const uint32_t nfull = NB / NBc;
+    if (b < nfull * NBc) {
+        c = b / NBc;
+        b0 = c * NBc;
+        nbc = NBc;
+        return;
+    }
+    const uint32_t rem = NB - nfull * NBc;
+    c = nfull;
+    b0 = nfull * NBc;
+    nbc = 0;
+    for (uint32_t bit = NBc >> 1; bit; bit >>= 1) {
+        if (!(rem & bit)) continue;
+        if (b < b0 + bit) {
+            nbc = bit;
+            return;
+        }
+        ++c;
+        b0 += bit;
+    }
+}
+
+// Word offset of tile (r, b) (its first slot) in the chunk-major layout.
+__host__ __device__ __forceinline__ size_t tile_word_offset(uint32_t r, uint32_t b, uint32_t R,
+                                                           uint32_t NB, uint32_t NBc,
+                                                           uint32_t slots) {
+    uint32_t c, b0, nbc;
+    chunk_of(b, NB, NBc, c, b0, nbc);
+    return ((size_t)b0 * R + (size_t)r * nbc + (b - b0)) * slots;
+}
+
+// Every product workspace starts with kWsHead reserved bytes; the data (P, transposed X)
+// follows.
+constexpr size_t kWsHead = 256;
+
 // Position of k (0..63) inside a 64-long block stored in the matrix-core k order: with
 // k = 16s + 4q + i (s, q, i in 0..3) it sits at 16q + 4s + i, so the 16 values a lane
 // feeds to four 16-deep MFMA steps are contiguous. An involution.

@@ -40,7 +40,6 @@ constexpr int kThreads = 256;  // 4 waves
 constexpr int kMaxAtoms = 1024;
 constexpr int kMaxMTile = 256;
 constexpr int kGroup = 8;
-constexpr size_t kWsHeader = 256;
 constexpr int kMfmaMinM = 2;  // smallest batch routed to this path (M = 1: the P-path GEMV)
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -168,13 +167,11 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
             xr[i] = *reinterpret_cast<const u32x4*>(
                 d.xt + part * nxt + (size_t)(p.m0 + mrow) * d.C_full + (size_t)nb * 64 + gr * 8);
         }
-        const int c = nb / d.NBc, bb = nb - c * d.NBc;
-        const int nbc = min(d.NBc, d.NB - c * d.NBc);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             const int r = min(nstrip * kStripRows + wave * 32 + rt * 16 + rl, d.R - 1);
             const uint32_t* cw =
-                d.codes + ((size_t)c * d.NBc * d.R + (size_t)r * nbc + bb) * d.slots;
+                d.codes + csdr::tile_word_offset(r, nb, d.R, d.NB, d.NBc, d.slots);
 #pragma unroll
             for (int j4 = 0; j4 < 4; ++j4)
                 cr[rt][j4] = *reinterpret_cast<const u32x4*>(cw + min(j4 * 4, d.slots - 4));
@@ -374,7 +371,7 @@ bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M) {
 }
 
 size_t mfma_workspace_bytes(int n, const csdr_hsdb* const* segs, int M) {
-    size_t t = kWsHeader;
+    size_t t = csdr::kWsHead;
     for (int i = 0; i < n; ++i) t += xt_bytes(segs[i], M);
     return t;
 }
@@ -393,7 +390,7 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
     p.x_f16 = (x_dtype == CSDR_F16);
     p.accumulate = accumulate;
     char* ws = static_cast<char*>(workspace);
-    size_t off = kWsHeader;
+    size_t off = csdr::kWsHead;
     size_t max_elems = 0;
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];

@@ -114,8 +114,9 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
 /* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
  * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
  * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
- * column into the workspace, Y = 0) and a gather launch (Y += the coded rows gathered from
- * P), all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots (the threshold
+ * column into the workspace, Y = 0 or bias) and a gather launch (Y += the coded rows gathered
+ * from P; at M == 1 with 4, 8 or 16 slots one 1024-thread workgroup per CU streams the codes),
+ * all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots (the threshold
  * is CSDR_HSDB_MFMA_MIN_M, default 2): an init launch and a matrix-core launch that decodes 64-column
  * tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
  * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
@@ -129,7 +130,7 @@ CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const v
                                     size_t workspace_bytes, void* hip_stream);
 /* The two launches of the P path of csdr_hsdb_matmul_group, separately, at any M (same
  * arguments; dx must precede gather on the stream, with the same workspace and X; the
- * workspace must hold P: NB * K * M floats per matrix plus 256 bytes, rounded up to 256). */
+ * workspace is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes). */
 CSDR_API int csdr_hsdb_dx_group(int n, const csdr_hsdb* const* segs, const void* const* x,
                                 int x_dtype, int M, float* const* y, void* workspace,
                                 size_t workspace_bytes, void* hip_stream);

