@@ -44,6 +44,10 @@ using csdr::set_error;
 
 constexpr int kThreads = 256;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Word 3 of a raw (stride 0) buffer resource on CDNA: 32-bit data format, no swizzle; with it a
+// lane whose offset is at or past num_records reads zeros and makes no memory access.
+constexpr int kRawBufferDword3 = 0x00020000;
+constexpr int kCachePolicyNT = 2;  // buffer load cache policy: nontemporal (streaming)
 
 // Launch-shape defaults, overridable for tuning sweeps through the environment
 // (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_CHUNK_BYTES).
@@ -98,7 +102,6 @@ struct Params {
     const float* nw;  // RMSNorm weights (C)
     float eps;
     int nsplit, hd;   // attention combine: splits and head size of the partials in x
-    int gpre;         // M == 1 gather: code loads per wave issued before the P slice's
 };
 
 template <int CTRL>
@@ -126,6 +129,9 @@ __device__ __forceinline__ float xload(const void* x, int f16, size_t i) {
 
 // xs[i] = float(src[i]) for i < n by the whole workgroup, kStageBatch independent loads
 // per thread in flight at a time (branch-free: out-of-range lanes reload the last element).
+// (clamped loads and unconditional clamped stores: lanes past the end rewrite element n - 1
+// with its own value; a conditional store would let the compiler sink each load into its
+// branch and wait for all loads in flight before every store)
 template <typename T, int NT = kThreads>
 __device__ __forceinline__ void stage_to_lds(const T* __restrict__ src, int n, float* xs) {
     const int tid = threadIdx.x;
@@ -135,10 +141,7 @@ __device__ __forceinline__ void stage_to_lds(const T* __restrict__ src, int n, f
         for (int j = 0; j < kStageBatch; ++j)
             v[j] = csdr::to_f32(src[min(i0 + j * NT + tid, n - 1)]);
 #pragma unroll
-        for (int j = 0; j < kStageBatch; ++j) {
-            const int i = i0 + j * NT + tid;
-            if (i < n) xs[i] = v[j];
-        }
+        for (int j = 0; j < kStageBatch; ++j) xs[min(i0 + j * NT + tid, n - 1)] = v[j];
     }
 }
 
@@ -153,10 +156,7 @@ __device__ __forceinline__ void copy_to_lds4(const float* __restrict__ src, int 
 #pragma unroll
         for (int j = 0; j < kStageBatch; ++j) v[j] = s4[min(i0 + j * kThreads + tid, n4 - 1)];
 #pragma unroll
-        for (int j = 0; j < kStageBatch; ++j) {
-            const int i = i0 + j * kThreads + tid;
-            if (i < n4) d4[i] = v[j];
-        }
+        for (int j = 0; j < kStageBatch; ++j) d4[min(i0 + j * kThreads + tid, n4 - 1)] = v[j];
     }
 }
 
@@ -209,14 +209,14 @@ __device__ __forceinline__ float xop_apply(const Params& p, const MatDesc& d, fl
 
 // Stages x features [64 b0, 64 (b0 + nb)) x M columns into xs (fp32, [feature][column])
 // with the call's x op applied (RMSNorm, SiLU(x) * x2, attention combine); with do_xe also
-// writes the transformed edge-strip inputs to xe_out (d.xe, or an LDS vector). A workgroup
-// of NT threads; ends with a barrier.
+// writes the transformed edge-strip inputs to d.xe. A workgroup of NT threads; ends with a
+// barrier.
 template <int NT = kThreads>
 __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb, float* xs,
-                              bool do_xe, float* xe_out = nullptr) {
+                              bool do_xe) {
     const int tid = threadIdx.x;
     const int M = p.M;
-    float* const xe = xe_out ? xe_out : d.xe;
+    float* const xe = d.xe;
     const size_t xbase = (size_t)b0 * 64 * M;
     const int nx = nb * 64 * M;
     __shared__ float inv[kMaxXopM];
@@ -427,41 +427,45 @@ __device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, in
     return s;
 }
 
-
-
 // ---- kernel 2, M == 1: the gather, 1024-thread workgroups
 // Workgroup = (matrix, chunk c, row range s), about kGWgsPerCu per CU in all
-// (CSDR_GATHER_WGS_PER_CU to change), each streaming about the same code bytes (plan_gather_splits), numbered
-// chunk-fastest so that consecutive ids (which dispatch round-robin over the 8 XCDs) spread
-// every matrix over all XCDs. Each of its 16 waves takes a contiguous sixteenth of the
-// workgroup's code run and first issues DEPTH 1 KiB loads of it (kept in registers); the
-// workgroup then stages the chunk's P slice (nbc * K floats, written by the dx launch) in LDS
-// and the waves stream their parts: per lane a fixed tile and slot quarter (each row of a
-// chunk spans a power of two of 16-byte pieces, 64 % pieces == 0), row totals as DPP /
-// shuffle butterflies over the row's lanes and one device-scope float atomic per
-// (row, chunk) into Y (initialised by the dx launch).
+// (CSDR_GATHER_WGS_PER_CU to change), each streaming about the same code bytes
+// (plan_gather_splits), numbered chunk-fastest so that consecutive ids (which dispatch
+// round-robin over the 8 XCDs) spread every matrix over all XCDs. The workgroup issues its
+// chunk's P slice loads (nbc * K floats, written by the dx launch), then each of its 16 waves
+// issues the first DEPTH 1 KiB loads of its contiguous sixteenth of the code run (bounded
+// buffer loads, kept in a ring of registers); P goes to LDS and the waves stream their parts:
+// per lane a fixed tile and slot quarter (each row of a chunk spans a power of two of 16-byte
+// pieces, 64 % pieces == 0), row totals as DPP / shuffle butterflies over the row's lanes,
+// kept in LDS, and after the stream one device-scope float atomic per (row, chunk) into Y
+// (initialised by the dx launch).
 constexpr int kGThreads = 1024;
 constexpr int kGWaves = kGThreads / 64;
 constexpr int kGDepth = 4;  // code loads in flight per wave
-constexpr int kGPre = 4;    // of which issued before the P slice's loads
 constexpr int kGWgsPerCu = 2;  // gather workgroups per CU (measured: 2 ahead of 1 by ~6%)
 constexpr size_t kGMaxP = 4 * 4 * kGThreads;  // P slice floats: 4 float4 per thread
-constexpr size_t kCodePad = 1024;             // bytes after the codes (one wave load)
+// rows per gather workgroup (their totals wait in LDS): with a 64 KiB P slice two workgroups
+// still fit in a CU's 160 KiB
+constexpr int kGMaxRows = 3840;
 
 // Optional per-workgroup timeline of the gather launch (built only with
 // -DCSDR_GATHER_TIMELINE, for measurement): stamps and the hardware ids per workgroup id.
 #ifdef CSDR_GATHER_TIMELINE
 constexpr int kTlWgs = 4096;
-constexpr int kTlSlots = 8;  // stamps 0..6, then (XCC id << 32 | HW_ID)
+// stamps 0..6, then (XCC id << 32 | HW_ID), the shader clock at stamp 0 and at the latest stamp
+constexpr int kTlSlots = 10;
 __device__ unsigned long long g_timeline[kTlWgs * kTlSlots];
 #define CSDR_TL(slot)                                                                       \
     do {                                                                                    \
         if (threadIdx.x == 0 && blockIdx.x < (unsigned)kTlWgs) {                            \
             g_timeline[blockIdx.x * kTlSlots + (slot)] = wall_clock64();                   \
-            if ((slot) == 0)                                                                \
+            g_timeline[blockIdx.x * kTlSlots + 9] = clock64();                             \
+            if ((slot) == 0) {                                                              \
                 g_timeline[blockIdx.x * kTlSlots + 7] =                                    \
                     ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | \
                     (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);                   \
+                g_timeline[blockIdx.x * kTlSlots + 8] = clock64();                         \
+            }                                                                               \
         }                                                                                   \
     } while (0)
 #else
@@ -470,8 +474,19 @@ __device__ unsigned long long g_timeline[kTlWgs * kTlSlots];
     } while (0)
 #endif
 
-template <int SLOTS, int DEPTH>
-__global__ __launch_bounds__(kGThreads) void gatherw_kernel(Params p) {
+// Slot gamma i of a matrix as a wave-uniform scalar: the readfirstlane keeps the per-lane
+// select over these values a select (otherwise the compiler turns it into a per-lane memory
+// load, whose wait then lands inside the streaming loops)
+__device__ __forceinline__ float sgam_at(const MatDesc& d, int i) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, d.sgam[i])));
+}
+
+// kGWgsPerCu 1024-thread workgroups per CU = 8 waves per SIMD: at most 64 VGPRs
+// P4: K % 4 == 0, the P slice is staged as float4
+template <int SLOTS, int DEPTH, bool P4>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(kGWgsPerCu * 4)))
+void gatherw_kernel(Params p) {
     extern __shared__ float smem[];
     const int wg = (int)blockIdx.x;
     int g = 0;
@@ -503,56 +518,70 @@ __global__ __launch_bounds__(kGThreads) void gatherw_kernel(Params p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     CSDR_TL(0);
 
-    // Every wave first issues its first DEPTH code loads, then the workgroup stages the chunk's
-    // P slice (nbc * K <= kGMaxP floats, written by the dx launch) in LDS: measured, P loads
-    // issued first (all CUs at once on the same ~1 MB of P) land later than behind the codes.
+    // The workgroup's P slice loads (nbc * K <= kGMaxP floats, written by the dx launch) are
+    // issued first, then every wave's first DEPTH code loads, and only then are the P values
+    // stored to LDS: VMEM loads complete in issue order, so P issued behind the code loads of
+    // all waves (most of the launch's bytes at once) would wait for them.
     constexpr int PPB = SLOTS / 4;  // 16-byte pieces per tile
     const int ppr = nbc * PPB;      // pieces per row: a power of two <= 64
     const int npieces = (rend - rbeg) * ppr;
     const int nload = (npieces + 63) >> 6;
-    // wave w streams its own contiguous part of the run (wave loads [w per, (w + 1) per)), so
-    // the workgroup's concurrent row atomics fall on 16 different lines of Y
+    // wave w streams its own contiguous part of the run (wave loads [w per, (w + 1) per));
+    // the trip count is wave-uniform
     const int per = (nload + kGWaves - 1) / kGWaves;
-    const int nk = max(0, min(per, nload - wave * per));
-    // the run, then this lane: loads past the run's end stay inside the codes allocation
-    // (kCodePad) and their lanes are discarded
-    const u32x4* lrun = reinterpret_cast<const u32x4*>(d.codes + (size_t)b0 * d.R * SLOTS +
-                                                       (size_t)rbeg * nbc * SLOTS) +
-                        wave * per * 64 + lane;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int nk = max(0, min(per, nload - wv * per));
+    // The wave's part is read through a raw buffer resource bounded to its valid bytes: every
+    // load is issued unconditionally (the compiler then waits for exactly the load it needs,
+    // where a conditional load would make it wait for all loads in flight), and a load at or
+    // past the end returns zeros without touching memory.
+    const int wfirst = wv * per * 64;  // the wave's first piece in the run
+    const int wvalid = max(0, min(per * 64, npieces - wfirst));
+    const uint32_t* wbase = d.codes + (size_t)b0 * d.R * SLOTS + (size_t)rbeg * nbc * SLOTS +
+                            (size_t)wfirst * 4;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, wvalid * 16, kRawBufferDword3);
     constexpr int kStep = 64;  // pieces between a wave's consecutive loads
-    u32x4 buf[DEPTH];
-    const int pre = p.gpre;  // code loads issued before the P slice's loads
-#pragma unroll
-    for (int k = 0; k < DEPTH; ++k)
-        if (k < nk && k < pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
+    auto piece = [&](int k) -> u32x4 {
+        return __builtin_amdgcn_raw_buffer_load_b128(rs, (k * kStep + lane) * 16, 0, kCachePolicyNT);
+    };
 
     float* Ps = smem;               // nbc * K floats
     float* xe = Ps + d.NBc * d.K;   // Ce (< 64) floats
+    float* rowt = xe + 64;          // rend - rbeg <= kGMaxRows row totals
     const bool edge = (c == d.nchunks - 1) && d.Ce > 0;
-    {
-        const float* Pg = d.P + (size_t)b0 * d.K;
-        const int np = nbc * d.K;
-        if ((d.K & 3) == 0) {
-            const float4* s4 = reinterpret_cast<const float4*>(Pg);
-            float4* d4 = reinterpret_cast<float4*>(Ps);
-            const int np4 = np >> 2;
-            float4 pv[4];
+    const float* Pg = d.P + (size_t)b0 * d.K;
+    const int np = nbc * d.K;
+    const int np4 = np >> 2;
+    const float4* s4 = reinterpret_cast<const float4*>(Pg);
+    float4* d4 = reinterpret_cast<float4*>(Ps);
+    // clamped loads and stores, no branches (lanes past the end rewrite the last element with
+    // its own value): a conditional store lets the compiler sink its load into the branch and
+    // wait for every load in flight before it
+    // (four named values, not an array: an array held across the scheduling barrier below is
+    // kept in scratch memory)
+    float4 pv0{}, pv1{}, pv2{}, pv3{};
+    if constexpr (P4) {
+        pv0 = s4[min(tid, np4 - 1)];
+        pv1 = s4[min(kGThreads + tid, np4 - 1)];
+        pv2 = s4[min(2 * kGThreads + tid, np4 - 1)];
+        pv3 = s4[min(3 * kGThreads + tid, np4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the P loads ahead of the code loads
+    // a ring of DEPTH + 1 register buffers: piece k sits in buf[k % (DEPTH + 1)], and the load of
+    // piece k + DEPTH goes into the buffer that piece k - 1 has left, so no live value is ever
+    // overwritten and the compiler needs no register copies (which would wait for the loads)
+    constexpr int NBUF = DEPTH + 1;
+    u32x4 buf[NBUF];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) pv[jj] = s4[min(jj * kGThreads + tid, np4 - 1)];
-#pragma unroll
-            for (int k = 0; k < DEPTH; ++k)
-                if (k < nk && k >= pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-                if (jj * kGThreads + tid < np4) d4[jj * kGThreads + tid] = pv[jj];
-        } else {
-#pragma unroll
-            for (int k = 0; k < DEPTH; ++k)
-                if (k < nk && k >= pre) buf[k] = __builtin_nontemporal_load(lrun + k * kStep);
-            stage_to_lds<float, kGThreads>(Pg, np, Ps);
-        }
-        if (edge && tid < d.Ce)
-            xe[tid] = d.xe ? d.xe[tid] : xload(d.x, p.x_f16, (size_t)d.C_full + tid);
+    for (int k = 0; k < DEPTH; ++k) buf[k] = piece(k);
+    if constexpr (P4) {
+        d4[min(tid, np4 - 1)] = pv0;
+        d4[min(kGThreads + tid, np4 - 1)] = pv1;
+        d4[min(2 * kGThreads + tid, np4 - 1)] = pv2;
+        d4[min(3 * kGThreads + tid, np4 - 1)] = pv3;
+    } else {
+        stage_to_lds<float, kGThreads>(Pg, np, Ps);
     }
     __syncthreads();
     CSDR_TL(1);
@@ -566,51 +595,65 @@ __global__ __launch_bounds__(kGThreads) void gatherw_kernel(Params p) {
     float gm[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        gm[e] = d.sgam[e];
+        gm[e] = sgam_at(d, e);
 #pragma unroll
         for (int hh = 1; hh < PPB; ++hh)
-            if (h == hh) gm[e] = d.sgam[hh * 4 + e];
+            if (h == hh) gm[e] = sgam_at(d, hh * 4 + e);
     }
     const bool gu = d.gunif != 0;
     const float g0 = d.sgam[0];
     const bool head = (pl == 0);
-    const int q0 = wave * per * 64 + lane;  // this lane's piece in the wave's first load
-    for (int k0 = 0; k0 < nk; k0 += DEPTH) {
+    const int q0 = wfirst + lane;  // this lane's piece in the wave's first load
+    // one piece: lane partial, row total over the row's lanes, the head lane keeps it
+    auto consume = [&](const u32x4& w, int k) {
+        const int qp = q0 + k * kStep;
+        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+        float acc = 0.0f;
+        if (gu) {
 #pragma unroll
-        for (int jj = 0; jj < DEPTH; ++jj) {
-            const int k = k0 + jj;
-            if (k >= nk) break;
-            const int qp = q0 + k * kStep;
-            const u32x4 w = buf[jj];
-            if (k + DEPTH < nk) buf[jj] = __builtin_nontemporal_load(lrun + (k + DEPTH) * kStep);
-            const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
-            float acc = 0.0f;
-            if (gu) {
+            for (int e = 0; e < 4; ++e)
+                acc = fmaf(csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
+        } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc = fmaf(csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc = fmaf(gm[e] * csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
-            }
-            if (qp >= npieces) acc = 0.0f;
-            if (ppr > 1) acc += dpp_move<0xB1>(acc);   // quad_perm [1,0,3,2]
-            if (ppr > 2) acc += dpp_move<0x4E>(acc);   // quad_perm [2,3,0,1]
-            if (ppr > 4) acc += dpp_move<0x141>(acc);  // row_half_mirror
-            if (ppr > 8) acc += dpp_move<0x140>(acc);  // row_mirror
-            if (ppr > 16) acc += __shfl_xor(acc, 16, 64);
-            if (ppr > 32) acc += __shfl_xor(acc, 32, 64);
-            if (head && qp < npieces) {
-                const int r = rbeg + (qp >> lg_ppr);
-                if (gu) acc *= g0;
-                if (edge) {
-                    const float* er = d.edge + (size_t)r * d.Ce;
-                    for (int cc = 0; cc < d.Ce; ++cc) acc = fmaf(er[cc], xe[cc], acc);
-                }
-                __hip_atomic_fetch_add(d.y + r, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            for (int e = 0; e < 4; ++e)
+                acc = fmaf(gm[e] * csdr::h2f(w4[e] >> 16), Pb[(uint16_t)w4[e]], acc);
         }
+        if (qp >= npieces) acc = 0.0f;
+        if (ppr > 1) acc += dpp_move<0xB1>(acc);   // quad_perm [1,0,3,2]
+        if (ppr > 2) acc += dpp_move<0x4E>(acc);   // quad_perm [2,3,0,1]
+        if (ppr > 4) acc += dpp_move<0x141>(acc);  // row_half_mirror
+        if (ppr > 8) acc += dpp_move<0x140>(acc);  // row_mirror
+        if (ppr > 16) acc += __shfl_xor(acc, 16, 64);
+        if (ppr > 32) acc += __shfl_xor(acc, 32, 64);
+        if (head && qp < npieces) rowt[qp >> lg_ppr] = gu ? acc * g0 : acc;
+    };
+    // Whole groups of NBUF pieces with no exit inside (an exit that rejoins the loop would
+    // leave the compiler unsure how many loads are in flight at the top, and it would wait for
+    // nearly all), then the last nk % NBUF pieces, whose loads were all issued already.
+    int k0 = 0;
+    for (; k0 + NBUF <= nk; k0 += NBUF) {
+#pragma unroll
+        for (int jj = 0; jj < NBUF; ++jj) {
+            const u32x4 w = buf[jj];
+            buf[(jj + DEPTH) % NBUF] = piece(k0 + jj + DEPTH);
+            consume(w, k0 + jj);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NBUF - 1; ++jj)
+        if (k0 + jj < nk) consume(buf[jj], k0 + jj);
+    // Row totals into Y after the stream, one device-scope atomic per row, 64 rows per
+    // instruction (atomics inside the stream would count among its loads in flight and make
+    // the compiler wait for all of them), with the top-right strip on the last chunk.
+    if (edge && tid < d.Ce) xe[tid] = d.xe ? d.xe[tid] : xload(d.x, p.x_f16, (size_t)d.C_full + tid);
+    __syncthreads();
+    for (int rr = tid; rr < rend - rbeg; rr += kGThreads) {
+        float v = rowt[rr];
+        if (edge) {
+            const float* er = d.edge + (size_t)(rbeg + rr) * d.Ce;
+            for (int cc = 0; cc < d.Ce; ++cc) v = fmaf(er[cc], xe[cc], v);
+        }
+        __hip_atomic_fetch_add(d.y + rbeg + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     CSDR_TL(2);
 }
@@ -882,10 +925,7 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     const size_t b_gamma = slot_gamma.size() * 4;
     const size_t b_edge = edge_bytes;
     CSDR_HIP_CHECK(hipMalloc(&s->d_dict, std::max<size_t>(b_dict, 4)));
-    // + kCodePad zero bytes: a gather wave load may read up to 1 KiB past the end of the last
-    // row range's run (those lanes' results are discarded)
-    CSDR_HIP_CHECK(hipMalloc(&s->d_codes, b_codes + kCodePad));
-    CSDR_HIP_CHECK(hipMemsetAsync(reinterpret_cast<char*>(s->d_codes) + b_codes, 0, kCodePad, st));
+    CSDR_HIP_CHECK(hipMalloc(&s->d_codes, std::max<size_t>(b_codes, 4)));
     CSDR_HIP_CHECK(hipMalloc(&s->d_slot_gamma, b_gamma));
     CSDR_HIP_CHECK(hipMalloc(&s->d_edge, std::max<size_t>(b_edge, 4)));
     s->device_bytes = b_dict + b_codes + b_gamma + b_edge;
@@ -956,26 +996,28 @@ size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
     return p_path_ws_bytes(n, segs, M);
 }
 
-template <int DEPTH>
-void launch_gatherw_d(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
+template <bool P4>
+void launch_gatherw_p(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
     switch (slots) {
         case 4:
-            gatherw_kernel<4, DEPTH><<<grid, kGThreads, lds, st>>>(p);
+            gatherw_kernel<4, kGDepth, P4><<<grid, kGThreads, lds, st>>>(p);
             break;
         case 8:
-            gatherw_kernel<8, DEPTH><<<grid, kGThreads, lds, st>>>(p);
+            gatherw_kernel<8, kGDepth, P4><<<grid, kGThreads, lds, st>>>(p);
             break;
         default:
-            gatherw_kernel<16, DEPTH><<<grid, kGThreads, lds, st>>>(p);
+            gatherw_kernel<16, kGDepth, P4><<<grid, kGThreads, lds, st>>>(p);
             break;
     }
 }
 
 void launch_gatherw(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
-    if (env_int("CSDR_GATHER_DEPTH", kGDepth) >= 8)
-        launch_gatherw_d<8>(p, slots, grid, lds, st);
+    bool p4 = true;
+    for (int i = 0; i < p.G; ++i) p4 = p4 && (p.m[i].K & 3) == 0;
+    if (p4)
+        launch_gatherw_p<true>(p, slots, grid, lds, st);
     else
-        launch_gatherw_d<kGDepth>(p, slots, grid, lds, st);
+        launch_gatherw_p<false>(p, slots, grid, lds, st);
 }
 
 // Row ranges for the M == 1 gather, balanced by bytes: a workgroup of a chunk of nbc block
@@ -1004,6 +1046,7 @@ void plan_gather_splits(Params& p, int n, long long target) {
         auto add = [&](int j, int width, int count) {
             Cls c{i, j, width, count, d.R, 1};
             c.splits = (int)std::max(1.0, std::floor((double)d.R * width / U));
+            c.splits = std::max(c.splits, (d.R + kGMaxRows - 1) / kGMaxRows);
             c.splits = std::min(c.splits, d.R);
             used += (long long)c.splits * count;
             cls[ncls++] = c;
@@ -1190,12 +1233,14 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             ncu = v;
     }
     int base = 0;
-    p.gpre = env_int("CSDR_GATHER_PRE", kGPre);
     if (fast) {
         plan_gather_splits(p, n, (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGWgsPerCu));
         for (int i = 0; i < n; ++i) {
             const MatDesc& d = p.m[i];
-            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64) * 4);
+            int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup (<= kGMaxRows)
+            for (int j = 0; j < 4; ++j)
+                if (d.rsplit[j]) rows = std::max(rows, d.rrpw[j]);
+            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64 + rows) * 4);
             base += d.g_count;
         }
     } else {

@@ -1,10 +1,11 @@
 """GPU parity of the M == 1 block-coded product (a dx launch writing P = D . x per block
-column and Y's start value, then the 1024-thread-per-CU gather launch) against the CPU
+column and Y's start value, then the gather launch of 1024-thread workgroups) against the CPU
 oracle, through the C-ABI, over the chunk layouts the segment loader produces (full chunks
-of 16 block columns, power-of-two remainders, edge strips, 4 / 8 / 16 slots).
+of 16 block columns, power-of-two remainders, edge strips, 4 / 8 / 16 slots, K not a
+multiple of 4).
 
-Bar: relative L2 <= 1e-3 at fp32 accumulation (the paths here all compute P in fp32, so
-they agree with the oracle to ~1e-6).
+Bar: relative L2 <= 1e-3 at fp32 accumulation (P is computed in fp32, so the results agree
+with the oracle to ~1e-6).
 """
 import ctypes as C
 
@@ -37,6 +38,7 @@ def _segs(streams):
     (37, 200, 64, 4, np.float32),         # ragged, edge strip, one short chunk
     (1, 512, 128, 8, np.float32),         # a single row
     (64, 4096, 2048, 8, np.float16),      # large dictionary: narrower chunks
+    (130, 640, 60, 8, np.float32),        # K not a multiple of 4 or 16
 ])
 def test_gather_parity(gpu, R, Cc, K, s, dtype):
     stream = synth.hsdb_layer(R, Cc, K, s, seed_dict=11, seed_codes=12)
@@ -201,3 +203,35 @@ def test_groups_share_one_workspace(gpu):
     for sg in segs:
         for s in sg:
             s.free()
+
+
+@pytest.mark.parametrize("R,Cc,K,s", [
+    (896, 4864, 1024, 8),   # the down projection of a 0.5B-shaped layer: 76 block columns
+    (300, 1000, 256, 16),   # edge strip
+    (40, 2048, 128, 4),
+])
+def test_accumulate_without_bias_wide(gpu, R, Cc, K, s):
+    """Y += W.x (a residual add folded into the product, no bias): the gather workgroups add
+    their row totals atomically into Y's existing values."""
+    from cortexsdr_amd import _lib
+
+    lib = _lib.load()
+    stream = synth.hsdb_layer(R, Cc, K, s, seed_dict=4, seed_codes=5)
+    (seg,) = _segs([stream])
+    from cortexsdr_amd.hsdr import group_workspace
+
+    ws = group_workspace([seg], 1)
+    rng = np.random.default_rng(11)
+    y0 = rng.standard_normal((R, 1)).astype(np.float32)
+    hs = (C.c_void_p * 1)(seg._h.value)
+    for it in range(2):
+        x = synth.activations(Cc, 1, seed=60 + it)
+        xd = gpu.from_numpy(x).cuda()
+        yd = gpu.from_numpy(y0.copy()).cuda()
+        xp = (C.c_void_p * 1)(xd.data_ptr())
+        yp = (C.c_void_p * 1)(yd.data_ptr())
+        _lib.check(lib.csdr_hsdb_matmul_group_ex(1, hs, xp, 0, 1, yp, None, 1, ws.data_ptr(),
+                                                  ws.numel(), None))
+        ref = y0 + oracle.hsdb_matmul(stream, x)
+        assert rel_l2(yd.cpu().numpy(), ref) <= TOL
+    seg.free()
