@@ -39,9 +39,9 @@ MALL_BYTES = 256 * 1024 * 1024
 # HBM bytes per gather launch (cfg2, M = 1, both matrices) from two rocprofv3 --pmc runs of
 # this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
 # counter reads for a plain 256 MiB device copy in the same run (--calibrate-copy: FETCH_SIZE
-# reads 0.5x the bytes copied, WRITE_SIZE 1.0x): 22549.2 KiB / 0.5 + 1376.0 KiB / 1.0.
+# reads 0.5x the bytes copied, WRITE_SIZE 1.0x): 23946.6 KiB / 0.5 + 1455.9 KiB / 1.0.
 # Summary and commands: profiles/hsdb_gather_cfg2_hbm_traffic.md. Update with the kernel.
-GATHER_TRAFFIC_BYTES = int((22549.2 / 0.5 + 1376.0 / 1.0) * 1024)
+GATHER_TRAFFIC_BYTES = int((23946.6 / 0.5 + 1455.9 / 1.0) * 1024)
 
 
 def parse():
@@ -313,7 +313,7 @@ def main():
             "gather_kernel_ms_events": round(kern_ms, 6),
         },
         "roofline": {
-            "kernel": "gather1_kernel<8,2> (csdr_hsdb_gather_group, both matrices)",
+            "kernel": "gatherw_kernel<8,4,true> (csdr_hsdb_gather_group, both matrices)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,

@@ -59,7 +59,7 @@ int env_int(const char* name, int dflt) {
 }
 
 constexpr uint32_t kMaxChunkBlocks = 16;
-constexpr uint32_t kChunkPBytes = 65536;  // P slice of one chunk (nbc * K fp32), at most
+constexpr uint32_t kChunkPBytes = 16384;  // P slice of one chunk (nbc * K fp32), at most
 
 
 // ------------------------------------------------------------------ matmul kernels
