@@ -292,6 +292,107 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
     __syncthreads();
 }
 
+// M == 1 staging of x features [64 b0, 64 (b0 + nb)) (nb * 64 <= 4 NT) with the call's x op
+// applied, into xs, and with do_xe the transformed edge-strip inputs into d.xe. Every global
+// load is issued before the first wait, so the staging costs one memory round trip where the
+// generic one makes up to three dependent ones (RMSNorm: the sum of squares, then x, then the
+// weights). The attention combine is one pass over the splits, four at a time, with a running
+// maximum (online softmax). Ends with a barrier.
+// XOP: the call's x op (CSDR_XOP_*), fixed at compile time so that each kind gets only the
+// registers it needs.
+template <int NT, int XOP>
+__device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, float* xs,
+                           bool do_xe) {
+    constexpr int kPer = 4;         // features per thread
+    constexpr int kSlots = kPer + 1;  // + the edge-strip input
+    const int tid = threadIdx.x;
+    const int nx = nb * 64, f0 = b0 * 64;
+    const int C = d.C_full + d.Ce;
+    __shared__ float red[NT / 64];
+    int feat[kSlots];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) feat[i] = f0 + min(tid + i * NT, nx - 1);
+    feat[kPer] = min(d.C_full + tid, C - 1);
+    float v[kSlots];
+    if constexpr (XOP == CSDR_XOP_ATTN) {
+        const float* part = static_cast<const float*>(d.x);
+        const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
+        const float* pp[kSlots];
+        float M[kSlots], den[kSlots], num[kSlots];
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i) {
+            const int h = feat[i] / hd;
+            pp[i] = part + (size_t)h * ns * ps;
+            M[i] = -INFINITY;
+            den[i] = 0.f;
+            num[i] = 0.f;
+        }
+        for (int s0 = 0; s0 < ns; s0 += 4) {
+            float ms[kSlots][4], ls[kSlots][4], os[kSlots][4];
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) {
+                const int dd = feat[i] - (feat[i] / hd) * hd;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float* q = pp[i] + (size_t)min(s0 + j, ns - 1) * ps;
+                    ms[i][j] = q[0];
+                    ls[i][j] = q[1];
+                    os[i][j] = q[2 + dd];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (s0 + j >= ns || ms[i][j] == -INFINITY) continue;
+                    const float Mn = fmaxf(M[i], ms[i][j]);
+                    const float a = expf(M[i] - Mn), b = expf(ms[i][j] - Mn);
+                    den[i] = fmaf(den[i], a, b * ls[i][j]);
+                    num[i] = fmaf(num[i], a, b * os[i][j]);
+                    M[i] = Mn;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i) v[i] = den[i] > 0.f ? num[i] / den[i] : 0.f;
+    } else {
+        float w[kSlots];
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i) {
+            v[i] = xload(d.x, p.x_f16, (size_t)feat[i]);
+            if constexpr (XOP == CSDR_XOP_RMSNORM) w[i] = p.nw[feat[i]];
+            if constexpr (XOP == CSDR_XOP_SILU_MUL) w[i] = static_cast<const float*>(d.x2)[feat[i]];
+        }
+        if constexpr (XOP == CSDR_XOP_RMSNORM) {
+            // 1 / rms over all C features (x ops take fp32 x)
+            const float* xf = static_cast<const float*>(d.x);
+            float ss = 0.f;
+            for (int j0 = 0; j0 < C; j0 += NT * kStageBatch) {
+                float t[kStageBatch];
+#pragma unroll
+                for (int j = 0; j < kStageBatch; ++j) t[j] = xf[min(j0 + j * NT + tid, C - 1)];
+#pragma unroll
+                for (int j = 0; j < kStageBatch; ++j)
+                    if (j0 + j * NT + tid < C) ss = fmaf(t[j], t[j], ss);
+            }
+            ss = wg_sum<NT>(ss, red);
+            const float inv = 1.0f / sqrtf(ss / (float)C + p.eps);
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) v[i] = v[i] * inv * w[i];
+        } else if constexpr (XOP == CSDR_XOP_SILU_MUL) {
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) v[i] = (v[i] * (1.0f / (1.0f + expf(-v[i])))) * w[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (tid + i * NT < nx) xs[tid + i * NT] = v[i];
+    if (do_xe && XOP != CSDR_XOP_NONE && d.xe && tid < d.Ce) d.xe[tid] = v[kPer];
+    __syncthreads();
+}
+
+// XOP: p.xop at compile time (the M == 1 staging's registers depend on it)
+template <int XOP>
 __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     extern __shared__ float smem[];
     const int wg = blockIdx.x;
@@ -326,7 +427,10 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
         float4 dv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (live) dv = reinterpret_cast<const float4*>(d.dict + (size_t)a * 64)[l16];
         float* xs = smem;  // [bb][t][m], nb * 64 * M floats (x rows are contiguous)
-        stage_x_chunk(p, d, b0, nb, xs, u == 0);
+        if (M == 1 && nb * 64 <= 4 * kThreads)
+            stage_x_m1<kThreads, XOP>(p, d, b0, nb, xs, u == 0);
+        else
+            stage_x_chunk(p, d, b0, nb, xs, u == 0);
         float* const Pout = d.P + (size_t)b0 * d.K * M + (size_t)a * M;  // + bb*K*M + m
         const size_t pstride = (size_t)d.K * M;
         int bb = 0;
@@ -1258,7 +1362,20 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     if (lds_g > 160 * 1024 || lds_dx > 160 * 1024)
         return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: dictionary too large for LDS");
     if (phases & kPhaseDx) {
-        dx_kernel<<<ndx, kThreads, lds_dx, st>>>(p);
+        switch (p.xop) {
+            case CSDR_XOP_RMSNORM:
+                dx_kernel<CSDR_XOP_RMSNORM><<<ndx, kThreads, lds_dx, st>>>(p);
+                break;
+            case CSDR_XOP_SILU_MUL:
+                dx_kernel<CSDR_XOP_SILU_MUL><<<ndx, kThreads, lds_dx, st>>>(p);
+                break;
+            case CSDR_XOP_ATTN:
+                dx_kernel<CSDR_XOP_ATTN><<<ndx, kThreads, lds_dx, st>>>(p);
+                break;
+            default:
+                dx_kernel<CSDR_XOP_NONE><<<ndx, kThreads, lds_dx, st>>>(p);
+                break;
+        }
         CSDR_LAUNCH_CHECK("hsdb dx");
     }
     if (phases & kPhaseGather) {
