@@ -12,6 +12,8 @@
 // captured once in a HIP graph and replayed for every token.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include <cmath>
 #include <string>
 
@@ -251,13 +253,25 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
                 vnew;
         }
     }
+    // every K and V row of this lane's positions is loaded before the first use (one memory
+    // round trip for the split, instead of one per pass and operand)
+    constexpr int kMaxPass = 256 / NG;  // S <= 256
+    const int npass = (p1 - p0 + NG - 1) / NG;
+    h8 kr[kMaxPass], vr[kMaxPass];
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        if (j < npass) {
+            const int p = min(p0 + lg + j * NG, p1 - 1);
+            kr[j] = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
+            vr[j] = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+        }
+    }
     // scores
-    for (int p = p0 + lg; p < p1; p += NG) {
-        h8 kv;
-        if (ROPE && p == plast)
-            kv = knew;
-        else
-            kv = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        const int p = p0 + lg + j * NG;
+        if (j >= npass || p >= p1) continue;
+        const h8 kv = (ROPE && p == plast) ? knew : kr[j];
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             float d = 0.f;
@@ -294,12 +308,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     for (int g = 0; g < GW; ++g)
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
-    for (int p = p0 + lg; p < p1; p += NG) {
-        h8 vv;
-        if (ROPE && p == plast)
-            vv = vnew;
-        else
-            vv = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        const int p = p0 + lg + j * NG;
+        if (j >= npass || p >= p1) continue;
+        const h8 vv = (ROPE && p == plast) ? vnew : vr[j];
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             const float e = sc[g][p - p0];
@@ -454,10 +467,19 @@ constexpr int kSelectBlocks = 256;
 
 // Positions per split: the power of two in [64, 256] that gives about 512 workgroups (at
 // least 64 positions per split keeps the partial count small for short contexts).
+// Positions per split: about T / 8 rounded up to a power of two in [64, 256], so a head has at
+// most 8 splits up to 2048 positions (every split's K/V rows are loaded in one round trip, and
+// the consumer's combine reads nsplit partials per feature; measured on cfg4, 640 positions:
+// 128 ahead of 64 and 256). CSDR_ATTN_SPLIT = 64, 128 or 256 forces a length.
 int attn_split_len(int B, int Hkv, int zsplit, int T) {
-    const long long want = (long long)T * B * Hkv * zsplit / 512;
+    (void)B;
+    (void)Hkv;
+    (void)zsplit;
+    const char* ev = std::getenv("CSDR_ATTN_SPLIT");
+    const int forced = ev ? std::atoi(ev) : 0;
+    if (forced == 64 || forced == 128 || forced == 256) return forced;
     int S = 64;
-    while (S < 256 && S < want) S *= 2;
+    while (S < 256 && 8LL * S < T) S *= 2;
     return S;
 }
 
