@@ -115,7 +115,7 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
  * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
  * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
  * column into the workspace, Y = 0 or bias) and a gather launch (Y += the coded rows gathered
- * from P; at M == 1 with 4, 8 or 16 slots one 1024-thread workgroup per CU streams the codes),
+ * from P; at M == 1 with 4, 8 or 16 slots two 1024-thread workgroups per CU stream the codes),
  * all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots (the threshold
  * is CSDR_HSDB_MFMA_MIN_M, default 2): an init launch and a matrix-core launch that decodes 64-column
  * tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
@@ -233,7 +233,8 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
 /* Decode attention: out (B x Hq x hd) = softmax(q.K^T * scale) V over cached positions
  * [0, len_b) (len_b = lens_dev[b], or len_host when lens_dev is NULL); caches (B x T x Hkv x
  * hd) fp16; GQA as repeat_kv_heads (cortex_sdk.cpp:1453-1478); scale 0 = 1/sqrt(hd).
- * Split over 256-position chunks (workspace csdr_attn_decode_workspace_bytes) then combined.
+ * Split over chunks of 64..256 positions (about T / 8; workspace csdr_attn_decode_workspace_bytes)
+ * then combined.
  * head_dim 64 or 128. Replaces Kernels::multi_head_attention's full-context recompute
  * (attention_kernels.cpp:26-113) with the cached form flash_attention.cpp:165-247 intends. */
 CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T);
