@@ -160,14 +160,17 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q,
 
 // ---------------------------------------------------------------- flash-decode attention
 
-// Partial softmax-attention over positions [s*S, min(L, (s+1)*S)) for the GW query heads
-// (of one batch entry) that share KV head kvh: part = (max score m, sum of exp l,
-// o[hd] = sum exp * v) per head. LPP = HD/8 lanes hold one position's 16-byte K/V pieces
-// (one coalesced HD*2-byte row per position), so each K/V byte is read once for all the
-// query heads of its group; scores go through LDS for the softmax.
-// Fused form (ROPE): the query is rotated in registers at position L - 1, position L - 1's key
-// and value come from the projections (k_new rotated, both rounded to fp16 as the cache holds
-// them), and the workgroup whose split holds L - 1 appends them to the caches.
+// Split attention over positions [s*S, min(L, (s+1)*S)) (n <= 256) for the GW query heads (of
+// one batch entry) that share KV head kvh, staged through LDS: every K and V piece of the
+// split's rows is loaded up front (one memory round trip) and stored to LDS as fp16, rows
+// padded by 16 bytes against bank conflicts; scores with one thread per position (its K row
+// read once, the query heads broadcast from LDS); softmax statistics per head by one wave;
+// P.V with threads over the (head, dim) outputs, reading V columns from LDS (no cross-lane
+// reductions). Writes part = (max score m, sum of exp l, o[hd] = sum exp * v) per head, or
+// the normalised output when the call has one split and an output.
+// ROPE: the query is rotated in registers at position L - 1, position L - 1's key and value
+// come from the projections (k_new rotated, both rounded to fp16 as the cache holds them),
+// and the workgroup whose split holds L - 1 appends them to the caches.
 struct RopeArgs {
     const float* knew;  // B x Hkv x HD (fp32, unrotated)
     const float* vnew;
@@ -176,6 +179,226 @@ struct RopeArgs {
     float theta;
 };
 
+constexpr int kAttnMaxS = 256;  // positions per split, at most (one thread per position)
+
+// LDS bytes of attn_lds_kernel<HD, GW> at split length S
+constexpr size_t attn_lds_bytes(int HD, int GW, int S) {
+    return (size_t)2 * S * (HD + 8) * 2 + (size_t)GW * HD * 4 + (size_t)GW * S * 4 +
+           (size_t)GW * 2 * 4 + (size_t)kThreads * 4;
+}
+
+template <int HD, int GW, bool ROPE>
+__global__ __launch_bounds__(kThreads) void attn_lds_kernel(
+    const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
+    const int* __restrict__ lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
+    float* __restrict__ part, float* __restrict__ out, int nsplit, RopeArgs ra) {
+    constexpr int HDP = HD + 8;                             // padded row, halves
+    constexpr int PPR = HD / 8;                             // 16-byte pieces per row
+    constexpr int kPPT = kAttnMaxS * PPR / kThreads;        // pieces per thread, at most
+    extern __shared__ float smem[];
+    _Float16* tk = reinterpret_cast<_Float16*>(smem);       // S x HDP
+    _Float16* tv = tk + (size_t)S * HDP;                    // S x HDP
+    float* qs = reinterpret_cast<float*>(tv + (size_t)S * HDP);  // GW x HD
+    float* sc = qs + GW * HD;                               // GW x S
+    float* stat = sc + GW * S;                              // GW x 2
+    float* red = stat + GW * 2;                             // kThreads
+    const int G = Hq / Hkv;
+    const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
+    const int s = blockIdx.y;
+    const int h0 = kvh * G + blockIdx.z * GW;
+    const int nh = min(GW, G - (int)blockIdx.z * GW);
+    const int L = lens ? lens[b] : len_host;
+    const int p0 = s * S, p1 = min(L, p0 + S);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool direct = (nsplit == 1 && out != nullptr);
+    if (p0 >= p1) {  // empty split (the length is below this split's range)
+        for (int g = 0; g < nh; ++g) {
+            const int bh = b * Hq + h0 + g;
+            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            if (!direct) {
+                if (tid == 0) {
+                    pp[0] = -INFINITY;
+                    pp[1] = 0.f;
+                }
+                for (int i = tid; i < HD; i += kThreads) pp[2 + i] = 0.f;
+            } else {
+                for (int i = tid; i < HD; i += kThreads) out[(size_t)bh * HD + i] = 0.f;
+            }
+        }
+        return;
+    }
+    const int n = p1 - p0;
+    const size_t rstride = (size_t)Hkv * HD;
+    const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD;
+    const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD;
+
+    // 1. the split's K and V rows, every load issued before the first use
+    h8 kr[kPPT], vr[kPPT];
+#pragma unroll
+    for (int k = 0; k < kPPT; ++k) {
+        const int idx = tid + k * kThreads, p = idx / PPR, j = idx - p * PPR;
+        if (p < n) {
+            kr[k] = *reinterpret_cast<const h8*>(kb + (size_t)(p0 + p) * rstride + j * 8);
+            vr[k] = *reinterpret_cast<const h8*>(vb + (size_t)(p0 + p) * rstride + j * 8);
+        }
+    }
+    // the query heads (rotated at L - 1), into LDS
+    const int plast = L - 1;
+    for (int e = tid; e < nh * (HD / 2); e += kThreads) {
+        const int g = e / (HD / 2), i2 = 2 * (e - g * (HD / 2));
+        const float* qh = q + ((size_t)b * Hq + h0 + g) * HD;
+        float x0 = qh[i2], x1 = qh[i2 + 1];
+        if constexpr (ROPE) {
+            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
+            const float ang = (float)plast * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            const float r0 = fmaf(x0, c, -(x1 * sn)), r1 = fmaf(x0, sn, x1 * c);
+            x0 = r0;
+            x1 = r1;
+        }
+        qs[g * HD + i2] = x0;
+        qs[g * HD + i2 + 1] = x1;
+    }
+#pragma unroll
+    for (int k = 0; k < kPPT; ++k) {
+        const int idx = tid + k * kThreads, p = idx / PPR, j = idx - p * PPR;
+        if (p < n) {
+            *reinterpret_cast<h8*>(tk + (size_t)p * HDP + j * 8) = kr[k];
+            *reinterpret_cast<h8*>(tv + (size_t)p * HDP + j * 8) = vr[k];
+        }
+    }
+    if constexpr (ROPE) {
+        // position L - 1: the new key (rotated) and value, rounded to fp16, in the tile and,
+        // from the split that holds it, appended to the caches
+        if (plast >= p0 && plast < p1 && tid < HD / 2) {
+            const int i2 = 2 * tid;
+            const float* kn = ra.knew + ((size_t)b * Hkv + kvh) * HD;
+            const float* vn = ra.vnew + ((size_t)b * Hkv + kvh) * HD;
+            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
+            const float ang = (float)plast * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            const float k0 = kn[i2], k1 = kn[i2 + 1];
+            const _Float16 a0 = (_Float16)fmaf(k0, c, -(k1 * sn));
+            const _Float16 a1 = (_Float16)fmaf(k0, sn, k1 * c);
+            const _Float16 w0 = (_Float16)vn[i2], w1 = (_Float16)vn[i2 + 1];
+            const int pr = plast - p0;
+            tk[(size_t)pr * HDP + i2] = a0;
+            tk[(size_t)pr * HDP + i2 + 1] = a1;
+            tv[(size_t)pr * HDP + i2] = w0;
+            tv[(size_t)pr * HDP + i2 + 1] = w1;
+            if (blockIdx.z == 0) {
+                const size_t at = ((size_t)b * T + plast) * rstride + (size_t)kvh * HD + i2;
+                ra.kcw[at] = a0;
+                ra.kcw[at + 1] = a1;
+                ra.vcw[at] = w0;
+                ra.vcw[at + 1] = w1;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. scores: thread p over the query heads
+    if (tid < n) {
+        float acc[GW];
+#pragma unroll
+        for (int g = 0; g < GW; ++g) acc[g] = 0.f;
+        const _Float16* kr0 = tk + (size_t)tid * HDP;
+#pragma unroll 4
+        for (int j = 0; j < PPR; ++j) {
+            const h8 kv = *reinterpret_cast<const h8*>(kr0 + j * 8);
+#pragma unroll
+            for (int g = 0; g < GW; ++g) {
+                if (g < nh) {
+                    const float4 qa = *reinterpret_cast<const float4*>(qs + g * HD + j * 8);
+                    const float4 qb = *reinterpret_cast<const float4*>(qs + g * HD + j * 8 + 4);
+                    float d = acc[g];
+                    d = fmaf(qa.x, (float)kv[0], d);
+                    d = fmaf(qa.y, (float)kv[1], d);
+                    d = fmaf(qa.z, (float)kv[2], d);
+                    d = fmaf(qa.w, (float)kv[3], d);
+                    d = fmaf(qb.x, (float)kv[4], d);
+                    d = fmaf(qb.y, (float)kv[5], d);
+                    d = fmaf(qb.z, (float)kv[6], d);
+                    d = fmaf(qb.w, (float)kv[7], d);
+                    acc[g] = d;
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GW; ++g)
+            if (g < nh) sc[g * S + tid] = acc[g] * scale;
+    }
+    __syncthreads();
+
+    // 3. softmax statistics per head (wave w handles heads w, w + 4, ...)
+    for (int g = wave; g < nh; g += kThreads / 64) {
+        float m = -INFINITY;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[g * S + j]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int j = lane; j < n; j += 64) {
+            const float e = expf(sc[g * S + j] - m);
+            sc[g * S + j] = e;
+            l += e;
+        }
+        l = csdr::wave_sum(l);
+        if (lane == 0) {
+            stat[g * 2] = m;
+            stat[g * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+
+    // 4. P.V over the (head, dim) outputs; positions split into `parts` interleaved ranges
+    // when there are fewer outputs than threads
+    const int O = nh * HD;
+    const int parts = O >= kThreads ? 1 : kThreads / O;
+    auto finish = [&](int o, float v) {
+        const int g = o / HD, d = o - g * HD;
+        const int bh = b * Hq + h0 + g;
+        if (direct) {
+            out[(size_t)bh * HD + d] = v / stat[g * 2 + 1];
+        } else {
+            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            pp[2 + d] = v;
+            if (d == 0) {
+                pp[0] = stat[g * 2];
+                pp[1] = stat[g * 2 + 1];
+            }
+        }
+    };
+    if (parts == 1) {
+        for (int o = tid; o < O; o += kThreads) {
+            const int g = o / HD, d = o - g * HD;
+            const float* e = sc + g * S;
+            float acc = 0.f;
+            for (int p = 0; p < n; ++p) acc = fmaf(e[p], (float)tv[(size_t)p * HDP + d], acc);
+            finish(o, acc);
+        }
+    } else {
+        const int o = tid % O, pt = tid / O;
+        float acc = 0.f;
+        if (pt < parts) {
+            const int g = o / HD, d = o - g * HD;
+            const float* e = sc + g * S;
+            for (int p = pt; p < n; p += parts)
+                acc = fmaf(e[p], (float)tv[(size_t)p * HDP + d], acc);
+        }
+        red[tid] = acc;
+        __syncthreads();
+        if (tid < O) {
+            float v = 0.f;
+            for (int k = 0; k < parts; ++k) v += red[tid + k * O];
+            finish(tid, v);
+        }
+    }
+}
+
+// Lane-per-position form, for one query head per KV head (no grouped heads to share a staged
+// K/V tile): LPP = HD/8 lanes hold one position's 16-byte K/V pieces (one coalesced HD*2-byte
+// row per position); every K and V row of the split is loaded before the first use; scores go
+// through LDS for the softmax; P.V accumulates per lane and reduces across lanes and waves.
+// Same partials and ROPE behaviour as attn_lds_kernel.
 template <int HD, int GW, bool ROPE>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
@@ -465,8 +688,6 @@ __global__ __launch_bounds__(kThreads) void select2_kernel(const float* __restri
 
 constexpr int kSelectBlocks = 256;
 
-// Positions per split: the power of two in [64, 256] that gives about 512 workgroups (at
-// least 64 positions per split keeps the partial count small for short contexts).
 // Positions per split: about T / 8 rounded up to a power of two in [64, 256], so a head has at
 // most 8 splits up to 2048 positions (every split's K/V rows are loaded in one round trip, and
 // the consumer's combine reads nsplit partials per feature; measured on cfg4, 640 positions:
@@ -487,14 +708,17 @@ template <int HD, bool ROPE>
 void launch_attn(dim3 grid, int G, const float* q, const _Float16* k16, const _Float16* v16,
                  const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
                  float* part, float* out, int nsplit, const RopeArgs& ra, hipStream_t st) {
+    // one query head per KV head: the lane-per-position kernel (measured at Llama-7B shape,
+    // head_dim 128, 4096 positions: 20.5 vs 29.1 us; its small LDS footprint keeps several
+    // workgroups per CU where the staged tile would allow one)
     if (G == 1)
         attn_split_kernel<HD, 1, ROPE><<<grid, kThreads, 0, st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
     else if (G <= 4)
-        attn_split_kernel<HD, 4, ROPE><<<grid, kThreads, 0, st>>>(
+        attn_lds_kernel<HD, 4, ROPE><<<grid, kThreads, attn_lds_bytes(HD, 4, S), st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
     else
-        attn_split_kernel<HD, 8, ROPE><<<grid, kThreads, 0, st>>>(
+        attn_lds_kernel<HD, 8, ROPE><<<grid, kThreads, attn_lds_bytes(HD, 8, S), st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
 }
 
