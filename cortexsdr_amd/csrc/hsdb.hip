@@ -547,6 +547,8 @@ constexpr int kGThreads = 1024;
 constexpr int kGWaves = kGThreads / 64;
 constexpr int kGDepth = 4;  // code loads in flight per wave
 constexpr int kGWgsPerCu = 2;  // gather workgroups per CU (measured: 2 ahead of 1 by ~6%)
+constexpr int kGMinWgBytes = 16384;  // code bytes per gather workgroup, at least (cfg4 decode: 694
+                                     // tokens/s vs 681 at 1, 684 at 32 KiB)
 constexpr size_t kGMaxP = 4 * 4 * kGThreads;  // P slice floats: 4 float4 per thread
 // rows per gather workgroup (their totals wait in LDS): with a 64 KiB P slice two workgroups
 // still fit in a CU's 160 KiB
@@ -1338,7 +1340,14 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     int base = 0;
     if (fast) {
-        plan_gather_splits(p, n, (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGWgsPerCu));
+        // kGWgsPerCu workgroups per CU, fewer for small groups: at least CSDR_GATHER_WG_BYTES
+        // of codes per workgroup (each one stages a P slice of up to 16 KiB first)
+        long long target = (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGWgsPerCu);
+        long long code_bytes = 0;
+        for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
+        const long long min_bytes = env_int("CSDR_GATHER_WG_BYTES", kGMinWgBytes);
+        target = std::max(1LL, std::min(target, code_bytes / std::max(1LL, min_bytes)));
+        plan_gather_splits(p, n, target);
         for (int i = 0; i < n; ++i) {
             const MatDesc& d = p.m[i];
             int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup (<= kGMaxRows)
