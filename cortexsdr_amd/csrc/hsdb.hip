@@ -296,7 +296,7 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
 // applied, into xs, and with do_xe the transformed edge-strip inputs into d.xe. Every global
 // load is issued before the first wait, so the staging costs one memory round trip where the
 // generic one makes up to three dependent ones (RMSNorm: the sum of squares, then x, then the
-// weights). The attention combine is one pass over the splits, four at a time, with a running
+// weights). The attention combine is one pass over the splits, eight at a time, with a running
 // maximum (online softmax). Ends with a barrier.
 // XOP: the call's x op (CSDR_XOP_*), fixed at compile time so that each kind gets only the
 // registers it needs.
@@ -327,13 +327,14 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
             den[i] = 0.f;
             num[i] = 0.f;
         }
-        for (int s0 = 0; s0 < ns; s0 += 4) {
-            float ms[kSlots][4], ls[kSlots][4], os[kSlots][4];
+        constexpr int kSB = 8;  // splits per round trip
+        for (int s0 = 0; s0 < ns; s0 += kSB) {
+            float ms[kSlots][kSB], ls[kSlots][kSB], os[kSlots][kSB];
 #pragma unroll
             for (int i = 0; i < kSlots; ++i) {
                 const int dd = feat[i] - (feat[i] / hd) * hd;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < kSB; ++j) {
                     const float* q = pp[i] + (size_t)min(s0 + j, ns - 1) * ps;
                     ms[i][j] = q[0];
                     ls[i][j] = q[1];
@@ -343,7 +344,7 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
 #pragma unroll
             for (int i = 0; i < kSlots; ++i) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < kSB; ++j) {
                     if (s0 + j >= ns || ms[i][j] == -INFINITY) continue;
                     const float Mn = fmaxf(M[i], ms[i][j]);
                     const float a = expf(M[i] - Mn), b = expf(ms[i][j] - Mn);
