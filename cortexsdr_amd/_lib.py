@@ -60,6 +60,11 @@ SIGNATURES = {
     "csdr_q4k_linear": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                   _vp]),
     "csdr_q4k_dequant": (C.c_int, [_vp, _sz, C.c_int, _vp, _vp]),
+    "csdr_gguf_format": (C.c_int, [C.c_char_p]),
+    "csdr_gguf_block": (C.c_int, [C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "csdr_gguf_linear": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
+                                   _vp]),
+    "csdr_gguf_dequant": (C.c_int, [_vp, C.c_int, _sz, _vp, _vp]),
     "csdr_hsdb_matmul_group_ex": (C.c_int, [C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
                                             C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
                                             _vp, _sz, _vp]),

@@ -8,7 +8,8 @@
 //
 // One engine = one open .sdr archive (archive.cpp) + a device cache of loaded segments keyed
 // by index entry: strategy 5 payloads become csdr_hsdb segments, uncoded fp32 2-D tensors and
-// strategy-0 q4_k tensors are uploaded as they are. Every product runs on the engine's HIP
+// strategy-0 GGUF block tensors (every format decodeSupportedGGUFQuantized decodes,
+// SparseInferenceEngine.cpp:276-469) are uploaded as they are. Every product runs on the engine's HIP
 // stream; host buffers are staged through pinned-free device staging buffers owned by the
 // engine. generate_text builds a csdr_decoder from the archive's blk.N.* tensors.
 #include <hip/hip_runtime.h>
@@ -59,12 +60,13 @@ std::string lower(std::string s) {
     return s;
 }
 
-enum Kind { kHsdb, kDense, kQ4k };
+enum Kind { kHsdb, kDense, kQ4k, kGguf };
 
 struct Cached {
     Kind kind = kHsdb;
+    int gguf = -1;        // kGguf: CSDR_GGUF_* format
     csdr_hsdb* seg = nullptr;
-    void* dev = nullptr;  // dense fp32 W or Q4_K blocks
+    void* dev = nullptr;  // dense fp32 W or GGUF blocks
     uint32_t R = 0, C = 0;
     size_t bytes = 0;
     uint64_t last_use = 0;
@@ -174,7 +176,8 @@ CortexError load(CortexInferenceEngine* e, size_t idx, Cached** out) {
         c.R = hi.rows;
         c.C = hi.cols;
         c.bytes = hi.device_bytes;
-    } else if (info.strategy_id == 0 && (fmt == "q4_k" || fmt == "f32" || fmt == "fp32" ||
+    } else if (info.strategy_id == 0 && (csdr_gguf_format(fmt.c_str()) >= 0 || fmt == "f32" ||
+                                         fmt == "fp32" ||
                                          (fmt.empty() && info.original_type == 1))) {
         if (!info.has_metadata || info.n_dims != 2)
             return fail(CORTEX_ERROR_INFERENCE,
@@ -183,8 +186,16 @@ CortexError load(CortexInferenceEngine* e, size_t idx, Cached** out) {
         c.R = info.dims[0];
         c.C = info.dims[1];
         const bool q4k = (fmt == "q4_k");
-        const size_t want = q4k ? (size_t)c.R * c.C / 256 * 144 : (size_t)c.R * c.C * 4;
-        if ((q4k && c.C % 256) || bytes.size() != want)
+        const int gg = q4k ? -1 : csdr_gguf_format(fmt.c_str());
+        int bb = 4, be = 1;  // bytes per element group (fp32: 4 bytes per element)
+        if (q4k) {
+            bb = 144;
+            be = 256;
+        } else if (gg >= 0) {
+            csdr_gguf_block(gg, &bb, &be);
+        }
+        const size_t want = (size_t)c.R * c.C / be * bb;
+        if (c.C % be || bytes.size() != want)
             return fail(CORTEX_ERROR_INFERENCE, "matmulForLayer: segment '" + name + "' holds " +
                                                     std::to_string(bytes.size()) +
                                                     " bytes, expected " + std::to_string(want));
@@ -195,14 +206,15 @@ CortexError load(CortexInferenceEngine* e, size_t idx, Cached** out) {
             (void)hipFree(c.dev);
             return fail(CORTEX_ERROR_INFERENCE, "upload of '" + name + "' failed");
         }
-        c.kind = q4k ? kQ4k : kDense;
+        c.kind = q4k ? kQ4k : (gg >= 0 ? kGguf : kDense);
+        c.gguf = gg;
         c.bytes = want;
     } else {
         return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
                     "segment '" + name + "' (strategy " + std::to_string(info.strategy_id) +
                         ", format '" + info.data_format +
                         "') is not served by the device path: strategy 5 (HSDR/HSDB), or "
-                        "strategy 0 with fp32 or q4_k data");
+                        "strategy 0 with fp32 or a GGUF block format the engine decodes");
     }
     c.last_use = ++e->tick;
     e->cache_bytes += c.bytes;
@@ -545,13 +557,16 @@ CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHand
         if (hipMemcpyAsync(e->xd, input, input_size * 4, hipMemcpyHostToDevice, e->st) != hipSuccess)
             return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
         (void)hipEventRecord(ev0, e->st);
-        if (c->kind == kQ4k) {
+        if (c->kind == kQ4k || c->kind == kGguf) {
             // fp32 activations take the GEMV form row by row (the matrix-core form reads
             // fp16 activations)
             rc = CSDR_OK;
             for (size_t m = 0; m < M && rc == CSDR_OK; ++m)
-                rc = csdr_q4k_linear(c->dev, (int)R, (int)C, CSDR_Q4K_GGML, e->xd + m * C,
-                                     CSDR_F32, 1, e->yd + m * R, e->st);
+                rc = c->kind == kQ4k
+                         ? csdr_q4k_linear(c->dev, (int)R, (int)C, CSDR_Q4K_GGML, e->xd + m * C,
+                                           CSDR_F32, 1, e->yd + m * R, e->st)
+                         : csdr_gguf_linear(c->dev, c->gguf, (int)R, (int)C, e->xd + m * C,
+                                            CSDR_F32, 1, e->yd + m * R, e->st);
         } else {
             rc = csdr_dense_linear(static_cast<const float*>(c->dev), (int)R, (int)C, e->xd,
                                    (int)M, e->yd, e->st);
@@ -581,7 +596,10 @@ CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHand
         std::memcpy(output, host.data(), M * R * 4);
     }
     const auto t2 = std::chrono::steady_clock::now();
-    const char* path = c->kind == kHsdb ? "hsdb" : (c->kind == kQ4k ? "q4_k" : "dense_f32");
+    const char* path = c->kind == kHsdb   ? "hsdb"
+                       : c->kind == kQ4k  ? "q4_k"
+                       : c->kind == kGguf ? "gguf"
+                                          : "dense_f32";
     char buf[512];
     std::snprintf(buf, sizeof buf,
                   "{\"layer\":\"%s\",\"path\":\"%s\",\"rows\":%zu,\"cols\":%zu,\"batch\":%zu,"

@@ -30,6 +30,9 @@
  *   csdr_q4k_linear / csdr_q4k_dequant
  *       decodeSupportedGGUFQuantized q4_k (SparseInferenceEngine.cpp:266-274, 362-384) followed
  *       by Kernels::linear_forward (kernels/blas_kernels.cpp:264-293).
+ *   csdr_gguf_format / csdr_gguf_block / csdr_gguf_linear / csdr_gguf_dequant
+ *       decodeSupportedGGUFQuantized for every format it decodes (SparseInferenceEngine.cpp:
+ *       181-231 block sizes, 276-469 decode) followed by Kernels::linear_forward.
  */
 #ifndef CORTEXSDR_HIP_H
 #define CORTEXSDR_HIP_H
@@ -209,6 +212,64 @@ CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void*
  * reference: (d*sc)*q - dmin*m. */
 CSDR_API int csdr_q4k_dequant(const void* w, size_t n_blocks, int order, float* out,
                               void* hip_stream);
+
+/* ======================================================================
+ * GGUF block formats of the engine (strategy-0 tensors), dequant-matmul
+ * ==================================================================== */
+
+/* Format ids (ggml's type numbers). Decoded exactly as the reference engine does
+ * (SparseInferenceEngine.cpp:276-469), including its element orders: q4_0 / q4_1 / q5_0 / q5_1
+ * take element i from byte i/2 (low nibble for even i); q6_k's four 32-element quarters of
+ * each 128-element half use that half's scales 0, 2, 4, 6; q8_1's scale is read as fp32, q8_k's
+ * as fp16 with quants at byte 4. Formats without an exact decoder in the reference (q2_k, q3_k,
+ * q5_k, iq*, tq*, q4_0_x_y) take its generic rule: `bits` per element packed LSB-first at the
+ * end of the block, centred on 2^(bits-1), times the fp16 scale at the block start (1 when
+ * that is not finite or below 1e-12). */
+#define CSDR_GGUF_Q4_0 2
+#define CSDR_GGUF_Q4_1 3
+#define CSDR_GGUF_Q5_0 6
+#define CSDR_GGUF_Q5_1 7
+#define CSDR_GGUF_Q8_0 8
+#define CSDR_GGUF_Q8_1 9
+#define CSDR_GGUF_Q2_K 10
+#define CSDR_GGUF_Q3_K 11
+#define CSDR_GGUF_Q4_K 12
+#define CSDR_GGUF_Q5_K 13
+#define CSDR_GGUF_Q6_K 14
+#define CSDR_GGUF_Q8_K 15
+#define CSDR_GGUF_IQ2_XXS 16
+#define CSDR_GGUF_IQ2_XS 17
+#define CSDR_GGUF_IQ3_XXS 18
+#define CSDR_GGUF_IQ1_S 19
+#define CSDR_GGUF_IQ4_NL 20
+#define CSDR_GGUF_IQ3_S 21
+#define CSDR_GGUF_IQ2_S 22
+#define CSDR_GGUF_IQ4_XS 23
+#define CSDR_GGUF_IQ1_M 29
+#define CSDR_GGUF_Q4_0_4_4 31
+#define CSDR_GGUF_Q4_0_4_8 32
+#define CSDR_GGUF_Q4_0_8_8 33
+#define CSDR_GGUF_TQ1_0 34
+#define CSDR_GGUF_TQ2_0 35
+
+/* The format id of a GGUF type name as segment data_format holds it (case-insensitive),
+ * or -1. */
+CSDR_API int csdr_gguf_format(const char* name);
+
+/* Bytes and elements per block of a format (ggufBlockBytesForFormat /
+ * ggufBlockElementsForFormat, SparseInferenceEngine.cpp:181-231). */
+CSDR_API int csdr_gguf_block(int format, int* block_bytes, int* block_elems);
+
+/* y (M x R, fp32) = x (M x C) . dequant(W)^T, W = R rows of C / block_elems blocks (row-major
+ * device memory, any alignment). M == 1 takes fp32 or fp16 x; M > 1 takes fp16 x (8-byte
+ * aligned) and needs C % 16 == 0 (matrix-core path, dequantised values split into fp16 hi +
+ * lo, fp32 accumulation). C must be a multiple of the block's elements. No workspace. */
+CSDR_API int csdr_gguf_linear(const void* w, int format, int R, int C, const void* x,
+                              int x_dtype, int M, float* y, void* hip_stream);
+
+/* Dequantise n_blocks blocks to fp32 with the reference's arithmetic. */
+CSDR_API int csdr_gguf_dequant(const void* w, int format, size_t n_blocks, float* out,
+                               void* hip_stream);
 
 /* ======================================================================
  * Decoder ops (api/cortex_sdk.cpp run_transformer_decode building blocks)

@@ -82,6 +82,9 @@ def orc():
         L.orc_q5k_dequant.argtypes = [_u8p, _sz, _f32p]
         L.orc_q6k_dequant.argtypes = [_u8p, _sz, _f32p]
         L.orc_q4k_linear.argtypes = [_u8p, _sz, _sz, C.c_int, _f32p, _sz, _f32p]
+        L.orc_gguf_block.argtypes = [C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.orc_gguf_dequant.argtypes = [_u8p, C.c_int, _sz, _f32p]
+        L.orc_gguf_linear.argtypes = [_u8p, C.c_int, _sz, _sz, _f32p, _sz, _f32p]
         L.orc_mha_causal.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz]
         L.orc_attn_decode.argtypes = [_f32p, _u16p, _u16p, C.c_void_p, _sz, _sz, _sz, _sz,
                                       _sz, C.c_float, _f32p]
@@ -228,6 +231,40 @@ def q4k_linear(w, R: int, Cc: int, x: np.ndarray, order: int = ORC_Q4K_GGML) -> 
     M = x.shape[0] if x.ndim == 2 else 1
     y = np.zeros(M * R, np.float32)
     _check(orc().orc_q4k_linear(b, R, Cc, order, x.ravel(), M, y), "q4k_linear")
+    return y.reshape(M, R)
+
+
+# engine GGUF formats (ids = ggml type numbers; include/cortexsdr_hip.h CSDR_GGUF_*)
+GGUF_FORMATS = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "q8_1": 9, "q2_k": 10,
+                "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14, "q8_k": 15, "iq2_xxs": 16,
+                "iq2_xs": 17, "iq3_xxs": 18, "iq1_s": 19, "iq4_nl": 20, "iq3_s": 21,
+                "iq2_s": 22, "iq4_xs": 23, "iq1_m": 29, "q4_0_4_4": 31, "q4_0_4_8": 32,
+                "q4_0_8_8": 33, "tq1_0": 34, "tq2_0": 35}
+
+
+def gguf_block(fmt: int):
+    """(bytes, elements) per block."""
+    bb, be = C.c_int(0), C.c_int(0)
+    _check(orc().orc_gguf_block(fmt, C.byref(bb), C.byref(be)), "gguf_block")
+    return bb.value, be.value
+
+
+def gguf_dequant(blocks, fmt: int) -> np.ndarray:
+    b = _u8(blocks)
+    bb, be = gguf_block(fmt)
+    nb = b.size // bb
+    out = np.empty(nb * be, np.float32)
+    _check(orc().orc_gguf_dequant(b, fmt, nb, out), "gguf_dequant")
+    return out
+
+
+def gguf_linear(w, fmt: int, R: int, Cc: int, x: np.ndarray) -> np.ndarray:
+    """y (M, R) = x (M, C) . dequant(W)^T."""
+    b = _u8(w)
+    x = np.ascontiguousarray(x, np.float32)
+    M = x.shape[0] if x.ndim == 2 else 1
+    y = np.zeros(M * R, np.float32)
+    _check(orc().orc_gguf_linear(b, fmt, R, Cc, x.ravel(), M, y), "gguf_linear")
     return y.reshape(M, R)
 
 

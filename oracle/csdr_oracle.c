@@ -447,6 +447,168 @@ int orc_q4k_linear(const uint8_t* w, size_t R, size_t C, int order, const float*
     return ORC_OK;
 }
 
+/* --------------------------------------------------------------- engine GGUF formats */
+
+/* decodeSupportedGGUFQuantized (SparseInferenceEngine.cpp:276-469) with the block sizes of
+ * ggufBlockBytesForFormat / ggufBlockElementsForFormat / ggufQuantBitsForFormat (:181-252).
+ * Format ids are ggml's type numbers (as include/cortexsdr_hip.h CSDR_GGUF_*). bits > 0 marks
+ * a format decoded by the reference's generic rule (:439-465). */
+static int gguf_table(int fmt, int* bb, int* be, int* bits) {
+    static const int T[][4] = {
+        {2, 18, 32, 0},    {3, 20, 32, 0},    {6, 22, 32, 0},    {7, 24, 32, 0},
+        {8, 34, 32, 0},    {9, 40, 32, 0},    {10, 84, 256, 2},  {11, 110, 256, 3},
+        {12, 144, 256, 0}, {13, 176, 256, 5}, {14, 210, 256, 0}, {15, 292, 256, 0},
+        {16, 66, 256, 2},  {17, 74, 256, 2},  {18, 98, 256, 3},  {19, 50, 256, 1},
+        {20, 18, 32, 4},   {21, 110, 256, 3}, {22, 82, 256, 2},  {23, 136, 256, 4},
+        {29, 56, 256, 1},  {31, 72, 128, 4},  {32, 144, 256, 4}, {33, 144, 256, 4},
+        {34, 54, 256, 1},  {35, 66, 256, 2}};
+    for (size_t i = 0; i < sizeof(T) / sizeof(T[0]); ++i)
+        if (T[i][0] == fmt) {
+            *bb = T[i][1];
+            *be = T[i][2];
+            *bits = T[i][3];
+            return 0;
+        }
+    return -1;
+}
+
+int orc_gguf_block(int fmt, int* block_bytes, int* block_elems) {
+    int bits;
+    return gguf_table(fmt, block_bytes, block_elems, &bits) ? ORC_E_GEOMETRY : ORC_OK;
+}
+
+static uint32_t packed_bits_lsb(const uint8_t* bytes, size_t bit_offset, size_t count) {
+    /* readPackedBitsLSB, SparseInferenceEngine.cpp:254-264 */
+    uint32_t v = 0;
+    for (size_t b = 0; b < count; ++b) {
+        const size_t a = bit_offset + b;
+        v |= (uint32_t)((bytes[a / 8] >> (a % 8)) & 1u) << b;
+    }
+    return v;
+}
+
+int orc_gguf_dequant(const uint8_t* blocks, int fmt, size_t n_blocks, float* out) {
+    int bb, be, bits;
+    if (gguf_table(fmt, &bb, &be, &bits)) return ORC_E_GEOMETRY;
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* p = blocks + b * (size_t)bb;
+        float* o = out + b * (size_t)be;
+        if (bits) { /* :439-465 */
+            const size_t packed = ((size_t)be * bits + 7) / 8;
+            const uint8_t* data = p + (bb - packed);
+            float d = orc_f16_to_f32(rd16(p));
+            if (!isfinite(d) || fabsf(d) < 1e-12f) d = 1.0f;
+            const int32_t centre = (int32_t)(1u << (bits - 1));
+            for (int i = 0; i < be; ++i)
+                o[i] = (float)((int32_t)packed_bits_lsb(data, (size_t)i * bits, bits) - centre) * d;
+            continue;
+        }
+        switch (fmt) {
+            case 8: { /* q8_0, :310-316 */
+                const float d = orc_f16_to_f32(rd16(p));
+                for (int i = 0; i < 32; ++i) o[i] = (float)(int8_t)p[2 + i] * d;
+                break;
+            }
+            case 9: { /* q8_1, :319-326: the scale read as fp32 */
+                float d;
+                memcpy(&d, p, 4);
+                for (int i = 0; i < 32; ++i) o[i] = (float)(int8_t)p[8 + i] * d;
+                break;
+            }
+            case 14: { /* q6_k, :329-359 */
+                const uint8_t* ql = p;
+                const uint8_t* qh = p + 128;
+                const int8_t* sc = (const int8_t*)(p + 192);
+                const float d = orc_f16_to_f32(rd16(p + 208));
+                int k = 0;
+                for (int half = 0; half < 2; ++half) {
+                    const uint8_t* qlh = ql + half * 64;
+                    const uint8_t* qhh = qh + half * 32;
+                    const int8_t* sh = sc + half * 8;
+                    for (int l = 0; l < 32; ++l)
+                        o[k++] = d * (float)(sh[0] * ((int)((qlh[l] & 0x0F) | (((qhh[l] >> 0) & 3) << 4)) - 32));
+                    for (int l = 0; l < 32; ++l)
+                        o[k++] = d * (float)(sh[2] * ((int)((qlh[l + 32] & 0x0F) | (((qhh[l] >> 2) & 3) << 4)) - 32));
+                    for (int l = 0; l < 32; ++l)
+                        o[k++] = d * (float)(sh[4] * ((int)(((qlh[l] >> 4) & 0x0F) | (((qhh[l] >> 4) & 3) << 4)) - 32));
+                    for (int l = 0; l < 32; ++l)
+                        o[k++] = d * (float)(sh[6] * ((int)(((qlh[l + 32] >> 4) & 0x0F) | (((qhh[l] >> 6) & 3) << 4)) - 32));
+                }
+                break;
+            }
+            case 12: /* q4_k, :362-384 (ggml order) */
+                orc_q4k_dequant(p, 1, ORC_Q4K_GGML, o);
+                break;
+            case 15: { /* q8_k, :387-395: fp16 scale, quants at byte 4 */
+                const float d = orc_f16_to_f32(rd16(p));
+                for (int i = 0; i < 256; ++i) o[i] = (float)(int8_t)p[4 + i] * d;
+                break;
+            }
+            case 2: { /* q4_0, :398-406 */
+                const float d = orc_f16_to_f32(rd16(p));
+                for (int i = 0; i < 32; ++i) {
+                    const uint8_t nb = (i & 1) == 0 ? (p[2 + i / 2] & 0x0F) : (p[2 + i / 2] >> 4);
+                    o[i] = ((float)nb - 8.0f) * d;
+                }
+                break;
+            }
+            case 3: { /* q4_1, :408-417 (x * d + m as one fused multiply-add) */
+                const float d = orc_f16_to_f32(rd16(p)), m = orc_f16_to_f32(rd16(p + 2));
+                for (int i = 0; i < 32; ++i) {
+                    const uint8_t nb = (i & 1) == 0 ? (p[4 + i / 2] & 0x0F) : (p[4 + i / 2] >> 4);
+                    o[i] = fmaf((float)nb, d, m);
+                }
+                break;
+            }
+            case 6:
+            case 7: { /* q5_0 / q5_1, :419-436 */
+                const int has_m = fmt == 7;
+                const float d = orc_f16_to_f32(rd16(p));
+                const float m = has_m ? orc_f16_to_f32(rd16(p + 2)) : 0.0f;
+                const uint8_t* qh = p + (has_m ? 4 : 2);
+                const uint8_t* qs = p + (has_m ? 8 : 6);
+                const uint32_t hb = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) |
+                                    ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+                for (int i = 0; i < 32; ++i) {
+                    uint8_t q = (i & 1) == 0 ? (qs[i / 2] & 0x0F) : (qs[i / 2] >> 4);
+                    q |= (uint8_t)(((hb >> i) & 1u) << 4);
+                    o[i] = has_m ? fmaf((float)q, d, m) : ((float)q - 16.0f) * d;
+                }
+                break;
+            }
+            default:
+                return ORC_E_GEOMETRY;
+        }
+    }
+    return ORC_OK;
+}
+
+int orc_gguf_linear(const uint8_t* w, int fmt, size_t R, size_t C, const float* x, size_t M,
+                    float* y) {
+    int bb, be, bits;
+    if (gguf_table(fmt, &bb, &be, &bits) || C % (size_t)be) return ORC_E_GEOMETRY;
+    const size_t nb = C / (size_t)be;
+    /* decode, then out[m, r] = sum_c in[m, c] * W[r, c] (blas_kernels.cpp:264-293) */
+    int rc = ORC_OK;
+#pragma omp parallel
+    {
+        float* row = (float*)malloc(C * 4);
+#pragma omp for schedule(static)
+        for (long long rr = 0; rr < (long long)R; ++rr) {
+            const size_t r = (size_t)rr;
+            if (orc_gguf_dequant(w + r * nb * (size_t)bb, fmt, nb, row)) rc = ORC_E_GEOMETRY;
+            for (size_t m = 0; m < M; ++m) {
+                float acc = 0.0f;
+                const float* xm = x + m * C;
+                for (size_t c = 0; c < C; ++c) acc = fmaf(xm[c], row[c], acc);
+                y[m * R + r] = acc;
+            }
+        }
+        free(row);
+    }
+    return rc;
+}
+
 /* --------------------------------------------------------------- attention */
 
 static void softmax_row(float* s, size_t n) {

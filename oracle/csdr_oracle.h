@@ -98,6 +98,12 @@ void orc_q6k_dequant(const uint8_t* blocks, size_t n_blocks, float* out);
 /* Q4_K linear: y (M x R) = x (M x C) . dequant(W)^T, W = R rows of C/256 super-blocks
  * (GGUF row-major). Dequant then linear_forward semantics (blas_kernels.cpp:264-293,
  * BLAS-less row loop :101-143), fp32 accumulation in column order. */
+/* Engine GGUF formats (ids = ggml type numbers, include/cortexsdr_hip.h CSDR_GGUF_*):
+ * decodeSupportedGGUFQuantized (SparseInferenceEngine.cpp:276-469), then linear_forward. */
+int orc_gguf_block(int fmt, int* block_bytes, int* block_elems);
+int orc_gguf_dequant(const uint8_t* blocks, int fmt, size_t n_blocks, float* out);
+int orc_gguf_linear(const uint8_t* w, int fmt, size_t R, size_t C, const float* x, size_t M,
+                    float* y);
 int orc_q4k_linear(const uint8_t* w, size_t R, size_t C, int order, const float* x,
                    size_t M, float* y);
 

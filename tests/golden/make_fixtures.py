@@ -21,7 +21,12 @@ and tests/golden/hsda_fixtures.npz (`hsda` argument):
                  block tensors; hsda_x (64 x 3); per segment i: hsda_name_i, hsda_w_i
                  (HSDAReader::decompress), hsda_y_i (HSDAReader::matmul)
 
-Usage: python tests/golden/make_fixtures.py [hsda]
+and, added to ref_fixtures.npz without touching its other arrays (`gguf` argument):
+
+  q40/q80_*  random Q4_0 / Q8_0 blocks through dequantizeToFP32 (the compress side's decode,
+             which equals the engine's decodeSupportedGGUFQuantized for these two formats)
+
+Usage: python tests/golden/make_fixtures.py [hsda | gguf]
 """
 from __future__ import annotations
 
@@ -95,6 +100,26 @@ def main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def gguf_main() -> None:
+    oracle.build(ref=True)
+    if oracle.ref() is None:
+        raise SystemExit("oracle/_ref/libcsdr_ref.so is missing: run make -C oracle ref")
+    path = os.path.join(HERE, "ref_fixtures.npz")
+    with np.load(path) as z:
+        out = {k: z[k] for k in z.files}
+    rng = np.random.default_rng(20261203)
+    for name, nbytes in (("q4_0", 18), ("q8_0", 34)):
+        blocks = rng.integers(0, 256, (40, nbytes), dtype=np.uint8)
+        for i in range(40):  # finite, modest fp16 scales
+            v = np.float16(rng.uniform(0.001, 0.05) * rng.choice([-1, 1])).view(np.uint16)
+            blocks[i, 0:2] = np.array([v], "<u2").view(np.uint8)
+        key = name.replace("_", "")
+        out[f"{key}_blocks"] = blocks
+        out[f"{key}_ref"] = oracle.ref_dequant(blocks.ravel(), name, 5, 256)
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
 def hsda_main() -> None:
     oracle.build(ref=True)
     if oracle.ref() is None:
@@ -119,5 +144,7 @@ def hsda_main() -> None:
 if __name__ == "__main__":
     if sys.argv[1:] == ["hsda"]:
         hsda_main()
+    elif sys.argv[1:] == ["gguf"]:
+        gguf_main()
     else:
         main()

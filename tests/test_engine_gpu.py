@@ -1,5 +1,6 @@
 """GPU parity of the SDK surface: cortex_inference_engine_* over .sdr archives (run_layer
-routing for strategy-5 HSDR/HSDB, uncoded fp32 and q4_k segments; memory options;
+routing for strategy-5 HSDR/HSDB, uncoded fp32, q4_k and the other GGUF block segments;
+memory options;
 generate_text through the native decoder), HSDA/HSDC loads, against the CPU oracle and the
 reference's own fixtures."""
 import os
@@ -21,6 +22,23 @@ def q4k_entry(name, R, Cc, seed):
                             original_size=R * Cc * 4, dims=(R, Cc)), blob
 
 
+def gguf_entry(name, fmt, R, Cc, seed):
+    """Random blocks of a GGUF format with finite fp16 scales (q6_k's at byte 208)."""
+    rng = np.random.default_rng(seed)
+    bb, be = oracle.gguf_block(oracle.GGUF_FORMATS[fmt.lower()])
+    b = rng.integers(0, 256, (R * Cc // be, bb), dtype=np.uint8)
+    off = 208 if fmt.lower() == "q6_k" else 0
+    b[:, off:off + 2] = rng.uniform(0.002, 0.03, b.shape[0]).astype(np.float16).view(
+        np.uint8).reshape(-1, 2)
+    blob = b.tobytes()
+    return formats.SdrEntry(name=name, payload=blob, data_format=fmt, original_type=3,
+                            original_size=R * Cc * 4, dims=(R, Cc)), blob
+
+
+GGUF_ENTRIES = [("blk.0.attn_v.weight", "q6_k", 6, 512), ("blk.0.ffn_gate.weight", "q8_0", 9, 96),
+                ("blk.0.attn_k.weight", "q5_k", 4, 256), ("blk.0.ffn_up.weight", "Q4_0", 5, 64)]
+
+
 @pytest.fixture(scope="module")
 def model(tmp_path_factory, golden):
     path = str(tmp_path_factory.mktemp("sdr") / "model.sdr")
@@ -37,8 +55,13 @@ def model(tmp_path_factory, golden):
         q4e,
         formats.SdrEntry(name="rle.weight", payload=b"\x00" * 16, strategy_id=2, dims=(2, 2)),
     ]
+    gg = {}
+    for i, (name, fmt, R, Cc) in enumerate(GGUF_ENTRIES):
+        e, blob = gguf_entry(name, fmt, R, Cc, 20 + i)
+        ents.append(e)
+        gg[name] = blob
     formats.write_sdr(path, ents)
-    return dict(path=path, hsdb=hsdb, hsdb_edge=hsdb_edge, dense=dense, q4=q4blob)
+    return dict(path=path, hsdb=hsdb, hsdb_edge=hsdb_edge, dense=dense, q4=q4blob, gguf=gg)
 
 
 def test_run_layer_routes(gpu, model, golden):
@@ -63,6 +86,22 @@ def test_run_layer_routes(gpu, model, golden):
         ref = oracle.q4k_linear(model["q4"], 8, 512, xq.T.copy())
         assert rel_l2(Y, ref) < 1e-5
         assert eng.memory_usage() > 0
+    finally:
+        eng.close()
+
+
+def test_run_layer_gguf_formats(gpu, model):
+    """Strategy-0 tensors in the other GGUF block formats route to csdr_gguf_linear with the
+    reference engine's decode (its data_format names, any case)."""
+    eng = InferenceEngine(model["path"])
+    try:
+        for name, fmt, R, Cc in GGUF_ENTRIES:
+            x = np.random.default_rng(R).normal(size=(2, Cc)).astype(np.float32)
+            Y = eng.run_layer(name, x).reshape(2, R)
+            ref = oracle.gguf_linear(model["gguf"][name], oracle.GGUF_FORMATS[fmt.lower()], R,
+                                     Cc, x)
+            assert rel_l2(Y, ref) < 1e-5, fmt
+            assert eng.stats()["path"] == "gguf"
     finally:
         eng.close()
 
