@@ -108,6 +108,44 @@ def bench_q4k(torch, R, Cc, M, steps, order=0):
             "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
 
 
+def gguf_matrix(fmt: int, R: int, Cc: int, seed: int) -> bytes:
+    """Random blocks of a GGUF format with fp16 scales ~U(0.001, 0.05) (q6_k's at byte 208,
+    q8_1's fp32), like synth.q4k_matrix for Q4_K."""
+    from . import gguf
+
+    bb, be = gguf.block(fmt)
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (R * Cc // be, bb), dtype=np.uint8)
+    off = 208 if fmt == 14 else 0
+    b[:, off:off + 2] = rng.uniform(0.001, 0.05, b.shape[0]).astype(np.float16).view(
+        np.uint8).reshape(-1, 2)
+    return b.tobytes()
+
+
+def bench_gguf(torch, fmt_name, R, Cc, M, steps):
+    """The engine's other GGUF formats at cfg3's shapes (csdr_gguf_linear)."""
+    from . import _lib, gguf
+
+    fmt = gguf.format_id(fmt_name)
+    blob = gguf_matrix(fmt, R, Cc, seed=7)
+    ncp = _copies(len(blob))
+    ws = [gguf.upload(blob) for _ in range(ncp)]
+    x = torch.from_numpy(synth.activations(Cc, M, seed=11).T.copy().astype(np.float16)).cuda()
+    y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    lib = _lib.load()
+
+    def fn(i):
+        sp = int(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.csdr_gguf_linear(ws[i].data_ptr(), fmt, R, Cc, x.data_ptr(), 1, M,
+                                        y.data_ptr(), sp))
+
+    us = time_graph(torch, fn, ncp, steps)
+    alg = len(blob) + Cc * M * 2 + R * M * 4
+    return {"format": fmt_name, "R": R, "C": Cc, "M": M, "us": round(us, 3),
+            "GBps": round(alg / us / 1e3, 1), "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4),
+            "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
+
+
 def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
     """Config 4: Qwen2-0.5B-shaped decoder, all linears HSDB-coded (1024 x 64 shared
     dictionary, 8 nnz per block), prompt of uniform random ids, greedy (plain argmax)."""
@@ -299,6 +337,14 @@ def main(argv=None) -> int:
                 out.append(bench_q4k(torch, R, Cc, M, args.steps))
                 print(json.dumps(out[-1]), flush=True)
         res["results"]["cfg3"] = out
+    if "gguf" in cfgs:  # the engine's other block formats at cfg3's shapes
+        out = []
+        for fmt in ("q6_k", "q8_0", "q4_0", "q5_k"):
+            for (R, Cc) in ((4096, 4096), (4096, 14336)):
+                for M in (1, 32):
+                    out.append(bench_gguf(torch, fmt, R, Cc, M, args.steps))
+                    print(json.dumps(out[-1]), flush=True)
+        res["results"]["gguf"] = out
     if "cfg5" in cfgs:
         res["results"]["cfg5"] = bench_decoder_7b(torch)
         print(json.dumps(res["results"]["cfg5"]), flush=True)

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -51,6 +52,13 @@ constexpr int kCachePolicyNT = 2;  // buffer load cache policy: nontemporal (str
 
 // Launch-shape defaults, overridable for tuning sweeps through the environment
 // (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_CHUNK_BYTES).
+// A switch from the environment: "0" is off, any other value on, unset is dflt.
+bool env_flag(const char* name, bool dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return v[0] != '0';
+}
+
 int env_int(const char* name, int dflt) {
     const char* v = std::getenv(name);
     if (!v || !*v) return dflt;
@@ -936,6 +944,99 @@ int grid_for(size_t work) {
     return (int)std::max<size_t>(1, std::min<size_t>(g, 65536));
 }
 
+// ---- device dictionaries shared between segments
+// Segments on one device whose dictionaries have the same bytes and tile shape share one
+// device copy (fp32, and the fp16 matrix-core copy for 64-wide 1-row tiles), as the
+// reference's shared-dictionary archive (HSDA) shares one dictionary among many code streams
+// (HierarchicalSDRStrategy.cpp:1904-2081). Reference counted; CSDR_HSDB_SHARE_DICT=0 gives
+// every segment its own copy.
+struct DictEntry {
+    int device = 0;
+    uint32_t tile_rows = 0, tile_cols = 0, K = 0;
+    std::vector<uint8_t> bytes;
+    float* d32 = nullptr;
+    _Float16* d16p = nullptr;
+    size_t dev_bytes = 0;
+    int refs = 0;
+};
+std::mutex g_dict_mu;
+std::vector<DictEntry*> g_dicts;
+
+int acquire_dict(csdr_hsdb* s, const uint8_t* dict, size_t b_dict, hipStream_t st) {
+    const bool share = env_flag("CSDR_HSDB_SHARE_DICT", true);
+    const bool want16 = s->tile_rows == 1 && s->tile_cols == 64;
+    std::lock_guard<std::mutex> lock(g_dict_mu);
+    if (share) {
+        for (DictEntry* e : g_dicts) {
+            if (e->device == s->device && e->tile_rows == s->tile_rows &&
+                e->tile_cols == s->tile_cols && e->K == s->K && e->bytes.size() == b_dict &&
+                std::memcmp(e->bytes.data(), dict, b_dict) == 0) {
+                ++e->refs;
+                s->dict_ref = e;
+                s->d_dict = e->d32;
+                s->d_dict16p = e->d16p;
+                s->device_bytes += e->dev_bytes;
+                return CSDR_OK;
+            }
+        }
+    }
+    auto* e = new DictEntry;
+    e->device = s->device;
+    e->tile_rows = s->tile_rows;
+    e->tile_cols = s->tile_cols;
+    e->K = s->K;
+    e->bytes.assign(dict, dict + b_dict);
+    e->refs = 1;
+    auto fail = [&](hipError_t err) {
+        if (e->d32) (void)hipFree(e->d32);
+        if (e->d16p) (void)hipFree(e->d16p);
+        delete e;
+        return set_error(CSDR_E_HIP, std::string("hsdb_load: ") + hipGetErrorString(err));
+    };
+    hipError_t err = hipMalloc(&e->d32, std::max<size_t>(b_dict, 4));
+    if (err != hipSuccess) return fail(err);
+    err = hipMemcpyAsync(e->d32, dict, b_dict, hipMemcpyHostToDevice, st);
+    if (err != hipSuccess) return fail(err);
+    e->dev_bytes = b_dict;
+    if (want16) {
+        // the fp16 copy (round to nearest even), each 64-row in the matrix-core k order
+        // (csdr::kperm64), for the batched product
+        const size_t n = (size_t)s->K * 64;
+        std::vector<_Float16> dict16(n);
+        std::vector<float> d32(n);
+        std::memcpy(d32.data(), dict, n * 4);
+        for (size_t i = 0; i < n; ++i)
+            dict16[(i & ~(size_t)63) + csdr::kperm64((int)(i & 63))] = (_Float16)d32[i];
+        err = hipMalloc(&e->d16p, n * 2);
+        if (err != hipSuccess) return fail(err);
+        err = hipMemcpyAsync(e->d16p, dict16.data(), n * 2, hipMemcpyHostToDevice, st);
+        if (err == hipSuccess) err = hipStreamSynchronize(st);  // dict16 dies with this call
+        if (err != hipSuccess) return fail(err);
+        e->dev_bytes += n * 2;
+    }
+    s->dict_ref = e;
+    s->d_dict = e->d32;
+    s->d_dict16p = e->d16p;
+    s->device_bytes += e->dev_bytes;
+    if (share) g_dicts.push_back(e);
+    return CSDR_OK;
+}
+
+void release_dict(csdr_hsdb* s) {
+    auto* e = static_cast<DictEntry*>(s->dict_ref);
+    if (!e) return;
+    std::lock_guard<std::mutex> lock(g_dict_mu);
+    if (--e->refs == 0) {
+        (void)hipFree(e->d32);
+        if (e->d16p) (void)hipFree(e->d16p);
+        g_dicts.erase(std::remove(g_dicts.begin(), g_dicts.end(), e), g_dicts.end());
+        delete e;
+    }
+    s->dict_ref = nullptr;
+    s->d_dict = nullptr;
+    s->d_dict16p = nullptr;
+}
+
 // Stream parse with the reference's checks (HierarchicalSDRStrategy.cpp:1265-1290 and
 // readBuffer's truncation check) plus index < n_atoms.
 int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s) {
@@ -1031,27 +1132,14 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
     const size_t b_codes = n_codes * 4;
     const size_t b_gamma = slot_gamma.size() * 4;
     const size_t b_edge = edge_bytes;
-    CSDR_HIP_CHECK(hipMalloc(&s->d_dict, std::max<size_t>(b_dict, 4)));
+    {
+        const int rc = acquire_dict(s, buf + off_dict, b_dict, st);
+        if (rc) return rc;
+    }
     CSDR_HIP_CHECK(hipMalloc(&s->d_codes, std::max<size_t>(b_codes, 4)));
     CSDR_HIP_CHECK(hipMalloc(&s->d_slot_gamma, b_gamma));
     CSDR_HIP_CHECK(hipMalloc(&s->d_edge, std::max<size_t>(b_edge, 4)));
-    s->device_bytes = b_dict + b_codes + b_gamma + b_edge;
-    CSDR_HIP_CHECK(hipMemcpyAsync(s->d_dict, buf + off_dict, b_dict, hipMemcpyHostToDevice, st));
-    // 64-wide blocks: the dictionary also as fp16 (round to nearest even), each 64-row in
-    // the matrix-core k order (csdr::kperm64), for the batched product
-    std::vector<_Float16> dict16;
-    if (s->tile_rows == 1 && s->tile_cols == 64) {
-        const size_t n = (size_t)s->K * 64;
-        dict16.resize(n);
-        std::vector<float> d32(n);
-        std::memcpy(d32.data(), buf + off_dict, n * 4);
-        for (size_t i = 0; i < n; ++i)
-            dict16[(i & ~(size_t)63) + csdr::kperm64((int)(i & 63))] = (_Float16)d32[i];
-        CSDR_HIP_CHECK(hipMalloc(&s->d_dict16p, n * 2));
-        s->device_bytes += n * 2;
-        CSDR_HIP_CHECK(
-            hipMemcpyAsync(s->d_dict16p, dict16.data(), n * 2, hipMemcpyHostToDevice, st));
-    }
+    s->device_bytes += b_codes + b_gamma + b_edge;
     if (b_codes)
         CSDR_HIP_CHECK(
             hipMemcpyAsync(s->d_codes, words.data(), b_codes, hipMemcpyHostToDevice, st));
@@ -1066,8 +1154,7 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
 
 void release(csdr_hsdb* s) {
     if (!s) return;
-    if (s->d_dict) (void)hipFree(s->d_dict);
-    if (s->d_dict16p) (void)hipFree(s->d_dict16p);
+    release_dict(s);
     if (s->d_codes) (void)hipFree(s->d_codes);
     if (s->d_slot_gamma) (void)hipFree(s->d_slot_gamma);
     if (s->d_edge) (void)hipFree(s->d_edge);

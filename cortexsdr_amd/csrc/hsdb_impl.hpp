@@ -15,13 +15,16 @@ struct csdr_hsdb {
     uint32_t NBc = 1, nchunks = 1;
     int is_hsdb = 0;
     int device = 0;
-    float* d_dict = nullptr;        // K x tile_dim fp32
+    float* d_dict = nullptr;        // K x tile_dim fp32 (shared, see dict_ref)
     _Float16* d_dict16p = nullptr;  // 64-wide blocks: K x 64 fp16, rows in kperm64 order
     uint32_t* d_codes = nullptr;    // n_tiles * slots words
     float* d_slot_gamma = nullptr;  // slots floats: gamma[j / k]
     float* d_edge = nullptr;        // top-right strip (R_full x Ce) then bottom strip
     float h_slot_gamma[32] = {};    // host copy of the first 32 slot gammas (kernel args)
     size_t edge_floats = 0;
+    // the device dictionary (d_dict, d_dict16p) is held through a reference-counted entry
+    // shared by every segment on the device with the same dictionary bytes and tile shape
+    void* dict_ref = nullptr;
     size_t device_bytes = 0;
 };
 

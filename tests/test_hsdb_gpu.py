@@ -173,3 +173,33 @@ def test_errors_are_reported(gpu, golden):
     with pytest.raises(CompressionError) as e:
         seg2d.matmul(x)
     assert e.value.code == -2
+
+
+@pytest.mark.parametrize("share", ["1", "0"])
+def test_shared_dictionary_lifetime(gpu, monkeypatch, share):
+    """Segments with the same dictionary bytes share one device copy (CSDR_HSDB_SHARE_DICT,
+    default on): a segment keeps working after another user of its dictionary is freed, and
+    segments with another dictionary are unaffected (M = 1 fp32 path and the fp16 batched
+    path, which reads the fp16 copy)."""
+    from cortexsdr_amd.hsdr import HsdbSegment
+
+    monkeypatch.setenv("CSDR_HSDB_SHARE_DICT", share)
+    st = {k: synth.hsdb_layer(96, 256, 64, 8, seed_dict=sd, seed_codes=sc)
+          for k, (sd, sc) in {"a": (1, 2), "b": (1, 3), "c": (4, 5), "d": (1, 6)}.items()}
+    segs = {k: HsdbSegment(v) for k, v in st.items() if k != "d"}
+
+    def check(k, seg):
+        for M in (1, 16):
+            x = synth.activations(256, M, seed=ord(k) + M)
+            y = seg.matmul(gpu.from_numpy(x).cuda()).cpu().numpy()
+            assert rel_l2(y, oracle.hsdb_matmul(st[k], x)) < 1e-3, (k, M)
+
+    segs["a"].free()
+    check("b", segs["b"])
+    check("c", segs["c"])
+    segs["d"] = HsdbSegment(st["d"])
+    segs["b"].free()
+    check("d", segs["d"])
+    check("c", segs["c"])
+    segs["d"].free()
+    segs["c"].free()
