@@ -259,10 +259,12 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
         qs[g * HD + i2] = x0;
         qs[g * HD + i2 + 1] = x1;
     }
+    // (with ROPE the row of position L - 1 is written below, from the new key and value, and
+    // by no other thread: the cache row there is not written yet)
 #pragma unroll
     for (int k = 0; k < kPPT; ++k) {
         const int idx = tid + k * kThreads, p = idx / PPR, j = idx - p * PPR;
-        if (p < n) {
+        if (p < n && !(ROPE && p0 + p == plast)) {
             *reinterpret_cast<h8*>(tk + (size_t)p * HDP + j * 8) = kr[k];
             *reinterpret_cast<h8*>(tv + (size_t)p * HDP + j * 8) = vr[k];
         }
@@ -579,6 +581,265 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     }
 }
 
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Grouped-query decode attention on the matrix cores, for 2..16 query heads per KV head: one
+// workgroup of 16 waves per (batch entry, KV head, split of up to 256 positions). The splits
+// spread the K/V reads over many CUs: one workgroup per KV head holding 640 positions (cfg4)
+// measured 13.9 us against 5.9 us for 128-position splits, its loads limited by what one CU
+// keeps in flight.
+//  * loads: each wave's K rows go straight from memory into v_mfma_f32_16x16x16f16 B operands
+//    (lane: position tile * 16 + lane % 16, dims [lane / 16 * HD / 4, + HD / 4); the
+//    contraction runs over the dims in that order and the query operand is read in the same
+//    order); V rows are staged in LDS; every load is issued before the first wait;
+//  * scores (q * scale) K^T: q rotated (ROPE) and scaled in fp32, then split into fp16 hi + lo
+//    (two MFMAs per 16 dims, fp32 accumulate: the fp32 product to about 2^-22);
+//  * softmax per head, one wave per head, in LDS;
+//  * O = P V: P split into hi + lo, V read from LDS four positions per lane; the 16 waves are
+//    (HD / 16 dim tiles) x (position groups), and the groups are summed through LDS.
+constexpr int kMW = 16;  // waves per workgroup
+constexpr int kMThreads = kMW * 64;
+constexpr int kAttnMfmaMaxG = 16;  // query heads per KV head: the rows of one MFMA tile
+
+constexpr size_t attn_mfma_lds_bytes(int HD, int G, int S) {
+    return (size_t)S * (HD + 8) * 2 + (size_t)2 * 16 * HD * 2 + (size_t)HD * 2 +
+           (size_t)G * S * 4 + 16 * 2 * 4 + (size_t)(kMW / (HD / 16) - 1) * (HD / 16) * 64 * 16;
+}
+
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(kMThreads) void attn_mfma_kernel(
+    const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
+    const int* __restrict__ lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
+    float* __restrict__ part, float* __restrict__ out, int nsplit, RopeArgs ra) {
+    constexpr int SMAX = kAttnMaxS;
+    constexpr int HDP = HD + 8;                      // padded V row, halves
+    constexpr int NDT = HD / 16;                     // 16-dim output tiles
+    constexpr int NPG = kMW / NDT;                   // position groups of P.V
+    constexpr int DPL = HD / 4;                      // dims per lane group in the score operands
+    constexpr int KPL = DPL / 8;                     // 16-byte K pieces per lane and tile
+    constexpr int TW = (SMAX / 16 + kMW - 1) / kMW;  // position tiles per wave, at most
+    constexpr int PPR = HD / 8;                      // 16-byte pieces per row
+    constexpr int VPT = SMAX * PPR / kMThreads;      // V pieces per thread, at most
+    static_assert(VPT * kMThreads == SMAX * PPR, "V pieces must divide evenly");
+    extern __shared__ float smem[];
+    const int G = Hq / Hkv;
+    const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv, s = blockIdx.y;
+    const int h0 = kvh * G;
+    const int L = lens ? lens[b] : len_host;
+    const int p0 = s * S, p1 = min(L, p0 + S);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const bool direct = (nsplit == 1 && out != nullptr);
+    if (p0 >= p1) {  // empty split (the length is below this split's range)
+        for (int e = tid; e < G * HD; e += kMThreads) {
+            const int g = e / HD, d = e - g * HD;
+            const int bh = b * Hq + h0 + g;
+            if (direct) {
+                out[(size_t)bh * HD + d] = 0.f;
+            } else {
+                float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+                pp[2 + d] = 0.f;
+                if (d == 0) {
+                    pp[0] = -INFINITY;
+                    pp[1] = 0.f;
+                }
+            }
+        }
+        return;
+    }
+    const int n = p1 - p0, n16 = (n + 15) & ~15;
+    const int plast = L - 1;
+    const size_t rstride = (size_t)Hkv * HD;
+    const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD;
+    const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD;
+    _Float16* tv = reinterpret_cast<_Float16*>(smem);     // S x HDP
+    _Float16* qh = tv + (size_t)S * HDP;                   // 16 x HD: q hi
+    _Float16* ql = qh + 16 * HD;                           // 16 x HD: q lo
+    _Float16* kn = ql + 16 * HD;                           // HD: the new key (ROPE)
+    float* sc = reinterpret_cast<float*>(kn + HD);         // G x S: scores, then P
+    float* stat = sc + (size_t)G * S;                      // 16 x (max, sum)
+    floatx4* red = reinterpret_cast<floatx4*>(stat + 32);  // (NPG - 1) x NDT x 64
+
+    // 1. loads. Rows past the split's n positions are clamped (their scores are masked).
+    h8 kr[TW][KPL];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tile = wave + t * kMW;
+        if (tile * 16 < n) {
+            const int p = min(tile * 16 + c16, n - 1);
+            const _Float16* src = kb + (size_t)(p0 + p) * rstride + g4 * DPL;
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) kr[t][j] = *reinterpret_cast<const h8*>(src + j * 8);
+        }
+    }
+    h8 vr[VPT];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int idx = tid + k * kMThreads, p = idx / PPR, j = idx - p * PPR;
+        if (p < n) vr[k] = *reinterpret_cast<const h8*>(vb + (size_t)(p0 + p) * rstride + j * 8);
+    }
+    // the query heads, rotated at L - 1 and scaled, as fp16 hi + lo
+    for (int e = tid; e < G * (HD / 2); e += kMThreads) {
+        const int g = e / (HD / 2), i2 = 2 * (e - g * (HD / 2));
+        const float* qp = q + ((size_t)b * Hq + h0 + g) * HD;
+        float x0 = qp[i2], x1 = qp[i2 + 1];
+        if constexpr (ROPE) {
+            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
+            const float ang = (float)plast * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            const float r0 = fmaf(x0, c, -(x1 * sn)), r1 = fmaf(x0, sn, x1 * c);
+            x0 = r0;
+            x1 = r1;
+        }
+        x0 *= scale;
+        x1 *= scale;
+        const _Float16 a0 = (_Float16)x0, a1 = (_Float16)x1;
+        qh[g * HD + i2] = a0;
+        qh[g * HD + i2 + 1] = a1;
+        ql[g * HD + i2] = (_Float16)(x0 - (float)a0);
+        ql[g * HD + i2 + 1] = (_Float16)(x1 - (float)a1);
+    }
+    // V rows into LDS, zeros on [n, n16) (P is zero there; the rows must be finite). With ROPE
+    // the row of position L - 1 is written below, from the new value, and by no other thread.
+    const h8 zero8 = {};
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int idx = tid + k * kMThreads, p = idx / PPR, j = idx - p * PPR;
+        if (p < n16 && !(ROPE && p0 + p == plast))
+            *reinterpret_cast<h8*>(tv + (size_t)p * HDP + j * 8) = p < n ? vr[k] : zero8;
+    }
+    if constexpr (ROPE) {
+        // position L - 1: the new key (rotated) and value, rounded to fp16, into LDS and, from
+        // the split that holds it, appended to the caches
+        if (plast >= p0 && plast < p1 && tid < HD / 2) {
+            const int i2 = 2 * tid;
+            const float* knp = ra.knew + ((size_t)b * Hkv + kvh) * HD;
+            const float* vnp = ra.vnew + ((size_t)b * Hkv + kvh) * HD;
+            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
+            const float ang = (float)plast * freq;
+            const float c = cosf(ang), sn = sinf(ang);
+            const float k0 = knp[i2], k1 = knp[i2 + 1];
+            const _Float16 a0 = (_Float16)fmaf(k0, c, -(k1 * sn));
+            const _Float16 a1 = (_Float16)fmaf(k0, sn, k1 * c);
+            const _Float16 w0 = (_Float16)vnp[i2], w1 = (_Float16)vnp[i2 + 1];
+            const int pr = plast - p0;
+            kn[i2] = a0;
+            kn[i2 + 1] = a1;
+            tv[(size_t)pr * HDP + i2] = w0;
+            tv[(size_t)pr * HDP + i2 + 1] = w1;
+            const size_t at = ((size_t)b * T + plast) * rstride + (size_t)kvh * HD + i2;
+            ra.kcw[at] = a0;
+            ra.kcw[at + 1] = a1;
+            ra.vcw[at] = w0;
+            ra.vcw[at + 1] = w1;
+        }
+    }
+    __syncthreads();
+
+    // 2. scores: wave w takes position tiles w, w + 16, ...; A rows past G repeat head G - 1
+    const int hr = min(c16, G - 1);
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tile = wave + t * kMW;
+        if (tile * 16 >= n) break;
+        const int p = tile * 16 + c16;
+        if constexpr (ROPE) {
+            if (p0 + p == plast) {
+#pragma unroll
+                for (int j = 0; j < KPL; ++j)
+                    kr[t][j] = *reinterpret_cast<const h8*>(kn + g4 * DPL + j * 8);
+            }
+        }
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ++ks) {
+            const h8 kv = kr[t][ks / 2];
+            const half4 bk = (ks & 1) ? __builtin_shufflevector(kv, kv, 4, 5, 6, 7)
+                                      : __builtin_shufflevector(kv, kv, 0, 1, 2, 3);
+            const int qo = hr * HD + g4 * DPL + ks * 4;
+            const half4 ah = *reinterpret_cast<const half4*>(qh + qo);
+            const half4 al = *reinterpret_cast<const half4*>(ql + qo);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bk, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bk, acc, 0, 0, 0);
+        }
+        // lane holds heads 4 (lane / 16) + i at position p
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = g4 * 4 + i;
+            if (h < G) sc[h * S + p] = p < n ? acc[i] : -INFINITY;
+        }
+    }
+    __syncthreads();
+
+    // 3. softmax statistics, wave h for head h; P = exp(s - max) in place, zero on [n, n16)
+    if (wave < G) {
+        float* row = sc + wave * S;
+        float m = -INFINITY;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, row[j]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int j = lane; j < n16; j += 64) {
+            const float e = j < n ? expf(row[j] - m) : 0.f;
+            row[j] = e;
+            l += e;
+        }
+        l = csdr::wave_sum(l);
+        if (lane == 0) {
+            stat[wave * 2] = m;
+            stat[wave * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+
+    // 4. O = P V: wave = (dim tile dt, position group pg), 16 positions per step
+    const int dt = wave % NDT, pg = wave / NDT;
+    floatx4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int kt = pg; kt * 16 < n16; kt += NPG) {
+        const float4 pv = *reinterpret_cast<const float4*>(sc + hr * S + kt * 16 + g4 * 4);
+        half4 ph, pl;
+        ph[0] = (_Float16)pv.x;
+        ph[1] = (_Float16)pv.y;
+        ph[2] = (_Float16)pv.z;
+        ph[3] = (_Float16)pv.w;
+        pl[0] = (_Float16)(pv.x - (float)ph[0]);
+        pl[1] = (_Float16)(pv.y - (float)ph[1]);
+        pl[2] = (_Float16)(pv.z - (float)ph[2]);
+        pl[3] = (_Float16)(pv.w - (float)ph[3]);
+        const _Float16* vp = tv + (size_t)(kt * 16 + g4 * 4) * HDP + dt * 16 + c16;
+        half4 bv;
+        bv[0] = vp[0];
+        bv[1] = vp[HDP];
+        bv[2] = vp[2 * HDP];
+        bv[3] = vp[3 * HDP];
+        o = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bv, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bv, o, 0, 0, 0);
+    }
+    if (pg > 0) red[((pg - 1) * NDT + dt) * 64 + lane] = o;
+    __syncthreads();
+    if (pg == 0) {
+#pragma unroll
+        for (int k = 1; k < NPG; ++k) o += red[((k - 1) * NDT + dt) * 64 + lane];
+        const int d = dt * 16 + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = g4 * 4 + i;
+            if (h >= G) continue;
+            const int bh = b * Hq + h0 + h;
+            if (direct) {
+                out[(size_t)bh * HD + d] = o[i] / stat[h * 2 + 1];
+            } else {
+                float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+                pp[2 + d] = o[i];
+                if (d == 0) {
+                    pp[0] = stat[h * 2];
+                    pp[1] = stat[h * 2 + 1];
+                }
+            }
+        }
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part,
                                                           int nsplit, float* __restrict__ out) {
@@ -704,31 +965,78 @@ int attn_split_len(int B, int Hkv, int zsplit, int T) {
     return S;
 }
 
+// Dynamic LDS above 64 KiB: a kernel's limit is raised once, to its largest shape (one
+// instantiation per kernel: KIND tells the kernels of one HD and ROPE apart).
+template <int KIND, int HD, bool ROPE>
+void raise_lds_once(const void* fn, size_t bytes) {
+    static const bool raised = [&] {
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        return true;
+    }();
+    (void)raised;
+}
+
+// Whether grouped-query shapes take attn_mfma_kernel (CSDR_ATTN_MFMA=0 keeps the VALU kernels).
+bool attn_mfma_enabled() {
+    const char* e = std::getenv("CSDR_ATTN_MFMA");
+    return !(e && e[0] == '0');
+}
+
 template <int HD, bool ROPE>
-void launch_attn(dim3 grid, int G, const float* q, const _Float16* k16, const _Float16* v16,
-                 const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
-                 float* part, float* out, int nsplit, const RopeArgs& ra, hipStream_t st) {
+void launch_attn_mfma(dim3 grid, int G, const float* q, const _Float16* k16, const _Float16* v16,
+                      const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
+                      float* part, float* out, int nsplit, const RopeArgs& ra, hipStream_t st) {
+    raise_lds_once<0, HD, ROPE>(reinterpret_cast<const void*>(&attn_mfma_kernel<HD, ROPE>),
+                   attn_mfma_lds_bytes(HD, kAttnMfmaMaxG, kAttnMaxS));
+    attn_mfma_kernel<HD, ROPE><<<grid, kMThreads, attn_mfma_lds_bytes(HD, G, S), st>>>(
+        q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
+}
+
+template <int HD, bool ROPE>
+void launch_attn(dim3 grid, int G, bool mfma, const float* q, const _Float16* k16,
+                 const _Float16* v16, const int* lens, int len_host, int T, int Hq, int Hkv,
+                 float scale, int S, float* part, float* out, int nsplit, const RopeArgs& ra,
+                 hipStream_t st) {
+    if (mfma) {
+        launch_attn_mfma<HD, ROPE>(grid, G, q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S,
+                                   part, out, nsplit, ra, st);
+        return;
+    }
     // one query head per KV head: the lane-per-position kernel (measured at Llama-7B shape,
     // head_dim 128, 4096 positions: 20.5 vs 29.1 us; its small LDS footprint keeps several
     // workgroups per CU where the staged tile would allow one)
     if (G == 1)
         attn_split_kernel<HD, 1, ROPE><<<grid, kThreads, 0, st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
-    else if (G <= 4)
+    else if (G <= 4) {
+        raise_lds_once<1, HD, ROPE>(reinterpret_cast<const void*>(&attn_lds_kernel<HD, 4, ROPE>),
+                                    attn_lds_bytes(HD, 4, kAttnMaxS));
         attn_lds_kernel<HD, 4, ROPE><<<grid, kThreads, attn_lds_bytes(HD, 4, S), st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
-    else
+    } else {
+        raise_lds_once<2, HD, ROPE>(reinterpret_cast<const void*>(&attn_lds_kernel<HD, 8, ROPE>),
+                                    attn_lds_bytes(HD, 8, kAttnMaxS));
         attn_lds_kernel<HD, 8, ROPE><<<grid, kThreads, attn_lds_bytes(HD, 8, S), st>>>(
             q, k16, v16, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
+    }
 }
 
 struct AttnShape {
     int G, GW, zsplit, S, nsplit;
+    bool mfma;
 };
 
-AttnShape attn_shape(int B, int Hq, int Hkv, int T) {
+AttnShape attn_shape(int B, int Hq, int Hkv, int hd, int T) {
     AttnShape a;
     a.G = Hq / Hkv;
+    a.mfma = a.G >= 2 && a.G <= kAttnMfmaMaxG && (hd == 64 || hd == 128) && attn_mfma_enabled();
+    if (a.mfma) {
+        a.GW = a.G;
+        a.zsplit = 1;
+        a.S = attn_split_len(B, Hkv, 1, T);
+        a.nsplit = (T + a.S - 1) / a.S;
+        return a;
+    }
     a.GW = a.G == 1 ? 1 : (a.G <= 4 ? 4 : 8);
     a.zsplit = (a.G + a.GW - 1) / a.GW;
     a.S = attn_split_len(B, Hkv, a.zsplit, T);
@@ -739,7 +1047,7 @@ AttnShape attn_shape(int B, int Hq, int Hkv, int T) {
 int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* lens_dev,
              int len_host, int B, int T, int Hq, int Hkv, int hd, float scale, float* out,
              void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t st) {
-    const AttnShape sh = attn_shape(B, Hq, Hkv, T);
+    const AttnShape sh = attn_shape(B, Hq, Hkv, hd, T);
     const bool partials = sh.nsplit > 1 || out == nullptr;
     if (partials &&
         (!workspace || workspace_bytes < csdr_attn_decode_workspace_bytes(B, Hq, hd, T)))
@@ -752,19 +1060,20 @@ int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, con
     const RopeArgs none{};
     if (hd == 64) {
         if (ra)
-            launch_attn<64, true>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale,
-                                  sh.S, part, out, sh.nsplit, *ra, st);
+            launch_attn<64, true>(grid, sh.G, sh.mfma, q, k16, v16, lens_dev, len_host, T, Hq,
+                                  Hkv, scale, sh.S, part, out, sh.nsplit, *ra, st);
         else
-            launch_attn<64, false>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv, scale,
-                                   sh.S, part, out, sh.nsplit, none, st);
-        if (out && sh.nsplit > 1) attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, sh.nsplit, out);
+            launch_attn<64, false>(grid, sh.G, sh.mfma, q, k16, v16, lens_dev, len_host, T, Hq,
+                                   Hkv, scale, sh.S, part, out, sh.nsplit, none, st);
+        if (out && sh.nsplit > 1)
+            attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, sh.nsplit, out);
     } else {
         if (ra)
-            launch_attn<128, true>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv,
-                                   scale, sh.S, part, out, sh.nsplit, *ra, st);
+            launch_attn<128, true>(grid, sh.G, sh.mfma, q, k16, v16, lens_dev, len_host, T, Hq,
+                                   Hkv, scale, sh.S, part, out, sh.nsplit, *ra, st);
         else
-            launch_attn<128, false>(grid, sh.G, q, k16, v16, lens_dev, len_host, T, Hq, Hkv,
-                                    scale, sh.S, part, out, sh.nsplit, none, st);
+            launch_attn<128, false>(grid, sh.G, sh.mfma, q, k16, v16, lens_dev, len_host, T, Hq,
+                                    Hkv, scale, sh.S, part, out, sh.nsplit, none, st);
         if (out && sh.nsplit > 1)
             attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, sh.nsplit, out);
     }
@@ -840,9 +1149,8 @@ CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint
 }
 
 CSDR_API int csdr_attn_decode_splits(int B, int Hq, int Hkv, int hd, int T) {
-    (void)hd;
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || Hq % Hkv) return -1;
-    return attn_shape(B, Hq, Hkv, T).nsplit;
+    return attn_shape(B, Hq, Hkv, hd, T).nsplit;
 }
 
 CSDR_API int csdr_attn_decode_rope(const float* q, const float* k_new, const float* v_new,

@@ -76,6 +76,7 @@ constexpr int kMaxGroup = 8;
 constexpr int kMaxSlotsArg = 32;
 constexpr int kStageBatch = 8;  // global loads in flight per thread while staging to LDS
 constexpr int kMaxXopM = 16;  // columns an x op supports
+constexpr int kAttnStatMax = 2048;  // (head, split) partials whose weights the combine keeps in LDS
 
 // One coded matrix of a grouped launch.
 struct MatDesc {
@@ -304,8 +305,9 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
 // applied, into xs, and with do_xe the transformed edge-strip inputs into d.xe. Every global
 // load is issued before the first wait, so the staging costs one memory round trip where the
 // generic one makes up to three dependent ones (RMSNorm: the sum of squares, then x, then the
-// weights). The attention combine is one pass over the splits, eight at a time, with a running
-// maximum (online softmax). Ends with a barrier.
+// weights). The attention combine weighs each split by exp(m_j - M) / sum_j exp(m_j - M) l_j,
+// computed once per head into LDS (a single split is a division; more partials than the LDS
+// table holds take one pass with a running maximum). Ends with a barrier.
 // XOP: the call's x op (CSDR_XOP_*), fixed at compile time so that each kind gets only the
 // registers it needs.
 template <int NT, int XOP>
@@ -325,45 +327,121 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
     if constexpr (XOP == CSDR_XOP_ATTN) {
         const float* part = static_cast<const float*>(d.x);
         const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
+        const int nst = (C / hd) * ns;  // (head, split) partials
         const float* pp[kSlots];
-        float M[kSlots], den[kSlots], num[kSlots];
+        int dd[kSlots];
 #pragma unroll
         for (int i = 0; i < kSlots; ++i) {
             const int h = feat[i] / hd;
             pp[i] = part + (size_t)h * ns * ps;
-            M[i] = -INFINITY;
-            den[i] = 0.f;
-            num[i] = 0.f;
+            dd[i] = feat[i] - h * hd;
         }
         constexpr int kSB = 8;  // splits per round trip
-        for (int s0 = 0; s0 < ns; s0 += kSB) {
-            float ms[kSlots][kSB], ls[kSlots][kSB], os[kSlots][kSB];
+        if (ns == 1) {
+            // one split: its sum over its normaliser
 #pragma unroll
             for (int i = 0; i < kSlots; ++i) {
-                const int dd = feat[i] - (feat[i] / hd) * hd;
+                const float m = pp[i][0], l = pp[i][1], o = pp[i][2 + dd[i]];
+                v[i] = (m != -INFINITY && l > 0.f) ? o / l : 0.f;
+            }
+        } else if (nst <= kAttnStatMax) {
+            // The split weights exp(m_j - M) / sum_j exp(m_j - M) l_j depend on the head only:
+            // computed once per head into LDS (every (head, split) max and sum loaded in the
+            // same round trip as this thread's first partial values), then each feature is a
+            // weighted sum of its splits.
+            __shared__ float wst[kAttnStatMax], lst[kAttnStatMax];
+            constexpr int kStatPT = kAttnStatMax / NT;
+            float mv[kStatPT], lv[kStatPT];
 #pragma unroll
-                for (int j = 0; j < kSB; ++j) {
-                    const float* q = pp[i] + (size_t)min(s0 + j, ns - 1) * ps;
-                    ms[i][j] = q[0];
-                    ls[i][j] = q[1];
-                    os[i][j] = q[2 + dd];
+            for (int k = 0; k < kStatPT; ++k) {
+                const int e = min(tid + k * NT, nst - 1);
+                mv[k] = part[(size_t)e * ps];
+                lv[k] = part[(size_t)e * ps + 1];
+            }
+            float os[kSlots][kSB];
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i)
+#pragma unroll
+                for (int j = 0; j < kSB; ++j) os[i][j] = pp[i][(size_t)min(j, ns - 1) * ps + 2 + dd[i]];
+#pragma unroll
+            for (int k = 0; k < kStatPT; ++k)
+                if (tid + k * NT < nst) {
+                    wst[tid + k * NT] = mv[k];
+                    lst[tid + k * NT] = lv[k];
+                }
+            __syncthreads();
+            for (int h = tid; h < C / hd; h += NT) {
+                float* wr = wst + h * ns;
+                const float* lr = lst + h * ns;
+                float M = -INFINITY;
+                for (int j = 0; j < ns; ++j) M = fmaxf(M, wr[j]);
+                float den = 0.f;
+                for (int j = 0; j < ns; ++j)
+                    if (wr[j] != -INFINITY) den = fmaf(expf(wr[j] - M), lr[j], den);
+                for (int j = 0; j < ns; ++j)
+                    wr[j] = (wr[j] != -INFINITY && den > 0.f) ? expf(wr[j] - M) / den : 0.f;
+            }
+            __syncthreads();
+            float acc[kSlots];
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) acc[i] = 0.f;
+            for (int s0 = 0; s0 < ns; s0 += kSB) {
+                if (s0 > 0) {
+#pragma unroll
+                    for (int i = 0; i < kSlots; ++i)
+#pragma unroll
+                        for (int j = 0; j < kSB; ++j)
+                            os[i][j] = pp[i][(size_t)min(s0 + j, ns - 1) * ps + 2 + dd[i]];
+                }
+#pragma unroll
+                for (int i = 0; i < kSlots; ++i) {
+                    const float* wr = wst + (feat[i] / hd) * ns + s0;
+#pragma unroll
+                    for (int j = 0; j < kSB; ++j)
+                        if (s0 + j < ns) acc[i] = fmaf(wr[j], os[i][j], acc[i]);
                 }
             }
 #pragma unroll
-            for (int i = 0; i < kSlots; ++i) {
+            for (int i = 0; i < kSlots; ++i) v[i] = acc[i];
+        } else {
+            // more partials than the LDS table holds: one pass over the splits, four at a
+            // time, with a running maximum (online softmax)
+            constexpr int kSBo = 4;
+            float M[kSlots], den[kSlots], num[kSlots];
 #pragma unroll
-                for (int j = 0; j < kSB; ++j) {
-                    if (s0 + j >= ns || ms[i][j] == -INFINITY) continue;
-                    const float Mn = fmaxf(M[i], ms[i][j]);
-                    const float a = expf(M[i] - Mn), b = expf(ms[i][j] - Mn);
-                    den[i] = fmaf(den[i], a, b * ls[i][j]);
-                    num[i] = fmaf(num[i], a, b * os[i][j]);
-                    M[i] = Mn;
+            for (int i = 0; i < kSlots; ++i) {
+                M[i] = -INFINITY;
+                den[i] = 0.f;
+                num[i] = 0.f;
+            }
+            for (int s0 = 0; s0 < ns; s0 += kSBo) {
+                float ms[kSlots][kSBo], ls[kSlots][kSBo], os[kSlots][kSBo];
+#pragma unroll
+                for (int i = 0; i < kSlots; ++i) {
+#pragma unroll
+                    for (int j = 0; j < kSBo; ++j) {
+                        const float* q = pp[i] + (size_t)min(s0 + j, ns - 1) * ps;
+                        ms[i][j] = q[0];
+                        ls[i][j] = q[1];
+                        os[i][j] = q[2 + dd[i]];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < kSlots; ++i) {
+#pragma unroll
+                    for (int j = 0; j < kSBo; ++j) {
+                        if (s0 + j >= ns || ms[i][j] == -INFINITY) continue;
+                        const float Mn = fmaxf(M[i], ms[i][j]);
+                        const float a = expf(M[i] - Mn), b = expf(ms[i][j] - Mn);
+                        den[i] = fmaf(den[i], a, b * ls[i][j]);
+                        num[i] = fmaf(num[i], a, b * os[i][j]);
+                        M[i] = Mn;
+                    }
                 }
             }
+#pragma unroll
+            for (int i = 0; i < kSlots; ++i) v[i] = den[i] > 0.f ? num[i] / den[i] : 0.f;
         }
-#pragma unroll
-        for (int i = 0; i < kSlots; ++i) v[i] = den[i] > 0.f ? num[i] / den[i] : 0.f;
     } else {
         float w[kSlots];
 #pragma unroll

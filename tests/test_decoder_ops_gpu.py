@@ -85,8 +85,15 @@ def test_rope_kv(gpu, pos):
     (1, 4096, 4096, 32, 32, 128), # config 5 shape, batch 1
     (2, 300, None, 8, 2, 128),    # per-batch lengths
     (1, 256, 256, 4, 1, 64),      # exactly one split
+    (1, 1280, 641, 14, 2, 64),    # two 640-position splits, the second holding one position
+    (1, 2000, 1999, 32, 2, 128),  # 16 query heads per KV head, six splits
+    (3, 700, None, 12, 4, 64),    # three query heads per KV head, ragged lengths
+    (1, 48, 37, 6, 3, 128),       # a length that is not a multiple of 16
 ])
-def test_attn_decode(gpu, B, T, L, Hq, Hkv, hd):
+@pytest.mark.parametrize("mfma", ["1", "0"])
+def test_attn_decode(gpu, B, T, L, Hq, Hkv, hd, mfma, monkeypatch):
+    # CSDR_ATTN_MFMA=0 keeps the VALU kernels for grouped heads (attn_lds_kernel)
+    monkeypatch.setenv("CSDR_ATTN_MFMA", mfma)
     rng = np.random.default_rng(4)
     q = rng.normal(size=(B, Hq, hd)).astype(np.float32)
     kc = rng.normal(size=(B, T, Hkv, hd)).astype(np.float16)
@@ -194,7 +201,11 @@ def test_matmul_xop_rmsnorm_and_silu(gpu, M):
 
 
 @pytest.mark.parametrize("Hq,Hkv,hd,L,T", [(14, 2, 64, 300, 640), (32, 32, 128, 1000, 4096),
-                                           (4, 4, 64, 1, 64)])
+                                           (4, 4, 64, 1, 64), (32, 2, 128, 700, 1000),
+                                           (14, 2, 64, 641, 1280), (8, 4, 64, 16, 640),
+                                           # 67 splits x 32 heads: more partials than the
+                                           # o projection's LDS weight table holds
+                                           (32, 32, 64, 16999, 17000)])
 def test_attn_rope_fused_matches_unfused(gpu, Hq, Hkv, hd, L, T):
     from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
 
