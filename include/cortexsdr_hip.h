@@ -295,7 +295,8 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
  * [0, len_b) (len_b = lens_dev[b], or len_host when lens_dev is NULL); caches (B x T x Hkv x
  * hd) fp16; GQA as repeat_kv_heads (cortex_sdk.cpp:1453-1478); scale 0 = 1/sqrt(hd).
  * Split over chunks of 64..256 positions (about T / 8; workspace csdr_attn_decode_workspace_bytes)
- * then combined.
+ * then combined. 2..16 query heads per KV head run on the matrix cores (fp16 hi + lo operands,
+ * fp32 accumulate); CSDR_ATTN_MFMA=0 selects the vector-ALU kernel instead.
  * head_dim 64 or 128. Replaces Kernels::multi_head_attention's full-context recompute
  * (attention_kernels.cpp:26-113) with the cached form flash_attention.cpp:165-247 intends. */
 CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T);
