@@ -18,6 +18,10 @@ const char* last_error();
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Decode attention split partials in a workspace, n of them: the n (max, sum) pairs, then the
+// n unnormalised head_dim vectors from this float offset (16-byte aligned).
+__host__ __device__ inline size_t attn_vec_offset(size_t n) { return (2 * n + 3) & ~(size_t)3; }
+
 #define CSDR_HIP_CHECK(expr)                                                          \
     do {                                                                               \
         hipError_t e_ = (expr);                                                        \

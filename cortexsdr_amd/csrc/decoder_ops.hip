@@ -21,6 +21,7 @@
 
 namespace {
 
+using csdr::attn_vec_offset;
 using csdr::set_error;
 
 constexpr int kThreads = 256;
@@ -181,6 +182,10 @@ struct RopeArgs {
 
 constexpr int kAttnMaxS = 256;  // positions per split, at most (one thread per position)
 
+// Split partials in the workspace: n = B * Hq * nsplit of them, partial i = (b * Hq + h) *
+// nsplit + s; the n (max, sum) pairs come first (a consumer loads the whole table coalesced),
+// then, from the next 16-byte boundary (attn_vec_offset), the n unnormalised HD-vectors.
+
 // LDS bytes of attn_lds_kernel<HD, GW> at split length S
 constexpr size_t attn_lds_bytes(int HD, int GW, int S) {
     return (size_t)2 * S * (HD + 8) * 2 + (size_t)GW * HD * 4 + (size_t)GW * S * 4 +
@@ -203,6 +208,7 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
     float* stat = sc + GW * S;                              // GW x 2
     float* red = stat + GW * 2;                             // kThreads
     const int G = Hq / Hkv;
+    const size_t npart = (size_t)(gridDim.x / Hkv) * Hq * nsplit;  // partials in the workspace
     const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
     const int s = blockIdx.y;
     const int h0 = kvh * G + blockIdx.z * GW;
@@ -214,13 +220,15 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
     if (p0 >= p1) {  // empty split (the length is below this split's range)
         for (int g = 0; g < nh; ++g) {
             const int bh = b * Hq + h0 + g;
-            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            const size_t pi = (size_t)bh * nsplit + s;
+            float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+            float* pst = part + 2 * pi;              // its (max, sum)
             if (!direct) {
                 if (tid == 0) {
-                    pp[0] = -INFINITY;
-                    pp[1] = 0.f;
+                    pst[0] = -INFINITY;
+                    pst[1] = 0.f;
                 }
-                for (int i = tid; i < HD; i += kThreads) pp[2 + i] = 0.f;
+                for (int i = tid; i < HD; i += kThreads) pp[i] = 0.f;
             } else {
                 for (int i = tid; i < HD; i += kThreads) out[(size_t)bh * HD + i] = 0.f;
             }
@@ -361,11 +369,13 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
         if (direct) {
             out[(size_t)bh * HD + d] = v / stat[g * 2 + 1];
         } else {
-            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
-            pp[2 + d] = v;
+            const size_t pi = (size_t)bh * nsplit + s;
+            float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+            float* pst = part + 2 * pi;              // its (max, sum)
+            pp[d] = v;
             if (d == 0) {
-                pp[0] = stat[g * 2];
-                pp[1] = stat[g * 2 + 1];
+                pst[0] = stat[g * 2];
+                pst[1] = stat[g * 2 + 1];
             }
         }
     };
@@ -413,6 +423,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     __shared__ float stat[GW][2];
     __shared__ float red[kThreads / 64][GW][HD];
     const int G = Hq / Hkv;
+    const size_t npart = (size_t)(gridDim.x / Hkv) * Hq * nsplit;  // partials in the workspace
     const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
     const int s = blockIdx.y;
     const int h0 = kvh * G + blockIdx.z * GW;
@@ -425,13 +436,15 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     if (p0 >= p1) {  // empty split (the length is below this split's range)
         for (int g = 0; g < nh; ++g) {
             const int bh = b * Hq + h0 + g;
-            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
+            const size_t pi = (size_t)bh * nsplit + s;
+            float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+            float* pst = part + 2 * pi;              // its (max, sum)
             if (!direct) {
                 if (tid == 0) {
-                    pp[0] = -INFINITY;
-                    pp[1] = 0.f;
+                    pst[0] = -INFINITY;
+                    pst[1] = 0.f;
                 }
-                for (int i = tid; i < HD; i += kThreads) pp[2 + i] = 0.f;
+                for (int i = tid; i < HD; i += kThreads) pp[i] = 0.f;
             } else {
                 for (int i = tid; i < HD; i += kThreads) out[(size_t)bh * HD + i] = 0.f;
             }
@@ -571,11 +584,13 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
         if (direct) {
             out[(size_t)bh * HD + d] = sum / stat[g][1];
         } else {
-            float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
-            pp[2 + d] = sum;
+            const size_t pi = (size_t)bh * nsplit + s;
+            float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+            float* pst = part + 2 * pi;              // its (max, sum)
+            pp[d] = sum;
             if (d == 0) {
-                pp[0] = stat[g][0];
-                pp[1] = stat[g][1];
+                pst[0] = stat[g][0];
+                pst[1] = stat[g][1];
             }
         }
     }
@@ -624,6 +639,7 @@ __global__ __launch_bounds__(kMThreads) void attn_mfma_kernel(
     static_assert(VPT * kMThreads == SMAX * PPR, "V pieces must divide evenly");
     extern __shared__ float smem[];
     const int G = Hq / Hkv;
+    const size_t npart = (size_t)(gridDim.x / Hkv) * Hq * nsplit;  // partials in the workspace
     const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv, s = blockIdx.y;
     const int h0 = kvh * G;
     const int L = lens ? lens[b] : len_host;
@@ -638,11 +654,13 @@ __global__ __launch_bounds__(kMThreads) void attn_mfma_kernel(
             if (direct) {
                 out[(size_t)bh * HD + d] = 0.f;
             } else {
-                float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
-                pp[2 + d] = 0.f;
+                const size_t pi = (size_t)bh * nsplit + s;
+                float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+                float* pst = part + 2 * pi;              // its (max, sum)
+                pp[d] = 0.f;
                 if (d == 0) {
-                    pp[0] = -INFINITY;
-                    pp[1] = 0.f;
+                    pst[0] = -INFINITY;
+                    pst[1] = 0.f;
                 }
             }
         }
@@ -829,11 +847,13 @@ __global__ __launch_bounds__(kMThreads) void attn_mfma_kernel(
             if (direct) {
                 out[(size_t)bh * HD + d] = o[i] / stat[h * 2 + 1];
             } else {
-                float* pp = part + ((size_t)bh * nsplit + s) * (HD + 2);
-                pp[2 + d] = o[i];
+                const size_t pi = (size_t)bh * nsplit + s;
+                float* pp = part + attn_vec_offset(npart) + pi * HD;  // the partial's vector
+                float* pst = part + 2 * pi;              // its (max, sum)
+                pp[d] = o[i];
                 if (d == 0) {
-                    pp[0] = stat[h * 2];
-                    pp[1] = stat[h * 2 + 1];
+                    pst[0] = stat[h * 2];
+                    pst[1] = stat[h * 2 + 1];
                 }
             }
         }
@@ -844,16 +864,18 @@ template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ part,
                                                           int nsplit, float* __restrict__ out) {
     const int bh = blockIdx.x;
-    const float* pp = part + (size_t)bh * nsplit * (HD + 2);
+    const size_t npart = (size_t)gridDim.x * nsplit;
+    const float* pst = part + (size_t)2 * bh * nsplit;             // (max, sum) per split
+    const float* pv = part + attn_vec_offset(npart) + (size_t)bh * nsplit * HD;  // per split
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pst[2 * s]);
     float num = 0.f, den = 0.f;
     for (int s = 0; s < nsplit; ++s) {
-        const float ms = pp[(size_t)s * (HD + 2)];
+        const float ms = pst[2 * s];
         if (ms == -INFINITY) continue;
         const float w = expf(ms - M);
-        den = fmaf(w, pp[(size_t)s * (HD + 2) + 1], den);
-        num = fmaf(w, pp[(size_t)s * (HD + 2) + 2 + threadIdx.x], num);
+        den = fmaf(w, pst[2 * s + 1], den);
+        num = fmaf(w, pv[(size_t)s * HD + threadIdx.x], num);
     }
     out[(size_t)bh * HD + threadIdx.x] = den > 0.f ? num / den : 0.f;
 }
@@ -1130,7 +1152,7 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
 
 CSDR_API size_t csdr_attn_decode_workspace_bytes(int B, int Hq, int hd, int T) {
     const int nsplit = (T + 63) / 64;  // the shortest split bounds the count
-    return (size_t)B * Hq * nsplit * (hd + 2) * 4;
+    return (size_t)B * Hq * nsplit * (hd + 2) * 4 + 16;  // + the vectors' 16-byte alignment
 }
 
 CSDR_API int csdr_attn_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,

@@ -187,20 +187,32 @@ __device__ __forceinline__ float wg_sum(float v, float* red) {
     return t;
 }
 
-// Attention output feature k (head k / hd, dim k % hd) combined from the split partials
-// (m, l, o[hd]) of attn_decode's workspace layout.
-__device__ __forceinline__ float attn_feature(const Params& p, const float* part, int k) {
-    const int h = k / p.hd, dd = k - h * p.hd;
-    const float* pp = part + (size_t)h * p.nsplit * (p.hd + 2);
+// Attention split partials in attn_decode's workspace (M == 1, so n = heads * nsplit of them,
+// partial i = head * nsplit + split): the n (max, sum) pairs first, then the n unnormalised
+// head_dim vectors (from csdr::attn_vec_offset(n)).
+__device__ __forceinline__ const float* attn_stats(const float* part, int h, int ns) {
+    return part + (size_t)2 * h * ns;
+}
+__device__ __forceinline__ const float* attn_vecs(const float* part, int nh, int h, int ns,
+                                                  int hd) {
+    return part + csdr::attn_vec_offset((size_t)nh * ns) + (size_t)h * ns * hd;
+}
+
+// Attention output feature k (head k / hd, dim k % hd) of nh heads combined from the split
+// partials.
+__device__ __forceinline__ float attn_feature(const Params& p, const float* part, int nh, int k) {
+    const int h = k / p.hd, dd = k - h * p.hd, ns = p.nsplit;
+    const float* pst = attn_stats(part, h, ns);
+    const float* pv = attn_vecs(part, nh, h, ns, p.hd) + dd;
     float Mx = -INFINITY;
-    for (int s = 0; s < p.nsplit; ++s) Mx = fmaxf(Mx, pp[(size_t)s * (p.hd + 2)]);
+    for (int s = 0; s < ns; ++s) Mx = fmaxf(Mx, pst[2 * s]);
     float num = 0.f, den = 0.f;
-    for (int s = 0; s < p.nsplit; ++s) {
-        const float ms = pp[(size_t)s * (p.hd + 2)];
+    for (int s = 0; s < ns; ++s) {
+        const float ms = pst[2 * s];
         if (ms == -INFINITY) continue;
         const float w = expf(ms - Mx);
-        den = fmaf(w, pp[(size_t)s * (p.hd + 2) + 1], den);
-        num = fmaf(w, pp[(size_t)s * (p.hd + 2) + 2 + dd], num);
+        den = fmaf(w, pst[2 * s + 1], den);
+        num = fmaf(w, pv[(size_t)s * p.hd], num);
     }
     return den > 0.f ? num / den : 0.f;
 }
@@ -249,20 +261,20 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
         // per head of this range: split weights exp(m_s - max) and 1 / sum(w_s l_s) in
         // LDS once, then every feature is one weighted sum over the splits
         const float* part = static_cast<const float*>(d.x);
-        const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
+        const int hd = p.hd, ns = p.nsplit, nh = (d.C_full + d.Ce) / hd;
         const int h0 = (b0 * 64) / hd, h1 = (b0 * 64 + nx - 1) / hd + 1;
         float* wts = xs + nx;  // (h1 - h0) x (ns + 1)
         for (int h = h0 + tid; h < h1; h += NT) {
-            const float* pp = part + (size_t)h * ns * ps;
+            const float* pst = attn_stats(part, h, ns);
             float Mx = -INFINITY;
-            for (int s2 = 0; s2 < ns; ++s2) Mx = fmaxf(Mx, pp[(size_t)s2 * ps]);
+            for (int s2 = 0; s2 < ns; ++s2) Mx = fmaxf(Mx, pst[2 * s2]);
             float den = 0.f;
             float* wh = wts + (h - h0) * (ns + 1);
             for (int s2 = 0; s2 < ns; ++s2) {
-                const float ms = pp[(size_t)s2 * ps];
+                const float ms = pst[2 * s2];
                 const float w = ms == -INFINITY ? 0.f : expf(ms - Mx);
                 wh[s2] = w;
-                den = fmaf(w, pp[(size_t)s2 * ps + 1], den);
+                den = fmaf(w, pst[2 * s2 + 1], den);
             }
             wh[ns] = den > 0.f ? 1.0f / den : 0.f;
         }
@@ -270,9 +282,9 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
         for (int i = tid; i < nx; i += NT) {
             const int k = b0 * 64 + i, h = k / hd, dd = k - h * hd;
             const float* wh = wts + (h - h0) * (ns + 1);
-            const float* po = part + (size_t)h * ns * ps + 2 + dd;
+            const float* po = attn_vecs(part, nh, h, ns, hd) + dd;
             float num = 0.f;
-            for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * ps], num);
+            for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * hd], num);
             xs[i] = num * wh[ns];
         }
     } else if (p.x_f16) {
@@ -296,7 +308,8 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
         }
     } else if (p.xop == CSDR_XOP_ATTN && do_xe && xe) {
         const float* part = static_cast<const float*>(d.x);
-        for (int t = tid; t < d.Ce; t += NT) xe[t] = attn_feature(p, part, d.C_full + t);
+        const int nh = (d.C_full + d.Ce) / p.hd;
+        for (int t = tid; t < d.Ce; t += NT) xe[t] = attn_feature(p, part, nh, d.C_full + t);
     }
     __syncthreads();
 }
@@ -325,123 +338,107 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
     feat[kPer] = min(d.C_full + tid, C - 1);
     float v[kSlots];
     if constexpr (XOP == CSDR_XOP_ATTN) {
+        // thread t: features 4t .. 4t + 3 of the range, one head (head_dim % 4 == 0), one
+        // 16-byte load per split
         const float* part = static_cast<const float*>(d.x);
-        const int hd = p.hd, ns = p.nsplit, ps = hd + 2;
-        const int nst = (C / hd) * ns;  // (head, split) partials
-        const float* pp[kSlots];
-        int dd[kSlots];
-#pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-            const int h = feat[i] / hd;
-            pp[i] = part + (size_t)h * ns * ps;
-            dd[i] = feat[i] - h * hd;
-        }
+        const int hd = p.hd, ns = p.nsplit, nh = C / hd;
+        const int nst = nh * ns;  // (head, split) partials
+        const int fl = min(4 * tid, nx - 4), f = f0 + fl;
+        const int h = ((hd & (hd - 1)) == 0) ? f >> (__ffs(hd) - 1) : f / hd;
+        const float* pst = attn_stats(part, h, ns);
+        const float4* pv = reinterpret_cast<const float4*>(attn_vecs(part, nh, h, ns, hd) + (f - h * hd));
+        const int vs = hd / 4;  // float4 stride between splits
         constexpr int kSB = 8;  // splits per round trip
+        float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
         if (ns == 1) {
             // one split: its sum over its normaliser
-#pragma unroll
-            for (int i = 0; i < kSlots; ++i) {
-                const float m = pp[i][0], l = pp[i][1], o = pp[i][2 + dd[i]];
-                v[i] = (m != -INFINITY && l > 0.f) ? o / l : 0.f;
-            }
-        } else if (nst <= kAttnStatMax) {
-            // The split weights exp(m_j - M) / sum_j exp(m_j - M) l_j depend on the head only:
-            // computed once per head into LDS (every (head, split) max and sum loaded in the
-            // same round trip as this thread's first partial values), then each feature is a
-            // weighted sum of its splits.
-            __shared__ float wst[kAttnStatMax], lst[kAttnStatMax];
+            const float m = pst[0], l = pst[1];
+            const float4 o = pv[0];
+            if (m != -INFINITY && l > 0.f) r = make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+        } else if (ns <= 64 && nst * 2 <= kAttnStatMax) {
+            // The split weights w_j = exp(m_j - M) / sum_j exp(m_j - M) l_j depend on the head
+            // only: thread (head, split) pairs in lane groups of GS >= ns splits (max and sum
+            // by shuffles within the group), loaded in the same round trip as this thread's
+            // first partial values, weights into LDS; then each feature is a weighted sum.
+            __shared__ float wst[kAttnStatMax];
             constexpr int kStatPT = kAttnStatMax / NT;
-            float mv[kStatPT], lv[kStatPT];
+            int GS = 1;
+            while (GS < ns) GS <<= 1;
+            const int ngs = nh * GS;  // < 2 nst
+            float2 ml[kStatPT];
 #pragma unroll
             for (int k = 0; k < kStatPT; ++k) {
-                const int e = min(tid + k * NT, nst - 1);
-                mv[k] = part[(size_t)e * ps];
-                lv[k] = part[(size_t)e * ps + 1];
+                const int e = tid + k * NT, hh = min(e / GS, nh - 1), j = min(e % GS, ns - 1);
+                if (k * NT < ngs) ml[k] = reinterpret_cast<const float2*>(part)[hh * ns + j];
             }
-            float os[kSlots][kSB];
+            float4 os[kSB];
 #pragma unroll
-            for (int i = 0; i < kSlots; ++i)
+            for (int j = 0; j < kSB; ++j) os[j] = pv[min(j, ns - 1) * vs];
 #pragma unroll
-                for (int j = 0; j < kSB; ++j) os[i][j] = pp[i][(size_t)min(j, ns - 1) * ps + 2 + dd[i]];
-#pragma unroll
-            for (int k = 0; k < kStatPT; ++k)
-                if (tid + k * NT < nst) {
-                    wst[tid + k * NT] = mv[k];
-                    lst[tid + k * NT] = lv[k];
-                }
-            __syncthreads();
-            for (int h = tid; h < C / hd; h += NT) {
-                float* wr = wst + h * ns;
-                const float* lr = lst + h * ns;
-                float M = -INFINITY;
-                for (int j = 0; j < ns; ++j) M = fmaxf(M, wr[j]);
-                float den = 0.f;
-                for (int j = 0; j < ns; ++j)
-                    if (wr[j] != -INFINITY) den = fmaf(expf(wr[j] - M), lr[j], den);
-                for (int j = 0; j < ns; ++j)
-                    wr[j] = (wr[j] != -INFINITY && den > 0.f) ? expf(wr[j] - M) / den : 0.f;
+            for (int k = 0; k < kStatPT; ++k) {
+                if (k * NT >= ngs) break;
+                const int e = tid + k * NT, hh = e / GS, j = e % GS;
+                const bool live = hh < nh && j < ns;
+                const float m = live ? ml[k].x : -INFINITY;
+                float M = m;
+                for (int off = GS >> 1; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+                const float ex = m == -INFINITY ? 0.f : expf(m - M);
+                float den = live ? ex * ml[k].y : 0.f;
+                for (int off = GS >> 1; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+                if (live) wst[hh * ns + j] = den > 0.f ? ex / den : 0.f;
             }
             __syncthreads();
-            float acc[kSlots];
-#pragma unroll
-            for (int i = 0; i < kSlots; ++i) acc[i] = 0.f;
+            const float* wr = wst + h * ns;
             for (int s0 = 0; s0 < ns; s0 += kSB) {
                 if (s0 > 0) {
 #pragma unroll
-                    for (int i = 0; i < kSlots; ++i)
-#pragma unroll
-                        for (int j = 0; j < kSB; ++j)
-                            os[i][j] = pp[i][(size_t)min(s0 + j, ns - 1) * ps + 2 + dd[i]];
+                    for (int j = 0; j < kSB; ++j) os[j] = pv[min(s0 + j, ns - 1) * vs];
                 }
 #pragma unroll
-                for (int i = 0; i < kSlots; ++i) {
-                    const float* wr = wst + (feat[i] / hd) * ns + s0;
-#pragma unroll
-                    for (int j = 0; j < kSB; ++j)
-                        if (s0 + j < ns) acc[i] = fmaf(wr[j], os[i][j], acc[i]);
+                for (int j = 0; j < kSB; ++j) {
+                    if (s0 + j >= ns) break;
+                    const float w = wr[s0 + j];
+                    r.x = fmaf(w, os[j].x, r.x);
+                    r.y = fmaf(w, os[j].y, r.y);
+                    r.z = fmaf(w, os[j].z, r.z);
+                    r.w = fmaf(w, os[j].w, r.w);
                 }
             }
-#pragma unroll
-            for (int i = 0; i < kSlots; ++i) v[i] = acc[i];
         } else {
             // more partials than the LDS table holds: one pass over the splits, four at a
             // time, with a running maximum (online softmax)
             constexpr int kSBo = 4;
-            float M[kSlots], den[kSlots], num[kSlots];
-#pragma unroll
-            for (int i = 0; i < kSlots; ++i) {
-                M[i] = -INFINITY;
-                den[i] = 0.f;
-                num[i] = 0.f;
-            }
+            float M = -INFINITY, den = 0.f;
+            float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int s0 = 0; s0 < ns; s0 += kSBo) {
-                float ms[kSlots][kSBo], ls[kSlots][kSBo], os[kSlots][kSBo];
+                float ms[kSBo], ls[kSBo];
+                float4 os[kSBo];
 #pragma unroll
-                for (int i = 0; i < kSlots; ++i) {
-#pragma unroll
-                    for (int j = 0; j < kSBo; ++j) {
-                        const float* q = pp[i] + (size_t)min(s0 + j, ns - 1) * ps;
-                        ms[i][j] = q[0];
-                        ls[i][j] = q[1];
-                        os[i][j] = q[2 + dd[i]];
-                    }
+                for (int j = 0; j < kSBo; ++j) {
+                    const int sj = min(s0 + j, ns - 1);
+                    ms[j] = pst[2 * sj];
+                    ls[j] = pst[2 * sj + 1];
+                    os[j] = pv[sj * vs];
                 }
 #pragma unroll
-                for (int i = 0; i < kSlots; ++i) {
-#pragma unroll
-                    for (int j = 0; j < kSBo; ++j) {
-                        if (s0 + j >= ns || ms[i][j] == -INFINITY) continue;
-                        const float Mn = fmaxf(M[i], ms[i][j]);
-                        const float a = expf(M[i] - Mn), b = expf(ms[i][j] - Mn);
-                        den[i] = fmaf(den[i], a, b * ls[i][j]);
-                        num[i] = fmaf(num[i], a, b * os[i][j]);
-                        M[i] = Mn;
-                    }
+                for (int j = 0; j < kSBo; ++j) {
+                    if (s0 + j >= ns || ms[j] == -INFINITY) continue;
+                    const float Mn = fmaxf(M, ms[j]);
+                    const float a = expf(M - Mn), b = expf(ms[j] - Mn);
+                    den = fmaf(den, a, b * ls[j]);
+                    num.x = fmaf(num.x, a, b * os[j].x);
+                    num.y = fmaf(num.y, a, b * os[j].y);
+                    num.z = fmaf(num.z, a, b * os[j].z);
+                    num.w = fmaf(num.w, a, b * os[j].w);
+                    M = Mn;
                 }
             }
-#pragma unroll
-            for (int i = 0; i < kSlots; ++i) v[i] = den[i] > 0.f ? num[i] / den[i] : 0.f;
+            if (den > 0.f) r = make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
         }
+        if (4 * tid < nx) *reinterpret_cast<float4*>(xs + 4 * tid) = r;
+        if (do_xe && d.xe && tid < d.Ce) d.xe[tid] = attn_feature(p, part, nh, d.C_full + tid);
+        __syncthreads();
+        return;
     } else {
         float w[kSlots];
 #pragma unroll
@@ -1400,8 +1397,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
                                                  std::to_string(kMaxXopM));
         if (xa.xop == CSDR_XOP_RMSNORM && !xa.nw)
             return set_error(CSDR_E_INVALID, "hsdb_matmul: RMSNorm x op needs weights");
-        if (xa.xop == CSDR_XOP_ATTN && (M != 1 || xa.nsplit <= 0 || xa.hd <= 0))
-            return set_error(CSDR_E_INVALID, "hsdb_matmul: attention x op needs M == 1, splits, hd");
+        if (xa.xop == CSDR_XOP_ATTN && (M != 1 || xa.nsplit <= 0 || xa.hd <= 0 || xa.hd % 4))
+            return set_error(CSDR_E_INVALID, "hsdb_matmul: attention x op needs M == 1, splits, hd % 4 == 0");
         for (int i = 0; i < n; ++i) {
             if (segs[i]->tile_cols != 64)
                 return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: x ops need 64-column blocks");
