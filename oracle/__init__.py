@@ -92,6 +92,8 @@ def orc():
         L.orc_silu_mul.argtypes = [_f32p, _f32p, _sz, _f32p]
         L.orc_rope.argtypes = [_f32p, _sz, _sz, _sz, C.c_float, _sz]
         L.orc_select_best.argtypes = [_f32p, _sz, C.c_void_p, C.c_float, C.c_float]
+        L.orc_hsdr_mp.argtypes = [_f32p, _sz, _sz, _f32p, _sz, _sz, _sz, _f32p, _u16p]
+        L.orc_hsdr_mp.restype = None
         L.orc_select_best.restype = C.c_int
         _orc = L
     return _orc
@@ -493,3 +495,16 @@ def ref_mha(q, k, v, heads, causal=True, flash=False):
        np.ascontiguousarray(v, np.float32).ravel(), out.reshape(-1), B, T, H, heads,
        1 if causal else 0)
     return out
+
+
+def hsdr_mp(tiles: np.ndarray, D: np.ndarray, gamma, S: int, k: int) -> np.ndarray:
+    """Packed u16 codes (n_tiles x S*k) of hierarchical binary matching pursuit
+    (hierarchicalBinaryCode, HierarchicalSDRStrategy.cpp:219-262) of tiles (n x C) against
+    D (K x C) with stage scales gamma."""
+    t = np.ascontiguousarray(tiles, np.float32)
+    d = np.ascontiguousarray(D, np.float32)
+    g = np.ascontiguousarray(gamma, np.float32)
+    codes = np.zeros((t.shape[0], S * k), np.uint16)
+    orc().orc_hsdr_mp(t.ravel(), t.shape[0], t.shape[1], d.ravel(), d.shape[0], S, k, g,
+                      codes.ravel())
+    return codes

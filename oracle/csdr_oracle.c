@@ -746,3 +746,63 @@ int orc_select_best(const float* logits, size_t n, const uint8_t* repeated, floa
     }
     return tok;
 }
+
+/* ------------------------------------------------------------------ HSDR encoder */
+
+/* dot_product_simd (HierarchicalSDRStrategy.cpp:157-190) in its AVX2 lane order */
+static float dot_avx2_order(const float* a, const float* b, size_t n) {
+    float acc[16] = {0};  /* acc0 = lanes 0..7, acc1 = lanes 8..15 */
+    size_t c = 0;
+    for (; c + 16 <= n; c += 16)
+        for (int l = 0; l < 16; ++l) acc[l] = fmaf(a[c + l], b[c + l], acc[l]);
+    for (; c + 8 <= n; c += 8)
+        for (int l = 0; l < 8; ++l) acc[l] = fmaf(a[c + l], b[c + l], acc[l]);
+    float v[8], h[4];
+    for (int l = 0; l < 8; ++l) v[l] = acc[l] + acc[8 + l];   /* acc0 + acc1 */
+    for (int i = 0; i < 4; ++i) h[i] = v[i] + v[i + 4];        /* low + high 128 */
+    float s = (h[0] + h[1]) + (h[2] + h[3]);                   /* two horizontal adds */
+    for (; c < n; ++c) s = fmaf(a[c], b[c], s);                /* scalar tail, contracted */
+    return s;
+}
+
+void orc_hsdr_mp(const float* tiles, size_t n_tiles, size_t C, const float* D, size_t K,
+                 size_t S, size_t k, const float* gamma, uint16_t* codes) {
+    /* hierarchicalBinaryCode :219-262, one tile per iteration (the reference's encode_all
+     * loop, :556-567) */
+    long i;
+#pragma omp parallel for schedule(static)
+    for (i = 0; i < (long)n_tiles; ++i) {
+        float* r = (float*)malloc(C * sizeof(float));
+        float* proj = (float*)malloc(K * sizeof(float));
+        uint8_t* used = (uint8_t*)malloc(K);
+        memcpy(r, tiles + (size_t)i * C, C * sizeof(float));
+        for (size_t l = 0; l < S; ++l) {
+            memset(used, 0, K);
+            for (size_t st = 0; st < k; ++st) {
+                for (size_t j = 0; j < K; ++j) {
+                    const float sj = dot_avx2_order(D + j * C, r, C);
+                    proj[j] = used[j] ? 0.0f : sj;
+                }
+                size_t best = 0;
+                float best_abs = 0.0f;
+                for (size_t j = 0; j < K; ++j) {
+                    const float a = fabsf(proj[j]);
+                    if (a > best_abs) {
+                        best_abs = a;
+                        best = j;
+                    }
+                }
+                const int sign = proj[best] >= 0.0f ? 1 : -1;
+                codes[(size_t)i * S * k + l * k + st] =
+                    (uint16_t)((best & 0x7FFFu) | (sign < 0 ? 0x8000u : 0u));
+                used[best] = 1;
+                const float scale = gamma[l] * (float)sign;
+                const float* atom = D + best * C;
+                for (size_t c = 0; c < C; ++c) r[c] = fmaf(-atom[c], scale, r[c]);
+            }
+        }
+        free(r);
+        free(proj);
+        free(used);
+    }
+}

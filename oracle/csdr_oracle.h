@@ -136,6 +136,18 @@ void orc_rope(float* x, size_t ntok, size_t heads, size_t head_dim, float theta,
 int orc_select_best(const float* logits, size_t n, const uint8_t* repeated, float temperature,
                     float penalty);
 
+/* ---- HSDR encoder (HierarchicalSDRStrategy.cpp) ----
+ * Hierarchical binary matching pursuit, hierarchicalBinaryCode :219-262, over n_tiles tiles
+ * of C floats against D (K x C): per stage l (gamma[l]) k greedy picks of argmax |<D_j, r>|
+ * (first maximum, strict '>', atoms picked earlier in the stage score 0), sign = +1 when the
+ * projection is >= 0, r -= gamma_l * sign * D_best. Projections in dot_product_simd's
+ * (:157-190) AVX2 order: 16 lane sums over 16-element chunks (two 8-lane FMA accumulators),
+ * an 8-element chunk into the first, then (acc0 + acc1), low + high halves, two horizontal
+ * adds, then a contracted scalar tail. The update as axpy_subtract_simd (:193-216): fused
+ * r - atom * scale. codes: packIndexSign (:76-80), tile-major, stage-major slots. */
+void orc_hsdr_mp(const float* tiles, size_t n_tiles, size_t C, const float* D, size_t K,
+                 size_t S, size_t k, const float* gamma, uint16_t* codes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,17 @@ and, added to ref_fixtures.npz without touching its other arrays (`gguf` argumen
   q40/q80_*  random Q4_0 / Q8_0 blocks through dequantizeToFP32 (the compress side's decode,
              which equals the engine's decodeSupportedGGUFQuantized for these two formats)
 
-Usage: python tests/golden/make_fixtures.py [hsda | gguf]
+and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
+
+  enc_<i>_w, enc_<i>_stream, enc_<i>_cfg  HierarchicalSDRStrategy::compress with
+             ksvd_iters = 0 (dictionary initialised from random tiles, then one pass of
+             hierarchical matching pursuit) on: random matrices (1-row tiles, C = 48..256,
+             and 8 x 16 / 8 x 8 tiles), and matrices whose rows are random rows A, their
+             reversals, and reversal-symmetric rows, so that projections onto atom pairs
+             (A, reversed A) tie in exact arithmetic and the float summation order decides the
+             pick. cfg = (tile_rows, tile_cols, K, stages, k per stage).
+
+Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode]
 """
 from __future__ import annotations
 
@@ -141,8 +151,44 @@ def hsda_main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def symmetric_pairs(C: int, seed: int) -> np.ndarray:
+    """Rows: 24 random A, their reversals, 40 reversal-symmetric rows; shuffled."""
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal((24, C)) * 0.02).astype(np.float32)
+    sy = (rng.standard_normal((40, C)) * 0.02).astype(np.float32)
+    sy = np.maximum(sy, sy[:, ::-1])
+    w = np.concatenate([a, a[:, ::-1], sy])
+    return np.ascontiguousarray(w[rng.permutation(w.shape[0])])
+
+
+def encode_main() -> None:
+    oracle.build(ref=True)
+    if oracle.ref() is None:
+        raise SystemExit("oracle/_ref/libcsdr_ref.so is not built")
+    rng = np.random.default_rng(20261203)
+    cases = []
+    for (R, Cc, tr, tc, K, S, k) in [(64, 48, 1, 48, 16, 2, 3), (160, 256, 1, 256, 64, 3, 4),
+                                     (96, 96, 8, 16, 32, 3, 2), (200, 72, 1, 72, 40, 2, 5),
+                                     (130, 132, 8, 8, 24, 2, 3)]:
+        cases.append(((rng.standard_normal((R, Cc)) * 0.02).astype(np.float32), (tr, tc, K, S, k)))
+    for C, seed in [(48, 3), (48, 11), (48, 12), (64, 1), (72, 2), (80, 13)]:
+        cases.append((symmetric_pairs(C, seed), (1, C, 48, 2, 2)))
+    out = {}
+    for i, (w, cfg) in enumerate(cases):
+        tr, tc, K, S, k = cfg
+        out[f"enc_{i}_w"] = w
+        out[f"enc_{i}_stream"] = np.frombuffer(
+            oracle.ref_hsdr_compress(w, tr, tc, K, S, k, ksvd_iters=0), np.uint8)
+        out[f"enc_{i}_cfg"] = np.array(cfg, np.int32)
+    path = os.path.join(HERE, "hsdr_encode_fixtures.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
 if __name__ == "__main__":
-    if sys.argv[1:] == ["hsda"]:
+    if sys.argv[1:] == ["encode"]:
+        encode_main()
+    elif sys.argv[1:] == ["hsda"]:
         hsda_main()
     elif sys.argv[1:] == ["gguf"]:
         gguf_main()
