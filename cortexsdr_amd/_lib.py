@@ -143,6 +143,15 @@ SIGNATURES.update({
                                              C.POINTER(_vp), C.c_int, C.c_int, _vp, C.c_float,
                                              C.c_int, C.c_int, _vp, _sz, _vp]),
     "csdr_attn_decode_splits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "csdr_hsdr_encode": (C.c_int, [_vp, _sz, C.c_int, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp,
+                                   _vp]),
+    "csdr_hsdr_init_dictionary": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.c_uint16,
+                                            C.c_uint8, C.c_uint8, _vp]),
+    "csdr_hsdr_compress_bytes": (_sz, [C.c_uint32, C.c_uint32, C.c_uint16, C.c_uint16,
+                                       C.c_uint16, C.c_uint8, C.c_uint8]),
+    "csdr_hsdr_compress": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.c_uint16, C.c_uint16,
+                                     C.c_uint16, C.c_uint8, C.c_uint8, C.c_uint8, C.c_float,
+                                     _vp, _sz, _vp]),
     "csdr_attn_decode_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
                                         C.c_int, C.c_int, C.c_float, C.c_float, _vp, _vp, _sz,
                                         _vp]),

@@ -1,0 +1,70 @@
+"""HSDR encoder on the MI355X kernels (the compress side of HierarchicalSDRStrategy).
+
+Reference: HierarchicalSDRStrategy.cpp hierarchicalBinaryCode (:219-262), fitHierarchicalKSVD
+(:495-602) and HierarchicalSDRStrategy::compress (:1064-1237).
+  encode(tiles, D, stage_scales, n_stages, k)   -> packed codes (device, n_tiles x slots)
+  init_dictionary(tiles, n_atoms, n_stages, k)  -> the fit's initial dictionary (host)
+  compress(w, tile_rows, tile_cols, n_atoms, n_stages, k, ksvd_iters=0, stage_decay=0.5)
+                                                -> HSDR v2 stream bytes
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .hsdr import _check, _torch
+
+
+def encode(tiles, D, stage_scales, n_stages: int, k_per_stage: int):
+    """Packed (sign << 15 | index) codes of matching pursuit of device tiles (n x C fp32)
+    against the device dictionary D (K x C fp32), as a device uint16 tensor (n x S*k)."""
+    torch = _torch()
+    if tiles.dtype != torch.float32 or D.dtype != torch.float32:
+        raise TypeError("tiles and D must be float32")
+    n, c = tiles.shape
+    K = D.shape[0]
+    if D.shape[1] != c:
+        raise ValueError("D and tiles differ in tile size")
+    g = np.ascontiguousarray(stage_scales, np.float32)
+    if g.size < n_stages:
+        raise ValueError("one stage scale per stage")
+    codes = torch.empty((n, n_stages * k_per_stage), dtype=torch.int16, device=tiles.device)
+    st = torch.cuda.current_stream(tiles.device).cuda_stream
+    _check(_lib.load().csdr_hsdr_encode(tiles.data_ptr(), n, c, D.data_ptr(), K, n_stages,
+                                        k_per_stage, g.ctypes.data, codes.data_ptr(), st))
+    return codes
+
+
+def init_dictionary(tiles: np.ndarray, n_atoms: int, n_stages: int, k_per_stage: int):
+    """fitHierarchicalKSVD's initial dictionary (n_atoms x tile_dim, host fp32) of host
+    tiles (n x tile_dim), in the reference build's arithmetic."""
+    t = np.ascontiguousarray(tiles, np.float32)
+    D = np.zeros((n_atoms, t.shape[1]), np.float32)
+    _check(_lib.load().csdr_hsdr_init_dictionary(t.ctypes.data, t.shape[0], t.shape[1], n_atoms,
+                                                 n_stages, k_per_stage, D.ctypes.data))
+    return D
+
+
+def compress(w: np.ndarray, tile_rows: int, tile_cols: int, n_atoms: int, n_stages: int,
+             k_per_stage: int, ksvd_iters: int = 0, stage_decay: float = 0.5) -> bytes:
+    """HSDR v2 stream of the fp32 matrix w (rows x cols), as HierarchicalSDRStrategy::compress
+    with the given config (tile_rows == 1 widens the tiles to whole rows)."""
+    torch = _torch()
+    w = np.ascontiguousarray(w, np.float32)
+    R, Cc = w.shape
+    lib = _lib.load()
+    n = lib.csdr_hsdr_compress_bytes(R, Cc, tile_rows, tile_cols, n_atoms, n_stages, k_per_stage)
+    if n == 0:
+        raise ValueError("shape cannot be compressed with this config (no full tile, or "
+                         "fewer tiles than atoms)")
+    out = np.zeros(n, np.uint8)
+    st = torch.cuda.current_stream().cuda_stream
+    _check(lib.csdr_hsdr_compress(w.ctypes.data, R, Cc, tile_rows, tile_cols, n_atoms, n_stages,
+                                  k_per_stage, ksvd_iters, C.c_float(stage_decay),
+                                  out.ctypes.data, n, st))
+    return out.tobytes()
+
+
+__all__ = ["encode", "init_dictionary", "compress"]

@@ -33,6 +33,10 @@
  *   csdr_gguf_format / csdr_gguf_block / csdr_gguf_linear / csdr_gguf_dequant
  *       decodeSupportedGGUFQuantized for every format it decodes (SparseInferenceEngine.cpp:
  *       181-231 block sizes, 276-469 decode) followed by Kernels::linear_forward.
+ *   csdr_hsdr_encode / csdr_hsdr_init_dictionary / csdr_hsdr_compress(_bytes)
+ *       the encode side: hierarchicalBinaryCode (HierarchicalSDRStrategy.cpp:219-262) over
+ *       many tiles, fitHierarchicalKSVD's initialisation (:507-541), and
+ *       HierarchicalSDRStrategy::compress (:1064-1237) around them.
  */
 #ifndef CORTEXSDR_HIP_H
 #define CORTEXSDR_HIP_H
@@ -186,6 +190,48 @@ CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* seg, float* w, void* hip_stre
  * Both are device buffers of n_tiles * slots uint16 (coef_abs may be NULL). */
 CSDR_API int csdr_hsdb_export_codes(const csdr_hsdb* seg, uint16_t* packed, uint16_t* coef_abs,
                                     void* hip_stream);
+
+/* ======================================================================
+ * HSDR encoder (compress side)
+ * ==================================================================== */
+
+/* Hierarchical binary matching pursuit of n_tiles tiles (device, n_tiles x tile_dim fp32)
+ * against D (device, n_atoms x tile_dim fp32), hierarchicalBinaryCode
+ * (HierarchicalSDRStrategy.cpp:219-262): per stage l (stage_scales[l], a host array of
+ * n_stages floats) k_per_stage greedy picks of the first maximum of |<D_j, r>| (atoms already
+ * picked in the stage score 0), sign = +1 when that projection is >= 0, r -= scale * sign *
+ * D_best. Projections are summed in the reference's AVX2 order (dot_product_simd :157-190),
+ * so the picks are the reference's bit for bit. codes (device, n_tiles x n_stages *
+ * k_per_stage uint16): packIndexSign (:76-80), tile-major, stage-major. tile_dim must be a
+ * multiple of 8; n_atoms <= 32768; n_stages <= 32. */
+CSDR_API int csdr_hsdr_encode(const float* tiles, size_t n_tiles, int tile_dim, const float* D,
+                              int n_atoms, int n_stages, int k_per_stage,
+                              const float* stage_scales, uint16_t* codes, void* hip_stream);
+/* Size of the HSDR v2 stream csdr_hsdr_compress writes for this shape and config (0 when the
+ * shape cannot be compressed: no full tile, fewer tiles than atoms). */
+CSDR_API size_t csdr_hsdr_compress_bytes(uint32_t rows, uint32_t cols, uint16_t tile_rows,
+                                         uint16_t tile_cols, uint16_t n_atoms,
+                                         uint8_t n_stages, uint8_t k_per_stage);
+/* The dictionary initialisation of fitHierarchicalKSVD (HierarchicalSDRStrategy.cpp:507-541),
+ * host code: atom j = the tile std::uniform_int_distribution picks over std::mt19937(0xC0DE),
+ * unit length, all scaled by the mean tile norm / max(1, sqrt(n_stages * k_per_stage)); in
+ * the reference build's arithmetic (its -ffast-math 1/sqrt is the CPU's approximate
+ * reciprocal square root plus one Newton step, reproduced instruction for instruction), so
+ * D (host, n_atoms x tile_dim) is the reference's bit for bit on the same CPU. tiles: host,
+ * n_tiles x tile_dim. */
+CSDR_API int csdr_hsdr_init_dictionary(const float* tiles, uint32_t n_tiles, uint32_t tile_dim,
+                                       uint16_t n_atoms, uint8_t n_stages, uint8_t k_per_stage,
+                                       float* D);
+/* HierarchicalSDRStrategy::compress (HierarchicalSDRStrategy.cpp:1064-1237) of an fp32
+ * rows x cols host matrix w into out (csdr_hsdr_compress_bytes bytes): tile_rows == 1 widens
+ * tiles to whole rows (configFor :1024-1046); dictionary as csdr_hsdr_init_dictionary, one
+ * matching-pursuit pass on the GPU (csdr_hsdr_encode), edge strips as fp32, stage scales
+ * stage_decay^l: the reference's stream byte for byte on the same CPU. ksvd_iters must be 0
+ * (the atom update is not built: CSDR_E_UNSUPPORTED). */
+CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, uint16_t tile_rows,
+                                uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages,
+                                uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
+                                uint8_t* out, size_t out_bytes, void* hip_stream);
 
 /* ======================================================================
  * GGUF Q4_K dequant-matmul (engine path, no fp32 W materialised)

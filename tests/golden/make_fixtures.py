@@ -34,7 +34,9 @@ and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
              and 8 x 16 / 8 x 8 tiles), and matrices whose rows are random rows A, their
              reversals, and reversal-symmetric rows, so that projections onto atom pairs
              (A, reversed A) tie in exact arithmetic and the float summation order decides the
-             pick. cfg = (tile_rows, tile_cols, K, stages, k per stage).
+             pick. cfg = (tile_rows, tile_cols, K, stages, k per stage). cpu_model: the CPU
+             the reference ran on (its dictionary initialisation uses that CPU's approximate
+             reciprocal square root).
 
 Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode]
 """
@@ -151,6 +153,16 @@ def hsda_main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def cpu_model() -> str:
+    """/proc/cpuinfo's model name: the reference's dictionary initialisation depends on the
+    CPU's approximate reciprocal square root (its -ffast-math build)."""
+    with open("/proc/cpuinfo") as f:
+        for line in f:
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    return ""
+
+
 def symmetric_pairs(C: int, seed: int) -> np.ndarray:
     """Rows: 24 random A, their reversals, 40 reversal-symmetric rows; shuffled."""
     rng = np.random.default_rng(seed)
@@ -180,6 +192,7 @@ def encode_main() -> None:
         out[f"enc_{i}_stream"] = np.frombuffer(
             oracle.ref_hsdr_compress(w, tr, tc, K, S, k, ksvd_iters=0), np.uint8)
         out[f"enc_{i}_cfg"] = np.array(cfg, np.int32)
+    out["cpu_model"] = np.frombuffer(cpu_model().encode(), np.uint8)
     path = os.path.join(HERE, "hsdr_encode_fixtures.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")

@@ -1,0 +1,101 @@
+"""GPU parity of the HSDR encoder (csdr_hsdr_encode, csdr_hsdr_compress) through the C-ABI.
+
+Bars:
+  * matching pursuit: codes bit-exact against the reference's compress fixtures (given the
+    stream's dictionary) and against the oracle (pinned in test_hsdr_encode_oracle.py) on
+    larger random cases; K, tile sizes with and without an 8-element chunk, many tiles per
+    workgroup and one;
+  * compress (ksvd_iters = 0): the reference's stream byte for byte (on a CPU whose
+    approximate reciprocal square root is the fixtures'; elsewhere header, stage scales, edge
+    strips and codes exact around a dictionary within 8 ulp).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from test_hsdr_encode_oracle import stream_parts, tiles_of
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def enc():
+    return np.load(os.path.join(GOLDEN, "hsdr_encode_fixtures.npz"), allow_pickle=False)
+
+
+def n_cases(enc):
+    return len([k for k in enc.files if k.endswith("_stream")])
+
+
+def gpu_codes(gpu, tiles, D, g, S, k):
+    from cortexsdr_amd import encode
+
+    t = gpu.from_numpy(np.array(tiles, np.float32)).cuda()
+    d = gpu.from_numpy(np.array(D, np.float32)).cuda()
+    return encode.encode(t, d, g, S, k).cpu().numpy().view(np.uint16)
+
+
+def test_encode_matches_reference_fixtures(gpu, enc):
+    for i in range(n_cases(enc)):
+        v, D, g, codes = stream_parts(enc[f"enc_{i}_stream"].tobytes())
+        t = tiles_of(enc[f"enc_{i}_w"], v.tile_rows, v.tile_cols)
+        got = gpu_codes(gpu, t, D, g, v.n_stages, v.k_per_stage)
+        assert np.array_equal(got, codes), f"case {i}"
+
+
+@pytest.mark.parametrize("n,C,K,S,k", [(1000, 64, 256, 3, 5), (333, 200, 100, 2, 8),
+                                       (40, 1024, 512, 3, 4), (7, 4096, 64, 2, 3),
+                                       (1, 8, 8, 2, 4)])
+def test_encode_matches_oracle(gpu, n, C, K, S, k):
+    rng = np.random.default_rng(n + C + K)
+    t = (rng.standard_normal((n, C)) * 0.02).astype(np.float32)
+    D = rng.standard_normal((K, C)).astype(np.float32)
+    D /= np.linalg.norm(D, axis=1, keepdims=True)
+    D *= 0.02 * np.sqrt(C / (S * k))
+    g = (0.5 ** np.arange(S)).astype(np.float32)
+    want = oracle.hsdr_mp(t, D, g, S, k)
+    got = gpu_codes(gpu, t, D, g, S, k)
+    assert np.array_equal(got, want)
+
+
+def test_compress_matches_reference(gpu, enc):
+    """The whole stream is the reference's byte for byte when this CPU's reciprocal square
+    root is the one the fixtures were written with (the dictionary is then identical, see
+    test_init_dictionary_matches_reference); on another CPU model the dictionary may differ
+    in the last bits (as the reference's own would), and the rest is checked around it."""
+    from cortexsdr_amd import encode
+
+    for i in range(n_cases(enc)):
+        w, ref = enc[f"enc_{i}_w"], enc[f"enc_{i}_stream"].tobytes()
+        tr, tc, K, S, k = (int(x) for x in enc[f"enc_{i}_cfg"])
+        s = encode.compress(w, tr, tc, K, S, k, ksvd_iters=0, stage_decay=0.5)
+        assert len(s) == len(ref)
+        v, D, g, codes = stream_parts(s)
+        rv, rD, rg, rcodes = stream_parts(ref)
+        assert s[:36] == ref[:36] and np.array_equal(g, rg)
+        assert s[v.off_edge:] == ref[rv.off_edge:]
+        if np.array_equal(D.view(np.uint32), rD.view(np.uint32)):
+            assert s == ref, f"case {i}"
+        else:
+            ulp = np.abs(D.view(np.int32).astype(np.int64) - rD.view(np.int32).astype(np.int64))
+            # two Newton-refined reciprocal square roots (atom norm, global scale), each
+            # within ~3 ulp of the CPU-independent value
+            assert ulp.max() <= 8, f"case {i}: dictionary differs by {ulp.max()} ulp"
+            t = tiles_of(w, v.tile_rows, v.tile_cols)
+            assert np.array_equal(codes, gpu_codes(gpu, t, D, g, S, k))
+        assert oracle.hsdr_decompress(s).shape == w.shape
+
+
+def test_compress_rejects(gpu):
+    from cortexsdr_amd import _lib, encode
+
+    w = np.zeros((10, 64), np.float32)
+    with pytest.raises(ValueError):   # fewer tiles than atoms
+        encode.compress(w, 1, 64, 16, 2, 2)
+    with pytest.raises(_lib.CsdrError):
+        encode.compress(np.ones((64, 64), np.float32), 1, 64, 16, 2, 2, ksvd_iters=1)
+    with pytest.raises(_lib.CsdrError):   # tile size not a multiple of 8
+        encode.compress(np.ones((64, 60), np.float32), 1, 60, 16, 2, 2)

@@ -89,3 +89,28 @@ def test_fixtures_distinguish_summation_order(enc):
         v, D, g, codes = stream_parts(stream)
         wrong += int((sequential_mp(w, D, g, v.n_stages, v.k_per_stage) != codes).any(1).sum())
     assert wrong > 0
+
+
+def test_init_dictionary_matches_reference(enc):
+    """The library's host-side initialisation (csdr_hsdr_init_dictionary, host code: no GPU)
+    against the dictionaries the reference's compress wrote for the same tiles: bit for bit on
+    the CPU model the fixtures were written on (the reference's 1/sqrt is that CPU's
+    approximate reciprocal square root, which the library reproduces instruction for
+    instruction), within 8 ulp on another."""
+    from cortexsdr_amd import encode
+
+    import sys
+    sys.path.insert(0, GOLDEN)
+    from make_fixtures import cpu_model
+
+    same_cpu = cpu_model() == enc["cpu_model"].tobytes().decode()
+    for i, (w, stream, cfg) in enumerate(cases(enc)):
+        v, D, g, codes = stream_parts(stream)
+        t = tiles_of(w, v.tile_rows, v.tile_cols)
+        got = encode.init_dictionary(t, v.n_atoms, v.n_stages, v.k_per_stage)
+        if same_cpu:
+            assert np.array_equal(got.view(np.uint32), D.view(np.uint32)), f"case {i}"
+        else:   # another CPU's reciprocal square root: two Newton-refined factors, ~3 ulp each
+            ulp = np.abs(got.view(np.int32).astype(np.int64) - D.view(np.int32).astype(np.int64))
+            assert ulp.max() <= 8, f"case {i}"
+
