@@ -30,10 +30,13 @@
 #include "common.hpp"
 
 namespace csdr {
-// fitHierarchicalKSVD's dictionary initialisation, in the reference build's arithmetic
-// (hsdr_init.cpp).
+// fitHierarchicalKSVD's dictionary initialisation, in the reference build's arithmetic, the
+// mean tile norm and atomUpdateStep's re-seed of an atom (hsdr_init.cpp).
 void hsdr_init_dictionary(const float* tiles, uint32_t n, uint32_t C, uint16_t K, uint32_t slots,
-                          float* D);
+                          float* D, std::mt19937* rng);
+double hsdr_mean_tile_norm(const float* tiles, uint32_t n, uint32_t C);
+void hsdr_reseed_atom(const float* tiles, uint32_t n, uint32_t C, uint64_t base_seed, uint32_t j,
+                      uint32_t mul, double target_norm, float* atom);
 }  // namespace csdr
 
 namespace {
@@ -200,6 +203,99 @@ int launch_mp(const float* tiles, long long n, int C, const float* D, int K, int
     return CSDR_OK;
 }
 
+// ---------------------------------------------------------------- K-SVD atom update
+
+// atomUpdateStep (HierarchicalSDRStrategy.cpp:281-490) on the device, per refinement pass:
+//  residual_kernel: residual = tile - sum over slots of gamma_l * sign * D[idx], one thread
+//    per element, slots in order, each term fused (the reference's r[c] += scale * atom[c],
+//    :300-311), then tile - recon (:316-320);
+//  atom_update_kernel: one workgroup per atom with users; correction[c] = sum over the atom's
+//    users, in (tile, slot) order, of sign * gamma * residual (double, fused: :428-437), the
+//    new value atom + correction * (0.5 / sum gamma^2) rounded to float (:448-458), a
+//    non-finite value flags the atom for the host's re-seed (:461), the squared norm summed
+//    in element order as the reference's loop does (:456), and atoms longer than the cap
+//    scaled back to the target norm (:482-487). Atoms without users are re-seeded by the
+//    host (:411-425).
+struct ResArgs {
+    const float* tiles;
+    const float* D;
+    const uint16_t* codes;
+    float* res;
+    long long n;
+    int C, S, k;
+    float gamma[kMaxStages];
+};
+
+__global__ __launch_bounds__(kEThreads) void residual_kernel(ResArgs a) {
+    const long long total = a.n * a.C;
+    const int slots = a.S * a.k;
+    for (long long e = (long long)blockIdx.x * kEThreads + threadIdx.x; e < total;
+         e += (long long)gridDim.x * kEThreads) {
+        const long long i = e / a.C;
+        const int c = (int)(e - i * a.C);
+        const uint16_t* cd = a.codes + i * slots;
+        float rec = 0.0f;
+        for (int sl = 0; sl < slots; ++sl) {
+            const uint16_t v = cd[sl];
+            const float scale = a.gamma[sl / a.k] * ((v & 0x8000) ? -1.0f : 1.0f);
+            rec = fmaf(scale, a.D[(size_t)(v & 0x7FFF) * a.C + c], rec);
+        }
+        a.res[e] = a.tiles[e] - rec;
+    }
+}
+
+constexpr uint8_t kAtomKept = 0, kAtomNonFinite = 1, kAtomDead = 2;
+
+__global__ __launch_bounds__(kEThreads) void atom_update_kernel(
+    const float* __restrict__ res, int C, float* __restrict__ D, const int* __restrict__ off,
+    const uint32_t* __restrict__ utile, const double* __restrict__ ucoef,
+    const double* __restrict__ inv_w, double cap, double target, uint8_t* __restrict__ flag) {
+    extern __shared__ float nv[];  // C: the atom's new values
+    __shared__ double nsq_s;
+    const int j = blockIdx.x, tid = threadIdx.x;
+    const int u0 = off[j], u1 = off[j + 1];
+    if (u0 == u1) {
+        if (tid == 0) flag[j] = kAtomDead;
+        return;
+    }
+    const double iw = inv_w[j];
+    if (iw == 0.0) {  // sum of gamma^2 <= 1e-12: the atom stays
+        if (tid == 0) flag[j] = kAtomKept;
+        return;
+    }
+    float* atom = D + (size_t)j * C;
+    int bad = 0;
+    for (int c = tid; c < C; c += kEThreads) {
+        double corr = 0.0;
+        for (int u = u0; u < u1; ++u)
+            corr = fma(ucoef[u], (double)res[(size_t)utile[u] * C + c], corr);
+        const double v = fma(corr, iw, (double)atom[c]);
+        const float vf = (float)v;
+        if (!isfinite(v) || !isfinite(vf)) bad = 1;
+        nv[c] = vf;
+    }
+    if (__syncthreads_or(bad)) {
+        if (tid == 0) flag[j] = kAtomNonFinite;
+        return;
+    }
+    if (tid == 0) {
+        double sq = 0.0;
+        for (int c = 0; c < C; ++c) sq = fma((double)nv[c], (double)nv[c], sq);
+        nsq_s = sq;
+        flag[j] = isfinite(sq) ? kAtomKept : kAtomNonFinite;
+    }
+    __syncthreads();
+    const double nsq = nsq_s;
+    if (!isfinite(nsq)) return;
+    const double nn = sqrt(nsq);
+    if (nn > cap) {
+        const double sc = target / nn;
+        for (int c = tid; c < C; c += kEThreads) atom[c] = (float)((double)nv[c] * sc);
+    } else {
+        for (int c = tid; c < C; c += kEThreads) atom[c] = nv[c];
+    }
+}
+
 // ---------------------------------------------------------------- compress (host side)
 
 struct Geometry {
@@ -239,6 +335,115 @@ size_t stream_bytes(const Geometry& g) {
            (size_t)g.n_tiles * g.S * g.k * 2 + (size_t)g.edge_floats * 4;
 }
 
+// A device allocation freed with its scope.
+struct DevBuf {
+    void* p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    float* f() const { return static_cast<float*>(p); }
+    uint16_t* u16() const { return static_cast<uint16_t*>(p); }
+};
+
+// One atomUpdateStep per pass (HierarchicalSDRStrategy.cpp:281-490): the users of every atom
+// gathered on the host from the current codes in (tile, slot) order (:325-339) with their
+// sign * gamma and the sum of gamma^2 (fused, :428-437), the residuals and the updates on the
+// device, the re-seeds on the host from the fit's generator (base seed :403).
+struct Refine {
+    DevBuf res, off, utile, ucoef, invw, flag;
+    double target = 0.0, cap = 0.0;
+
+    int init(const Geometry& g, const std::vector<float>& tiles, hipStream_t) {
+        const size_t slots = (size_t)g.S * g.k, ncodes = (size_t)g.n_tiles * slots;
+        target = std::max(1e-6, csdr::hsdr_mean_tile_norm(tiles.data(), g.n_tiles, g.tile_dim) /
+                                    std::sqrt((double)slots));  // :390-392
+        cap = 1.5 * target;
+        CSDR_HIP_CHECK(hipMalloc(&res.p, tiles.size() * 4));
+        CSDR_HIP_CHECK(hipMalloc(&off.p, ((size_t)g.K + 1) * 4));
+        CSDR_HIP_CHECK(hipMalloc(&utile.p, std::max<size_t>(ncodes, 1) * 4));
+        CSDR_HIP_CHECK(hipMalloc(&ucoef.p, std::max<size_t>(ncodes, 1) * 8));
+        CSDR_HIP_CHECK(hipMalloc(&invw.p, (size_t)g.K * 8));
+        CSDR_HIP_CHECK(hipMalloc(&flag.p, (size_t)g.K));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&atom_update_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)(g.tile_dim * 4));
+        return CSDR_OK;
+    }
+
+    int pass(const Geometry& g, const std::vector<float>& tiles, const std::vector<float>& gamma,
+             const float* d_tiles, float* d_D, const uint16_t* d_codes, std::mt19937& rng,
+             hipStream_t st) {
+        const size_t slots = (size_t)g.S * g.k, ncodes = (size_t)g.n_tiles * slots;
+        const uint32_t C = g.tile_dim;
+        std::vector<uint16_t> codes(ncodes);
+        CSDR_HIP_CHECK(
+            hipMemcpyAsync(codes.data(), d_codes, ncodes * 2, hipMemcpyDeviceToHost, st));
+        CSDR_HIP_CHECK(hipStreamSynchronize(st));
+        std::vector<int> offs((size_t)g.K + 1, 0);
+        for (uint16_t v : codes) {
+            if ((v & 0x7FFF) >= g.K) return set_error(CSDR_E_INVALID, "hsdr_compress: bad code");
+            ++offs[(v & 0x7FFF) + 1];
+        }
+        for (uint32_t j = 0; j < g.K; ++j) offs[j + 1] += offs[j];
+        std::vector<int> pos(offs.begin(), offs.end() - 1);
+        std::vector<uint32_t> ut(ncodes);
+        std::vector<double> uc(ncodes), wsum(g.K, 0.0), iw(g.K, 0.0);
+        for (size_t i = 0; i < g.n_tiles; ++i)
+            for (size_t sl = 0; sl < slots; ++sl) {
+                const uint16_t v = codes[i * slots + sl];
+                const uint32_t j = v & 0x7FFF;
+                const double gm = (double)gamma[sl / g.k];
+                const int p = pos[j]++;
+                ut[p] = (uint32_t)i;
+                uc[p] = ((v & 0x8000) ? -1.0 : 1.0) * gm;
+                wsum[j] = std::fma(gm, gm, wsum[j]);
+            }
+        for (uint32_t j = 0; j < g.K; ++j) iw[j] = wsum[j] <= 1e-12 ? 0.0 : 0.5 / wsum[j];
+        CSDR_HIP_CHECK(
+            hipMemcpyAsync(off.p, offs.data(), offs.size() * 4, hipMemcpyHostToDevice, st));
+        CSDR_HIP_CHECK(hipMemcpyAsync(utile.p, ut.data(), ncodes * 4, hipMemcpyHostToDevice, st));
+        CSDR_HIP_CHECK(hipMemcpyAsync(ucoef.p, uc.data(), ncodes * 8, hipMemcpyHostToDevice, st));
+        CSDR_HIP_CHECK(hipMemcpyAsync(invw.p, iw.data(), iw.size() * 8, hipMemcpyHostToDevice, st));
+        const uint64_t base_seed = static_cast<uint64_t>(rng()) ^ 0xA0B1C2D3u;
+
+        ResArgs ra{};
+        ra.tiles = d_tiles;
+        ra.D = d_D;
+        ra.codes = d_codes;
+        ra.res = res.f();
+        ra.n = g.n_tiles;
+        ra.C = (int)C;
+        ra.S = g.S;
+        ra.k = g.k;
+        for (uint32_t l = 0; l < g.S; ++l) ra.gamma[l] = gamma[l];
+        const long long total = (long long)g.n_tiles * C;
+        const int rgrid = (int)std::min<long long>((total + kEThreads - 1) / kEThreads, 16384);
+        residual_kernel<<<rgrid, kEThreads, 0, st>>>(ra);
+        CSDR_LAUNCH_CHECK("hsdr_compress residual");
+        atom_update_kernel<<<g.K, kEThreads, (size_t)C * 4, st>>>(
+            res.f(), (int)C, d_D, static_cast<const int*>(off.p),
+            static_cast<const uint32_t*>(utile.p), static_cast<const double*>(ucoef.p),
+            static_cast<const double*>(invw.p), cap, target, static_cast<uint8_t*>(flag.p));
+        CSDR_LAUNCH_CHECK("hsdr_compress atom update");
+        std::vector<uint8_t> fl(g.K);
+        CSDR_HIP_CHECK(hipMemcpyAsync(fl.data(), flag.p, g.K, hipMemcpyDeviceToHost, st));
+        CSDR_HIP_CHECK(hipStreamSynchronize(st));
+        std::vector<float> atom(C);
+        for (uint32_t j = 0; j < g.K; ++j) {
+            if (fl[j] == kAtomKept) continue;
+            csdr::hsdr_reseed_atom(tiles.data(), g.n_tiles, C, base_seed, j,
+                                   fl[j] == kAtomDead ? 0x9E3779B1u : 0xB7E15163u, target,
+                                   atom.data());
+            CSDR_HIP_CHECK(hipMemcpy(d_D + (size_t)j * C, atom.data(), (size_t)C * 4,
+                                     hipMemcpyHostToDevice));
+        }
+        return CSDR_OK;
+    }
+};
+
 template <class T>
 void put(std::vector<uint8_t>& out, const T& v) {
     const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
@@ -267,7 +472,7 @@ CSDR_API int csdr_hsdr_init_dictionary(const float* tiles, uint32_t n_tiles, uin
         k_per_stage == 0)
         return set_error(CSDR_E_INVALID, "hsdr_init_dictionary: bad argument");
     csdr::hsdr_init_dictionary(tiles, n_tiles, tile_dim, n_atoms,
-                               (uint32_t)n_stages * k_per_stage, D);
+                               (uint32_t)n_stages * k_per_stage, D, nullptr);
     return CSDR_OK;
 }
 
@@ -291,8 +496,9 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
     if (rc != CSDR_OK) return rc;
     if (out_bytes < stream_bytes(g))
         return set_error(CSDR_E_INVALID, "hsdr_compress: output buffer too small");
-    if (ksvd_iters != 0)
-        return set_error(CSDR_E_UNSUPPORTED, "hsdr_compress: K-SVD refinement not built");
+    if (ksvd_iters != 0 && g.tile_dim > 32768)
+        return set_error(CSDR_E_UNSUPPORTED,
+                         "hsdr_compress: K-SVD refinement takes tiles of at most 32768 values");
     rc = check_mp_shape(g.n_tiles, (int)g.tile_dim, g.K, g.S, g.k);
     if (rc != CSDR_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
@@ -311,45 +517,37 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
     std::vector<float> gamma(g.S), D;
     for (uint32_t l = 0; l < g.S; ++l) gamma[l] = std::pow(stage_decay, (float)l);
     D.assign((size_t)g.K * g.tile_dim, 0.0f);
+    std::mt19937 rng(0xC0DE);  // the fit's generator (:513), through init and every pass
     csdr::hsdr_init_dictionary(tiles.data(), g.n_tiles, g.tile_dim, g.K, (uint32_t)g.S * g.k,
-                               D.data());
+                               D.data(), &rng);
 
     const size_t slots = (size_t)g.S * g.k, ncodes = (size_t)g.n_tiles * slots;
     std::vector<uint16_t> codes(ncodes);
-    float *d_tiles = nullptr, *d_D = nullptr;
-    uint16_t* d_codes = nullptr;
-    auto cleanup = [&] {
-        if (d_tiles) (void)hipFree(d_tiles);
-        if (d_D) (void)hipFree(d_D);
-        if (d_codes) (void)hipFree(d_codes);
-    };
-    auto hip_fail = [&](hipError_t e, const char* what) {
-        cleanup();
-        return set_error(CSDR_E_HIP, std::string("hsdr_compress: ") + what + ": " +
-                                         hipGetErrorString(e));
-    };
-    hipError_t e;
-    if ((e = hipMalloc(&d_tiles, tiles.size() * 4)) != hipSuccess) return hip_fail(e, "malloc");
-    if ((e = hipMalloc(&d_D, D.size() * 4)) != hipSuccess) return hip_fail(e, "malloc");
-    if ((e = hipMalloc(&d_codes, std::max<size_t>(ncodes * 2, 2))) != hipSuccess)
-        return hip_fail(e, "malloc");
-    if ((e = hipMemcpyAsync(d_tiles, tiles.data(), tiles.size() * 4, hipMemcpyHostToDevice,
-                            st)) != hipSuccess)
-        return hip_fail(e, "upload");
-    if ((e = hipMemcpyAsync(d_D, D.data(), D.size() * 4, hipMemcpyHostToDevice, st)) !=
-        hipSuccess)
-        return hip_fail(e, "upload");
-    rc = launch_mp(d_tiles, g.n_tiles, (int)g.tile_dim, d_D, g.K, g.S, g.k, gamma.data(),
-                   d_codes, st);
-    if (rc != CSDR_OK) {
-        cleanup();
-        return rc;
+    DevBuf d_tiles, d_D, d_codes;
+    CSDR_HIP_CHECK(hipMalloc(&d_tiles.p, tiles.size() * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_D.p, D.size() * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_codes.p, std::max<size_t>(ncodes * 2, 2)));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_tiles.p, tiles.data(), tiles.size() * 4,
+                                  hipMemcpyHostToDevice, st));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_D.p, D.data(), D.size() * 4, hipMemcpyHostToDevice, st));
+    rc = launch_mp(d_tiles.f(), g.n_tiles, (int)g.tile_dim, d_D.f(), g.K, g.S, g.k,
+                   gamma.data(), d_codes.u16(), st);
+    if (rc != CSDR_OK) return rc;
+    if (ksvd_iters) {
+        Refine rf;
+        rc = rf.init(g, tiles, st);
+        if (rc != CSDR_OK) return rc;
+        for (int it = 0; it < ksvd_iters; ++it) {  // atom update, then encode again (:570-573)
+            rc = rf.pass(g, tiles, gamma, d_tiles.f(), d_D.f(), d_codes.u16(), rng, st);
+            if (rc != CSDR_OK) return rc;
+            rc = launch_mp(d_tiles.f(), g.n_tiles, (int)g.tile_dim, d_D.f(), g.K, g.S, g.k,
+                           gamma.data(), d_codes.u16(), st);
+            if (rc != CSDR_OK) return rc;
+        }
+        CSDR_HIP_CHECK(hipMemcpyAsync(D.data(), d_D.p, D.size() * 4, hipMemcpyDeviceToHost, st));
     }
-    if ((e = hipMemcpyAsync(codes.data(), d_codes, ncodes * 2, hipMemcpyDeviceToHost, st)) !=
-        hipSuccess)
-        return hip_fail(e, "download");
-    if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "synchronize");
-    cleanup();
+    CSDR_HIP_CHECK(hipMemcpyAsync(codes.data(), d_codes.p, ncodes * 2, hipMemcpyDeviceToHost, st));
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
     for (float& x : D)  // the fit's final sanitisation (:592-601)
         if (!std::isfinite(x)) x = 0.0f;
 

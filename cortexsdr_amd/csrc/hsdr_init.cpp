@@ -17,6 +17,8 @@
 //     rsqrtss differs between CPU models, and so does the reference's dictionary; this code
 //     reproduces the reference on the CPU it runs on;
 //   * the mean tile norm in double (FMA sums), divided by n, rounded to float.
+// The atom re-seeding of atomUpdateStep (:411-425, :461-474) is here too: a tile picked by a
+// per-atom generator, scaled to the target norm in double.
 #include <immintrin.h>
 
 #include <algorithm>
@@ -62,9 +64,24 @@ float squared_norm(const float* d, uint32_t C) {
 
 }  // namespace
 
+// Mean of the tiles' Euclidean norms, in double (fitHierarchicalKSVD :529-536, atomUpdateStep
+// :374-383, whose OpenMP reduction sums per-thread partials: its last bits follow the thread
+// count).
+double hsdr_mean_tile_norm(const float* tiles, uint32_t n, uint32_t C) {
+    double norm_sum = 0.0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const float* t = tiles + (size_t)i * C;
+        double sq = 0.0;
+        for (uint32_t c = 0; c < C; ++c) sq = std::fma((double)t[c], (double)t[c], sq);
+        norm_sum += std::sqrt(sq);
+    }
+    return norm_sum / (double)std::max<uint32_t>(1u, n);
+}
+
 void hsdr_init_dictionary(const float* tiles, uint32_t n, uint32_t C, uint16_t K,
-                          uint32_t slots, float* D) {
-    std::mt19937 rng(0xC0DE);
+                          uint32_t slots, float* D, std::mt19937* rng_io) {
+    std::mt19937 local(0xC0DE);
+    std::mt19937& rng = rng_io ? *rng_io : local;  // the fit's generator, seeded 0xC0DE
     std::uniform_int_distribution<uint32_t> pick(0, n - 1);
     for (uint32_t j = 0; j < K; ++j) {
         const uint32_t src = pick(rng);
@@ -73,17 +90,25 @@ void hsdr_init_dictionary(const float* tiles, uint32_t n, uint32_t C, uint16_t K
         const float r = rsqrt_newton(std::max(squared_norm(d, C), 1e-24f));
         for (uint32_t c = 0; c < C; ++c) d[c] = d[c] * r;
     }
-    double norm_sum = 0.0;
-    for (uint32_t i = 0; i < n; ++i) {
-        const float* t = tiles + (size_t)i * C;
-        double sq = 0.0;
-        for (uint32_t c = 0; c < C; ++c) sq = std::fma((double)t[c], (double)t[c], sq);
-        norm_sum += std::sqrt(sq);
-    }
-    float scale = (float)(norm_sum / (double)std::max<uint32_t>(1u, n));
+    float scale = (float)(hsdr_mean_tile_norm(tiles, n, C));
     const float s = (float)slots;
     if (s > 1.0f) scale = scale * rsqrt_newton(s);
     for (size_t i = 0; i < (size_t)K * C; ++i) D[i] = D[i] * scale;
+}
+
+// atomUpdateStep's re-seed of atom j (:411-425 for an atom nobody uses, seed constant
+// 0x9E3779B1; :461-474 for one whose update was not finite, 0xB7E15163; base_seed :403): the
+// tile picked by
+// std::mt19937((uint32_t)(base_seed ^ (j * mul))) over [0, n - 1], scaled to target_norm.
+void hsdr_reseed_atom(const float* tiles, uint32_t n, uint32_t C, uint64_t base_seed, uint32_t j,
+                      uint32_t mul, double target_norm, float* atom) {
+    std::mt19937 local(static_cast<uint32_t>(base_seed ^ (uint64_t)(j * mul)));
+    std::uniform_int_distribution<uint32_t> pick(0, n - 1);
+    const float* src = tiles + (size_t)pick(local) * C;
+    double sq = 0.0;
+    for (uint32_t c = 0; c < C; ++c) sq = std::fma((double)src[c], (double)src[c], sq);
+    const double s = target_norm / std::sqrt(std::max(sq, 1e-30));
+    for (uint32_t c = 0; c < C; ++c) atom[c] = (float)((double)src[c] * s);
 }
 
 }  // namespace csdr

@@ -226,8 +226,11 @@ CSDR_API int csdr_hsdr_init_dictionary(const float* tiles, uint32_t n_tiles, uin
  * rows x cols host matrix w into out (csdr_hsdr_compress_bytes bytes): tile_rows == 1 widens
  * tiles to whole rows (configFor :1024-1046); dictionary as csdr_hsdr_init_dictionary, one
  * matching-pursuit pass on the GPU (csdr_hsdr_encode), edge strips as fp32, stage scales
- * stage_decay^l: the reference's stream byte for byte on the same CPU. ksvd_iters must be 0
- * (the atom update is not built: CSDR_E_UNSUPPORTED). */
+ * stage_decay^l: with ksvd_iters = 0 the reference's stream byte for byte on the same CPU.
+ * ksvd_iters > 0 adds that many atomUpdateStep passes (:281-490: users per atom in (tile,
+ * slot) order, double corrections damped by 0.5 / sum gamma^2, the norm cap, re-seeds from the
+ * fit's generator; residuals and updates on the GPU), each followed by matching pursuit again
+ * (:570-573); tiles of at most 32768 values. */
 CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, uint16_t tile_rows,
                                 uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages,
                                 uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,

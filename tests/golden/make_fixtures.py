@@ -37,6 +37,8 @@ and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
              pick. cfg = (tile_rows, tile_cols, K, stages, k per stage). cpu_model: the CPU
              the reference ran on (its dictionary initialisation uses that CPU's approximate
              reciprocal square root).
+  fit_<i>_w, fit_<i>_stream, fit_<i>_cfg  the same compress with ksvd_iters = 3..6 (atom
+             updates and re-encodes); cfg = (tile_rows, tile_cols, K, stages, k, iters).
 
 Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode]
 """
@@ -192,6 +194,15 @@ def encode_main() -> None:
         out[f"enc_{i}_stream"] = np.frombuffer(
             oracle.ref_hsdr_compress(w, tr, tc, K, S, k, ksvd_iters=0), np.uint8)
         out[f"enc_{i}_cfg"] = np.array(cfg, np.int32)
+    for i, (R, Cc, tr, tc, K, S, k, it) in enumerate([(64, 256, 1, 256, 32, 3, 4, 4),
+                                                       (200, 96, 1, 96, 48, 2, 3, 3),
+                                                       (96, 96, 8, 16, 32, 3, 2, 3),
+                                                       (256, 64, 1, 64, 64, 3, 5, 6)]):
+        w = (rng.standard_normal((R, Cc)) * 0.02).astype(np.float32)
+        out[f"fit_{i}_w"] = w
+        out[f"fit_{i}_stream"] = np.frombuffer(
+            oracle.ref_hsdr_compress(w, tr, tc, K, S, k, ksvd_iters=it), np.uint8)
+        out[f"fit_{i}_cfg"] = np.array([tr, tc, K, S, k, it], np.int32)
     out["cpu_model"] = np.frombuffer(cpu_model().encode(), np.uint8)
     path = os.path.join(HERE, "hsdr_encode_fixtures.npz")
     np.savez_compressed(path, **out)

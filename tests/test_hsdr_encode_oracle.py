@@ -25,7 +25,7 @@ def enc():
 
 
 def cases(enc):
-    n = len([k for k in enc.files if k.endswith("_stream")])
+    n = len([k for k in enc.files if k.startswith("enc_") and k.endswith("_stream")])
     return [(enc[f"enc_{i}_w"], enc[f"enc_{i}_stream"].tobytes(), enc[f"enc_{i}_cfg"])
             for i in range(n)]
 
