@@ -21,6 +21,9 @@ The JSON line carries:
                 HSDB-coded against one shared 1024 x 64 dictionary), 512-token prompt of
                 uniform random ids, then greedy decode of 128 tokens; tokens/s of the decode
                 phase next to a KV-cached CPU decode step of the same model (oracle/)
+  encode        the compress side: GPU matching pursuit (rows/s, TFLOP/s against the fp32
+                vector peak) and compress wall time on Qwen2-0.5B-shaped attention / MLP
+                matrices, next to the reference's own compress (oracle/_ref)
 """
 from __future__ import annotations
 
@@ -54,6 +57,7 @@ def parse():
     ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2"])
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
     ap.add_argument("--decode-cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--no-encode", action="store_true", help="skip the HSDR encoder leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy 5 times (the reference dispatch "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -180,6 +184,75 @@ def decode_leg(args):
             "value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": (f"{n} KV-cached decode steps at context {n_prompt + n_new // 2} through "
                        f"oracle/ (orc_hsdb_matmul OpenMP linears), {dt * 1e3:.0f} ms/token")}
+    return out
+
+
+# fp32 vector FMA peak without packed-FP32 instructions (this build disables them):
+# 256 CUs x 64 FMA lanes x 2 FLOP x 2.4 GHz
+VALU_FP32_PEAK_TFLOPS = 78.6
+
+
+def encode_leg(args):
+    """The compress side (HSDR encoder): matching pursuit of every row of a Qwen2-0.5B-shaped
+    attention (896 x 896, the reference's default K=256, 3 x 5 picks) and MLP (4864 x 896,
+    forMLP: K=512, 3 x 8) matrix, 1-row tiles, on the GPU (csdr_hsdr_encode), and compress with
+    the reference's default refinement passes (8 / 12); next to the reference's own compress
+    (oracle/_ref, its OpenMP build) with no refinement on the same matrices."""
+    import ctypes as C
+
+    import torch
+
+    import oracle
+    from cortexsdr_amd import _lib, encode
+
+    lib = _lib.load()
+    rng = np.random.default_rng(9)
+    out = []
+    for name, R, Cc, K, S, k, iters in (("attn 896x896", 896, 896, 256, 3, 5, 8),
+                                        ("mlp 4864x896", 4864, 896, 512, 3, 8, 12)):
+        w = (rng.standard_normal((R, Cc)) * 0.02).astype(np.float32)
+        D = encode.init_dictionary(w, K, S, k)
+        g = (0.5 ** np.arange(S)).astype(np.float32)
+        td = torch.from_numpy(w).cuda()
+        Dd = torch.from_numpy(D).cuda()
+        codes = torch.empty((R, S * k), dtype=torch.int16, device="cuda")
+        st = torch.cuda.current_stream()
+        args_ = (td.data_ptr(), R, Cc, Dd.data_ptr(), K, S, k, g.ctypes.data, codes.data_ptr(),
+                 st.cuda_stream)
+        _lib.check(lib.csdr_hsdr_encode(*args_))
+        reps = 20
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            _lib.check(lib.csdr_hsdr_encode(*args_))
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        flops = 2.0 * R * S * k * K * Cc
+        encode.compress(w, 1, Cc, K, S, k, ksvd_iters=0)   # warm
+        t0 = time.perf_counter()
+        encode.compress(w, 1, Cc, K, S, k, ksvd_iters=0)
+        gpu_c0 = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        encode.compress(w, 1, Cc, K, S, k, ksvd_iters=iters)
+        gpu_fit = time.perf_counter() - t0
+        row = {"matrix": name, "K": K, "stages": S, "k_per_stage": k,
+               "encode_us": round(us, 1), "rows_per_s": round(R / (us * 1e-6), 1),
+               "encode_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+               "valu_frac": round(flops / (us * 1e-6) / 1e12 / VALU_FP32_PEAK_TFLOPS, 4),
+               "compress_s": round(gpu_c0, 4), "ksvd_iters": iters,
+               "compress_fit_s": round(gpu_fit, 4), "cpu_reference": None}
+        if not args.no_cpu and oracle.ref() is not None:
+            oracle.ref_hsdr_compress(w[:64], 1, Cc, min(K, 64), S, k, ksvd_iters=0)
+            t0 = time.perf_counter()
+            oracle.ref_hsdr_compress(w, 1, Cc, K, S, k, ksvd_iters=0)
+            dt = time.perf_counter() - t0
+            threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+            row["cpu_reference"] = {
+                "compress_s": round(dt, 4), "cores": threads, "kind": "reference",
+                "sample": "HierarchicalSDRStrategy::compress, ksvd_iters = 0, same matrix"}
+        out.append(row)
     return out
 
 
@@ -337,6 +410,8 @@ def main():
         }
     if not args.no_decode:
         out["decode"] = decode_leg(args)
+    if not args.no_encode:
+        out["encode"] = encode_leg(args)
     if args.calibrate_copy:
         a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)

@@ -46,6 +46,7 @@ using csdr::set_error;
 constexpr int kEThreads = 256;
 constexpr int kEGroups = kEThreads / 16;
 constexpr int kMaxTT = 8;        // tiles per workgroup, at most
+constexpr int kDB = 16;          // chunks of an atom loaded per block
 constexpr int kMaxStages = 32;
 constexpr size_t kLdsSoft = 64 * 1024;    // several workgroups per CU below this
 constexpr size_t kLdsHard = 160 * 1024;
@@ -59,57 +60,66 @@ struct MpArgs {
     float gamma[kMaxStages];
 };
 
+template <int TT>
 __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
     extern __shared__ float smem[];
-    const int tt = a.tt, C = a.C, K = a.K;
+    const int tt = TT, C = a.C, K = a.K;
     const long long t0 = (long long)blockIdx.x * tt;
     const int nt = (int)min((long long)tt, a.n - t0);
     float* r = smem;                                                    // nt x C residuals
     float* proj = r + (size_t)tt * C;                                   // nt x K scores
     uint8_t* used = reinterpret_cast<uint8_t*>(proj + (size_t)tt * K);  // nt x K
-    __shared__ int best_s[kMaxTT];
-    __shared__ float scale_s[kMaxTT];
+    __shared__ int best_s[TT];
+    __shared__ float scale_s[TT];
     const int tid = threadIdx.x, l16 = tid & 15, grp = tid >> 4;
     const int lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < nt * C; i += kEThreads) r[i] = a.tiles[t0 * C + i];
+    for (int i = tid; i < TT * C; i += kEThreads) r[i] = i < nt * C ? a.tiles[t0 * C + i] : 0.f;
     const int C16 = C & ~15, C8 = C & ~7;  // end of the 16-element chunks, of the 8-element one
+    const int nch = C16 / 16;  // full 16-element chunks (block loads clamp into them)
     const int slots = a.S * a.k;
     for (int l = 0; l < a.S; ++l) {
         for (int i = tid; i < nt * K; i += kEThreads) used[i] = 0;
         __syncthreads();
         for (int st = 0; st < a.k; ++st) {
-            // 1. projections of every tile onto every atom
+            // 1. projections of every tile onto every atom: the atom's values 16 chunks at
+            // a time, the next block in flight while this one is used (loads clamp into the
+            // row's full chunks: in bounds, uniform, so the waits stay per block); tile slots
+            // past nt hold zeros and are computed too (no per-tile branches)
             for (int j = grp; j < K; j += kEGroups) {
-                const float* dj = a.D + (size_t)j * C;
-                float p[kMaxTT];
+                const float* dj = a.D + (size_t)j * C + l16;
+                float p[TT];
 #pragma unroll
-                for (int t = 0; t < kMaxTT; ++t) p[t] = 0.f;
-                for (int c = l16; c < C16; c += 16) {
-                    const float dv = dj[c];
+                for (int t = 0; t < TT; ++t) p[t] = 0.f;
+                float cur[kDB], nxt[kDB];
 #pragma unroll
-                    for (int t = 0; t < kMaxTT; ++t)
-                        if (t < nt) p[t] = fmaf(dv, r[t * C + c], p[t]);
+                for (int q = 0; q < kDB; ++q) cur[q] = nch ? dj[min(q, nch - 1) * 16] : 0.f;
+                for (int b0 = 0; b0 < nch; b0 += kDB) {
+#pragma unroll
+                    for (int q = 0; q < kDB; ++q) nxt[q] = dj[min(b0 + kDB + q, nch - 1) * 16];
+#pragma unroll
+                    for (int q = 0; q < kDB; ++q) {
+                        if (b0 + q >= nch) break;
+                        const float* rc = r + (b0 + q) * 16 + l16;
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) p[t] = fmaf(cur[q], rc[t * C], p[t]);
+                    }
+#pragma unroll
+                    for (int q = 0; q < kDB; ++q) cur[q] = nxt[q];
                 }
                 if (C8 > C16 && l16 < 8) {
-                    const int c = C16 + l16;
-                    const float dv = dj[c];
+                    const float dv = dj[C16];
+                    const float* rc = r + C16 + l16;
 #pragma unroll
-                    for (int t = 0; t < kMaxTT; ++t)
-                        if (t < nt) p[t] = fmaf(dv, r[t * C + c], p[t]);
+                    for (int t = 0; t < TT; ++t) p[t] = fmaf(dv, rc[t * C], p[t]);
                 }
 #pragma unroll
-                for (int t = 0; t < kMaxTT; ++t) {
+                for (int t = 0; t < TT; ++t) {
                     float v = p[t];
                     v += __shfl_xor(v, 8, 16);  // acc0 + acc1
                     v += __shfl_xor(v, 4, 16);  // low + high 128 bits
                     v += __shfl_xor(v, 1, 16);  // horizontal add
                     v += __shfl_xor(v, 2, 16);  // horizontal add
-                    p[t] = v;
-                }
-                if (l16 == 0) {
-#pragma unroll
-                    for (int t = 0; t < kMaxTT; ++t)
-                        if (t < nt) proj[t * K + j] = used[t * K + j] ? 0.0f : p[t];
+                    if (l16 == 0 && t < nt) proj[t * K + j] = used[t * K + j] ? 0.0f : v;
                 }
             }
             __syncthreads();
@@ -157,11 +167,13 @@ size_t mp_lds_bytes(int tt, int C, int K) {
     return (size_t)tt * ((size_t)C + K) * 4 + csdr::align_up((size_t)tt * K, 16);
 }
 
-// Tiles per workgroup: as many as fit (up to 8) under the soft LDS size, else one tile under
-// the hard one, else 0 (too large).
-int mp_tiles_per_wg(int C, int K) {
-    for (int tt = kMaxTT; tt >= 1; --tt)
-        if (mp_lds_bytes(tt, C, K) <= kLdsSoft) return tt;
+// Tiles per workgroup: about n / 256 (a grid that covers the CUs; every workgroup reads all
+// of D once per pick, so more tiles per workgroup is less D traffic), at most 8 and what fits
+// under the soft LDS size; else one tile under the hard size; else 0 (too large).
+int mp_tiles_per_wg(long long n, int C, int K) {
+    const long long want = std::min<long long>(kMaxTT, std::max<long long>(1, n / 256));
+    for (int tt = kMaxTT; tt >= 1; tt >>= 1)  // a power of two (the kernel's template)
+        if (tt <= want && mp_lds_bytes(tt, C, K) <= kLdsSoft) return tt;
     return mp_lds_bytes(1, C, K) <= kLdsHard ? 1 : 0;
 }
 
@@ -173,7 +185,7 @@ int check_mp_shape(long long n, int C, int K, int S, int k) {
     if (K > 32768) return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: at most 32768 atoms");
     if (S > kMaxStages) return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: at most 32 stages");
     if (k > K) return set_error(CSDR_E_INVALID, "hsdr_encode: more picks per stage than atoms");
-    if (mp_tiles_per_wg(C, K) == 0)
+    if (mp_tiles_per_wg(n, C, K) == 0)
         return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: tile and dictionary exceed LDS");
     return CSDR_OK;
 }
@@ -190,15 +202,23 @@ int launch_mp(const float* tiles, long long n, int C, const float* D, int K, int
     a.K = K;
     a.S = S;
     a.k = k;
-    a.tt = mp_tiles_per_wg(C, K);
+    a.tt = mp_tiles_per_wg(n, C, K);
     for (int l = 0; l < S; ++l) a.gamma[l] = gamma[l];
     const size_t lds = mp_lds_bytes(a.tt, C, K);
-    if (lds > 64 * 1024)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&mp_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     const long long grid = (n + a.tt - 1) / a.tt;
     if (grid > 0x7fffffffLL) return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: too many tiles");
-    mp_kernel<<<(unsigned)grid, kEThreads, lds, st>>>(a);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        kern<<<(unsigned)grid, kEThreads, lds, st>>>(a);
+    };
+    switch (a.tt) {
+        case 8: go(&mp_kernel<8>); break;
+        case 4: go(&mp_kernel<4>); break;
+        case 2: go(&mp_kernel<2>); break;
+        default: go(&mp_kernel<1>); break;
+    }
     CSDR_LAUNCH_CHECK("hsdr_encode");
     return CSDR_OK;
 }
