@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <random>
 #include <string>
@@ -60,20 +61,47 @@ struct MpArgs {
     float gamma[kMaxStages];
 };
 
+// The TT tiles' residual values of one element (TT * 4 bytes, aligned to that size) in one
+// or two wide LDS reads.
+template <int TT>
+__device__ __forceinline__ void load_tiles(const float* rc, float* rv) {
+    if constexpr (TT % 4 == 0) {
+#pragma unroll
+        for (int t4 = 0; t4 < TT / 4; ++t4) {
+            const float4 v = reinterpret_cast<const float4*>(rc)[t4];
+            rv[4 * t4] = v.x;
+            rv[4 * t4 + 1] = v.y;
+            rv[4 * t4 + 2] = v.z;
+            rv[4 * t4 + 3] = v.w;
+        }
+    } else if constexpr (TT == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(rc);
+        rv[0] = v.x;
+        rv[1] = v.y;
+    } else {
+        rv[0] = rc[0];
+    }
+}
+
 template <int TT>
 __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
     extern __shared__ float smem[];
     const int tt = TT, C = a.C, K = a.K;
     const long long t0 = (long long)blockIdx.x * tt;
     const int nt = (int)min((long long)tt, a.n - t0);
-    float* r = smem;                                                    // nt x C residuals
+    float* r = smem;                                                    // C x TT residuals
     float* proj = r + (size_t)tt * C;                                   // nt x K scores
     uint8_t* used = reinterpret_cast<uint8_t*>(proj + (size_t)tt * K);  // nt x K
     __shared__ int best_s[TT];
     __shared__ float scale_s[TT];
     const int tid = threadIdx.x, l16 = tid & 15, grp = tid >> 4;
     const int lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < TT * C; i += kEThreads) r[i] = i < nt * C ? a.tiles[t0 * C + i] : 0.f;
+    // residuals tile-minor, r[c * TT + t] (one 16-byte LDS read gives four tiles' values of an
+    // element); slots past nt hold zeros
+    for (int i = tid; i < TT * C; i += kEThreads) {
+        const int c = i / TT, t = i - c * TT;
+        r[i] = t < nt ? a.tiles[(t0 + t) * C + c] : 0.f;
+    }
     const int C16 = C & ~15, C8 = C & ~7;  // end of the 16-element chunks, of the 8-element one
     const int nch = C16 / 16;  // full 16-element chunks (block loads clamp into them)
     const int slots = a.S * a.k;
@@ -99,18 +127,19 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
 #pragma unroll
                     for (int q = 0; q < kDB; ++q) {
                         if (b0 + q >= nch) break;
-                        const float* rc = r + (b0 + q) * 16 + l16;
+                        float rv[TT];
+                        load_tiles<TT>(r + ((b0 + q) * 16 + l16) * TT, rv);
 #pragma unroll
-                        for (int t = 0; t < TT; ++t) p[t] = fmaf(cur[q], rc[t * C], p[t]);
+                        for (int t = 0; t < TT; ++t) p[t] = fmaf(cur[q], rv[t], p[t]);
                     }
 #pragma unroll
                     for (int q = 0; q < kDB; ++q) cur[q] = nxt[q];
                 }
                 if (C8 > C16 && l16 < 8) {
                     const float dv = dj[C16];
-                    const float* rc = r + C16 + l16;
+                    const float* rc = r + (C16 + l16) * TT;
 #pragma unroll
-                    for (int t = 0; t < TT; ++t) p[t] = fmaf(dv, rc[t * C], p[t]);
+                    for (int t = 0; t < TT; ++t) p[t] = fmaf(dv, rc[t], p[t]);
                 }
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
@@ -156,7 +185,8 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
             // 3. r -= scale * D[best], fused
             for (int i = tid; i < nt * C; i += kEThreads) {
                 const int t = i / C, c = i - t * C;
-                r[i] = fmaf(-a.D[(size_t)best_s[t] * C + c], scale_s[t], r[i]);
+                float& rv = r[c * TT + t];
+                rv = fmaf(-a.D[(size_t)best_s[t] * C + c], scale_s[t], rv);
             }
             __syncthreads();
         }
@@ -167,11 +197,15 @@ size_t mp_lds_bytes(int tt, int C, int K) {
     return (size_t)tt * ((size_t)C + K) * 4 + csdr::align_up((size_t)tt * K, 16);
 }
 
-// Tiles per workgroup: about n / 256 (a grid that covers the CUs; every workgroup reads all
-// of D once per pick, so more tiles per workgroup is less D traffic), at most 8 and what fits
-// under the soft LDS size; else one tile under the hard size; else 0 (too large).
+// Tiles per workgroup: about n / 1024, at least 2 (measured on the Qwen2-0.5B shapes, 1-row
+// tiles: 896 x 896 best at 2 (0.93 ms vs 1.00 at 4, 1.31 at 8), 4864 x 896 at 4 (4.5 ms vs 5.0
+// at 8, 7.3 at 2): enough workgroups per CU to hide latency, and every workgroup reads all of
+// D once per pick, so more tiles each is less D traffic), a power of two, at most 8 and what
+// fits under the soft LDS size; else one tile under the hard size; else 0 (too large).
 int mp_tiles_per_wg(long long n, int C, int K) {
-    const long long want = std::min<long long>(kMaxTT, std::max<long long>(1, n / 256));
+    const char* ev = std::getenv("CSDR_HSDR_TILES_PER_WG");  // tuning override: 1, 2, 4 or 8
+    long long want = std::min<long long>(kMaxTT, std::max<long long>(2, n / 1024));
+    if (ev && std::atoi(ev) >= 1) want = std::min(kMaxTT, std::atoi(ev));
     for (int tt = kMaxTT; tt >= 1; tt >>= 1)  // a power of two (the kernel's template)
         if (tt <= want && mp_lds_bytes(tt, C, K) <= kLdsSoft) return tt;
     return mp_lds_bytes(1, C, K) <= kLdsHard ? 1 : 0;
