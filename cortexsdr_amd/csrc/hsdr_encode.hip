@@ -47,7 +47,7 @@ using csdr::set_error;
 constexpr int kEThreads = 256;
 constexpr int kEGroups = kEThreads / 16;
 constexpr int kMaxTT = 8;        // tiles per workgroup, at most
-constexpr int kDB = 16;          // chunks of an atom loaded per block
+constexpr int kDB = 8;           // chunks of an atom loaded per block
 constexpr int kMaxStages = 32;
 constexpr size_t kLdsSoft = 64 * 1024;    // several workgroups per CU below this
 constexpr size_t kLdsHard = 160 * 1024;
@@ -113,42 +113,71 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
             // a time, the next block in flight while this one is used (loads clamp into the
             // row's full chunks: in bounds, uniform, so the waits stay per block); tile slots
             // past nt hold zeros and are computed too (no per-tile branches)
-            for (int j = grp; j < K; j += kEGroups) {
-                const float* dj = a.D + (size_t)j * C + l16;
-                float p[TT];
+            // two atoms per group at a time (j and j + 16): each residual read feeds both
+            for (int j = grp; j < K; j += 2 * kEGroups) {
+                const int j1 = j + kEGroups;
+                const bool two = j1 < K;
+                const float* dj0 = a.D + (size_t)j * C + l16;
+                const float* dj1 = a.D + (size_t)(two ? j1 : j) * C + l16;
+                float p0[TT], p1[TT];
 #pragma unroll
-                for (int t = 0; t < TT; ++t) p[t] = 0.f;
-                float cur[kDB], nxt[kDB];
+                for (int t = 0; t < TT; ++t) {
+                    p0[t] = 0.f;
+                    p1[t] = 0.f;
+                }
+                float c0[kDB], c1[kDB], n0[kDB], n1[kDB];
 #pragma unroll
-                for (int q = 0; q < kDB; ++q) cur[q] = nch ? dj[min(q, nch - 1) * 16] : 0.f;
+                for (int q = 0; q < kDB; ++q) {
+                    c0[q] = nch ? dj0[min(q, nch - 1) * 16] : 0.f;
+                    c1[q] = nch ? dj1[min(q, nch - 1) * 16] : 0.f;
+                }
                 for (int b0 = 0; b0 < nch; b0 += kDB) {
 #pragma unroll
-                    for (int q = 0; q < kDB; ++q) nxt[q] = dj[min(b0 + kDB + q, nch - 1) * 16];
+                    for (int q = 0; q < kDB; ++q) {
+                        n0[q] = dj0[min(b0 + kDB + q, nch - 1) * 16];
+                        n1[q] = dj1[min(b0 + kDB + q, nch - 1) * 16];
+                    }
 #pragma unroll
                     for (int q = 0; q < kDB; ++q) {
                         if (b0 + q >= nch) break;
                         float rv[TT];
                         load_tiles<TT>(r + ((b0 + q) * 16 + l16) * TT, rv);
 #pragma unroll
-                        for (int t = 0; t < TT; ++t) p[t] = fmaf(cur[q], rv[t], p[t]);
+                        for (int t = 0; t < TT; ++t) {
+                            p0[t] = fmaf(c0[q], rv[t], p0[t]);
+                            p1[t] = fmaf(c1[q], rv[t], p1[t]);
+                        }
                     }
 #pragma unroll
-                    for (int q = 0; q < kDB; ++q) cur[q] = nxt[q];
+                    for (int q = 0; q < kDB; ++q) {
+                        c0[q] = n0[q];
+                        c1[q] = n1[q];
+                    }
                 }
                 if (C8 > C16 && l16 < 8) {
-                    const float dv = dj[C16];
+                    const float d0 = dj0[C16], d1 = dj1[C16];
                     const float* rc = r + (C16 + l16) * TT;
 #pragma unroll
-                    for (int t = 0; t < TT; ++t) p[t] = fmaf(dv, rc[t], p[t]);
+                    for (int t = 0; t < TT; ++t) {
+                        p0[t] = fmaf(d0, rc[t], p0[t]);
+                        p1[t] = fmaf(d1, rc[t], p1[t]);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
-                    float v = p[t];
+                    float v = p0[t], w = p1[t];
                     v += __shfl_xor(v, 8, 16);  // acc0 + acc1
+                    w += __shfl_xor(w, 8, 16);
                     v += __shfl_xor(v, 4, 16);  // low + high 128 bits
+                    w += __shfl_xor(w, 4, 16);
                     v += __shfl_xor(v, 1, 16);  // horizontal add
+                    w += __shfl_xor(w, 1, 16);
                     v += __shfl_xor(v, 2, 16);  // horizontal add
-                    if (l16 == 0 && t < nt) proj[t * K + j] = used[t * K + j] ? 0.0f : v;
+                    w += __shfl_xor(w, 2, 16);
+                    if (l16 == 0 && t < nt) {
+                        proj[t * K + j] = used[t * K + j] ? 0.0f : v;
+                        if (two) proj[t * K + j1] = used[t * K + j1] ? 0.0f : w;
+                    }
                 }
             }
             __syncthreads();
