@@ -102,6 +102,9 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
         const int c = i / TT, t = i - c * TT;
         r[i] = t < nt ? a.tiles[(t0 + t) * C + c] : 0.f;
     }
+    // atoms per 16-lane group at a time: 4 with up to 2 tiles, 2 with more (registers: measured
+    // 896 x 896 at 2 tiles 0.60 -> 0.51 ms with 4; 4864 x 896 at 4 tiles 3.48 -> 4.01 ms)
+    constexpr int kNA = TT <= 2 ? 4 : 2;
     const int C16 = C & ~15, C8 = C & ~7;  // end of the 16-element chunks, of the 8-element one
     const int nch = C16 / 16;  // full 16-element chunks (block loads clamp into them)
     const int slots = a.S * a.k;
@@ -113,70 +116,66 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
             // a time, the next block in flight while this one is used (loads clamp into the
             // row's full chunks: in bounds, uniform, so the waits stay per block); tile slots
             // past nt hold zeros and are computed too (no per-tile branches)
-            // two atoms per group at a time (j and j + 16): each residual read feeds both
-            for (int j = grp; j < K; j += 2 * kEGroups) {
-                const int j1 = j + kEGroups;
-                const bool two = j1 < K;
-                const float* dj0 = a.D + (size_t)j * C + l16;
-                const float* dj1 = a.D + (size_t)(two ? j1 : j) * C + l16;
-                float p0[TT], p1[TT];
+            // kNA atoms per group at a time (j, j + 16, ...): each residual read feeds all
+            for (int j = grp; j < K; j += kNA * kEGroups) {
+                const float* dj[kNA];
 #pragma unroll
-                for (int t = 0; t < TT; ++t) {
-                    p0[t] = 0.f;
-                    p1[t] = 0.f;
+                for (int u = 0; u < kNA; ++u) {
+                    const int ju = j + u * kEGroups;
+                    dj[u] = a.D + (size_t)(ju < K ? ju : j) * C + l16;
                 }
-                float c0[kDB], c1[kDB], n0[kDB], n1[kDB];
+                float p[kNA][TT];
 #pragma unroll
-                for (int q = 0; q < kDB; ++q) {
-                    c0[q] = nch ? dj0[min(q, nch - 1) * 16] : 0.f;
-                    c1[q] = nch ? dj1[min(q, nch - 1) * 16] : 0.f;
-                }
+                for (int u = 0; u < kNA; ++u)
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) p[u][t] = 0.f;
+                float cv[kNA][kDB], nv[kNA][kDB];
+#pragma unroll
+                for (int u = 0; u < kNA; ++u)
+#pragma unroll
+                    for (int q = 0; q < kDB; ++q) cv[u][q] = nch ? dj[u][min(q, nch - 1) * 16] : 0.f;
                 for (int b0 = 0; b0 < nch; b0 += kDB) {
 #pragma unroll
-                    for (int q = 0; q < kDB; ++q) {
-                        n0[q] = dj0[min(b0 + kDB + q, nch - 1) * 16];
-                        n1[q] = dj1[min(b0 + kDB + q, nch - 1) * 16];
-                    }
+                    for (int u = 0; u < kNA; ++u)
+#pragma unroll
+                        for (int q = 0; q < kDB; ++q)
+                            nv[u][q] = dj[u][min(b0 + kDB + q, nch - 1) * 16];
 #pragma unroll
                     for (int q = 0; q < kDB; ++q) {
                         if (b0 + q >= nch) break;
                         float rv[TT];
                         load_tiles<TT>(r + ((b0 + q) * 16 + l16) * TT, rv);
 #pragma unroll
-                        for (int t = 0; t < TT; ++t) {
-                            p0[t] = fmaf(c0[q], rv[t], p0[t]);
-                            p1[t] = fmaf(c1[q], rv[t], p1[t]);
-                        }
+                        for (int u = 0; u < kNA; ++u)
+#pragma unroll
+                            for (int t = 0; t < TT; ++t) p[u][t] = fmaf(cv[u][q], rv[t], p[u][t]);
                     }
 #pragma unroll
-                    for (int q = 0; q < kDB; ++q) {
-                        c0[q] = n0[q];
-                        c1[q] = n1[q];
-                    }
+                    for (int u = 0; u < kNA; ++u)
+#pragma unroll
+                        for (int q = 0; q < kDB; ++q) cv[u][q] = nv[u][q];
                 }
                 if (C8 > C16 && l16 < 8) {
-                    const float d0 = dj0[C16], d1 = dj1[C16];
                     const float* rc = r + (C16 + l16) * TT;
 #pragma unroll
-                    for (int t = 0; t < TT; ++t) {
-                        p0[t] = fmaf(d0, rc[t], p0[t]);
-                        p1[t] = fmaf(d1, rc[t], p1[t]);
+                    for (int u = 0; u < kNA; ++u) {
+                        const float dv = dj[u][C16];
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) p[u][t] = fmaf(dv, rc[t], p[u][t]);
                     }
                 }
 #pragma unroll
-                for (int t = 0; t < TT; ++t) {
-                    float v = p0[t], w = p1[t];
-                    v += __shfl_xor(v, 8, 16);  // acc0 + acc1
-                    w += __shfl_xor(w, 8, 16);
-                    v += __shfl_xor(v, 4, 16);  // low + high 128 bits
-                    w += __shfl_xor(w, 4, 16);
-                    v += __shfl_xor(v, 1, 16);  // horizontal add
-                    w += __shfl_xor(w, 1, 16);
-                    v += __shfl_xor(v, 2, 16);  // horizontal add
-                    w += __shfl_xor(w, 2, 16);
-                    if (l16 == 0 && t < nt) {
-                        proj[t * K + j] = used[t * K + j] ? 0.0f : v;
-                        if (two) proj[t * K + j1] = used[t * K + j1] ? 0.0f : w;
+                for (int u = 0; u < kNA; ++u) {
+                    const int ju = j + u * kEGroups;
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        float v = p[u][t];
+                        v += __shfl_xor(v, 8, 16);  // acc0 + acc1
+                        v += __shfl_xor(v, 4, 16);  // low + high 128 bits
+                        v += __shfl_xor(v, 1, 16);  // horizontal add
+                        v += __shfl_xor(v, 2, 16);  // horizontal add
+                        if (l16 == 0 && t < nt && ju < K)
+                            proj[t * K + ju] = used[t * K + ju] ? 0.0f : v;
                     }
                 }
             }
