@@ -122,3 +122,46 @@ def test_decoder_fused_equals_unfused(gpu):
             dec.close()
     assert np.array_equal(runs[0][0], runs[1][0])
     assert rel_l2(runs[0][1], runs[1][1]) < 1e-5
+
+
+def test_load_kv_continues_like_prefill(gpu):
+    """csdr_decoder_load_kv takes K/V [position][kv head][head_dim]: importing the prompt's
+    K/V for positions [0, n - 1), computed by the oracle's ops, then one step at position
+    n - 1 gives the scores a prefill of the whole prompt gives (K/V rounding aside: 1e-3
+    relative L2)."""
+    from oracle.decoder import _linear, embed_rows, mha_causal, rms_norm, rope, silu_mul
+
+    spec = DecoderSpec(2, 256, 4, 2, 64, 256, 300, 40)
+    s = spec
+    w = synthetic_weights(spec, n_atoms=128, nnz=8, seed=5, sigma=0.1)
+    prompt = ((np.arange(13) * 7919 + 3) % spec.vocab).astype(np.int32)
+    a = Decoder(w)
+    b = Decoder(w)
+    try:
+        a.prefill(prompt, 0.0, 0.0)
+        ref = a.logits()
+        T = len(prompt) - 1
+        hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
+        x = embed_rows(w, prompt[:-1]).astype(np.float32)
+        for li, L in enumerate(w.layers):
+            h = rms_norm(x, L["attn_norm"], s.rms_eps)
+            q = rope(_linear(L["q"], h, L.get("bq")), Hq, hd, s.rope_theta, 0)
+            k = rope(_linear(L["k"], h, L.get("bk")), Hkv, hd, s.rope_theta, 0)
+            v = _linear(L["v"], h, L.get("bv"))
+            kc = np.ascontiguousarray(k.reshape(T, Hkv, hd).astype(np.float16))
+            vc = np.ascontiguousarray(v.reshape(T, Hkv, hd).astype(np.float16))
+            b.load_kv(li, kc, vc, T)
+            rep = Hq // Hkv
+            ke = np.repeat(k.reshape(T, Hkv, hd), rep, axis=1).reshape(T, Hq * hd)
+            ve = np.repeat(v.reshape(T, Hkv, hd), rep, axis=1).reshape(T, Hq * hd)
+            att = mha_causal(q[None], ke[None], ve[None], Hq)[0]
+            x = (x + _linear(L["o"], att)).astype(np.float32)
+            h = rms_norm(x, L["ffn_norm"], s.rms_eps)
+            x = (x + _linear(L["down"], silu_mul(_linear(L["gate"], h), _linear(L["up"], h)))
+                 ).astype(np.float32)
+        b.set_position(T, int(prompt[-1]))
+        b.decode(1, 0.0, 0.0)
+        assert rel_l2(b.logits(), ref) < 1e-3
+    finally:
+        a.close()
+        b.close()
