@@ -460,18 +460,38 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const size_t rstride = (size_t)Hkv * HD;
     const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
     const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    // every K and V row of this lane's positions is loaded before the first use (one memory
+    // round trip for the split, instead of one per pass and operand)
+    constexpr int kMaxPass = 256 / NG;  // S <= 256
+    const int npass = (p1 - p0 + NG - 1) / NG;
+    h8 kr[kMaxPass], vr[kMaxPass];
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j) {
+        if (j < npass) {
+            const int p = min(p0 + lg + j * NG, p1 - 1);
+            kr[j] = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
+            vr[j] = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+        }
+    }
     const int plast = L - 1;
     h8 knew = {}, vnew = {};
     if constexpr (ROPE) {
-        // rotate this lane's 8 query dims of every head, and the new key, at position L - 1
+        // rotate this lane's 8 query dims of every head, and the new key, at position L - 1;
+        // each pair's (cos, sin) evaluated once per workgroup (the lanes of a position group
+        // share dims), while the K/V loads above are in flight
+        __shared__ float2 cs[HD / 2];
+        for (int i = tid; i < HD / 2; i += kThreads) {
+            const float freq = powf(ra.theta, -((float)(2 * i) / (float)HD));
+            const float ang = (float)plast * freq;
+            cs[i] = make_float2(cosf(ang), sinf(ang));
+        }
+        __syncthreads();
         const float* kn = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
         const float* vn = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
-            const int i2 = li * 8 + i;
-            const float freq = powf(ra.theta, -((float)i2 / (float)HD));
-            const float ang = (float)plast * freq;
-            const float c = cosf(ang), sn = sinf(ang);
+            const float2 csv = cs[(li * 8 + i) / 2];
+            const float c = csv.x, sn = csv.y;
 #pragma unroll
             for (int g = 0; g < GW; ++g) {
                 const float x0 = qv[g][i], x1 = qv[g][i + 1];
@@ -489,19 +509,6 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
                 knew;
             *reinterpret_cast<h8*>(ra.vcw + ((size_t)b * T + plast) * rstride + kvh * HD + li * 8) =
                 vnew;
-        }
-    }
-    // every K and V row of this lane's positions is loaded before the first use (one memory
-    // round trip for the split, instead of one per pass and operand)
-    constexpr int kMaxPass = 256 / NG;  // S <= 256
-    const int npass = (p1 - p0 + NG - 1) / NG;
-    h8 kr[kMaxPass], vr[kMaxPass];
-#pragma unroll
-    for (int j = 0; j < kMaxPass; ++j) {
-        if (j < npass) {
-            const int p = min(p0 + lg + j * NG, p1 - 1);
-            kr[j] = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
-            vr[j] = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
         }
     }
     // scores
