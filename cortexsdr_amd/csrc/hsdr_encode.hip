@@ -47,7 +47,6 @@ using csdr::set_error;
 constexpr int kEThreads = 256;
 constexpr int kEGroups = kEThreads / 16;
 constexpr int kMaxTT = 8;        // tiles per workgroup, at most
-constexpr int kDB = 8;           // chunks of an atom loaded per block
 constexpr int kMaxStages = 32;
 constexpr size_t kLdsSoft = 64 * 1024;    // several workgroups per CU below this
 constexpr size_t kLdsHard = 160 * 1024;
@@ -102,9 +101,11 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
         const int c = i / TT, t = i - c * TT;
         r[i] = t < nt ? a.tiles[(t0 + t) * C + c] : 0.f;
     }
-    // atoms per 16-lane group at a time: 4 with up to 2 tiles, 2 with more (registers: measured
-    // 896 x 896 at 2 tiles 0.60 -> 0.51 ms with 4; 4864 x 896 at 4 tiles 3.48 -> 4.01 ms)
-    constexpr int kNA = TT <= 2 ? 4 : 2;
+    // atoms per 16-lane group at a time: 8 with up to 2 tiles (D blocks of 4 chunks), 2 with
+    // more (registers; measured 896 x 896 at 2 tiles: 0.60 ms with 2, 0.51 with 4, 0.45 with 8;
+    // 4864 x 896 at 4 tiles: 3.48 ms with 2, 4.01 with 4)
+    constexpr int kNA = TT <= 2 ? 8 : 2;
+    constexpr int kDB = kNA >= 8 ? 4 : 8;  // chunks of an atom loaded per block
     const int C16 = C & ~15, C8 = C & ~7;  // end of the 16-element chunks, of the 8-element one
     const int nch = C16 / 16;  // full 16-element chunks (block loads clamp into them)
     const int slots = a.S * a.k;
