@@ -178,6 +178,41 @@ SIGNATURES.update({
 })
 
 
+class CompressionOptions(C.Structure):
+    _fields_ = [
+        ("num_threads", C.c_size_t), ("verbose", C.c_int), ("show_stats", C.c_int),
+        ("use_delta_encoding", C.c_int), ("use_rle", C.c_int), ("compression_level", C.c_int),
+        ("use_quantization", C.c_int), ("quantization_bits", C.c_int), ("use_hsdr", C.c_int),
+        ("sparsity", C.c_float),
+    ]
+
+
+SIGNATURES["csdr_hsdb_matmul_noalloc"] = (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp])
+
+
+# the rest of the reference SDK surface (compressor family: unsupported here)
+SIGNATURES.update({
+    "cortex_compression_options_init": (_ce, [C.POINTER(CompressionOptions)]),
+    "cortex_error_string": (C.c_char_p, [C.c_int]),
+    "cortex_model_get_parts": (C.c_int, [C.c_char_p, C.POINTER(C.POINTER(C.c_void_p)),
+                                         C.POINTER(C.c_int)]),
+    "cortex_archive_get_tokenizer_info": (_ce, [C.c_char_p, C.POINTER(C.c_int),
+                                                C.POINTER(C.c_void_p)]),
+    "cortex_compressor_create": (_ce, [C.c_char_p, C.c_char_p, C.POINTER(CompressionOptions),
+                                       C.POINTER(_vp)]),
+    "cortex_compressor_add_file": (_ce, [_vp, C.c_char_p]),
+    "cortex_compressor_compress": (_ce, [_vp, C.c_char_p]),
+    "cortex_compressor_get_stats": (_ce, [_vp, C.POINTER(_sz), C.POINTER(_sz),
+                                          C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "cortex_compressor_free": (_ce, [_vp]),
+    "cortex_decompressor_create": (_ce, [C.c_char_p, C.POINTER(_vp), C.c_float]),
+    "cortex_decompressor_decompress": (_ce, [_vp, C.c_char_p, C.c_char_p]),
+    "cortex_decompressor_free": (_ce, [_vp]),
+    "cortex_archive_extract": (_ce, [C.c_char_p, C.c_char_p, C.c_float]),
+    "cortex_compress_from_url": (_ce, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_float]),
+})
+
+
 class DecoderConfig(C.Structure):
     _fields_ = [
         ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int),

@@ -21,6 +21,7 @@
 // the tile, as reassembleTiles leaves them) and loaded through csdr_hsdb_load.
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <memory>
 #include <new>
 #include <string>
@@ -131,7 +132,14 @@ int codes_to_hsdr(const uint8_t* buf, size_t n, const Dict& d, std::vector<uint8
                                             std::to_string((size_t)K * tile_dim));
     if (d.scales.size() < S) return set_error(CSDR_E_FORMAT, "HSDC: dictionary lacks stage scales");
     const uint32_t R_full = R / tr * tr, C_full = C / tc * tc;
+    // the header's shape must describe exactly n_tiles tiles, and the zero edge strips the
+    // equivalent stream carries must fit its u32 byte count (a corrupt R or C would otherwise
+    // size an allocation from unchecked fields)
+    if ((uint64_t)(R / tr) * (C / tc) != n_tiles)
+        return set_error(CSDR_E_FORMAT, "HSDC: tile count does not match the stream's shape");
     const uint64_t edge_floats = (uint64_t)R_full * (C - C_full) + (uint64_t)(R - R_full) * C;
+    if (edge_floats * 4 > 0xFFFFFFFFull || edge_floats > (uint64_t)R * C)
+        return set_error(CSDR_E_FORMAT, "HSDC: edge strips exceed the stream format's limits");
     out.clear();
     out.reserve(36 + 4 * S + 4 * d.atoms.size() + 2 * n_codes + 4 * edge_floats);
     auto put = [&](const void* p, size_t b) {
@@ -158,11 +166,17 @@ int codes_to_hsdr(const uint8_t* buf, size_t n, const Dict& d, std::vector<uint8
     return CSDR_OK;
 }
 
+// Exceptions (allocation failures of a large but well-formed stream) stay inside: the caller
+// gets a status, as from every entry point of this library.
 int load_codes(const uint8_t* buf, size_t n, const Dict& d, void* hip_stream, csdr_hsdb** out) {
-    std::vector<uint8_t> hsdr;
-    int rc = codes_to_hsdr(buf, n, d, hsdr);
-    if (rc) return rc;
-    return csdr_hsdb_load(hsdr.data(), hsdr.size(), hip_stream, out);
+    try {
+        std::vector<uint8_t> hsdr;
+        int rc = codes_to_hsdr(buf, n, d, hsdr);
+        if (rc) return rc;
+        return csdr_hsdb_load(hsdr.data(), hsdr.size(), hip_stream, out);
+    } catch (const std::exception& ex) {
+        return set_error(CSDR_E_FORMAT, std::string("HSDC: cannot build the segment: ") + ex.what());
+    }
 }
 
 }  // namespace
@@ -253,7 +267,7 @@ int parse_index(csdr_archive* a) {
         if (!c.ok)
             return set_error(CSDR_E_TRUNCATED, "Failed to read segment header information from "
                                                "index (entry " + std::to_string(i) + ").");
-        if (e.offset + e.comp > index_off)
+        if (e.comp > index_off || e.offset > index_off - e.comp)
             return set_error(CSDR_E_FORMAT, "segment '" + e.name + "' payload overlaps the index");
         a->by_name.emplace(e.name, a->entries.size());  // first entry of a name wins
         a->entries.push_back(std::move(e));
@@ -400,6 +414,8 @@ CSDR_API int csdr_hsdb_load_codes(const void* codes, size_t nbytes, const csdr_d
                                   void* hip_stream, csdr_hsdb** out) {
     if (!codes || !dict || !out || !dict->atoms || !dict->stage_scales)
         return set_error(CSDR_E_INVALID, "hsdb_load_codes: null argument");
+    if (dict->n_atom_floats > ((size_t)1 << 34) || dict->n_stage_scales > 255)
+        return set_error(CSDR_E_INVALID, "hsdb_load_codes: dictionary sizes out of range");
     Dict d;
     d.tile_rows = (uint16_t)dict->tile_rows;
     d.tile_cols = (uint16_t)dict->tile_cols;
@@ -407,8 +423,12 @@ CSDR_API int csdr_hsdb_load_codes(const void* codes, size_t nbytes, const csdr_d
     d.n_stages = (uint8_t)dict->n_stages;
     d.k = (uint8_t)dict->k_per_stage;
     d.stage_decay = dict->stage_decay;
-    d.scales.assign(dict->stage_scales, dict->stage_scales + dict->n_stage_scales);
-    d.atoms.assign(dict->atoms, dict->atoms + dict->n_atom_floats);
+    try {
+        d.scales.assign(dict->stage_scales, dict->stage_scales + dict->n_stage_scales);
+        d.atoms.assign(dict->atoms, dict->atoms + dict->n_atom_floats);
+    } catch (const std::bad_alloc&) {
+        return set_error(CSDR_E_INVALID, "hsdb_load_codes: out of host memory");
+    }
     return load_codes(static_cast<const uint8_t*>(codes), nbytes, d, hip_stream, out);
 }
 

@@ -213,7 +213,8 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
     const int s = blockIdx.y;
     const int h0 = kvh * G + blockIdx.z * GW;
     const int nh = min(GW, G - (int)blockIdx.z * GW);
-    const int L = lens ? lens[b] : len_host;
+    // a length beyond the cache capacity is clamped to it (no K/V row past T is read or written)
+    const int L = min(max(lens ? lens[b] : len_host, 0), T);
     const int p0 = s * S, p1 = min(L, p0 + S);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool direct = (nsplit == 1 && out != nullptr);
@@ -428,7 +429,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const int s = blockIdx.y;
     const int h0 = kvh * G + blockIdx.z * GW;
     const int nh = min(GW, G - (int)blockIdx.z * GW);
-    const int L = lens ? lens[b] : len_host;
+    // a length beyond the cache capacity is clamped to it (no K/V row past T is read or written)
+    const int L = min(max(lens ? lens[b] : len_host, 0), T);
     const int p0 = s * S, p1 = min(L, p0 + S);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lg = tid / LPP, li = tid % LPP;
@@ -649,7 +651,8 @@ __global__ __launch_bounds__(kMThreads) void attn_mfma_kernel(
     const size_t npart = (size_t)(gridDim.x / Hkv) * Hq * nsplit;  // partials in the workspace
     const int b = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv, s = blockIdx.y;
     const int h0 = kvh * G;
-    const int L = lens ? lens[b] : len_host;
+    // a length beyond the cache capacity is clamped to it (no K/V row past T is read or written)
+    const int L = min(max(lens ? lens[b] : len_host, 0), T);
     const int p0 = s * S, p1 = min(L, p0 + S);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c16 = lane & 15, g4 = lane >> 4;
@@ -981,14 +984,11 @@ constexpr int kSelectBlocks = 256;
 // Positions per split: about T / 8 rounded up to a power of two in [64, 256], so a head has at
 // most 8 splits up to 2048 positions (every split's K/V rows are loaded in one round trip, and
 // the consumer's combine reads nsplit partials per feature; measured on cfg4, 640 positions:
-// 128 ahead of 64 and 256). CSDR_ATTN_SPLIT = 64, 128 or 256 forces a length.
+// 128 ahead of 64 and 256).
 int attn_split_len(int B, int Hkv, int zsplit, int T) {
     (void)B;
     (void)Hkv;
     (void)zsplit;
-    const char* ev = std::getenv("CSDR_ATTN_SPLIT");
-    const int forced = ev ? std::atoi(ev) : 0;
-    if (forced == 64 || forced == 128 || forced == 256) return forced;
     int S = 64;
     while (S < 256 && 8LL * S < T) S *= 2;
     return S;

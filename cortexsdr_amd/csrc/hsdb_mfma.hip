@@ -357,9 +357,7 @@ namespace csdr {
 bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M) {
     const char* e = std::getenv("CSDR_HSDB_MFMA");
     if (e && *e && std::atoi(e) == 0) return false;
-    const char* mm = std::getenv("CSDR_HSDB_MFMA_MIN_M");
-    const int min_m = (mm && std::atoi(mm) > 1) ? std::atoi(mm) : kMfmaMinM;
-    if (M < min_m) return false;
+    if (M < kMfmaMinM) return false;
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
         if (!s || s->tile_rows != 1 || s->tile_cols != 64 || s->K > (uint32_t)kMaxAtoms ||

@@ -102,6 +102,76 @@ CSDR_API CortexError cortex_inference_engine_generate_text(CortexInferenceEngine
 CSDR_API CortexError cortex_inference_engine_free(CortexInferenceEngineHandle handle);
 CSDR_API const char* cortex_sdk_version(void);
 
+/* ======================================================================
+ * The rest of the reference SDK surface (api/c_api.hpp:46-117, api/cortex_sdk.h:42-103,
+ * 252-281), so that the reference CLI (src/cortexsdr_cli.cpp:918, :1639) and its Python
+ * wrapper (python/cortexsdr_sdk/_bindings.cpp:28, :55) link unchanged. Host-only functions
+ * behave as the reference's; the compression / extraction family returns
+ * CORTEX_ERROR_UNSUPPORTED_FORMAT (model parsers, strategy chain and archive writer are not
+ * part of this inference library) and never yields a handle.
+ * ==================================================================== */
+
+/* c_api.hpp:18-24 status codes of the compressor API */
+#define CORTEX_OK 0
+#define CORTEX_ERR_INVALID_ARG 1
+#define CORTEX_ERR_FILE_NOT_FOUND 2
+#define CORTEX_ERR_UNSUPPORTED_FORMAT 3
+#define CORTEX_ERR_INTERNAL 100
+
+typedef struct CortexCompressor* CortexCompressorHandle;
+typedef void* CortexDecompressorHandle;
+
+/* c_api.hpp:32-43 */
+typedef struct {
+    size_t num_threads;
+    int verbose;
+    int show_stats;
+    int use_delta_encoding;
+    int use_rle;
+    int compression_level;
+    int use_quantization;
+    int quantization_bits;
+    int use_hsdr;
+    float sparsity;
+} CortexCompressionOptions;
+
+/* Reference defaults (c_api.cpp:298-317). */
+CSDR_API CortexError cortex_compression_options_init(CortexCompressionOptions* options);
+/* c_api.cpp:680-689. */
+CSDR_API const char* cortex_error_string(int code);
+/* findModelParts (c_api.cpp:55-110, 490-514): the existing parts of a
+ * "<base>-NNNNN-of-MMMMM<ext>" set, else the path itself; returns the count. *parts_out is a
+ * malloc'd array of malloc'd strings (free each with cortex_free_string, then the array). */
+CSDR_API int cortex_model_get_parts(const char* model_path, char*** parts_out, int* num_parts);
+/* cortex_sdk.cpp:2096-2150: tokenizer assets by segment name (sentencepiece / gpt2-bpe);
+ * *out_tokenizer_type is freed with cortex_free_string. */
+CSDR_API CortexError cortex_archive_get_tokenizer_info(const char* archive_path,
+                                                       int* out_has_tokenizer,
+                                                       char** out_tokenizer_type);
+/* Unsupported here (see above). */
+CSDR_API CortexError cortex_compressor_create(const char* model_path, const char* format,
+                                              const CortexCompressionOptions* options,
+                                              CortexCompressorHandle* handle);
+CSDR_API CortexError cortex_compressor_add_file(CortexCompressorHandle handle,
+                                                const char* model_path);
+CSDR_API CortexError cortex_compressor_compress(CortexCompressorHandle handle,
+                                                const char* output_path);
+CSDR_API CortexError cortex_compressor_get_stats(CortexCompressorHandle handle,
+                                                 size_t* original_size, size_t* compressed_size,
+                                                 double* compression_ratio,
+                                                 double* compression_time_ms);
+CSDR_API CortexError cortex_compressor_free(CortexCompressorHandle handle);
+CSDR_API CortexError cortex_decompressor_create(const char* compressed_path,
+                                                CortexDecompressorHandle* handle, float sparsity);
+CSDR_API CortexError cortex_decompressor_decompress(CortexDecompressorHandle handle,
+                                                    const char* compressed_path,
+                                                    const char* output_path);
+CSDR_API CortexError cortex_decompressor_free(CortexDecompressorHandle handle);
+CSDR_API CortexError cortex_archive_extract(const char* compressed_path, const char* output_dir,
+                                            float sparsity);
+CSDR_API CortexError cortex_compress_from_url(const char* url_or_path, const char* format,
+                                              const char* output_path, float sparsity);
+
 /* Device-side form of run_layer for callers whose activations already live in HBM: x is
  * C x M feature-major (matmulRowMajor's convention), y R x M fp32, both device pointers, on
  * hip_stream. Strategy-5 segments only. */

@@ -63,6 +63,41 @@ def test_encode_matches_oracle(gpu, n, C, K, S, k):
     assert np.array_equal(got, want)
 
 
+# Each tiles-per-workgroup instantiation of the matching-pursuit kernel (1: the large-tile LDS
+# fallback; 4 and 8: what matrices of >= 4096 tiles take, with 2 atoms per lane group and
+# float4 tile loads), forced through the kernel's selection override, bit-exact against the
+# oracle; ragged last workgroups (n not a multiple of TT), tiles with an 8-element chunk
+# (C % 16 == 8) and without, and a case whose natural selection is TT = 1 (C x K too large
+# for two tiles under the soft LDS size).
+@pytest.mark.parametrize("tt", [1, 4, 8])
+@pytest.mark.parametrize("n,C,K,S,k", [(203, 72, 128, 3, 4), (1031, 64, 256, 3, 5),
+                                       (37, 200, 64, 2, 8), (45, 896, 160, 3, 3)])
+def test_encode_tiles_per_workgroup_match_oracle(gpu, monkeypatch, tt, n, C, K, S, k):
+    monkeypatch.setenv("CSDR_HSDR_TILES_PER_WG", str(tt))
+    rng = np.random.default_rng(7 * n + C + K + tt)
+    t = (rng.standard_normal((n, C)) * 0.02).astype(np.float32)
+    D = rng.standard_normal((K, C)).astype(np.float32)
+    D /= np.linalg.norm(D, axis=1, keepdims=True)
+    D *= 0.02 * np.sqrt(C / (S * k))
+    g = (0.5 ** np.arange(S)).astype(np.float32)
+    want = oracle.hsdr_mp(t, D, g, S, k)
+    got = gpu_codes(gpu, t, D, g, S, k)
+    assert np.array_equal(got, want), f"TT={tt}"
+
+
+def test_encode_large_tile_falls_back_to_one_per_workgroup(gpu, monkeypatch):
+    # 2 x (C + K) x 4 bytes > 64 KiB: the natural choice is one tile per workgroup
+    monkeypatch.delenv("CSDR_HSDR_TILES_PER_WG", raising=False)
+    n, C, K, S, k = 9, 4096, 4096, 2, 3
+    rng = np.random.default_rng(11)
+    t = (rng.standard_normal((n, C)) * 0.02).astype(np.float32)
+    D = rng.standard_normal((K, C)).astype(np.float32)
+    D /= np.linalg.norm(D, axis=1, keepdims=True)
+    D *= 0.02 * np.sqrt(C / (S * k))
+    g = (0.5 ** np.arange(S)).astype(np.float32)
+    assert np.array_equal(gpu_codes(gpu, t, D, g, S, k), oracle.hsdr_mp(t, D, g, S, k))
+
+
 def test_compress_matches_reference(gpu, enc):
     """The whole stream is the reference's byte for byte when this CPU's reciprocal square
     root is the one the fixtures were written with (the dictionary is then identical, see
