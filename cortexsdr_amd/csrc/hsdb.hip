@@ -50,20 +50,11 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRawBufferDword3 = 0x00020000;
 constexpr int kCachePolicyNT = 2;  // buffer load cache policy: nontemporal (streaming)
 
-// Launch-shape defaults, overridable for tuning sweeps through the environment
-// (CSDR_DX_WORK, CSDR_GATHER_WGS_PER_CU, CSDR_CHUNK_BYTES).
 // A switch from the environment: "0" is off, any other value on, unset is dflt.
 bool env_flag(const char* name, bool dflt) {
     const char* v = std::getenv(name);
     if (!v || !*v) return dflt;
     return v[0] != '0';
-}
-
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    if (!v || !*v) return dflt;
-    const int x = std::atoi(v);
-    return x > 0 ? x : dflt;
 }
 
 constexpr uint32_t kMaxChunkBlocks = 16;
@@ -616,8 +607,7 @@ __device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, in
 }
 
 // ---- kernel 2, M == 1: the gather, 1024-thread workgroups
-// Workgroup = (matrix, chunk c, row range s), about kGWgsPerCu per CU in all
-// (CSDR_GATHER_WGS_PER_CU to change), each streaming about the same code bytes
+// Workgroup = (matrix, chunk c, row range s), about kGWgsPerCu per CU in all, each streaming about the same code bytes
 // (plan_gather_splits), numbered chunk-fastest so that consecutive ids (which dispatch
 // round-robin over the 8 XCDs) spread every matrix over all XCDs. The workgroup issues its
 // chunk's P slice loads (nbc * K floats, written by the dx launch), then each of its 16 waves
@@ -637,32 +627,6 @@ constexpr size_t kGMaxP = 4 * 4 * kGThreads;  // P slice floats: 4 float4 per th
 // rows per gather workgroup (their totals wait in LDS): with a 64 KiB P slice two workgroups
 // still fit in a CU's 160 KiB
 constexpr int kGMaxRows = 3840;
-
-// Optional per-workgroup timeline of the gather launch (built only with
-// -DCSDR_GATHER_TIMELINE, for measurement): stamps and the hardware ids per workgroup id.
-#ifdef CSDR_GATHER_TIMELINE
-constexpr int kTlWgs = 4096;
-// stamps 0..6, then (XCC id << 32 | HW_ID), the shader clock at stamp 0 and at the latest stamp
-constexpr int kTlSlots = 10;
-__device__ unsigned long long g_timeline[kTlWgs * kTlSlots];
-#define CSDR_TL(slot)                                                                       \
-    do {                                                                                    \
-        if (threadIdx.x == 0 && blockIdx.x < (unsigned)kTlWgs) {                            \
-            g_timeline[blockIdx.x * kTlSlots + (slot)] = wall_clock64();                   \
-            g_timeline[blockIdx.x * kTlSlots + 9] = clock64();                             \
-            if ((slot) == 0) {                                                              \
-                g_timeline[blockIdx.x * kTlSlots + 7] =                                    \
-                    ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | \
-                    (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);                   \
-                g_timeline[blockIdx.x * kTlSlots + 8] = clock64();                         \
-            }                                                                               \
-        }                                                                                   \
-    } while (0)
-#else
-#define CSDR_TL(slot) \
-    do {              \
-    } while (0)
-#endif
 
 // Slot gamma i of a matrix as a wave-uniform scalar: the readfirstlane keeps the per-lane
 // select over these values a select (otherwise the compiler turns it into a per-lane memory
@@ -706,7 +670,6 @@ void gatherw_kernel(Params p) {
     const int rbeg = sidx * rpw;
     const int rend = min(d.R, rbeg + rpw);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    CSDR_TL(0);
 
     // The workgroup's P slice loads (nbc * K <= kGMaxP floats, written by the dx launch) are
     // issued first, then every wave's first DEPTH code loads, and only then are the P values
@@ -774,7 +737,6 @@ void gatherw_kernel(Params p) {
         stage_to_lds<float, kGThreads>(Pg, np, Ps);
     }
     __syncthreads();
-    CSDR_TL(1);
 
     // per lane a fixed tile and slot quarter; word = (signed fp16 coefficient << 16) | index,
     // the low half is the index itself (bit 15 is 0)
@@ -845,7 +807,6 @@ void gatherw_kernel(Params p) {
         }
         __hip_atomic_fetch_add(d.y + rbeg + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    CSDR_TL(2);
 }
 
 // ---- kernel 2, any M / any slot count: workgroup = (chunk, row tile of Rt rows); the
@@ -1166,9 +1127,9 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
         return set_error(CSDR_E_FORMAT, "hsdb_load: zero coded slots per tile");
 
     // chunking of block columns (1-row tiles): the P slice of a chunk (nbc * K fp32, staged
-    // in LDS by the M == 1 products) at most kChunkPBytes (CSDR_CHUNK_BYTES overrides)
+    // in LDS by the M == 1 products) at most kChunkPBytes
     if (s->tile_rows == 1) {
-        const size_t cap = (size_t)env_int("CSDR_CHUNK_BYTES", (int)kChunkPBytes);
+        const size_t cap = kChunkPBytes;
         uint32_t nbc = kMaxChunkBlocks;
         while (nbc > 1 && (size_t)nbc * s->K * 4 > cap) nbc >>= 1;
         while (nbc > 1 && nbc > s->NB) nbc >>= 1;
@@ -1241,8 +1202,8 @@ void release(csdr_hsdb* s) {
 // Block columns per dx workgroup (block length 64): about `work` (block, column) dot
 // products per 16-lane group.
 inline int producer_blocks(int M) {
-    const int work = env_int("CSDR_DX_WORK", 16);
-    return M >= work ? 1 : work / M;
+    constexpr int kWork = 16;
+    return M >= kWork ? 1 : kWork / M;
 }
 
 size_t p_bytes(const csdr_hsdb* s, int M) {
@@ -1503,12 +1464,12 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     int base = 0;
     if (fast) {
-        // kGWgsPerCu workgroups per CU, fewer for small groups: at least CSDR_GATHER_WG_BYTES
-        // of codes per workgroup (each one stages a P slice of up to 16 KiB first)
-        long long target = (long long)ncu * env_int("CSDR_GATHER_WGS_PER_CU", kGWgsPerCu);
+        // kGWgsPerCu workgroups per CU, fewer for small groups: at least kGMinWgBytes of
+        // codes per workgroup (each one stages a P slice of up to 16 KiB first)
+        long long target = (long long)ncu * kGWgsPerCu;
         long long code_bytes = 0;
         for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
-        const long long min_bytes = env_int("CSDR_GATHER_WG_BYTES", kGMinWgBytes);
+        const long long min_bytes = kGMinWgBytes;
         target = std::max(1LL, std::min(target, code_bytes / std::max(1LL, min_bytes)));
         plan_gather_splits(p, n, target);
         for (int i = 0; i < n; ++i) {
@@ -1695,23 +1656,6 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
     return matmul_group(n, segs, x, x_dtype, M, y, workspace, workspace_bytes,
                         static_cast<hipStream_t>(hip_stream), kPhaseGather);
 }
-
-#ifdef CSDR_GATHER_TIMELINE
-// Copies the gather launch timeline (4 stamps per workgroup id, wall-clock ticks) to host and
-// clears it; *rate_hz gets the wall-clock rate.
-CSDR_API int csdr_debug_timeline(unsigned long long* host, size_t n, long long* rate_hz) {
-    n = std::min<size_t>(n, (size_t)kTlWgs * kTlSlots);
-    CSDR_HIP_CHECK(hipDeviceSynchronize());
-    CSDR_HIP_CHECK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), n * 8));
-    std::vector<unsigned long long> z((size_t)kTlWgs * kTlSlots, 0ull);
-    CSDR_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), z.data(), z.size() * 8));
-    int dev = 0, r = 0;
-    (void)hipGetDevice(&dev);
-    (void)hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev);
-    *rate_hz = (long long)r * 1000;
-    return CSDR_OK;
-}
-#endif
 
 CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* s, float* w, void* hip_stream) {
     if (!s || !w) return set_error(CSDR_E_INVALID, "hsdb_decompress: bad argument");

@@ -123,9 +123,8 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
  * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
  * column into the workspace, Y = 0 or bias) and a gather launch (Y += the coded rows gathered
  * from P; at M == 1 with 4, 8 or 16 slots two 1024-thread workgroups per CU stream the codes),
- * all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots (the threshold
- * is CSDR_HSDB_MFMA_MIN_M, default 2): an init launch and a matrix-core launch that decodes 64-column
- * tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
+ * all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch
+ * and a matrix-core launch that decodes 64-column tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
  * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
  * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace
  * is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes. csdr_hsdb_matmul is the n = 1 case.
@@ -341,7 +340,8 @@ CSDR_API int csdr_rope_kv(float* q, float* k, const float* v, int ntok, int Hq, 
                           const int* pos_dev, float theta, uint16_t* kcache, uint16_t* vcache,
                           int max_ctx, void* hip_stream);
 /* Decode attention: out (B x Hq x hd) = softmax(q.K^T * scale) V over cached positions
- * [0, len_b) (len_b = lens_dev[b], or len_host when lens_dev is NULL); caches (B x T x Hkv x
+ * [0, len_b) (len_b = lens_dev[b], or len_host when lens_dev is NULL; a length outside
+ * [0, T] is clamped into it, so no row past the cache is read or written); caches (B x T x Hkv x
  * hd) fp16; GQA as repeat_kv_heads (cortex_sdk.cpp:1453-1478); scale 0 = 1/sqrt(hd).
  * Split over chunks of 64..256 positions (about T / 8; workspace csdr_attn_decode_workspace_bytes)
  * then combined. 2..16 query heads per KV head run on the matrix cores (fp16 hi + lo operands,
