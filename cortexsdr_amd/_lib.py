@@ -187,6 +187,9 @@ class CompressionOptions(C.Structure):
     ]
 
 
+SIGNATURES["csdr_hsdb_matmul_noalloc"] = (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp])
+
+
 # the rest of the reference SDK surface (compressor family: unsupported here)
 SIGNATURES.update({
     "cortex_compression_options_init": (_ce, [C.POINTER(CompressionOptions)]),

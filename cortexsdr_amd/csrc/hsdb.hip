@@ -1523,6 +1523,39 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     return CSDR_OK;
 }
 
+// ---- the allocation-free product's scratch memory
+// A file-scope device array that holds the product's workspace (P slices, or the transposed
+// X of the matrix-core path) for callers that cannot allocate (code under HIP graph capture,
+// serving loops). Each device holds its own copy for the life of the process; its address on
+// a device comes from hipGetSymbolAddress, taken once per device with that device current
+// (the array's name in host code is not a device address). Every call on a device shares
+// that device's copy, so calls that overlap on one device race.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address (taken on its first use), or null with the error recorded.
+void* scratch_for(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error(CSDR_E_INVALID, "hsdb_matmul_noalloc: device ordinal out of range");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error(CSDR_E_HIP, std::string("hsdb_matmul_noalloc: hipGetSymbolAddress: ") +
+                                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -1591,6 +1624,31 @@ CSDR_API size_t csdr_hsdb_group_workspace_bytes(int n, const csdr_hsdb* const* s
 CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* s, const void* x, int x_dtype, int M, float* y,
                               void* workspace, size_t workspace_bytes, void* hip_stream) {
     return matmul_group(1, &s, &x, x_dtype, M, &y, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(hip_stream));
+}
+
+CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* s, const void* x, int x_dtype, int M,
+                                      float* y, void* hip_stream) {
+    if (!s || !x || !y || M <= 0)
+        return set_error(CSDR_E_INVALID, "hsdb_matmul_noalloc: bad argument");
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return set_error(CSDR_E_HIP, "hsdb_matmul_noalloc: no HIP device");
+    if (dev != s->device)
+        return set_error(CSDR_E_INVALID,
+                         "hsdb_matmul_noalloc: the segment lives on device " +
+                             std::to_string(s->device) + ", the current device is " +
+                             std::to_string(dev));
+    const size_t need = group_ws_bytes(1, &s, M);
+    if (need > kScratchBytes)
+        return set_error(CSDR_E_WORKSPACE,
+                         "hsdb_matmul_noalloc: this product needs " + std::to_string(need) +
+                             " bytes of scratch, the allocation-free entry point has " +
+                             std::to_string(kScratchBytes) +
+                             "; use csdr_hsdb_matmul with a caller workspace");
+    void* ws = scratch_for(dev);
+    if (!ws) return CSDR_E_HIP;
+    return matmul_group(1, &s, &x, x_dtype, M, &y, ws, kScratchBytes,
                         static_cast<hipStream_t>(hip_stream));
 }
 

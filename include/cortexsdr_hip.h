@@ -118,6 +118,17 @@ CSDR_API int csdr_hsdb_matmul(const csdr_hsdb* seg, const void* x, int x_dtype, 
                               float* y, void* workspace, size_t workspace_bytes,
                               void* hip_stream);
 
+/* csdr_hsdb_matmul without a workspace argument and without any allocation: the product's
+ * scratch memory (the P slices, or the transposed X of the matrix-core path) is a
+ * file-scope device array of 8 MiB per device, held until the process ends. No counterpart
+ * in the reference: for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Products whose csdr_hsdb_workspace_bytes(seg, M)
+ * exceeds 8 MiB are rejected with CSDR_E_WORKSPACE. Every call on a device shares that
+ * device's scratch, so calls that overlap on one device (other streams, other threads) race;
+ * serialise them. The segment must live on the current device. */
+CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* seg, const void* x, int x_dtype, int M,
+                                      float* y, void* hip_stream);
+
 /* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
  * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
  * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
