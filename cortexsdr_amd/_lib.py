@@ -69,6 +69,7 @@ SIGNATURES = {
                                             C.c_int, C.POINTER(_vp), C.POINTER(_vp), C.c_int,
                                             _vp, _sz, _vp]),
     "csdr_hsdb_decode_row": (C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+    "csdr_hsdb_decode_rows": (C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
     "csdr_rms_norm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "csdr_silu_mul": (C.c_int, [_vp, _vp, _sz, _vp, _vp]),
     "csdr_rope_kv": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp,
@@ -87,11 +88,14 @@ SIGNATURES = {
     "csdr_decoder_decode": (C.c_int, [_vp, C.c_int, C.c_float, C.c_float]),
     "csdr_decoder_tokens": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
     "csdr_decoder_generate": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, C.c_float,
-                                        C.c_int, _vp, C.POINTER(C.c_int)]),
+                                        C.c_int, _vp, _vp]),
     "csdr_decoder_logits": (C.c_int, [_vp, _vp]),
     "csdr_decoder_position": (C.c_int, [_vp]),
     "csdr_decoder_load_kv": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int]),
     "csdr_decoder_set_position": (C.c_int, [_vp, C.c_int, C.c_int32]),
+    "csdr_decoder_create_batched": (C.c_int, [_vp, C.c_int, C.POINTER(_vp)]),
+    "csdr_decoder_batch": (C.c_int, [_vp]),
+    "csdr_decoder_set_position_batch": (C.c_int, [_vp, C.c_int, _vp]),
 }
 
 

@@ -183,10 +183,11 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
         dec.close()
 
 
-def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5):
+def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
     """Config 5: Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads of 128, SwiGLU
     11008, vocab 32000, all linears HSDB-coded: 1024 x 64 dictionary, 8 nnz per block) at
-    context `ctx` with the fp16 KV cache filled with N(0,1), batch 1, weights resident.
+    context `ctx` with the fp16 KV cache filled with N(0,1), `batch` sequences, weights
+    resident.
     Two distinct coded layers are generated and loaded 16 times each: every layer has its own
     device copy, so HBM traffic per step is that of 32 distinct layers."""
     import dataclasses
@@ -198,11 +199,11 @@ def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5):
     w2 = synthetic_weights(dataclasses.replace(spec, n_layers=2), seed=seed)
     w = DecoderWeights(spec, [w2.layers[l % 2] for l in range(32)], w2.lm_head, w2.final_norm)
     t_build = time.time() - t0
-    dec = Decoder(w)
+    dec = Decoder(w, batch=batch)
     try:
         for l in range(spec.n_layers):
-            k = torch.randn((ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
-            v = torch.randn((ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
+            k = torch.randn((batch, ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
+            v = torch.randn((batch, ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
             dec.load_kv(l, k, v, ctx)
             del k, v
         torch.cuda.synchronize()
@@ -213,10 +214,10 @@ def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5):
         dec.decode(steps, 0.0, 0.0)
         dt = (time.perf_counter() - t0) / steps
         code = w.code_bytes()
-        kv = 2 * spec.n_layers * (ctx + steps // 2) * spec.n_kv_heads * spec.head_dim * 2
+        kv = 2 * spec.n_layers * (ctx + steps // 2) * spec.n_kv_heads * spec.head_dim * 2 * batch
         return {"layers": 32, "hidden": 4096, "heads": 32, "head_dim": 128, "ffn": 11008,
-                "vocab": 32000, "context": ctx, "batch": 1, "steps": steps,
-                "ms_per_step": round(dt * 1e3, 3), "tokens_per_s": round(1.0 / dt, 1),
+                "vocab": 32000, "context": ctx, "batch": batch, "steps": steps,
+                "ms_per_step": round(dt * 1e3, 3), "tokens_per_s": round(batch / dt, 1),
                 "code_GB_per_step": round(code / 1e9, 3), "kv_GB_per_step": round(kv / 1e9, 3),
                 "alg_GBps": round((code + kv) / dt / 1e9, 1),
                 "hbm_frac": round((code + kv) / dt / HBM_PEAK, 4),

@@ -22,6 +22,14 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // n unnormalised head_dim vectors from this float offset (16-byte aligned).
 __host__ __device__ inline size_t attn_vec_offset(size_t n) { return (2 * n + 3) & ~(size_t)3; }
 
+// Penalised argmax of `rows` rows of n scores (csdr_select_best per row; the position
+// advances once). Workspace select_workspace_rows(rows) bytes.
+size_t select_workspace_rows(int rows);
+int select_best_rows(const float* logits, int n, int rows, const uint8_t* repeated,
+                     float temperature, float penalty, int* out_tokens, int* pos_dev,
+                     uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
+                     hipStream_t st);
+
 #define CSDR_HIP_CHECK(expr)                                                          \
     do {                                                                               \
         hipError_t e_ = (expr);                                                        \

@@ -20,6 +20,12 @@
 // Biases fold into the projections' output initialisation and the residual adds into the
 // o/down projections (CSDR_HSDB_ACCUMULATE); the embedding is the lm_head row of the token
 // (tied embeddings, decoded on the device) unless a separate coded embedding is set.
+//
+// Batch: B sequences advance in lockstep (one position for all; sequence b has its own token
+// ring, K/V cache and generated-token set). Activations are token-major [b][feature], so
+// every projection is one product of M = B columns (CSDR_HSDB_TOKEN_MAJOR; B <= 8 streams
+// each code word once for all B columns) and the attention reads q/k/v rows as they are
+// written. At B = 1 the attention's split combine is fused into the o projection's input.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,13 +42,16 @@ namespace {
 using csdr::set_error;
 
 constexpr int kSanThreads = 256;
+constexpr int kMaxBatch = 16;  // sequences per decoder (the fused x ops take up to 16 columns)
 
+// Sequence b (thread b < B): its length and the token at the current position.
 __global__ void step_begin_kernel(const int* __restrict__ pos, const int* __restrict__ ring,
-                                  int cap, int* __restrict__ tok, int* __restrict__ len) {
-    if (threadIdx.x == 0) {
+                                  int cap, int B, int* __restrict__ tok, int* __restrict__ len) {
+    const int b = threadIdx.x;
+    if (b < B) {
         const int p = *pos;
-        *len = p + 1;
-        *tok = (p >= 0 && p < cap) ? ring[p] : -1;
+        len[b] = p + 1;
+        tok[b] = (p >= 0 && p < cap) ? ring[(size_t)b * cap + p] : -1;
     }
 }
 
@@ -51,18 +60,22 @@ __global__ void advance_kernel(int* __restrict__ pos) {
     if (threadIdx.x == 0) *pos += 1;
 }
 
-// Head step end (after select_best advanced the position): ring[pos] = selected token.
+// Head step end (after select_best advanced the position): sequence b's ring[pos] = its
+// selected token.
 __global__ void record_kernel(const int* __restrict__ tok, const int* __restrict__ pos,
-                              int* __restrict__ ring, int cap) {
-    if (threadIdx.x == 0) {
+                              int* __restrict__ ring, int cap, int B) {
+    const int b = threadIdx.x;
+    if (b < B) {
         const int p = *pos;
-        if (p >= 0 && p < cap) ring[p] = *tok;
+        if (p >= 0 && p < cap) ring[(size_t)b * cap + p] = tok[b];
     }
 }
 
-// sanitize_hidden_for_sampling (cortex_sdk.cpp:959-976) in place: non-finite -> 0, then a
-// uniform scale to max |h| = 1000 when the largest finite magnitude exceeds 1000.
+// sanitize_hidden_for_sampling (cortex_sdk.cpp:959-976) in place on row blockIdx.x of n
+// floats: non-finite -> 0, then a uniform scale to max |h| = 1000 when the largest finite
+// magnitude exceeds 1000.
 __global__ __launch_bounds__(kSanThreads) void sanitize_kernel(float* __restrict__ h, int n) {
+    h += (size_t)blockIdx.x * n;
     __shared__ float red[kSanThreads];
     float m = 0.0f;
     for (int i = threadIdx.x; i < n; i += kSanThreads) {
@@ -98,6 +111,7 @@ struct Layer {
 
 struct csdr_decoder {
     csdr_decoder_config cfg{};
+    int B = 1;  // sequences decoded in lockstep
     std::vector<Layer> layers;
     const csdr_hsdb* lm = nullptr;
     const csdr_hsdb* emb = nullptr;
@@ -172,8 +186,9 @@ int mm(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x, flo
        const float* const* bias, int flags, hipStream_t st) {
     const void* xs[4];
     for (int i = 0; i < n; ++i) xs[i] = x;
-    return csdr_hsdb_matmul_group_ex(n, segs, xs, CSDR_F32, 1, ys, bias, flags, d->ws_hsdb,
-                                     d->ws_hsdb_bytes, st);
+    return csdr_hsdb_matmul_group_ex(n, segs, xs, CSDR_F32, d->B, ys, bias,
+                                     flags | CSDR_HSDB_TOKEN_MAJOR, d->ws_hsdb, d->ws_hsdb_bytes,
+                                     st);
 }
 
 int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x, const float* x2,
@@ -186,7 +201,8 @@ int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x,
         x2s[i] = x2;
     }
     const csdr_decoder_config& c = d->cfg;
-    return csdr_hsdb_matmul_group_xop(n, segs, xs, x2s, 1, ys, bias, flags, xop, nw, c.rms_eps,
+    return csdr_hsdb_matmul_group_xop(n, segs, xs, x2s, d->B, ys, bias,
+                                      flags | CSDR_HSDB_TOKEN_MAJOR, xop, nw, c.rms_eps,
                                       d->attn_splits, c.head_dim, d->ws_hsdb, d->ws_hsdb_bytes,
                                       st);
 }
@@ -196,10 +212,10 @@ int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x,
 int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, float penalty) {
     const csdr_decoder_config& c = d->cfg;
     const int H = c.hidden, Hq = c.n_heads, Hkv = c.n_kv_heads, hd = c.head_dim;
-    const int cap = c.max_ctx + 1;
-    step_begin_kernel<<<1, 64, 0, st>>>(d->pos, d->ring, cap, d->tok, d->len);
+    const int cap = c.max_ctx + 1, B = d->B;
+    step_begin_kernel<<<1, 64, 0, st>>>(d->pos, d->ring, cap, B, d->tok, d->len);
     CSDR_LAUNCH_CHECK("decoder step_begin");
-    RC(csdr_hsdb_decode_row(d->emb, d->tok, 0, d->x, st));
+    RC(csdr_hsdb_decode_rows(d->emb, d->tok, B, d->x, st));
     for (int l = 0; l < c.n_layers && d->fused; ++l) {
         // fused form: 5 calls (9 launches) per block; the normed inputs, the rotated q/k, the
         // attention output and silu(gate)*up are never written out
@@ -210,13 +226,19 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
             const float* bias[3] = {L.bq, L.bk, L.bv};
             RC(mm_xop(d, 3, segs, d->x, nullptr, ys, bias, 0, CSDR_XOP_RMSNORM, L.attn_norm, st));
         }
-        RC(csdr_attn_decode_rope(d->q, d->k, d->v, L.kc, L.vc, d->len, 1, c.max_ctx, Hq, Hkv, hd,
-                                 c.rope_theta, 0.0f, nullptr, d->ws_attn, d->ws_attn_bytes, st));
+        // B == 1: the split partials stay in the workspace and the o projection combines
+        // them while staging its input; B > 1: combined into a (B x H) first
+        RC(csdr_attn_decode_rope(d->q, d->k, d->v, L.kc, L.vc, d->len, B, c.max_ctx, Hq, Hkv, hd,
+                                 c.rope_theta, 0.0f, B > 1 ? d->a : nullptr, d->ws_attn,
+                                 d->ws_attn_bytes, st));
         {
             const csdr_hsdb* segs[1] = {L.o};
             float* ys[1] = {d->x};  // x += o(attention)
-            RC(mm_xop(d, 1, segs, static_cast<const float*>(d->ws_attn), nullptr, ys, nullptr,
-                      CSDR_HSDB_ACCUMULATE, CSDR_XOP_ATTN, nullptr, st));
+            if (B == 1)
+                RC(mm_xop(d, 1, segs, static_cast<const float*>(d->ws_attn), nullptr, ys, nullptr,
+                          CSDR_HSDB_ACCUMULATE, CSDR_XOP_ATTN, nullptr, st));
+            else
+                RC(mm(d, 1, segs, d->a, ys, nullptr, CSDR_HSDB_ACCUMULATE, st));
         }
         {
             const csdr_hsdb* segs[2] = {L.gate, L.up};
@@ -230,6 +252,8 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
                       CSDR_XOP_SILU_MUL, nullptr, st));
         }
     }
+    if (!d->fused && B > 1)
+        return set_error(CSDR_E_UNSUPPORTED, "decoder: the unfused step runs batch 1 only");
     for (int l = 0; l < c.n_layers && !d->fused; ++l) {
         const Layer& L = d->layers[l];
         RC(csdr_rms_norm(d->x, L.attn_norm, 1, H, c.rms_eps, d->h, st));
@@ -266,18 +290,18 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
         CSDR_LAUNCH_CHECK("decoder advance");
         return CSDR_OK;
     }
-    if (d->final_norm) RC(csdr_rms_norm(d->x, d->final_norm, 1, H, c.rms_eps, d->h, st));
-    else CSDR_HIP_CHECK(hipMemcpyAsync(d->h, d->x, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
-    sanitize_kernel<<<1, kSanThreads, 0, st>>>(d->h, H);
+    if (d->final_norm) RC(csdr_rms_norm(d->x, d->final_norm, B, H, c.rms_eps, d->h, st));
+    else CSDR_HIP_CHECK(hipMemcpyAsync(d->h, d->x, (size_t)B * H * 4, hipMemcpyDeviceToDevice, st));
+    sanitize_kernel<<<B, kSanThreads, 0, st>>>(d->h, H);
     CSDR_LAUNCH_CHECK("decoder sanitize");
     {
         const csdr_hsdb* segs[1] = {d->lm};
         float* ys[1] = {d->logits};
         RC(mm(d, 1, segs, d->h, ys, nullptr, 0, st));
     }
-    RC(csdr_select_best(d->logits, c.vocab, d->repeated, temperature, penalty, d->tok, d->pos,
-                        d->repeated, d->ws_sel, d->ws_sel_bytes, st));
-    record_kernel<<<1, 64, 0, st>>>(d->tok, d->pos, d->ring, cap);
+    RC(csdr::select_best_rows(d->logits, c.vocab, B, d->repeated, temperature, penalty, d->tok,
+                              d->pos, d->repeated, d->ws_sel, d->ws_sel_bytes, st));
+    record_kernel<<<1, 64, 0, st>>>(d->tok, d->pos, d->ring, cap, B);
     CSDR_LAUNCH_CHECK("decoder record");
     return CSDR_OK;
 }
@@ -347,8 +371,16 @@ int run_step(csdr_decoder* d, int i, float temperature, float penalty) {
 extern "C" {
 
 CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** out) {
+    return csdr_decoder_create_batched(cfg, 1, out);
+}
+
+CSDR_API int csdr_decoder_create_batched(const csdr_decoder_config* cfg, int batch,
+                                         csdr_decoder** out) {
     if (!cfg || !out) return set_error(CSDR_E_INVALID, "decoder_create: null argument");
     *out = nullptr;
+    if (batch < 1 || batch > kMaxBatch)
+        return set_error(CSDR_E_INVALID, "decoder_create: batch must be 1.." +
+                                             std::to_string(kMaxBatch));
     const csdr_decoder_config& c = *cfg;
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
         c.n_heads % c.n_kv_heads || c.head_dim * c.n_heads != c.hidden || c.ffn <= 0 ||
@@ -358,38 +390,41 @@ CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** 
     csdr_decoder* d = new (std::nothrow) csdr_decoder();
     if (!d) return set_error(CSDR_E_INVALID, "decoder_create: out of host memory");
     d->cfg = c;
+    d->B = batch;
+    const int B = batch;
     d->layers.resize(c.n_layers);
     if (const char* e = getenv("CSDR_DECODER_GRAPH")) d->use_graph = atoi(e) != 0;
     if (const char* e = getenv("CSDR_DECODER_FUSED")) d->fused = atoi(e) != 0;
-    d->attn_splits = csdr_attn_decode_splits(1, c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx);
+    d->attn_splits = csdr_attn_decode_splits(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx);
     int rc = CSDR_OK;
-    const size_t kvn = (size_t)c.max_ctx * c.n_kv_heads * c.head_dim;
+    // per layer: sequence b's cache at b * max_ctx positions
+    const size_t kvn = (size_t)B * c.max_ctx * c.n_kv_heads * c.head_dim;
     for (auto& L : d->layers)
         if ((rc = dalloc(d, &L.kc, kvn)) || (rc = dalloc(d, &L.vc, kvn))) break;
-    const int kvw = c.n_kv_heads * c.head_dim;
-    const int wide = std::max(c.hidden, c.ffn);
-    if (!rc) rc = dalloc(d, &d->x, c.hidden);
-    if (!rc) rc = dalloc(d, &d->h, c.hidden);
-    if (!rc) rc = dalloc(d, &d->q, c.hidden);
-    if (!rc) rc = dalloc(d, &d->k, kvw);
-    if (!rc) rc = dalloc(d, &d->v, kvw);
-    if (!rc) rc = dalloc(d, &d->a, wide);
-    if (!rc) rc = dalloc(d, &d->g, c.ffn);
-    if (!rc) rc = dalloc(d, &d->u, c.ffn);
-    if (!rc) rc = dalloc(d, &d->logits, c.vocab);
-    if (!rc) rc = dalloc(d, &d->tok, 1);
+    const size_t kvw = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t wide = std::max(c.hidden, c.ffn);
+    if (!rc) rc = dalloc(d, &d->x, (size_t)B * c.hidden);
+    if (!rc) rc = dalloc(d, &d->h, (size_t)B * c.hidden);
+    if (!rc) rc = dalloc(d, &d->q, (size_t)B * c.hidden);
+    if (!rc) rc = dalloc(d, &d->k, B * kvw);
+    if (!rc) rc = dalloc(d, &d->v, B * kvw);
+    if (!rc) rc = dalloc(d, &d->a, B * wide);
+    if (!rc) rc = dalloc(d, &d->g, (size_t)B * c.ffn);
+    if (!rc) rc = dalloc(d, &d->u, (size_t)B * c.ffn);
+    if (!rc) rc = dalloc(d, &d->logits, (size_t)B * c.vocab);
+    if (!rc) rc = dalloc(d, &d->tok, (size_t)B);
     if (!rc) rc = dalloc(d, &d->pos, 1);
-    if (!rc) rc = dalloc(d, &d->len, 1);
-    if (!rc) rc = dalloc(d, &d->ring, (size_t)c.max_ctx + 1);
-    if (!rc) rc = dalloc(d, &d->repeated, c.vocab);
+    if (!rc) rc = dalloc(d, &d->len, (size_t)B);
+    if (!rc) rc = dalloc(d, &d->ring, (size_t)B * (c.max_ctx + 1));
+    if (!rc) rc = dalloc(d, &d->repeated, (size_t)B * c.vocab);
     if (!rc) {
-        d->ws_attn_bytes = csdr_attn_decode_workspace_bytes(1, c.n_heads, c.head_dim, c.max_ctx);
+        d->ws_attn_bytes = csdr_attn_decode_workspace_bytes(B, c.n_heads, c.head_dim, c.max_ctx);
         unsigned char* p = nullptr;
         rc = dalloc(d, &p, d->ws_attn_bytes);
         d->ws_attn = p;
     }
     if (!rc) {
-        d->ws_sel_bytes = csdr_select_workspace_bytes();
+        d->ws_sel_bytes = csdr::select_workspace_rows(B);
         unsigned char* p = nullptr;
         rc = dalloc(d, &p, d->ws_sel_bytes);
         d->ws_sel = p;
@@ -442,10 +477,11 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* d, int layer, const csdr_hsdb*
     RC(upload_vec(d, &L.bv, bv, kvw));
     const csdr_hsdb* qkv[3] = {wq, wk, wv};
     const csdr_hsdb* gu[2] = {wgate, wup};
-    d->ws_hsdb_bytes = std::max({d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(3, qkv, 1),
-                                 csdr_hsdb_group_workspace_bytes(1, &wo, 1),
-                                 csdr_hsdb_group_workspace_bytes(2, gu, 1),
-                                 csdr_hsdb_group_workspace_bytes(1, &wdown, 1)});
+    const int B = d->B;
+    d->ws_hsdb_bytes = std::max({d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(3, qkv, B),
+                                 csdr_hsdb_group_workspace_bytes(1, &wo, B),
+                                 csdr_hsdb_group_workspace_bytes(2, gu, B),
+                                 csdr_hsdb_group_workspace_bytes(1, &wdown, B)});
     return CSDR_OK;
 }
 
@@ -461,7 +497,7 @@ CSDR_API int csdr_decoder_set_output(csdr_decoder* d, const csdr_hsdb* lm_head,
     d->emb = embedding ? embedding : lm_head;
     RC(upload_vec(d, &d->final_norm, final_norm, c.hidden));
     d->ws_hsdb_bytes =
-        std::max(d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(1, &lm_head, 1));
+        std::max(d->ws_hsdb_bytes, csdr_hsdb_group_workspace_bytes(1, &lm_head, d->B));
     return CSDR_OK;
 }
 
@@ -473,7 +509,8 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
         return set_error(CSDR_E_INVALID, "decoder_prefill: empty prompt");
     if (n_prompt > c.max_ctx)
         return set_error(CSDR_E_INVALID, "decoder_prefill: prompt longer than the context");
-    for (int i = 0; i < n_prompt; ++i)
+    const int B = d->B;
+    for (long long i = 0; i < (long long)B * n_prompt; ++i)
         if (prompt[i] < 0 || prompt[i] >= c.vocab)
             return set_error(CSDR_E_INVALID, "decoder_prefill: token id out of range");
     if (d->use_graph) {
@@ -482,10 +519,12 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
     }
     hipStream_t st = d->stream;
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
+    const size_t cap = (size_t)c.max_ctx + 1;
     CSDR_HIP_CHECK(hipMemset(d->pos, 0, 4));
-    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, c.vocab));
-    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)(c.max_ctx + 1) * 4));
-    CSDR_HIP_CHECK(hipMemcpy(d->ring, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, (size_t)B * c.vocab));
+    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)B * cap * 4));
+    CSDR_HIP_CHECK(hipMemcpy2D(d->ring, cap * 4, prompt, (size_t)n_prompt * 4,
+                               (size_t)n_prompt * 4, B, hipMemcpyHostToDevice));
     for (int i = 0; i + 1 < n_prompt; ++i) RC(run_step(d, 0, temperature, penalty));
     RC(run_step(d, 1, temperature, penalty));
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
@@ -511,8 +550,10 @@ CSDR_API int csdr_decoder_tokens(const csdr_decoder* d, int first, int count, in
     if (!d || !out || first < 0 || count < 0 || first + count > d->cfg.max_ctx + 1)
         return set_error(CSDR_E_INVALID, "decoder_tokens: bad argument");
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    const size_t cap = (size_t)d->cfg.max_ctx + 1;
     if (count)
-        CSDR_HIP_CHECK(hipMemcpy(out, d->ring + first, (size_t)count * 4, hipMemcpyDeviceToHost));
+        CSDR_HIP_CHECK(hipMemcpy2D(out, (size_t)count * 4, d->ring + first, cap * 4,
+                                   (size_t)count * 4, d->B, hipMemcpyDeviceToHost));
     return CSDR_OK;
 }
 
@@ -528,21 +569,27 @@ CSDR_API int csdr_decoder_generate(csdr_decoder* d, const int32_t* prompt, int n
     RC(csdr_decoder_prefill(d, prompt, n_prompt, temperature, penalty));
     RC(csdr_decoder_decode(d, steps - 1, temperature, penalty));
     RC(csdr_decoder_tokens(d, n_prompt, steps, out_tokens));
-    int n = 0;
-    while (n < steps) {
-        if (out_tokens[n] < 0) break;  // no finite score: the reference fails the step
-        ++n;
-        if (eos_id >= 0 && out_tokens[n - 1] == eos_id) break;
+    bool any = false;
+    for (int b = 0; b < d->B; ++b) {
+        const int32_t* t = out_tokens + (size_t)b * steps;
+        int n = 0;
+        while (n < steps) {
+            if (t[n] < 0) break;  // no finite score: the reference fails the step
+            ++n;
+            if (eos_id >= 0 && t[n - 1] == eos_id) break;
+        }
+        n_generated[b] = n;
+        any = any || n > 0;
     }
-    *n_generated = n;
-    if (n == 0) return set_error(CSDR_E_UNSUPPORTED, "decoder_generate: no finite logit");
+    if (!any) return set_error(CSDR_E_UNSUPPORTED, "decoder_generate: no finite logit");
     return CSDR_OK;
 }
 
 CSDR_API int csdr_decoder_logits(const csdr_decoder* d, float* out) {
     if (!d || !out) return set_error(CSDR_E_INVALID, "decoder_logits: bad argument");
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
-    CSDR_HIP_CHECK(hipMemcpy(out, d->logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    CSDR_HIP_CHECK(
+        hipMemcpy(out, d->logits, (size_t)d->B * d->cfg.vocab * 4, hipMemcpyDeviceToHost));
     return CSDR_OK;
 }
 
@@ -554,11 +601,15 @@ CSDR_API int csdr_decoder_load_kv(csdr_decoder* d, int layer, const uint16_t* k,
                                   int n) {
     if (!d || layer < 0 || layer >= d->cfg.n_layers || !k || !v || n < 0 || n > d->cfg.max_ctx)
         return set_error(CSDR_E_INVALID, "decoder_load_kv: bad argument");
-    const size_t bytes = (size_t)n * d->cfg.n_kv_heads * d->cfg.head_dim * 2;
+    // sequence b's n rows follow sequence b - 1's in the source, and start at b * max_ctx in
+    // the cache
+    const size_t row = (size_t)d->cfg.n_kv_heads * d->cfg.head_dim * 2;
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
-    if (bytes) {
-        CSDR_HIP_CHECK(hipMemcpy(d->layers[layer].kc, k, bytes, hipMemcpyDefault));
-        CSDR_HIP_CHECK(hipMemcpy(d->layers[layer].vc, v, bytes, hipMemcpyDefault));
+    if (n) {
+        CSDR_HIP_CHECK(hipMemcpy2D(d->layers[layer].kc, row * d->cfg.max_ctx, k, row * n, row * n,
+                                   d->B, hipMemcpyDefault));
+        CSDR_HIP_CHECK(hipMemcpy2D(d->layers[layer].vc, row * d->cfg.max_ctx, v, row * n, row * n,
+                                   d->B, hipMemcpyDefault));
     }
     return CSDR_OK;
 }
@@ -567,16 +618,30 @@ CSDR_API int csdr_decoder_load_kv(csdr_decoder* d, int layer, const uint16_t* k,
 // `token` is the token at `position` (the next decode step consumes it). The
 // generated-token set starts empty.
 CSDR_API int csdr_decoder_set_position(csdr_decoder* d, int position, int32_t token) {
-    if (!d || position < 0 || position >= d->cfg.max_ctx || token < 0 || token >= d->cfg.vocab)
+    if (!d) return set_error(CSDR_E_INVALID, "decoder_set_position: bad argument");
+    std::vector<int32_t> t((size_t)d->B, token);
+    return csdr_decoder_set_position_batch(d, position, t.data());
+}
+
+CSDR_API int csdr_decoder_set_position_batch(csdr_decoder* d, int position,
+                                             const int32_t* tokens) {
+    if (!d || !tokens || position < 0 || position >= d->cfg.max_ctx)
         return set_error(CSDR_E_INVALID, "decoder_set_position: bad argument");
+    for (int b = 0; b < d->B; ++b)
+        if (tokens[b] < 0 || tokens[b] >= d->cfg.vocab)
+            return set_error(CSDR_E_INVALID, "decoder_set_position: token id out of range");
+    const size_t cap = (size_t)d->cfg.max_ctx + 1;
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
     CSDR_HIP_CHECK(hipMemcpy(d->pos, &position, 4, hipMemcpyHostToDevice));
-    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, d->cfg.vocab));
-    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)(d->cfg.max_ctx + 1) * 4));
-    CSDR_HIP_CHECK(hipMemcpy(d->ring + position, &token, 4, hipMemcpyHostToDevice));
+    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, (size_t)d->B * d->cfg.vocab));
+    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)d->B * cap * 4));
+    CSDR_HIP_CHECK(hipMemcpy2D(d->ring + position, cap * 4, tokens, 4, 4, d->B,
+                               hipMemcpyHostToDevice));
     d->host_pos = position;
     d->n_prompt = std::max(1, position);
     return CSDR_OK;
 }
+
+CSDR_API int csdr_decoder_batch(const csdr_decoder* d) { return d ? d->B : -1; }
 
 }  // extern "C"

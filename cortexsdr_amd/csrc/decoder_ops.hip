@@ -12,6 +12,7 @@
 // captured once in a HIP graph and replayed for every token.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 
 #include <cmath>
@@ -901,11 +902,17 @@ __device__ __forceinline__ void better(float& bs, int& bi, float s, int i) {
     }
 }
 
+// Row blockIdx.y of `rows` rows of n scores (one per sequence of a batch): logits, repeated
+// and the workspace pairs are offset by the row.
 __global__ __launch_bounds__(kThreads) void select1_kernel(const float* __restrict__ logits, int n,
                                                            const uint8_t* __restrict__ repeated,
                                                            float ts, float penalty,
                                                            float* __restrict__ ws_s,
                                                            int* __restrict__ ws_i) {
+    logits += (size_t)blockIdx.y * n;
+    if (repeated) repeated += (size_t)blockIdx.y * n;
+    ws_s += (size_t)blockIdx.y * gridDim.x;
+    ws_i += (size_t)blockIdx.y * gridDim.x;
     __shared__ float ss[kThreads];
     __shared__ int si[kThreads];
     float bs = -INFINITY;
@@ -940,11 +947,18 @@ __global__ __launch_bounds__(kThreads) void select1_kernel(const float* __restri
     }
 }
 
+// Row blockIdx.x: its nb stage-1 pairs, its token out[row], its generated-token set; the
+// position advances once (row 0).
 __global__ __launch_bounds__(kThreads) void select2_kernel(const float* __restrict__ ws_s,
                                                            const int* __restrict__ ws_i, int nb,
                                                            int* __restrict__ out,
                                                            int* __restrict__ pos_dev,
-                                                           uint8_t* __restrict__ repeated) {
+                                                           uint8_t* __restrict__ repeated, int n) {
+    const int row = blockIdx.x;
+    ws_s += (size_t)row * nb;
+    ws_i += (size_t)row * nb;
+    out += row;
+    if (repeated) repeated += (size_t)row * n;
     __shared__ float ss[kThreads];
     __shared__ int si[kThreads];
     float bs = -INFINITY;
@@ -974,7 +988,7 @@ __global__ __launch_bounds__(kThreads) void select2_kernel(const float* __restri
     }
     if (threadIdx.x == 0) {
         *out = si[0];
-        if (pos_dev) *pos_dev += 1;                       // next decode position
+        if (pos_dev && row == 0) *pos_dev += 1;           // next decode position
         if (repeated && si[0] >= 0) repeated[si[0]] = 1;  // generated-token set
     }
 }
@@ -1112,6 +1126,32 @@ int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, con
 
 }  // namespace
 
+namespace csdr {
+
+size_t select_workspace_rows(int rows) { return (size_t)kSelectBlocks * 8 * (size_t)rows; }
+
+int select_best_rows(const float* logits, int n, int rows, const uint8_t* repeated,
+                     float temperature, float penalty, int* out_tokens, int* pos_dev,
+                     uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
+                     hipStream_t st) {
+    if (!logits || n <= 0 || rows <= 0 || !out_tokens)
+        return set_error(CSDR_E_INVALID, "select_best: bad argument");
+    if (!workspace || workspace_bytes < select_workspace_rows(rows))
+        return set_error(CSDR_E_WORKSPACE, "select_best: workspace too small");
+    const float ts = temperature > 0.0f ? 1.0f / temperature : 1.0f;
+    const int nb = std::min(kSelectBlocks, (n + kThreads - 1) / kThreads);
+    float* ws_s = static_cast<float*>(workspace);
+    int* ws_i = reinterpret_cast<int*>(ws_s + (size_t)nb * rows);
+    select1_kernel<<<dim3(nb, rows), kThreads, 0, st>>>(logits, n, repeated, ts, penalty, ws_s,
+                                                        ws_i);
+    select2_kernel<<<rows, kThreads, 0, st>>>(ws_s, ws_i, nb, out_tokens, pos_dev,
+                                              repeated_update, n);
+    CSDR_LAUNCH_CHECK("select_best");
+    return CSDR_OK;
+}
+
+}  // namespace csdr
+
 extern "C" {
 
 CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, float eps, float* y,
@@ -1204,18 +1244,9 @@ CSDR_API int csdr_select_best(const float* logits, int n, const uint8_t* repeate
                               float temperature, float penalty, int* out_token, int* pos_dev,
                               uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
                               void* hip_stream) {
-    if (!logits || n <= 0 || !out_token) return set_error(CSDR_E_INVALID, "select_best: bad argument");
-    if (!workspace || workspace_bytes < csdr_select_workspace_bytes())
-        return set_error(CSDR_E_WORKSPACE, "select_best: workspace too small");
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    const float ts = temperature > 0.0f ? 1.0f / temperature : 1.0f;
-    float* ws_s = static_cast<float*>(workspace);
-    int* ws_i = reinterpret_cast<int*>(ws_s + kSelectBlocks);
-    const int nb = std::min(kSelectBlocks, (n + kThreads - 1) / kThreads);
-    select1_kernel<<<nb, kThreads, 0, st>>>(logits, n, repeated, ts, penalty, ws_s, ws_i);
-    select2_kernel<<<1, kThreads, 0, st>>>(ws_s, ws_i, nb, out_token, pos_dev, repeated_update);
-    CSDR_LAUNCH_CHECK("select_best");
-    return CSDR_OK;
+    return csdr::select_best_rows(logits, n, 1, repeated, temperature, penalty, out_token,
+                                  pos_dev, repeated_update, workspace, workspace_bytes,
+                                  static_cast<hipStream_t>(hip_stream));
 }
 
 }  // extern "C"

@@ -67,6 +67,7 @@ constexpr int kMaxGroup = 8;
 constexpr int kMaxSlotsArg = 32;
 constexpr int kStageBatch = 8;  // global loads in flight per thread while staging to LDS
 constexpr int kMaxXopM = 16;  // columns an x op supports
+constexpr int kMaxVecM = 8;   // columns of the streaming multi-column gather
 constexpr int kAttnStatMax = 2048;  // (head, split) partials whose weights the combine keeps in LDS
 
 // One coded matrix of a grouped launch.
@@ -96,6 +97,7 @@ struct MatDesc {
 struct Params {
     MatDesc m[kMaxGroup];
     int G, M, MVz, x_f16;
+    int tm;  // token-major X (M x C) and Y (M x R) instead of feature-major (C x M, R x M)
     int accumulate;  // 1: Y += W.X (+ bias); 0: Y = W.X (+ bias)
     // input transform applied while staging x (csdr_hsdb_matmul_group_xop)
     int xop;          // CSDR_XOP_*
@@ -125,6 +127,16 @@ __device__ __forceinline__ float xval(const void* x, size_t i) {
 }
 __device__ __forceinline__ float xload(const void* x, int f16, size_t i) {
     return f16 ? xval<_Float16>(x, i) : xval<float>(x, i);
+}
+
+// Element (feature k, column m) of X (and of the x op's second input), and element (row r,
+// column m) of Y, in the call's layout: feature-major (the reference matmulRowMajor's C x M /
+// R x M) or token-major (linear_forward's M x C / M x R).
+__device__ __forceinline__ size_t xi(const Params& p, const MatDesc& d, int k, int m) {
+    return p.tm ? (size_t)m * (d.C_full + d.Ce) + k : (size_t)k * p.M + m;
+}
+__device__ __forceinline__ size_t yi(const Params& p, const MatDesc& d, int r, int m) {
+    return p.tm ? (size_t)m * d.R + r : (size_t)r * p.M + m;
 }
 
 // xs[i] = float(src[i]) for i < n by the whole workgroup, kStageBatch independent loads
@@ -213,7 +225,7 @@ __device__ __forceinline__ float xop_apply(const Params& p, const MatDesc& d, fl
                                            int m, const float* inv) {
     if (p.xop == CSDR_XOP_RMSNORM) return v * inv[m] * p.nw[k];
     if (p.xop == CSDR_XOP_SILU_MUL) {
-        const float u = static_cast<const float*>(d.x2)[(size_t)k * p.M + m];
+        const float u = static_cast<const float*>(d.x2)[xi(p, d, k, m)];
         return (v * (1.0f / (1.0f + expf(-v)))) * u;
     }
     return v;
@@ -241,7 +253,7 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
         for (int m = 0; m < M; ++m) {
             float ss = 0.f;
             for (int k = tid; k < C; k += NT) {
-                const float v = xf[(size_t)k * M + m];
+                const float v = xf[xi(p, d, k, m)];
                 ss = fmaf(v, v, ss);
             }
             ss = wg_sum<NT>(ss, red);
@@ -278,6 +290,19 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
             for (int s2 = 0; s2 < ns; ++s2) num = fmaf(wh[s2], po[(size_t)s2 * hd], num);
             xs[i] = num * wh[ns];
         }
+    } else if (p.tm && M > 1) {
+        // token-major X: element (feature f0 + i / M, column i % M), kStageBatch loads in flight
+        const int f0 = b0 * 64;
+        for (int i0 = 0; i0 < nx; i0 += NT * kStageBatch) {
+            float v[kStageBatch];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = min(i0 + j * NT + tid, nx - 1);
+                v[j] = xload(d.x, p.x_f16, xi(p, d, f0 + i / M, i % M));
+            }
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) xs[min(i0 + j * NT + tid, nx - 1)] = v[j];
+        }
     } else if (p.x_f16) {
         stage_to_lds<_Float16, NT>(static_cast<const _Float16*>(d.x) + xbase, nx, xs);
     } else {
@@ -294,7 +319,7 @@ __device__ void stage_x_chunk(const Params& p, const MatDesc& d, int b0, int nb,
             for (int t = tid; t < d.Ce * M; t += NT) {
                 const int cc = t / M, m = t % M;
                 const int k = d.C_full + cc;
-                xe[t] = xop_apply(p, d, xf[(size_t)k * M + m], k, m, inv);
+                xe[t] = xop_apply(p, d, xf[xi(p, d, k, m)], k, m, inv);
             }
         }
     } else if (p.xop == CSDR_XOP_ATTN && do_xe && xe) {
@@ -483,7 +508,7 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
         const size_t ye = min(ytot, (size_t)(u + 1) * yper);
         for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
-            const float bv = d.bias ? d.bias[i / M] : 0.0f;
+            const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
             d.y[i] = p.accumulate ? d.y[i] + bv : bv;
         }
     }
@@ -563,10 +588,11 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
             const float* drow = d.dict + (size_t)a * d.blen;
             for (int t = lane; t < d.blen; t += 64) {
                 const float dv = drow[t];
-                const size_t xo = ((size_t)b * d.blen + t) * M + m0;
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (j < nm) acc[j] = fmaf(dv, xload(d.x, p.x_f16, xo + j), acc[j]);
+                    if (j < nm)
+                        acc[j] = fmaf(dv, xload(d.x, p.x_f16, xi(p, d, b * d.blen + t, m0 + j)),
+                                      acc[j]);
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = csdr::wave_sum(acc[j]);
@@ -602,7 +628,7 @@ __device__ __forceinline__ float edge_term(const Params& p, const MatDesc& d, in
         return s;
     }
     for (int cc = 0; cc < d.Ce; ++cc)
-        s = fmaf(e[cc], xload(d.x, p.x_f16, (size_t)(d.C_full + cc) * p.M + m), s);
+        s = fmaf(e[cc], xload(d.x, p.x_f16, xi(p, d, d.C_full + cc, m)), s);
     return s;
 }
 
@@ -809,6 +835,189 @@ void gatherw_kernel(Params p) {
     }
 }
 
+// ---- kernel 2, 2 <= M <= 8: the same streaming gather with MC columns per code read
+// Workgroup = (matrix, chunk, row range) as in gatherw_kernel; the chunk's P slice is staged
+// in LDS as [block][atom][MC] fp32 (columns past M zero), so each slot's MC values are one or
+// two 16-byte LDS reads and every code word feeds MC fused multiply-adds: the codes are read
+// from HBM once for all M columns. Row totals (MC per row) wait in LDS and go into Y with one
+// device-scope atomic per (row, column) after the stream. WPE: waves per SIMD the register
+// budget is pinned for (1 workgroup per CU for the 128 KiB slice at MC = 8, 2 below).
+constexpr int kGvMaxRows = 512;  // rows per workgroup (row totals in LDS: 16 KiB at MC = 8)
+
+template <int SLOTS, int MC, int DEPTH, int WPE>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
+void gatherv_kernel(Params p) {
+    extern __shared__ float smem[];
+    const int wg = (int)blockIdx.x;
+    int g = 0;
+    while (g + 1 < p.G && wg >= p.m[g + 1].g_base) ++g;
+    const MatDesc& d = p.m[g];
+    const int u = wg - d.g_base;
+    const int nfull = d.NB / d.NBc;
+    int c, sidx, rpw;
+    if (u < nfull * d.splits) {
+        c = u % nfull;
+        sidx = u / nfull;
+        rpw = d.rows_per_wg;
+    } else {
+        int v = u - nfull * d.splits, j = 0;
+        while (j < 4 && v >= d.rsplit[j]) v -= d.rsplit[j++];
+        if (j == 4) return;
+        c = nfull + j;
+        sidx = v;
+        rpw = d.rrpw[j];
+    }
+    uint32_t b0u, nbcu;
+    csdr::chunk_span((uint32_t)c, (uint32_t)d.NB, (uint32_t)d.NBc, b0u, nbcu);
+    const int b0 = (int)b0u, nbc = (int)nbcu;
+    const int rbeg = sidx * rpw;
+    const int rend = min(d.R, rbeg + rpw);
+    const int M = p.M;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    constexpr int PPB = SLOTS / 4;  // 16-byte pieces per tile
+    const int ppr = nbc * PPB;      // pieces per row: a power of two <= 64
+    const int npieces = (rend - rbeg) * ppr;
+    const int nload = (npieces + 63) >> 6;
+    const int per = (nload + kGWaves - 1) / kGWaves;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int nk = max(0, min(per, nload - wv * per));
+    const int wfirst = wv * per * 64;
+    const int wvalid = max(0, min(per * 64, npieces - wfirst));
+    const uint32_t* wbase = d.codes + (size_t)b0 * d.R * SLOTS + (size_t)rbeg * nbc * SLOTS +
+                            (size_t)wfirst * 4;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, wvalid * 16, kRawBufferDword3);
+    constexpr int kStep = 64;
+    auto piece = [&](int k) -> u32x4 {
+        return __builtin_amdgcn_raw_buffer_load_b128(rs, (k * kStep + lane) * 16, 0, kCachePolicyNT);
+    };
+
+    float* Ps = smem;                          // NBc * K * MC floats
+    float* xe = Ps + (size_t)d.NBc * d.K * MC;  // Ce (< 64) x MC floats
+    float* rowt = xe + 64 * MC;                 // (rend - rbeg) x MC row totals
+    const bool edge = (c == d.nchunks - 1) && d.Ce > 0;
+
+    // the wave's first code loads go out before the P slice is staged (they overlap it)
+    constexpr int NBUF = DEPTH + 1;
+    u32x4 buf[NBUF];
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k) buf[k] = piece(k);
+    {
+        // P slice: global [block][atom][M] -> LDS [block][atom][MC], kStageBatch loads in flight
+        const float* Pg = d.P + (size_t)b0 * d.K * M;
+        const int n = nbc * d.K * MC;
+        for (int i0 = 0; i0 < n; i0 += kGThreads * kStageBatch) {
+            float v[kStageBatch];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = min(i0 + j * kGThreads + tid, n - 1);
+                const int e = i / MC, m = i - e * MC;
+                v[j] = Pg[(size_t)e * M + min(m, M - 1)];
+                if (m >= M) v[j] = 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) Ps[min(i0 + j * kGThreads + tid, n - 1)] = v[j];
+        }
+    }
+    __syncthreads();
+
+    const int pl = lane & (ppr - 1);
+    const int lg_ppr = __builtin_ctz((unsigned)ppr);
+    const int bb = pl / PPB, h = pl - bb * PPB;
+    const float* Pb = Ps + (size_t)bb * d.K * MC;
+    float gm[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        gm[e] = sgam_at(d, e);
+#pragma unroll
+        for (int hh = 1; hh < PPB; ++hh)
+            if (h == hh) gm[e] = sgam_at(d, hh * 4 + e);
+    }
+    const bool gu = d.gunif != 0;
+    const float g0 = d.sgam[0];
+    const bool head = (pl == 0);
+    const int q0 = wfirst + lane;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    auto consume = [&](const u32x4& w, int k) {
+        const int qp = q0 + k * kStep;
+        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+        float acc[MC];
+#pragma unroll
+        for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float cf = gu ? csdr::h2f(w4[e] >> 16) : gm[e] * csdr::h2f(w4[e] >> 16);
+            const float* pv = Pb + (size_t)(uint16_t)w4[e] * MC;
+#pragma unroll
+            for (int m4 = 0; m4 < MC; m4 += 4) {
+                if constexpr (MC >= 4) {
+                    const f4 v = *reinterpret_cast<const f4*>(pv + m4);
+                    acc[m4] = fmaf(cf, v.x, acc[m4]);
+                    acc[m4 + 1] = fmaf(cf, v.y, acc[m4 + 1]);
+                    acc[m4 + 2] = fmaf(cf, v.z, acc[m4 + 2]);
+                    acc[m4 + 3] = fmaf(cf, v.w, acc[m4 + 3]);
+                } else {
+#pragma unroll
+                    for (int m = 0; m < MC; ++m) acc[m] = fmaf(cf, pv[m], acc[m]);
+                }
+            }
+        }
+        const bool live = qp < npieces;
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+            float a = live ? acc[m] : 0.0f;
+            if (ppr > 1) a += dpp_move<0xB1>(a);
+            if (ppr > 2) a += dpp_move<0x4E>(a);
+            if (ppr > 4) a += dpp_move<0x141>(a);
+            if (ppr > 8) a += dpp_move<0x140>(a);
+            if (ppr > 16) a += __shfl_xor(a, 16, 64);
+            if (ppr > 32) a += __shfl_xor(a, 32, 64);
+            acc[m] = a;
+        }
+        if (head && live) {
+            float* rt = rowt + (size_t)(qp >> lg_ppr) * MC;
+#pragma unroll
+            for (int m = 0; m < MC; ++m) rt[m] = gu ? acc[m] * g0 : acc[m];
+        }
+    };
+    int k0 = 0;
+    for (; k0 + NBUF <= nk; k0 += NBUF) {
+#pragma unroll
+        for (int jj = 0; jj < NBUF; ++jj) {
+            const u32x4 w = buf[jj];
+            buf[(jj + DEPTH) % NBUF] = piece(k0 + jj + DEPTH);
+            consume(w, k0 + jj);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NBUF - 1; ++jj)
+        if (k0 + jj < nk) consume(buf[jj], k0 + jj);
+    // the top-right strip's inputs of the last chunk: [cc][m] (x-op transformed when given)
+    if (edge) {
+        for (int t = tid; t < d.Ce * MC; t += kGThreads) {
+            const int cc = t / MC, m = t - cc * MC;
+            float v = 0.0f;
+            if (m < M)
+                v = d.xe ? d.xe[(size_t)cc * M + m] : xload(d.x, p.x_f16, xi(p, d, d.C_full + cc, m));
+            xe[t] = v;
+        }
+    }
+    __syncthreads();
+    const int nr = rend - rbeg;
+    for (int t = tid; t < nr * M; t += kGThreads) {
+        // consecutive threads on consecutive Y addresses in either layout
+        const int rr = p.tm ? t % nr : t / M, m = p.tm ? t / nr : t - (t / M) * M;
+        float v = rowt[(size_t)rr * MC + m];
+        if (edge) {
+            const float* er = d.edge + (size_t)(rbeg + rr) * d.Ce;
+            for (int cc = 0; cc < d.Ce; ++cc) v = fmaf(er[cc], xe[cc * MC + m], v);
+        }
+        __hip_atomic_fetch_add(d.y + yi(p, d, rbeg + rr, m), v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ---- kernel 2, any M / any slot count: workgroup = (chunk, row tile of Rt rows); the
 // chunk's P slice is staged MV columns at a time, code words are read per pair.
 template <int MV>
@@ -867,7 +1076,7 @@ __global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
             for (int bb = 0; bb < nbc; ++bb) sum += part[(rr * nbc + bb) * MV + mm];
             const int r = r0 + rr;
             if (last_chunk && d.Ce > 0) sum += edge_term(p, d, r, m);
-            __hip_atomic_fetch_add(d.y + (size_t)r * M + m, sum, __ATOMIC_RELAXED,
+            __hip_atomic_fetch_add(d.y + yi(p, d, r, m), sum, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
     }
@@ -905,13 +1114,15 @@ __global__ __launch_bounds__(kThreads) void decode_dense_kernel(csdr_hsdb s,
     }
 }
 
-// One row of W (1-row tiles) into out[C]: the row's tiles decoded as decode_dense_kernel
-// does, then its edge columns. The row index is read from device memory (a token id).
+// Rows of W (1-row tiles) into out[blockIdx.y][C]: each row's tiles decoded as
+// decode_dense_kernel does, then its edge columns. Row blockIdx.y's index is read from device
+// memory (a token id) when row_dev is given; an index outside [0, R) leaves its row untouched.
 __global__ __launch_bounds__(kThreads) void decode_row_kernel(csdr_hsdb s,
                                                               const int* __restrict__ row_dev,
                                                               int row_host, float* __restrict__ out) {
-    const int r = row_dev ? *row_dev : row_host;
+    const int r = row_dev ? row_dev[blockIdx.y] : row_host;
     if (r < 0 || r >= (int)s.R) return;
+    out += (size_t)blockIdx.y * s.C;
     const uint32_t B = s.tile_cols;
     for (uint32_t g = blockIdx.x * kThreads + threadIdx.x; g < s.C; g += gridDim.x * kThreads) {
         if (g >= s.C_full) {
@@ -1250,6 +1461,36 @@ void launch_gatherw(const Params& p, int slots, int grid, size_t lds, hipStream_
         launch_gatherw_p<false>(p, slots, grid, lds, st);
 }
 
+// The 2 <= M <= 8 gather: MC = M rounded up to 2, 4 or 8; the 128 KiB P slice of MC = 8 allows
+// one workgroup per CU (4 waves per SIMD for the register budget), the smaller ones two.
+template <int MC, int WPE>
+void launch_gatherv_mc(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
+    constexpr int kDepth = MC == 8 ? 6 : 4;
+    const void* fn = nullptr;
+    switch (slots) {
+        case 4: fn = reinterpret_cast<const void*>(&gatherv_kernel<4, MC, kDepth, WPE>); break;
+        case 8: fn = reinterpret_cast<const void*>(&gatherv_kernel<8, MC, kDepth, WPE>); break;
+        default: fn = reinterpret_cast<const void*>(&gatherv_kernel<16, MC, kDepth, WPE>); break;
+    }
+    if (lds > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    switch (slots) {
+        case 4: gatherv_kernel<4, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
+        case 8: gatherv_kernel<8, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
+        default: gatherv_kernel<16, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
+    }
+}
+
+inline int gatherv_mc(int M) { return M <= 2 ? 2 : (M <= 4 ? 4 : 8); }
+inline int gatherv_wgs_per_cu(int mc) { return mc == 8 ? 1 : 2; }
+
+void launch_gatherv(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
+    switch (gatherv_mc(p.M)) {
+        case 2: launch_gatherv_mc<2, 8>(p, slots, grid, lds, st); break;
+        case 4: launch_gatherv_mc<4, 8>(p, slots, grid, lds, st); break;
+        default: launch_gatherv_mc<8, 4>(p, slots, grid, lds, st); break;
+    }
+}
+
 // Row ranges for the M == 1 gather, balanced by bytes: a workgroup of a chunk of nbc block
 // columns gets about U / nbc rows, U = all block-rows / target, so every workgroup streams
 // about the same code bytes whatever its chunk's width. Per matrix, the full chunks share one
@@ -1258,7 +1499,7 @@ void launch_gatherw(const Params& p, int slots, int grid, size_t lds, hipStream_
 // ranges per chunk, ranges are added one class at a time (all full chunks of a matrix, or one
 // remainder chunk) to the class with the most block-rows per workgroup while the total stays
 // within the target.
-void plan_gather_splits(Params& p, int n, long long target) {
+void plan_gather_splits(Params& p, int n, long long target, int max_rows) {
     struct Cls {
         int g, j;       // matrix, remainder index (-1: the full chunks)
         int width, count, R;
@@ -1276,7 +1517,7 @@ void plan_gather_splits(Params& p, int n, long long target) {
         auto add = [&](int j, int width, int count) {
             Cls c{i, j, width, count, d.R, 1};
             c.splits = (int)std::max(1.0, std::floor((double)d.R * width / U));
-            c.splits = std::max(c.splits, (d.R + kGMaxRows - 1) / kGMaxRows);
+            c.splits = std::max(c.splits, (d.R + max_rows - 1) / max_rows);
             c.splits = std::min(c.splits, d.R);
             used += (long long)c.splits * count;
             cls[ncls++] = c;
@@ -1367,10 +1608,22 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
                 return set_error(CSDR_E_INVALID, "hsdb_matmul: SiLU x op needs x2");
         }
     }
-    if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE &&
+    const bool tm = (flags & CSDR_HSDB_TOKEN_MAJOR) && M > 1;
+    // 2 <= M <= 8: the streaming multi-column gather reads every code once for all columns
+    // (fp32 throughout), where the matrix-core path decodes each weight through the LDS
+    // dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count in the group) and
+    // a P slice within the gather's budget
+    bool vec = M >= 2 && M <= kMaxVecM;
+    for (int i = 0; i < n && vec; ++i) {
+        const csdr_hsdb* s = segs[i];
+        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMaxRows) * 4 * gatherv_mc(M);
+        vec = s->tile_rows == 1 && s->NB > 0 && (s->slots == 4 || s->slots == 8 || s->slots == 16) &&
+              s->slots == segs[0]->slots && lds <= 160 * 1024;
+    }
+    if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE && !vec &&
         csdr::mfma_eligible(n, segs, M))
         return csdr::mfma_matmul(n, segs, xs, x_dtype, M, ys, bias,
-                                 (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0, workspace,
+                                 (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0, tm ? 1 : 0, workspace,
                                  workspace_bytes, st);
     const size_t need = p_path_ws_bytes(n, segs, M);
     if (!workspace || workspace_bytes < need)
@@ -1385,6 +1638,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     const int MV = (M == 1 || max_pk * 4 * 4 > 96 * 1024) ? 1 : 4;
     p.MVz = (M + MV - 1) / MV;
     p.x_f16 = (x_dtype == CSDR_F16);
+    p.tm = tm ? 1 : 0;
     p.accumulate = (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0;
     p.xop = xa.xop;
     p.nw = xa.nw;
@@ -1463,21 +1717,23 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             ncu = v;
     }
     int base = 0;
-    if (fast) {
-        // kGWgsPerCu workgroups per CU, fewer for small groups: at least kGMinWgBytes of
-        // codes per workgroup (each one stages a P slice of up to 16 KiB first)
-        long long target = (long long)ncu * kGWgsPerCu;
+    if (fast || vec) {
+        // M == 1: kGWgsPerCu workgroups per CU; 2 <= M <= 8: as many as the P slice of MC
+        // columns allows; fewer for small groups: at least kGMinWgBytes of codes per workgroup
+        // (each one stages a P slice first)
+        const int mc = fast ? 1 : gatherv_mc(M);
+        long long target = (long long)ncu * (fast ? kGWgsPerCu : gatherv_wgs_per_cu(mc));
         long long code_bytes = 0;
         for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
         const long long min_bytes = kGMinWgBytes;
         target = std::max(1LL, std::min(target, code_bytes / std::max(1LL, min_bytes)));
-        plan_gather_splits(p, n, target);
+        plan_gather_splits(p, n, target, fast ? kGMaxRows : kGvMaxRows);
         for (int i = 0; i < n; ++i) {
             const MatDesc& d = p.m[i];
-            int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup (<= kGMaxRows)
+            int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup
             for (int j = 0; j < 4; ++j)
                 if (d.rsplit[j]) rows = std::max(rows, d.rrpw[j]);
-            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64 + rows) * 4);
+            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64 + rows) * 4 * mc);
             base += d.g_count;
         }
     } else {
@@ -1514,6 +1770,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     if (phases & kPhaseGather) {
         if (fast)
             launch_gatherw(p, slots, base, lds_g, st);
+        else if (vec)
+            launch_gatherv(p, slots, base, lds_g, st);
         else if (MV == 1)
             gatherm_kernel<1><<<base, kThreads, lds_g, st>>>(p);
         else
@@ -1698,6 +1956,18 @@ CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* s, const int* row_dev, int ro
     decode_row_kernel<<<grid_for(s->C), kThreads, 0, static_cast<hipStream_t>(hip_stream)>>>(
         *s, row_dev, row_host, out);
     CSDR_LAUNCH_CHECK("hsdb decode_row");
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_hsdb_decode_rows(const csdr_hsdb* s, const int* rows_dev, int n, float* out,
+                                   void* hip_stream) {
+    if (!s || !rows_dev || !out || n <= 0 || n > 65535)
+        return set_error(CSDR_E_INVALID, "hsdb_decode_rows: bad argument");
+    if (s->tile_rows != 1)
+        return set_error(CSDR_E_FORMAT, "hsdb_decode_rows: needs 1-row tiles");
+    decode_row_kernel<<<dim3(grid_for(s->C), n), kThreads, 0,
+                        static_cast<hipStream_t>(hip_stream)>>>(*s, rows_dev, 0, out);
+    CSDR_LAUNCH_CHECK("hsdb decode_rows");
     return CSDR_OK;
 }
 

@@ -114,8 +114,9 @@ __host__ __device__ __forceinline__ int kperm64(int k) {
 // and 4, 8 or 16 slots, and CSDR_HSDB_MFMA is not 0.
 bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M);
 size_t mfma_workspace_bytes(int n, const csdr_hsdb* const* segs, int M);
+// token_major: X is M x C and Y is M x R (else C x M and R x M).
 int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
-                float* const* ys, const float* const* bias, int accumulate, void* workspace,
-                size_t workspace_bytes, hipStream_t st);
+                float* const* ys, const float* const* bias, int accumulate, int token_major,
+                void* workspace, size_t workspace_bytes, hipStream_t st);
 
 }  // namespace csdr

@@ -63,10 +63,13 @@ struct MDesc {
 struct MParams {
     MDesc m[kGroup];
     int G, M, Mpad, x_f16, accumulate, total_units;
+    int tm;  // token-major X (M x C) and Y (M x R)
     int m0;  // first column of this launch (the launch covers 16 * NT columns)
 };
 
-__device__ __forceinline__ float xget(const MParams& p, const MDesc& d, size_t i) {
+// X element (feature k, column m) in the call's layout.
+__device__ __forceinline__ float xget(const MParams& p, const MDesc& d, int k, int m) {
+    const size_t i = p.tm ? (size_t)m * (d.C_full + d.Ce) + k : (size_t)k * p.M + m;
     return p.x_f16 ? (float)static_cast<const _Float16*>(d.x)[i]
                    : static_cast<const float*>(d.x)[i];
 }
@@ -82,14 +85,15 @@ __global__ __launch_bounds__(kThreads) void mfma_init_kernel(MParams p) {
     const size_t stride = (size_t)gridDim.x * kThreads;
     for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < ny + ngr; t += stride) {
         if (t < ny) {
-            const int r = (int)(t / M), m = (int)(t - (size_t)r * M);
+            const int r = p.tm ? (int)(t % d.R) : (int)(t / M);
+            const int m = p.tm ? (int)(t / d.R) : (int)(t - (size_t)r * M);
             float v = p.accumulate ? d.y[t] : 0.0f;
             if (d.bias) v += d.bias[r];
             if (d.Ce > 0) {
                 const float* e = d.edge + (size_t)r * d.Ce;
                 float s = 0.0f;
                 for (int cc = 0; cc < d.Ce; ++cc)
-                    s = fmaf(e[cc], xget(p, d, (size_t)(d.C_full + cc) * M + m), s);
+                    s = fmaf(e[cc], xget(p, d, d.C_full + cc, m), s);
                 v += s;
             }
             d.y[t] = v;
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void mfma_init_kernel(MParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int k = b * 64 + csdr::kperm64(g * 8 + j);
-                const float xv = (m < M) ? xget(p, d, (size_t)k * M + m) : 0.0f;
+                const float xv = (m < M) ? xget(p, d, k, m) : 0.0f;
                 hi[j] = (_Float16)xv;
                 lo[j] = (_Float16)(xv - (float)hi[j]);
             }
@@ -190,7 +194,8 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
                 for (int i = 0; i < 4; ++i) {
                     const int r = rbase + i;
                     if (r < d.R && m < M)
-                        __hip_atomic_fetch_add(d.y + (size_t)r * M + m, acc[rt][nt][i],
+                        __hip_atomic_fetch_add(d.y + (p.tm ? (size_t)m * d.R + r : (size_t)r * M + m),
+                                               acc[rt][nt][i],
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
@@ -375,8 +380,8 @@ size_t mfma_workspace_bytes(int n, const csdr_hsdb* const* segs, int M) {
 }
 
 int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
-                float* const* ys, const float* const* bias, int accumulate, void* workspace,
-                size_t workspace_bytes, hipStream_t st) {
+                float* const* ys, const float* const* bias, int accumulate, int token_major,
+                void* workspace, size_t workspace_bytes, hipStream_t st) {
     const size_t need = mfma_workspace_bytes(n, segs, M);
     if (!workspace || workspace_bytes < need)
         return set_error(CSDR_E_WORKSPACE,
@@ -387,6 +392,7 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
     p.Mpad = padded_m(M);
     p.x_f16 = (x_dtype == CSDR_F16);
     p.accumulate = accumulate;
+    p.tm = token_major;
     char* ws = static_cast<char*>(workspace);
     size_t off = csdr::kWsHead;
     size_t max_elems = 0;

@@ -111,9 +111,10 @@ def _fptr(a):
 
 
 class Decoder:
-    """A device decoder over resident HSDB segments (batch 1, greedy / penalised argmax)."""
+    """A device decoder over resident HSDB segments (greedy / penalised argmax) decoding
+    `batch` sequences in lockstep; per-sequence arrays are sequence-major (batch, ...)."""
 
-    def __init__(self, weights: DecoderWeights):
+    def __init__(self, weights: DecoderWeights, batch: int = 1):
         import torch
 
         if not torch.cuda.is_available():
@@ -123,8 +124,9 @@ class Decoder:
         cfg = _lib.DecoderConfig(s.n_layers, s.hidden, s.n_heads, s.n_kv_heads, s.head_dim,
                                  s.ffn, s.vocab, s.max_ctx, s.rope_theta, s.rms_eps)
         h = C.c_void_p()
-        _lib.check(self._lib.csdr_decoder_create(C.byref(cfg), C.byref(h)))
+        _lib.check(self._lib.csdr_decoder_create_batched(C.byref(cfg), int(batch), C.byref(h)))
         self._h = h
+        self.batch = int(batch)
         self._segs = []
         self._keep = []
         try:
@@ -166,31 +168,37 @@ class Decoder:
 
     # ------------------------------------------------------------------ generation
     def prefill(self, prompt, temperature: float = 0.8, penalty: float = 1.5) -> None:
-        p = np.ascontiguousarray(prompt, np.int32)
-        _lib.check(self._lib.csdr_decoder_prefill(self._h, _fptr(p), p.size, temperature,
+        """prompt: n ids (batch 1) or (batch, n) ids."""
+        p = np.ascontiguousarray(prompt, np.int32).reshape(self.batch, -1)
+        _lib.check(self._lib.csdr_decoder_prefill(self._h, _fptr(p), p.shape[1], temperature,
                                                   penalty))
 
     def decode(self, n_steps: int, temperature: float = 0.8, penalty: float = 1.5) -> None:
         _lib.check(self._lib.csdr_decoder_decode(self._h, n_steps, temperature, penalty))
 
     def tokens(self, first: int, count: int) -> np.ndarray:
-        out = np.empty(count, np.int32)
+        """(count,) at batch 1, else (batch, count)."""
+        out = np.empty((self.batch, count), np.int32)
         _lib.check(self._lib.csdr_decoder_tokens(self._h, first, count, _fptr(out)))
-        return out
+        return out[0] if self.batch == 1 else out
 
     def logits(self) -> np.ndarray:
-        out = np.empty(self.spec.vocab, np.float32)
+        """(vocab,) at batch 1, else (batch, vocab)."""
+        out = np.empty((self.batch, self.spec.vocab), np.float32)
         _lib.check(self._lib.csdr_decoder_logits(self._h, _fptr(out)))
-        return out
+        return out[0] if self.batch == 1 else out
 
     def load_kv(self, layer: int, k, v, n: int) -> None:
-        """Import fp16 K/V of positions [0, n) (device torch tensors or host numpy arrays)."""
+        """Import fp16 K/V of positions [0, n), (batch, n, kv heads, head_dim) contiguous
+        (device torch tensors or host numpy arrays)."""
         kp = k.data_ptr() if hasattr(k, "data_ptr") else k.ctypes.data
         vp = v.data_ptr() if hasattr(v, "data_ptr") else v.ctypes.data
         _lib.check(self._lib.csdr_decoder_load_kv(self._h, layer, kp, vp, n))
 
-    def set_position(self, position: int, token: int) -> None:
-        _lib.check(self._lib.csdr_decoder_set_position(self._h, position, token))
+    def set_position(self, position: int, token) -> None:
+        """token: one id for every sequence, or batch ids."""
+        t = np.ascontiguousarray(np.broadcast_to(np.asarray(token, np.int32), (self.batch,)))
+        _lib.check(self._lib.csdr_decoder_set_position_batch(self._h, position, _fptr(t)))
 
     def position(self) -> int:
         return int(self._lib.csdr_decoder_position(self._h))
@@ -198,10 +206,12 @@ class Decoder:
     def generate(self, prompt, max_new_tokens: int, temperature: float = 0.8,
                  penalty: float = 1.5, eos_id: int = -1) -> np.ndarray:
         """generate_text's loop (api/cortex_sdk.cpp:1951-2054) on token ids."""
-        p = np.ascontiguousarray(prompt, np.int32)
+        p = np.ascontiguousarray(prompt, np.int32).reshape(self.batch, -1)
         n = max(1, int(max_new_tokens))
-        out = np.empty(n, np.int32)
-        ng = C.c_int(0)
-        _lib.check(self._lib.csdr_decoder_generate(self._h, _fptr(p), p.size, n, temperature,
-                                                   penalty, eos_id, _fptr(out), C.byref(ng)))
-        return out[:ng.value]
+        out = np.empty((self.batch, n), np.int32)
+        ng = (C.c_int * self.batch)()
+        _lib.check(self._lib.csdr_decoder_generate(self._h, _fptr(p), p.shape[1], n, temperature,
+                                                   penalty, eos_id, _fptr(out), ng))
+        if self.batch == 1:
+            return out[0, :ng[0]]
+        return [out[b, :ng[b]] for b in range(self.batch)]

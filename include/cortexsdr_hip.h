@@ -157,8 +157,13 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
 
 /* As csdr_hsdb_matmul_group with per-matrix bias (bias[i] = NULL or R_i floats added to every
  * column; bias itself may be NULL) and flags: CSDR_HSDB_ACCUMULATE makes Y += W.X (+ bias)
- * instead of Y = W.X (+ bias), which folds a residual add into the product. */
+ * instead of Y = W.X (+ bias), which folds a residual add into the product;
+ * CSDR_HSDB_TOKEN_MAJOR takes X as M x C and writes Y as M x R (token-major, the layout of
+ * Kernels::linear_forward, blas_kernels.cpp:264-293, and of the SDK's run_layer) instead of
+ * C x M and R x M (identical at M == 1). 2 <= M <= 8 (1-row tiles of 4, 8 or 16 slots) runs
+ * the streaming gather with M columns per code read (fp32 throughout). */
 #define CSDR_HSDB_ACCUMULATE 1
+#define CSDR_HSDB_TOKEN_MAJOR 2
 CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, const void* const* x,
                                        int x_dtype, int M, float* const* y,
                                        const float* const* bias, int flags, void* workspace,
@@ -190,6 +195,11 @@ CSDR_API int csdr_hsdb_matmul_group_xop(int n, const csdr_hsdb* const* segs,
  * unpacking of HierarchicalSDRStrategy.cpp:81-84. */
 CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* seg, const int* row_dev, int row_host,
                                   float* out, void* hip_stream);
+/* n rows at once: row i's index is rows_dev[i] (device int32), decoded into out + i * C
+ * (n x C fp32, token-major). Indices outside [0, R) leave their output row untouched. The
+ * batched form of the embedding lookup (build_token_embeddings, cortex_sdk.cpp:1480-1541). */
+CSDR_API int csdr_hsdb_decode_rows(const csdr_hsdb* seg, const int* rows_dev, int n, float* out,
+                                   void* hip_stream);
 
 /* Dense decode to device W (R x C fp32 row-major), bit-identical to the reference decode
  * order (stage-major slot accumulation with fused multiply-adds, then the edge strips). */
@@ -469,6 +479,12 @@ CSDR_API int csdr_hsda_load(const csdr_hsda* hsda, const char* name, void* hip_s
  * (cortex_sdk.cpp:1032-1206): output RMSNorm, sanitize_hidden_for_sampling (:959-976), lm_head
  * scores, select_best_from_logits with `temperature` and `penalty` for tokens generated so far
  * (the reference's generate_text uses 0.8 and 1.5). Not reentrant: one thread per decoder.
+ *
+ * Batch: csdr_decoder_create_batched decodes `batch` (1..16) sequences in lockstep, one
+ * position for all (the batch of an SDK engine, cortex_inference_engine_set_batch_size,
+ * cortex_sdk.cpp:1793-1802). Per-sequence data is sequence-major: prompts and tokens
+ * batch x count, logits batch x vocab, imported K/V batch x n positions; every projection
+ * is one product over the batch's columns.
  * ==================================================================== */
 typedef struct csdr_decoder csdr_decoder;
 typedef struct csdr_decoder_config {
@@ -478,6 +494,10 @@ typedef struct csdr_decoder_config {
 } csdr_decoder_config;
 
 CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** out);
+CSDR_API int csdr_decoder_create_batched(const csdr_decoder_config* cfg, int batch,
+                                         csdr_decoder** out);
+/* Sequences per step (-1 for NULL). */
+CSDR_API int csdr_decoder_batch(const csdr_decoder* dec);
 CSDR_API int csdr_decoder_free(csdr_decoder* dec);
 /* Block `layer`'s weights (transformer_blocks names attn_q/k/v/output, ffn_gate/up/down,
  * attn_norm, ffn_norm; cortex_sdk.cpp:1570-1660). Shapes: q,o H x H; k,v (Hkv*hd) x H;
@@ -494,30 +514,36 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* dec, int layer, const csdr_hsd
 CSDR_API int csdr_decoder_set_output(csdr_decoder* dec, const csdr_hsdb* lm_head,
                                      const float* final_norm, const csdr_hsdb* embedding);
 /* Runs the prompt from position 0 (resetting the cache and the generated-token set) and
- * selects the first new token (it lands at position n_prompt). */
+ * selects the first new token (it lands at position n_prompt). prompt: batch x n_prompt ids. */
 CSDR_API int csdr_decoder_prefill(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
                                   float temperature, float penalty);
 /* n_steps further tokens, one graph replay each; synchronises at the end. */
 CSDR_API int csdr_decoder_decode(csdr_decoder* dec, int n_steps, float temperature,
                                  float penalty);
-/* Host copy of the tokens at positions [first, first + count) (prompt, then generated). */
+/* Host copy of the tokens at positions [first, first + count) (prompt, then generated):
+ * batch x count. */
 CSDR_API int csdr_decoder_tokens(const csdr_decoder* dec, int first, int count, int32_t* out);
 /* generate_text's loop: prefill, then max_new_tokens - 1 decode steps; out_tokens receives
- * up to max_new_tokens ids, *n_generated stops after eos_id (eos_id < 0: none). */
+ * batch x max_new_tokens ids, n_generated[b] (batch ints) stops after eos_id (eos_id < 0:
+ * none). */
 CSDR_API int csdr_decoder_generate(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
                                    int max_new_tokens, float temperature, float penalty,
                                    int eos_id, int32_t* out_tokens, int* n_generated);
-/* Host copy of the last head step's lm_head scores (vocab floats, before temperature). */
+/* Host copy of the last head step's lm_head scores (batch x vocab floats, before
+ * temperature). */
 CSDR_API int csdr_decoder_logits(const csdr_decoder* dec, float* out);
 /* Number of positions processed so far (-1 for NULL). */
 CSDR_API int csdr_decoder_position(const csdr_decoder* dec);
 /* Import a precomputed context (a cached prompt prefix): fp16 K and V of positions [0, n) for
- * one layer, [position][kv head][head_dim], from host or device memory. */
+ * one layer, [sequence][position][kv head][head_dim], from host or device memory. */
 CSDR_API int csdr_decoder_load_kv(csdr_decoder* dec, int layer, const uint16_t* k,
                                   const uint16_t* v, int n);
 /* Continue from an imported context: positions [0, position) count as processed and `token`
- * is the token at `position`, consumed by the next csdr_decoder_decode step. */
+ * is the token at `position` of every sequence, consumed by the next csdr_decoder_decode step
+ * (the _batch form: tokens[b] for sequence b). */
 CSDR_API int csdr_decoder_set_position(csdr_decoder* dec, int position, int32_t token);
+CSDR_API int csdr_decoder_set_position_batch(csdr_decoder* dec, int position,
+                                             const int32_t* tokens);
 
 #ifdef __cplusplus
 }

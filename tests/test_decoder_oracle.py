@@ -101,3 +101,35 @@ def test_oracle_generate_forced_matches_free():
         rep[toks[:i]] = True
         ts = np.where(rep, ts - 1.5, ts)
         assert toks[i] == int(np.argmax(ts))
+
+
+@pytest.mark.parametrize("spec", [DecoderSpec(2, 256, 4, 2, 64, 96, 150, 32),
+                                  DecoderSpec(1, 256, 2, 2, 128, 128, 90, 32)])
+def test_cached_step_equals_whole_context_recompute(spec):
+    """oracle.decoder.step_cached (cached fp16 K/V context, the device decoder's form) against
+    the whole-context recompute of the same sequences: the scores after a context of n tokens
+    plus one more agree to the fp16 rounding of the context's K/V, per sequence of a batch of
+    sequences that differ; the returned K/V row of position n is the recompute's (fp16)."""
+    w = synthetic_weights(spec, n_atoms=64, nnz=4, seed=23, sigma=0.1, norm_jitter=0.1)
+    rng = np.random.default_rng(5)
+    B, n = 3, 9
+    seqs = rng.integers(0, spec.vocab, size=(B, n + 1)).astype(np.int32)
+    ctx = [odec.context_kv(w, seqs[b, :n]) for b in range(B)]
+    kv = []
+    for l in range(spec.n_layers):
+        k = np.stack([ctx[b][l][0] for b in range(B)])
+        v = np.stack([ctx[b][l][1] for b in range(B)])
+        kv.append((oracle.f32_to_f16(k).reshape(k.shape), oracle.f32_to_f16(v).reshape(v.shape)))
+    scores, rows = odec.step_cached(w, seqs[:, n], kv, n)
+    assert scores.shape == (B, spec.vocab)
+    for b in range(B):
+        full = odec.step_scores(w, seqs[b])
+        assert rel_l2(scores[b], full) < 1e-3, b
+        kn, vn = odec.context_kv(w, seqs[b])[0]
+        assert np.allclose(oracle.f16_to_f32(rows[0][0][b]).reshape(kn[n].shape), kn[n],
+                           rtol=2e-3, atol=2e-3)
+        assert np.allclose(oracle.f16_to_f32(rows[0][1][b]).reshape(vn[n].shape), vn[n],
+                           rtol=2e-3, atol=2e-3)
+    # the batch rows are independent: one sequence alone gives its row
+    s1, _ = odec.step_cached(w, seqs[1:2, n], [(k[1:2], v[1:2]) for k, v in kv], n)
+    assert np.array_equal(s1[0], scores[1])
