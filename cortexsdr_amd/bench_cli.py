@@ -302,6 +302,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--out", default=None)
     ap.add_argument("--cfg2-batches", default="1,16,64,256")
+    ap.add_argument("--cfg5-batches", default="1,8")
     ap.add_argument("--suite", default=None, help="run a bench suite JSON through the text CLI")
     args = ap.parse_args(argv)
     if args.suite:
@@ -347,8 +348,12 @@ def main(argv=None) -> int:
                     print(json.dumps(out[-1]), flush=True)
         res["results"]["gguf"] = out
     if "cfg5" in cfgs:
-        res["results"]["cfg5"] = bench_decoder_7b(torch)
-        print(json.dumps(res["results"]["cfg5"]), flush=True)
+        out = []
+        for B in (int(v) for v in args.cfg5_batches.split(",")):
+            out.append(bench_decoder_7b(torch, batch=B))
+            print(json.dumps(out[-1]), flush=True)
+            torch.cuda.empty_cache()
+        res["results"]["cfg5"] = out
     if "cfg4" in cfgs:
         res["results"]["cfg4"] = bench_decoder(torch)
         print(json.dumps(res["results"]["cfg4"]), flush=True)

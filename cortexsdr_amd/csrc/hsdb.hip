@@ -102,6 +102,7 @@ struct Params {
     // input transform applied while staging x (csdr_hsdb_matmul_group_xop)
     int xop;          // CSDR_XOP_*
     const float* nw;  // RMSNorm weights (C)
+    float* inv;       // M > 1: per (matrix, column) 1 / rms, [g * 16 + m] (workspace head)
     float eps;
     int nsplit, hd;   // attention combine: splits and head size of the partials in x
 };
@@ -602,6 +603,156 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     }
 }
 
+// ---- RMSNorm statistics at M > 1: p.inv[g * 16 + m] = 1 / sqrt(mean_k x[k][m]^2 + eps) for
+// matrix g = blockIdx.y, column m = blockIdx.x (one workgroup per column, once per call, so
+// the dx workgroups read M values instead of all C x M inputs each).
+__global__ __launch_bounds__(kThreads) void rms_inv_kernel(Params p) {
+    const MatDesc& d = p.m[blockIdx.y];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int C = d.C_full + d.Ce;
+    const float* xf = static_cast<const float*>(d.x);
+    __shared__ float red[kThreads / 64];
+    float ss = 0.0f;
+    for (int k0 = 0; k0 < C; k0 += kThreads * kStageBatch) {
+        float v[kStageBatch];
+#pragma unroll
+        for (int j = 0; j < kStageBatch; ++j) v[j] = xf[xi(p, d, min(k0 + j * kThreads + tid, C - 1), m)];
+#pragma unroll
+        for (int j = 0; j < kStageBatch; ++j)
+            if (k0 + j * kThreads + tid < C) ss = fmaf(v[j], v[j], ss);
+    }
+    ss = wg_sum<kThreads>(ss, red);
+    if (tid == 0) p.inv[blockIdx.y * 16 + m] = 1.0f / sqrtf(ss / (float)C + p.eps);
+}
+
+// ---- kernel 1, 2 <= M <= 16 and 64-long blocks: P[b][a][m] = D[a] . X[64b : 64b+64, m]
+// One thread per atom with the atom's 64 values in registers; a workgroup covers 256 atoms
+// and PB block columns, whose X (with the call's x op applied) is staged in LDS as
+// [block][t][MC] (columns past M zero) and read as broadcasts, so each thread runs 64 * MC
+// fused multiply-adds per block with no cross-lane reduction and writes its M values of P
+// contiguously. Y is initialised as in dx_kernel. RMSNorm reads the column statistics of
+// rms_inv_kernel.
+constexpr int kDxmAtoms = kThreads;
+
+template <int XOP, int MC>
+__global__ __launch_bounds__(kThreads) void dxm_kernel(Params p) {
+    extern __shared__ float smem[];
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int wg = blockIdx.x;
+    int g = 0;
+    while (g + 1 < p.G && wg >= p.m[g + 1].dx_base) ++g;
+    const MatDesc& d = p.m[g];
+    const int u = wg - d.dx_base;
+    const int tid = threadIdx.x;
+    const int M = p.M;
+    const int C = d.C_full + d.Ce;
+    {
+        const size_t ytot = (size_t)d.R * M;
+        const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
+        const size_t ye = min(ytot, (size_t)(u + 1) * yper);
+        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
+            const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
+            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        }
+    }
+    const int na = (d.K + kDxmAtoms - 1) / kDxmAtoms;
+    const int ag = u % na, bg = u / na;
+    const int a = ag * kDxmAtoms + tid;
+    const bool live = a < d.K;
+    const int b0 = bg * d.PB;
+    const int nb = min(d.PB, d.NB - b0);
+    // the atom's row, 16 independent 16-byte loads in flight
+    f4 dr[16];
+    {
+        const f4* src = reinterpret_cast<const f4*>(d.dict + (size_t)min(a, d.K - 1) * 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dr[i] = src[i];
+    }
+    __shared__ float inv[MC];
+    if constexpr (XOP == CSDR_XOP_RMSNORM) {
+        // per-column 1 / rms, computed once per call by rms_inv_kernel
+        if (tid < MC) inv[tid] = tid < M ? p.inv[g * 16 + tid] : 0.0f;
+        __syncthreads();
+    }
+    // X of this workgroup's block columns -> LDS [bb][t][MC], the x op applied
+    float* xs = smem;
+    {
+        const int n = nb * 64 * MC;
+        const int f0 = b0 * 64;
+        for (int i0 = 0; i0 < n; i0 += kThreads * kStageBatch) {
+            float v[kStageBatch], w2[kStageBatch];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = min(i0 + j * kThreads + tid, n - 1);
+                const int f = f0 + i / MC, m = min(i % MC, M - 1);
+                const size_t xo = xi(p, d, f, m);
+                v[j] = xload(d.x, p.x_f16, xo);
+                if constexpr (XOP == CSDR_XOP_RMSNORM) w2[j] = p.nw[f];
+                if constexpr (XOP == CSDR_XOP_SILU_MUL) w2[j] = static_cast<const float*>(d.x2)[xo];
+            }
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = min(i0 + j * kThreads + tid, n - 1);
+                const int m = i % MC;
+                float x = v[j];
+                if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * inv[min(m, MC - 1)] * w2[j];
+                if constexpr (XOP == CSDR_XOP_SILU_MUL) x = (x * (1.0f / (1.0f + expf(-x)))) * w2[j];
+                xs[i] = m < M ? x : 0.0f;
+            }
+        }
+        if (u == 0 && XOP != CSDR_XOP_NONE && d.xe) {
+            // the transformed edge-strip inputs, [cc][m]
+            for (int t = tid; t < d.Ce * M; t += kThreads) {
+                const int cc = t / M, m = t - cc * M, f = d.C_full + cc;
+                const size_t xo = xi(p, d, f, m);
+                float x = xload(d.x, p.x_f16, xo);
+                if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * inv[m] * p.nw[f];
+                if constexpr (XOP == CSDR_XOP_SILU_MUL)
+                    x = (x * (1.0f / (1.0f + expf(-x)))) * static_cast<const float*>(d.x2)[xo];
+                d.xe[t] = x;
+            }
+        }
+    }
+    __syncthreads();
+    float* Pa = d.P + ((size_t)b0 * d.K + a) * M;
+    const size_t pstride = (size_t)d.K * M;
+    for (int bb = 0; bb < nb; ++bb) {
+        float acc[MC];
+#pragma unroll
+        for (int mm = 0; mm < MC; ++mm) acc[mm] = 0.0f;
+        const float* xb = xs + bb * 64 * MC;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dv = dr[i][e];
+                const float* xt = xb + (4 * i + e) * MC;
+#pragma unroll
+                for (int q = 0; q < MC; q += 4) {
+                    const f4 xv = *reinterpret_cast<const f4*>(xt + q);
+                    acc[q] = fmaf(dv, xv.x, acc[q]);
+                    acc[q + 1] = fmaf(dv, xv.y, acc[q + 1]);
+                    acc[q + 2] = fmaf(dv, xv.z, acc[q + 2]);
+                    acc[q + 3] = fmaf(dv, xv.w, acc[q + 3]);
+                }
+            }
+            // one group of four x rows at a time: the accumulators are pinned here (an empty
+            // asm that reads and writes them emits no instruction), so this group's
+            // multiply-adds complete before the next group's loads; otherwise every group's
+            // LDS loads are hoisted above the multiply-adds, 16 * MC registers on top of the
+            // atom's 64
+#pragma unroll
+            for (int mm = 0; mm < MC; ++mm) asm volatile("" : "+v"(acc[mm]));
+        }
+        if (live) {
+            float* out = Pa + bb * pstride;
+#pragma unroll
+            for (int mm = 0; mm < MC; ++mm)
+                if (mm < M) out[mm] = acc[mm];
+        }
+    }
+}
+
 // Finds this gather workgroup's matrix and (chunk, split); false for padding slots.
 // Workgroups of one chunk are numbered to share an XCD (dispatch is round-robin over the
 // 8 XCDs), so that chunk's P slice is fetched into one L2 only.
@@ -842,7 +993,97 @@ void gatherw_kernel(Params p) {
 // from HBM once for all M columns. Row totals (MC per row) wait in LDS and go into Y with one
 // device-scope atomic per (row, column) after the stream. WPE: waves per SIMD the register
 // budget is pinned for (1 workgroup per CU for the 128 KiB slice at MC = 8, 2 below).
-constexpr int kGvMaxRows = 512;  // rows per workgroup (row totals in LDS: 16 KiB at MC = 8)
+constexpr int kGvMinRows = 256;  // rows per workgroup the LDS share must hold, at least
+
+// The 2 <= M <= 8 gather's stream for one chunk width: PPR lanes per row (each lane a fixed
+// tile and slot quarter), `buf` holding the first DEPTH pieces already issued. Lanes past the
+// wave's valid pieces read zeros (coefficient 0), and a row's lanes are all valid or all past
+// the end, so no selects are needed before the row reductions.
+template <int SLOTS, int MC, int DEPTH, int PPR, typename PieceFn>
+__device__ __forceinline__ void gatherv_stream(const Params& p, const MatDesc& d,
+                                               const float* Ps, float* rowt, u32x4* buf,
+                                               PieceFn piece, int nk, int wfirst, int npieces) {
+    (void)p;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int PPB = SLOTS / 4;
+    constexpr int kStep = 64;
+    constexpr int lg_ppr = PPR == 1 ? 0 : PPR == 2 ? 1 : PPR == 4 ? 2 : PPR == 8 ? 3
+                         : PPR == 16 ? 4 : PPR == 32 ? 5 : 6;
+    const int lane = threadIdx.x & 63;
+    const int pl = lane & (PPR - 1);
+    const int bb = pl / PPB, h = pl - bb * PPB;
+    const float* Pb = Ps + (size_t)bb * d.K * MC;
+    float gm[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        gm[e] = sgam_at(d, e);
+#pragma unroll
+        for (int hh = 1; hh < PPB; ++hh)
+            if (h == hh) gm[e] = sgam_at(d, hh * 4 + e);
+    }
+    const bool gu = d.gunif != 0;
+    const float g0 = d.sgam[0];
+    if (gu) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gm[e] = 1.0f;
+    }
+    const bool head = (pl == 0);
+    const int q0 = wfirst + lane;
+    auto consume = [&](const u32x4& w, int k) {
+        const int qp = q0 + k * kStep;
+        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+        float acc[MC];
+#pragma unroll
+        for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float cf = gm[e] * csdr::h2f(w4[e] >> 16);
+            const float* pv = Pb + (size_t)(uint16_t)w4[e] * MC;
+            if constexpr (MC >= 4) {
+#pragma unroll
+                for (int m4 = 0; m4 < MC; m4 += 4) {
+                    const f4 v = *reinterpret_cast<const f4*>(pv + m4);
+                    acc[m4] = fmaf(cf, v.x, acc[m4]);
+                    acc[m4 + 1] = fmaf(cf, v.y, acc[m4 + 1]);
+                    acc[m4 + 2] = fmaf(cf, v.z, acc[m4 + 2]);
+                    acc[m4 + 3] = fmaf(cf, v.w, acc[m4 + 3]);
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < MC; ++m) acc[m] = fmaf(cf, pv[m], acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+            float a = acc[m];
+            if constexpr (PPR > 1) a += dpp_move<0xB1>(a);
+            if constexpr (PPR > 2) a += dpp_move<0x4E>(a);
+            if constexpr (PPR > 4) a += dpp_move<0x141>(a);
+            if constexpr (PPR > 8) a += dpp_move<0x140>(a);
+            if constexpr (PPR > 16) a += __shfl_xor(a, 16, 64);
+            if constexpr (PPR > 32) a += __shfl_xor(a, 32, 64);
+            acc[m] = a;
+        }
+        if (head && qp < npieces) {
+            float* rt = rowt + (size_t)(qp >> lg_ppr) * MC;
+#pragma unroll
+            for (int m = 0; m < MC; ++m) rt[m] = gu ? acc[m] * g0 : acc[m];
+        }
+    };
+    constexpr int NBUF = DEPTH + 1;
+    int k0 = 0;
+    for (; k0 + NBUF <= nk; k0 += NBUF) {
+#pragma unroll
+        for (int jj = 0; jj < NBUF; ++jj) {
+            const u32x4 w = buf[jj];
+            buf[(jj + DEPTH) % NBUF] = piece(k0 + jj + DEPTH);
+            consume(w, k0 + jj);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NBUF - 1; ++jj)
+        if (k0 + jj < nk) consume(buf[jj], k0 + jj);
+}
 
 template <int SLOTS, int MC, int DEPTH, int WPE>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
@@ -903,7 +1144,21 @@ void gatherv_kernel(Params p) {
     u32x4 buf[NBUF];
 #pragma unroll
     for (int k = 0; k < DEPTH; ++k) buf[k] = piece(k);
-    {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    if (M == MC && (d.K * MC) % 4 == 0) {
+        // P slice: global [block][atom][M] -> LDS, a straight copy of 16-byte pieces (at most 8
+        // per thread: one round trip)
+        const f4* Pg = reinterpret_cast<const f4*>(d.P + (size_t)b0 * d.K * M);
+        f4* Pl = reinterpret_cast<f4*>(Ps);
+        const int n4 = nbc * d.K * MC / 4;
+        for (int i0 = 0; i0 < n4; i0 += kGThreads * 8) {
+            f4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = Pg[min(i0 + j * kGThreads + tid, n4 - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Pl[min(i0 + j * kGThreads + tid, n4 - 1)] = v[j];
+        }
+    } else {
         // P slice: global [block][atom][M] -> LDS [block][atom][MC], kStageBatch loads in flight
         const float* Pg = d.P + (size_t)b0 * d.K * M;
         const int n = nbc * d.K * MC;
@@ -922,77 +1177,17 @@ void gatherv_kernel(Params p) {
     }
     __syncthreads();
 
-    const int pl = lane & (ppr - 1);
-    const int lg_ppr = __builtin_ctz((unsigned)ppr);
-    const int bb = pl / PPB, h = pl - bb * PPB;
-    const float* Pb = Ps + (size_t)bb * d.K * MC;
-    float gm[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        gm[e] = sgam_at(d, e);
-#pragma unroll
-        for (int hh = 1; hh < PPB; ++hh)
-            if (h == hh) gm[e] = sgam_at(d, hh * 4 + e);
+    // the stream, specialised on the lanes per row (a power of two fixed per chunk width), so
+    // each column's row reduction is a straight DPP / shuffle sequence
+    switch (ppr) {
+        case 1: gatherv_stream<SLOTS, MC, DEPTH, 1>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        case 2: gatherv_stream<SLOTS, MC, DEPTH, 2>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        case 4: gatherv_stream<SLOTS, MC, DEPTH, 4>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        case 8: gatherv_stream<SLOTS, MC, DEPTH, 8>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        case 16: gatherv_stream<SLOTS, MC, DEPTH, 16>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        case 32: gatherv_stream<SLOTS, MC, DEPTH, 32>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+        default: gatherv_stream<SLOTS, MC, DEPTH, 64>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
     }
-    const bool gu = d.gunif != 0;
-    const float g0 = d.sgam[0];
-    const bool head = (pl == 0);
-    const int q0 = wfirst + lane;
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    auto consume = [&](const u32x4& w, int k) {
-        const int qp = q0 + k * kStep;
-        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
-        float acc[MC];
-#pragma unroll
-        for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float cf = gu ? csdr::h2f(w4[e] >> 16) : gm[e] * csdr::h2f(w4[e] >> 16);
-            const float* pv = Pb + (size_t)(uint16_t)w4[e] * MC;
-#pragma unroll
-            for (int m4 = 0; m4 < MC; m4 += 4) {
-                if constexpr (MC >= 4) {
-                    const f4 v = *reinterpret_cast<const f4*>(pv + m4);
-                    acc[m4] = fmaf(cf, v.x, acc[m4]);
-                    acc[m4 + 1] = fmaf(cf, v.y, acc[m4 + 1]);
-                    acc[m4 + 2] = fmaf(cf, v.z, acc[m4 + 2]);
-                    acc[m4 + 3] = fmaf(cf, v.w, acc[m4 + 3]);
-                } else {
-#pragma unroll
-                    for (int m = 0; m < MC; ++m) acc[m] = fmaf(cf, pv[m], acc[m]);
-                }
-            }
-        }
-        const bool live = qp < npieces;
-#pragma unroll
-        for (int m = 0; m < MC; ++m) {
-            float a = live ? acc[m] : 0.0f;
-            if (ppr > 1) a += dpp_move<0xB1>(a);
-            if (ppr > 2) a += dpp_move<0x4E>(a);
-            if (ppr > 4) a += dpp_move<0x141>(a);
-            if (ppr > 8) a += dpp_move<0x140>(a);
-            if (ppr > 16) a += __shfl_xor(a, 16, 64);
-            if (ppr > 32) a += __shfl_xor(a, 32, 64);
-            acc[m] = a;
-        }
-        if (head && live) {
-            float* rt = rowt + (size_t)(qp >> lg_ppr) * MC;
-#pragma unroll
-            for (int m = 0; m < MC; ++m) rt[m] = gu ? acc[m] * g0 : acc[m];
-        }
-    };
-    int k0 = 0;
-    for (; k0 + NBUF <= nk; k0 += NBUF) {
-#pragma unroll
-        for (int jj = 0; jj < NBUF; ++jj) {
-            const u32x4 w = buf[jj];
-            buf[(jj + DEPTH) % NBUF] = piece(k0 + jj + DEPTH);
-            consume(w, k0 + jj);
-        }
-    }
-#pragma unroll
-    for (int jj = 0; jj < NBUF - 1; ++jj)
-        if (k0 + jj < nk) consume(buf[jj], k0 + jj);
     // the top-right strip's inputs of the last chunk: [cc][m] (x-op transformed when given)
     if (edge) {
         for (int t = tid; t < d.Ce * MC; t += kGThreads) {
@@ -1616,9 +1811,10 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     bool vec = M >= 2 && M <= kMaxVecM;
     for (int i = 0; i < n && vec; ++i) {
         const csdr_hsdb* s = segs[i];
-        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMaxRows) * 4 * gatherv_mc(M);
+        const int mc = gatherv_mc(M);
+        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMinRows) * 4 * mc;
         vec = s->tile_rows == 1 && s->NB > 0 && (s->slots == 4 || s->slots == 8 || s->slots == 16) &&
-              s->slots == segs[0]->slots && lds <= 160 * 1024;
+              s->slots == segs[0]->slots && lds <= (size_t)160 * 1024 / gatherv_wgs_per_cu(mc);
     }
     if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE && !vec &&
         csdr::mfma_eligible(n, segs, M))
@@ -1647,12 +1843,17 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     p.hd = xa.hd;
     char* ws = static_cast<char*>(workspace);
     size_t off = csdr::kWsHead;
+    p.inv = reinterpret_cast<float*>(ws);
     // the register-resident M == 1 gather needs every matrix at 4, 8 or 16 slots (16-byte
     // pieces) and the same count across the group; anything else takes the generic gather
     int slots = -1;
     bool fast = (M == 1);
     int ndx = 0;
     size_t lds_dx = 0, lds_g = 0;
+    // 2 <= M <= 16 with 64-long blocks everywhere: the thread-per-atom dx kernel
+    bool dxm = M >= 2 && M <= kMaxXopM;
+    for (int i = 0; i < n; ++i) dxm = dxm && segs[i] && segs[i]->tile_cols == 64;
+    const int dxm_mc = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
         if (!s || !xs[i] || !ys[i]) return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
@@ -1696,7 +1897,13 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.Ce = (int)s->Ce;
         d.C_full = (int)s->C_full;
         d.PB = producer_blocks(M);
-        if (d.blen == 64) {
+        if (dxm) {
+            // about 256 workgroups per matrix: block columns per workgroup from the atom tiles
+            const int na = (d.K + kDxmAtoms - 1) / kDxmAtoms;
+            d.PB = std::max(1, std::min(8, d.NB * na / 256));
+            d.dx_count = na * ((d.NB + d.PB - 1) / d.PB);
+            lds_dx = std::max(lds_dx, (size_t)d.PB * 64 * dxm_mc * 4);
+        } else if (d.blen == 64) {
             d.dx_count = ((d.K + 15) / 16) * ((d.NB + d.PB - 1) / d.PB);
             size_t extra = 0;
             if (xa.xop == CSDR_XOP_ATTN)  // split weights of the heads a workgroup covers
@@ -1722,12 +1929,22 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         // columns allows; fewer for small groups: at least kGMinWgBytes of codes per workgroup
         // (each one stages a P slice first)
         const int mc = fast ? 1 : gatherv_mc(M);
-        long long target = (long long)ncu * (fast ? kGWgsPerCu : gatherv_wgs_per_cu(mc));
+        const int wpc = fast ? kGWgsPerCu : gatherv_wgs_per_cu(mc);
+        long long target = (long long)ncu * wpc;
+        // rows per workgroup: M == 1 kGMaxRows; else what the LDS share left by the widest P
+        // slice holds (row totals of mc floats)
+        int max_rows = kGMaxRows;
+        if (!fast) {
+            size_t pk = 0;
+            for (int i = 0; i < n; ++i) pk = std::max(pk, (size_t)segs[i]->NBc * segs[i]->K);
+            const size_t share = (size_t)160 * 1024 / wpc;
+            max_rows = (int)std::min<size_t>(kGMaxRows, (share - (pk + 64) * mc * 4) / (mc * 4));
+        }
         long long code_bytes = 0;
         for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
         const long long min_bytes = kGMinWgBytes;
         target = std::max(1LL, std::min(target, code_bytes / std::max(1LL, min_bytes)));
-        plan_gather_splits(p, n, target, fast ? kGMaxRows : kGvMaxRows);
+        plan_gather_splits(p, n, target, max_rows);
         for (int i = 0; i < n; ++i) {
             const MatDesc& d = p.m[i];
             int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup
@@ -1750,7 +1967,27 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     if (lds_g > 160 * 1024 || lds_dx > 160 * 1024)
         return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: dictionary too large for LDS");
-    if (phases & kPhaseDx) {
+    if ((phases & kPhaseDx) && dxm) {
+        if (p.xop == CSDR_XOP_RMSNORM) {
+            rms_inv_kernel<<<dim3(M, n), kThreads, 0, st>>>(p);
+            CSDR_LAUNCH_CHECK("hsdb rms");
+        }
+        auto go = [&](auto kern) { kern<<<ndx, kThreads, lds_dx, st>>>(p); };
+        const int key = p.xop * 100 + dxm_mc;
+        switch (key) {
+            case CSDR_XOP_NONE * 100 + 4: go(dxm_kernel<CSDR_XOP_NONE, 4>); break;
+            case CSDR_XOP_NONE * 100 + 8: go(dxm_kernel<CSDR_XOP_NONE, 8>); break;
+            case CSDR_XOP_NONE * 100 + 16: go(dxm_kernel<CSDR_XOP_NONE, 16>); break;
+            case CSDR_XOP_RMSNORM * 100 + 4: go(dxm_kernel<CSDR_XOP_RMSNORM, 4>); break;
+            case CSDR_XOP_RMSNORM * 100 + 8: go(dxm_kernel<CSDR_XOP_RMSNORM, 8>); break;
+            case CSDR_XOP_RMSNORM * 100 + 16: go(dxm_kernel<CSDR_XOP_RMSNORM, 16>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 4: go(dxm_kernel<CSDR_XOP_SILU_MUL, 4>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 8: go(dxm_kernel<CSDR_XOP_SILU_MUL, 8>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 16: go(dxm_kernel<CSDR_XOP_SILU_MUL, 16>); break;
+            default: return set_error(CSDR_E_INVALID, "hsdb_matmul: x op not available at M > 1");
+        }
+        CSDR_LAUNCH_CHECK("hsdb dx");
+    } else if (phases & kPhaseDx) {
         switch (p.xop) {
             case CSDR_XOP_RMSNORM:
                 dx_kernel<CSDR_XOP_RMSNORM><<<ndx, kThreads, lds_dx, st>>>(p);

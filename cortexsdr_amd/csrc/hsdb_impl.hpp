@@ -98,9 +98,9 @@ __host__ __device__ __forceinline__ size_t tile_word_offset(uint32_t r, uint32_t
     return ((size_t)b0 * R + (size_t)r * nbc + (b - b0)) * slots;
 }
 
-// Every product workspace starts with kWsHead reserved bytes; the data (P, transposed X)
-// follows.
-constexpr size_t kWsHead = 256;
+// Every product workspace starts with kWsHead bytes (the RMSNorm x op's per-column 1 / rms at
+// M > 1: 16 floats per matrix of a group of up to 8); the data (P, transposed X) follows.
+constexpr size_t kWsHead = 1024;
 
 // Position of k (0..63) inside a 64-long block stored in the matrix-core k order: with
 // k = 16s + 4q + i (s, q, i in 0..3) it sits at 16q + 4s + i, so the 16 values a lane

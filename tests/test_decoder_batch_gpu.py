@@ -104,14 +104,15 @@ def test_batched_generate_matches_oracle_and_batch_one(gpu):
             assert np.array_equal(again[b], toks[b])
     finally:
         dec.close()
-    # every sequence alone at batch 1 chooses the same tokens with the same scores (to the
-    # different summation order of the one- and multi-column products)
+    # every sequence alone at batch 1 chooses the same tokens with the same scores, to the
+    # different summation order of the one- and multi-column products (a last-bit difference
+    # can round a cached K/V value to the neighbouring fp16 value: 2e-4)
     one = Decoder(w, batch=1)
     try:
         for b in range(B):
             one.prefill(prompts[b], 0.8, 1.5)
             s0 = one.logits()
-            assert rel_l2(s0, scores[0][b]) < 1e-5
+            assert rel_l2(s0, scores[0][b]) < 2e-4
             one.decode(n_new - 1, 0.8, 1.5)
             assert np.array_equal(one.tokens(n_prompt, n_new), toks[b])
     finally:
