@@ -11,16 +11,28 @@ accumulation). value = algorithmic bytes of a step / step time, where algorithmi
 Inputs are resident in HBM before timing. Each step uses a different copy of the coded
 matrices (a rotation over > 3 x 256 MiB) so the Infinity Cache cannot serve them.
 
+Timing: the K steps are captured once into a HIP graph; the timed region is one replay
+(exactly K steps, bracketed by synchronize) and gives `value` / `ms_per_step`; `replays`
+adds the median, min and max per-step time over 100 further replays of the same graph,
+each bracketed by HIP events.
+
 The JSON line carries:
-  roofline      the dominant kernel (the gather launch over both matrices), timed with
-                HIP events around K back-to-back gather launches on its stream
+  roofline      the dominant kernel (the gather launch over both matrices): median over 100
+                replays of a graph of K back-to-back gather launches, HIP events on the
+                launch stream; `traffic` = HBM bytes per launch from the committed rocprofv3
+                --pmc measurement of the current kernel (profiles/hsdb_gather_cfg2_traffic.json)
   cpu_baseline  the CPU restatement of the reference algorithm (oracle/, OpenMP) on a
-                bounded sample of the same workload, on this host's cores
+                bounded sample of the same workload, on this host's cores, with the CPU
+                model, its physical cores and a single-thread time (the reference's fused
+                path is single-threaded)
   decode        the metric's second half, configs[3]: Qwen2-0.5B-shaped decoder (24 layers,
                 hidden 896, 14/2 heads of 64, FFN 4864, vocab 151936, every linear
                 HSDB-coded against one shared 1024 x 64 dictionary), 512-token prompt of
                 uniform random ids, then greedy decode of 128 tokens; tokens/s of the decode
                 phase next to a KV-cached CPU decode step of the same model (oracle/)
+  decode_7b     configs[4]: the Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads
+                of 128, SwiGLU 11008, vocab 32000, HSDB-coded linears) over an fp16 KV
+                context of 4096 positions, batch 1 and 8, weights and KV resident
   encode        the compress side: GPU matching pursuit (rows/s, TFLOP/s against the fp32
                 vector peak) and compress wall time on Qwen2-0.5B-shaped attention / MLP
                 matrices, next to the reference's own compress (oracle/_ref)
@@ -39,12 +51,54 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
 
-# HBM bytes per gather launch (cfg2, M = 1, both matrices) from two rocprofv3 --pmc runs of
-# this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
-# counter reads for a plain 256 MiB device copy in the same run (--calibrate-copy: FETCH_SIZE
-# reads 0.5x the bytes copied, WRITE_SIZE 1.0x): 23946.6 KiB / 0.5 + 1455.9 KiB / 1.0.
-# Summary and commands: profiles/hsdb_gather_cfg2_hbm_traffic.md. Update with the kernel.
-GATHER_TRAFFIC_BYTES = int((23946.6 / 0.5 + 1455.9 / 1.0) * 1024)
+# HBM bytes per gather launch (cfg2, M = 1, both matrices): two rocprofv3 --pmc runs of this
+# script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same counter
+# reads for a plain 256 MiB device copy in the same run (--calibrate-copy); the measured
+# values, the scale factors and the commands are in this JSON file, written from those runs.
+TRAFFIC_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "hsdb_gather_cfg2_traffic.json")
+
+
+def gather_traffic():
+    """(bytes per launch, kernel name) from the committed PMC measurement, or (None, None)."""
+    try:
+        with open(TRAFFIC_JSON) as f:
+            t = json.load(f)
+        return int(t["traffic_bytes"]), t.get("kernel")
+    except (OSError, ValueError, KeyError):
+        return None, None
+
+
+def cpu_info():
+    """CPU model name, physical cores (distinct (package, core) pairs) and logical CPUs."""
+    model, pairs, logical = None, set(), 0
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    logical += 1
+                elif k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    pairs.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            pairs.add((phys, core))
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "physical_cores": len(pairs) or None,
+            "logical_cpus": logical or os.cpu_count(), "usable_cpus": usable}
 
 
 def parse():
@@ -58,6 +112,9 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode leg")
     ap.add_argument("--decode-cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-encode", action="store_true", help="skip the HSDR encoder leg")
+    ap.add_argument("--no-7b", action="store_true", help="skip the config-5 decode-step leg")
+    ap.add_argument("--replays", type=int, default=100,
+                    help="graph replays for the median / min / max statistics")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy 5 times (the reference dispatch "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -83,22 +140,29 @@ def alg_bytes(w, M=1):
     return dict(op=codes + dict_b + xb + yb, gather=codes + P + yb, codes=codes)
 
 
-def cpu_baseline(streams, xs, seconds):
+def cpu_baseline(streams, xs, seconds, threads=None):
+    """Seconds per step of the CPU restatement, `threads` OpenMP threads (default: the
+    OMP_NUM_THREADS / CPU count the run was given)."""
     import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    xs32 = [x.astype(np.float32) for x in xs]
-    for s, x in zip(streams, xs32):  # warm-up
-        oracle.hsdb_matmul(s, x)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        for s, x in zip(streams, xs32):
+    if threads is None:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    prev = oracle.set_threads(threads)
+    try:
+        xs32 = [x.astype(np.float32) for x in xs]
+        for s, x in zip(streams, xs32):  # warm-up
             oracle.hsdb_matmul(s, x)
-        n += 1
-        if time.perf_counter() - t0 >= seconds and n >= 2:
-            break
-    dt = (time.perf_counter() - t0) / n
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            for s, x in zip(streams, xs32):
+                oracle.hsdb_matmul(s, x)
+            n += 1
+            if time.perf_counter() - t0 >= seconds and n >= 2:
+                break
+        dt = (time.perf_counter() - t0) / n
+    finally:
+        oracle.set_threads(prev)
     return dt, n, threads
 
 
@@ -184,6 +248,22 @@ def decode_leg(args):
             "value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": (f"{n} KV-cached decode steps at context {n_prompt + n_new // 2} through "
                        f"oracle/ (orc_hsdb_matmul OpenMP linears), {dt * 1e3:.0f} ms/token")}
+    return out
+
+
+def decode_7b_leg(torch):
+    """ms per decode step of the Llama-7B-shaped model at context 4096, batch 1 and
+    8 (bench_cli.bench_decoder_7b: HIP-graph steps, weights and the N(0,1) fp16 KV context
+    resident); HBM fraction from codes + KV bytes per step."""
+    from cortexsdr_amd import bench_cli
+
+    out = []
+    for B in (1, 8):
+        r = bench_cli.bench_decoder_7b(torch, batch=B)
+        out.append({k: r[k] for k in ("batch", "context", "ms_per_step", "tokens_per_s",
+                                      "code_GB_per_step", "kv_GB_per_step", "alg_GBps",
+                                      "hbm_frac")})
+        torch.cuda.empty_cache()
     return out
 
 
@@ -333,25 +413,34 @@ def main():
     ms_total = start.elapsed_time(end)
     ms_step = ms_total / args.steps
 
+    def replay_stats(g, per):
+        """Per-unit ms over args.replays replays of graph g (per units each), HIP events on
+        the launch stream around every replay: (median, min, max)."""
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.replays)]
+        torch.cuda.synchronize()
+        for e0, e1 in ev:
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        t = sorted(e0.elapsed_time(e1) / per for e0, e1 in ev)
+        return t[len(t) // 2], t[0], t[-1]
+
+    rep_med, rep_min, rep_max = replay_stats(graph, args.steps)
+
     # Dominant-kernel duration: the gather launch (both matrices), K launches back to back
-    # over the rotating copies between two HIP events on the launch stream (after one dx;
-    # repeated gathers only accumulate into y). Large GEMMs are queued first so the host
-    # runs ahead and the events bracket execution, not host launch gaps.
-    a = torch.randn(8192, 8192, device="cuda")
-    g0 = torch.cuda.Event(enable_timing=True)
-    g1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    for _ in range(3):
-        a = a @ a.T * 1e-4
+    # over the rotating copies captured in one graph (after one dx; repeated gathers only
+    # accumulate into y), the median over the replays.
     _lib.check(lib.csdr_hsdb_dx_group(n, hs[0], xp, xtype, 1, yp, ws.data_ptr(), ws.numel(), sp))
-    g0.record(stream)
-    for it in range(args.steps):
-        _lib.check(lib.csdr_hsdb_gather_group(n, hs[it % copies], xp, xtype, 1, yp,
-                                              ws.data_ptr(), ws.numel(), sp))
-    g1.record(stream)
-    torch.cuda.synchronize()
-    del a
-    kern_ms = g0.elapsed_time(g1) / args.steps
+    ggraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ggraph):
+        sp_cap = int(torch.cuda.current_stream().cuda_stream)
+        for it in range(args.steps):
+            _lib.check(lib.csdr_hsdb_gather_group(n, hs[it % copies], xp, xtype, 1, yp,
+                                                  ws.data_ptr(), ws.numel(), sp_cap))
+    ggraph.replay()
+    kern_ms, kern_min, kern_max = replay_stats(ggraph, args.steps)
 
     op_bytes = sum(alg_bytes(w)["op"] for w in wl)
     value = op_bytes / (ms_step * 1e-3) / 1e9
@@ -360,6 +449,7 @@ def main():
     g_bytes = sum(alg_bytes(w)["gather"] for w in wl)
     achieved = g_bytes / (kern_ms * 1e-3) / 1e9
 
+    traffic, traffic_kernel = gather_traffic() if args.config == "cfg2" else (None, None)
     out = {
         "metric": "fused decode-GEMV HBM GB/s",
         "value": round(value, 2),
@@ -385,31 +475,50 @@ def main():
             "wall_s_timed": round(wall, 4),
             "gather_kernel_ms_events": round(kern_ms, 6),
         },
+        "replays": {
+            "count": args.replays, "steps_per_replay": args.steps,
+            "median_ms_per_step": round(rep_med, 6), "min_ms_per_step": round(rep_min, 6),
+            "max_ms_per_step": round(rep_max, 6),
+            "median_value": round(op_bytes / (rep_med * 1e-3) / 1e9, 2),
+            "gather_median_ms": round(kern_ms, 6), "gather_min_ms": round(kern_min, 6),
+            "gather_max_ms": round(kern_max, 6),
+        },
         "roofline": {
             "kernel": "gatherw_kernel<8,4,true> (csdr_hsdb_gather_group, both matrices)",
+            "timing": f"median of {args.replays} graph replays of {args.steps} launches",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": GATHER_TRAFFIC_BYTES if args.config == "cfg2" else None,
+            "traffic": traffic,
+            "traffic_source": "profiles/hsdb_gather_cfg2_traffic.json" if traffic else None,
             "algorithmic_bytes_per_launch": g_bytes,
         },
         "cpu_baseline": None,
     }
     if not args.no_cpu:
         dt, n, threads = cpu_baseline(streams, xs, args.cpu_seconds)
+        dt1, n1, _ = cpu_baseline(streams, xs, args.cpu_seconds / 2, threads=1)
+        info = cpu_info()
         out["cpu_baseline"] = {
             "value": round(op_bytes / dt / 1e9, 3),
             "unit": "GB/s",
             "cores": threads,
             "kind": "port",
             "sample": (f"{n} full steps of the same workload (both matrices, M=1) through "
-                       f"oracle/csdr_oracle.c orc_hsdb_matmul with OpenMP, "
+                       f"oracle/csdr_oracle.c orc_hsdb_matmul with {threads} OpenMP threads, "
                        f"{dt * 1e3:.1f} ms/step"),
+            **info,
+            "single_thread": {
+                "value": round(op_bytes / dt1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "sample": f"{n1} steps on one thread, {dt1 * 1e3:.1f} ms/step (the reference's "
+                          "fused HSDR path is single-threaded)"},
         }
     if not args.no_decode:
         out["decode"] = decode_leg(args)
+    if not args.no_7b:
+        out["decode_7b"] = decode_7b_leg(torch)
     if not args.no_encode:
         out["encode"] = encode_leg(args)
     if args.calibrate_copy:

@@ -78,6 +78,8 @@ def orc():
         L.orc_hsdr_decompress.argtypes = [_u8p, _sz, _f32p, _sz]
         L.orc_hsdr_matmul_row_major.argtypes = [_u8p, _sz, _f32p, _sz, _f32p]
         L.orc_hsdb_matmul.argtypes = [_u8p, _sz, _f32p, _sz, _f32p]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_set_threads.restype = C.c_int
         L.orc_q4k_dequant.argtypes = [_u8p, _sz, C.c_int, _f32p]
         L.orc_q5k_dequant.argtypes = [_u8p, _sz, _f32p]
         L.orc_q6k_dequant.argtypes = [_u8p, _sz, _f32p]
@@ -508,3 +510,8 @@ def hsdr_mp(tiles: np.ndarray, D: np.ndarray, gamma, S: int, k: int) -> np.ndarr
     orc().orc_hsdr_mp(t.ravel(), t.shape[0], t.shape[1], d.ravel(), d.shape[0], S, k, g,
                       codes.ravel())
     return codes
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads of the restatement's parallel loops (previous setting returned)."""
+    return int(orc().orc_set_threads(int(n)))

@@ -806,3 +806,9 @@ void orc_hsdr_mp(const float* tiles, size_t n_tiles, size_t C, const float* D, s
         free(used);
     }
 }
+
+int orc_set_threads(int n) {
+    const int prev = omp_get_max_threads();
+    if (n > 0) omp_set_num_threads(n);
+    return prev;
+}

@@ -81,6 +81,9 @@ int orc_hsdr_matmul_row_major(const uint8_t* buf, size_t n, const float* x, size
  * times x[C_full:]. x is (C x M) row-major, y (R x M). Accepts HSDR streams with
  * tile_rows == 1 as well (binary codes). */
 int orc_hsdb_matmul(const uint8_t* buf, size_t n, const float* x, size_t M, float* y);
+/* OpenMP threads of the parallel loops from now on (the CPU baseline's single-thread time);
+ * returns the previous setting. */
+int orc_set_threads(int n);
 
 /* ---- GGUF K-quant dequant ----
  * ggml order (engine path, A7): SparseInferenceEngine.cpp:266-274 (scale/min unpack),
