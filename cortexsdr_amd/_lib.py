@@ -191,6 +191,10 @@ class CompressionOptions(C.Structure):
     ]
 
 
+SIGNATURES["csdr_attn_decode_rope_kv"] = (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int,
+                                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                                  C.c_float, _vp, _vp, _sz, _vp])
+SIGNATURES["csdr_attn_decode_splits_kv"] = (C.c_int, [C.c_int] * 6)
 SIGNATURES["csdr_hsdb_matmul_noalloc"] = (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp])
 
 
@@ -222,6 +226,7 @@ class DecoderConfig(C.Structure):
         ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int),
         ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
         ("max_ctx", C.c_int), ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+        ("kv_dtype", C.c_int),
     ]
 
 

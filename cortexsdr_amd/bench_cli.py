@@ -168,7 +168,7 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
         toks = dec.tokens(n_prompt, n_new)
         per_tok = t_decode / (n_new - 1)
         code = w.code_bytes()
-        kv = 2 * QWEN2_0_5B.n_layers * QWEN2_0_5B.n_kv_heads * QWEN2_0_5B.head_dim * 2
+        kv = 2 * QWEN2_0_5B.n_layers * QWEN2_0_5B.n_kv_heads * QWEN2_0_5B.head_dim * 4  # fp32 cache
         alg = code + kv * (n_prompt + n_new // 2)
         return {"n_prompt": n_prompt, "n_new": n_new,
                 "decode_tokens_per_s": round(1.0 / per_tok, 1),
@@ -186,15 +186,15 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
 def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
     """Config 5: Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads of 128, SwiGLU
     11008, vocab 32000, all linears HSDB-coded: 1024 x 64 dictionary, 8 nnz per block) at
-    context `ctx` with the fp16 KV cache filled with N(0,1), `batch` sequences, weights
-    resident.
+    context `ctx` with the fp16 KV cache (as configs[4] states) filled with N(0,1), `batch`
+    sequences, weights resident.
     Two distinct coded layers are generated and loaded 16 times each: every layer has its own
     device copy, so HBM traffic per step is that of 32 distinct layers."""
     import dataclasses
 
     from .decoder import Decoder, DecoderSpec, DecoderWeights, synthetic_weights
 
-    spec = DecoderSpec(32, 4096, 32, 32, 128, 11008, 32000, ctx + steps + 8)
+    spec = DecoderSpec(32, 4096, 32, 32, 128, 11008, 32000, ctx + steps + 8, kv_dtype="f16")
     t0 = time.time()
     w2 = synthetic_weights(dataclasses.replace(spec, n_layers=2), seed=seed)
     w = DecoderWeights(spec, [w2.layers[l % 2] for l in range(32)], w2.lm_head, w2.final_norm)

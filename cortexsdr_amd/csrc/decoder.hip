@@ -55,6 +55,17 @@ __global__ void step_begin_kernel(const int* __restrict__ pos, const int* __rest
     }
 }
 
+// fp16 K/V rows (each sequence's `per` values contiguous) into an fp32 cache whose sequences
+// start `pitch` values apart.
+__global__ void widen_kv_kernel(const uint16_t* __restrict__ src, size_t per, size_t pitch,
+                                size_t count, float* __restrict__ dst) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = i / per, j = i - b * per;
+        dst[b * pitch + j] = (float)__builtin_bit_cast(_Float16, src[i]);
+    }
+}
+
 // Body-only step end: advance the position.
 __global__ void advance_kernel(int* __restrict__ pos) {
     if (threadIdx.x == 0) *pos += 1;
@@ -104,7 +115,7 @@ struct Layer {
     const csdr_hsdb *gate = nullptr, *up = nullptr, *down = nullptr;
     float *attn_norm = nullptr, *ffn_norm = nullptr;
     float *bq = nullptr, *bk = nullptr, *bv = nullptr;
-    uint16_t *kc = nullptr, *vc = nullptr;
+    void *kc = nullptr, *vc = nullptr;  // cfg.kv_dtype elements
 };
 
 }  // namespace
@@ -228,9 +239,9 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
         }
         // B == 1: the split partials stay in the workspace and the o projection combines
         // them while staging its input; B > 1: combined into a (B x H) first
-        RC(csdr_attn_decode_rope(d->q, d->k, d->v, L.kc, L.vc, d->len, B, c.max_ctx, Hq, Hkv, hd,
-                                 c.rope_theta, 0.0f, B > 1 ? d->a : nullptr, d->ws_attn,
-                                 d->ws_attn_bytes, st));
+        RC(csdr_attn_decode_rope_kv(d->q, d->k, d->v, L.kc, L.vc, c.kv_dtype, d->len, B,
+                                    c.max_ctx, Hq, Hkv, hd, c.rope_theta, 0.0f,
+                                    B > 1 ? d->a : nullptr, d->ws_attn, d->ws_attn_bytes, st));
         {
             const csdr_hsdb* segs[1] = {L.o};
             float* ys[1] = {d->x};  // x += o(attention)
@@ -252,8 +263,9 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
                       CSDR_XOP_SILU_MUL, nullptr, st));
         }
     }
-    if (!d->fused && B > 1)
-        return set_error(CSDR_E_UNSUPPORTED, "decoder: the unfused step runs batch 1 only");
+    if (!d->fused && (B > 1 || c.kv_dtype != CSDR_F16))
+        return set_error(CSDR_E_UNSUPPORTED,
+                         "decoder: the unfused step runs batch 1 over an fp16 K/V cache only");
     for (int l = 0; l < c.n_layers && !d->fused; ++l) {
         const Layer& L = d->layers[l];
         RC(csdr_rms_norm(d->x, L.attn_norm, 1, H, c.rms_eps, d->h, st));
@@ -263,9 +275,12 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
             const float* bias[3] = {L.bq, L.bk, L.bv};
             RC(mm(d, 3, segs, d->h, ys, bias, 0, st));
         }
-        RC(csdr_rope_kv(d->q, d->k, d->v, 1, Hq, Hkv, hd, d->pos, c.rope_theta, L.kc, L.vc,
+        RC(csdr_rope_kv(d->q, d->k, d->v, 1, Hq, Hkv, hd, d->pos, c.rope_theta,
+                        static_cast<uint16_t*>(L.kc), static_cast<uint16_t*>(L.vc),
                         c.max_ctx, st));
-        RC(csdr_attn_decode(d->q, L.kc, L.vc, d->len, 0, 1, c.max_ctx, Hq, Hkv, hd, 0.0f, d->a,
+        RC(csdr_attn_decode(d->q, static_cast<const uint16_t*>(L.kc),
+                            static_cast<const uint16_t*>(L.vc), d->len, 0, 1, c.max_ctx, Hq, Hkv,
+                            hd, 0.0f, d->a,
                             d->ws_attn, d->ws_attn_bytes, st));
         {
             const csdr_hsdb* segs[1] = {L.o};
@@ -385,6 +400,7 @@ CSDR_API int csdr_decoder_create_batched(const csdr_decoder_config* cfg, int bat
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
         c.n_heads % c.n_kv_heads || c.head_dim * c.n_heads != c.hidden || c.ffn <= 0 ||
         c.vocab <= 0 || c.max_ctx <= 0 || (c.head_dim != 64 && c.head_dim != 128) ||
+        (c.kv_dtype != CSDR_F32 && c.kv_dtype != CSDR_F16) ||
         !(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f))
         return set_error(CSDR_E_INVALID, "decoder_create: inconsistent config");
     csdr_decoder* d = new (std::nothrow) csdr_decoder();
@@ -395,12 +411,18 @@ CSDR_API int csdr_decoder_create_batched(const csdr_decoder_config* cfg, int bat
     d->layers.resize(c.n_layers);
     if (const char* e = getenv("CSDR_DECODER_GRAPH")) d->use_graph = atoi(e) != 0;
     if (const char* e = getenv("CSDR_DECODER_FUSED")) d->fused = atoi(e) != 0;
-    d->attn_splits = csdr_attn_decode_splits(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx);
+    d->attn_splits = csdr_attn_decode_splits_kv(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx,
+                                                c.kv_dtype);
     int rc = CSDR_OK;
-    // per layer: sequence b's cache at b * max_ctx positions
-    const size_t kvn = (size_t)B * c.max_ctx * c.n_kv_heads * c.head_dim;
-    for (auto& L : d->layers)
-        if ((rc = dalloc(d, &L.kc, kvn)) || (rc = dalloc(d, &L.vc, kvn))) break;
+    // per layer: sequence b's cache at b * max_ctx positions, fp32 or fp16 elements
+    const size_t kvn = (size_t)B * c.max_ctx * c.n_kv_heads * c.head_dim *
+                       (c.kv_dtype == CSDR_F32 ? 2 : 1);
+    for (auto& L : d->layers) {
+        uint16_t *kc = nullptr, *vc = nullptr;
+        if ((rc = dalloc(d, &kc, kvn)) || (rc = dalloc(d, &vc, kvn))) break;
+        L.kc = kc;
+        L.vc = vc;
+    }
     const size_t kvw = (size_t)c.n_kv_heads * c.head_dim;
     const size_t wide = std::max(c.hidden, c.ffn);
     if (!rc) rc = dalloc(d, &d->x, (size_t)B * c.hidden);
@@ -603,15 +625,36 @@ CSDR_API int csdr_decoder_load_kv(csdr_decoder* d, int layer, const uint16_t* k,
         return set_error(CSDR_E_INVALID, "decoder_load_kv: bad argument");
     // sequence b's n rows follow sequence b - 1's in the source, and start at b * max_ctx in
     // the cache
-    const size_t row = (size_t)d->cfg.n_kv_heads * d->cfg.head_dim * 2;
+    const size_t kvw = (size_t)d->cfg.n_kv_heads * d->cfg.head_dim;
+    const size_t row = kvw * 2;
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
-    if (n) {
+    if (!n) return CSDR_OK;
+    if (d->cfg.kv_dtype == CSDR_F16) {
         CSDR_HIP_CHECK(hipMemcpy2D(d->layers[layer].kc, row * d->cfg.max_ctx, k, row * n, row * n,
                                    d->B, hipMemcpyDefault));
         CSDR_HIP_CHECK(hipMemcpy2D(d->layers[layer].vc, row * d->cfg.max_ctx, v, row * n, row * n,
                                    d->B, hipMemcpyDefault));
+        return CSDR_OK;
     }
-    return CSDR_OK;
+    // fp32 cache: the fp16 rows staged on the device, then widened into place
+    const size_t count = (size_t)d->B * n * kvw;
+    uint16_t* stage = nullptr;
+    CSDR_HIP_CHECK(hipMalloc(&stage, count * 2));
+    int rc = CSDR_OK;
+    for (int which = 0; which < 2 && rc == CSDR_OK; ++which) {
+        if (hipMemcpy(stage, which ? v : k, count * 2, hipMemcpyDefault) != hipSuccess) {
+            rc = set_error(CSDR_E_HIP, "decoder_load_kv: staging copy failed");
+            break;
+        }
+        float* dst = static_cast<float*>(which ? d->layers[layer].vc : d->layers[layer].kc);
+        widen_kv_kernel<<<(unsigned)std::min<size_t>((count + 255) / 256, 65536), 256, 0,
+                          d->stream>>>(stage, (size_t)n * kvw, (size_t)d->cfg.max_ctx * kvw,
+                                       count, dst);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(d->stream) != hipSuccess)
+            rc = set_error(CSDR_E_HIP, "decoder_load_kv: widening failed");
+    }
+    (void)hipFree(stage);
+    return rc;
 }
 
 // Continues from an imported context: positions [0, position) count as processed and

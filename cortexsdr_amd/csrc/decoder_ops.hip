@@ -176,10 +176,59 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q,
 struct RopeArgs {
     const float* knew;  // B x Hkv x HD (fp32, unrotated)
     const float* vnew;
-    _Float16* kcw;
+    _Float16* kcw;      // fp16 caches (written at position L - 1)
     _Float16* vcw;
     float theta;
+    float* kcw32;       // fp32 caches (the fp32 K/V form of attn_split_kernel)
+    float* vcw32;
 };
+
+// Eight consecutive K or V values of one cache row, as the cache stores them (fp16: one
+// 16-byte piece; fp32: two), read as fp32.
+template <typename KT>
+struct Row8;
+template <>
+struct Row8<_Float16> {
+    h8 v;
+    __device__ static Row8 load(const _Float16* p) {
+        Row8 r;
+        r.v = *reinterpret_cast<const h8*>(p);
+        return r;
+    }
+    __device__ void store(_Float16* p) const { *reinterpret_cast<h8*>(p) = v; }
+    __device__ float get(int i) const { return (float)v[i]; }
+    __device__ void set(int i, float x) { v[i] = (_Float16)x; }  // the cache's rounding
+};
+template <>
+struct Row8<float> {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 a, b;
+    __device__ static Row8 load(const float* p) {
+        Row8 r;
+        r.a = reinterpret_cast<const f4*>(p)[0];
+        r.b = reinterpret_cast<const f4*>(p)[1];
+        return r;
+    }
+    __device__ void store(float* p) const {
+        reinterpret_cast<f4*>(p)[0] = a;
+        reinterpret_cast<f4*>(p)[1] = b;
+    }
+    __device__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+    __device__ void set(int i, float x) {
+        if (i < 4) a[i] = x;
+        else b[i - 4] = x;
+    }
+};
+template <typename KT>
+__device__ __forceinline__ KT* cache_w(const RopeArgs& ra, bool v);
+template <>
+__device__ __forceinline__ _Float16* cache_w<_Float16>(const RopeArgs& ra, bool v) {
+    return v ? ra.vcw : ra.kcw;
+}
+template <>
+__device__ __forceinline__ float* cache_w<float>(const RopeArgs& ra, bool v) {
+    return v ? ra.vcw32 : ra.kcw32;
+}
 
 constexpr int kAttnMaxS = 256;  // positions per split, at most (one thread per position)
 
@@ -413,9 +462,12 @@ __global__ __launch_bounds__(kThreads) void attn_lds_kernel(
 // row per position); every K and V row of the split is loaded before the first use; scores go
 // through LDS for the softmax; P.V accumulates per lane and reduces across lanes and waves.
 // Same partials and ROPE behaviour as attn_lds_kernel.
-template <int HD, int GW, bool ROPE>
+// KT: the cache element (fp16, or fp32 for the fp32 K/V cache; fp32 splits hold at most 128
+// positions, kAttnMaxS32, to keep the split's rows in registers).
+constexpr int kAttnMaxS32 = 128;
+template <int HD, int GW, bool ROPE, typename KT = _Float16>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
-    const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
+    const float* __restrict__ q, const KT* __restrict__ kc, const KT* __restrict__ vc,
     const int* __restrict__ lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
     float* __restrict__ part, float* __restrict__ out, int nsplit, RopeArgs ra) {
     constexpr int LPP = HD / 8;          // lanes per position
@@ -461,23 +513,23 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
         for (int i = 0; i < 8; ++i)
             qv[g][i] = (g < nh) ? q[((size_t)b * Hq + h0 + g) * HD + li * 8 + i] : 0.f;
     const size_t rstride = (size_t)Hkv * HD;
-    const _Float16* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
-    const _Float16* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    const KT* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
+    const KT* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
     // every K and V row of this lane's positions is loaded before the first use (one memory
     // round trip for the split, instead of one per pass and operand)
-    constexpr int kMaxPass = 256 / NG;  // S <= 256
+    constexpr int kMaxPass = (sizeof(KT) == 4 ? kAttnMaxS32 : kAttnMaxS) / NG;
     const int npass = (p1 - p0 + NG - 1) / NG;
-    h8 kr[kMaxPass], vr[kMaxPass];
+    Row8<KT> kr[kMaxPass], vr[kMaxPass];
 #pragma unroll
     for (int j = 0; j < kMaxPass; ++j) {
         if (j < npass) {
             const int p = min(p0 + lg + j * NG, p1 - 1);
-            kr[j] = *reinterpret_cast<const h8*>(kb + (size_t)p * rstride);
-            vr[j] = *reinterpret_cast<const h8*>(vb + (size_t)p * rstride);
+            kr[j] = Row8<KT>::load(kb + (size_t)p * rstride);
+            vr[j] = Row8<KT>::load(vb + (size_t)p * rstride);
         }
     }
     const int plast = L - 1;
-    h8 knew = {}, vnew = {};
+    Row8<KT> knew{}, vnew{};
     if constexpr (ROPE) {
         // rotate this lane's 8 query dims of every head, and the new key, at position L - 1;
         // each pair's (cos, sin) evaluated once per workgroup (the lanes of a position group
@@ -502,16 +554,16 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
                 qv[g][i + 1] = fmaf(x0, sn, x1 * c);
             }
             const float k0 = kn[i], k1 = kn[i + 1];
-            knew[i] = (_Float16)fmaf(k0, c, -(k1 * sn));
-            knew[i + 1] = (_Float16)fmaf(k0, sn, k1 * c);
-            vnew[i] = (_Float16)vn[i];
-            vnew[i + 1] = (_Float16)vn[i + 1];
+            knew.set(i, fmaf(k0, c, -(k1 * sn)));
+            knew.set(i + 1, fmaf(k0, sn, k1 * c));
+            vnew.set(i, vn[i]);
+            vnew.set(i + 1, vn[i + 1]);
         }
         if (blockIdx.z == 0 && plast >= p0 && plast < p1 && lg == (plast - p0) % NG) {
-            *reinterpret_cast<h8*>(ra.kcw + ((size_t)b * T + plast) * rstride + kvh * HD + li * 8) =
-                knew;
-            *reinterpret_cast<h8*>(ra.vcw + ((size_t)b * T + plast) * rstride + kvh * HD + li * 8) =
-                vnew;
+            knew.store(cache_w<KT>(ra, false) + ((size_t)b * T + plast) * rstride + kvh * HD +
+                       li * 8);
+            vnew.store(cache_w<KT>(ra, true) + ((size_t)b * T + plast) * rstride + kvh * HD +
+                       li * 8);
         }
     }
     // scores
@@ -519,12 +571,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     for (int j = 0; j < kMaxPass; ++j) {
         const int p = p0 + lg + j * NG;
         if (j >= npass || p >= p1) continue;
-        const h8 kv = (ROPE && p == plast) ? knew : kr[j];
+        const Row8<KT> kv = (ROPE && p == plast) ? knew : kr[j];
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             float d = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], (float)kv[i], d);
+            for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kv.get(i), d);
 #pragma unroll
             for (int off = LPP / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
             if (li == 0 && g < nh) sc[g][p - p0] = d * scale;
@@ -560,12 +612,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     for (int j = 0; j < kMaxPass; ++j) {
         const int p = p0 + lg + j * NG;
         if (j >= npass || p >= p1) continue;
-        const h8 vv = (ROPE && p == plast) ? vnew : vr[j];
+        const Row8<KT> vv = (ROPE && p == plast) ? vnew : vr[j];
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
             const float e = sc[g][p - p0];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[g][i] = fmaf(e, (float)vv[i], o[g][i]);
+            for (int i = 0; i < 8; ++i) o[g][i] = fmaf(e, vv.get(i), o[g][i]);
         }
     }
 #pragma unroll
@@ -1069,9 +1121,19 @@ struct AttnShape {
     bool mfma;
 };
 
-AttnShape attn_shape(int B, int Hq, int Hkv, int hd, int T) {
+AttnShape attn_shape(int B, int Hq, int Hkv, int hd, int T, bool kv32 = false) {
     AttnShape a;
     a.G = Hq / Hkv;
+    if (kv32) {
+        // fp32 cache: the lane-per-position kernel, up to 4 query heads per pass, splits of at
+        // most kAttnMaxS32 positions
+        a.mfma = false;
+        a.GW = a.G == 1 ? 1 : 4;
+        a.zsplit = (a.G + a.GW - 1) / a.GW;
+        a.S = std::min(attn_split_len(B, Hkv, a.zsplit, T), kAttnMaxS32);
+        a.nsplit = (T + a.S - 1) / a.S;
+        return a;
+    }
     a.mfma = a.G >= 2 && a.G <= kAttnMfmaMaxG && (hd == 64 || hd == 128) && attn_mfma_enabled();
     if (a.mfma) {
         a.GW = a.G;
@@ -1087,10 +1149,23 @@ AttnShape attn_shape(int B, int Hq, int Hkv, int hd, int T) {
     return a;
 }
 
-int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, const int* lens_dev,
+template <int HD, bool ROPE>
+void launch_attn32(dim3 grid, int G, const float* q, const float* k32, const float* v32,
+                   const int* lens, int len_host, int T, int Hq, int Hkv, float scale, int S,
+                   float* part, float* out, int nsplit, const RopeArgs& ra, hipStream_t st) {
+    if (G == 1)
+        attn_split_kernel<HD, 1, ROPE, float><<<grid, kThreads, 0, st>>>(
+            q, k32, v32, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
+    else
+        attn_split_kernel<HD, 4, ROPE, float><<<grid, kThreads, 0, st>>>(
+            q, k32, v32, lens, len_host, T, Hq, Hkv, scale, S, part, out, nsplit, ra);
+}
+
+int attn_run(const float* q, const void* kcache, const void* vcache, const int* lens_dev,
              int len_host, int B, int T, int Hq, int Hkv, int hd, float scale, float* out,
-             void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t st) {
-    const AttnShape sh = attn_shape(B, Hq, Hkv, hd, T);
+             void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t st,
+             bool kv32 = false) {
+    const AttnShape sh = attn_shape(B, Hq, Hkv, hd, T, kv32);
     const bool partials = sh.nsplit > 1 || out == nullptr;
     if (partials &&
         (!workspace || workspace_bytes < csdr_attn_decode_workspace_bytes(B, Hq, hd, T)))
@@ -1098,9 +1173,34 @@ int attn_run(const float* q, const uint16_t* kcache, const uint16_t* vcache, con
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)hd);
     float* part = static_cast<float*>(workspace);
     dim3 grid(B * Hkv, sh.nsplit, sh.zsplit);
-    auto k16 = reinterpret_cast<const _Float16*>(kcache);
-    auto v16 = reinterpret_cast<const _Float16*>(vcache);
+    auto k16 = static_cast<const _Float16*>(kcache);
+    auto v16 = static_cast<const _Float16*>(vcache);
     const RopeArgs none{};
+    if (kv32) {
+        auto k32 = static_cast<const float*>(kcache);
+        auto v32 = static_cast<const float*>(vcache);
+        if (hd == 64) {
+            if (ra)
+                launch_attn32<64, true>(grid, sh.G, q, k32, v32, lens_dev, len_host, T, Hq, Hkv,
+                                        scale, sh.S, part, out, sh.nsplit, *ra, st);
+            else
+                launch_attn32<64, false>(grid, sh.G, q, k32, v32, lens_dev, len_host, T, Hq, Hkv,
+                                         scale, sh.S, part, out, sh.nsplit, none, st);
+            if (out && sh.nsplit > 1)
+                attn_combine_kernel<64><<<B * Hq, 64, 0, st>>>(part, sh.nsplit, out);
+        } else {
+            if (ra)
+                launch_attn32<128, true>(grid, sh.G, q, k32, v32, lens_dev, len_host, T, Hq, Hkv,
+                                         scale, sh.S, part, out, sh.nsplit, *ra, st);
+            else
+                launch_attn32<128, false>(grid, sh.G, q, k32, v32, lens_dev, len_host, T, Hq,
+                                          Hkv, scale, sh.S, part, out, sh.nsplit, none, st);
+            if (out && sh.nsplit > 1)
+                attn_combine_kernel<128><<<B * Hq, 128, 0, st>>>(part, sh.nsplit, out);
+        }
+        CSDR_LAUNCH_CHECK("attn_decode");
+        return CSDR_OK;
+    }
     if (hd == 64) {
         if (ra)
             launch_attn<64, true>(grid, sh.G, sh.mfma, q, k16, v16, lens_dev, len_host, T, Hq,
@@ -1232,10 +1332,35 @@ CSDR_API int csdr_attn_decode_rope(const float* q, const float* k_new, const flo
         return set_error(CSDR_E_INVALID, "attn_decode_rope: bad argument");
     if (hd != 64 && hd != 128)
         return set_error(CSDR_E_UNSUPPORTED, "attn_decode_rope: head_dim must be 64 or 128");
-    RopeArgs ra{k_new, v_new, reinterpret_cast<_Float16*>(kcache),
-                reinterpret_cast<_Float16*>(vcache), theta};
+    return csdr_attn_decode_rope_kv(q, k_new, v_new, kcache, vcache, CSDR_F16, lens_dev, B, T,
+                                    Hq, Hkv, hd, theta, scale, out, workspace, workspace_bytes,
+                                    hip_stream);
+}
+
+CSDR_API int csdr_attn_decode_rope_kv(const float* q, const float* k_new, const float* v_new,
+                                      void* kcache, void* vcache, int kv_dtype,
+                                      const int* lens_dev, int B, int T, int Hq, int Hkv, int hd,
+                                      float theta, float scale, float* out, void* workspace,
+                                      size_t workspace_bytes, void* hip_stream) {
+    if (!q || !k_new || !v_new || !kcache || !vcache || !lens_dev || B <= 0 || T <= 0 ||
+        Hq <= 0 || Hkv <= 0 || Hq % Hkv)
+        return set_error(CSDR_E_INVALID, "attn_decode_rope: bad argument");
+    if (hd != 64 && hd != 128)
+        return set_error(CSDR_E_UNSUPPORTED, "attn_decode_rope: head_dim must be 64 or 128");
+    if (kv_dtype != CSDR_F16 && kv_dtype != CSDR_F32)
+        return set_error(CSDR_E_INVALID, "attn_decode_rope: kv_dtype must be CSDR_F16 or CSDR_F32");
+    const bool kv32 = kv_dtype == CSDR_F32;
+    RopeArgs ra{k_new, v_new, kv32 ? nullptr : static_cast<_Float16*>(kcache),
+                kv32 ? nullptr : static_cast<_Float16*>(vcache), theta,
+                kv32 ? static_cast<float*>(kcache) : nullptr,
+                kv32 ? static_cast<float*>(vcache) : nullptr};
     return attn_run(q, kcache, vcache, lens_dev, 0, B, T, Hq, Hkv, hd, scale, out, workspace,
-                    workspace_bytes, &ra, static_cast<hipStream_t>(hip_stream));
+                    workspace_bytes, &ra, static_cast<hipStream_t>(hip_stream), kv32);
+}
+
+CSDR_API int csdr_attn_decode_splits_kv(int B, int Hq, int Hkv, int hd, int T, int kv_dtype) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0 || Hq % Hkv) return -1;
+    return attn_shape(B, Hq, Hkv, hd, T, kv_dtype == CSDR_F32).nsplit;
 }
 
 CSDR_API size_t csdr_select_workspace_bytes(void) { return (size_t)kSelectBlocks * 8; }

@@ -35,6 +35,7 @@ class DecoderSpec:
     max_ctx: int
     rope_theta: float = 1e6
     rms_eps: float = 1e-5
+    kv_dtype: str = "f32"   # K/V cache element: "f32" (the reference's precision) or "f16"
 
     def shapes(self) -> dict:
         """(rows, cols) of each linear of one block (y = W x, W row-major R x C)."""
@@ -121,8 +122,11 @@ class Decoder:
             raise RuntimeError("cortexsdr_amd.Decoder needs a HIP device (no CPU fallback)")
         self._lib = _lib.load()
         self.spec = s = weights.spec
+        if s.kv_dtype not in ("f32", "f16"):
+            raise ValueError("kv_dtype must be 'f32' or 'f16'")
         cfg = _lib.DecoderConfig(s.n_layers, s.hidden, s.n_heads, s.n_kv_heads, s.head_dim,
-                                 s.ffn, s.vocab, s.max_ctx, s.rope_theta, s.rms_eps)
+                                 s.ffn, s.vocab, s.max_ctx, s.rope_theta, s.rms_eps,
+                                 0 if s.kv_dtype == "f32" else 1)
         h = C.c_void_p()
         _lib.check(self._lib.csdr_decoder_create_batched(C.byref(cfg), int(batch), C.byref(h)))
         self._h = h

@@ -215,6 +215,9 @@ class SdrEntry:
     sparsity: float = 0.0
     input_shape: tuple = ()
     output_shape: tuple = ()
+    sorted_indices: bool = False       # metadata fields written only with dims (has_metadata)
+    scale: float | None = None
+    zero_point: float | None = None
 
 
 def _str(s: str) -> bytes:
@@ -244,7 +247,9 @@ def write_sdr(path: str, entries, version: int = 2) -> None:
         if e.dims is not None:
             out += struct.pack("<BB", 1, len(e.dims))
             out += struct.pack(f"<{len(e.dims)}I", *e.dims)
-            out += struct.pack("<fBBB", e.sparsity, 0, 0, 0)  # sparsity, sorted, no scale/zp
+            out += struct.pack("<fB", e.sparsity, 1 if e.sorted_indices else 0)
+            for opt in (e.scale, e.zero_point):
+                out += struct.pack("<Bf", 1, opt) if opt is not None else b"\x00"
         else:
             out += b"\x00"
         for shape in (e.input_shape, e.output_shape):

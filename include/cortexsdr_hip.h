@@ -388,6 +388,16 @@ CSDR_API int csdr_attn_decode_rope(const float* q, const float* k_new, const flo
                                    int T, int Hq, int Hkv, int hd, float theta, float scale,
                                    float* out, void* workspace, size_t workspace_bytes,
                                    void* hip_stream);
+/* As csdr_attn_decode_rope with the cache element type given: CSDR_F16 (the form above) or
+ * CSDR_F32 (caches of fp32 values, B x T x Hkv x hd; the K/V precision of the reference's
+ * recompute, run_transformer_decode cortex_sdk.cpp:1543-1696, on the vector ALU kernel).
+ * csdr_attn_decode_splits_kv: the split count such a call produces. */
+CSDR_API int csdr_attn_decode_rope_kv(const float* q, const float* k_new, const float* v_new,
+                                      void* kcache, void* vcache, int kv_dtype,
+                                      const int* lens_dev, int B, int T, int Hq, int Hkv, int hd,
+                                      float theta, float scale, float* out, void* workspace,
+                                      size_t workspace_bytes, void* hip_stream);
+CSDR_API int csdr_attn_decode_splits_kv(int B, int Hq, int Hkv, int hd, int T, int kv_dtype);
 /* Next token as select_best_from_logits (cortex_sdk.cpp:1005-1030): score = logit /
  * temperature (temperature <= 0: 1) minus penalty where repeated[i] != 0 (repeated may be
  * NULL); best finite score, lowest index on ties; -1 when none is finite. Writes the token to
@@ -473,8 +483,8 @@ CSDR_API int csdr_hsda_load(const csdr_hsda* hsda, const char* name, void* hip_s
  * cortex_inference_engine_generate_text :1951-2054, batch 1)
  *
  * A Llama/Qwen-style decoder whose linears are loaded csdr_hsdb segments (the decoder keeps
- * the pointers; the caller keeps the segments alive). K/V are kept in a per-layer fp16 cache
- * (max_ctx positions) instead of the reference's whole-context recompute; each step is one
+ * the pointers; the caller keeps the segments alive). K/V are kept in a per-layer cache
+ * (max_ctx positions, fp32 or fp16) instead of the reference's whole-context recompute; each step is one
  * replay of a captured HIP graph. Token choice as select_next_token_from_embedding_transpose
  * (cortex_sdk.cpp:1032-1206): output RMSNorm, sanitize_hidden_for_sampling (:959-976), lm_head
  * scores, select_best_from_logits with `temperature` and `penalty` for tokens generated so far
@@ -491,6 +501,10 @@ typedef struct csdr_decoder_config {
     int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
     float rope_theta; /* RoPE base (get_rope_cache, cortex_sdk.cpp:1363; 1e6 there) */
     float rms_eps;    /* RMSNorm epsilon (rms_norm, cortex_sdk.cpp:1212; 1e-5 there) */
+    int kv_dtype;     /* K/V cache element: CSDR_F32 (0, the precision of the reference's
+                       * recompute) or CSDR_F16 (half the bytes; its rounding is amplified by
+                       * sharp attention, e.g. 8e-3 of the scores on a random-init 24-layer
+                       * model) */
 } csdr_decoder_config;
 
 CSDR_API int csdr_decoder_create(const csdr_decoder_config* cfg, csdr_decoder** out);
@@ -535,7 +549,8 @@ CSDR_API int csdr_decoder_logits(const csdr_decoder* dec, float* out);
 /* Number of positions processed so far (-1 for NULL). */
 CSDR_API int csdr_decoder_position(const csdr_decoder* dec);
 /* Import a precomputed context (a cached prompt prefix): fp16 K and V of positions [0, n) for
- * one layer, [sequence][position][kv head][head_dim], from host or device memory. */
+ * one layer, [sequence][position][kv head][head_dim], from host or device memory (widened
+ * into an fp32 cache). */
 CSDR_API int csdr_decoder_load_kv(csdr_decoder* dec, int layer, const uint16_t* k,
                                   const uint16_t* v, int n);
 /* Continue from an imported context: positions [0, position) count as processed and `token`

@@ -40,7 +40,15 @@ and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
   fit_<i>_w, fit_<i>_stream, fit_<i>_cfg  the same compress with ksvd_iters = 3..6 (atom
              updates and re-encodes); cfg = (tile_rows, tile_cols, K, stages, k, iters).
 
-Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode]
+and tests/golden/sdr_fixtures.npz (`sdr` argument):
+
+  sdr_<i>_bytes, sdr_<i>_listing  .sdr archives written by cortexsdr_amd.formats.write_sdr
+             (version 2: a GGUF-named decoder's segments, raw segments with and without
+             metadata, with scale / zero point / sorted flags, input / output shapes) and the
+             reference's own index lister's output for them (src/tool_sdr_inspect.cpp --all,
+             compiled by `make -C oracle inspect`)
+
+Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode | sdr]
 """
 from __future__ import annotations
 
@@ -209,8 +217,57 @@ def encode_main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def sdr_archives():
+    """The archives of sdr_fixtures.npz, as (name, entries) (deterministic)."""
+    from cortexsdr_amd import formats
+    from cortexsdr_amd.decoder import DecoderSpec, synthetic_weights
+
+    spec = DecoderSpec(2, 64, 2, 1, 32, 128, 96, 16)
+    w = synthetic_weights(spec, n_atoms=16, nnz=2, seed=4)
+    dec = formats.decoder_entries(w)
+    rng = np.random.default_rng(8)
+    raw = [
+        formats.SdrEntry(name="meta.json", payload=b'{"arch": "llama"}', data_format="json",
+                         original_type=6),
+        formats.SdrEntry(name="conv1.weight", payload=rng.standard_normal(24).astype(np.float32)
+                         .tobytes(), dims=(2, 3, 4), sparsity=0.25, sorted_indices=True,
+                         scale=0.125, zero_point=-3.0, layer_type="Conv", layer_name="conv1",
+                         layer_index=7, input_shape=(1, 3, 8, 8), output_shape=(1, 2, 6, 6)),
+        formats.SdrEntry(name="q.weight", payload=bytes(range(200)), strategy_id=4,
+                         data_format="int8", original_size=800, dims=(10, 20), scale=0.02),
+        formats.SdrEntry(name="bias", payload=b"", dims=(0,), zero_point=1.5),
+        formats.SdrEntry(name="gguf_tokenizer_model", payload=b"gpt2", data_format="str",
+                         original_type=6, input_shape=(4,)),
+    ]
+    return [("decoder", dec), ("raw", raw), ("mixed", raw[:2] + dec[:5] + raw[2:])]
+
+
+def sdr_main() -> None:
+    import subprocess
+    import tempfile
+
+    from cortexsdr_amd import formats
+
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "inspect"], check=True)
+    tool = os.path.join(ROOT, "oracle", "_ref", "sdr_inspect")
+    out = {}
+    with tempfile.TemporaryDirectory() as td:
+        for i, (name, ents) in enumerate(sdr_archives()):
+            path = os.path.join(td, f"{name}.sdr")
+            formats.write_sdr(path, ents, version=2)
+            listing = subprocess.run([tool, path, "--all"], check=True, capture_output=True,
+                                     text=True).stdout
+            out[f"sdr_{i}_bytes"] = np.frombuffer(open(path, "rb").read(), np.uint8)
+            out[f"sdr_{i}_listing"] = np.frombuffer(listing.encode(), np.uint8)
+    path = os.path.join(HERE, "sdr_fixtures.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
 if __name__ == "__main__":
-    if sys.argv[1:] == ["encode"]:
+    if sys.argv[1:] == ["sdr"]:
+        sdr_main()
+    elif sys.argv[1:] == ["encode"]:
         encode_main()
     elif sys.argv[1:] == ["hsda"]:
         hsda_main()

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import GOLDEN
+from conftest import GOLDEN, ROOT
 from cortexsdr_amd import formats, synth
 from cortexsdr_amd._lib import CsdrError
 from cortexsdr_amd.archive import HsdaArchive, SdrArchive
@@ -110,3 +110,52 @@ def test_sdr_bad_archives_rejected(tmp_path):
             SdrArchive(p)
     with pytest.raises(CsdrError):
         SdrArchive(str(tmp_path / "does_not_exist.sdr"))
+
+
+def _listing(text):
+    """(version, n, index_offset, rows [(strategy, comp, orig, name)]) of the reference
+    lister's --all output (src/tool_sdr_inspect.cpp:47-108)."""
+    lines = text.splitlines()
+    head = dict(kv.split("=") for kv in lines[0].split())
+    rows = []
+    for ln in lines[3:]:
+        parts = ln.split(None, 3)
+        if len(parts) == 4 and parts[0].isdigit():
+            rows.append((int(parts[0]), int(parts[1]), int(parts[2]), parts[3]))
+    total = int(lines[-1].split("=")[1].split()[0])
+    return int(head["version"]), int(head["segments"]), int(head["index_offset"]), rows, total
+
+
+@pytest.mark.parametrize("i", [0, 1, 2])
+def test_sdr_reader_matches_reference_lister(tmp_path, i):
+    """The C++ .sdr reader against the reference's own index lister (tool_sdr_inspect.cpp,
+    compiled from the reference sources when the fixtures were written) on archives written
+    by formats.write_sdr: every segment's name, strategy id, compressed and original size in
+    index order, the index offset and the byte total; and the writer reproduces the fixture
+    archive byte for byte (the layout the lister parsed is the one write_sdr writes)."""
+    import sys
+
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from make_fixtures import sdr_archives
+
+    fx = np.load(os.path.join(ROOT, "tests", "golden", "sdr_fixtures.npz"), allow_pickle=False)
+    raw = fx[f"sdr_{i}_bytes"].tobytes()
+    version, n, index_off, rows, total = _listing(fx[f"sdr_{i}_listing"].tobytes().decode())
+    path = str(tmp_path / "a.sdr")
+    open(path, "wb").write(raw)
+    a = SdrArchive(path)
+    assert version == 2 and len(a) == n == len(rows)
+    assert sum(r[1] for r in rows) == total
+    for j, (strat, comp, orig, name) in enumerate(rows):
+        info = a.info(j)
+        assert (info["strategy_id"], info["compressed_size"], info["original_size"],
+                info["name"]) == (strat, comp, orig, name)
+        assert info["data_offset"] + comp <= index_off
+        assert len(a.read(j)) == comp
+    # the first payload starts right after the 28-byte header, the last ends at the index
+    assert a.info(0)["data_offset"] == 28
+    assert a.info(n - 1)["data_offset"] + rows[-1][1] == index_off
+    name, ents = sdr_archives()[i]
+    regen = str(tmp_path / "b.sdr")
+    formats.write_sdr(regen, ents, version=2)
+    assert open(regen, "rb").read() == raw

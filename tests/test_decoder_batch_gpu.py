@@ -1,8 +1,8 @@
 """GPU parity of the batched decoder (csdr_decoder_create_batched) against the oracle.
 
 * Full configs[4] width (hidden 4096, 32 heads of 128, SwiGLU 11008, dictionary 1024 x 64 with
-  8 nonzeros per block, vocab 32000) at reduced depth (2 layers), batch 1 and 8: each sequence
-  continues its own fp16 K/V context of 4095 positions (values N(0,1), as configs[4] states)
+  8 nonzeros per block, vocab 32000) at reduced depth (2 layers), batch 1 and 8, fp16 K/V
+  cache as configs[4] states: each sequence continues its own fp16 K/V context of 4095 positions (values N(0,1), as configs[4] states)
   for two steps; per sequence and step the lm_head scores are within 1e-3 relative L2 of
   oracle.decoder.step_cached (pinned against the whole-context recompute in
   test_decoder_oracle.py) and the greedy token is the oracle's unless its top two scores are
@@ -30,7 +30,7 @@ def _check_token(scores, tok, what):
 
 @pytest.fixture(scope="module")
 def cfg5_weights():
-    spec = DecoderSpec(2, 4096, 32, 32, 128, 11008, 32000, 4097)
+    spec = DecoderSpec(2, 4096, 32, 32, 128, 11008, 32000, 4097, kv_dtype="f16")
     return synthetic_weights(spec, n_atoms=1024, nnz=8, seed=5, norm_jitter=0.05)
 
 
