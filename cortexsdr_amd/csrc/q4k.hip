@@ -17,13 +17,21 @@
 //     super-block's quants plus the block header (the 8 lanes of a block read the same 16
 //     header bytes), so a wave load instruction covers 8 whole blocks. x is staged in LDS.
 //     Per piece: y += d*sc*(sum q*x) - dmin*m*(sum x) in fp32 (q stays an exact integer).
-//   q4k_mfma_kernel (M > 1): 16 rows per workgroup, the 4 waves split the super-blocks; each
-//     16-wide k step dequantises 4 values per lane in fp32, splits them into fp16 hi + lo and
-//     issues two v_mfma_f32_16x16x16f16 per 16 output columns (fp32 accumulate), then the
-//     waves' partial tiles are summed through LDS.
+//   q4k_mm_kernel (M > 1): a workgroup owns 16 RT rows and a range of super-blocks (split K);
+//     each wave holds RT 16-row tiles and takes every 4th super-block of the range (the next
+//     one's loads issued before the current one is multiplied). Per
+//     32-element sub-block a lane dequantises its 8 values of each row tile in fp32
+//     ((d*sc)*q - dmin*m, one fused multiply-add) and rounds them to fp16 once, and each
+//     16-column tile of X (fp16, read straight into the B operand, 16 bytes per lane) takes
+//     one v_mfma_f32_16x16x32_f16 (fp32 accumulate). The waves' tiles are summed through LDS
+//     and added into Y (zeroed by a fill launch) with one atomic per output per workgroup.
+//     The single fp16 rounding of W puts the product about 3e-4 (relative L2) from fp32.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -37,6 +45,7 @@ constexpr int kUnroll = 4;  // 8-block steps per wave issued back to back (gemv)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t byte_of(const u32x4& v, int k) {
@@ -273,6 +282,179 @@ __global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const uint8_t* __res
     }
 }
 
+// ---------------------------------------------------------------- M > 1, split-K MFMA
+
+// Launch shape of q4k_mm_kernel: RT 16-row tiles per wave (16 RT rows per workgroup) and KB
+// super-blocks per workgroup for NT 16-column tiles. Measured on cfg3 (4096 x 4096 and
+// 4096 x 14336, M = 16 / 32 / 64, including the fill launch): up to 32 columns two row tiles
+// and 8 super-blocks (16 past 32 super-blocks per row): 13.5 / 32.4 us at M = 32 against
+// 16.4 / 39.8 for four tiles and 4. At 64 columns four tiles and 16 super-blocks halve the
+// partial-sum atomics (43.0 us at 4096 x 14336 against 57.6) while that still gives 256
+// workgroups; below that (4096 x 4096: 64 workgroups, 33.3 us) two tiles and 8 (20.8 us).
+void q4k_mm_shape(int R, int nblk, int NT, int& RT, int& KB) {
+    RT = 2;
+    KB = nblk > 32 ? 16 : 8;
+    if (NT >= 4 && (size_t)((R + 63) / 64) * (size_t)((nblk + 15) / 16) >= 256) {
+        RT = 4;
+        KB = 16;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * kThreads)
+        y[i] = 0.0f;
+}
+
+// 8 quant values of sub-block s for this lane (k = 8 j .. 8 j + 7 of the sub-block, j = lane
+// group) as bytes, from the block's quants (ggml: the 8-byte piece of group s / 2, low nibbles
+// for even s; interleaved: the 4-byte piece of sub-block s, nibbles low / high alternating).
+template <int ORDER>
+__device__ __forceinline__ void quant8(const uint32_t* q, int s, uint32_t& w0, uint32_t& w1) {
+    if (ORDER == 0) {
+        const int sh = (s & 1) * 4;
+        w0 = (q[2 * (s >> 1)] >> sh) & 0x0F0F0F0Fu;
+        w1 = (q[2 * (s >> 1) + 1] >> sh) & 0x0F0F0F0Fu;
+    } else {
+        const uint32_t v = q[s];
+        const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        // element order lo.b0 hi.b0 lo.b1 hi.b1 | lo.b2 hi.b2 lo.b3 hi.b3 as bytes
+        w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+    }
+}
+
+template <int ORDER, int NT, int RT>
+__global__ __launch_bounds__(kThreads) void q4k_mm_kernel(const uint8_t* __restrict__ W, int R,
+                                                          int nblk, const _Float16* __restrict__ X,
+                                                          int M, float* __restrict__ Y, int KB) {
+    __shared__ floatx4 red[3][RT][NT][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane & 15, j = lane >> 4;
+    const int r0 = blockIdx.x * (16 * RT);
+    const int b0 = blockIdx.y * KB, b1 = min(nblk, b0 + KB);
+    const int n0 = blockIdx.z * 16 * NT;
+    const int C = nblk * 256;
+    floatx4 acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const _Float16* xr[NT];
+    bool xl[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int n = n0 + nt * 16 + rl;
+        xl[nt] = n < M;
+        xr[nt] = X + (size_t)min(n, M - 1) * C + 8 * j;
+    }
+    const uint8_t* wr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        wr[rt] = W + (size_t)min(r0 + rt * 16 + rl, R - 1) * nblk * kBlockBytes;
+    // a block's header and this lane's quants of every row tile
+    struct Blk {
+        u32x4 hdr[RT];
+        uint32_t q[RT][8];
+    };
+    auto load_blk = [&](int blk, Blk& o) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const uint8_t* bp = wr[rt] + (size_t)blk * kBlockBytes;
+            o.hdr[rt] = *reinterpret_cast<const u32x4*>(bp);
+            if (ORDER == 0) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint2 v = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * j);
+                    o.q[rt][2 * g] = v.x;
+                    o.q[rt][2 * g + 1] = v.y;
+                }
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < 8; ++sb)
+                    o.q[rt][sb] = *reinterpret_cast<const uint32_t*>(bp + 16 + 16 * sb + 4 * j);
+            }
+        }
+    };
+    auto compute_blk = [&](int blk, const Blk& cb) {
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) {
+            half8 bv[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const half8 v = *reinterpret_cast<const half8*>(xr[nt] + (size_t)blk * 256 + 32 * sb);
+                bv[nt] = xl[nt] ? v : half8{};
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                float sc, mn;
+                scale_min(cb.hdr[rt], sb, sc, mn);
+                const float ds = hdr_d(cb.hdr[rt]) * sc, dm = hdr_dmin(cb.hdr[rt]) * mn;
+                uint32_t w0, w1;
+                quant8<ORDER>(cb.q[rt], sb, w0, w1);
+                half8 a;
+                a[0] = (_Float16)fmaf(ds, (float)((w0 >> 0) & 0xFFu), -dm);
+                a[1] = (_Float16)fmaf(ds, (float)((w0 >> 8) & 0xFFu), -dm);
+                a[2] = (_Float16)fmaf(ds, (float)((w0 >> 16) & 0xFFu), -dm);
+                a[3] = (_Float16)fmaf(ds, (float)((w0 >> 24) & 0xFFu), -dm);
+                a[4] = (_Float16)fmaf(ds, (float)((w1 >> 0) & 0xFFu), -dm);
+                a[5] = (_Float16)fmaf(ds, (float)((w1 >> 8) & 0xFFu), -dm);
+                a[6] = (_Float16)fmaf(ds, (float)((w1 >> 16) & 0xFFu), -dm);
+                a[7] = (_Float16)fmaf(ds, (float)((w1 >> 24) & 0xFFu), -dm);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[nt], acc[rt][nt], 0, 0, 0);
+            }
+        }
+    };
+    // every 4th block of the range; the next block's loads go out before this one is
+    // multiplied (two buffers, named, so that both stay in registers)
+    int blk = b0 + wave;
+    if (blk < b1) {
+        Blk ba, bb;
+        load_blk(blk, ba);
+        for (;;) {
+            const int nb1 = blk + kThreads / 64;
+            if (nb1 < b1) load_blk(nb1, bb);
+            compute_blk(blk, ba);
+            if (nb1 >= b1) break;
+            const int nb2 = nb1 + kThreads / 64;
+            if (nb2 < b1) load_blk(nb2, ba);
+            compute_blk(nb1, bb);
+            if (nb2 >= b1) break;
+            blk = nb2;
+        }
+    }
+    // the 4 waves' tiles: waves 1..3 park theirs in LDS, wave 0 sums and adds into Y
+    if (wave > 0) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) red[wave - 1][rt][nt][lane] = acc[rt][nt];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                floatx4 v = acc[rt][nt];
+#pragma unroll
+                for (int w = 0; w < 3; ++w) v += red[w][rt][nt][lane];
+                // D tile: this lane holds rows 4 j + i, column rl
+                const int n = n0 + nt * 16 + rl;
+                if (n >= M) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = r0 + rt * 16 + 4 * j + i;
+                    if (r < R)
+                        __hip_atomic_fetch_add(Y + (size_t)n * R + r, v[i], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+    }
+}
+
 // ---------------------------------------------------------------- dequant to fp32
 
 template <int ORDER>
@@ -352,15 +534,34 @@ CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void*
     } else {
         if (x_dtype != CSDR_F16)
             return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: M > 1 takes fp16 x");
-        if (reinterpret_cast<uintptr_t>(x) % 8)
-            return set_error(CSDR_E_INVALID, "q4k_linear: x must be 8-byte aligned");
-        dim3 grid((R + 15) / 16, (M + 16 * kMaxNT - 1) / (16 * kMaxNT));
-        if (order == CSDR_Q4K_GGML)
-            q4k_mfma_kernel<0><<<grid, kThreads, 0, st>>>(static_cast<const uint8_t*>(w), R, nblk,
-                                                         static_cast<const _Float16*>(x), M, y);
-        else
-            q4k_mfma_kernel<1><<<grid, kThreads, 0, st>>>(static_cast<const uint8_t*>(w), R, nblk,
-                                                         static_cast<const _Float16*>(x), M, y);
+        if (reinterpret_cast<uintptr_t>(x) % 16 || C % 8)
+            return set_error(CSDR_E_INVALID, "q4k_linear: x must be 16-byte aligned");
+        // Y = 0, then the split-K tiles add into it
+        const size_t ny = (size_t)M * R;
+        fill_zero_kernel<<<(unsigned)std::min<size_t>((ny + kThreads - 1) / kThreads, 4096),
+                           kThreads, 0, st>>>(y, ny);
+        // launch shape: row tiles per wave (RT) and super-blocks per workgroup (KB)
+        const int NT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        int RT = 2, KB = 8;
+        q4k_mm_shape(R, nblk, NT, RT, KB);
+        dim3 grid((R + 16 * RT - 1) / (16 * RT), (nblk + KB - 1) / KB, (M + 16 * NT - 1) / (16 * NT));
+        const auto* wp = static_cast<const uint8_t*>(w);
+        const auto* xp = static_cast<const _Float16*>(x);
+        auto go = [&](auto kern) { kern<<<grid, kThreads, 0, st>>>(wp, R, nblk, xp, M, y, KB); };
+        auto pick = [&](auto ord) {
+            constexpr int O = decltype(ord)::value;
+            if (RT == 4) {
+                if (NT == 1) go(q4k_mm_kernel<O, 1, 4>);
+                else if (NT == 2) go(q4k_mm_kernel<O, 2, 4>);
+                else go(q4k_mm_kernel<O, 4, 4>);
+            } else {
+                if (NT == 1) go(q4k_mm_kernel<O, 1, 2>);
+                else if (NT == 2) go(q4k_mm_kernel<O, 2, 2>);
+                else go(q4k_mm_kernel<O, 4, 2>);
+            }
+        };
+        if (order == CSDR_Q4K_GGML) pick(std::integral_constant<int, 0>{});
+        else pick(std::integral_constant<int, 1>{});
     }
     CSDR_LAUNCH_CHECK("q4k_linear");
     return CSDR_OK;

@@ -38,10 +38,13 @@ def test_dequant_bitexact(gpu, order):
     (4096, 14336, 1, "ggml", np.float16),     # config 3, W 4096 x 14336
     (4096, 4096, 32, "ggml", np.float16),     # config 3, M = 32
     (4096, 14336, 32, "ggml", np.float16),
+    (4096, 14336, 64, "ggml", np.float16),    # four 16-row tiles per wave, 16 super-blocks
+    (4096, 4096, 64, "interleaved", np.float16),  # 64 columns, two row tiles per wave
+    (300, 1024, 24, "interleaved", np.float16),   # two column tiles, ragged rows
     (300, 1024, 1, "interleaved", np.float32),
     (300, 1024, 5, "interleaved", np.float16),
     (37, 256, 1, "ggml", np.float32),
-    (37, 512, 70, "ggml", np.float16),        # more than 64 columns: two launch slices
+    (37, 512, 70, "ggml", np.float16),        # more than 64 columns: two column groups
 ])
 def test_linear(gpu, R, C, M, order, xdt):
     from cortexsdr_amd import q4k
