@@ -275,3 +275,12 @@ def check(rc: int) -> None:
 
 def exported_symbols() -> list[str]:
     return list(SIGNATURES)
+SIGNATURES["csdr_dense_linear_ex"] = (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,
+                                              C.c_int, _vp])
+SIGNATURES["csdr_rope_kv_rows"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, C.c_float, _vp, _vp, C.c_int,
+                                           C.c_int, _vp])
+SIGNATURES["csdr_attn_prefill"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp,
+                                           _vp])
+SIGNATURES["csdr_decoder_set_prefill_chunk"] = (C.c_int, [_vp, C.c_int])

@@ -147,6 +147,12 @@ struct csdr_decoder {
     int attn_splits = 1;
     int n_prompt = 0;
     std::vector<void*> allocs;
+    // batched prefill: tokens per sequence per pass, and its buffers (rows = B x tokens)
+    int prefill_chunk = 512;
+    int pf_rows = 0;
+    float *pf_x = nullptr, *pf_h = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    float *pf_a = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_w = nullptr;
+    int* pf_tok = nullptr;
 };
 
 namespace {
@@ -216,6 +222,95 @@ int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x,
                                       flags | CSDR_HSDB_TOKEN_MAJOR, xop, nw, c.rms_eps,
                                       d->attn_splits, c.head_dim, d->ws_hsdb, d->ws_hsdb_bytes,
                                       st);
+}
+
+// Prefill pass rows: row b * T + t takes sequence b's token at position p0 + t.
+__global__ void pass_tokens_kernel(const int* __restrict__ ring, int cap, int B, int T, int p0,
+                                   int* __restrict__ tok) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < B * T) tok[i] = ring[(size_t)(i / T) * cap + p0 + i % T];
+}
+
+void free_prefill(csdr_decoder* d) {
+    for (float* p : {d->pf_x, d->pf_h, d->pf_q, d->pf_k, d->pf_v, d->pf_a, d->pf_g, d->pf_u,
+                     d->pf_w})
+        if (p) (void)hipFree(p);
+    if (d->pf_tok) (void)hipFree(d->pf_tok);
+    d->pf_x = d->pf_h = d->pf_q = d->pf_k = d->pf_v = d->pf_a = d->pf_g = d->pf_u = d->pf_w =
+        nullptr;
+    d->pf_tok = nullptr;
+    d->pf_rows = 0;
+}
+
+// Buffers of a prefill pass over `rows` token rows (kept for later passes of up to as many).
+int ensure_prefill(csdr_decoder* d, int rows) {
+    if (rows <= d->pf_rows) return CSDR_OK;
+    free_prefill(d);
+    const csdr_decoder_config& c = d->cfg;
+    const size_t n = (size_t)rows, H = c.hidden, F = c.ffn;
+    const size_t kvw = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t wmax = std::max({H * H, kvw * H, F * H});
+    const std::pair<float**, size_t> bufs[] = {
+        {&d->pf_x, n * H},   {&d->pf_h, n * H},   {&d->pf_q, n * H},
+        {&d->pf_k, n * kvw}, {&d->pf_v, n * kvw}, {&d->pf_a, n * std::max(H, F)},
+        {&d->pf_g, n * F},   {&d->pf_u, n * F},   {&d->pf_w, wmax}};
+    for (const auto& b : bufs) {
+        void* p = nullptr;
+        if (hipMalloc(&p, b.second * 4) != hipSuccess) {
+            free_prefill(d);
+            return set_error(CSDR_E_HIP, "decoder_prefill: out of device memory for " +
+                                             std::to_string(rows) + " prefill rows");
+        }
+        *b.first = static_cast<float*>(p);
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, n * 4) != hipSuccess) {
+        free_prefill(d);
+        return set_error(CSDR_E_HIP, "decoder_prefill: out of device memory");
+    }
+    d->pf_tok = static_cast<int*>(p);
+    d->pf_rows = rows;
+    return CSDR_OK;
+}
+
+// y (M x R) (+)= x (M x C) . W^T + bias for a coded W: decoded to dense fp32 once, then the
+// matrix-core product over all M rows.
+int pass_linear(csdr_decoder* d, const csdr_hsdb* w, const float* x, int M, float* y,
+                const float* bias, int flags, hipStream_t st) {
+    csdr_hsdb_info info;
+    RC(csdr_hsdb_get_info(w, &info));
+    RC(csdr_hsdb_decompress(w, d->pf_w, st));
+    return csdr_dense_linear_ex(d->pf_w, (int)info.rows, (int)info.cols, x, M, y, bias, flags, st);
+}
+
+// The decoder body (no head) over positions [p0, p0 + T) of every sequence as one pass of
+// M = B x T token rows: K/V of those positions land in the caches as the decode step would
+// write them.
+int prefill_pass(csdr_decoder* d, int p0, int T, hipStream_t st) {
+    const csdr_decoder_config& c = d->cfg;
+    const int B = d->B, M = B * T, H = c.hidden, F = c.ffn;
+    const int cap = c.max_ctx + 1;
+    pass_tokens_kernel<<<(M + 255) / 256, 256, 0, st>>>(d->ring, cap, B, T, p0, d->pf_tok);
+    CSDR_LAUNCH_CHECK("decoder pass tokens");
+    RC(csdr_hsdb_decode_rows(d->emb, d->pf_tok, M, d->pf_x, st));
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = d->layers[l];
+        RC(csdr_rms_norm(d->pf_x, L.attn_norm, M, H, c.rms_eps, d->pf_h, st));
+        RC(pass_linear(d, L.q, d->pf_h, M, d->pf_q, L.bq, 0, st));
+        RC(pass_linear(d, L.k, d->pf_h, M, d->pf_k, L.bk, 0, st));
+        RC(pass_linear(d, L.v, d->pf_h, M, d->pf_v, L.bv, 0, st));
+        RC(csdr_rope_kv_rows(d->pf_q, d->pf_k, d->pf_v, B, T, p0, c.n_heads, c.n_kv_heads,
+                             c.head_dim, c.rope_theta, L.kc, L.vc, c.kv_dtype, c.max_ctx, st));
+        RC(csdr_attn_prefill(d->pf_q, L.kc, L.vc, c.kv_dtype, B, T, p0, c.max_ctx, c.n_heads,
+                             c.n_kv_heads, c.head_dim, 0.0f, d->pf_a, st));
+        RC(pass_linear(d, L.o, d->pf_a, M, d->pf_x, nullptr, CSDR_HSDB_ACCUMULATE, st));
+        RC(csdr_rms_norm(d->pf_x, L.ffn_norm, M, H, c.rms_eps, d->pf_h, st));
+        RC(pass_linear(d, L.gate, d->pf_h, M, d->pf_g, nullptr, 0, st));
+        RC(pass_linear(d, L.up, d->pf_h, M, d->pf_u, nullptr, 0, st));
+        RC(csdr_silu_mul(d->pf_g, d->pf_u, (size_t)M * F, d->pf_a, st));
+        RC(pass_linear(d, L.down, d->pf_a, M, d->pf_x, nullptr, CSDR_HSDB_ACCUMULATE, st));
+    }
+    return CSDR_OK;
 }
 
 // One step at device position *pos for the token ring[*pos]; with_head adds the output norm,
@@ -466,6 +561,7 @@ CSDR_API int csdr_decoder_free(csdr_decoder* d) {
     if (d->stream) (void)hipStreamSynchronize(d->stream);
     destroy_graphs(d);
     if (d->stream) (void)hipStreamDestroy(d->stream);
+    free_prefill(d);
     for (void* p : d->allocs) (void)hipFree(p);
     delete d;
     return CSDR_OK;
@@ -547,11 +643,26 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
     CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)B * cap * 4));
     CSDR_HIP_CHECK(hipMemcpy2D(d->ring, cap * 4, prompt, (size_t)n_prompt * 4,
                                (size_t)n_prompt * 4, B, hipMemcpyHostToDevice));
-    for (int i = 0; i + 1 < n_prompt; ++i) RC(run_step(d, 0, temperature, penalty));
+    const int body = n_prompt - 1;
+    if (d->prefill_chunk > 0 && body > 0) {
+        // positions [0, body) in multi-token passes, then the last one as a decode step
+        const int chunk = std::min(d->prefill_chunk, body);
+        RC(ensure_prefill(d, B * chunk));
+        for (int p0 = 0; p0 < body; p0 += chunk) RC(prefill_pass(d, p0, std::min(chunk, body - p0), st));
+        CSDR_HIP_CHECK(hipMemcpyAsync(d->pos, &body, 4, hipMemcpyHostToDevice, st));
+    } else {
+        for (int i = 0; i < body; ++i) RC(run_step(d, 0, temperature, penalty));
+    }
     RC(run_step(d, 1, temperature, penalty));
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
     d->host_pos = n_prompt;
     d->n_prompt = n_prompt;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_set_prefill_chunk(csdr_decoder* d, int tokens) {
+    if (!d || tokens < 0) return set_error(CSDR_E_INVALID, "decoder_set_prefill_chunk: bad argument");
+    d->prefill_chunk = std::min(tokens, d->cfg.max_ctx);
     return CSDR_OK;
 }
 

@@ -88,24 +88,6 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float* __restrict_
 
 // ---------------------------------------------------------------- SiLU(g) * u
 
-// Dense fp32 linear for uncoded (strategy 0) 2-D weights: one wave per output row, lanes
-// stride over the input features, fp32 sums reduced across the wave.
-__global__ __launch_bounds__(kThreads) void dense_linear_kernel(const float* __restrict__ W, int R,
-                                                                int C, const float* __restrict__ x,
-                                                                int M, float* __restrict__ y) {
-    const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    if (r >= R) return;
-    const float* w = W + (size_t)r * C;
-    for (int m = 0; m < M; ++m) {
-        const float* xm = x + (size_t)m * C;
-        float acc = 0.0f;
-        for (int c = lane; c < C; c += 64) acc = fmaf(w[c], xm[c], acc);
-        acc = csdr::wave_sum(acc);
-        if (lane == 0) y[(size_t)m * R + r] = acc;
-    }
-}
-
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ g,
                                                             const float* __restrict__ u,
                                                             size_t n, float* __restrict__ y) {
@@ -1261,17 +1243,6 @@ CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, floa
     const int nt = n > 2048 ? 1024 : 256;
     rms_norm_kernel<<<ntok, nt, 0, static_cast<hipStream_t>(hip_stream)>>>(x, w, n, eps, y);
     CSDR_LAUNCH_CHECK("rms_norm");
-    return CSDR_OK;
-}
-
-CSDR_API int csdr_dense_linear(const float* w, int R, int C, const float* x, int M, float* y,
-                               void* hip_stream) {
-    if (!w || !x || !y || R <= 0 || C <= 0 || M <= 0)
-        return set_error(CSDR_E_INVALID, "dense_linear: bad argument");
-    const int rows_per_block = kThreads / 64;
-    dense_linear_kernel<<<(R + rows_per_block - 1) / rows_per_block, kThreads, 0,
-                          static_cast<hipStream_t>(hip_stream)>>>(w, R, C, x, M, y);
-    CSDR_LAUNCH_CHECK("dense_linear");
     return CSDR_OK;
 }
 

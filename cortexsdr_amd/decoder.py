@@ -115,7 +115,7 @@ class Decoder:
     """A device decoder over resident HSDB segments (greedy / penalised argmax) decoding
     `batch` sequences in lockstep; per-sequence arrays are sequence-major (batch, ...)."""
 
-    def __init__(self, weights: DecoderWeights, batch: int = 1):
+    def __init__(self, weights: DecoderWeights, batch: int = 1, prefill_chunk: int | None = None):
         import torch
 
         if not torch.cuda.is_available():
@@ -149,6 +149,8 @@ class Decoder:
                   if weights.final_norm is not None else None)
             _lib.check(self._lib.csdr_decoder_set_output(
                 self._h, self._lm._h, _fptr(fn), self._emb._h if self._emb else None))
+            if prefill_chunk is not None:
+                self.set_prefill_chunk(prefill_chunk)
         except Exception:
             self.close()
             raise
@@ -169,6 +171,11 @@ class Decoder:
             self.close()
         except Exception:
             pass
+
+    def set_prefill_chunk(self, tokens: int) -> None:
+        """Prompt tokens per sequence in one multi-token prefill pass (0: one decode step
+        per prompt position)."""
+        _lib.check(self._lib.csdr_decoder_set_prefill_chunk(self._h, int(tokens)))
 
     # ------------------------------------------------------------------ generation
     def prefill(self, prompt, temperature: float = 0.8, penalty: float = 1.5) -> None:

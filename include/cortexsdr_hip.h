@@ -352,6 +352,13 @@ CSDR_API int csdr_rms_norm(const float* x, const float* w, int ntok, int n, floa
  * segments (SparseInferenceEngine.cpp:1290-1311). */
 CSDR_API int csdr_dense_linear(const float* w, int R, int C, const float* x, int M, float* y,
                                void* hip_stream);
+/* As csdr_dense_linear, plus bias (R floats, may be NULL) and flags (CSDR_HSDB_ACCUMULATE:
+ * y += x . W^T + bias). M >= 8 (C % 4 == 0, w and x 16-byte aligned) runs on the fp32 matrix
+ * cores (v_mfma_f32_16x16x4_f32, fp32 accumulation); smaller M one wave per row of W. The
+ * decoder's batched prefill multiplies the prompt rows by each coded weight decoded once with
+ * csdr_hsdb_decompress through this call. */
+CSDR_API int csdr_dense_linear_ex(const float* w, int R, int C, const float* x, int M, float* y,
+                                  const float* bias, int flags, void* hip_stream);
 /* y = silu(g) * u (silu_mul, cortex_sdk.cpp:1245-1256). */
 CSDR_API int csdr_silu_mul(const float* g, const float* u, size_t n, float* y, void* hip_stream);
 /* RoPE on adjacent pairs (get_rope_cache/apply_rope_inplace, cortex_sdk.cpp:1363-1423) of
@@ -398,6 +405,22 @@ CSDR_API int csdr_attn_decode_rope_kv(const float* q, const float* k_new, const 
                                       float theta, float scale, float* out, void* workspace,
                                       size_t workspace_bytes, void* hip_stream);
 CSDR_API int csdr_attn_decode_splits_kv(int B, int Hq, int Hkv, int hd, int T, int kv_dtype);
+/* Multi-token (prefill) forms: B sequences of T new tokens each, row b * T + t of q
+ * (B T x Hq x hd), k and v (B T x Hkv x hd) at position p0 + t of sequence b; caches
+ * B x max_ctx x Hkv x hd of kv_dtype (CSDR_F32 or CSDR_F16) elements, p0 + T <= max_ctx.
+ * csdr_rope_kv_rows rotates q and k in place (apply_rope_inplace, cortex_sdk.cpp:1395-1423,
+ * the decode step's arithmetic) and appends k and v to the caches at their positions.
+ * csdr_attn_prefill then computes out (same layout as q) = causal softmax(q.K^T * scale) V
+ * over positions [0, p0 + t] of the caches (Kernels::multi_head_attention with the causal
+ * mask, attention_kernels.cpp:26-113, the tiled form flash_attention.cpp:17-163; GQA as
+ * repeat_kv_heads; scale 0 = 1/sqrt(hd)); head_dim 64 or 128, fp32 matrix-core products,
+ * 16-byte aligned buffers. */
+CSDR_API int csdr_rope_kv_rows(float* q, float* k, const float* v, int B, int T, int p0, int Hq,
+                               int Hkv, int hd, float theta, void* kcache, void* vcache,
+                               int kv_dtype, int max_ctx, void* hip_stream);
+CSDR_API int csdr_attn_prefill(const float* q, const void* kcache, const void* vcache,
+                               int kv_dtype, int B, int T, int p0, int max_ctx, int Hq, int Hkv,
+                               int hd, float scale, float* out, void* hip_stream);
 /* Next token as select_best_from_logits (cortex_sdk.cpp:1005-1030): score = logit /
  * temperature (temperature <= 0: 1) minus penalty where repeated[i] != 0 (repeated may be
  * NULL); best finite score, lowest index on ties; -1 when none is finite. Writes the token to
@@ -480,7 +503,7 @@ CSDR_API int csdr_hsda_load(const csdr_hsda* hsda, const char* name, void* hip_s
 
 /* ======================================================================
  * Decoder engine (api/cortex_sdk.cpp run_transformer_decode :1543-1696 and
- * cortex_inference_engine_generate_text :1951-2054, batch 1)
+ * cortex_inference_engine_generate_text :1951-2054)
  *
  * A Llama/Qwen-style decoder whose linears are loaded csdr_hsdb segments (the decoder keeps
  * the pointers; the caller keeps the segments alive). K/V are kept in a per-layer cache
@@ -528,9 +551,17 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* dec, int layer, const csdr_hsd
 CSDR_API int csdr_decoder_set_output(csdr_decoder* dec, const csdr_hsdb* lm_head,
                                      const float* final_norm, const csdr_hsdb* embedding);
 /* Runs the prompt from position 0 (resetting the cache and the generated-token set) and
- * selects the first new token (it lands at position n_prompt). prompt: batch x n_prompt ids. */
+ * selects the first new token (it lands at position n_prompt). prompt: batch x n_prompt ids.
+ * Positions 0 .. n_prompt - 2 run as multi-token passes of up to the prefill chunk tokens per
+ * sequence (csdr_decoder_set_prefill_chunk): every weight decoded once per pass to dense fp32
+ * and multiplied on the matrix cores for all the pass's tokens, causal prompt attention
+ * (csdr_attn_prefill); the last prompt position runs the decode step, which selects. */
 CSDR_API int csdr_decoder_prefill(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
                                   float temperature, float penalty);
+/* Tokens per sequence in one prefill pass (default 512); 0 runs every prompt position as a
+ * decode step instead (the token-at-a-time form). Buffers for B x chunk rows and one dense
+ * weight (the largest, F x H fp32) are allocated at the first prefill that needs them. */
+CSDR_API int csdr_decoder_set_prefill_chunk(csdr_decoder* dec, int tokens);
 /* n_steps further tokens, one graph replay each; synchronises at the end. */
 CSDR_API int csdr_decoder_decode(csdr_decoder* dec, int n_steps, float temperature,
                                  float penalty);

@@ -114,7 +114,7 @@ def test_decoder_fused_equals_unfused(gpu):
     for fused in ("1", "0"):
         os.environ["CSDR_DECODER_FUSED"] = fused
         try:
-            dec = Decoder(w)
+            dec = Decoder(w, prefill_chunk=0)   # every prompt position through the step
         finally:
             del os.environ["CSDR_DECODER_FUSED"]
         try:
