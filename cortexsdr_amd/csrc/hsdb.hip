@@ -603,6 +603,127 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     }
 }
 
+// ---- kernel 1 at M == 1 with 64-long blocks (no attention x op): P[b][a] = D[a] . x_b as a
+// small product P^T (K x NB) = D (K x 64) . [x_0 .. x_NB-1] (64 x NB) on the fp32 matrix
+// cores (v_mfma_f32_16x16x4_f32). Workgroup = NT / 64 waves x 16 atoms and 16 block
+// columns, wave w the atoms 16 w .. 16 w + 15 of the workgroup's; lane l supplies atom l % 16
+// (A) and block column l % 16 (B), and the contraction over a block's 64 features runs with
+// lane group l / 16 taking features 16 (l / 16) .. + 15 in its 16 steps, so each lane's
+// operands are one contiguous 64-byte run of the dictionary row and of x, loaded straight
+// from memory (no LDS, no cross-lane sums). Lane l ends with P[block l % 16][atoms
+// 4 (l / 16) .. + 3]. Y is initialised as in dx_kernel; the x op (RMSNorm with its statistic
+// over all C features, or SiLU . x2) is applied to the B operand in registers.
+template <int XOP, int NT>
+__device__ __forceinline__ void dx1_body(const Params& p, int wg) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    constexpr int kAtoms = NT / 4;  // 16 per wave
+    int g = 0;
+    while (g + 1 < p.G && wg >= p.m[g + 1].dx_base) ++g;
+    const MatDesc& d = p.m[g];
+    const int u = wg - d.dx_base;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    {
+        const size_t ytot = (size_t)d.R;
+        const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
+        const size_t ye = min(ytot, (size_t)(u + 1) * yper);
+        for (size_t i = (size_t)u * yper + tid; i < ye; i += NT) {
+            const float bv = d.bias ? d.bias[i] : 0.0f;
+            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        }
+    }
+    const int na = (d.K + kAtoms - 1) / kAtoms;
+    const int ag = u % na, bg = u / na;
+    const int a = min(ag * kAtoms + wave * 16 + li, d.K - 1);
+    const int b = min(bg * 16 + li, d.NB - 1);
+    const int f0 = b * 64 + lg * 16;  // this lane's 16 features
+    f4 dv[4];
+    {
+        const f4* src = reinterpret_cast<const f4*>(d.dict + (size_t)a * 64 + lg * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dv[i] = src[i];
+    }
+    float xv[16];
+    if (p.x_f16) {
+        const u4* src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(d.x) + f0);
+        const u4 h0 = src[0], h1 = src[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[2 * i] = csdr::h2f(h0[i] & 0xFFFFu);
+            xv[2 * i + 1] = csdr::h2f(h0[i] >> 16);
+            xv[8 + 2 * i] = csdr::h2f(h1[i] & 0xFFFFu);
+            xv[9 + 2 * i] = csdr::h2f(h1[i] >> 16);
+        }
+    } else {
+        const f4* src = reinterpret_cast<const f4*>(static_cast<const float*>(d.x) + f0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f4 v = src[i];
+            xv[4 * i] = v.x;
+            xv[4 * i + 1] = v.y;
+            xv[4 * i + 2] = v.z;
+            xv[4 * i + 3] = v.w;
+        }
+    }
+    const int C = d.C_full + d.Ce;
+    float inv = 1.0f;
+    if constexpr (XOP == CSDR_XOP_RMSNORM) {
+        // 1 / rms over all C features (x ops take fp32 x)
+        __shared__ float red[NT / 64];
+        const float* xf = static_cast<const float*>(d.x);
+        float ss = 0.f;
+        for (int j0 = 0; j0 < C; j0 += NT * kStageBatch) {
+            float t[kStageBatch];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) t[j] = xf[min(j0 + j * NT + tid, C - 1)];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j)
+                if (j0 + j * NT + tid < C) ss = fmaf(t[j], t[j], ss);
+        }
+        ss = wg_sum<NT>(ss, red);
+        inv = 1.0f / sqrtf(ss / (float)C + p.eps);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xv[i] = xv[i] * inv * p.nw[f0 + i];
+    } else if constexpr (XOP == CSDR_XOP_SILU_MUL) {
+        const float* x2 = static_cast<const float*>(d.x2) + f0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            xv[i] = (xv[i] * (1.0f / (1.0f + expf(-xv[i])))) * x2[i];
+    }
+    if (XOP != CSDR_XOP_NONE && u == 0 && d.xe) {
+        // the transformed edge-strip inputs
+        for (int t = tid; t < d.Ce; t += NT) {
+            const int f = d.C_full + t;
+            float x = xload(d.x, p.x_f16, (size_t)f);
+            if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * inv * p.nw[f];
+            if constexpr (XOP == CSDR_XOP_SILU_MUL)
+                x = (x * (1.0f / (1.0f + expf(-x)))) * static_cast<const float*>(d.x2)[f];
+            d.xe[t] = x;
+        }
+    }
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[s >> 2][s & 3], xv[s], acc, 0, 0, 0);
+    const int bo = bg * 16 + li, ao = ag * kAtoms + wave * 16 + 4 * lg;
+    if (bo < d.NB) {
+        float* out = d.P + (size_t)bo * d.K + ao;
+        if (ao + 3 < d.K && (d.K & 3) == 0) {
+            *reinterpret_cast<f4*>(out) = acc;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (ao + v < d.K) out[v] = acc[v];
+        }
+    }
+}
+
+template <int XOP>
+__global__ __launch_bounds__(kThreads) void dx1_mfma_kernel(Params p) {
+    dx1_body<XOP, kThreads>(p, (int)blockIdx.x);
+}
+
 // ---- RMSNorm statistics at M > 1: p.inv[g * 16 + m] = 1 / sqrt(mean_k x[k][m]^2 + eps) for
 // matrix g = blockIdx.y, column m = blockIdx.x (one workgroup per column, once per call, so
 // the dx workgroups read M values instead of all C x M inputs each).
@@ -816,10 +937,8 @@ __device__ __forceinline__ float sgam_at(const MatDesc& d, int i) {
 // kGWgsPerCu 1024-thread workgroups per CU = 8 waves per SIMD: at most 64 VGPRs
 // P4: K % 4 == 0, the P slice is staged as float4
 template <int SLOTS, int DEPTH, bool P4>
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(kGWgsPerCu * 4)))
-void gatherw_kernel(Params p) {
+__device__ __forceinline__ void gatherw_body(const Params& p, int wg) {
     extern __shared__ float smem[];
-    const int wg = (int)blockIdx.x;
     int g = 0;
     while (g + 1 < p.G && wg >= p.m[g + 1].g_base) ++g;
     const MatDesc& d = p.m[g];
@@ -984,6 +1103,12 @@ void gatherw_kernel(Params p) {
         }
         __hip_atomic_fetch_add(d.y + rbeg + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+template <int SLOTS, int DEPTH, bool P4>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(kGWgsPerCu * 4)))
+void gatherw_kernel(Params p) {
+    gatherw_body<SLOTS, DEPTH, P4>(p, (int)blockIdx.x);
 }
 
 // ---- kernel 2, 2 <= M <= 8: the same streaming gather with MC columns per code read
@@ -1853,6 +1978,14 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     // 2 <= M <= 16 with 64-long blocks everywhere: the thread-per-atom dx kernel
     bool dxm = M >= 2 && M <= kMaxXopM;
     for (int i = 0; i < n; ++i) dxm = dxm && segs[i] && segs[i]->tile_cols == 64;
+    // M == 1 with 64-long blocks, 16-byte aligned inputs and no attention x op: the
+    // matrix-core dx kernel
+    bool dx1 = M == 1 && xa.xop != CSDR_XOP_ATTN;
+    for (int i = 0; i < n && dx1; ++i) {
+        const uintptr_t al = reinterpret_cast<uintptr_t>(xs[i]) |
+                             (xa.xop == CSDR_XOP_SILU_MUL ? reinterpret_cast<uintptr_t>(xa.x2[i]) : 0);
+        dx1 = segs[i] && segs[i]->tile_cols == 64 && al % 16 == 0;
+    }
     const int dxm_mc = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
@@ -1897,7 +2030,10 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         d.Ce = (int)s->Ce;
         d.C_full = (int)s->C_full;
         d.PB = producer_blocks(M);
-        if (dxm) {
+        if (dx1) {
+            d.PB = 16;
+            d.dx_count = ((d.K + 63) / 64) * ((d.NB + 15) / 16);
+        } else if (dxm) {
             // about 256 workgroups per matrix: block columns per workgroup from the atom tiles
             const int na = (d.K + kDxmAtoms - 1) / kDxmAtoms;
             d.PB = std::max(1, std::min(8, d.NB * na / 256));
@@ -1967,7 +2103,14 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     if (lds_g > 160 * 1024 || lds_dx > 160 * 1024)
         return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: dictionary too large for LDS");
-    if ((phases & kPhaseDx) && dxm) {
+    if ((phases & kPhaseDx) && dx1) {
+        switch (p.xop) {
+            case CSDR_XOP_RMSNORM: dx1_mfma_kernel<CSDR_XOP_RMSNORM><<<ndx, kThreads, 0, st>>>(p); break;
+            case CSDR_XOP_SILU_MUL: dx1_mfma_kernel<CSDR_XOP_SILU_MUL><<<ndx, kThreads, 0, st>>>(p); break;
+            default: dx1_mfma_kernel<CSDR_XOP_NONE><<<ndx, kThreads, 0, st>>>(p); break;
+        }
+        CSDR_LAUNCH_CHECK("hsdb dx");
+    } else if ((phases & kPhaseDx) && dxm) {
         if (p.xop == CSDR_XOP_RMSNORM) {
             rms_inv_kernel<<<dim3(M, n), kThreads, 0, st>>>(p);
             CSDR_LAUNCH_CHECK("hsdb rms");

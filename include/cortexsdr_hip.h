@@ -134,7 +134,8 @@ CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* seg, const void* x, int x
  * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
  * column into the workspace, Y = 0 or bias) and a gather launch (Y += the coded rows gathered
  * from P; at M == 1 with 4, 8 or 16 slots two 1024-thread workgroups per CU stream the codes),
- * all fp32. M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch
+ * all fp32 (at M == 1 with 64-column blocks and 16-byte aligned x, the dx launch runs on
+ * the fp32 matrix cores). M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch
  * and a matrix-core launch that decodes 64-column tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
  * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
  * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace
