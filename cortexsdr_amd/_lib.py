@@ -284,3 +284,11 @@ SIGNATURES["csdr_attn_prefill"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.
                                            C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp,
                                            _vp])
 SIGNATURES["csdr_decoder_set_prefill_chunk"] = (C.c_int, [_vp, C.c_int])
+SIGNATURES["csdr_hsdr_source_format"] = (C.c_int, [C.c_char_p, C.c_int])
+SIGNATURES["csdr_hsdr_source_elements"] = (_sz, [C.c_int, _sz])
+SIGNATURES["csdr_hsdr_source_decode"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float, _vp,
+                                                 _vp])
+SIGNATURES["csdr_hsdr_compress_source"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float,
+                                                   C.c_uint32, C.c_uint32, C.c_uint16,
+                                                   C.c_uint16, C.c_uint16, C.c_uint8, C.c_uint8,
+                                                   C.c_uint8, C.c_float, _vp, _sz, _vp])

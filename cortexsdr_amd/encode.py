@@ -67,4 +67,43 @@ def compress(w: np.ndarray, tile_rows: int, tile_cols: int, n_atoms: int, n_stag
     return out.tobytes()
 
 
-__all__ = ["encode", "init_dictionary", "compress"]
+SOURCE_FORMATS = {"f32": 0, "f16": 1, "bf16": 2, "i8": 3, "q4_0": 4, "q8_0": 5, "q4_k": 6,
+                  "q5_k": 7, "q6_k": 8}
+
+
+def source_decode(src, fmt: str, scale: float = 1.0, zero_point: float = 0.0):
+    """dequantizeSegmentToFP32's decode of segment bytes (a device uint8 torch tensor) in the
+    compressor's element order: a device fp32 tensor."""
+    torch = _torch()
+    lib = _lib.load()
+    f = SOURCE_FORMATS[fmt]
+    n = int(lib.csdr_hsdr_source_elements(f, src.numel()))
+    out = torch.empty(max(n, 1), dtype=torch.float32, device=src.device)
+    _check(lib.csdr_hsdr_source_decode(src.data_ptr(), src.numel(), f, C.c_float(scale),
+                                       C.c_float(zero_point), out.data_ptr(),
+                                       torch.cuda.current_stream().cuda_stream))
+    return out[:n]
+
+
+def compress_source(src, fmt: str, rows: int, cols: int, tile_rows: int, tile_cols: int,
+                    n_atoms: int, n_stages: int, k_per_stage: int, ksvd_iters: int = 0,
+                    stage_decay: float = 0.5, scale: float = 1.0,
+                    zero_point: float = 0.0) -> bytes:
+    """compress of a quantized segment: the source bytes (device uint8 tensor) decoded on the
+    GPU, then compressed as compress()."""
+    torch = _torch()
+    lib = _lib.load()
+    n = lib.csdr_hsdr_compress_bytes(rows, cols, tile_rows, tile_cols, n_atoms, n_stages,
+                                     k_per_stage)
+    if n == 0:
+        raise ValueError("shape cannot be compressed with this config")
+    out = np.zeros(n, np.uint8)
+    _check(lib.csdr_hsdr_compress_source(
+        src.data_ptr(), src.numel(), SOURCE_FORMATS[fmt], C.c_float(scale),
+        C.c_float(zero_point), rows, cols, tile_rows, tile_cols, n_atoms, n_stages, k_per_stage,
+        ksvd_iters, C.c_float(stage_decay), out.ctypes.data, n,
+        torch.cuda.current_stream().cuda_stream))
+    return out.tobytes()
+
+
+__all__ = ["encode", "init_dictionary", "compress", "source_decode", "compress_source"]

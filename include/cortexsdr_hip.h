@@ -257,6 +257,39 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
                                 uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
                                 uint8_t* out, size_t out_bytes, void* hip_stream);
 
+/* The compressor's source decode, dequantizeSegmentToFP32 (HierarchicalSDRStrategy.cpp:
+ * 713-989), on the GPU: the bytes of a segment to the fp32 matrix the compressor tiles, the
+ * reference's values bit for bit. Formats (CSDR_SRC_*): f32, f16, bf16, int8 as
+ * (q - zero_point) * scale, and GGUF q4_0 / q8_0 (element 2j from the low nibble of byte j),
+ * q4_k / q5_k (element i from byte i/2, low nibble for even i) and q6_k in the compressor's
+ * element order, which for q4_k / q6_k differs from the engine's (csdr_q4k_linear,
+ * csdr_gguf_linear). csdr_hsdr_source_format maps a segment's data_format name and
+ * SegmentType (1 = WEIGHTS_FP32, 2 = WEIGHTS_FP16, 3 = WEIGHTS_INT8) to a format as the
+ * reference dispatches them, or -1; csdr_hsdr_source_elements gives the decoded value count
+ * (0 for a byte size that is not a whole number of blocks). src and out are device memory.
+ * csdr_hsdr_compress_source decodes on the GPU, then compresses as csdr_hsdr_compress (the
+ * decoded matrix is copied to the host for the dictionary initialisation): the reference's
+ * compress of a quantized segment. */
+#define CSDR_SRC_F32 0
+#define CSDR_SRC_F16 1
+#define CSDR_SRC_BF16 2
+#define CSDR_SRC_I8 3
+#define CSDR_SRC_Q4_0 4
+#define CSDR_SRC_Q8_0 5
+#define CSDR_SRC_Q4_K 6
+#define CSDR_SRC_Q5_K 7
+#define CSDR_SRC_Q6_K 8
+CSDR_API int csdr_hsdr_source_format(const char* data_format, int segment_type);
+CSDR_API size_t csdr_hsdr_source_elements(int format, size_t nbytes);
+CSDR_API int csdr_hsdr_source_decode(const void* src, size_t nbytes, int format, float scale,
+                                     float zero_point, float* out, void* hip_stream);
+CSDR_API int csdr_hsdr_compress_source(const void* src, size_t nbytes, int format, float scale,
+                                       float zero_point, uint32_t rows, uint32_t cols,
+                                       uint16_t tile_rows, uint16_t tile_cols, uint16_t n_atoms,
+                                       uint8_t n_stages, uint8_t k_per_stage, uint8_t ksvd_iters,
+                                       float stage_decay, uint8_t* out, size_t out_bytes,
+                                       void* hip_stream);
+
 /* ======================================================================
  * GGUF Q4_K dequant-matmul (engine path, no fp32 W materialised)
  * ==================================================================== */
