@@ -230,6 +230,34 @@ class DecoderConfig(C.Structure):
     ]
 
 
+SIGNATURES["csdr_dense_linear_ex"] = (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,
+                                              C.c_int, _vp])
+SIGNATURES["csdr_rope_kv_rows"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, C.c_float, _vp, _vp, C.c_int,
+                                           C.c_int, _vp])
+SIGNATURES["csdr_attn_prefill"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp,
+                                           _vp])
+SIGNATURES["csdr_decoder_set_prefill_chunk"] = (C.c_int, [_vp, C.c_int])
+SIGNATURES["csdr_hsdr_source_format"] = (C.c_int, [C.c_char_p, C.c_int])
+SIGNATURES["csdr_hsdr_source_elements"] = (_sz, [C.c_int, _sz])
+SIGNATURES["csdr_hsdr_source_decode"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float, _vp,
+                                                 _vp])
+SIGNATURES["csdr_hsdr_compress_source"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float,
+                                                   C.c_uint32, C.c_uint32, C.c_uint16,
+                                                   C.c_uint16, C.c_uint16, C.c_uint8, C.c_uint8,
+                                                   C.c_uint8, C.c_float, _vp, _sz, _vp])
+SIGNATURES["csdr_lazy_hsdr_load"] = (C.c_int, [_vp, _sz, C.c_int, _vp, _vp])
+SIGNATURES["csdr_lazy_hsdr_free"] = (C.c_int, [_vp])
+SIGNATURES["csdr_lazy_hsdr_info"] = (C.c_int, [_vp, _vp, _vp])
+SIGNATURES["csdr_lazy_hsdr_decode_rows"] = (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp])
+SIGNATURES["csdr_lazy_hsdr_workspace_bytes"] = (_sz, [_vp, C.c_int])
+SIGNATURES["csdr_lazy_hsdr_select"] = (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_float, C.c_float,
+                                               _vp, _vp, _vp, _vp, _vp, _sz, _vp])
+SIGNATURES["csdr_decoder_set_lazy_selection"] = (C.c_int, [_vp, _vp, C.c_float])
+SIGNATURES["cortex_inference_engine_set_lazy_hsdr_selection"] = (_ce, [_vp, C.c_int])
+
+
 def _hip_runtimes_mapped() -> set[str]:
     paths = set()
     try:
@@ -275,20 +303,3 @@ def check(rc: int) -> None:
 
 def exported_symbols() -> list[str]:
     return list(SIGNATURES)
-SIGNATURES["csdr_dense_linear_ex"] = (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,
-                                              C.c_int, _vp])
-SIGNATURES["csdr_rope_kv_rows"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
-                                           C.c_int, C.c_int, C.c_float, _vp, _vp, C.c_int,
-                                           C.c_int, _vp])
-SIGNATURES["csdr_attn_prefill"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
-                                           C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp,
-                                           _vp])
-SIGNATURES["csdr_decoder_set_prefill_chunk"] = (C.c_int, [_vp, C.c_int])
-SIGNATURES["csdr_hsdr_source_format"] = (C.c_int, [C.c_char_p, C.c_int])
-SIGNATURES["csdr_hsdr_source_elements"] = (_sz, [C.c_int, _sz])
-SIGNATURES["csdr_hsdr_source_decode"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float, _vp,
-                                                 _vp])
-SIGNATURES["csdr_hsdr_compress_source"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float,
-                                                   C.c_uint32, C.c_uint32, C.c_uint16,
-                                                   C.c_uint16, C.c_uint16, C.c_uint8, C.c_uint8,
-                                                   C.c_uint8, C.c_float, _vp, _sz, _vp])

@@ -147,6 +147,11 @@ struct csdr_decoder {
     int attn_splits = 1;
     int n_prompt = 0;
     std::vector<void*> allocs;
+    // lazy HSDR token choice (the text CLI's), when set
+    const csdr_lazy_hsdr* lazy = nullptr;
+    float lazy_penalty = 1.0f;
+    void* ws_lazy = nullptr;
+    size_t ws_lazy_bytes = 0;
     // batched prefill: tokens per sequence per pass, and its buffers (rows = B x tokens)
     int prefill_chunk = 512;
     int pf_rows = 0;
@@ -164,6 +169,8 @@ int dalloc(csdr_decoder* d, T** p, size_t count) {
     CSDR_HIP_CHECK(hipMalloc(&ptr, bytes));
     d->allocs.push_back(ptr);
     CSDR_HIP_CHECK(hipMemset(ptr, 0, bytes));
+    // the null stream's fill does not order the decoder's non-blocking stream
+    CSDR_HIP_CHECK(hipDeviceSynchronize());
     *p = static_cast<T*>(ptr);
     return CSDR_OK;
 }
@@ -402,6 +409,15 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
     }
     if (d->final_norm) RC(csdr_rms_norm(d->x, d->final_norm, B, H, c.rms_eps, d->h, st));
     else CSDR_HIP_CHECK(hipMemcpyAsync(d->h, d->x, (size_t)B * H * 4, hipMemcpyDeviceToDevice, st));
+    if (d->lazy) {
+        // the CLI's lazy HSDR scoring of the normed hidden state
+        RC(csdr_lazy_hsdr_select(d->lazy, d->h, B, d->repeated, temperature, d->lazy_penalty,
+                                 d->tok, d->pos, d->repeated, d->logits, d->ws_lazy,
+                                 d->ws_lazy_bytes, st));
+        record_kernel<<<1, 64, 0, st>>>(d->tok, d->pos, d->ring, cap, B);
+        CSDR_LAUNCH_CHECK("decoder record");
+        return CSDR_OK;
+    }
     sanitize_kernel<<<B, kSanThreads, 0, st>>>(d->h, H);
     CSDR_LAUNCH_CHECK("decoder sanitize");
     {
@@ -638,11 +654,12 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
     hipStream_t st = d->stream;
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
     const size_t cap = (size_t)c.max_ctx + 1;
-    CSDR_HIP_CHECK(hipMemset(d->pos, 0, 4));
-    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, (size_t)B * c.vocab));
-    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)B * cap * 4));
-    CSDR_HIP_CHECK(hipMemcpy2D(d->ring, cap * 4, prompt, (size_t)n_prompt * 4,
-                               (size_t)n_prompt * 4, B, hipMemcpyHostToDevice));
+    // resets on the decoder's stream (ordered before its steps)
+    CSDR_HIP_CHECK(hipMemsetAsync(d->pos, 0, 4, st));
+    CSDR_HIP_CHECK(hipMemsetAsync(d->repeated, 0, (size_t)B * c.vocab, st));
+    CSDR_HIP_CHECK(hipMemsetAsync(d->ring, 0xFF, (size_t)B * cap * 4, st));
+    CSDR_HIP_CHECK(hipMemcpy2DAsync(d->ring, cap * 4, prompt, (size_t)n_prompt * 4,
+                                    (size_t)n_prompt * 4, B, hipMemcpyHostToDevice, st));
     const int body = n_prompt - 1;
     if (d->prefill_chunk > 0 && body > 0) {
         // positions [0, body) in multi-token passes, then the last one as a decode step
@@ -657,6 +674,32 @@ CSDR_API int csdr_decoder_prefill(csdr_decoder* d, const int32_t* prompt, int n_
     CSDR_HIP_CHECK(hipStreamSynchronize(st));
     d->host_pos = n_prompt;
     d->n_prompt = n_prompt;
+    return CSDR_OK;
+}
+
+CSDR_API int csdr_decoder_set_lazy_selection(csdr_decoder* d, const csdr_lazy_hsdr* emb,
+                                             float penalty) {
+    if (!d) return set_error(CSDR_E_INVALID, "decoder_set_lazy_selection: null handle");
+    if (emb) {
+        uint32_t rows = 0, cols = 0;
+        RC(csdr_lazy_hsdr_info(emb, &rows, &cols));
+        if (rows != (uint32_t)d->cfg.vocab || cols != (uint32_t)d->cfg.hidden)
+            return set_error(CSDR_E_INVALID,
+                             "decoder_set_lazy_selection: embedding is " + std::to_string(rows) +
+                                 " x " + std::to_string(cols) + ", expected vocab x hidden " +
+                                 std::to_string(d->cfg.vocab) + " x " + std::to_string(d->cfg.hidden));
+        const size_t need = csdr_lazy_hsdr_workspace_bytes(emb, d->B);
+        if (need > d->ws_lazy_bytes) {
+            unsigned char* p = nullptr;
+            RC(dalloc(d, &p, need));
+            d->ws_lazy = p;
+            d->ws_lazy_bytes = need;
+        }
+    }
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    destroy_graphs(d);
+    d->lazy = emb;
+    d->lazy_penalty = penalty;
     return CSDR_OK;
 }
 
@@ -786,11 +829,13 @@ CSDR_API int csdr_decoder_set_position_batch(csdr_decoder* d, int position,
             return set_error(CSDR_E_INVALID, "decoder_set_position: token id out of range");
     const size_t cap = (size_t)d->cfg.max_ctx + 1;
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
-    CSDR_HIP_CHECK(hipMemcpy(d->pos, &position, 4, hipMemcpyHostToDevice));
-    CSDR_HIP_CHECK(hipMemset(d->repeated, 0, (size_t)d->B * d->cfg.vocab));
-    CSDR_HIP_CHECK(hipMemset(d->ring, 0xFF, (size_t)d->B * cap * 4));
-    CSDR_HIP_CHECK(hipMemcpy2D(d->ring + position, cap * 4, tokens, 4, 4, d->B,
-                               hipMemcpyHostToDevice));
+    hipStream_t st = d->stream;
+    CSDR_HIP_CHECK(hipMemcpyAsync(d->pos, &position, 4, hipMemcpyHostToDevice, st));
+    CSDR_HIP_CHECK(hipMemsetAsync(d->repeated, 0, (size_t)d->B * d->cfg.vocab, st));
+    CSDR_HIP_CHECK(hipMemsetAsync(d->ring, 0xFF, (size_t)d->B * cap * 4, st));
+    CSDR_HIP_CHECK(hipMemcpy2DAsync(d->ring + position, cap * 4, tokens, 4, 4, d->B,
+                                    hipMemcpyHostToDevice, st));
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
     d->host_pos = position;
     d->n_prompt = std::max(1, position);
     return CSDR_OK;

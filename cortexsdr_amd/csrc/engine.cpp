@@ -94,6 +94,10 @@ struct CortexInferenceEngine {
     std::string stats = "{}";
     csdr_decoder* dec = nullptr;
     int dec_ctx = 0;
+    std::string emb_name;           // the decoder's token embedding segment
+    int lazy_mode = 0;              // token choice by the CLI's lazy HSDR scoring (0 = off)
+    csdr_lazy_hsdr* lazy = nullptr;
+    int lazy_loaded_mode = 0;
 };
 
 namespace {
@@ -141,6 +145,9 @@ int grow(void** p, size_t* cap, size_t bytes) {
     *cap = 0;
     CSDR_HIP_CHECK(hipMalloc(p, std::max<size_t>(bytes, 256)));
     CSDR_HIP_CHECK(hipMemset(*p, 0, std::max<size_t>(bytes, 256)));
+    // the fill runs on the null stream, which does not order the engine's non-blocking
+    // stream: without this wait it can land after the next upload or product
+    CSDR_HIP_CHECK(hipDeviceSynchronize());
     *cap = bytes;
     return CSDR_OK;
 }
@@ -376,7 +383,40 @@ CortexError build_decoder(CortexInferenceEngine* e, int ctx) {
                                  embc == lmc ? nullptr : embc->seg);
     if (rc) return from_csdr(rc, "decoder output");
     e->dec_ctx = ctx;
+    e->emb_name = emb;
     return ok();
+}
+
+// The text CLI's lazy HSDR embedding of the decoder's token embedding (its raw strategy-5
+// stream, 1-row tiles), read with the mode's code reading; applied to the decoder, or removed.
+CortexError apply_lazy(CortexInferenceEngine* e) {
+    if (!e->lazy_mode) {
+        const int rc = csdr_decoder_set_lazy_selection(e->dec, nullptr, 0.0f);
+        return rc ? from_csdr(rc, "lazy selection") : ok();
+    }
+    if (!e->lazy || e->lazy_loaded_mode != e->lazy_mode) {
+        if (e->lazy) csdr_lazy_hsdr_free(e->lazy);
+        e->lazy = nullptr;
+        size_t idx;
+        if (!resolve(e, e->emb_name, &idx))
+            return fail(CORTEX_ERROR_INFERENCE, "Segment not found: " + e->emb_name);
+        csdr_segment_info info;
+        csdr_archive_info(e->ar, idx, &info);
+        if (info.strategy_id != 5)
+            return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
+                        "lazy HSDR selection: the token embedding is not HSDR-coded");
+        std::vector<uint8_t> bytes((size_t)info.compressed_size);
+        int rc = csdr_archive_read(e->ar, idx, bytes.data(), bytes.size(), nullptr);
+        if (rc) return from_csdr(rc, "lazy HSDR selection: read '" + e->emb_name + "'");
+        rc = csdr_lazy_hsdr_load(bytes.data(), bytes.size(),
+                                 e->lazy_mode == 2 ? CSDR_LAZY_UNPACK_CLI : CSDR_LAZY_UNPACK_PACKED,
+                                 e->st, &e->lazy);
+        if (rc) return from_csdr(rc, "lazy HSDR selection: '" + e->emb_name + "'");
+        e->lazy_loaded_mode = e->lazy_mode;
+    }
+    // select_next_token_from_lazy_hsdr's repeat penalty (cortexsdr_cli.cpp:723-725)
+    const int rc = csdr_decoder_set_lazy_selection(e->dec, e->lazy, 1.0f);
+    return rc ? from_csdr(rc, "lazy selection") : ok();
 }
 
 }  // namespace
@@ -416,6 +456,7 @@ CSDR_API CortexError cortex_inference_engine_free(CortexInferenceEngineHandle e)
     }
     (void)hipStreamSynchronize(e->st);
     if (e->dec) csdr_decoder_free(e->dec);
+    if (e->lazy) csdr_lazy_hsdr_free(e->lazy);
     for (auto& kv : e->cache) release(kv.second);
     if (e->ws) (void)hipFree(e->ws);
     if (e->xd) (void)hipFree(e->xd);
@@ -641,6 +682,15 @@ CSDR_API CortexError cortex_inference_engine_matmul_device(CortexInferenceEngine
     return ok();
 }
 
+CSDR_API CortexError cortex_inference_engine_set_lazy_hsdr_selection(CortexInferenceEngineHandle e,
+                                                                     int mode) {
+    CHECK_HANDLE(e);
+    if (mode < 0 || mode > 2)
+        return fail(CORTEX_ERROR_INVALID_ARGUMENT, "lazy HSDR selection mode must be 0, 1 or 2");
+    e->lazy_mode = mode;
+    return ok();
+}
+
 CSDR_API CortexError cortex_inference_engine_generate_text(CortexInferenceEngineHandle e,
                                                            const char* prompt, int max_new_tokens,
                                                            char** out_text) {
@@ -669,8 +719,13 @@ CSDR_API CortexError cortex_inference_engine_generate_text(CortexInferenceEngine
         CortexError r = build_decoder(e, ctx);
         if (r.code) return r;
     }
+    {
+        CortexError r = apply_lazy(e);
+        if (r.code) return r;
+    }
     const auto t1 = std::chrono::steady_clock::now();
-    // generate_text's sampling: temperature 0.8, repeat penalty 1.5 on generated tokens
+    // generate_text's sampling: temperature 0.8, repeat penalty 1.5 on generated tokens (the
+    // lazy HSDR choice applies its own penalty of 1.0)
     const float temperature = 0.8f, penalty = 1.5f;
     int rc = csdr_decoder_prefill(e->dec, ids.data(), (int)ids.size(), temperature, penalty);
     if (rc) return from_csdr(rc, "prefill");

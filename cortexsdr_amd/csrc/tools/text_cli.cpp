@@ -7,6 +7,10 @@
 // token ids (no tokenizer on this path) and the output is the generated ids.
 //
 //   cortexsdr_text_cli -p "1 2 3" -m 64 --profile out.json model.sdr
+//
+// --lazy-hsdr packed|cli chooses tokens as the reference CLI's native path does with an HSDR
+// token embedding (select_next_token_from_lazy_hsdr, cortexsdr_cli.cpp:687-732): the codes
+// read as written (packed) or with the CLI's own reading (cli, index = v >> 1, sign = v & 1).
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -19,10 +23,13 @@ namespace {
 
 void usage(const char* argv0) {
     std::printf(
-        "usage: %s [-p|--prompt \"ids\"] [-m|--max-length N] [--profile FILE] model.sdr\n"
+        "usage: %s [-p|--prompt \"ids\"] [-m|--max-length N] [--profile FILE]\n"
+        "          [--lazy-hsdr packed|cli] model.sdr\n"
         "  -p, --prompt      whitespace-separated token ids\n"
         "  -m, --max-length  tokens to generate (default 64)\n"
         "      --profile     write {duration_ms, tokens, tokens_per_sec, engine_stats} JSON\n"
+        "      --lazy-hsdr   choose tokens by lazy HSDR scoring of the token embedding\n"
+        "                    (codes read as written, or as the reference CLI reads them)\n"
         "  -v, --version     print the SDK version\n",
         argv0);
 }
@@ -37,6 +44,7 @@ int report(const CortexError& e, const char* what) {
 int main(int argc, char** argv) {
     std::string prompt, profile, model;
     int max_length = 64;
+    int lazy = 0;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "-h" || a == "--help") {
@@ -51,6 +59,13 @@ int main(int argc, char** argv) {
             max_length = std::atoi(argv[++i]);
         } else if (a == "--profile" && i + 1 < argc) {
             profile = argv[++i];
+        } else if (a == "--lazy-hsdr" && i + 1 < argc) {
+            const std::string m = argv[++i];
+            lazy = m == "packed" ? 1 : (m == "cli" ? 2 : -1);
+            if (lazy < 0) {
+                std::fprintf(stderr, "--lazy-hsdr takes packed or cli\n");
+                return 2;
+            }
         } else if (!a.empty() && a[0] != '-') {
             model = a;
         } else {
@@ -66,6 +81,14 @@ int main(int argc, char** argv) {
     CortexInferenceEngineHandle h = nullptr;
     CortexError e = cortex_inference_engine_create(model.c_str(), &h);
     if (e.code) return report(e, "create");
+    if (lazy) {
+        e = cortex_inference_engine_set_lazy_hsdr_selection(h, lazy);
+        if (e.code) {
+            report(e, "lazy-hsdr");
+            cortex_inference_engine_free(h);
+            return 1;
+        }
+    }
     std::printf("Generating response for: %s\n", prompt.c_str());
     const auto t0 = std::chrono::high_resolution_clock::now();
     char* text = nullptr;

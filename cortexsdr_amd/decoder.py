@@ -172,6 +172,14 @@ class Decoder:
         except Exception:
             pass
 
+    def set_lazy_selection(self, emb, penalty: float = 1.0) -> None:
+        """Choose tokens by the text CLI's lazy HSDR scoring against emb (a
+        LazyHsdrEmbedding of vocab x hidden, kept alive here), or by the lm_head scores
+        again when emb is None."""
+        self._lazy = emb
+        _lib.check(self._lib.csdr_decoder_set_lazy_selection(self._h, emb._h if emb else None,
+                                                             penalty))
+
     def set_prefill_chunk(self, tokens: int) -> None:
         """Prompt tokens per sequence in one multi-token prefill pass (0: one decode step
         per prompt position)."""

@@ -276,11 +276,16 @@ def vector_entry(name: str, v: np.ndarray, original_type: int = 14) -> SdrEntry:
 
 def decoder_entries(weights) -> list:
     """The segments of a DecoderWeights under GGUF tensor names (token_embd, output_norm,
-    blk.N.attn_q ... ffn_down), the names discover_native_llm_paths keys on
-    (api/cortex_sdk.cpp:477-545). Tied embeddings: token_embd holds the lm_head codes."""
+    output, blk.N.attn_q ... ffn_down), the names discover_native_llm_paths keys on
+    (api/cortex_sdk.cpp:477-545). Tied embeddings: token_embd holds the lm_head codes; a
+    separate embedding goes to token_embd and the lm_head to output."""
     names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
              "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}
-    ents = [hsdb_entry("token_embd.weight", weights.lm_head, original_type=13)]
+    if weights.embedding is None:
+        ents = [hsdb_entry("token_embd.weight", weights.lm_head, original_type=13)]
+    else:
+        ents = [hsdb_entry("token_embd.weight", weights.embedding, original_type=13),
+                hsdb_entry("output.weight", weights.lm_head, original_type=11)]
     if weights.final_norm is not None:
         ents.append(vector_entry("output_norm.weight", weights.final_norm))
     for l, L in enumerate(weights.layers):

@@ -207,3 +207,60 @@ def decompress(stream: bytes) -> np.ndarray:
         return seg.decompress().cpu().numpy()
     finally:
         seg.free()
+
+
+class LazyHsdrEmbedding:
+    """The text CLI's lazy HSDR embedding (csdr_lazy_hsdr_*): an HSDR stream with 1-row
+    tiles (vocabulary x width) kept as codes on the device; rows decoded and the vocabulary
+    scored from the codes. unpack: "packed" (packIndexSign's layout) or "cli" (the CLI's
+    index = v >> 1, sign = v & 1 reading)."""
+
+    def __init__(self, stream, unpack: str = "packed"):
+        torch = _torch()
+        lib = _lib.load()
+        b = np.frombuffer(bytes(stream), np.uint8)
+        h = C.c_void_p()
+        _check(lib.csdr_lazy_hsdr_load(b.ctypes.data, b.size, {"packed": 0, "cli": 1}[unpack],
+                                       torch.cuda.current_stream().cuda_stream, C.byref(h)))
+        self._h = h
+        r, c = C.c_uint32(), C.c_uint32()
+        _check(lib.csdr_lazy_hsdr_info(h, C.byref(r), C.byref(c)))
+        self.rows, self.cols = r.value, c.value
+
+    def decode_rows(self, ids):
+        """Rows of the given token ids (device int32 tensor or sequence), (n, width) fp32."""
+        torch = _torch()
+        ids = torch.as_tensor(ids, dtype=torch.int32, device="cuda").reshape(-1)
+        out = torch.empty((ids.numel(), self.cols), dtype=torch.float32, device="cuda")
+        _check(_lib.load().csdr_lazy_hsdr_decode_rows(self._h, ids.data_ptr(), 0, ids.numel(),
+                                                      out.data_ptr(),
+                                                      torch.cuda.current_stream().cuda_stream))
+        return out
+
+    def select(self, hidden, repeated=None, temperature: float = 0.8, penalty: float = 1.0):
+        """(tokens, raw scores) for hidden states (rows, width) on the device."""
+        torch = _torch()
+        lib = _lib.load()
+        hid = hidden.reshape(-1, self.cols).contiguous()
+        rows = hid.shape[0]
+        ws = torch.zeros(int(lib.csdr_lazy_hsdr_workspace_bytes(self._h, rows)),
+                         dtype=torch.uint8, device="cuda")
+        tok = torch.empty(rows, dtype=torch.int32, device="cuda")
+        scores = torch.empty((rows, self.rows), dtype=torch.float32, device="cuda")
+        rp = repeated.data_ptr() if repeated is not None else None
+        _check(lib.csdr_lazy_hsdr_select(self._h, hid.data_ptr(), rows, rp, C.c_float(temperature),
+                                         C.c_float(penalty), tok.data_ptr(), None, None,
+                                         scores.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         torch.cuda.current_stream().cuda_stream))
+        return tok, scores
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().csdr_lazy_hsdr_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -180,6 +180,16 @@ CSDR_API CortexError cortex_inference_engine_matmul_device(CortexInferenceEngine
                                                            const void* x, int x_dtype, int M,
                                                            float* y, void* hip_stream);
 
+/* Extension (no SDK counterpart): generate_text chooses tokens as the text CLI's native path
+ * does with an HSDR token embedding, select_next_token_from_lazy_hsdr
+ * (src/cortexsdr_cli.cpp:687-732: the decoder's output-normed hidden state scored against
+ * the embedding's codes, temperature 0.8, repeat penalty 1.0), instead of the SDK's lm_head
+ * choice. mode 0: off (default); 1: codes read as packIndexSign wrote them; 2: codes read
+ * as the CLI reads them (index = v >> 1, sign = v & 1, :545-546). The token embedding must
+ * be a strategy-5 HSDR segment with 1-row tiles. */
+CSDR_API CortexError cortex_inference_engine_set_lazy_hsdr_selection(CortexInferenceEngineHandle handle,
+                                                                     int mode);
+
 #ifdef __cplusplus
 }
 #endif

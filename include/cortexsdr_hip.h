@@ -466,6 +466,40 @@ CSDR_API int csdr_select_best(const float* logits, int n, const uint8_t* repeate
                               uint8_t* repeated_update, void* workspace, size_t workspace_bytes,
                               void* hip_stream);
 
+/* Lazy HSDR embedding of the text CLI (src/cortexsdr_cli.cpp): rows decoded and the
+ * vocabulary scored straight from the codes of an HSDR stream with 1-row tiles (vocabulary =
+ * n_tiles rows of tile_cols), no dense table. csdr_lazy_hsdr_load reads the stream as
+ * parse_hsdr_codes_for_embedding (:488-534; magic HSDR, version not checked), with code words
+ * read as packIndexSign wrote them (CSDR_LAZY_UNPACK_PACKED: bit 15 sign, bits 0-14 index,
+ * HierarchicalSDRStrategy.cpp:76-84) or as the CLI reads them (CSDR_LAZY_UNPACK_CLI: index =
+ * v >> 1, sign = v & 1, :545-546, :716-717, a compatibility reading); indices >= K are
+ * skipped. csdr_lazy_hsdr_decode_rows: hsdr_decode_row (:536-554) for n tokens (device ids
+ * rows_dev[i], or row_host when rows_dev is NULL; a device id outside the vocabulary gives a
+ * zero row), out n x cols. csdr_lazy_hsdr_select: select_next_token_from_lazy_hsdr
+ * (:687-732) for `rows` hidden states (rows x cols, device): atom . hidden summed in fp64 and
+ * rounded to float, per token the float sum over its slots in order of (gamma * sign) *
+ * (atom . hidden), times 1 / temperature when temperature > 0, minus `penalty` (the CLI:
+ * 1.0) where repeated[row][token] != 0 (repeated may be NULL); the first strictly largest
+ * score wins (-1 when none beats -infinity). tokens (device, rows) receive the choice;
+ * pos_dev (may be NULL) is incremented once, repeated_update (may be NULL) marks the chosen
+ * tokens, scores (may be NULL, rows x vocabulary) receives the sums before temperature and
+ * penalty. No counterpart for the CLI's host-side tokenizer. */
+typedef struct csdr_lazy_hsdr csdr_lazy_hsdr;
+#define CSDR_LAZY_UNPACK_PACKED 0
+#define CSDR_LAZY_UNPACK_CLI 1
+CSDR_API int csdr_lazy_hsdr_load(const void* stream, size_t nbytes, int unpack, void* hip_stream,
+                                 csdr_lazy_hsdr** out);
+CSDR_API int csdr_lazy_hsdr_free(csdr_lazy_hsdr* h);
+CSDR_API int csdr_lazy_hsdr_info(const csdr_lazy_hsdr* h, uint32_t* rows, uint32_t* cols);
+CSDR_API int csdr_lazy_hsdr_decode_rows(const csdr_lazy_hsdr* h, const int* rows_dev,
+                                        int row_host, int n, float* out, void* hip_stream);
+CSDR_API size_t csdr_lazy_hsdr_workspace_bytes(const csdr_lazy_hsdr* h, int rows);
+CSDR_API int csdr_lazy_hsdr_select(const csdr_lazy_hsdr* h, const float* hidden, int rows,
+                                   const uint8_t* repeated, float temperature, float penalty,
+                                   int* tokens, int* pos_dev, uint8_t* repeated_update,
+                                   float* scores, void* workspace, size_t workspace_bytes,
+                                   void* hip_stream);
+
 /* ======================================================================
  * Containers: the .sdr archive, HSDC codes-only streams, the HSDA shared-dictionary archive
  * (host parsing; loads go to the current device)
@@ -592,6 +626,14 @@ CSDR_API int csdr_decoder_set_output(csdr_decoder* dec, const csdr_hsdb* lm_head
  * (csdr_attn_prefill); the last prompt position runs the decode step, which selects. */
 CSDR_API int csdr_decoder_prefill(csdr_decoder* dec, const int32_t* prompt, int n_prompt,
                                   float temperature, float penalty);
+/* Token choice by the text CLI's lazy HSDR scoring (select_next_token_from_lazy_hsdr,
+ * cortexsdr_cli.cpp:687-732) instead of the lm_head scores: each head step scores the
+ * output-normed hidden state (not sanitized, as the CLI passes its decoder output) against
+ * emb (vocab x hidden, kept alive by the caller) with the step's temperature and `penalty`
+ * for generated tokens (the CLI uses 0.8 and 1.0); csdr_decoder_logits then returns the raw
+ * lazy scores. emb NULL restores the lm_head choice. */
+CSDR_API int csdr_decoder_set_lazy_selection(csdr_decoder* dec, const csdr_lazy_hsdr* emb,
+                                             float penalty);
 /* Tokens per sequence in one prefill pass (default 512); 0 runs every prompt position as a
  * decode step instead (the token-at-a-time form). Buffers for B x chunk rows and one dense
  * weight (the largest, F x H fp32) are allocated at the first prefill that needs them. */

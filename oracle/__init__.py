@@ -97,6 +97,10 @@ def orc():
         L.orc_hsdr_mp.argtypes = [_f32p, _sz, _sz, _f32p, _sz, _sz, _sz, _f32p, _u16p]
         L.orc_hsdr_mp.restype = None
         L.orc_select_best.restype = C.c_int
+        L.orc_lazy_hsdr_info.argtypes = [_u8p, _sz, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
+        L.orc_lazy_hsdr_decode_row.argtypes = [_u8p, _sz, C.c_int, C.c_uint32, _f32p]
+        L.orc_lazy_hsdr_select.argtypes = [_u8p, _sz, C.c_int, _f32p, C.c_void_p, C.c_float,
+                                           C.c_float, _f32p, C.POINTER(C.c_int)]
         _orc = L
     return _orc
 
@@ -320,6 +324,42 @@ def rope(x, heads, head_dim, theta=1e6, pos0=0):
     ntok = x.size // (heads * head_dim)
     orc().orc_rope(x.reshape(-1), ntok, heads, head_dim, theta, pos0)
     return x
+
+
+ORC_LAZY_PACKED, ORC_LAZY_CLI = 0, 1
+
+
+def lazy_hsdr_info(stream):
+    """(vocabulary rows, width) of an HSDR embedding as the text CLI's lazy parse reads it."""
+    b = _u8(stream)
+    r, c = C.c_uint32(), C.c_uint32()
+    _check(orc().orc_lazy_hsdr_info(b, b.size, C.byref(r), C.byref(c)), "lazy parse")
+    return r.value, c.value
+
+
+def lazy_hsdr_decode_row(stream, row: int, unpack: int = ORC_LAZY_PACKED) -> np.ndarray:
+    b = _u8(stream)
+    _, cols = lazy_hsdr_info(b)
+    out = np.zeros(cols, np.float32)
+    _check(orc().orc_lazy_hsdr_decode_row(b, b.size, unpack, row, out), "lazy decode row")
+    return out
+
+
+def lazy_hsdr_select(stream, hidden, repeated=None, temperature=0.8, penalty=1.0,
+                     unpack: int = ORC_LAZY_PACKED):
+    """(token, raw scores) of the CLI's lazy HSDR vocabulary scoring."""
+    b = _u8(stream)
+    rows, _ = lazy_hsdr_info(b)
+    h = np.ascontiguousarray(hidden, np.float32)
+    scores = np.zeros(rows, np.float32)
+    rp = None
+    if repeated is not None:
+        repeated = np.ascontiguousarray(repeated, np.uint8)
+        rp = repeated.ctypes.data_as(C.c_void_p)
+    tok = C.c_int()
+    _check(orc().orc_lazy_hsdr_select(b, b.size, unpack, h, rp, temperature, penalty, scores,
+                                      C.byref(tok)), "lazy select")
+    return tok.value, scores
 
 
 def select_best(logits, repeated=None, temperature=0.0, penalty=1.5) -> int:

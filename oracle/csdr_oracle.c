@@ -812,3 +812,130 @@ int orc_set_threads(int n) {
     if (n > 0) omp_set_num_threads(n);
     return prev;
 }
+
+/* ---------------------------------------------------------------- A14 lazy HSDR (CLI) */
+
+typedef struct {
+    uint32_t R, C, K, S, k;
+    size_t off_gamma, off_atoms, off_packed;
+} lazy_view;
+
+/* parse_hsdr_codes_for_embedding, cortexsdr_cli.cpp:488-534 */
+static int lazy_parse(const uint8_t* buf, size_t n, lazy_view* v) {
+    if (!buf || !v) return ORC_E_ARG;
+    if (n < 36) return ORC_E_TRUNCATED;
+    if (memcmp(buf, "HSDR", 4) != 0) return ORC_E_MAGIC;
+    if (rd16(buf + 20) != 1) return ORC_E_GEOMETRY; /* 1-row tiles only, :520 */
+    v->R = rd32(buf + 16);
+    v->C = rd16(buf + 22);
+    v->K = rd16(buf + 24);
+    v->S = buf[26];
+    v->k = buf[27];
+    v->off_gamma = 36;
+    v->off_atoms = v->off_gamma + 4u * v->S;
+    v->off_packed = v->off_atoms + 4u * (size_t)v->K * v->C;
+    if (v->off_packed + 2u * (size_t)v->R * v->S * v->k > n) return ORC_E_TRUNCATED;
+    return ORC_OK;
+}
+
+static void lazy_code(uint16_t pk, int unpack, uint32_t* idx, float* sgn) {
+    if (unpack == ORC_LAZY_CLI) { /* :545-546, :716-717 */
+        *idx = pk >> 1;
+        *sgn = (pk & 1u) ? -1.0f : 1.0f;
+    } else { /* HierarchicalSDRStrategy.cpp:81-84 */
+        *idx = pk & 0x7FFFu;
+        *sgn = (pk & 0x8000u) ? -1.0f : 1.0f;
+    }
+}
+
+int orc_lazy_hsdr_info(const uint8_t* buf, size_t n, uint32_t* rows, uint32_t* cols) {
+    lazy_view v;
+    int rc = lazy_parse(buf, n, &v);
+    if (rc) return rc;
+    if (rows) *rows = v.R;
+    if (cols) *cols = v.C;
+    return ORC_OK;
+}
+
+int orc_lazy_hsdr_decode_row(const uint8_t* buf, size_t n, int unpack, uint32_t row, float* out) {
+    /* hsdr_decode_row, cortexsdr_cli.cpp:536-554 */
+    lazy_view v;
+    int rc = lazy_parse(buf, n, &v);
+    if (rc) return rc;
+    if (row >= v.R || !out) return ORC_E_ARG;
+    for (uint32_t c = 0; c < v.C; ++c) out[c] = 0.0f;
+    const size_t slots = (size_t)v.S * v.k;
+    for (uint32_t l = 0; l < v.S; ++l) {
+        float gamma;
+        memcpy(&gamma, buf + v.off_gamma + 4u * l, 4);
+        for (uint32_t b = 0; b < v.k; ++b) {
+            uint32_t idx;
+            float sgn;
+            lazy_code(rd16(buf + v.off_packed + 2u * ((size_t)row * slots + (size_t)l * v.k + b)),
+                      unpack, &idx, &sgn);
+            if (idx >= v.K) continue;
+            const float scale = gamma * sgn;
+            for (uint32_t c = 0; c < v.C; ++c) {
+                float a;
+                memcpy(&a, buf + v.off_atoms + 4u * ((size_t)idx * v.C + c), 4);
+                out[c] += scale * a;
+            }
+        }
+    }
+    return ORC_OK;
+}
+
+int orc_lazy_hsdr_select(const uint8_t* buf, size_t n, int unpack, const float* hidden,
+                         const uint8_t* repeated, float temperature, float penalty,
+                         float* scores, int* token) {
+    /* select_next_token_from_lazy_hsdr, cortexsdr_cli.cpp:687-732 */
+    lazy_view v;
+    int rc = lazy_parse(buf, n, &v);
+    if (rc) return rc;
+    if (!hidden || !token) return ORC_E_ARG;
+    float* ah = (float*)malloc(((size_t)v.K + 1) * 4);
+    float* gam = (float*)malloc(((size_t)v.S + 1) * 4);
+    if (!ah || !gam) {
+        free(ah);
+        free(gam);
+        return ORC_E_ARG;
+    }
+    memcpy(gam, buf + v.off_gamma, 4u * v.S);
+    for (uint32_t a = 0; a < v.K; ++a) {
+        double s = 0.0;
+        for (uint32_t c = 0; c < v.C; ++c) {
+            float x;
+            memcpy(&x, buf + v.off_atoms + 4u * ((size_t)a * v.C + c), 4);
+            s += (double)x * hidden[c];
+        }
+        ah[a] = (float)s;
+    }
+    const float temp_scale = temperature > 0.0f ? (1.0f / temperature) : 1.0f;
+    const size_t slots = (size_t)v.S * v.k;
+    int best = -1;
+    float best_score = -INFINITY;
+    for (uint32_t tok = 0; tok < v.R; ++tok) {
+        float score = 0.0f;
+        for (uint32_t l = 0; l < v.S; ++l) {
+            for (uint32_t b = 0; b < v.k; ++b) {
+                uint32_t idx;
+                float sgn;
+                lazy_code(rd16(buf + v.off_packed + 2u * ((size_t)tok * slots + (size_t)l * v.k + b)),
+                          unpack, &idx, &sgn);
+                if (idx >= v.K) continue;
+                score += gam[l] * sgn * ah[idx];
+            }
+        }
+        if (scores) scores[tok] = score;
+        score *= temp_scale;
+        if (repeated && repeated[tok]) score -= penalty;
+        if (score > best_score) {
+            best_score = score;
+            best = (int)tok;
+        }
+    }
+    free(ah);
+    free(gam);
+    *token = best;
+    return ORC_OK;
+}

@@ -151,6 +151,30 @@ int orc_select_best(const float* logits, size_t n, const uint8_t* repeated, floa
 void orc_hsdr_mp(const float* tiles, size_t n_tiles, size_t C, const float* D, size_t K,
                  size_t S, size_t k, const float* gamma, uint16_t* codes);
 
+/* ---- A14: the text CLI's lazy HSDR embedding (cortexsdr_cli.cpp:488-554, 687-732).
+ * The stream is read as parse_hsdr_codes_for_embedding does (:488-534): the 36-byte HSDR
+ * header (magic "HSDR", version not checked), 1-row tiles only, vocabulary R = n_tiles,
+ * width C = tile_cols, then stage scales, atoms (K x C), packed codes (R x S*k u16); a stream
+ * shorter than that is ORC_E_TRUNCATED (the CLI reads past it). unpack: ORC_LAZY_PACKED
+ * reads codes as packIndexSign wrote them (bit 15 sign, bits 0-14 index,
+ * HierarchicalSDRStrategy.cpp:76-84); ORC_LAZY_CLI as the CLI reads them (index = v >> 1,
+ * sign = v & 1, :545-546, :716-717). Indices >= K are skipped (:547, :718).
+ * decode_row: hsdr_decode_row (:536-554), out[c] += (gamma_l * sign) * atom[c] in float, slot
+ * order. select: select_next_token_from_lazy_hsdr (:687-732): ah[a] = float(sum over c of
+ * double(atom[a][c]) * hidden[c], c ascending); score = sum over the slots in order of
+ * (gamma_l * sign) * ah[idx] in float, times 1 / temperature when temperature > 0, minus
+ * penalty (1.0 in the CLI) when repeated[token] != 0 (repeated may be NULL); the first token
+ * with a strictly larger score wins (*token = -1 when none beats -infinity). scores (may be NULL)
+ * receives the sums before temperature and penalty. Evaluated in ISO order without
+ * contraction (the CLI's -ffast-math build may fuse or reorder, changing last bits). */
+#define ORC_LAZY_PACKED 0
+#define ORC_LAZY_CLI 1
+int orc_lazy_hsdr_info(const uint8_t* buf, size_t n, uint32_t* rows, uint32_t* cols);
+int orc_lazy_hsdr_decode_row(const uint8_t* buf, size_t n, int unpack, uint32_t row, float* out);
+int orc_lazy_hsdr_select(const uint8_t* buf, size_t n, int unpack, const float* hidden,
+                         const uint8_t* repeated, float temperature, float penalty,
+                         float* scores, int* token);
+
 #ifdef __cplusplus
 }
 #endif
