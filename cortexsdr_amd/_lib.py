@@ -256,6 +256,10 @@ SIGNATURES["csdr_lazy_hsdr_select"] = (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_flo
                                                _vp, _vp, _vp, _vp, _vp, _sz, _vp])
 SIGNATURES["csdr_decoder_set_lazy_selection"] = (C.c_int, [_vp, _vp, C.c_float])
 SIGNATURES["cortex_inference_engine_set_lazy_hsdr_selection"] = (_ce, [_vp, C.c_int])
+SIGNATURES["csdr_hsda_build"] = (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_uint16,
+                                         C.c_uint16, C.c_uint16, C.c_uint8, C.c_uint8, C.c_uint8,
+                                         C.c_float, C.c_uint32, _vp, _vp, _vp, _vp])
+SIGNATURES["csdr_free_buffer"] = (None, [_vp])
 
 
 def _hip_runtimes_mapped() -> set[str]:

@@ -26,6 +26,7 @@
 #include <cstring>
 #include <random>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "common.hpp"
@@ -533,6 +534,125 @@ void put(std::vector<uint8_t>& out, const T& v) {
     out.insert(out.end(), p, p + sizeof(T));
 }
 
+// fitHierarchicalKSVD (HierarchicalSDRStrategy.cpp:494-607) over host tiles (n x tile_dim):
+// the dictionary initialisation on the host from the fit's generator (mt19937(0xC0DE), :513),
+// matching pursuit on the GPU, then ksvd_iters atom-update passes each followed by matching
+// pursuit again (:570-573); D (K x tile_dim, non-finite values zeroed as :592-601) and, when
+// codes is not null, the final codes.
+int fit_tiles(const std::vector<float>& tiles, uint32_t n_tiles, uint32_t tile_dim, uint16_t K,
+              uint8_t S, uint8_t k, uint8_t ksvd_iters, const std::vector<float>& gamma,
+              std::vector<float>& D, std::vector<uint16_t>* codes_out, hipStream_t st) {
+    Geometry g{};
+    g.n_tiles = n_tiles;
+    g.tile_dim = tile_dim;
+    g.K = K;
+    g.S = S;
+    g.k = k;
+    if (ksvd_iters != 0 && tile_dim > 32768)
+        return set_error(CSDR_E_UNSUPPORTED,
+                         "hsdr_compress: K-SVD refinement takes tiles of at most 32768 values");
+    int rc = check_mp_shape(n_tiles, (int)tile_dim, K, S, k);
+    if (rc != CSDR_OK) return rc;
+    D.assign((size_t)K * tile_dim, 0.0f);
+    std::mt19937 rng(0xC0DE);  // the fit's generator (:513), through init and every pass
+    csdr::hsdr_init_dictionary(tiles.data(), n_tiles, tile_dim, K, (uint32_t)S * k, D.data(),
+                               &rng);
+    const size_t ncodes = (size_t)n_tiles * S * k;
+    DevBuf d_tiles, d_D, d_codes;
+    CSDR_HIP_CHECK(hipMalloc(&d_tiles.p, std::max<size_t>(tiles.size(), 1) * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_D.p, D.size() * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_codes.p, std::max<size_t>(ncodes * 2, 2)));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_tiles.p, tiles.data(), tiles.size() * 4,
+                                  hipMemcpyHostToDevice, st));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_D.p, D.data(), D.size() * 4, hipMemcpyHostToDevice, st));
+    rc = launch_mp(d_tiles.f(), n_tiles, (int)tile_dim, d_D.f(), K, S, k, gamma.data(),
+                   d_codes.u16(), st);
+    if (rc != CSDR_OK) return rc;
+    if (ksvd_iters) {
+        Refine rf;
+        rc = rf.init(g, tiles, st);
+        if (rc != CSDR_OK) return rc;
+        for (int it = 0; it < ksvd_iters; ++it) {  // atom update, then encode again (:570-573)
+            rc = rf.pass(g, tiles, gamma, d_tiles.f(), d_D.f(), d_codes.u16(), rng, st);
+            if (rc != CSDR_OK) return rc;
+            rc = launch_mp(d_tiles.f(), n_tiles, (int)tile_dim, d_D.f(), K, S, k, gamma.data(),
+                           d_codes.u16(), st);
+            if (rc != CSDR_OK) return rc;
+        }
+        CSDR_HIP_CHECK(hipMemcpyAsync(D.data(), d_D.p, D.size() * 4, hipMemcpyDeviceToHost, st));
+    }
+    if (codes_out) {
+        codes_out->resize(ncodes);
+        CSDR_HIP_CHECK(hipMemcpyAsync(codes_out->data(), d_codes.p, ncodes * 2,
+                                      hipMemcpyDeviceToHost, st));
+    }
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
+    for (float& x : D)  // the fit's final sanitisation (:592-601)
+        if (!std::isfinite(x)) x = 0.0f;
+    return CSDR_OK;
+}
+
+// Matching pursuit of host tiles against a fixed dictionary (encodeAllTilesAgainstDictionary,
+// the encode of compressFP32WithExternalDictionary :1690-1754).
+int encode_tiles(const float* tiles, uint32_t n_tiles, uint32_t tile_dim, const std::vector<float>& D,
+                 uint16_t K, uint8_t S, uint8_t k, const std::vector<float>& gamma,
+                 std::vector<uint16_t>& codes, hipStream_t st) {
+    int rc = check_mp_shape(n_tiles, (int)tile_dim, K, S, k);
+    if (rc != CSDR_OK) return rc;
+    const size_t ncodes = (size_t)n_tiles * S * k;
+    DevBuf d_tiles, d_D, d_codes;
+    CSDR_HIP_CHECK(hipMalloc(&d_tiles.p, std::max<size_t>((size_t)n_tiles * tile_dim, 1) * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_D.p, D.size() * 4));
+    CSDR_HIP_CHECK(hipMalloc(&d_codes.p, std::max<size_t>(ncodes * 2, 2)));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_tiles.p, tiles, (size_t)n_tiles * tile_dim * 4,
+                                  hipMemcpyHostToDevice, st));
+    CSDR_HIP_CHECK(hipMemcpyAsync(d_D.p, D.data(), D.size() * 4, hipMemcpyHostToDevice, st));
+    rc = launch_mp(d_tiles.f(), n_tiles, (int)tile_dim, d_D.f(), K, S, k, gamma.data(),
+                   d_codes.u16(), st);
+    if (rc != CSDR_OK) return rc;
+    codes.resize(ncodes);
+    CSDR_HIP_CHECK(hipMemcpyAsync(codes.data(), d_codes.p, ncodes * 2, hipMemcpyDeviceToHost, st));
+    CSDR_HIP_CHECK(hipStreamSynchronize(st));
+    return CSDR_OK;
+}
+
+// Tiles of an R x C matrix in row-major tile order (extractTiles :94-116), of its aligned
+// top-left block.
+std::vector<float> extract_tiles(const float* w, uint32_t R, uint32_t C, uint32_t tr,
+                                 uint32_t tc) {
+    const uint32_t nrt = R / tr, nct = C / tc;
+    std::vector<float> tiles((size_t)nrt * nct * tr * tc);
+    for (uint32_t br = 0; br < nrt; ++br)
+        for (uint32_t bc = 0; bc < nct; ++bc) {
+            float* dst = tiles.data() + (size_t)(br * nct + bc) * tr * tc;
+            for (uint32_t r = 0; r < tr; ++r)
+                std::memcpy(dst + (size_t)r * tc, w + (size_t)(br * tr + r) * C + (size_t)bc * tc,
+                            sizeof(float) * tc);
+        }
+    return tiles;
+}
+
+// compressGroupedSegments' bucket key and its hash (HierarchicalSDRStrategy.cpp:2088-2120),
+// so that the buckets come out of the same std::unordered_map in the same order.
+struct GroupKey {
+    uint16_t tile_rows, tile_cols, n_atoms;
+    uint8_t n_stages, k;
+    float decay;
+    bool operator==(const GroupKey& o) const {
+        return tile_rows == o.tile_rows && tile_cols == o.tile_cols && n_atoms == o.n_atoms &&
+               n_stages == o.n_stages && k == o.k && decay == o.decay;
+    }
+};
+struct GroupKeyHash {
+    size_t operator()(const GroupKey& g) const {
+        size_t h = std::hash<uint32_t>{}(((uint32_t)g.tile_rows << 16) | g.tile_cols);
+        h ^= std::hash<uint32_t>{}(((uint32_t)g.n_atoms << 16) | ((uint32_t)g.n_stages << 8) | g.k) +
+             0x9e3779b9 + (h << 6) + (h >> 2);
+        h ^= std::hash<float>{}(g.decay) + 0x9e3779b9 + (h << 6) + (h >> 2);
+        return h;
+    }
+};
+
 }  // namespace
 
 extern "C" {
@@ -582,57 +702,15 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
     if (ksvd_iters != 0 && g.tile_dim > 32768)
         return set_error(CSDR_E_UNSUPPORTED,
                          "hsdr_compress: K-SVD refinement takes tiles of at most 32768 values");
-    rc = check_mp_shape(g.n_tiles, (int)g.tile_dim, g.K, g.S, g.k);
-    if (rc != CSDR_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
-
     // tiles in row-major tile order (extractTiles :94-116) of the aligned block
-    const uint32_t nrt = g.R_full / g.tr, nct = g.C_full / g.tc;
-    std::vector<float> tiles((size_t)g.n_tiles * g.tile_dim);
-    for (uint32_t br = 0; br < nrt; ++br)
-        for (uint32_t bc = 0; bc < nct; ++bc) {
-            float* dst = tiles.data() + (size_t)(br * nct + bc) * g.tile_dim;
-            for (uint32_t r = 0; r < g.tr; ++r)
-                std::memcpy(dst + (size_t)r * g.tc,
-                            w + (size_t)(br * g.tr + r) * g.C + (size_t)bc * g.tc,
-                            sizeof(float) * g.tc);
-        }
+    std::vector<float> tiles = extract_tiles(w, g.R_full, g.C, g.tr, g.tc);
+    tiles.resize((size_t)g.n_tiles * g.tile_dim);
     std::vector<float> gamma(g.S), D;
     for (uint32_t l = 0; l < g.S; ++l) gamma[l] = std::pow(stage_decay, (float)l);
-    D.assign((size_t)g.K * g.tile_dim, 0.0f);
-    std::mt19937 rng(0xC0DE);  // the fit's generator (:513), through init and every pass
-    csdr::hsdr_init_dictionary(tiles.data(), g.n_tiles, g.tile_dim, g.K, (uint32_t)g.S * g.k,
-                               D.data(), &rng);
-
-    const size_t slots = (size_t)g.S * g.k, ncodes = (size_t)g.n_tiles * slots;
-    std::vector<uint16_t> codes(ncodes);
-    DevBuf d_tiles, d_D, d_codes;
-    CSDR_HIP_CHECK(hipMalloc(&d_tiles.p, tiles.size() * 4));
-    CSDR_HIP_CHECK(hipMalloc(&d_D.p, D.size() * 4));
-    CSDR_HIP_CHECK(hipMalloc(&d_codes.p, std::max<size_t>(ncodes * 2, 2)));
-    CSDR_HIP_CHECK(hipMemcpyAsync(d_tiles.p, tiles.data(), tiles.size() * 4,
-                                  hipMemcpyHostToDevice, st));
-    CSDR_HIP_CHECK(hipMemcpyAsync(d_D.p, D.data(), D.size() * 4, hipMemcpyHostToDevice, st));
-    rc = launch_mp(d_tiles.f(), g.n_tiles, (int)g.tile_dim, d_D.f(), g.K, g.S, g.k,
-                   gamma.data(), d_codes.u16(), st);
+    std::vector<uint16_t> codes;
+    rc = fit_tiles(tiles, g.n_tiles, g.tile_dim, g.K, g.S, g.k, ksvd_iters, gamma, D, &codes, st);
     if (rc != CSDR_OK) return rc;
-    if (ksvd_iters) {
-        Refine rf;
-        rc = rf.init(g, tiles, st);
-        if (rc != CSDR_OK) return rc;
-        for (int it = 0; it < ksvd_iters; ++it) {  // atom update, then encode again (:570-573)
-            rc = rf.pass(g, tiles, gamma, d_tiles.f(), d_D.f(), d_codes.u16(), rng, st);
-            if (rc != CSDR_OK) return rc;
-            rc = launch_mp(d_tiles.f(), g.n_tiles, (int)g.tile_dim, d_D.f(), g.K, g.S, g.k,
-                           gamma.data(), d_codes.u16(), st);
-            if (rc != CSDR_OK) return rc;
-        }
-        CSDR_HIP_CHECK(hipMemcpyAsync(D.data(), d_D.p, D.size() * 4, hipMemcpyDeviceToHost, st));
-    }
-    CSDR_HIP_CHECK(hipMemcpyAsync(codes.data(), d_codes.p, ncodes * 2, hipMemcpyDeviceToHost, st));
-    CSDR_HIP_CHECK(hipStreamSynchronize(st));
-    for (float& x : D)  // the fit's final sanitisation (:592-601)
-        if (!std::isfinite(x)) x = 0.0f;
 
     // serialisation (:1197-1237): header, stage scales, D, packed codes, edge strips
     std::vector<uint8_t> s;
@@ -659,5 +737,198 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
     std::memcpy(out, s.data(), s.size());
     return CSDR_OK;
 }
+
+CSDR_API int csdr_hsda_build(int n, const char* const* names, const float* const* w,
+                             const uint32_t* rows, const uint32_t* cols,
+                             const uint8_t* original_types, uint16_t tile_rows,
+                             uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages,
+                             uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
+                             uint32_t max_tiles_for_fit, uint8_t** out, size_t* out_size,
+                             uint8_t* skipped, void* hip_stream) {
+    if (n <= 0 || !names || !w || !rows || !cols || !out || !out_size)
+        return set_error(CSDR_E_INVALID, "hsda_build: bad argument");
+    if (tile_rows == 0 || tile_cols == 0 || n_atoms == 0 || n_stages == 0 || k_per_stage == 0)
+        return set_error(CSDR_E_INVALID, "hsda_build: bad config");
+    *out = nullptr;
+    *out_size = 0;
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    try {
+        // configFor per segment (1-row tiles widen to the row), suitability (:2147-2190:
+        // shape divisible by the tile; the caller's matrices are fp32), buckets by config
+        std::vector<GroupKey> keys(n);
+        std::unordered_map<GroupKey, std::vector<size_t>, GroupKeyHash> buckets;
+        std::vector<uint8_t> skip(n, 0);
+        for (int i = 0; i < n; ++i) {
+            if (!names[i] || !w[i]) return set_error(CSDR_E_INVALID, "hsda_build: null entry");
+            GroupKey key{tile_rows, (tile_rows == 1 && cols[i] <= 0xFFFFu) ? (uint16_t)cols[i]
+                                                                          : tile_cols,
+                         n_atoms, n_stages, k_per_stage, stage_decay};
+            keys[i] = key;
+            if (rows[i] == 0 || cols[i] == 0 || rows[i] % key.tile_rows ||
+                cols[i] % key.tile_cols) {
+                skip[i] = 1;
+                continue;
+            }
+            buckets[key].push_back((size_t)i);
+        }
+        std::vector<float> gamma(n_stages);
+        for (uint32_t l = 0; l < n_stages; ++l) gamma[l] = std::pow(stage_decay, (float)l);
+        struct Dict {
+            GroupKey key;
+            std::vector<float> atoms;
+        };
+        struct Entry {
+            size_t seg, dict;
+            std::vector<uint16_t> codes;
+            uint32_t n_tiles;
+        };
+        std::vector<Dict> dicts;
+        std::vector<Entry> entries;
+        for (auto& kv : buckets) {
+            const GroupKey& key = kv.first;
+            const uint32_t tr = key.tile_rows, tc = key.tile_cols, tile_dim = tr * tc;
+            uint64_t total = 0;
+            for (size_t i : kv.second) total += (uint64_t)(rows[i] / tr) * (cols[i] / tc);
+            const uint32_t pooled_count = total > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)total;
+            const uint32_t cap = (max_tiles_for_fit > 0 && total > max_tiles_for_fit)
+                                     ? max_tiles_for_fit
+                                     : pooled_count;
+            const bool reservoir = cap < pooled_count;
+            std::vector<float> pool((size_t)cap * tile_dim);
+            std::mt19937 res_rng(0xC0DECAFEu ^ cap);  // :2277
+            uint64_t seen = 0;
+            uint32_t fill = 0;
+            std::vector<size_t> pooled_segs;
+            std::vector<std::vector<float>> seg_tiles;
+            for (size_t i : kv.second) {
+                // per-segment non-finite gate (:2324-2358): probe 1 in 256, then sanitise and
+                // skip the segment when more than 1e-3 of it is bad
+                std::vector<float> m(w[i], w[i] + (size_t)rows[i] * cols[i]);
+                bool any_bad = false;
+                for (size_t j = 0; j < m.size(); j += 256)
+                    if (!std::isfinite(m[j])) {
+                        any_bad = true;
+                        break;
+                    }
+                if (any_bad) {
+                    size_t bad = 0;
+                    for (float& v : m)
+                        if (!std::isfinite(v)) {
+                            v = 0.0f;
+                            ++bad;
+                        }
+                    if ((double)bad / std::max<size_t>(1, m.size()) > 1e-3) {
+                        skip[i] = 1;
+                        continue;
+                    }
+                }
+                std::vector<float> t = (tr == 1 && tc == cols[i])
+                                           ? std::move(m)
+                                           : extract_tiles(m.data(), rows[i], cols[i], tr, tc);
+                const uint32_t nt = (rows[i] / tr) * (cols[i] / tc);
+                for (uint32_t j = 0; j < nt; ++j) {
+                    const float* src = t.data() + (size_t)j * tile_dim;
+                    if (!reservoir || fill < cap) {
+                        std::memcpy(pool.data() + (size_t)fill * tile_dim, src, tile_dim * 4);
+                        ++fill;
+                    } else {
+                        std::uniform_int_distribution<uint64_t> dist(0, seen);
+                        const uint64_t r = dist(res_rng);
+                        if (r < cap) std::memcpy(pool.data() + r * tile_dim, src, tile_dim * 4);
+                    }
+                    ++seen;
+                }
+                pooled_segs.push_back(i);
+                seg_tiles.push_back(std::move(t));
+            }
+            pool.resize((size_t)fill * tile_dim);
+            for (float& v : pool)  // pool integrity (:2403-2419)
+                if (!std::isfinite(v)) v = 0.0f;
+            if (fill < key.n_atoms) {  // too small to fit the dictionary: the bucket is skipped
+                for (size_t i : pooled_segs) skip[i] = 1;
+                continue;
+            }
+            Dict d;
+            d.key = key;
+            int rc = fit_tiles(pool, fill, tile_dim, key.n_atoms, key.n_stages, key.k, ksvd_iters,
+                               gamma, d.atoms, nullptr, st);
+            if (rc != CSDR_OK) return rc;
+            const size_t di = dicts.size();
+            dicts.push_back(std::move(d));
+            for (size_t q = 0; q < pooled_segs.size(); ++q) {
+                const size_t i = pooled_segs[q];
+                Entry e;
+                e.seg = i;
+                e.dict = di;
+                e.n_tiles = (rows[i] / tr) * (cols[i] / tc);
+                rc = encode_tiles(seg_tiles[q].data(), e.n_tiles, tile_dim, dicts[di].atoms,
+                                  key.n_atoms, key.n_stages, key.k, gamma, e.codes, st);
+                if (rc != CSDR_OK) return rc;
+                std::vector<float>().swap(seg_tiles[q]);
+                entries.push_back(std::move(e));
+            }
+        }
+        // SharedDictArchive::writeToStream (:1967-2002)
+        std::vector<uint8_t> s;
+        s.insert(s.end(), {'H', 'S', 'D', 'A'});
+        put<uint32_t>(s, 1);
+        put<uint32_t>(s, (uint32_t)dicts.size());
+        put<uint32_t>(s, (uint32_t)entries.size());
+        for (const Dict& d : dicts) {
+            // the 20-byte HierarchicalSDRConfig (HierarchicalSDRStrategy.hpp:43-58); its two
+            // padding bytes (10-11) written as zeros
+            put<uint16_t>(s, d.key.tile_rows);
+            put<uint16_t>(s, d.key.tile_cols);
+            put<uint16_t>(s, d.key.n_atoms);
+            put<uint8_t>(s, d.key.n_stages);
+            put<uint8_t>(s, d.key.k);
+            put<uint8_t>(s, ksvd_iters);
+            put<uint8_t>(s, 0);  // reserved_pad
+            put<uint16_t>(s, 0);
+            put<float>(s, d.key.decay);
+            put<uint32_t>(s, max_tiles_for_fit);
+            put<uint32_t>(s, (uint32_t)gamma.size());
+            for (float x : gamma) put<float>(s, x);
+            put<uint32_t>(s, (uint32_t)d.atoms.size());
+            for (float x : d.atoms) put<float>(s, x);
+        }
+        for (const Entry& e : entries) {
+            const size_t i = e.seg;
+            const std::string name = names[i];
+            const GroupKey& key = dicts[e.dict].key;
+            put<uint32_t>(s, (uint32_t)name.size());
+            s.insert(s.end(), name.begin(), name.end());
+            put<uint32_t>(s, (uint32_t)e.dict);
+            put<uint64_t>(s, (uint64_t)rows[i] * cols[i] * 4);
+            put<uint8_t>(s, original_types ? original_types[i] : (uint8_t)1);
+            // compressFP32WithExternalDictionary's HSDC stream (:1732-1754): 32-byte header,
+            // packed codes
+            put<uint32_t>(s, (uint32_t)(32 + e.codes.size() * 2));
+            s.insert(s.end(), {'H', 'S', 'D', 'C'});
+            put<uint32_t>(s, 1);
+            put<uint32_t>(s, rows[i]);
+            put<uint32_t>(s, cols[i]);
+            put<uint32_t>(s, e.n_tiles);
+            put<uint16_t>(s, key.tile_rows);
+            put<uint16_t>(s, key.tile_cols);
+            put<uint16_t>(s, key.n_atoms);
+            put<uint8_t>(s, key.n_stages);
+            put<uint8_t>(s, key.k);
+            put<float>(s, key.decay);
+            for (uint16_t c : e.codes) put<uint16_t>(s, c);
+        }
+        uint8_t* buf = static_cast<uint8_t*>(std::malloc(std::max<size_t>(s.size(), 1)));
+        if (!buf) return set_error(CSDR_E_INVALID, "hsda_build: out of host memory");
+        std::memcpy(buf, s.data(), s.size());
+        *out = buf;
+        *out_size = s.size();
+        if (skipped) std::memcpy(skipped, skip.data(), skip.size());
+    } catch (const std::exception& ex) {
+        return set_error(CSDR_E_INVALID, std::string("hsda_build: ") + ex.what());
+    }
+    return CSDR_OK;
+}
+
+CSDR_API void csdr_free_buffer(void* p) { std::free(p); }
 
 }  // extern "C"

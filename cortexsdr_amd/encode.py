@@ -106,4 +106,34 @@ def compress_source(src, fmt: str, rows: int, cols: int, tile_rows: int, tile_co
     return out.tobytes()
 
 
-__all__ = ["encode", "init_dictionary", "compress", "source_decode", "compress_source"]
+def hsda_build(mats: dict, tile_rows: int, tile_cols: int, n_atoms: int, n_stages: int,
+               k_per_stage: int, ksvd_iters: int = 0, stage_decay: float = 0.5,
+               max_tiles_for_fit: int = 0, original_types=None):
+    """compressGroupedSegments + SharedDictArchive::writeToStream: {name: (R x C) fp32} ->
+    (HSDA archive bytes, names the pipeline skipped)."""
+    torch = _torch()
+    lib = _lib.load()
+    names = list(mats)
+    arrs = [np.ascontiguousarray(mats[n], np.float32) for n in names]
+    n = len(arrs)
+    nm = (C.c_char_p * n)(*[x.encode() for x in names])
+    ws = (C.c_void_p * n)(*[a.ctypes.data for a in arrs])
+    rows = (C.c_uint32 * n)(*[a.shape[0] for a in arrs])
+    cols = (C.c_uint32 * n)(*[a.shape[1] for a in arrs])
+    types = None
+    if original_types is not None:
+        types = (C.c_uint8 * n)(*original_types)
+    skipped = np.zeros(n, np.uint8)
+    out = C.POINTER(C.c_uint8)()
+    size = C.c_size_t()
+    _check(lib.csdr_hsda_build(n, nm, ws, rows, cols, types, tile_rows, tile_cols, n_atoms,
+                               n_stages, k_per_stage, ksvd_iters, C.c_float(stage_decay),
+                               max_tiles_for_fit, C.byref(out), C.byref(size),
+                               skipped.ctypes.data, torch.cuda.current_stream().cuda_stream))
+    data = bytes(C.string_at(out, size.value))
+    lib.csdr_free_buffer(out)
+    return data, [nme for nme, s in zip(names, skipped) if s]
+
+
+__all__ = ["encode", "init_dictionary", "compress", "source_decode", "compress_source",
+           "hsda_build"]

@@ -257,6 +257,28 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
                                 uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
                                 uint8_t* out, size_t out_bytes, void* hip_stream);
 
+/* Shared-dictionary compression of a group of fp32 matrices (host, row-major):
+ * compressGroupedSegments (HierarchicalSDRStrategy.cpp:2212-2502) written as
+ * SharedDictArchive::writeToStream (:1967-2002). Matrices are bucketed by their config (1-row
+ * tiles widen to each matrix's width; one dictionary per bucket, buckets in the order of the
+ * reference's std::unordered_map over the same key and hash); a matrix whose shape is not a
+ * whole number of tiles, or with more than 1e-3 non-finite values, is skipped (others are
+ * zeroed); each bucket's tiles are pooled, reservoir-sampled to max_tiles_for_fit when that
+ * is non-zero and smaller (mt19937(0xC0DECAFE ^ cap), :2277-2395), the dictionary fitted on
+ * the pool as csdr_hsdr_compress fits one matrix (ksvd_iters passes), and every matrix of
+ * the bucket encoded against it as an HSDC codes stream (compressFP32WithExternalDictionary,
+ * :1690-1754). The archive is returned in *out (malloc'd; release with csdr_free_buffer);
+ * skipped (may be NULL) receives one flag per matrix; original_types (may be NULL: 1,
+ * WEIGHTS_FP32) is stored per segment. The config's two padding bytes are written as zero. */
+CSDR_API int csdr_hsda_build(int n, const char* const* names, const float* const* w,
+                             const uint32_t* rows, const uint32_t* cols,
+                             const uint8_t* original_types, uint16_t tile_rows,
+                             uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages,
+                             uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
+                             uint32_t max_tiles_for_fit, uint8_t** out, size_t* out_size,
+                             uint8_t* skipped, void* hip_stream);
+CSDR_API void csdr_free_buffer(void* p);
+
 /* The compressor's source decode, dequantizeSegmentToFP32 (HierarchicalSDRStrategy.cpp:
  * 713-989), on the GPU: the bytes of a segment to the fp32 matrix the compressor tiles, the
  * reference's values bit for bit. Formats (CSDR_SRC_*): f32, f16, bf16, int8 as

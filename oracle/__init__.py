@@ -125,6 +125,12 @@ def ref():
                                      C.POINTER(C.c_uint32), C.c_uint32, C.c_uint16, C.c_uint8,
                                      C.c_uint8, C.c_uint8, C.c_float,
                                      C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]
+        L.ref_hsda_build_ex.argtypes = [C.c_uint32, C.POINTER(C.c_char_p),
+                                        C.POINTER(C.c_void_p), C.POINTER(C.c_uint32),
+                                        C.POINTER(C.c_uint32), C.c_uint16, C.c_uint16,
+                                        C.c_uint16, C.c_uint8, C.c_uint8, C.c_uint8, C.c_float,
+                                        C.c_uint32, C.c_void_p,
+                                        C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]
         L.ref_hsda_matmul.argtypes = [_u8p, _sz, C.c_char_p, _f32p, _sz, _f32p, _sz]
         L.ref_hsda_decompress.argtypes = [_u8p, _sz, C.c_char_p, _f32p, _sz]
         _ref = L
@@ -459,6 +465,30 @@ def ref_hsda_build(mats: dict, n_atoms, n_stages, k_per_stage, ksvd_iters=4,
     data = bytes(C.string_at(out, n.value))
     L.ref_free(out)
     return data
+
+
+def ref_hsda_build_ex(mats: dict, tile_rows, tile_cols, n_atoms, n_stages, k_per_stage,
+                      ksvd_iters, stage_decay=0.5, max_tiles_for_fit=0):
+    """{name: (R_i x C_i) fp32} -> (HSDA bytes, skipped flags) from the reference's
+    compressGroupedSegments with the given tile geometry and fit-pool cap."""
+    L = ref()
+    names = list(mats)
+    arrs = [np.ascontiguousarray(mats[n], np.float32) for n in names]
+    nm = (C.c_char_p * len(names))(*[n.encode() for n in names])
+    ws = (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    rows = (C.c_uint32 * len(arrs))(*[a.shape[0] for a in arrs])
+    cols = (C.c_uint32 * len(arrs))(*[a.shape[1] for a in arrs])
+    skipped = np.zeros(len(arrs), np.uint8)
+    out = C.POINTER(C.c_uint8)()
+    n = _sz()
+    rc = L.ref_hsda_build_ex(len(names), nm, ws, rows, cols, tile_rows, tile_cols, n_atoms,
+                             n_stages, k_per_stage, ksvd_iters, stage_decay, max_tiles_for_fit,
+                             skipped.ctypes.data, C.byref(out), C.byref(n))
+    if rc:
+        raise RuntimeError(L.ref_last_error().decode())
+    data = bytes(C.string_at(out, n.value))
+    L.ref_free(out)
+    return data, skipped
 
 
 def ref_hsda_matmul(data, name: str, x, R: int) -> np.ndarray:

@@ -163,6 +163,54 @@ int ref_hsda_build(uint32_t n, const char* const* names, const float* const* ws,
     }
 }
 
+// compressGroupedSegments with per-segment widths, a tile geometry and the fit-pool cap:
+// skipped[i] = 1 for the segments the pipeline skipped (out_skipped_names).
+int ref_hsda_build_ex(uint32_t n, const char* const* names, const float* const* ws,
+                      const uint32_t* rows, const uint32_t* cols, uint16_t tile_rows,
+                      uint16_t tile_cols, uint16_t n_atoms, uint8_t n_stages,
+                      uint8_t k_per_stage, uint8_t ksvd_iters, float stage_decay,
+                      uint32_t max_tiles_for_fit, uint8_t* skipped, uint8_t** out,
+                      size_t* out_n) {
+    try {
+        HierarchicalSDRConfig cfg;
+        cfg.tile_rows = tile_rows;
+        cfg.tile_cols = tile_cols;
+        cfg.n_atoms = n_atoms;
+        cfg.n_stages = n_stages;
+        cfg.active_bits_per_stage = k_per_stage;
+        cfg.ksvd_iters = ksvd_iters;
+        cfg.stage_decay = stage_decay;
+        cfg.max_tiles_for_fit = max_tiles_for_fit;
+        HierarchicalSDRStrategy strat(cfg, cfg);
+        std::vector<ModelSegment> segs;
+        for (uint32_t i = 0; i < n; ++i) {
+            ModelSegment seg(SegmentType::WEIGHTS_FP32, names[i],
+                             as_bytes(ws[i], sizeof(float) * size_t(rows[i]) * cols[i]));
+            TensorMetadata meta;
+            meta.dimensions = {rows[i], cols[i]};
+            seg.tensor_metadata = meta;
+            seg.data_format = "f32";
+            segs.push_back(std::move(seg));
+        }
+        std::vector<std::string> sk;
+        auto archive = strat.compressGroupedSegments(segs, &sk);
+        for (uint32_t i = 0; i < n; ++i) {
+            skipped[i] = 0;
+            for (const auto& nm : sk)
+                if (nm == names[i]) skipped[i] = 1;
+        }
+        std::ostringstream os;
+        archive.writeToStream(os);
+        const std::string b = os.str();
+        *out_n = b.size();
+        *out = static_cast<uint8_t*>(std::malloc(b.size() ? b.size() : 1));
+        std::memcpy(*out, b.data(), b.size());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, -1);
+    }
+}
+
 int ref_hsda_matmul(const uint8_t* data, size_t n, const char* name, const float* x,
                     size_t batch, float* y, size_t y_floats) {
     try {

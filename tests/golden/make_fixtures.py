@@ -48,7 +48,11 @@ and tests/golden/sdr_fixtures.npz (`sdr` argument):
              reference's own index lister's output for them (src/tool_sdr_inspect.cpp --all,
              compiled by `make -C oracle inspect`)
 
-Usage: python tests/golden/make_fixtures.py [hsda | gguf | encode | sdr]
+and tests/golden/hsda_grouped_fixtures.npz (`hsda_grouped` argument): compressGroupedSegments
+with a capped fit pool (reservoir sampling, max_tiles_for_fit), several 1-row tile widths (one
+dictionary per width) and 2-D tiles with a skipped matrix, inputs included.
+
+Usage: python tests/golden/make_fixtures.py [hsda | hsda_grouped | gguf | encode | sdr]
 """
 from __future__ import annotations
 
@@ -163,6 +167,41 @@ def hsda_main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
 
 
+def hsda_grouped_main() -> None:
+    """tests/golden/hsda_grouped_fixtures.npz: compressGroupedSegments cases with their
+    inputs: g<i>_name_<j>, g<i>_w_<j> (inputs), g<i>_cfg (tile_rows, tile_cols, K, stages,
+    k, ksvd_iters, max_tiles_for_fit), g<i>_bytes (the archive), g<i>_skipped."""
+    oracle.build(ref=True)
+    if oracle.ref() is None:
+        raise SystemExit("oracle/_ref/libcsdr_ref.so is not built")
+    rng = np.random.default_rng(20261203)
+    cases = [
+        # a capped fit pool: 97 tiles reservoir-sampled into 40
+        (["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.1.ffn_up.weight"],
+         [(32, 64), (20, 64), (45, 64)], (1, 64, 16, 2, 2, 2, 40)),
+        # 1-row tiles of different widths: one dictionary per width, in the bucket map's order;
+        # a matrix whose rows are not a whole number of 2-row tiles is skipped in 2-D mode
+        (["a.weight", "b.weight", "c.weight", "d.weight"],
+         [(40, 64), (36, 32), (24, 64), (30, 48)], (1, 64, 8, 2, 2, 1, 0)),
+        (["e.weight", "f.weight", "g.weight"],
+         [(16, 32), (15, 32), (24, 32)], (2, 8, 8, 2, 2, 1, 0)),
+    ]
+    out = {}
+    for i, (names, shapes, cfg) in enumerate(cases):
+        mats = {n: rng.normal(0, 0.05, sh).astype(np.float32) for n, sh in zip(names, shapes)}
+        tr, tc, K, S, k, it, cap = cfg
+        data, skipped = oracle.ref_hsda_build_ex(mats, tr, tc, K, S, k, it, 0.5, cap)
+        for j, n in enumerate(names):
+            out[f"g{i}_name_{j}"] = np.frombuffer(n.encode(), np.uint8)
+            out[f"g{i}_w_{j}"] = mats[n]
+        out[f"g{i}_cfg"] = np.array(cfg, np.int64)
+        out[f"g{i}_bytes"] = np.frombuffer(data, np.uint8)
+        out[f"g{i}_skipped"] = skipped
+    path = os.path.join(HERE, "hsda_grouped_fixtures.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
 def cpu_model() -> str:
     """/proc/cpuinfo's model name: the reference's dictionary initialisation depends on the
     CPU's approximate reciprocal square root (its -ffast-math build)."""
@@ -271,6 +310,8 @@ if __name__ == "__main__":
         encode_main()
     elif sys.argv[1:] == ["hsda"]:
         hsda_main()
+    elif sys.argv[1:] == ["hsda_grouped"]:
+        hsda_grouped_main()
     elif sys.argv[1:] == ["gguf"]:
         gguf_main()
     else:
