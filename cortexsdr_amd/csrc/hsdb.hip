@@ -105,6 +105,7 @@ struct Params {
     float* inv;       // M > 1: per (matrix, column) 1 / rms, [g * 16 + m] (workspace head)
     float eps;
     int nsplit, hd;   // attention combine: splits and head size of the partials in x
+    int gtotal;       // 2 <= M <= 8: gather units of all matrices (the launch is padded to 8s)
 };
 
 template <int CTRL>
@@ -746,27 +747,85 @@ __global__ __launch_bounds__(kThreads) void rms_inv_kernel(Params p) {
     if (tid == 0) p.inv[blockIdx.y * 16 + m] = 1.0f / sqrtf(ss / (float)C + p.eps);
 }
 
-// ---- kernel 1, 2 <= M <= 16 and 64-long blocks: P[b][a][m] = D[a] . X[64b : 64b+64, m]
-// One thread per atom with the atom's 64 values in registers; a workgroup covers 256 atoms
-// and PB block columns, whose X (with the call's x op applied) is staged in LDS as
-// [block][t][MC] (columns past M zero) and read as broadcasts, so each thread runs 64 * MC
-// fused multiply-adds per block with no cross-lane reduction and writes its M values of P
-// contiguously. Y is initialised as in dx_kernel. RMSNorm reads the column statistics of
-// rms_inv_kernel.
-constexpr int kDxmAtoms = kThreads;
+// ---- kernel 1 at 2 <= M <= 16 with 64-long blocks: P[b][a][m] = D[a] . X'[64b : 64b + 64, m]
+// on the fp32 matrix cores, the M = 1 product widened: the N dimension of
+// v_mfma_f32_16x16x4_f32 runs over (block column, column) pairs, 16 / MC block columns of MC
+// columns per 16-wide tile (columns past M contribute zeros and are not stored). Workgroup =
+// 4 waves x 16 atoms by one N tile. The tile's X' (X with the call's x op: RMSNorm by
+// rms_inv_kernel's column statistic, or SiLU . x2) is staged once in LDS with coalesced loads,
+// as [pair][feature] rows padded to 68 floats (the 16-byte reads of 8 consecutive pairs then
+// meet distinct banks). Lane l supplies atom l % 16 (A, one contiguous 64-byte run of the
+// dictionary row) and pair l % 16 (B, four 16-byte LDS reads); lane group l / 16 takes features
+// 16 (l / 16) .. + 15 of the block in its 16 steps. Lane l ends with P[pair l % 16][atoms
+// 4 (l / 16) .. + 3]. Y is initialised as in dx_kernel.
+constexpr int kXsStride = 68;
 
 template <int XOP, int MC>
-__global__ __launch_bounds__(kThreads) void dxm_kernel(Params p) {
-    extern __shared__ float smem[];
+__global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
     typedef float f4 __attribute__((ext_vector_type(4)));
+    static_assert(MC == 2 || MC == 4 || MC == 8 || MC == 16, "MC");
+    static_assert(kThreads == 256, "one X element per thread and pass");
+    constexpr int BPT = 16 / MC;  // block columns per N tile
+    __shared__ __attribute__((aligned(16))) float xs[16 * kXsStride];
     const int wg = blockIdx.x;
     int g = 0;
     while (g + 1 < p.G && wg >= p.m[g + 1].dx_base) ++g;
     const MatDesc& d = p.m[g];
     const int u = wg - d.dx_base;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
     const int M = p.M;
-    const int C = d.C_full + d.Ce;
+    const int na = (d.K + 63) / 64;
+    const int ag = u % na, ng = u / na;
+    const int a0 = ag * 64 + wave * 16;
+    // dictionary operand first (the longest round trip), then the X tile
+    f4 dv[4];
+    {
+        const f4* src = reinterpret_cast<const f4*>(d.dict + (size_t)min(a0 + li, d.K - 1) * 64 +
+                                                    lg * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dv[i] = src[i];
+    }
+    {
+        // 16 pairs x 64 features, 4 per thread
+        float v[4], w2[4], iv[4];
+        int dst[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // e -> (block column bl of the tile, column m, feature f) in memory order: features
+            // fastest for token-major X (M x C), columns fastest for feature-major (C x M)
+            const int e = i * kThreads + tid;
+            const int bl = e / (64 * MC), r = e - bl * 64 * MC;
+            int m, f;
+            if (p.tm) {
+                m = r / 64;
+                f = r - m * 64;
+            } else {
+                f = r / MC;
+                m = r - f * MC;
+            }
+            const int n = bl * MC + m;
+            const int b = ng * BPT + bl;
+            ok[i] = b < d.NB && m < M;
+            const int fg = min(b, d.NB - 1) * 64 + f, mg = min(m, M - 1);
+            const size_t xo = xi(p, d, fg, mg);
+            v[i] = xload(d.x, p.x_f16, xo);
+            if constexpr (XOP == CSDR_XOP_RMSNORM) {
+                iv[i] = p.inv[g * 16 + mg];
+                w2[i] = p.nw[fg];
+            }
+            if constexpr (XOP == CSDR_XOP_SILU_MUL) w2[i] = static_cast<const float*>(d.x2)[xo];
+            dst[i] = n * kXsStride + f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float x = v[i];
+            if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * iv[i] * w2[i];
+            if constexpr (XOP == CSDR_XOP_SILU_MUL) x = (x * (1.0f / (1.0f + expf(-x)))) * w2[i];
+            xs[dst[i]] = ok[i] ? x : 0.0f;
+        }
+    }
     {
         const size_t ytot = (size_t)d.R * M;
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
@@ -776,100 +835,34 @@ __global__ __launch_bounds__(kThreads) void dxm_kernel(Params p) {
             d.y[i] = p.accumulate ? d.y[i] + bv : bv;
         }
     }
-    const int na = (d.K + kDxmAtoms - 1) / kDxmAtoms;
-    const int ag = u % na, bg = u / na;
-    const int a = ag * kDxmAtoms + tid;
-    const bool live = a < d.K;
-    const int b0 = bg * d.PB;
-    const int nb = min(d.PB, d.NB - b0);
-    // the atom's row, 16 independent 16-byte loads in flight
-    f4 dr[16];
-    {
-        const f4* src = reinterpret_cast<const f4*>(d.dict + (size_t)min(a, d.K - 1) * 64);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dr[i] = src[i];
-    }
-    __shared__ float inv[MC];
-    if constexpr (XOP == CSDR_XOP_RMSNORM) {
-        // per-column 1 / rms, computed once per call by rms_inv_kernel
-        if (tid < MC) inv[tid] = tid < M ? p.inv[g * 16 + tid] : 0.0f;
-        __syncthreads();
-    }
-    // X of this workgroup's block columns -> LDS [bb][t][MC], the x op applied
-    float* xs = smem;
-    {
-        const int n = nb * 64 * MC;
-        const int f0 = b0 * 64;
-        for (int i0 = 0; i0 < n; i0 += kThreads * kStageBatch) {
-            float v[kStageBatch], w2[kStageBatch];
-#pragma unroll
-            for (int j = 0; j < kStageBatch; ++j) {
-                const int i = min(i0 + j * kThreads + tid, n - 1);
-                const int f = f0 + i / MC, m = min(i % MC, M - 1);
-                const size_t xo = xi(p, d, f, m);
-                v[j] = xload(d.x, p.x_f16, xo);
-                if constexpr (XOP == CSDR_XOP_RMSNORM) w2[j] = p.nw[f];
-                if constexpr (XOP == CSDR_XOP_SILU_MUL) w2[j] = static_cast<const float*>(d.x2)[xo];
-            }
-#pragma unroll
-            for (int j = 0; j < kStageBatch; ++j) {
-                const int i = min(i0 + j * kThreads + tid, n - 1);
-                const int m = i % MC;
-                float x = v[j];
-                if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * inv[min(m, MC - 1)] * w2[j];
-                if constexpr (XOP == CSDR_XOP_SILU_MUL) x = (x * (1.0f / (1.0f + expf(-x)))) * w2[j];
-                xs[i] = m < M ? x : 0.0f;
-            }
-        }
-        if (u == 0 && XOP != CSDR_XOP_NONE && d.xe) {
-            // the transformed edge-strip inputs, [cc][m]
-            for (int t = tid; t < d.Ce * M; t += kThreads) {
-                const int cc = t / M, m = t - cc * M, f = d.C_full + cc;
-                const size_t xo = xi(p, d, f, m);
-                float x = xload(d.x, p.x_f16, xo);
-                if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * inv[m] * p.nw[f];
-                if constexpr (XOP == CSDR_XOP_SILU_MUL)
-                    x = (x * (1.0f / (1.0f + expf(-x)))) * static_cast<const float*>(d.x2)[xo];
-                d.xe[t] = x;
-            }
+    if (u == 0 && XOP != CSDR_XOP_NONE && d.xe) {
+        // the transformed edge-strip inputs, [cc][m]
+        for (int t = tid; t < d.Ce * M; t += kThreads) {
+            const int cc = t / M, m = t - cc * M, f = d.C_full + cc;
+            const size_t xo = xi(p, d, f, m);
+            float x = xload(d.x, p.x_f16, xo);
+            if constexpr (XOP == CSDR_XOP_RMSNORM) x = x * p.inv[g * 16 + m] * p.nw[f];
+            if constexpr (XOP == CSDR_XOP_SILU_MUL)
+                x = (x * (1.0f / (1.0f + expf(-x)))) * static_cast<const float*>(d.x2)[xo];
+            d.xe[t] = x;
         }
     }
     __syncthreads();
-    float* Pa = d.P + ((size_t)b0 * d.K + a) * M;
-    const size_t pstride = (size_t)d.K * M;
-    for (int bb = 0; bb < nb; ++bb) {
-        float acc[MC];
+    f4 xb[4];
 #pragma unroll
-        for (int mm = 0; mm < MC; ++mm) acc[mm] = 0.0f;
-        const float* xb = xs + bb * 64 * MC;
+    for (int i = 0; i < 4; ++i)
+        xb[i] = *reinterpret_cast<const f4*>(xs + li * kXsStride + lg * 16 + 4 * i);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+    for (int s = 0; s < 16; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[s >> 2][s & 3], xb[s >> 2][s & 3], acc, 0, 0, 0);
+    const int bj = ng * BPT + li / MC, mj = li % MC;
+    if (bj < d.NB && mj < M) {
+        float* out = d.P + (size_t)bj * d.K * M + mj;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float dv = dr[i][e];
-                const float* xt = xb + (4 * i + e) * MC;
-#pragma unroll
-                for (int q = 0; q < MC; q += 4) {
-                    const f4 xv = *reinterpret_cast<const f4*>(xt + q);
-                    acc[q] = fmaf(dv, xv.x, acc[q]);
-                    acc[q + 1] = fmaf(dv, xv.y, acc[q + 1]);
-                    acc[q + 2] = fmaf(dv, xv.z, acc[q + 2]);
-                    acc[q + 3] = fmaf(dv, xv.w, acc[q + 3]);
-                }
-            }
-            // one group of four x rows at a time: the accumulators are pinned here (an empty
-            // asm that reads and writes them emits no instruction), so this group's
-            // multiply-adds complete before the next group's loads; otherwise every group's
-            // LDS loads are hoisted above the multiply-adds, 16 * MC registers on top of the
-            // atom's 64
-#pragma unroll
-            for (int mm = 0; mm < MC; ++mm) asm volatile("" : "+v"(acc[mm]));
-        }
-        if (live) {
-            float* out = Pa + bb * pstride;
-#pragma unroll
-            for (int mm = 0; mm < MC; ++mm)
-                if (mm < M) out[mm] = acc[mm];
+        for (int v = 0; v < 4; ++v) {
+            const int a = a0 + 4 * lg + v;
+            if (a < d.K) out[(size_t)a * M] = acc[v];
         }
     }
 }
@@ -1114,94 +1107,95 @@ void gatherw_kernel(Params p) {
 // ---- kernel 2, 2 <= M <= 8: the same streaming gather with MC columns per code read
 // Workgroup = (matrix, chunk, row range) as in gatherw_kernel; the chunk's P slice is staged
 // in LDS as [block][atom][MC] fp32 (columns past M zero), so each slot's MC values are one or
-// two 16-byte LDS reads and every code word feeds MC fused multiply-adds: the codes are read
-// from HBM once for all M columns. Row totals (MC per row) wait in LDS and go into Y with one
-// device-scope atomic per (row, column) after the stream. WPE: waves per SIMD the register
-// budget is pinned for (1 workgroup per CU for the 128 KiB slice at MC = 8, 2 below).
+// two LDS reads and every code word feeds MC fused multiply-adds: the codes are read from HBM
+// once for all M columns. A lane takes one tile (one row's slots of one block column), so a
+// row's partial sums meet across the chunk's block columns only (one DPP step per doubling),
+// and every slot's stage gain is the same for all lanes. Row totals (MC per row) wait
+// in LDS and go into Y with one device-scope atomic per (row, column) after the stream. WPE:
+// waves per SIMD the register budget is pinned for (1 workgroup per CU for the 128 KiB slice
+// at MC = 8, 2 below).
 constexpr int kGvMinRows = 256;  // rows per workgroup the LDS share must hold, at least
 
-// The 2 <= M <= 8 gather's stream for one chunk width: PPR lanes per row (each lane a fixed
-// tile and slot quarter), `buf` holding the first DEPTH pieces already issued. Lanes past the
-// wave's valid pieces read zeros (coefficient 0), and a row's lanes are all valid or all past
-// the end, so no selects are needed before the row reductions.
-template <int SLOTS, int MC, int DEPTH, int PPR, typename PieceFn>
-__device__ __forceinline__ void gatherv_stream(const Params& p, const MatDesc& d,
-                                               const float* Ps, float* rowt, u32x4* buf,
-                                               PieceFn piece, int nk, int wfirst, int npieces) {
-    (void)p;
+// The 2 <= M <= 8 gather's stream for one chunk width: LPR lanes per row (lane = block column
+// of the row), `buf` holding the first TD tiles already issued. Lanes past the wave's valid
+// tiles read zeros (coefficient 0), and a row's lanes are all valid or all past the end, so no
+// selects are needed before the row reductions.
+template <int SLOTS, int MC, int TD, int LPR, typename TileFn>
+__device__ __forceinline__ void gatherv_stream(const MatDesc& d, const float* Ps, float* rowt,
+                                               u32x4 (*buf)[SLOTS / 4], TileFn tile, int nk,
+                                               int wfirst, int ntiles) {
     typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
     constexpr int PPB = SLOTS / 4;
+    constexpr int G = MC / 4;
     constexpr int kStep = 64;
-    constexpr int lg_ppr = PPR == 1 ? 0 : PPR == 2 ? 1 : PPR == 4 ? 2 : PPR == 8 ? 3
-                         : PPR == 16 ? 4 : PPR == 32 ? 5 : 6;
+    constexpr int lg_lpr = LPR == 1 ? 0 : LPR == 2 ? 1 : LPR == 4 ? 2 : LPR == 8 ? 3
+                         : LPR == 16 ? 4 : LPR == 32 ? 5 : 6;
     const int lane = threadIdx.x & 63;
-    const int pl = lane & (PPR - 1);
-    const int bb = pl / PPB, h = pl - bb * PPB;
-    const float* Pb = Ps + (size_t)bb * d.K * MC;
-    float gm[4];
+    const int bb = lane & (LPR - 1);
+    const int ebase = bb * d.K;
+    float gm[SLOTS];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        gm[e] = sgam_at(d, e);
-#pragma unroll
-        for (int hh = 1; hh < PPB; ++hh)
-            if (h == hh) gm[e] = sgam_at(d, hh * 4 + e);
-    }
-    const bool gu = d.gunif != 0;
-    const float g0 = d.sgam[0];
-    if (gu) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) gm[e] = 1.0f;
-    }
-    const bool head = (pl == 0);
+    for (int j = 0; j < SLOTS; ++j) gm[j] = sgam_at(d, j);
+    const bool head = (bb == 0);
     const int q0 = wfirst + lane;
-    auto consume = [&](const u32x4& w, int k) {
-        const int qp = q0 + k * kStep;
-        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+    auto consume = [&](const u32x4* w, int k) {
+        const int tq = q0 + k * kStep;
         float acc[MC];
 #pragma unroll
         for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float cf = gm[e] * csdr::h2f(w4[e] >> 16);
-            const float* pv = Pb + (size_t)(uint16_t)w4[e] * MC;
-            if constexpr (MC >= 4) {
-#pragma unroll
-                for (int m4 = 0; m4 < MC; m4 += 4) {
-                    const f4 v = *reinterpret_cast<const f4*>(pv + m4);
-                    acc[m4] = fmaf(cf, v.x, acc[m4]);
-                    acc[m4 + 1] = fmaf(cf, v.y, acc[m4 + 1]);
-                    acc[m4 + 2] = fmaf(cf, v.z, acc[m4 + 2]);
-                    acc[m4 + 3] = fmaf(cf, v.w, acc[m4 + 3]);
-                }
+        for (int j = 0; j < SLOTS; ++j) {
+            const uint32_t word = w[j >> 2][j & 3];
+            const float cf = gm[j] * csdr::h2f(word >> 16);
+            const int e = ebase + (int)(uint16_t)word;
+            if constexpr (MC == 2) {
+                const f2 v = *reinterpret_cast<const f2*>(Ps + (size_t)e * 2);
+                acc[0] = fmaf(cf, v.x, acc[0]);
+                acc[1] = fmaf(cf, v.y, acc[1]);
             } else {
 #pragma unroll
-                for (int m = 0; m < MC; ++m) acc[m] = fmaf(cf, pv[m], acc[m]);
+                for (int h = 0; h < G; ++h) {
+                    const f4 v = *reinterpret_cast<const f4*>(Ps + (size_t)e * MC + 4 * h);
+                    acc[4 * h] = fmaf(cf, v.x, acc[4 * h]);
+                    acc[4 * h + 1] = fmaf(cf, v.y, acc[4 * h + 1]);
+                    acc[4 * h + 2] = fmaf(cf, v.z, acc[4 * h + 2]);
+                    acc[4 * h + 3] = fmaf(cf, v.w, acc[4 * h + 3]);
+                }
             }
         }
 #pragma unroll
         for (int m = 0; m < MC; ++m) {
             float a = acc[m];
-            if constexpr (PPR > 1) a += dpp_move<0xB1>(a);
-            if constexpr (PPR > 2) a += dpp_move<0x4E>(a);
-            if constexpr (PPR > 4) a += dpp_move<0x141>(a);
-            if constexpr (PPR > 8) a += dpp_move<0x140>(a);
-            if constexpr (PPR > 16) a += __shfl_xor(a, 16, 64);
-            if constexpr (PPR > 32) a += __shfl_xor(a, 32, 64);
+            if constexpr (LPR > 1) a += dpp_move<0xB1>(a);
+            if constexpr (LPR > 2) a += dpp_move<0x4E>(a);
+            if constexpr (LPR > 4) a += dpp_move<0x141>(a);
+            if constexpr (LPR > 8) a += dpp_move<0x140>(a);
+            if constexpr (LPR > 16) a += __shfl_xor(a, 16, 64);
+            if constexpr (LPR > 32) a += __shfl_xor(a, 32, 64);
             acc[m] = a;
         }
-        if (head && qp < npieces) {
-            float* rt = rowt + (size_t)(qp >> lg_ppr) * MC;
+        if (head && tq < ntiles) {
+            float* rt = rowt + (size_t)(tq >> lg_lpr) * MC;
+            if constexpr (MC >= 4) {
 #pragma unroll
-            for (int m = 0; m < MC; ++m) rt[m] = gu ? acc[m] * g0 : acc[m];
+                for (int m4 = 0; m4 < MC; m4 += 4)
+                    *reinterpret_cast<f4*>(rt + m4) = f4{acc[m4], acc[m4 + 1], acc[m4 + 2], acc[m4 + 3]};
+            } else {
+#pragma unroll
+                for (int m = 0; m < MC; ++m) rt[m] = acc[m];
+            }
         }
     };
-    constexpr int NBUF = DEPTH + 1;
+    constexpr int NBUF = TD + 1;
     int k0 = 0;
     for (; k0 + NBUF <= nk; k0 += NBUF) {
 #pragma unroll
         for (int jj = 0; jj < NBUF; ++jj) {
-            const u32x4 w = buf[jj];
-            buf[(jj + DEPTH) % NBUF] = piece(k0 + jj + DEPTH);
+            u32x4 w[PPB];
+#pragma unroll
+            for (int i = 0; i < PPB; ++i) w[i] = buf[jj][i];
+            tile(k0 + jj + TD, buf[(jj + TD) % NBUF]);
             consume(w, k0 + jj);
         }
     }
@@ -1214,7 +1208,14 @@ template <int SLOTS, int MC, int DEPTH, int WPE>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gatherv_kernel(Params p) {
     extern __shared__ float smem[];
-    const int wg = (int)blockIdx.x;
+    // Workgroups go to the eight XCDs round-robin (workgroup b on XCD b % 8). XCD x takes the
+    // x-th eighth of the units in chunk-major order, so the row ranges of one chunk share the
+    // L2 that holds its P slice (MC columns make the slice a quarter of the chunk's codes and
+    // more: fetched into several L2s it would double the HBM bytes). The launch is padded to
+    // a multiple of 8; padding workgroups exit.
+    const int per_xcd = (p.gtotal + 7) >> 3;
+    const int wg = ((int)blockIdx.x & 7) * per_xcd + ((int)blockIdx.x >> 3);
+    if (wg >= p.gtotal) return;
     int g = 0;
     while (g + 1 < p.G && wg >= p.m[g + 1].g_base) ++g;
     const MatDesc& d = p.m[g];
@@ -1222,8 +1223,8 @@ void gatherv_kernel(Params p) {
     const int nfull = d.NB / d.NBc;
     int c, sidx, rpw;
     if (u < nfull * d.splits) {
-        c = u % nfull;
-        sidx = u / nfull;
+        c = u / d.splits;
+        sidx = u - c * d.splits;
         rpw = d.rows_per_wg;
     } else {
         int v = u - nfull * d.splits, j = 0;
@@ -1242,21 +1243,24 @@ void gatherv_kernel(Params p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     constexpr int PPB = SLOTS / 4;  // 16-byte pieces per tile
-    const int ppr = nbc * PPB;      // pieces per row: a power of two <= 64
-    const int npieces = (rend - rbeg) * ppr;
-    const int nload = (npieces + 63) >> 6;
+    // tiles in flight per wave: about DEPTH pieces, at least two tiles
+    constexpr int TD = DEPTH / PPB > 2 ? DEPTH / PPB : 2;
+    const int ntiles = (rend - rbeg) * nbc;  // tile t = (row t / nbc, block column t % nbc)
+    const int nload = (ntiles + 63) >> 6;
     const int per = (nload + kGWaves - 1) / kGWaves;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int nk = max(0, min(per, nload - wv * per));
     const int wfirst = wv * per * 64;
-    const int wvalid = max(0, min(per * 64, npieces - wfirst));
+    const int wvalid = max(0, min(per * 64, ntiles - wfirst));
     const uint32_t* wbase = d.codes + (size_t)b0 * d.R * SLOTS + (size_t)rbeg * nbc * SLOTS +
-                            (size_t)wfirst * 4;
+                            (size_t)wfirst * SLOTS;
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, wvalid * 16, kRawBufferDword3);
-    constexpr int kStep = 64;
-    auto piece = [&](int k) -> u32x4 {
-        return __builtin_amdgcn_raw_buffer_load_b128(rs, (k * kStep + lane) * 16, 0, kCachePolicyNT);
+        __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, wvalid * SLOTS * 4, kRawBufferDword3);
+    auto tile = [&](int k, u32x4* out) {
+        const int o = (k * 64 + lane) * SLOTS * 4;
+#pragma unroll
+        for (int i = 0; i < PPB; ++i)
+            out[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + i * 16, 0, kCachePolicyNT);
     };
 
     float* Ps = smem;                          // NBc * K * MC floats
@@ -1264,11 +1268,11 @@ void gatherv_kernel(Params p) {
     float* rowt = xe + 64 * MC;                 // (rend - rbeg) x MC row totals
     const bool edge = (c == d.nchunks - 1) && d.Ce > 0;
 
-    // the wave's first code loads go out before the P slice is staged (they overlap it)
-    constexpr int NBUF = DEPTH + 1;
-    u32x4 buf[NBUF];
-#pragma unroll
-    for (int k = 0; k < DEPTH; ++k) buf[k] = piece(k);
+    // The P slice loads go out first (L2 / Infinity Cache hits: queued behind the code loads'
+    // HBM misses they would wait for them), then the wave's first code loads, which overlap
+    // the P round trip and the barrier.
+    constexpr int NBUF = TD + 1;
+    u32x4 buf[NBUF][PPB];
     typedef float f4 __attribute__((ext_vector_type(4)));
     if (M == MC && (d.K * MC) % 4 == 0) {
         // P slice: global [block][atom][M] -> LDS, a straight copy of 16-byte pieces (at most 8
@@ -1280,10 +1284,16 @@ void gatherv_kernel(Params p) {
             f4 v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = Pg[min(i0 + j * kGThreads + tid, n4 - 1)];
+            if (i0 == 0) {
+#pragma unroll
+                for (int k = 0; k < TD; ++k) tile(k, buf[k]);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) Pl[min(i0 + j * kGThreads + tid, n4 - 1)] = v[j];
         }
     } else {
+#pragma unroll
+        for (int k = 0; k < TD; ++k) tile(k, buf[k]);
         // P slice: global [block][atom][M] -> LDS [block][atom][MC], kStageBatch loads in flight
         const float* Pg = d.P + (size_t)b0 * d.K * M;
         const int n = nbc * d.K * MC;
@@ -1302,16 +1312,16 @@ void gatherv_kernel(Params p) {
     }
     __syncthreads();
 
-    // the stream, specialised on the lanes per row (a power of two fixed per chunk width), so
-    // each column's row reduction is a straight DPP / shuffle sequence
-    switch (ppr) {
-        case 1: gatherv_stream<SLOTS, MC, DEPTH, 1>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        case 2: gatherv_stream<SLOTS, MC, DEPTH, 2>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        case 4: gatherv_stream<SLOTS, MC, DEPTH, 4>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        case 8: gatherv_stream<SLOTS, MC, DEPTH, 8>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        case 16: gatherv_stream<SLOTS, MC, DEPTH, 16>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        case 32: gatherv_stream<SLOTS, MC, DEPTH, 32>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
-        default: gatherv_stream<SLOTS, MC, DEPTH, 64>(p, d, Ps, rowt, buf, piece, nk, wfirst, npieces); break;
+    // the stream, specialised on the lanes per row (the chunk's block columns, a power of two),
+    // so each column's row reduction is a straight DPP / shuffle sequence
+    switch (nbc) {
+        case 1: gatherv_stream<SLOTS, MC, TD, 1>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 2: gatherv_stream<SLOTS, MC, TD, 2>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 4: gatherv_stream<SLOTS, MC, TD, 4>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 8: gatherv_stream<SLOTS, MC, TD, 8>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 16: gatherv_stream<SLOTS, MC, TD, 16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 32: gatherv_stream<SLOTS, MC, TD, 32>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        default: gatherv_stream<SLOTS, MC, TD, 64>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
     }
     // the top-right strip's inputs of the last chunk: [cc][m] (x-op transformed when given)
     if (edge) {
@@ -1819,7 +1829,7 @@ void launch_gatherv(const Params& p, int slots, int grid, size_t lds, hipStream_
 // ranges per chunk, ranges are added one class at a time (all full chunks of a matrix, or one
 // remainder chunk) to the class with the most block-rows per workgroup while the total stays
 // within the target.
-void plan_gather_splits(Params& p, int n, long long target, int max_rows) {
+void plan_gather_splits(Params& p, int n, long long target, int max_rows, long long round) {
     struct Cls {
         int g, j;       // matrix, remainder index (-1: the full chunks)
         int width, count, R;
@@ -1847,6 +1857,9 @@ void plan_gather_splits(Params& p, int n, long long target, int max_rows) {
         for (int bit = d.NBc >> 1; bit; bit >>= 1)
             if ((d.NB % d.NBc) & bit) add(j++, bit, 1);
     }
+    // more workgroups than one round of the chip holds (the row limit forces it): fill whole
+    // rounds, so the last one is not a fraction of the chip doing full-size work units
+    if (used > target && round > 0) target = (used + round - 1) / round * round;
     for (;;) {
         int best = -1;
         double best_b = 0.0;
@@ -1986,7 +1999,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
                              (xa.xop == CSDR_XOP_SILU_MUL ? reinterpret_cast<uintptr_t>(xa.x2[i]) : 0);
         dx1 = segs[i] && segs[i]->tile_cols == 64 && al % 16 == 0;
     }
-    const int dxm_mc = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
+    const int dxm_mc = M <= 2 ? 2 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16));
     for (int i = 0; i < n; ++i) {
         const csdr_hsdb* s = segs[i];
         if (!s || !xs[i] || !ys[i]) return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
@@ -2034,11 +2047,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             d.PB = 16;
             d.dx_count = ((d.K + 63) / 64) * ((d.NB + 15) / 16);
         } else if (dxm) {
-            // about 256 workgroups per matrix: block columns per workgroup from the atom tiles
-            const int na = (d.K + kDxmAtoms - 1) / kDxmAtoms;
-            d.PB = std::max(1, std::min(8, d.NB * na / 256));
-            d.dx_count = na * ((d.NB + d.PB - 1) / d.PB);
-            lds_dx = std::max(lds_dx, (size_t)d.PB * 64 * dxm_mc * 4);
+            // 64 atoms by one 16-wide tile of (block column, column) pairs per workgroup
+            d.dx_count = ((d.K + 63) / 64) * ((d.NB * dxm_mc + 15) / 16);
         } else if (d.blen == 64) {
             d.dx_count = ((d.K + 15) / 16) * ((d.NB + d.PB - 1) / d.PB);
             size_t extra = 0;
@@ -2080,7 +2090,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
         const long long min_bytes = kGMinWgBytes;
         target = std::max(1LL, std::min(target, code_bytes / std::max(1LL, min_bytes)));
-        plan_gather_splits(p, n, target, max_rows);
+        plan_gather_splits(p, n, target, max_rows, (long long)ncu * wpc);
         for (int i = 0; i < n; ++i) {
             const MatDesc& d = p.m[i];
             int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup
@@ -2115,18 +2125,21 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             rms_inv_kernel<<<dim3(M, n), kThreads, 0, st>>>(p);
             CSDR_LAUNCH_CHECK("hsdb rms");
         }
-        auto go = [&](auto kern) { kern<<<ndx, kThreads, lds_dx, st>>>(p); };
+        auto go = [&](auto kern) { kern<<<ndx, kThreads, 0, st>>>(p); };
         const int key = p.xop * 100 + dxm_mc;
         switch (key) {
-            case CSDR_XOP_NONE * 100 + 4: go(dxm_kernel<CSDR_XOP_NONE, 4>); break;
-            case CSDR_XOP_NONE * 100 + 8: go(dxm_kernel<CSDR_XOP_NONE, 8>); break;
-            case CSDR_XOP_NONE * 100 + 16: go(dxm_kernel<CSDR_XOP_NONE, 16>); break;
-            case CSDR_XOP_RMSNORM * 100 + 4: go(dxm_kernel<CSDR_XOP_RMSNORM, 4>); break;
-            case CSDR_XOP_RMSNORM * 100 + 8: go(dxm_kernel<CSDR_XOP_RMSNORM, 8>); break;
-            case CSDR_XOP_RMSNORM * 100 + 16: go(dxm_kernel<CSDR_XOP_RMSNORM, 16>); break;
-            case CSDR_XOP_SILU_MUL * 100 + 4: go(dxm_kernel<CSDR_XOP_SILU_MUL, 4>); break;
-            case CSDR_XOP_SILU_MUL * 100 + 8: go(dxm_kernel<CSDR_XOP_SILU_MUL, 8>); break;
-            case CSDR_XOP_SILU_MUL * 100 + 16: go(dxm_kernel<CSDR_XOP_SILU_MUL, 16>); break;
+            case CSDR_XOP_NONE * 100 + 2: go(dxmm_kernel<CSDR_XOP_NONE, 2>); break;
+            case CSDR_XOP_NONE * 100 + 4: go(dxmm_kernel<CSDR_XOP_NONE, 4>); break;
+            case CSDR_XOP_NONE * 100 + 8: go(dxmm_kernel<CSDR_XOP_NONE, 8>); break;
+            case CSDR_XOP_NONE * 100 + 16: go(dxmm_kernel<CSDR_XOP_NONE, 16>); break;
+            case CSDR_XOP_RMSNORM * 100 + 2: go(dxmm_kernel<CSDR_XOP_RMSNORM, 2>); break;
+            case CSDR_XOP_RMSNORM * 100 + 4: go(dxmm_kernel<CSDR_XOP_RMSNORM, 4>); break;
+            case CSDR_XOP_RMSNORM * 100 + 8: go(dxmm_kernel<CSDR_XOP_RMSNORM, 8>); break;
+            case CSDR_XOP_RMSNORM * 100 + 16: go(dxmm_kernel<CSDR_XOP_RMSNORM, 16>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 2: go(dxmm_kernel<CSDR_XOP_SILU_MUL, 2>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 4: go(dxmm_kernel<CSDR_XOP_SILU_MUL, 4>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 8: go(dxmm_kernel<CSDR_XOP_SILU_MUL, 8>); break;
+            case CSDR_XOP_SILU_MUL * 100 + 16: go(dxmm_kernel<CSDR_XOP_SILU_MUL, 16>); break;
             default: return set_error(CSDR_E_INVALID, "hsdb_matmul: x op not available at M > 1");
         }
         CSDR_LAUNCH_CHECK("hsdb dx");
@@ -2150,8 +2163,10 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     if (phases & kPhaseGather) {
         if (fast)
             launch_gatherw(p, slots, base, lds_g, st);
-        else if (vec)
-            launch_gatherv(p, slots, base, lds_g, st);
+        else if (vec) {
+            p.gtotal = base;
+            launch_gatherv(p, slots, (base + 7) / 8 * 8, lds_g, st);
+        }
         else if (MV == 1)
             gatherm_kernel<1><<<base, kThreads, lds_g, st>>>(p);
         else
