@@ -3,7 +3,7 @@ device form of SparseInferenceEngine.cpp decodeSupportedGGUFQuantized + linear_f
 against the oracle (pinned in test_gguf_oracle.py), through the C-ABI.
 
 Bars: dequant bit-exact; the products within 1e-3 relative L2 (M == 1 accumulates in fp32;
-M > 1 splits the decoded values into fp16 hi + lo for the matrix cores, ~1e-6).
+M > 1 rounds the decoded values to fp16 once for the matrix cores, ~2e-4).
 """
 import numpy as np
 import pytest
