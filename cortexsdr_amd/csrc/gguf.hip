@@ -212,12 +212,36 @@ struct Dec8<Packed<BB_, BE_, BITS>> {
     }
 };
 
+// x[e0 .. e0 + 7] in fp32 (e0 % 8 == 0): one or two 16-byte loads when x is 16-byte aligned
+template <typename XT>
+__device__ __forceinline__ void x8(const XT* __restrict__ x, int e0, bool vec, float* o) {
+    if (vec) {
+        if constexpr (sizeof(XT) == 2) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 v = *reinterpret_cast<const h8*>(x + e0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = (float)v[i];
+        } else {
+            const floatx4 a = *reinterpret_cast<const floatx4*>(x + e0);
+            const floatx4 b = *reinterpret_cast<const floatx4*>(x + e0 + 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[i] = a[i];
+                o[4 + i] = b[i];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = csdr::to_f32(x[e0 + i]);
+    }
+}
+
 // ---- kernels
 template <class F, typename XT>
 __global__ __launch_bounds__(kThreads) void gguf_gemv_kernel(const uint8_t* __restrict__ W,
                                                              int R, int C,
                                                              const XT* __restrict__ x,
-                                                             float* __restrict__ y) {
+                                                             float* __restrict__ y, int xvec) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = blockIdx.x * (kThreads / 64) + wave;
     if (r >= R) return;  // (no barriers below)
@@ -227,10 +251,11 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_kernel(const uint8_t* __re
 #pragma unroll 2
     for (int g = lane; g < (C >> 3); g += 64) {
         const int e0 = g << 3, b = e0 / F::BE;
-        float w8[8];
+        float w8[8], xv[8];
         Dec8<F>::run(rowp + (size_t)b * F::BB, e0 - b * F::BE, w8);
+        x8(x, e0, xvec, xv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], csdr::to_f32(x[e0 + i]), acc);
+        for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], xv[i], acc);
     }
     acc = csdr::wave_sum(acc);
     if (lane == 0) y[r] = acc;
@@ -436,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* 
                                                                  int R, int C,
                                                                  const XT* __restrict__ x,
                                                                  float* __restrict__ y,
-                                                                 int aligned4) {
+                                                                 int aligned4, int xvec) {
     extern __shared__ uint8_t srow[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = blockIdx.x * (kThreads / 64) + wave;
@@ -458,10 +483,11 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* 
 #pragma unroll 2
     for (int g = lane; g < (C >> 3); g += 64) {
         const int e0 = g << 3, b = e0 / F::BE;
-        float w8[8];
+        float w8[8], xv[8];
         Dec8<F>::run(my + (size_t)b * F::BB, e0 - b * F::BE, w8);
+        x8(x, e0, xvec, xv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], csdr::to_f32(x[e0 + i]), acc);
+        for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], xv[i], acc);
     }
     acc = csdr::wave_sum(acc);
     if (lane == 0) y[r] = acc;
@@ -478,22 +504,23 @@ int linear_of(const uint8_t* w, int R, int C, const void* x, int x_dtype, int M,
               hipStream_t st) {
     if (M == 1) {
         const int grid = (R + kThreads / 64 - 1) / (kThreads / 64);
+        const int xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
         const size_t rowbytes = (size_t)(C / F::BE) * F::BB;
         const size_t lds = (kThreads / 64) * ((rowbytes + 3) & ~(size_t)3);
         if (StageRow<F>::value && lds <= kGemvLdsMax) {
             const int a4 = (rowbytes % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 4 == 0);
             if (x_dtype == CSDR_F16)
                 gguf_gemv_lds_kernel<F, _Float16><<<grid, kThreads, lds, st>>>(
-                    w, R, C, static_cast<const _Float16*>(x), y, a4);
+                    w, R, C, static_cast<const _Float16*>(x), y, a4, xvec);
             else
                 gguf_gemv_lds_kernel<F, float><<<grid, kThreads, lds, st>>>(
-                    w, R, C, static_cast<const float*>(x), y, a4);
+                    w, R, C, static_cast<const float*>(x), y, a4, xvec);
         } else if (x_dtype == CSDR_F16)
             gguf_gemv_kernel<F, _Float16><<<grid, kThreads, 0, st>>>(
-                w, R, C, static_cast<const _Float16*>(x), y);
+                w, R, C, static_cast<const _Float16*>(x), y, xvec);
         else
             gguf_gemv_kernel<F, float><<<grid, kThreads, 0, st>>>(
-                w, R, C, static_cast<const float*>(x), y);
+                w, R, C, static_cast<const float*>(x), y, xvec);
     } else {
         if (x_dtype != CSDR_F16)
             return set_error(CSDR_E_UNSUPPORTED, "gguf_linear: M > 1 takes fp16 x");
