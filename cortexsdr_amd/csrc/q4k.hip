@@ -44,7 +44,6 @@ constexpr int kBlockBytes = 144;
 constexpr int kUnroll = 4;  // 8-block steps per wave issued back to back (gemv)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -191,94 +190,6 @@ __global__ __launch_bounds__(kThreads) void q4k_gemv_kernel(const uint8_t* __res
         }
         acc = csdr::wave_sum(acc);
         if (lane == 0) y[r] = acc;
-    }
-}
-
-// ---------------------------------------------------------------- M > 1 (MFMA)
-
-constexpr int kMaxNT = 4;  // up to 64 output columns per launch slice (grid.y covers more)
-
-template <int ORDER>
-__global__ __launch_bounds__(kThreads) void q4k_mfma_kernel(const uint8_t* __restrict__ W, int R,
-                                                            int nblk,
-                                                            const _Float16* __restrict__ X,
-                                                            int M, float* __restrict__ Y) {
-    __shared__ floatx4 red[3][kMaxNT][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int r0 = blockIdx.x * 16;
-    const int n0 = blockIdx.y * 16 * kMaxNT;
-    const int C = nblk * 256;
-    const int arow = min(r0 + (lane & 15), R - 1);  // A operand row of this lane
-    const int kq = lane >> 4;                        // 4-value k quad within a 16-k step
-    const uint8_t* rowp = W + (size_t)arow * nblk * kBlockBytes;
-    floatx4 acc[kMaxNT];
-#pragma unroll
-    for (int t = 0; t < kMaxNT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    int nt_live = min(kMaxNT, (M - n0 + 15) / 16);
-
-    for (int blk = wave; blk < nblk; blk += kThreads / 64) {
-        const uint8_t* bp = rowp + (size_t)blk * kBlockBytes;
-        const u32x4 hdr = *reinterpret_cast<const u32x4*>(bp);
-        const float d = hdr_d(hdr), dmin = hdr_dmin(hdr);
-        for (int sb = 0; sb < 8; ++sb) {
-            float sc, m;
-            scale_min(hdr, sb, sc, m);
-            const float ds = d * sc, dm = dmin * m;
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int e0 = sb * 32 + kk * 16 + kq * 4;  // element index in the block
-                float q[4];
-                if (ORDER == 0) {
-                    const uint32_t v =
-                        *reinterpret_cast<const uint32_t*>(bp + 16 + (sb >> 1) * 32 + (e0 & 31));
-                    const int sh = (sb & 1) * 4;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) q[i] = (float)((v >> (8 * i + sh)) & 0xFu);
-                } else {
-                    const uint16_t v = *reinterpret_cast<const uint16_t*>(bp + 16 + e0 / 2);
-                    q[0] = (float)(v & 0xFu);
-                    q[1] = (float)((v >> 4) & 0xFu);
-                    q[2] = (float)((v >> 8) & 0xFu);
-                    q[3] = (float)((v >> 12) & 0xFu);
-                }
-                half4 ahi, alo;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float wv = fmaf(ds, q[i], -dm);
-                    const _Float16 h = (_Float16)wv;
-                    ahi[i] = h;
-                    alo[i] = (_Float16)(wv - (float)h);
-                }
-                const int kcol = blk * 256 + e0;
-                for (int t = 0; t < nt_live; ++t) {
-                    const int n = n0 + t * 16 + (lane & 15);
-                    half4 bv = half4{0, 0, 0, 0};
-                    if (n < M) bv = *reinterpret_cast<const half4*>(X + (size_t)n * C + kcol);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, bv, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(alo, bv, acc[t], 0, 0, 0);
-                }
-            }
-        }
-    }
-    // sum the 4 waves' tiles: waves 1..3 park theirs in LDS, wave 0 adds and stores
-    if (wave > 0)
-        for (int t = 0; t < nt_live; ++t) red[wave - 1][t][lane] = acc[t];
-    __syncthreads();
-    if (wave == 0) {
-        for (int t = 0; t < nt_live; ++t) {
-            floatx4 s = acc[t];
-#pragma unroll
-            for (int w = 0; w < 3; ++w) s += red[w][t][lane];
-            // D[i][j] of the 16x16 tile: lane holds rows (lane/16)*4 + i, column lane%16
-            const int n = n0 + t * 16 + (lane & 15);
-            if (n >= M) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = r0 + (lane >> 4) * 4 + i;
-                if (r < R) Y[(size_t)n * R + r] = s[i];
-            }
-        }
     }
 }
 
