@@ -1761,9 +1761,11 @@ size_t p_path_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
 
 // Workspace of a full product at batch M, large enough for every batch <= M as well (the
 // matrix-core path can need less than the P path at a smaller M).
+// Enough for every path and phase a call at this M can take: the matrix-core path of a plain
+// product, and the P path of x-op calls (M <= 16) and of the separate dx / gather phases.
 size_t group_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
     if (csdr::mfma_eligible(n, segs, M))
-        return std::max(csdr::mfma_workspace_bytes(n, segs, M), p_path_ws_bytes(n, segs, 15));
+        return std::max(csdr::mfma_workspace_bytes(n, segs, M), p_path_ws_bytes(n, segs, M));
     return p_path_ws_bytes(n, segs, M);
 }
 

@@ -131,17 +131,19 @@ CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* seg, const void* x, int x
 
 /* Grouped form: n (1..8) independent products Y_i = W_i . X_i (all with the same M and
  * x_dtype), e.g. the q/k/v or gate/up projections of a decoder layer, in two launches.
- * M == 1 (and matrices the matrix-core path does not take): a dx launch (P = D . X per block
- * column into the workspace, Y = 0 or bias) and a gather launch (Y += the coded rows gathered
- * from P; at M == 1 with 4, 8 or 16 slots two 1024-thread workgroups per CU stream the codes),
- * all fp32 (at M == 1 with 64-column blocks and 16-byte aligned x, the dx launch runs on
- * the fp32 matrix cores). M >= 2 with 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch
- * and a matrix-core launch that decodes 64-column tiles (dictionary and decoded weights rounded to fp16, fp32 X split into fp16 hi + lo,
- * fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
+ * The P path, all fp32: a dx launch (P = D . X per block column into the workspace, Y = 0 or
+ * bias; on the fp32 matrix cores for 64-column blocks) and a gather launch (Y += the coded
+ * rows gathered from P). It serves M == 1 (4, 8 or 16 slots: two 1024-thread workgroups per
+ * CU stream the codes), 2 <= M <= 8 with 1-row tiles of 4/8/16 slots (the codes streamed once
+ * for all M columns), and matrices the matrix-core path does not take. Other M >= 2 with
+ * 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch and a matrix-core launch that
+ * decodes 64-column tiles (dictionary and decoded weights rounded to fp16, fp32 X split into
+ * fp16 hi + lo, fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
  * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace
- * is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes. csdr_hsdb_matmul is the n = 1 case.
- * Y rows are accumulated over block-column ranges with device-scope float atomics, so
- * repeated calls agree to fp32 rounding, not bit for bit. */
+ * is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes, enough for every path and phase at
+ * that M (x-op calls and the separate dx / gather phases take the P path). csdr_hsdb_matmul
+ * is the n = 1 case. Y rows are accumulated over block-column ranges with device-scope float
+ * atomics, so repeated calls agree to fp32 rounding, not bit for bit. */
 CSDR_API size_t csdr_hsdb_group_workspace_bytes(int n, const csdr_hsdb* const* segs, int M);
 CSDR_API int csdr_hsdb_matmul_group(int n, const csdr_hsdb* const* segs, const void* const* x,
                                     int x_dtype, int M, float* const* y, void* workspace,

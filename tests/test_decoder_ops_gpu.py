@@ -168,7 +168,7 @@ def test_decode_row_and_bias_accumulate(gpu):
     assert rel_l2(y.cpu().numpy()[:, 0], 2 * wx + bias) < 1e-5
 
 
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 8, 12, 16])
 def test_matmul_xop_rmsnorm_and_silu(gpu, M):
     from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
 
