@@ -75,11 +75,14 @@ def test_cfg5_width_decode_steps_match_oracle(gpu, cfg5_weights, B):
         dec.close()
 
 
-def test_batched_generate_matches_oracle_and_batch_one(gpu):
+@pytest.mark.parametrize("B", [3, 16])
+def test_batched_generate_matches_oracle_and_batch_one(gpu, B):
+    # B = 3: the streaming multi-column gather; B = 16 (the largest batch): the matrix-core
+    # P producer with the x ops and the generic gather
     spec = DecoderSpec(2, 128, 2, 1, 64, 200, 300, 40)
     w = synthetic_weights(spec, n_atoms=128, nnz=8, seed=41, sigma=0.1, norm_jitter=0.1,
                           bias_sigma=0.1)
-    B, n_prompt, n_new = 3, 7, 6
+    n_prompt, n_new = 7, 6
     prompts = ((np.arange(B * n_prompt).reshape(B, n_prompt) * 7919 + 13) % spec.vocab
                ).astype(np.int32)
     dec = Decoder(w, batch=B)
@@ -106,13 +109,15 @@ def test_batched_generate_matches_oracle_and_batch_one(gpu):
         dec.close()
     # every sequence alone at batch 1 chooses the same tokens with the same scores, to the
     # different summation order of the one- and multi-column products (a last-bit difference
-    # can round a cached K/V value to the neighbouring fp16 value: 2e-4)
+    # can round a cached K/V value to the neighbouring fp16 value: 2e-4); past 8 columns the
+    # plain products take the matrix-core path, whose fp16 weights are its 1e-3 bar
+    tol = 2e-4 if B <= 8 else 1e-3
     one = Decoder(w, batch=1)
     try:
         for b in range(B):
             one.prefill(prompts[b], 0.8, 1.5)
             s0 = one.logits()
-            assert rel_l2(s0, scores[0][b]) < 2e-4
+            assert rel_l2(s0, scores[0][b]) < tol
             one.decode(n_new - 1, 0.8, 1.5)
             assert np.array_equal(one.tokens(n_prompt, n_new), toks[b])
     finally:
