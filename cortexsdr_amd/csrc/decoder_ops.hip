@@ -1113,6 +1113,9 @@ AttnShape attn_shape(int B, int Hq, int Hkv, int hd, int T, bool kv32 = false) {
         a.GW = a.G == 1 ? 1 : 4;
         a.zsplit = (a.G + a.GW - 1) / a.GW;
         a.S = std::min(attn_split_len(B, Hkv, a.zsplit, T), kAttnMaxS32);
+        // fewer than 256 workgroups at that length: 64-position splits (cfg4, 2 KV heads x 640
+        // positions: 20 workgroups; 771 -> 784 decode tokens/s; 32 positions: 751)
+        if ((long long)B * Hkv * a.zsplit * ((T + a.S - 1) / a.S) < 256) a.S = std::min(a.S, 64);
         a.nsplit = (T + a.S - 1) / a.S;
         return a;
     }
