@@ -8,15 +8,17 @@
 //
 // Decode: W[r][k] = sum_j c_j * D[idx_j][k] in fp32 over the row's slots, with the dictionary
 // held in LDS as fp16 (K <= 1024 atoms: 128 KiB), then rounded to fp16 for the MFMA
-// (v_mfma_f32_16x16x16f16, fp32 accumulation). X is fp16 as given, or split into fp16
-// hi + lo parts for fp32 input (two MFMAs). The two fp16 roundings (D, decoded W) keep the
-// product within ~2e-4 relative L2 of the fp32 decode.
+// (v_mfma_f32_16x16x32_f16, fp32 accumulation; gfx950 runs it at full rate, the 16-deep
+// form at half). X is fp16 as given, or split into fp16 hi + lo parts for fp32 input (two
+// MFMAs). The two fp16 roundings (D, decoded W) keep the product within ~2e-4 relative L2
+// of the fp32 decode.
 //
-// Layout. MFMA 16x16x16: lane l holds A[l%16][4(l/16)+i], B[4(l/16)+i][l%16] and the
-// result D[4(l/16)+i][l%16] (i = 0..3). Every 64-long k range (one block column) is stored
-// permuted, k = 16s + 4q + i at position 16q + 4s + i, in both the LDS dictionary and the
-// transposed X, so lane l (q = l/16) reads its 16 k values for the four 16-deep MFMA steps
-// as one contiguous 32-byte run.
+// Layout. Every 64-long k range (one block column) is stored permuted (kperm64), in both the
+// LDS dictionary and the transposed X, so that lane l (q = l/16) reads 16 consecutive
+// positions 16q .. 16q + 15 as one contiguous 32-byte run; the block's two 32-deep MFMA steps
+// take positions 16q + 8c .. + 7 (c = 0, 1) as lane group q's 8 k values in both operands
+// (any common bijection of k leaves the product unchanged). The result: lane l holds rows
+// 4(l/16) + i (i = 0..3) of column l % 16.
 //
 // Launches: an init kernel (Y = bias (+ Y when accumulating) + the fp32 edge strip times X,
 // and X transposed to fp16 [m][k] with the permutation, in the workspace), then one
@@ -42,10 +44,9 @@ constexpr int kMaxMTile = 256;
 constexpr int kGroup = 8;
 constexpr int kMfmaMinM = 2;  // smallest batch routed to this path (M = 1: the P-path GEMV)
 
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 struct MDesc {
     const uint32_t* codes;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
         __syncthreads();
         if (u + 1 < u1) prefetch(u + 1);
         // decode this lane's 16 k values of its two rows (fp32 sums of fp16 atoms)
-        half4 a[2][4];
+        half8 a[2][2];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             float w[16];
@@ -291,11 +292,12 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
                 }
             }
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                a[rt][s] = half4{(_Float16)w[4 * s], (_Float16)w[4 * s + 1],
-                                 (_Float16)w[4 * s + 2], (_Float16)w[4 * s + 3]};
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[rt][c][i] = (_Float16)w[8 * c + i];
         }
-        // MFMA over the four 16-deep steps of the block column
+        // two 32-deep steps over the block column: lane group q holds positions 16 q + 8 c ..
+        // + 7 of the permuted k order in step c, in both operands
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int n = nt * 16 + rl;
@@ -303,19 +305,15 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
 #pragma unroll
             for (int part = 0; part < (XS ? 2 : 1); ++part) {
                 const _Float16* xrow = Xs + (size_t)part * MT * 64 + n * 64;
-                const u32x4 b0 = *reinterpret_cast<const u32x4*>(xrow + g0 * 8);
-                const u32x4 b1 = *reinterpret_cast<const u32x4*>(xrow + g1 * 8);
-                half4 bs[4];
-                bs[0] = __builtin_bit_cast(half4, u32x2{b0[0], b0[1]});
-                bs[1] = __builtin_bit_cast(half4, u32x2{b0[2], b0[3]});
-                bs[2] = __builtin_bit_cast(half4, u32x2{b1[0], b1[1]});
-                bs[3] = __builtin_bit_cast(half4, u32x2{b1[2], b1[3]});
+                half8 bs[2];
+                bs[0] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g0 * 8));
+                bs[1] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g1 * 8));
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                for (int c = 0; c < 2; ++c)
 #pragma unroll
                     for (int rt = 0; rt < 2; ++rt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                            a[rt][s], bs[s], acc[rt][nt], 0, 0, 0);
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            a[rt][c], bs[c], acc[rt][nt], 0, 0, 0);
             }
         }
     }
