@@ -130,10 +130,10 @@ __device__ __forceinline__ int find_matrix(const MParams& p, int u, int g) {
 // 32 rows (strip = 32 W rows). The codes and X slice of unit u + 1 are loaded into registers
 // while unit u is decoded and multiplied. One workgroup per CU (the dictionary fills most of
 // the LDS), so latency is hidden by the W waves of that workgroup.
-template <int NT, bool XS, int W>
+template <int NT, bool XS, int W, int RT>
 __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     constexpr int kThreads = W * 64;
-    constexpr int kStripRows = W * 32;
+    constexpr int kStripRows = W * 16 * RT;
     extern __shared__ __attribute__((aligned(16))) _Float16 smem16[];
     constexpr int MT = NT * 16;
     constexpr int NGR = MT * 8 * (XS ? 2 : 1);  // 16-byte X granules per unit
@@ -151,9 +151,9 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     _Float16* Xs = smem16 + (size_t)kMaxAtoms * 64;  // MT x 64 (hi), then MT x 64 (lo)
     const int M = p.M;
 
-    floatx4 acc[2][NT];
+    floatx4 acc[RT][NT];
     u32x4 xr[GPT];   // prefetched X granules of the next unit
-    u32x4 cr[2][4];  // prefetched code words of the next unit (2 row tiles, <= 16 slots)
+    u32x4 cr[RT][4];  // prefetched code words of the next unit (RT row tiles, <= 16 slots)
     int ng = -1, nstrip = 0, nb = 0;  // the prefetched unit
 
     auto prefetch = [&](int u) {
@@ -173,8 +173,8 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
                 d.xt + part * nxt + (size_t)(p.m0 + mrow) * d.C_full + (size_t)nb * 64 + gr * 8);
         }
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int r = min(nstrip * kStripRows + wave * 32 + rt * 16 + rl, d.R - 1);
+        for (int rt = 0; rt < RT; ++rt) {
+            const int r = min(nstrip * kStripRows + wave * 16 * RT + rt * 16 + rl, d.R - 1);
             const uint32_t* cw =
                 d.codes + csdr::tile_word_offset(r, nb, d.R, d.NB, d.NBc, d.slots);
 #pragma unroll
@@ -186,8 +186,8 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     auto flush = [&](int g, int strip) {
         const MDesc& d = p.m[g];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int rbase = strip * kStripRows + wave * 32 + rt * 16 + q * 4;
+        for (int rt = 0; rt < RT; ++rt) {
+            const int rbase = strip * kStripRows + wave * 16 * RT + rt * 16 + q * 4;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int m = p.m0 + nt * 16 + rl;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
         if (g != cur_g || strip != cur_strip) {
             if (cur_strip >= 0) flush(cur_g, cur_strip);
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
             if (g != cur_g) {
@@ -249,9 +249,9 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
             *reinterpret_cast<u32x4*>(Xs + (size_t)part * MT * 64 + mrow * 64 +
                                       ((gr ^ (mrow & 7)) * 8)) = xr[i];
         }
-        u32x4 cc[2][4];
+        u32x4 cc[RT][4];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int j4 = 0; j4 < 4; ++j4) cc[rt][j4] = cr[rt][j4];
         const int slots = d.slots;
@@ -261,9 +261,9 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
         __syncthreads();
         if (u + 1 < u1) prefetch(u + 1);
         // decode this lane's 16 k values of its two rows (fp32 sums of fp16 atoms)
-        half8 a[2][2];
+        half8 a[RT][2];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
             float w[16];
 #pragma unroll
             for (int t = 0; t < 16; ++t) w[t] = 0.0f;
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
-                    for (int rt = 0; rt < 2; ++rt)
+                    for (int rt = 0; rt < RT; ++rt)
                         acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             a[rt][c], bs[c], acc[rt][nt], 0, 0, 0);
             }
@@ -334,16 +334,21 @@ size_t xt_bytes(const csdr_hsdb* s, int M) {
     return csdr::align_up(2 * mpad * s->C_full * sizeof(_Float16), 256);
 }
 
-// Waves per workgroup for a column tile of 16 NT: more waves hide more load latency; the
-// register budget (accumulators grow with NT) caps it.
-constexpr int waves_for(int nt) { return nt <= 1 ? 16 : (nt <= 4 ? 8 : 4); }
+// Waves per workgroup and 16-row tiles per wave for a column tile of 16 NT: more waves hide
+// more load latency and let one wave's decode run beside another's matrix-core steps; the
+// register budget (accumulators grow with NT and RT) caps them. Measured on cfg2 against two
+// row tiles per wave (16 waves to 16 columns, 8 to 64, 4 beyond): one row tile, 16 waves to
+// 64 columns and 8 beyond: M = 32 / 64 / 128 / 256 at 4096 x 11008: 47.1 -> 44.0, 58.6 ->
+// 52.2, 78.2 -> 68.7, 105.5 -> 98.6 us (M = 16 unchanged).
+constexpr int waves_for(int nt) { return nt <= 4 ? 16 : 8; }
+constexpr int rows_for(int) { return 1; }
 
 template <int NT, bool XS>
 int launch_one(const MParams& p, int grid, size_t lds, hipStream_t st) {
-    constexpr int W = waves_for(NT);
-    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W>);
+    constexpr int W = waves_for(NT), RT = rows_for(NT);
+    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W, RT>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    mfma_kernel<NT, XS, W><<<grid, W * 64, lds, st>>>(p);
+    mfma_kernel<NT, XS, W, RT><<<grid, W * 64, lds, st>>>(p);
     CSDR_LAUNCH_CHECK("hsdb mfma");
     return CSDR_OK;
 }
@@ -441,7 +446,14 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
     if (lds > (size_t)lds_max)
         return set_error(CSDR_E_UNSUPPORTED, "hsdb_matmul: LDS too small for the MFMA path");
     const int nt = mt / 16;
-    const int strip_rows = 32 * waves_for(nt);
+    int strip_rows = 16 * 2 * waves_for(1);
+    switch (nt) {
+        case 16: strip_rows = 16 * rows_for(16) * waves_for(16); break;
+        case 8: strip_rows = 16 * rows_for(8) * waves_for(8); break;
+        case 4: strip_rows = 16 * rows_for(4) * waves_for(4); break;
+        case 2: strip_rows = 16 * rows_for(2) * waves_for(2); break;
+        default: strip_rows = 16 * rows_for(1) * waves_for(1); break;
+    }
     int units = 0;
     for (int i = 0; i < n; ++i) {
         MDesc& d = p.m[i];
