@@ -89,6 +89,9 @@ def test_rope_kv(gpu, pos):
     (1, 2000, 1999, 32, 2, 128),  # 16 query heads per KV head, six splits
     (3, 700, None, 12, 4, 64),    # three query heads per KV head, ragged lengths
     (1, 48, 37, 6, 3, 128),       # a length that is not a multiple of 16
+    (8, 4096, None, 32, 32, 128), # config 5 shape, batch 8 (several rounds of splits),
+                                  # ragged lengths
+    (6, 2000, None, 16, 16, 64),  # the same at head size 64
 ])
 @pytest.mark.parametrize("mfma", ["1", "0"])
 def test_attn_decode(gpu, B, T, L, Hq, Hkv, hd, mfma, monkeypatch):
