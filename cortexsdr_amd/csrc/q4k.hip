@@ -13,10 +13,11 @@
 //   interleaved order: element i of the super-block is byte i/2, low nibble when i is even.
 //
 // Kernels
-//   q4k_gemv_kernel (M == 1): one wave per row. Every lane takes one 16-byte piece of a
-//     super-block's quants plus the block header (the 8 lanes of a block read the same 16
-//     header bytes), so a wave load instruction covers 8 whole blocks. x is staged in LDS.
-//     Per piece: y += d*sc*(sum q*x) - dmin*m*(sum x) in fp32 (q stays an exact integer).
+//   q4k_gemv_kernel (M == 1): 16 waves per workgroup, a wave per row at a time; a lane takes
+//     one 32-byte quant group of a super-block plus the block header, so a wave step covers
+//     16 blocks, and a wave keeps up to 2 steps in flight. x is staged once per workgroup in a
+//     lane-major LDS layout with the sub-block sums of x. Per group:
+//     y += d*sc*(sum q*x) - dmin*m*(sum x), the products exact and summed in fp32.
 //   q4k_mm_kernel (M > 1): a workgroup owns 16 RT rows and a range of super-blocks (split K);
 //     each wave holds RT 16-row tiles and takes every 4th super-block of the range (the next
 //     one's loads issued before the current one is multiplied). Per
@@ -41,7 +42,6 @@ using csdr::set_error;
 
 constexpr int kThreads = 256;
 constexpr int kBlockBytes = 144;
-constexpr int kUnroll = 4;  // 8-block steps per wave issued back to back (gemv)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -69,129 +69,328 @@ __device__ __forceinline__ void scale_min(const u32x4& hdr, int j, float& sc, fl
 __device__ __forceinline__ float hdr_d(const u32x4& h) { return csdr::h2f(h.x & 0xFFFFu); }
 __device__ __forceinline__ float hdr_dmin(const u32x4& h) { return csdr::h2f(h.x >> 16); }
 
-// x (C elements, C % 256 == 0, 16-byte aligned) -> LDS in 16-byte pieces, up to 8 pieces
-// per thread in flight per batch (one batch covers C <= 64K fp16 / 32K fp32 values).
+// ---------------------------------------------------------------- M == 1
+//
+// A workgroup of 16 waves owns 16 rpw rows (rpw consecutive rows per wave). A wave step covers
+// 16 super-blocks of one row: lane l takes block l / 4 of the step and its 32-byte quant group
+// g = l % 4 (64 values, sub-blocks 2g and 2g+1 in both element orders), loading the block
+// header and the group with three 16-byte loads. Each wave keeps RING steps in flight,
+// issuing step t + RING as soon as step t is multiplied, and runs straight on from one of
+// its rows into the next.
+//
+// x is staged once per workgroup in a lane-major layout, so each lane reads its values with
+// 16-byte LDS reads that no two lanes of a wave share a bank for: chunk k (k = 0..7) of lane
+// l holds the x values of quant bytes 4k .. 4k+3 of its group, ordered to match how a quant
+// dword splits into value pairs. With fp16 x two nibbles masked in place (w & 0x000F000F,
+// w & 0x00F000F0) are two fp16 subnormals, q * 2^-24 or q * 2^-20, so one v_dot2_f32_f16
+// takes two exact products into an fp32 sum; the powers of two go into d. With fp32 x the
+// nibbles are converted with v_cvt_f32_ubyteN and multiplied in fp32. The per-sub-block sums
+// of x for the dmin * m term are formed once, at staging.
+constexpr int kGvWaves = 16;
+constexpr int kRawBufferDword3 = 0x00020000;  // raw buffer resource word 3 (bounds-checked)
+constexpr int kGvThreads = 64 * kGvWaves;
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// 16-byte LDS chunks per lane per 16-block step: 8 with fp16 x, 16 with fp32 (lo and hi halves)
 template <typename XT>
-__device__ __forceinline__ void stage_x(const XT* __restrict__ x, int C, XT* xs) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(x);
-    u32x4* dst = reinterpret_cast<u32x4*>(xs);
-    const int n16 = C * (int)sizeof(XT) / 16;
-    for (int i0 = 0; i0 < n16; i0 += kThreads * 8) {
-        u32x4 v[8];
+constexpr int gv_chunks() {
+    return sizeof(XT) == 2 ? 8 : 16;
+}
+
+// LDS bytes of the staged x and sub-block sums for nblk super-blocks
+template <typename XT>
+size_t gv_lds_bytes(int nblk) {
+    const size_t ng = (size_t)(nblk + 15) / 16;
+    return ng * gv_chunks<XT>() * 64 * 16 + ng * 16 * 8 * sizeof(float);
+}
+
+// One quant dword (bytes b0..b3) of a lane's group against its staged x chunk, into a
+// low-nibble sum sl and a high-nibble sum sh.
+// fp16 chunk: pairs (b0.lo, b2.lo) (b0.hi, b2.hi) (b1.lo, b3.lo) (b1.hi, b3.hi). A nibble
+// masked in place is an fp16 subnormal: a low nibble at bits 0-3 is q * 2^-24, a high one at
+// bits 4-7 is q * 2^-20, so sl gathers sum q x * 2^-24 and sh sum q x * 2^-20 exactly.
+__device__ __forceinline__ void gv_dot_h(uint32_t w, const u32x4& xc, float& sl, float& sh) {
+    const uint32_t w8 = w >> 8;
+    const half2v p0 = __builtin_bit_cast(half2v, w & 0x000F000Fu);
+    const half2v p1 = __builtin_bit_cast(half2v, w & 0x00F000F0u);
+    const half2v p2 = __builtin_bit_cast(half2v, w8 & 0x000F000Fu);
+    const half2v p3 = __builtin_bit_cast(half2v, w8 & 0x00F000F0u);
+    // (the x dwords go through named copies: a bit cast of a vector element expression
+    // reads element 0 with this compiler)
+    const uint32_t x0 = xc.x, x1 = xc.y, x2 = xc.z, x3 = xc.w;
+    sl = __builtin_amdgcn_fdot2(p0, __builtin_bit_cast(half2v, x0), sl, false);
+    sh = __builtin_amdgcn_fdot2(p1, __builtin_bit_cast(half2v, x1), sh, false);
+    sl = __builtin_amdgcn_fdot2(p2, __builtin_bit_cast(half2v, x2), sl, false);
+    sh = __builtin_amdgcn_fdot2(p3, __builtin_bit_cast(half2v, x3), sh, false);
+}
+// byte I of w as a float (one v_cvt_f32_ubyteI)
+template <int I>
+__device__ __forceinline__ float ub(uint32_t w) {
+    return (float)((w >> (8 * I)) & 0xFFu);
+}
+// fp32 chunks: lo = x of the low nibbles of b0..b3, hi = of the high nibbles
+__device__ __forceinline__ void gv_dot_f(uint32_t w, const floatx4& lo, const floatx4& hi,
+                                         float& s0, float& s1) {
+    const uint32_t a = w & 0x0F0F0F0Fu, b = (w >> 4) & 0x0F0F0F0Fu;
+    s0 = fmaf(ub<0>(a), lo.x, s0);
+    s0 = fmaf(ub<1>(a), lo.y, s0);
+    s0 = fmaf(ub<2>(a), lo.z, s0);
+    s0 = fmaf(ub<3>(a), lo.w, s0);
+    s1 = fmaf(ub<0>(b), hi.x, s1);
+    s1 = fmaf(ub<1>(b), hi.y, s1);
+    s1 = fmaf(ub<2>(b), hi.z, s1);
+    s1 = fmaf(ub<3>(b), hi.w, s1);
+}
+
+// Scales and mins of sub-blocks j = 2g and 2g + 1 (the same unpacking as scale_min, for a pair)
+__device__ __forceinline__ void scale_min_pair(const u32x4& hdr, int g, float& sc0, float& m0,
+                                               float& sc1, float& m1) {
+    const int sh = (g & 1) * 16;  // byte (2g) & 3 of the scale words
+    const uint32_t Y = hdr.y >> sh, Z = hdr.z >> sh, Wd = hdr.w >> sh;
+    // sub-blocks 0-3 keep 6 bits in one byte, 4-7 split them over two; both forms are formed
+    // and one selected (a lane's g never changes, and a branch would split the wave)
+    const uint32_t la0 = Y & 63u, la1 = (Y >> 8) & 63u, lb0 = Z & 63u, lb1 = (Z >> 8) & 63u;
+    const uint32_t ha0 = (Wd & 15u) | ((Y >> 2) & 48u);
+    const uint32_t ha1 = ((Wd >> 8) & 15u) | ((Y >> 10) & 48u);
+    const uint32_t hb0 = ((Wd >> 4) & 15u) | ((Z >> 2) & 48u);
+    const uint32_t hb1 = ((Wd >> 12) & 15u) | ((Z >> 10) & 48u);
+    const bool low = g < 2;
+    sc0 = (float)(low ? la0 : ha0);
+    sc1 = (float)(low ? la1 : ha1);
+    m0 = (float)(low ? lb0 : hb0);
+    m1 = (float)(low ? lb1 : hb1);
+}
+
+// x -> LDS in the lane-major chunk layout, and the 32-value sub-block sums of x. An item is
+// (block, group g, chunk k), 32 per block, k fastest so that the 8 items of a (block, g) sit
+// in 8 neighbouring lanes and their partial sums meet by lane exchange. Chunk index
+// ((G * CH + k) * 64 + l) for 16-block group G and lane l = 4 (block % 16) + g; with fp32 x
+// chunk k is two LDS chunks, 2k (low-nibble values) and 2k + 1 (high).
+constexpr int kStageItems = 2;  // items per thread per staging batch
+
+struct GvStageRaw {
+    u32x4 a, b;
+};
+
+template <int ORDER, typename XT>
+__device__ __forceinline__ void gv_stage_load(const XT* __restrict__ x, int nblk, int batch,
+                                              GvStageRaw (&raw)[kStageItems]) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = src[min(i0 + j * kThreads + (int)threadIdx.x, n16 - 1)];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = i0 + j * kThreads + threadIdx.x;
-            if (i < n16) dst[i] = v[j];
+    for (int j = 0; j < kStageItems; ++j) {
+        const int it = (batch * kStageItems + j) * kGvThreads + threadIdx.x;
+        const int blk = min(it >> 5, nblk - 1), g = (it >> 3) & 3, k = it & 7;
+        const XT* xb = x + (size_t)blk * 256 + 64 * g;
+        if constexpr (sizeof(XT) == 2) {
+            if (ORDER == 0) {
+                const uint2 lo = *reinterpret_cast<const uint2*>(xb + 4 * k);
+                const uint2 hi = *reinterpret_cast<const uint2*>(xb + 32 + 4 * k);
+                raw[j].a = u32x4{lo.x, lo.y, hi.x, hi.y};
+            } else {
+                raw[j].a = *reinterpret_cast<const u32x4*>(xb + 8 * k);
+            }
+        } else {
+            const int o0 = ORDER == 0 ? 4 * k : 8 * k, o1 = ORDER == 0 ? 32 + 4 * k : 8 * k + 4;
+            raw[j].a = *reinterpret_cast<const u32x4*>(xb + o0);
+            raw[j].b = *reinterpret_cast<const u32x4*>(xb + o1);
         }
     }
-}
-
-// sum over 16 consecutive x values of q_i * x_i (q = nibble NIB of byte i of `q`) and of x_i
-template <typename XT, int NIB>
-__device__ __forceinline__ void dot16(const u32x4& q, const XT* xp, float& sq, float& sx) {
-    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float xv = csdr::to_f32(xp[wi * 4 + b]);
-            const float qv = (float)((w4[wi] >> (8 * b + 4 * NIB)) & 0xFu);
-            sq = fmaf(qv, xv, sq);
-            sx += xv;
-        }
-}
-
-// 32 interleaved values: byte i -> elements 2i (low nibble), 2i+1 (high nibble)
-template <typename XT>
-__device__ __forceinline__ void dot32i(const u32x4& q, const XT* xp, float& sq, float& sx) {
-    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int i = wi * 4 + b;
-            const float x0 = csdr::to_f32(xp[2 * i]), x1 = csdr::to_f32(xp[2 * i + 1]);
-            const uint32_t byte = (w4[wi] >> (8 * b)) & 0xFFu;
-            sq = fmaf((float)(byte & 0xFu), x0, sq);
-            sq = fmaf((float)(byte >> 4), x1, sq);
-            sx += x0 + x1;
-        }
 }
 
 template <int ORDER, typename XT>
-__global__ __launch_bounds__(kThreads) void q4k_gemv_kernel(const uint8_t* __restrict__ W, int R,
-                                                            int nblk, const XT* __restrict__ x,
-                                                            float* __restrict__ y,
-                                                            int rows_per_wave) {
-    extern __shared__ unsigned char smem_raw[];
-    XT* xs = reinterpret_cast<XT*>(smem_raw);
-    const int C = nblk * 256;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int piece = lane & 7;  // which 16 bytes of the block's quants
-    const int bl = lane >> 3;    // which of the 8 blocks of a step
-    const int row0 = (blockIdx.x * (kThreads / 64) + wave) * rows_per_wave;
-    auto load_step = [&](int r, int b0, u32x4 (&hdr)[kUnroll], u32x4 (&qs)[kUnroll]) {
-        const uint8_t* rowp = W + (size_t)min(r, R - 1) * nblk * kBlockBytes;
+__device__ __forceinline__ void gv_stage_store(int nblk, int batch,
+                                               const GvStageRaw (&raw)[kStageItems], u32x4* xs,
+                                               float* sums) {
+    constexpr int CH = gv_chunks<XT>();
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int blk = min(b0 + u * 8 + bl, nblk - 1);
-            const u32x4* bp = reinterpret_cast<const u32x4*>(rowp + (size_t)blk * kBlockBytes);
-            hdr[u] = __builtin_nontemporal_load(bp);
-            qs[u] = __builtin_nontemporal_load(bp + 1 + piece);
-        }
-    };
-    // the first weight loads go out before x is staged (they overlap the staging latency)
-    u32x4 hdr0[kUnroll], qs0[kUnroll];
-    load_step(row0, 0, hdr0, qs0);
-    stage_x(x, C, xs);
-    __syncthreads();
-    for (int rr = 0; rr < rows_per_wave; ++rr) {
-        const int r = row0 + rr;
-        if (r >= R) break;
-        float acc = 0.0f;
-        for (int b0 = 0; b0 < nblk; b0 += 8 * kUnroll) {
-            u32x4 hdr[kUnroll], qs[kUnroll];
-            if (rr == 0 && b0 == 0) {
-#pragma unroll
-                for (int u = 0; u < kUnroll; ++u) {
-                    hdr[u] = hdr0[u];
-                    qs[u] = qs0[u];
-                }
+    for (int j = 0; j < kStageItems; ++j) {
+        const int it = (batch * kStageItems + j) * kGvThreads + threadIdx.x;
+        const int blk = it >> 5, g = (it >> 3) & 3, k = it & 7;
+        const bool valid = blk < nblk;
+        const int G = blk >> 4, l = (blk & 15) * 4 + g;
+        float s0, s1;  // ggml: low- and high-nibble values; interleaved: all 8 (s0)
+        if constexpr (sizeof(XT) == 2) {
+            const u32x4 e = raw[j].a;
+            u32x4 out;
+            if (ORDER == 0) {  // e = lo0 lo1 lo2 lo3 hi0 hi1 hi2 hi3
+                out.x = __builtin_amdgcn_perm(e.y, e.x, 0x05040100u);
+                out.y = __builtin_amdgcn_perm(e.w, e.z, 0x05040100u);
+                out.z = __builtin_amdgcn_perm(e.y, e.x, 0x07060302u);
+                out.w = __builtin_amdgcn_perm(e.w, e.z, 0x07060302u);
+            } else {  // e = 8 consecutive values: lo t = value 2t, hi t = value 2t + 1
+                out.x = __builtin_amdgcn_perm(e.z, e.x, 0x05040100u);
+                out.y = __builtin_amdgcn_perm(e.z, e.x, 0x07060302u);
+                out.z = __builtin_amdgcn_perm(e.w, e.y, 0x05040100u);
+                out.w = __builtin_amdgcn_perm(e.w, e.y, 0x07060302u);
+            }
+            if (valid) xs[(G * CH + k) * 64 + l] = out;
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 v = __builtin_bit_cast(h8, e);
+            const float a = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+            const float b = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
+            s0 = ORDER == 0 ? a : a + b;
+            s1 = b;
+        } else {
+            const floatx4 a = __builtin_bit_cast(floatx4, raw[j].a);
+            const floatx4 b = __builtin_bit_cast(floatx4, raw[j].b);
+            floatx4 lo, hi;
+            if (ORDER == 0) {
+                lo = a;
+                hi = b;
             } else {
-                load_step(r, b0, hdr, qs);
+                lo = floatx4{a.x, a.z, b.x, b.z};
+                hi = floatx4{a.y, a.w, b.y, b.w};
             }
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int blk = b0 + u * 8 + bl;
-                if (blk >= nblk) continue;
-                const float d = hdr_d(hdr[u]), dmin = hdr_dmin(hdr[u]);
-                const XT* xb = xs + (size_t)blk * 256;
-                if (ORDER == 0) {
-                    const int g = piece >> 1, h = piece & 1;
-                    float sc0, m0, sc1, m1;
-                    scale_min(hdr[u], 2 * g, sc0, m0);
-                    scale_min(hdr[u], 2 * g + 1, sc1, m1);
-                    float sq0 = 0.f, sx0 = 0.f, sq1 = 0.f, sx1 = 0.f;
-                    dot16<XT, 0>(qs[u], xb + 64 * g + 16 * h, sq0, sx0);
-                    dot16<XT, 1>(qs[u], xb + 64 * g + 32 + 16 * h, sq1, sx1);
-                    acc += (d * sc0) * sq0 - (dmin * m0) * sx0;
-                    acc += (d * sc1) * sq1 - (dmin * m1) * sx1;
-                } else {
-                    float sc, m;
-                    scale_min(hdr[u], piece, sc, m);
-                    float sq = 0.f, sx = 0.f;
-                    dot32i<XT>(qs[u], xb + 32 * piece, sq, sx);
-                    acc += (d * sc) * sq - (dmin * m) * sx;
-                }
+            if (valid) {
+                xs[(G * CH + 2 * k) * 64 + l] = __builtin_bit_cast(u32x4, lo);
+                xs[(G * CH + 2 * k + 1) * 64 + l] = __builtin_bit_cast(u32x4, hi);
             }
+            const float sl = (lo.x + lo.y) + (lo.z + lo.w), sh = (hi.x + hi.y) + (hi.z + hi.w);
+            s0 = ORDER == 0 ? sl : sl + sh;
+            s1 = sh;
         }
-        acc = csdr::wave_sum(acc);
-        if (lane == 0) y[r] = acc;
+        // sub-block sums: ggml sums s0 / s1 over the 8 chunks of (block, g) into sub-blocks
+        // 2g / 2g + 1; interleaved sums s0 over chunks 0-3 (sub-block 2g) and 4-7 (2g + 1)
+        s0 += __shfl_xor(s0, 1);
+        s0 += __shfl_xor(s0, 2);
+        if (ORDER == 0) {
+            s1 += __shfl_xor(s1, 1);
+            s1 += __shfl_xor(s1, 2);
+            s0 += __shfl_xor(s0, 4);
+            s1 += __shfl_xor(s1, 4);
+            if (valid && k == 0) reinterpret_cast<float2*>(sums)[blk * 4 + g] = float2{s0, s1};
+        } else {
+            if (valid && (k & 3) == 0) sums[blk * 8 + 2 * g + (k >> 2)] = s0;
+        }
     }
 }
+
+struct GvSlot {
+    u32x4 h, q0, q1;
+};
+
+template <int ORDER, typename XT, int RING>
+__global__ __launch_bounds__(kGvThreads) void q4k_gemv_kernel(const uint8_t* __restrict__ W, int R,
+                                                              int nblk, const XT* __restrict__ x,
+                                                              float* __restrict__ y, int rpw) {
+    constexpr int CH = gv_chunks<XT>();
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_smem[];
+    const int spr = (nblk + 15) >> 4;  // wave steps per row (at least RING)
+    u32x4* xs = reinterpret_cast<u32x4*>(gv_smem);
+    float* sums = reinterpret_cast<float*>(gv_smem + (size_t)spr * CH * 64 * 16);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int bl = lane >> 2, g = lane & 3;
+    const int row0 = (blockIdx.x * kGvWaves + wave) * rpw;
+    const int nrows = max(0, min(rpw, R - row0));
+    const int T = nrows * spr;  // this wave's steps: none, or at least RING
+    // The wave's rows are read through a raw buffer resource bounded to them, so that a lane
+    // past a row's last block loads without a branch (and gets zeros without touching
+    // memory). A wave with rows has at least RING steps, so the first RING loads, and those
+    // of the steady-state loop below, are unconditional: the compiler then waits for exactly
+    // the step being multiplied. (A wave without rows loads zeros only.)
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W + (size_t)min(row0, R - 1) * nblk * kBlockBytes), (short)0,
+        nrows * nblk * kBlockBytes, kRawBufferDword3);
+    int lr = 0, ls = 0;  // row and step of the next load
+    auto load = [&](GvSlot& sl) {
+        const int blk = ls * 16 + bl;
+        const uint32_t off = blk < nblk ? (uint32_t)(lr * nblk + blk) * kBlockBytes : 0x80000000u;
+        sl.h = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        sl.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 + 32 * g, 0, 0);
+        sl.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32 + 32 * g, 0, 0);
+        if (++ls == spr) {
+            ls = 0;
+            ++lr;
+        }
+    };
+    int cr = 0, cs = 0;  // row and step being multiplied
+    float acc = 0.0f;
+    auto step = [&](const GvSlot& sl) {
+        const int blk = cs * 16 + bl;
+        // per-nibble sums: ggml puts low nibbles in sub-block 2g (a0, a1) and high ones in
+        // 2g + 1 (b0, b1); interleaved puts dwords 0-3 in 2g (low a0, high a1) and 4-7 in
+        // 2g + 1 (b0, b1)
+        float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+        const uint32_t qd[8] = {sl.q0.x, sl.q0.y, sl.q0.z, sl.q0.w,
+                                sl.q1.x, sl.q1.y, sl.q1.z, sl.q1.w};
+        const u32x4* xc = xs + (size_t)cs * CH * 64 + lane;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float& u0 = ORDER == 0 ? ((c & 1) ? a1 : a0) : (c < 4 ? a0 : b0);
+            float& u1 = ORDER == 0 ? ((c & 1) ? b1 : b0) : (c < 4 ? a1 : b1);
+            if constexpr (sizeof(XT) == 2) {
+                gv_dot_h(qd[c], xc[c * 64], u0, u1);
+            } else {
+                const floatx4 lo = __builtin_bit_cast(floatx4, xc[(2 * c) * 64]);
+                const floatx4 hi = __builtin_bit_cast(floatx4, xc[(2 * c + 1) * 64]);
+                gv_dot_f(qd[c], lo, hi, u0, u1);
+            }
+        }
+        // sub-block sums of q x (fp16 x: high-nibble sums carry 2^-20 where low ones 2^-24)
+        constexpr float kH = sizeof(XT) == 2 ? 0.0625f : 1.0f;
+        const float A = ORDER == 0 ? a0 + a1 : a0 + kH * a1;
+        const float B = ORDER == 0 ? kH * (b0 + b1) : b0 + kH * b1;
+        float sc0, m0, sc1, m1;
+        scale_min_pair(sl.h, g, sc0, m0, sc1, m1);
+        const float d = hdr_d(sl.h) * (sizeof(XT) == 2 ? 16777216.0f : 1.0f);
+        const float dm = hdr_dmin(sl.h);
+        const float2 sx = reinterpret_cast<const float2*>(sums)[min(blk, nblk - 1) * 4 + g];
+        const float part =
+            ((d * sc0) * A - (dm * m0) * sx.x) + ((d * sc1) * B - (dm * m1) * sx.y);
+        acc += blk < nblk ? part : 0.0f;
+        if (++cs == spr) {
+            acc = csdr::wave_sum(acc);
+            if (lane == 0) y[row0 + cr] = acc;
+            acc = 0.0f;
+            cs = 0;
+            ++cr;
+        }
+    };
+    // x's first staging batch goes out first, then the weight steps, so that staging waits
+    // only for its own loads
+    GvStageRaw raw[kStageItems];
+    gv_stage_load<ORDER, XT>(x, nblk, 0, raw);
+    // Only the first step goes out before the barrier: every wave's first step is then
+    // ahead of any wave's second in the memory pipeline
+    GvSlot ring[RING];
+    load(ring[0]);
+    gv_stage_store<ORDER, XT>(nblk, 0, raw, xs, sums);
+    const int nbatch = (nblk * 32 + kGvThreads * kStageItems - 1) / (kGvThreads * kStageItems);
+    for (int b = 1; b < nbatch; ++b) {
+        gv_stage_load<ORDER, XT>(x, nblk, b, raw);
+        gv_stage_store<ORDER, XT>(nblk, b, raw, xs, sums);
+    }
+    __syncthreads();
+    if (T == 0) return;  // (no barriers below)
+#pragma unroll
+    for (int k = 1; k < RING; ++k) load(ring[k]);
+    int t0 = 0;
+    for (; t0 + 2 * RING <= T; t0 += RING) {  // every step's follow-up load is in range
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            step(ring[k]);
+            load(ring[k]);
+        }
+    }
+    for (; t0 < T; t0 += RING) {  // the last steps: loads only up to step T - 1
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            if (t0 + k < T) step(ring[k]);
+            if (t0 + k + RING < T) load(ring[k]);
+        }
+    }
+}
+
+template <typename T>
+struct TypeTag {
+    using type = T;
+};
+
+// Steps a wave keeps in flight for rows of spr steps: at most spr, so that a wave with rows
+// has at least that many. Measured at 4096 x 14336, fp16 x (4 steps per row): 9.9 us with
+// two, 10.1 with one, 10.8 with four (a wave's steps queue ahead of other waves' first ones).
+int gv_ring_for(int spr) { return spr >= 2 ? 2 : 1; }
 
 // ---------------------------------------------------------------- M > 1, split-K MFMA
 
@@ -417,31 +616,44 @@ CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void*
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     const int nblk = C / 256;
     if (M == 1) {
-        const int rpw = R >= 8192 ? 2 : 1;
-        const int grid = (R + (kThreads / 64) * rpw - 1) / ((kThreads / 64) * rpw);
+        // rows per wave: one round of at most 256 workgroups (one per CU) of 16 waves
+        const int rpw = (R + 16 * 256 - 1) / (16 * 256);
+        const int grid = (R + kGvWaves * rpw - 1) / (kGvWaves * rpw);
         if (reinterpret_cast<uintptr_t>(x) % 16)
             return set_error(CSDR_E_INVALID, "q4k_linear: x must be 16-byte aligned");
+        // a wave's rows (and the steps it loads past them) are addressed with 32-bit offsets
+        if ((size_t)(rpw + 4) * nblk * kBlockBytes >= ((size_t)1 << 31))
+            return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: rows too long for M = 1");
+        const auto* wp = static_cast<const uint8_t*>(w);
+        auto go = [&](auto kern, size_t lds, const auto* xp) -> int {
+            if (lds > 160 * 1024) return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: C too large");
+            if (lds > 64 * 1024)
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            kern<<<grid, kGvThreads, lds, st>>>(wp, R, nblk, xp, y, rpw);
+            return CSDR_OK;
+        };
+        const int ring = gv_ring_for((nblk + 15) / 16);
+        auto pick = [&](auto ord, auto xt) -> int {
+            constexpr int O = decltype(ord)::value;
+            using XT = typename decltype(xt)::type;
+            const auto* xp = static_cast<const XT*>(x);
+            const size_t lds = gv_lds_bytes<XT>(nblk);
+            return ring == 1 ? go(q4k_gemv_kernel<O, XT, 1>, lds, xp)
+                             : go(q4k_gemv_kernel<O, XT, 2>, lds, xp);
+        };
+        using G = std::integral_constant<int, 0>;
+        using I = std::integral_constant<int, 1>;
         if (x_dtype == CSDR_F16) {
-            const size_t lds = (size_t)C * 2;
-            if (lds > 160 * 1024) return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: C too large");
-            if (order == CSDR_Q4K_GGML)
-                q4k_gemv_kernel<0, _Float16><<<grid, kThreads, lds, st>>>(
-                    static_cast<const uint8_t*>(w), R, nblk, static_cast<const _Float16*>(x), y, rpw);
-            else
-                q4k_gemv_kernel<1, _Float16><<<grid, kThreads, lds, st>>>(
-                    static_cast<const uint8_t*>(w), R, nblk, static_cast<const _Float16*>(x), y, rpw);
+            using H = TypeTag<_Float16>;
+            rc = order == CSDR_Q4K_GGML ? pick(G{}, H{}) : pick(I{}, H{});
         } else if (x_dtype == CSDR_F32) {
-            const size_t lds = (size_t)C * 4;
-            if (lds > 160 * 1024) return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: C too large");
-            if (order == CSDR_Q4K_GGML)
-                q4k_gemv_kernel<0, float><<<grid, kThreads, lds, st>>>(
-                    static_cast<const uint8_t*>(w), R, nblk, static_cast<const float*>(x), y, rpw);
-            else
-                q4k_gemv_kernel<1, float><<<grid, kThreads, lds, st>>>(
-                    static_cast<const uint8_t*>(w), R, nblk, static_cast<const float*>(x), y, rpw);
+            using F = TypeTag<float>;
+            rc = order == CSDR_Q4K_GGML ? pick(G{}, F{}) : pick(I{}, F{});
         } else {
             return set_error(CSDR_E_INVALID, "q4k_linear: x_dtype must be CSDR_F32 or CSDR_F16");
         }
+        if (rc) return rc;
     } else {
         if (x_dtype != CSDR_F16)
             return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: M > 1 takes fp16 x");

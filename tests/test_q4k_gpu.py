@@ -1,7 +1,8 @@
 """GPU parity of the Q4_K dequant-matmul (HK5) against the CPU oracle, through the C-ABI.
 
 Bar: dequantised values bit-exact (same arithmetic order as the reference); products at
-relative L2 <= 1e-3 (fp32 accumulation)."""
+relative L2 <= 1e-3 where W is rounded to fp16 for the matrix cores (M > 1), <= 1e-5 for the
+M = 1 product (exact products, fp32 sums)."""
 import functools
 
 import numpy as np
@@ -45,6 +46,11 @@ def test_dequant_bitexact(gpu, order):
     (300, 1024, 5, "interleaved", np.float16),
     (37, 256, 1, "ggml", np.float32),
     (37, 512, 70, "ggml", np.float16),        # more than 64 columns: two column groups
+    (4096, 4096, 1, "interleaved", np.float16),
+    (8200, 2048, 1, "interleaved", np.float16),  # three rows per wave, ragged last workgroup
+    (64, 18432, 1, "ggml", np.float16),       # two x staging batches, partial last wave step
+    (96, 18432, 1, "interleaved", np.float32),  # fp32 x: more than 64 KiB of LDS
+    (40, 4352, 1, "ggml", np.float32),        # 17 super-blocks: one block in the last step
 ])
 def test_linear(gpu, R, C, M, order, xdt):
     from cortexsdr_amd import q4k
@@ -56,7 +62,7 @@ def test_linear(gpu, R, C, M, order, xdt):
     ref = oracle.q4k_linear(blob, R, C, x.astype(np.float32), ORDERS[order])
     err = rel_l2(y, ref)
     print(f"R={R} C={C} M={M} {order} rel_l2={err:.3e}")
-    assert err <= 1e-3
+    assert err <= (1e-4 if M == 1 else 1e-3)
 
 
 def test_kat_blocks_through_gpu(gpu):
