@@ -15,11 +15,11 @@
 // when that is not finite or below 1e-12). q4_k is served by q4k.hip and also here.
 //
 // Kernels (a template per format, so each decode is straight-line code)
-//   gguf_gemv_lds_kernel (M == 1): one wave per row; the row's blocks staged in LDS with
-//     coalesced loads, then lane l takes values 8 g .. 8 g + 7 for g = l, l + 64, ... of the
-//     row, decodes them from their block (Dec8: the block's header read once for the 8) and
-//     multiplies by x in fp32; gguf_gemv_kernel is the same from memory, for the 8-bit
-//     formats and rows longer than the LDS budget.
+//   gguf_gemv_lds_kernel (M == 1): one wave per row; the row's bytes staged in LDS with
+//     16-byte loads all in flight at once, then lane l takes values 8 g .. 8 g + 7 for
+//     g = l, l + 64, ... of the row, decodes them from their block (Dec8: the block's header
+//     read once for the 8) and multiplies by x in fp32; gguf_gemv_kernel is the same from
+//     memory, for the 8-bit formats and rows longer than the LDS budget.
 //   gguf_mm_kernel (M > 1, fp16 X): split-K over 256-element steps of the row, 16 RT rows per
 //     workgroup, the 4 waves taking every 4th step. A wave stages its rows' bytes of a step in
 //     LDS with dword loads issued one step ahead (a row's step need not start 4-byte aligned),
@@ -429,16 +429,17 @@ __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* _
     }
 }
 
-// M == 1 with the row staged in LDS: each wave copies its row's blocks with coalesced dword
-// loads (byte loads when the row is not 4-byte aligned), then decodes from LDS as
-// gguf_gemv_kernel does from memory (the per-element header and quant bytes are LDS reads
-// instead of scattered vector-memory loads).
-constexpr size_t kGemvLdsMax = 64 * 1024;
+// M == 1 with the row staged in LDS. A workgroup's 4 waves take a row each; a wave copies its
+// row's bytes with 16-byte loads from the 16-byte boundary at or below the row's start, all of
+// them issued before the first is waited for. Lane l then decodes values 8 g .. 8 g + 7 for
+// g = l, l + 64, ... from its block in LDS (Dec8: the block's header read once for the 8) and
+// multiplies them by x in fp32 (x read through the caches: staging it in LDS per workgroup
+// of 4 rows measured slower, 4096 x 14336 q4_0 19.2 us against 17.9).
+constexpr int kRowLoads = 16;  // 16-byte row loads per lane in flight (16 KiB per wave)
 
 // Whether a format's M == 1 product stages its rows in LDS: yes where an element's decode reads
-// several scattered bytes (measured at 4096 x 4096: q5_k 36.7 -> 20.4 us, q6_k 25.8 -> 24.5,
-// q4_0 16.4 -> 15.5), no for the 8-bit formats (one byte and the scale per element; q8_0
-// 15.1 -> 18.0 us staged).
+// several scattered bytes, no for the 8-bit formats (one byte and the scale per element; q8_0
+// at 4096 x 14336: 25.3 us from memory against 29.3 staged).
 template <class F>
 struct StageRow {
     static constexpr bool value = true;
@@ -456,35 +457,70 @@ struct StageRow<Q8_K> {
     static constexpr bool value = false;
 };
 
+// LDS bytes of one wave's row slot (the row plus the up to 15 bytes before it)
+template <class F>
+size_t gv_row_slot(int C) {
+    return ((size_t)(C / F::BE) * F::BB + 15 + 15) & ~(size_t)15;
+}
+
 template <class F, typename XT>
 __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* __restrict__ W,
                                                                  int R, int C,
                                                                  const XT* __restrict__ x,
                                                                  float* __restrict__ y,
-                                                                 int aligned4, int xvec) {
-    extern __shared__ uint8_t srow[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                                                 int slot, int xvec) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int r = blockIdx.x * (kThreads / 64) + wave;
-    const int rowbytes = (C / F::BE) * F::BB, stride = (rowbytes + 3) & ~3;
-    uint8_t* my = srow + (size_t)wave * stride;
-    if (r < R) {
-        const uint8_t* rowp = W + (size_t)r * rowbytes;
-        if (aligned4) {
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp);
-            uint32_t* dst = reinterpret_cast<uint32_t*>(my);
-            for (int i = lane; i < rowbytes / 4; i += 64) dst[i] = src[i];
-        } else {
-            for (int i = lane; i < rowbytes; i += 64) my[i] = rowp[i];
-        }
+    const size_t rowbytes = (size_t)(C / F::BE) * F::BB;
+    // The row from the 16-byte boundary (of the address) at or below its start, in 16-byte
+    // pieces up to the boundary at or above its end. A 16-byte aligned piece never crosses a
+    // page, so the bytes it holds outside W share a page with bytes of W.
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
+    const uintptr_t start = wa + (size_t)min(r, R - 1) * rowbytes, a0 = start & ~(uintptr_t)15;
+    const uintptr_t wend = (wa + (size_t)R * rowbytes + 15) & ~(uintptr_t)15;
+    const int lead = (int)(start - a0), npiece = (int)((lead + rowbytes + 15) >> 4);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(a0), (short)0, (int)min(wend - a0, (uintptr_t)0x7FFFFFF0),
+        0x00020000);
+    uint8_t* my = gsm + (size_t)wave * slot;
+    u32x4* myv = reinterpret_cast<u32x4*>(my);
+    u32x4 v[kRowLoads];
+    const bool has_row = r < R;
+    const int np = has_row ? npiece : 0;
+    auto load = [&](int p) {  // piece p of the row, or zeros past its end
+        return __builtin_amdgcn_raw_buffer_load_b128(
+            rs, p < np ? (uint32_t)p * 16 : 0x80000000u, 0, 0);
+    };
+    // the row in batches of kRowLoads pieces per lane
+#pragma unroll
+    for (int i = 0; i < kRowLoads; ++i)
+        if (i * 64 < np) v[i] = load(i * 64 + lane);
+#pragma unroll
+    for (int i = 0; i < kRowLoads; ++i)
+        if (i * 64 + lane < np) myv[i * 64 + lane] = v[i];
+    for (int p0 = kRowLoads * 64; p0 < np; p0 += kRowLoads * 64) {
+#pragma unroll
+        for (int i = 0; i < kRowLoads; ++i)
+            if (p0 + i * 64 < np) v[i] = load(p0 + i * 64 + lane);
+#pragma unroll
+        for (int i = 0; i < kRowLoads; ++i)
+            if (p0 + i * 64 + lane < np) myv[p0 + i * 64 + lane] = v[i];
     }
-    __syncthreads();
-    if (r >= R) return;  // (no barriers below)
+    if (!has_row) return;
+    // the row slot is this wave's own: its copy needs only a wave-level ordering
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint8_t* row = my + lead;
     float acc = 0.0f;
 #pragma unroll 2
     for (int g = lane; g < (C >> 3); g += 64) {
         const int e0 = g << 3, b = e0 / F::BE;
         float w8[8], xv[8];
-        Dec8<F>::run(my + (size_t)b * F::BB, e0 - b * F::BE, w8);
+        Dec8<F>::run(row + (size_t)b * F::BB, e0 - b * F::BE, w8);
         x8(x, e0, xvec, xv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], xv[i], acc);
@@ -505,16 +541,19 @@ int linear_of(const uint8_t* w, int R, int C, const void* x, int x_dtype, int M,
     if (M == 1) {
         const int grid = (R + kThreads / 64 - 1) / (kThreads / 64);
         const int xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
-        const size_t rowbytes = (size_t)(C / F::BE) * F::BB;
-        const size_t lds = (kThreads / 64) * ((rowbytes + 3) & ~(size_t)3);
-        if (StageRow<F>::value && lds <= kGemvLdsMax) {
-            const int a4 = (rowbytes % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 4 == 0);
+        const size_t slot = gv_row_slot<F>(C);
+        const size_t lds = (kThreads / 64) * slot;
+        if (StageRow<F>::value && lds <= 160 * 1024) {
+            auto go = [&](auto kern, const auto* xp) {
+                if (lds > 64 * 1024)
+                    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                kern<<<grid, kThreads, lds, st>>>(w, R, C, xp, y, (int)slot, xvec);
+            };
             if (x_dtype == CSDR_F16)
-                gguf_gemv_lds_kernel<F, _Float16><<<grid, kThreads, lds, st>>>(
-                    w, R, C, static_cast<const _Float16*>(x), y, a4, xvec);
+                go(gguf_gemv_lds_kernel<F, _Float16>, static_cast<const _Float16*>(x));
             else
-                gguf_gemv_lds_kernel<F, float><<<grid, kThreads, lds, st>>>(
-                    w, R, C, static_cast<const float*>(x), y, a4, xvec);
+                go(gguf_gemv_lds_kernel<F, float>, static_cast<const float*>(x));
         } else if (x_dtype == CSDR_F16)
             gguf_gemv_kernel<F, _Float16><<<grid, kThreads, 0, st>>>(
                 w, R, C, static_cast<const _Float16*>(x), y, xvec);

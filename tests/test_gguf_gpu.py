@@ -79,6 +79,28 @@ def test_linear_m1(gpu, fmt, R, nblk):
     assert rel_l2(yh, ref_h) <= TOL
 
 
+@pytest.mark.parametrize("fmt,R,Cc", [
+    ("q6_k", 64, 24576),   # 20160-byte rows: two batches of row loads, over 64 KiB of LDS
+    ("q4_0", 40, 4128),    # 2322-byte rows: rows start off 16-byte boundaries
+    ("q8_0", 48, 14336),
+    ("q5_k", 33, 14336),
+])
+def test_linear_m1_long_rows(gpu, fmt, R, Cc):
+    from cortexsdr_amd import gguf
+
+    rng = np.random.default_rng(300 + F[fmt])
+    _, be = oracle.gguf_block(F[fmt])
+    w = blocks(fmt, R * Cc // be, rng)
+    wd = _dev(gpu, w.ravel())
+    for dt in (np.float32, np.float16):
+        x = rng.normal(size=(1, Cc)).astype(dt)
+        ref = oracle.gguf_linear(w.ravel(), F[fmt], R, Cc, x.astype(np.float32))
+        y = gguf.linear(wd, F[fmt], R, Cc, _dev(gpu, x)).cpu().numpy()
+        err = rel_l2(y, ref)
+        print(f"{fmt} R={R} C={Cc} {np.dtype(dt).name}: rel_l2={err:.2e}", flush=True)
+        assert err <= TOL
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q5_1", "q8_0", "q6_k", "q4_k", "q3_k"])
 @pytest.mark.parametrize("M", [3, 17, 64])
 def test_linear_batched(gpu, fmt, M):
