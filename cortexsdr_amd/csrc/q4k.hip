@@ -18,15 +18,12 @@
 //     16 blocks, and a wave keeps up to 2 steps in flight. x is staged once per workgroup in a
 //     lane-major LDS layout with the sub-block sums of x. Per group:
 //     y += d*sc*(sum q*x) - dmin*m*(sum x), the products exact and summed in fp32.
-//   q4k_mm_kernel (M > 1): a workgroup owns 16 RT rows and a range of super-blocks (split K);
-//     each wave holds RT 16-row tiles and takes every 4th super-block of the range (the next
-//     one's loads issued before the current one is multiplied). Per
-//     32-element sub-block a lane dequantises its 8 values of each row tile in fp32
-//     ((d*sc)*q - dmin*m, one fused multiply-add) and rounds them to fp16 once, and each
-//     16-column tile of X (fp16, read straight into the B operand, 16 bytes per lane) takes
-//     one v_mfma_f32_16x16x32_f16 (fp32 accumulate). The waves' tiles are summed through LDS
-//     and added into Y (zeroed by a fill launch) with one atomic per output per workgroup.
-//     The single fp16 rounding of W puts the product about 3e-4 (relative L2) from fp32.
+//   q4k_mm_kernel (M > 1): 8 waves own 128 rows and a range of super-blocks (split K). Per
+//     super-block a lane forms q * sc for 8 values of each sub-block of its row as exact fp16
+//     subnormals, and v_mfma_f32_16x16x32_f16 multiplies them with fp16 X (staged in LDS in
+//     the matching k order) into an fp32 tile scaled by d per super-block; the dmin * m term
+//     is a second small product with the sub-block sums of X. No rounding of W: the product
+//     is within about 1e-6 (relative L2) of fp32. Workgroups of one row range add into Y.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -392,176 +389,231 @@ struct TypeTag {
 // two, 10.1 with one, 10.8 with four (a wave's steps queue ahead of other waves' first ones).
 int gv_ring_for(int spr) { return spr >= 2 ? 2 : 1; }
 
-// ---------------------------------------------------------------- M > 1, split-K MFMA
-
-// Launch shape of q4k_mm_kernel: RT 16-row tiles per wave (16 RT rows per workgroup) and KB
-// super-blocks per workgroup for NT 16-column tiles. Measured on cfg3 (4096 x 4096 and
-// 4096 x 14336, M = 16 / 32 / 64, including the fill launch): up to 32 columns two row tiles
-// and 8 super-blocks (16 past 32 super-blocks per row): 13.5 / 32.4 us at M = 32 against
-// 16.4 / 39.8 for four tiles and 4. At 64 columns four tiles and 16 super-blocks halve the
-// partial-sum atomics (43.0 us at 4096 x 14336 against 57.6) while that still gives 256
-// workgroups; below that (4096 x 4096: 64 workgroups, 33.3 us) two tiles and 8 (20.8 us).
-void q4k_mm_shape(int R, int nblk, int NT, int& RT, int& KB) {
-    RT = 2;
-    KB = nblk > 32 ? 16 : 8;
-    if (NT >= 4 && (size_t)((R + 63) / 64) * (size_t)((nblk + 15) / 16) >= 256) {
-        RT = 4;
-        KB = 16;
-    }
-}
-
 __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__ y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n;
          i += (size_t)gridDim.x * kThreads)
         y[i] = 0.0f;
 }
 
-// 8 quant values of sub-block s for this lane (k = 8 j .. 8 j + 7 of the sub-block, j = lane
-// group) as bytes, from the block's quants (ggml: the 8-byte piece of group s / 2, low nibbles
-// for even s; interleaved: the 4-byte piece of sub-block s, nibbles low / high alternating).
-template <int ORDER>
-__device__ __forceinline__ void quant8(const uint32_t* q, int s, uint32_t& w0, uint32_t& w1) {
-    if (ORDER == 0) {
-        const int sh = (s & 1) * 4;
-        w0 = (q[2 * (s >> 1)] >> sh) & 0x0F0F0F0Fu;
-        w1 = (q[2 * (s >> 1) + 1] >> sh) & 0x0F0F0F0Fu;
-    } else {
-        const uint32_t v = q[s];
-        const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
-        // element order lo.b0 hi.b0 lo.b1 hi.b1 | lo.b2 hi.b2 lo.b3 hi.b3 as bytes
-        w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-        w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-    }
+// ---------------------------------------------------------------- M > 1, exact quants
+//
+// A workgroup of 8 waves owns 128 rows (a 16-row tile per wave), the range of super-blocks
+// blockIdx.y covers (split K) and 16 NT columns. Per super-block every wave multiplies its
+// tile on v_mfma_f32_16x16x32_f16 with W as the B operand (k x rows) and X as A (columns x k),
+// so each output element a lane holds belongs to the lane's own W row:
+//   * a lane (row rl = l % 16, k-slice j = l / 16) takes the 8 values 8j .. 8j + 7 of each
+//     32-element sub-block s of its row; q * sc (at most 15 * 63 = 945) is formed as a pair of
+//     16-bit integers with one v_pk_mul_lo_u16 and read as two fp16 subnormals q * sc * 2^-24,
+//     exact, so the 8 sub-blocks of a super-block accumulate in one fp32 D tile;
+//   * the min term sum_s m_s * (sum of x over s) is one more product, of the sub-block sums
+//     of X (split into fp16 hi + lo parts, two steps) with m_s (6-bit, exact in fp16);
+//   * per super-block: acc += (d * 2^24) * D - dmin * Dm in fp32.
+// The k order inside a lane's 8 values follows how a quant dword splits into value pairs; X
+// is staged in LDS in the same order, one super-block ahead (two buffers), with the
+// sub-block sums. Workgroups of one row range add their partial sums into Y (zeroed first).
+constexpr int kMmWaves = 8;
+constexpr int kMmThreads = 64 * kMmWaves;
+constexpr int kMmRows = 16 * kMmWaves;
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// 16-byte LDS chunks of one super-block buffer: per column tile 8 X tiles and 2 sum tiles
+template <int NT>
+constexpr int mm_buf_chunks() {
+    return NT * 10 * 64;
 }
 
-template <int ORDER, int NT, int RT>
-__global__ __launch_bounds__(kThreads) void q4k_mm_kernel(const uint8_t* __restrict__ W, int R,
-                                                          int nblk, const _Float16* __restrict__ X,
-                                                          int M, float* __restrict__ Y, int KB) {
-    __shared__ floatx4 red[3][RT][NT][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// x values e0..e7 (dwords d = (e0,e1) (e2,e3) (e4,e5) (e6,e7)) in the order the quant pairs
+// take them: ggml (e0,e2) (e1,e3) (e4,e6) (e5,e7), interleaved (e0,e4) (e1,e5) (e2,e6) (e3,e7)
+template <int ORDER>
+__device__ __forceinline__ u32x4 mm_x_order(const u32x4& d) {
+    u32x4 o;
+    if (ORDER == 0) {
+        o.x = __builtin_amdgcn_perm(d.y, d.x, 0x05040100u);
+        o.y = __builtin_amdgcn_perm(d.y, d.x, 0x07060302u);
+        o.z = __builtin_amdgcn_perm(d.w, d.z, 0x05040100u);
+        o.w = __builtin_amdgcn_perm(d.w, d.z, 0x07060302u);
+    } else {
+        o.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+        o.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+        o.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+        o.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+    }
+    return o;
+}
+
+// one nibble pair (bits 0-3 and 16-19 of v) times the sub-block scale, as two fp16 subnormals
+__device__ __forceinline__ uint32_t mm_qs(uint32_t v, uint32_t sc2) {
+    const u16x2 q = __builtin_bit_cast(u16x2, v & 0x000F000Fu);
+    return __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(u16x2, sc2));
+}
+
+template <int ORDER, int NT>
+__global__ __launch_bounds__(kMmThreads) void q4k_mm_kernel(const uint8_t* __restrict__ W, int R,
+                                                            int nblk, const _Float16* __restrict__ X,
+                                                            int M, float* __restrict__ Y, int KB) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char mm_smem[];
+    u32x4* xl = reinterpret_cast<u32x4*>(mm_smem);  // [2][mm_buf_chunks<NT>()]
+    constexpr int kBuf = mm_buf_chunks<NT>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int rl = lane & 15, j = lane >> 4;
-    const int r0 = blockIdx.x * (16 * RT);
+    const int r0 = blockIdx.x * kMmRows + wave * 16;
     const int b0 = blockIdx.y * KB, b1 = min(nblk, b0 + KB);
     const int n0 = blockIdx.z * 16 * NT;
     const int C = nblk * 256;
-    floatx4 acc[RT][NT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const _Float16* xr[NT];
-    bool xl[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int n = n0 + nt * 16 + rl;
-        xl[nt] = n < M;
-        xr[nt] = X + (size_t)min(n, M - 1) * C + 8 * j;
+    // the sum tiles hold values at k < 8 only (lanes 0-15): zero the rest once
+    for (int i = threadIdx.x; i < 2 * NT * 2 * 48; i += kMmThreads) {
+        const int l = 16 + i % 48, t = i / 48;  // t: buffer * 2 NT + nt * 2 + hi/lo
+        const int buf = t / (2 * NT), nt = (t / 2) % NT, hl = t & 1;
+        xl[buf * kBuf + (nt * 10 + 8 + hl) * 64 + l] = u32x4{0u, 0u, 0u, 0u};
     }
-    const uint8_t* wr[RT];
+    // X staging: piece p = (column, sub-block, k-slice), 16 NT * 32 per super-block, NT per
+    // thread
+    auto stage_load = [&](int b, u32x4 (&xr)[NT]) {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-        wr[rt] = W + (size_t)min(r0 + rt * 16 + rl, R - 1) * nblk * kBlockBytes;
-    // a block's header and this lane's quants of every row tile
+        for (int i = 0; i < NT; ++i) {
+            const int p = i * kMmThreads + threadIdx.x;
+            const int col = n0 + (p >> 5), s = (p >> 2) & 7, jj = p & 3;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(X + (size_t)min(col, M - 1) * C +
+                                                            (size_t)b * 256 + 32 * s + 8 * jj);
+            xr[i] = col < M ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto stage_store = [&](int buf, const u32x4 (&xr)[NT]) {
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const int p = i * kMmThreads + threadIdx.x;
+            const int c = p >> 5, s = (p >> 2) & 7, jj = p & 3;
+            const int nt = c >> 4, l = (c & 15) + 16 * jj;
+            xl[buf * kBuf + (nt * 10 + s) * 64 + l] = mm_x_order<ORDER>(xr[i]);
+            // the sub-block sum of this column: 4 neighbouring threads hold its 4 slices
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 v = __builtin_bit_cast(h8, xr[i]);
+            float sm = (((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3])) +
+                       (((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]));
+            sm += __shfl_xor(sm, 1);
+            sm += __shfl_xor(sm, 2);
+            if (jj == 0) {
+                const _Float16 hi = (_Float16)sm;
+                const _Float16 lo = (_Float16)(sm - (float)hi);
+                _Float16* th = reinterpret_cast<_Float16*>(xl + buf * kBuf + (nt * 10 + 8) * 64);
+                _Float16* tl = reinterpret_cast<_Float16*>(xl + buf * kBuf + (nt * 10 + 9) * 64);
+                th[(c & 15) * 8 + s] = hi;
+                tl[(c & 15) * 8 + s] = lo;
+            }
+        }
+    };
+    // this lane's bytes of a super-block of its row: header, and per sub-block pair (ggml) or
+    // sub-block (interleaved) the 8 or 4 bytes of its k-slice
     struct Blk {
-        u32x4 hdr[RT];
-        uint32_t q[RT][8];
+        u32x4 hdr;
+        uint32_t q[8];
     };
-    auto load_blk = [&](int blk, Blk& o) {
+    const uint8_t* wrow = W + (size_t)min(r0 + rl, R - 1) * nblk * kBlockBytes;
+    auto load_blk = [&](int b, Blk& o) {
+        const uint8_t* bp = wrow + (size_t)b * kBlockBytes;
+        o.hdr = *reinterpret_cast<const u32x4*>(bp);
+        if (ORDER == 0) {
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const uint8_t* bp = wr[rt] + (size_t)blk * kBlockBytes;
-            o.hdr[rt] = *reinterpret_cast<const u32x4*>(bp);
+            for (int g = 0; g < 4; ++g) {
+                const uint2 v = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * j);
+                o.q[2 * g] = v.x;
+                o.q[2 * g + 1] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                o.q[s] = *reinterpret_cast<const uint32_t*>(bp + 16 + 16 * s + 4 * j);
+        }
+    };
+    floatx4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf, const Blk& cb) {
+        // B operands: q * sc per sub-block, and m at k = s for the min product
+        half8 bq[8];
+        float scf[8], mnf[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) scale_min(cb.hdr, s, scf[s], mnf[s]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t sc = (uint32_t)scf[s], sc2 = sc | (sc << 16);
+            uint32_t w0, w1;  // this lane's 8 (ggml) or 4 (interleaved) bytes of sub-block s
             if (ORDER == 0) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const uint2 v = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * j);
-                    o.q[rt][2 * g] = v.x;
-                    o.q[rt][2 * g + 1] = v.y;
-                }
+                const int sh = (s & 1) * 4;  // odd sub-blocks: high nibbles
+                w0 = cb.q[2 * (s >> 1)] >> sh;
+                w1 = cb.q[2 * (s >> 1) + 1] >> sh;
+                bq[s] = __builtin_bit_cast(
+                    half8, u32x4{mm_qs(w0, sc2), mm_qs(w0 >> 8, sc2), mm_qs(w1, sc2),
+                                 mm_qs(w1 >> 8, sc2)});
             } else {
-#pragma unroll
-                for (int sb = 0; sb < 8; ++sb)
-                    o.q[rt][sb] = *reinterpret_cast<const uint32_t*>(bp + 16 + 16 * sb + 4 * j);
+                w0 = cb.q[s];
+                bq[s] = __builtin_bit_cast(
+                    half8, u32x4{mm_qs(w0, sc2), mm_qs(w0 >> 4, sc2), mm_qs(w0 >> 8, sc2),
+                                 mm_qs(w0 >> 12, sc2)});
             }
+        }
+        half8 bm;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) bm[s] = j == 0 ? (_Float16)mnf[s] : (_Float16)0.0f;
+        const float d24 = hdr_d(cb.hdr) * 16777216.0f, dm = hdr_dmin(cb.hdr);
+        const u32x4* xb = xl + buf * kBuf + lane;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            floatx4 D = {0.f, 0.f, 0.f, 0.f}, Dm = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const half8 a = __builtin_bit_cast(half8, xb[(nt * 10 + s) * 64]);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[s], D, 0, 0, 0);
+            }
+            const half8 ah = __builtin_bit_cast(half8, xb[(nt * 10 + 8) * 64]);
+            const half8 al = __builtin_bit_cast(half8, xb[(nt * 10 + 9) * 64]);
+            Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bm, Dm, 0, 0, 0);
+            Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bm, Dm, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nt][i] += d24 * D[i] - dm * Dm[i];
         }
     };
-    auto compute_blk = [&](int blk, const Blk& cb) {
-#pragma unroll
-        for (int sb = 0; sb < 8; ++sb) {
-            half8 bv[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const half8 v = *reinterpret_cast<const half8*>(xr[nt] + (size_t)blk * 256 + 32 * sb);
-                bv[nt] = xl[nt] ? v : half8{};
-            }
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                float sc, mn;
-                scale_min(cb.hdr[rt], sb, sc, mn);
-                const float ds = hdr_d(cb.hdr[rt]) * sc, dm = hdr_dmin(cb.hdr[rt]) * mn;
-                uint32_t w0, w1;
-                quant8<ORDER>(cb.q[rt], sb, w0, w1);
-                half8 a;
-                a[0] = (_Float16)fmaf(ds, (float)((w0 >> 0) & 0xFFu), -dm);
-                a[1] = (_Float16)fmaf(ds, (float)((w0 >> 8) & 0xFFu), -dm);
-                a[2] = (_Float16)fmaf(ds, (float)((w0 >> 16) & 0xFFu), -dm);
-                a[3] = (_Float16)fmaf(ds, (float)((w0 >> 24) & 0xFFu), -dm);
-                a[4] = (_Float16)fmaf(ds, (float)((w1 >> 0) & 0xFFu), -dm);
-                a[5] = (_Float16)fmaf(ds, (float)((w1 >> 8) & 0xFFu), -dm);
-                a[6] = (_Float16)fmaf(ds, (float)((w1 >> 16) & 0xFFu), -dm);
-                a[7] = (_Float16)fmaf(ds, (float)((w1 >> 24) & 0xFFu), -dm);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[nt], acc[rt][nt], 0, 0, 0);
-            }
-        }
-    };
-    // every 4th block of the range; the next block's loads go out before this one is
-    // multiplied (two buffers, named, so that both stay in registers)
-    int blk = b0 + wave;
-    if (blk < b1) {
-        Blk ba, bb;
-        load_blk(blk, ba);
-        for (;;) {
-            const int nb1 = blk + kThreads / 64;
-            if (nb1 < b1) load_blk(nb1, bb);
-            compute_blk(blk, ba);
-            if (nb1 >= b1) break;
-            const int nb2 = nb1 + kThreads / 64;
-            if (nb2 < b1) load_blk(nb2, ba);
-            compute_blk(nb1, bb);
-            if (nb2 >= b1) break;
-            blk = nb2;
-        }
-    }
-    // the 4 waves' tiles: waves 1..3 park theirs in LDS, wave 0 sums and adds into Y
-    if (wave > 0) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) red[wave - 1][rt][nt][lane] = acc[rt][nt];
+    // the range's super-blocks, two at a time (named buffers keep both in registers); X and
+    // W of the next super-block are loaded while this one is multiplied
+    Blk ba, bb;
+    u32x4 xa[NT], xb2[NT];
+    if (b0 < b1) {
+        stage_load(b0, xa);
+        load_blk(b0, ba);
+        stage_store(0, xa);
     }
     __syncthreads();
-    if (wave == 0) {
+    for (int b = b0; b < b1; b += 2) {
+        if (b + 1 < b1) {
+            stage_load(b + 1, xb2);
+            load_blk(b + 1, bb);
+        }
+        compute(0, ba);
+        if (b + 1 < b1) stage_store(1, xb2);
+        __syncthreads();
+        if (b + 1 >= b1) break;
+        if (b + 2 < b1) {
+            stage_load(b + 2, xa);
+            load_blk(b + 2, ba);
+        }
+        compute(1, bb);
+        if (b + 2 < b1) stage_store(0, xa);
+        __syncthreads();
+    }
+    // D tile: this lane holds columns 4 j + i of its row rl
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+    for (int nt = 0; nt < NT; ++nt) {
+        const int r = r0 + rl;
+        if (r >= R) continue;
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                floatx4 v = acc[rt][nt];
-#pragma unroll
-                for (int w = 0; w < 3; ++w) v += red[w][rt][nt][lane];
-                // D tile: this lane holds rows 4 j + i, column rl
-                const int n = n0 + nt * 16 + rl;
-                if (n >= M) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = r0 + rt * 16 + 4 * j + i;
-                    if (r < R)
-                        __hip_atomic_fetch_add(Y + (size_t)n * R + r, v[i], __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int n = n0 + nt * 16 + 4 * j + i;
+            if (n < M)
+                __hip_atomic_fetch_add(Y + (size_t)n * R + r, acc[nt][i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -663,25 +715,27 @@ CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void*
         const size_t ny = (size_t)M * R;
         fill_zero_kernel<<<(unsigned)std::min<size_t>((ny + kThreads - 1) / kThreads, 4096),
                            kThreads, 0, st>>>(y, ny);
-        // launch shape: row tiles per wave (RT) and super-blocks per workgroup (KB)
+        // 128-row workgroups, 16 NT columns each, and the super-blocks split so that the grid
+        // holds about 256 workgroups
         const int NT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-        int RT = 2, KB = 8;
-        q4k_mm_shape(R, nblk, NT, RT, KB);
-        dim3 grid((R + 16 * RT - 1) / (16 * RT), (nblk + KB - 1) / KB, (M + 16 * NT - 1) / (16 * NT));
+        const int gx = (R + kMmRows - 1) / kMmRows, gz = (M + 16 * NT - 1) / (16 * NT);
+        const int pk = std::max(1, std::min(nblk, (256 + gx * gz - 1) / (gx * gz)));
+        const int KB = (nblk + pk - 1) / pk;
+        dim3 grid(gx, (nblk + KB - 1) / KB, gz);
+        const size_t lds = (size_t)2 * 10 * 64 * 16 * NT;
         const auto* wp = static_cast<const uint8_t*>(w);
         const auto* xp = static_cast<const _Float16*>(x);
-        auto go = [&](auto kern) { kern<<<grid, kThreads, 0, st>>>(wp, R, nblk, xp, M, y, KB); };
+        auto go = [&](auto kern) {
+            if (lds > 64 * 1024)
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            kern<<<grid, kMmThreads, lds, st>>>(wp, R, nblk, xp, M, y, KB);
+        };
         auto pick = [&](auto ord) {
             constexpr int O = decltype(ord)::value;
-            if (RT == 4) {
-                if (NT == 1) go(q4k_mm_kernel<O, 1, 4>);
-                else if (NT == 2) go(q4k_mm_kernel<O, 2, 4>);
-                else go(q4k_mm_kernel<O, 4, 4>);
-            } else {
-                if (NT == 1) go(q4k_mm_kernel<O, 1, 2>);
-                else if (NT == 2) go(q4k_mm_kernel<O, 2, 2>);
-                else go(q4k_mm_kernel<O, 4, 2>);
-            }
+            if (NT == 1) go(q4k_mm_kernel<O, 1>);
+            else if (NT == 2) go(q4k_mm_kernel<O, 2>);
+            else go(q4k_mm_kernel<O, 4>);
         };
         if (order == CSDR_Q4K_GGML) pick(std::integral_constant<int, 0>{});
         else pick(std::integral_constant<int, 1>{});
