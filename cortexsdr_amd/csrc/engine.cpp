@@ -168,7 +168,13 @@ CortexError load(CortexInferenceEngine* e, size_t idx, Cached** out) {
     csdr_segment_info info;
     csdr_archive_info(e->ar, idx, &info);
     const std::string name = info.name;
-    std::vector<uint8_t> bytes((size_t)info.compressed_size);
+    // the size is bounded by the archive file (the index reader checks every entry against it)
+    std::vector<uint8_t> bytes;
+    try {
+        bytes.resize((size_t)info.compressed_size);
+    } catch (const std::exception&) {
+        return fail(CORTEX_ERROR_MEMORY, "out of host memory reading '" + name + "'");
+    }
     int rc = csdr_archive_read(e->ar, idx, bytes.data(), bytes.size(), nullptr);
     if (rc) return from_csdr(rc, "load '" + name + "'");
     Cached c;

@@ -169,6 +169,7 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
 #pragma unroll
                 for (int u = 0; u < kNA; ++u) {
                     const int ju = j + u * kEGroups;
+                    const float* dt = dj[u] - l16;  // the atom's row
 #pragma unroll
                     for (int t = 0; t < TT; ++t) {
                         float v = p[u][t];
@@ -176,6 +177,8 @@ __global__ __launch_bounds__(kEThreads) void mp_kernel(MpArgs a) {
                         v += __shfl_xor(v, 4, 16);  // low + high 128 bits
                         v += __shfl_xor(v, 1, 16);  // horizontal add
                         v += __shfl_xor(v, 2, 16);  // horizontal add
+                        // the last C % 8 elements: the scalar tail, in element order
+                        for (int c = C8; c < C; ++c) v = fmaf(dt[c], r[c * TT + t], v);
                         if (l16 == 0 && t < nt && ju < K)
                             proj[t * K + ju] = used[t * K + ju] ? 0.0f : v;
                     }
@@ -244,8 +247,6 @@ int mp_tiles_per_wg(long long n, int C, int K) {
 int check_mp_shape(long long n, int C, int K, int S, int k) {
     if (n < 0 || C <= 0 || K <= 0 || S <= 0 || k <= 0)
         return set_error(CSDR_E_INVALID, "hsdr_encode: bad shape");
-    if (C % 8)
-        return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: tile size must be a multiple of 8");
     if (K > 32768) return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: at most 32768 atoms");
     if (S > kMaxStages) return set_error(CSDR_E_UNSUPPORTED, "hsdr_encode: at most 32 stages");
     if (k > K) return set_error(CSDR_E_INVALID, "hsdr_encode: more picks per stage than atoms");

@@ -225,8 +225,9 @@ CSDR_API int csdr_hsdb_export_codes(const csdr_hsdb* seg, uint16_t* packed, uint
  * picked in the stage score 0), sign = +1 when that projection is >= 0, r -= scale * sign *
  * D_best. Projections are summed in the reference's AVX2 order (dot_product_simd :157-190),
  * so the picks are the reference's bit for bit. codes (device, n_tiles x n_stages *
- * k_per_stage uint16): packIndexSign (:76-80), tile-major, stage-major. tile_dim must be a
- * multiple of 8; n_atoms <= 32768; n_stages <= 32. */
+ * k_per_stage uint16): packIndexSign (:76-80), tile-major, stage-major. Any tile_dim (the
+ * last tile_dim % 8 elements are the reference's scalar tail); n_atoms <= 32768;
+ * n_stages <= 32. */
 CSDR_API int csdr_hsdr_encode(const float* tiles, size_t n_tiles, int tile_dim, const float* D,
                               int n_atoms, int n_stages, int k_per_stage,
                               const float* stage_scales, uint16_t* codes, void* hip_stream);

@@ -34,9 +34,10 @@ and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
              and 8 x 16 / 8 x 8 tiles), and matrices whose rows are random rows A, their
              reversals, and reversal-symmetric rows, so that projections onto atom pairs
              (A, reversed A) tie in exact arithmetic and the float summation order decides the
-             pick. cfg = (tile_rows, tile_cols, K, stages, k per stage). cpu_model: the CPU
-             the reference ran on (its dictionary initialisation uses that CPU's approximate
-             reciprocal square root).
+             pick; and tile sizes that are not a multiple of 8 (60, 3 x 13, 100, 5, 9, 18,
+             27, 30: the projection's scalar tail). cfg = (tile_rows, tile_cols, K, stages, k per
+             stage). cpu_model: the CPU the reference ran on (its dictionary initialisation
+             uses that CPU's approximate reciprocal square root).
   fit_<i>_w, fit_<i>_stream, fit_<i>_cfg  the same compress with ksvd_iters = 3..6 (atom
              updates and re-encodes); cfg = (tile_rows, tile_cols, K, stages, k, iters).
 
@@ -234,6 +235,17 @@ def encode_main() -> None:
         cases.append(((rng.standard_normal((R, Cc)) * 0.02).astype(np.float32), (tr, tc, K, S, k)))
     for C, seed in [(48, 3), (48, 11), (48, 12), (64, 1), (72, 2), (80, 13)]:
         cases.append((symmetric_pairs(C, seed), (1, C, 48, 2, 2)))
+    # tile sizes that are not a multiple of 8 (the projection's scalar tail, every length 1-7):
+    # 60 = 3 x 16 + 8 + 4, 3 x 13 = 39 = 2 x 16 + 7, 100 = 6 x 16 + 4, 5, 9, 18, 27 = 16 + 8 +
+    # 3, 30 = 16 + 8 + 6; own generator, so the cases above and the fit cases below keep their
+    # inputs
+    rng8 = np.random.default_rng(20261202)
+    for (R, Cc, tr, tc, K, S, k) in [(64, 60, 1, 60, 16, 2, 3), (90, 41, 3, 13, 20, 2, 2),
+                                     (48, 100, 1, 100, 32, 3, 2), (70, 5, 1, 5, 8, 2, 2),
+                                     (60, 9, 1, 9, 8, 2, 2), (60, 18, 1, 18, 8, 2, 2),
+                                     (60, 27, 1, 27, 12, 2, 2), (60, 30, 1, 30, 12, 2, 2)]:
+        cases.append(((rng8.standard_normal((R, Cc)) * 0.02).astype(np.float32),
+                      (tr, tc, K, S, k)))
     out = {}
     for i, (w, cfg) in enumerate(cases):
         tr, tc, K, S, k = cfg

@@ -50,7 +50,8 @@ def test_encode_matches_reference_fixtures(gpu, enc):
 
 @pytest.mark.parametrize("n,C,K,S,k", [(1000, 64, 256, 3, 5), (333, 200, 100, 2, 8),
                                        (40, 1024, 512, 3, 4), (7, 4096, 64, 2, 3),
-                                       (1, 8, 8, 2, 4)])
+                                       (1, 8, 8, 2, 4), (500, 60, 64, 2, 3), (300, 39, 48, 3, 2),
+                                       (64, 5, 8, 2, 2), (2000, 100, 128, 2, 4)])
 def test_encode_matches_oracle(gpu, n, C, K, S, k):
     rng = np.random.default_rng(n + C + K)
     t = (rng.standard_normal((n, C)) * 0.02).astype(np.float32)
@@ -158,5 +159,5 @@ def test_compress_rejects(gpu):
     w = np.zeros((10, 64), np.float32)
     with pytest.raises(ValueError):   # fewer tiles than atoms
         encode.compress(w, 1, 64, 16, 2, 2)
-    with pytest.raises(_lib.CsdrError):   # tile size not a multiple of 8
-        encode.compress(np.ones((64, 60), np.float32), 1, 60, 16, 2, 2)
+    with pytest.raises(_lib.CsdrError):   # K-SVD passes over tiles of more than 32768 values
+        encode.compress(np.ones((2, 40000), np.float32), 1, 40000, 1, 1, 1, ksvd_iters=1)
