@@ -457,11 +457,112 @@ struct StageRow<Q8_K> {
     static constexpr bool value = false;
 };
 
-// LDS bytes of one wave's row slot (the row plus the up to 15 bytes before it)
+// LDS bytes of one wave's row slot (the row plus the up to 15 bytes before it, and 16 more
+// for dword reads that end past the row)
 template <class F>
 size_t gv_row_slot(int C) {
-    return ((size_t)(C / F::BE) * F::BB + 15 + 15) & ~(size_t)15;
+    return ((size_t)(C / F::BE) * F::BB + 15 + 15 + 16) & ~(size_t)15;
 }
+
+// v_dot2_f32_f16 on two fp16 pairs held as dwords
+__device__ __forceinline__ float fdot2u(uint32_t a, uint32_t b, float c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+// The dword at byte offset o of LDS (any alignment): two aligned reads and a byte shift.
+__device__ __forceinline__ uint32_t lds32(const uint32_t* s32, int o) {
+    return __builtin_amdgcn_alignbyte(s32[(o >> 2) + 1], s32[o >> 2], (uint32_t)(o & 3));
+}
+
+// x[e .. e + 3] in fp32 (e % 4 == 0): one load when x is 16-byte aligned
+template <typename XT>
+__device__ __forceinline__ void x4(const XT* __restrict__ x, int e, bool vec, float* o) {
+    if (vec) {
+        if constexpr (sizeof(XT) == 2) {
+            const half4 v = *reinterpret_cast<const half4*>(x + e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (float)v[i];
+        } else {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(x + e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = v[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = csdr::to_f32(x[e + i]);
+    }
+}
+
+// Formats whose staged row is read in dword-wide units rather than 8 values at a time (Dec8):
+// kPerBlock units per block, dot() = the unit's values times x.
+template <class F>
+struct Units {
+    static constexpr bool value = false;
+};
+// q6_k (:329-359): unit u of a block = (half h, quad q): values h*128 + 32 t + 4 q + i of the
+// four quarters t (scale bytes 192 + 8 h + 2 t) and i = 0..3. The quarters' 6-bit quants come
+// from three dwords, ql[h*64 + 4q] (t = 0 low nibbles, t = 2 high), ql[h*64 + 32 + 4q] (t = 1,
+// 3) and qh[h*32 + 4q] (bit pair t of each byte), four per dword op. Per quarter
+// sum (q - 32) x = sum q x - 32 sum x, then d * sum_t sc_t * that.
+template <>
+struct Units<Q6_K> {
+    static constexpr bool value = true;
+    static constexpr int kPerBlock = 16;
+    template <typename XT>
+    __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                bool xvec) {
+        const int blk = u >> 4, h = (u >> 3) & 1, q = u & 7;
+        const int bo = ro + blk * Q6_K::BB;
+        const uint32_t qa = lds32(s32, bo + h * 64 + 4 * q);
+        const uint32_t qb = lds32(s32, bo + h * 64 + 32 + 4 * q);
+        const uint32_t qh = lds32(s32, bo + 128 + h * 32 + 4 * q);
+        const uint32_t s0 = lds32(s32, bo + 192 + h * 8), s1 = lds32(s32, bo + 196 + h * 8);
+        const float d = csdr::h2f(lds32(s32, bo + 208) & 0xFFFFu);
+        const uint32_t qt[4] = {(qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u),
+                                (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u),
+                                ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u),
+                                ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
+        const float sc[4] = {(float)(int8_t)(s0 & 0xFFu), (float)(int8_t)((s0 >> 16) & 0xFFu),
+                             (float)(int8_t)(s1 & 0xFFu), (float)(int8_t)((s1 >> 16) & 0xFFu)};
+        const int xb = blk * 256 + h * 128 + 4 * q;
+        float tot = 0.0f;
+        if constexpr (sizeof(XT) == 2) {
+            if (xvec) {
+                // fp16 x: the quants as fp16 subnormal pairs q 2^-24 (exact), one
+                // v_dot2_f32_f16 per two products and per two values of the x sum
+                typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+                constexpr uint32_t kOnes = 0x3C003C00u;  // (1.0, 1.0)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const u32x2 xw = *reinterpret_cast<const u32x2*>(x + xb + 32 * t);
+                    const uint32_t x01 = xw.x, x23 = xw.y;
+                    const uint32_t p01 = __builtin_amdgcn_perm(0u, qt[t], 0x0C010C00u);
+                    const uint32_t p23 = __builtin_amdgcn_perm(0u, qt[t], 0x0C030C02u);
+                    float a = fdot2u(p01, x01, 0.0f);
+                    a = fdot2u(p23, x23, a);
+                    float sx = fdot2u(x01, kOnes, 0.0f);
+                    sx = fdot2u(x23, kOnes, sx);
+                    tot = fmaf(sc[t], fmaf(-0x1p-19f, sx, a), tot);
+                }
+                return d * 0x1p24f * tot;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float xv[4];
+            x4(x, xb + 32 * t, xvec, xv);
+            float a = 0.0f, sx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a = fmaf((float)((qt[t] >> (8 * i)) & 0xFFu), xv[i], a);
+                sx += xv[i];
+            }
+            tot = fmaf(sc[t], fmaf(-32.0f, sx, a), tot);
+        }
+        return d * tot;
+    }
+};
 
 template <class F, typename XT>
 __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* __restrict__ W,
@@ -514,16 +615,24 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint8_t* row = my + lead;
     float acc = 0.0f;
+    if constexpr (Units<F>::value) {
+        const uint32_t* s32 = reinterpret_cast<const uint32_t*>(gsm);
+        const int ro = wave * slot + lead;
+        const int nu = (C / F::BE) * Units<F>::kPerBlock;
 #pragma unroll 2
-    for (int g = lane; g < (C >> 3); g += 64) {
-        const int e0 = g << 3, b = e0 / F::BE;
-        float w8[8], xv[8];
-        Dec8<F>::run(row + (size_t)b * F::BB, e0 - b * F::BE, w8);
-        x8(x, e0, xvec, xv);
+        for (int u = lane; u < nu; u += 64) acc += Units<F>::dot(s32, ro, u, x, xvec);
+    } else {
+        const uint8_t* row = my + lead;
+#pragma unroll 2
+        for (int g = lane; g < (C >> 3); g += 64) {
+            const int e0 = g << 3, b = e0 / F::BE;
+            float w8[8], xv[8];
+            Dec8<F>::run(row + (size_t)b * F::BB, e0 - b * F::BE, w8);
+            x8(x, e0, xvec, xv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], xv[i], acc);
+            for (int i = 0; i < 8; ++i) acc = fmaf(w8[i], xv[i], acc);
+        }
     }
     acc = csdr::wave_sum(acc);
     if (lane == 0) y[r] = acc;
