@@ -500,6 +500,131 @@ template <class F>
 struct Units {
     static constexpr bool value = false;
 };
+// x[e .. e + 7] in fp16 as four dwords of value pairs (16-byte aligned x)
+template <typename XT>
+__device__ __forceinline__ void xh8(const XT* __restrict__ x, int e, uint32_t* o) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + e);
+    o[0] = v.x;
+    o[1] = v.y;
+    o[2] = v.z;
+    o[3] = v.w;
+}
+
+constexpr uint32_t kOnesH2 = 0x3C003C00u;  // fp16 (1.0, 1.0)
+
+// q4_0 / q4_1 (:398-417): unit u = half u % 2 of block u / 2, 16 values from 8 quant bytes,
+// element i from byte i / 2 (low nibble for even i). With fp16 x each value pair (2k, 2k + 1)
+// of a quant dword becomes one exact fp16 subnormal pair q 2^-18 by a byte permute of its low
+// and high nibbles and a shift. q4_0: d * (sum q x - 8 sum x); q4_1: d * sum q x + m * sum x.
+template <bool HAS_M>
+struct UnitsQ4 {
+    static constexpr bool value = true;
+    static constexpr int kPerBlock = 2;
+    static constexpr int BB = HAS_M ? 20 : 18, kQs = HAS_M ? 4 : 2;
+    template <typename XT>
+    __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                bool xvec) {
+        const int blk = u >> 1, hf = u & 1;
+        const int bo = ro + blk * BB;
+        const uint32_t hd = lds32(s32, bo);
+        const float d = csdr::h2f(hd & 0xFFFFu);
+        const int xb = blk * 32 + hf * 16;
+        float a = 0.0f, sx = 0.0f;
+        if (sizeof(XT) == 2 && xvec) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const uint32_t w = lds32(s32, bo + kQs + hf * 8 + 4 * g);
+                const uint32_t L = w & 0x0F0F0F0Fu, H = (w >> 4) & 0x0F0F0F0Fu;
+                uint32_t xw[4];
+                xh8(x, xb + 8 * g, xw);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t pk = __builtin_amdgcn_perm(H, L, 0x0C040C00u + 0x00010001u * k)
+                                        << 6;
+                    a = fdot2u(pk, xw[k], a);
+                    sx = fdot2u(xw[k], kOnesH2, sx);
+                }
+            }
+            a *= 0x1p18f;
+        } else {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const uint32_t w = lds32(s32, bo + kQs + hf * 8 + 4 * g);
+                float xv[8];
+                x8(x, xb + 8 * g, xvec, xv);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t b = (w >> (8 * k)) & 0xFFu;
+                    a = fmaf((float)(b & 0x0Fu), xv[2 * k], a);
+                    a = fmaf((float)(b >> 4), xv[2 * k + 1], a);
+                    sx += xv[2 * k] + xv[2 * k + 1];
+                }
+            }
+        }
+        if constexpr (HAS_M) return fmaf(d, a, csdr::h2f(hd >> 16) * sx);
+        else return d * fmaf(-8.0f, sx, a);
+    }
+};
+template <>
+struct Units<Q4_0> : UnitsQ4<false> {};
+template <>
+struct Units<Q4_1> : UnitsQ4<true> {};
+
+// the generic rule (:439-465): unit u = values 16 j .. 16 j + 15 of block u / (BE / 16), two
+// groups of 8 values x BITS bits = BITS bytes each (byte aligned), read as two dwords and
+// split by funnel shifts; q - 2^(BITS-1) times the block's scale.
+template <int BB_, int BE_, int BITS>
+struct Units<Packed<BB_, BE_, BITS>> {
+    using F = Packed<BB_, BE_, BITS>;
+    static constexpr bool value = true;
+    static constexpr int kPerBlock = BE_ / 16;
+    template <typename XT>
+    __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                bool xvec) {
+        const int blk = u / kPerBlock, j = u - blk * kPerBlock;
+        const int bo = ro + blk * BB_;
+        float d = csdr::h2f(lds32(s32, bo) & 0xFFFFu);
+        if (!isfinite(d) || fabsf(d) < 1e-12f) d = 1.0f;
+        constexpr uint32_t kMask = (1u << BITS) - 1u;
+        constexpr int kUp = 10 - BITS;  // fp16 x: q 2^(kUp - 24), the widest exact subnormal
+        const int qo = bo + F::kData + j * 2 * BITS;
+        const int xb = blk * BE_ + j * 16;
+        float a = 0.0f, sx = 0.0f;
+        const bool h16x = sizeof(XT) == 2 && xvec;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t lo = lds32(s32, qo + g * BITS), hi = lds32(s32, qo + g * BITS + 4);
+            uint32_t qv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int sh = i * BITS;
+                qv[i] = (sh < 32 ? __builtin_amdgcn_alignbit(hi, lo, (uint32_t)sh)
+                                 : hi >> (sh - 32)) & kMask;
+            }
+            if (h16x) {
+                uint32_t xw[4];
+                xh8(x, xb + 8 * g, xw);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    a = fdot2u((qv[2 * k] | (qv[2 * k + 1] << 16)) << kUp, xw[k], a);
+                    sx = fdot2u(xw[k], kOnesH2, sx);
+                }
+            } else {
+                float xv[8];
+                x8(x, xb + 8 * g, xvec, xv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a = fmaf((float)qv[i], xv[i], a);
+                    sx += xv[i];
+                }
+            }
+        }
+        if (h16x) a *= (float)(1u << (24 - kUp));
+        return d * fmaf(-(float)(1 << (BITS - 1)), sx, a);
+    }
+};
+
 // q6_k (:329-359): unit u of a block = (half h, quad q): values h*128 + 32 t + 4 q + i of the
 // four quarters t (scale bytes 192 + 8 h + 2 t) and i = 0..3. The quarters' 6-bit quants come
 // from three dwords, ql[h*64 + 4q] (t = 0 low nibbles, t = 2 high), ql[h*64 + 32 + 4q] (t = 1,
@@ -529,7 +654,7 @@ struct Units<Q6_K> {
         float tot = 0.0f;
         if constexpr (sizeof(XT) == 2) {
             if (xvec) {
-                // fp16 x: the quants as fp16 subnormal pairs q 2^-24 (exact), one
+                // fp16 x: the quants as fp16 subnormal pairs q 2^-20 (exact), one
                 // v_dot2_f32_f16 per two products and per two values of the x sum
                 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
                 constexpr uint32_t kOnes = 0x3C003C00u;  // (1.0, 1.0)
@@ -537,15 +662,15 @@ struct Units<Q6_K> {
                 for (int t = 0; t < 4; ++t) {
                     const u32x2 xw = *reinterpret_cast<const u32x2*>(x + xb + 32 * t);
                     const uint32_t x01 = xw.x, x23 = xw.y;
-                    const uint32_t p01 = __builtin_amdgcn_perm(0u, qt[t], 0x0C010C00u);
-                    const uint32_t p23 = __builtin_amdgcn_perm(0u, qt[t], 0x0C030C02u);
+                    const uint32_t p01 = __builtin_amdgcn_perm(0u, qt[t], 0x0C010C00u) << 4;
+                    const uint32_t p23 = __builtin_amdgcn_perm(0u, qt[t], 0x0C030C02u) << 4;
                     float a = fdot2u(p01, x01, 0.0f);
                     a = fdot2u(p23, x23, a);
                     float sx = fdot2u(x01, kOnes, 0.0f);
                     sx = fdot2u(x23, kOnes, sx);
-                    tot = fmaf(sc[t], fmaf(-0x1p-19f, sx, a), tot);
+                    tot = fmaf(sc[t], fmaf(-0x1p-15f, sx, a), tot);
                 }
-                return d * 0x1p24f * tot;
+                return d * 0x1p20f * tot;
             }
         }
 #pragma unroll
