@@ -16,10 +16,13 @@
 //
 // Kernels (a template per format, so each decode is straight-line code)
 //   gguf_gemv_lds_kernel (M == 1): one wave per row; the row's bytes staged in LDS with
-//     16-byte loads all in flight at once, then lane l takes values 8 g .. 8 g + 7 for
-//     g = l, l + 64, ... of the row, decodes them from their block (Dec8: the block's header
-//     read once for the 8) and multiplies by x in fp32; gguf_gemv_kernel is the same from
-//     memory, for the 8-bit formats and rows longer than the LDS budget.
+//     16-byte loads all in flight at once. Formats with a dword-wide decode (Units: q4_0,
+//     q4_1, q6_k, the q8 family and the generic rule) give lane l units u = l, l + 64, ... of
+//     16 values read as dwords at any byte alignment; with fp16 x the quants become exact fp16
+//     subnormal pairs for v_dot2_f32_f16 (scaled into the widest exact range: at 2^-24 the
+//     dot's products lose precision). The others take values 8 g .. 8 g + 7 per lane (Dec8:
+//     the block's header read once for the 8) in fp32. gguf_gemv_kernel is the element-wise
+//     form from memory, for rows longer than the LDS budget.
 //   gguf_mm_kernel (M > 1, fp16 X): split-K over 256-element steps of the row, 16 RT rows per
 //     workgroup, the 4 waves taking every 4th step. A wave stages its rows' bytes of a step in
 //     LDS with dword loads issued one step ahead (a row's step need not start 4-byte aligned),
@@ -437,24 +440,11 @@ __global__ __launch_bounds__(kThreads) void gguf_dequant_kernel(const uint8_t* _
 // of 4 rows measured slower, 4096 x 14336 q4_0 19.2 us against 17.9).
 constexpr int kRowLoads = 16;  // 16-byte row loads per lane in flight (16 KiB per wave)
 
-// Whether a format's M == 1 product stages its rows in LDS: yes where an element's decode reads
-// several scattered bytes, no for the 8-bit formats (one byte and the scale per element; q8_0
-// at 4096 x 14336: 25.3 us from memory against 29.3 staged).
+// Every format's M == 1 product stages its rows in LDS (rows longer than the LDS budget read
+// from memory, gguf_gemv_kernel).
 template <class F>
 struct StageRow {
     static constexpr bool value = true;
-};
-template <>
-struct StageRow<Q8_0> {
-    static constexpr bool value = false;
-};
-template <>
-struct StageRow<Q8_1> {
-    static constexpr bool value = false;
-};
-template <>
-struct StageRow<Q8_K> {
-    static constexpr bool value = false;
 };
 
 // LDS bytes of one wave's row slot (the row plus the up to 15 bytes before it, and 16 more
@@ -570,6 +560,64 @@ template <>
 struct Units<Q4_0> : UnitsQ4<false> {};
 template <>
 struct Units<Q4_1> : UnitsQ4<true> {};
+
+// q8_0 / q8_1 / q8_k (:310-326, :387-395): unit u = values 16 j .. 16 j + 15 of block
+// u / (BE / 16), four quant dwords of signed bytes. With fp16 x the bytes are offset to
+// unsigned (b + 128, exact) and taken as fp16 subnormal pairs (b + 128) 2^-22:
+// d * (sum (b + 128) x - 128 sum x).
+template <int BB_, int BE_, int QOFF, bool SCALE_F32>
+struct UnitsQ8 {
+    static constexpr bool value = true;
+    static constexpr int kPerBlock = BE_ / 16;
+    template <typename XT>
+    __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                bool xvec) {
+        const int blk = u / kPerBlock, j = u - blk * kPerBlock;
+        const int bo = ro + blk * BB_;
+        const uint32_t hd = lds32(s32, bo);
+        const float d = SCALE_F32 ? __builtin_bit_cast(float, hd) : csdr::h2f(hd & 0xFFFFu);
+        const int qo = bo + QOFF + 16 * j;
+        const int xb = blk * BE_ + 16 * j;
+        float a = 0.0f, sx = 0.0f;
+        if (sizeof(XT) == 2 && xvec) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                uint32_t xw[4];
+                xh8(x, xb + 8 * g, xw);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t w = lds32(s32, qo + 8 * g + 4 * h) ^ 0x80808080u;
+                    const uint32_t p01 = __builtin_amdgcn_perm(0u, w, 0x0C010C00u) << 2;
+                    const uint32_t p23 = __builtin_amdgcn_perm(0u, w, 0x0C030C02u) << 2;
+                    a = fdot2u(p01, xw[2 * h], a);
+                    a = fdot2u(p23, xw[2 * h + 1], a);
+                    sx = fdot2u(xw[2 * h], kOnesH2, sx);
+                    sx = fdot2u(xw[2 * h + 1], kOnesH2, sx);
+                }
+            }
+            return d * fmaf(-128.0f, sx, a * 0x1p22f);
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            float xv[8];
+            x8(x, xb + 8 * g, xvec, xv);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t w = lds32(s32, qo + 8 * g + 4 * h);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    a = fmaf((float)(int8_t)((w >> (8 * i)) & 0xFFu), xv[4 * h + i], a);
+            }
+        }
+        return d * a;
+    }
+};
+template <>
+struct Units<Q8_0> : UnitsQ8<34, 32, 2, false> {};
+template <>
+struct Units<Q8_1> : UnitsQ8<40, 32, 8, true> {};
+template <>
+struct Units<Q8_K> : UnitsQ8<292, 256, 4, false> {};
 
 // the generic rule (:439-465): unit u = values 16 j .. 16 j + 15 of block u / (BE / 16), two
 // groups of 8 values x BITS bits = BITS bytes each (byte aligned), read as two dwords and

@@ -83,7 +83,25 @@ def test_linear_m1(gpu, fmt, R, nblk):
     assert rel_l2(yh, ref_h) <= TOL_M1
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q6_k", "q5_k", "q2_k", "iq4_xs"])
+@pytest.mark.parametrize("fmt,R,Cc", [("q6_k", 4100, 14336), ("q4_0", 9001, 4096),
+                                      ("q8_0", 8500, 4096)])
+def test_linear_m1_many_rows(gpu, fmt, R, Cc):
+    """More rows than the chip holds at once (several rounds of workgroups), ragged counts."""
+    from cortexsdr_amd import gguf
+
+    rng = np.random.default_rng(400 + F[fmt])
+    _, be = oracle.gguf_block(F[fmt])
+    w = blocks(fmt, R * Cc // be, rng)
+    wd = _dev(gpu, w.ravel())
+    x = rng.normal(size=(1, Cc)).astype(np.float16)
+    ref = oracle.gguf_linear(w.ravel(), F[fmt], R, Cc, x.astype(np.float32))
+    y = gguf.linear(wd, F[fmt], R, Cc, _dev(gpu, x)).cpu().numpy()
+    err = rel_l2(y, ref)
+    print(f"{fmt} R={R} C={Cc} float16: rel_l2={err:.2e}", flush=True)
+    assert err <= TOL_M1
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q6_k", "q5_k", "q2_k", "iq4_xs", "q8_0", "q8_k"])
 def test_linear_m1_unaligned_x(gpu, fmt):
     """x not 16-byte aligned (one element into a buffer): the element-wise x reads."""
     from cortexsdr_amd import gguf
