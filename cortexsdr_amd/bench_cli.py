@@ -86,6 +86,41 @@ def bench_hsdb(torch, R, Cc, K, s, M, xdtype, steps, seed=2):
             "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
 
 
+def bench_hsdb_layers(torch, R, Cc, K, s, G, xdtype, steps, seed=2):
+    """G independent layers of one shape in one grouped call (csdr_hsdb_matmul_group, one dx
+    and one gather launch for all G): microseconds per call and per layer."""
+    from . import _lib
+    from .hsdr import HsdbSegment, group_workspace
+
+    streams = [synth.hsdb_layer(R, Cc, K, s, seed_dict=1, seed_codes=seed + g) for g in range(G)]
+    codes = R * (Cc // 64) * s * 4
+    ncp = max(2, _copies(codes * G))
+    segs = [[HsdbSegment(st) for st in streams] for _ in range(ncp)]
+    xs = [torch.from_numpy(synth.activations(Cc, 1, seed=3 + g, dtype=xdtype)).cuda()
+          for g in range(G)]
+    ys = [torch.empty((R, 1), dtype=torch.float32, device="cuda") for _ in range(G)]
+    ws = group_workspace(segs[0], 1)
+    lib = _lib.load()
+    xt = 1 if xdtype == np.float16 else 0
+    xp = (C.c_void_p * G)(*[x.data_ptr() for x in xs])
+    yp = (C.c_void_p * G)(*[y.data_ptr() for y in ys])
+    hs = [(C.c_void_p * G)(*[sg._h.value for sg in cp]) for cp in segs]
+
+    def fn(i):
+        sp = int(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.csdr_hsdb_matmul_group(G, hs[i], xp, xt, 1, yp, ws.data_ptr(),
+                                              ws.numel(), sp))
+
+    us = time_graph(torch, fn, ncp, steps)
+    alg = G * (codes + K * 64 * 4 + Cc * np.dtype(xdtype).itemsize + R * 4)
+    for cp in segs:
+        for sg in cp:
+            sg.free()
+    return {"R": R, "C": Cc, "K": K, "nnz": s, "layers": G, "us": round(us, 3),
+            "us_per_layer": round(us / G, 3), "GBps": round(alg / us / 1e3, 1),
+            "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4), "copies": ncp}
+
+
 def bench_q4k(torch, R, Cc, M, steps, order=0):
     from . import _lib, q4k
 
@@ -323,7 +358,9 @@ def main(argv=None) -> int:
     t0 = time.time()
     if "cfg1" in cfgs:
         res["results"]["cfg1"] = [bench_hsdb(torch, 4096, 4096, 512, 4, 1, np.float32,
-                                             args.steps)]
+                                             args.steps),
+                                  bench_hsdb_layers(torch, 4096, 4096, 512, 4, 8, np.float32,
+                                                    args.steps)]
     if "cfg2" in cfgs:
         ms = [int(v) for v in args.cfg2_batches.split(",")]
         out = []
