@@ -57,6 +57,11 @@ __device__ __forceinline__ float nib(const uint8_t* qs, int e) {
     return (float)((e & 1) ? (b >> 4) : (b & 0x0Fu));
 }
 
+// The dword at byte offset o of LDS (any alignment): two aligned reads and a byte shift.
+__device__ __forceinline__ uint32_t lds32(const uint32_t* s32, int o) {
+    return __builtin_amdgcn_alignbyte(s32[(o >> 2) + 1], s32[o >> 2], (uint32_t)(o & 3));
+}
+
 // ---- one struct per format: BB bytes and BE elements per block, at(block, e) = value e
 struct Q4_0 {  // :398-406
     static constexpr int BB = 18, BE = 32;
@@ -279,6 +284,77 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__
         y[i] = 0.0f;
 }
 
+// ---- 8 consecutive values e0 .. e0 + 7 (e0 % 8 == 0) of the block at LDS byte offset bo, as
+// the reference's fp32 values (the same single rounding) converted to fp16, from dword reads
+// at any byte alignment (Dec8W<F>::value: a word-wide decode exists; else Dec8 byte reads,
+// which q8_0 keeps: its word-wide form measured slower, 4096 x 14336 at M = 32 37 -> 57 us)
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+template <class F>
+struct Dec8W {
+    static constexpr bool value = false;
+};
+template <>
+struct Dec8W<Q6_K> {  // d * (float)(sc * (q - 32)); sc * q - 32 sc is exact in fp32
+    static constexpr bool value = true;
+    __device__ static half8v run(const uint32_t* s32, int bo, int e0) {
+        const int half = e0 >> 7, r = e0 & 127, t = r >> 5, l0 = r & 31;
+        const int qlo = bo + half * 64 + l0 + ((t & 1) ? 32 : 0);
+        const int qho = bo + 128 + half * 32 + l0;
+        const float sc = (float)(int8_t)(lds32(s32, bo + 192 + half * 8 + 2 * t) & 0xFFu);
+        const float d = csdr::h2f(lds32(s32, bo + 208) & 0xFFFFu);
+        const float c = -32.0f * sc;
+        half8v o;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t l = lds32(s32, qlo + 4 * k), h = lds32(s32, qho + 4 * k);
+            const uint32_t lo = (t < 2) ? (l & 0x0F0F0F0Fu) : ((l >> 4) & 0x0F0F0F0Fu);
+            const uint32_t q = lo | (((h >> (2 * t)) & 0x03030303u) << 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[4 * k + i] = (_Float16)(d * fmaf((float)((q >> (8 * i)) & 0xFFu), sc, c));
+        }
+        return o;
+    }
+};
+template <>
+struct Dec8W<Q4_0> {  // (n - 8) * d = fma(n, d, -8 d) with one rounding
+    static constexpr bool value = true;
+    __device__ static half8v run(const uint32_t* s32, int bo, int e0) {
+        const float d = csdr::h2f(lds32(s32, bo) & 0xFFFFu), c = -8.0f * d;
+        const uint32_t w = lds32(s32, bo + 2 + (e0 >> 1));
+        const uint32_t L = w & 0x0F0F0F0Fu, H = (w >> 4) & 0x0F0F0F0Fu;
+        half8v o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o[2 * k] = (_Float16)fmaf((float)((L >> (8 * k)) & 0xFFu), d, c);
+            o[2 * k + 1] = (_Float16)fmaf((float)((H >> (8 * k)) & 0xFFu), d, c);
+        }
+        return o;
+    }
+};
+template <int BB_, int BE_, int BITS>
+struct Dec8W<Packed<BB_, BE_, BITS>> {  // (q - 2^(BITS-1)) * d = fma(q, d, -2^(BITS-1) d)
+    static constexpr bool value = true;
+    __device__ static half8v run(const uint32_t* s32, int bo, int e0) {
+        using F = Packed<BB_, BE_, BITS>;
+        float d = csdr::h2f(lds32(s32, bo) & 0xFFFFu);
+        if (!isfinite(d) || fabsf(d) < 1e-12f) d = 1.0f;
+        const float c = -(float)(1 << (BITS - 1)) * d;
+        const int qo = bo + F::kData + (e0 * BITS >> 3);
+        const uint32_t lo = lds32(s32, qo), hi = lds32(s32, qo + 4);
+        constexpr uint32_t kMask = (1u << BITS) - 1u;
+        half8v o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int sh = i * BITS;
+            const uint32_t q = (sh < 32 ? __builtin_amdgcn_alignbit(hi, lo, (uint32_t)sh)
+                                        : hi >> (sh - 32)) & kMask;
+            o[i] = (_Float16)fmaf((float)q, d, c);
+        }
+        return o;
+    }
+};
+
 // Two waves per SIMD: the decode and the step prefetch want registers more than occupancy
 // (measured at M = 32 against the default budget: q6_k 4096 x 14336 52.8 -> 42.5 us).
 template <class F, int NT, int RT>
@@ -338,7 +414,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
     };
     // 32-wide k step t of step s from the staged bytes
-    auto kstep = [&](int e0, const uint8_t* const* rowsb, int t) {
+    auto kstep = [&](int e0, const uint8_t* const* rowsb, const int* rowso, int t) {
         half8 bv[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -348,11 +424,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int e = 32 * t + 8 * j, b = e / F::BE;
-            float w8[8];
-            Dec8<F>::run(rowsb[rt] + b * F::BB, e - b * F::BE, w8);
             half8 a;
+            if constexpr (Dec8W<F>::value) {
+                a = Dec8W<F>::run(sw, rowso[rt] + b * F::BB, e - b * F::BE);
+            } else {
+                float w8[8];
+                Dec8<F>::run(rowsb[rt] + b * F::BB, e - b * F::BE, w8);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = (_Float16)w8[i];
+                for (int i = 0; i < 8; ++i) a[i] = (_Float16)w8[i];
+            }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
                 acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[nt], acc[rt][nt], 0, 0, 0);
@@ -374,18 +454,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         const int e0 = s * 256;
         const size_t soff = (size_t)s * Step<F>::kBytes;
         const uint8_t* rowsb[RT];
+        int rowso[RT];  // the same as byte offsets in the wave's stage
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int rr = rt * 16 + rl;
             const size_t start = (size_t)min(r0 + rr, R - 1) * rowbytes + soff;
-            rowsb[rt] = reinterpret_cast<const uint8_t*>(sw + rr * ND) + (start & 3);
+            rowso[rt] = rr * ND * 4 + (int)(start & 3);
+            rowsb[rt] = reinterpret_cast<const uint8_t*>(sw) + rowso[rt];
         }
         const int nsub = min(256, C - e0) / 32;  // 32-wide k steps (C is a multiple of BE >= 32)
         if (nsub == 8) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) kstep(e0, rowsb, t);
+            for (int t = 0; t < 8; ++t) kstep(e0, rowsb, rowso, t);
         } else {
-            for (int t = 0; t < nsub; ++t) kstep(e0, rowsb, t);
+            for (int t = 0; t < nsub; ++t) kstep(e0, rowsb, rowso, t);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -460,10 +542,6 @@ __device__ __forceinline__ float fdot2u(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
 }
 
-// The dword at byte offset o of LDS (any alignment): two aligned reads and a byte shift.
-__device__ __forceinline__ uint32_t lds32(const uint32_t* s32, int o) {
-    return __builtin_amdgcn_alignbyte(s32[(o >> 2) + 1], s32[o >> 2], (uint32_t)(o & 3));
-}
 
 // x[e .. e + 3] in fp32 (e % 4 == 0): one load when x is 16-byte aligned
 template <typename XT>
