@@ -604,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
     }
 }
 
-// ---- kernel 1 at M == 1 with 64-long blocks (no attention x op): P[b][a] = D[a] . x_b as a
+// ---- kernel 1 at M == 1 with 64-long blocks: P[b][a] = D[a] . x_b as a
 // small product P^T (K x NB) = D (K x 64) . [x_0 .. x_NB-1] (64 x NB) on the fp32 matrix
 // cores (v_mfma_f32_16x16x4_f32). Workgroup = NT / 64 waves x 16 atoms and 16 block
 // columns, wave w the atoms 16 w .. 16 w + 15 of the workgroup's; lane l supplies atom l % 16
@@ -613,7 +613,8 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
 // operands are one contiguous 64-byte run of the dictionary row and of x, loaded straight
 // from memory (no LDS, no cross-lane sums). Lane l ends with P[block l % 16][atoms
 // 4 (l / 16) .. + 3]. Y is initialised as in dx_kernel; the x op (RMSNorm with its statistic
-// over all C features, or SiLU . x2) is applied to the B operand in registers.
+// over all C features, or SiLU . x2) is applied to the B operand in registers; the attention
+// combine is staged for the workgroup's blocks in LDS first (stage_x_m1).
 template <int XOP, int NT>
 __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
     typedef float f4 __attribute__((ext_vector_type(4)));
@@ -646,7 +647,22 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
         for (int i = 0; i < 4; ++i) dv[i] = src[i];
     }
     float xv[16];
-    if (p.x_f16) {
+    if constexpr (XOP == CSDR_XOP_ATTN) {
+        // the split-attention combine for the workgroup's 16 blocks (1024 features, one per
+        // 4 threads' float4) into LDS, then this lane's 16 features from there
+        __shared__ __attribute__((aligned(16))) float xs_attn[16 * 64];
+        const int b0 = bg * 16;
+        stage_x_m1<NT, XOP>(p, d, b0, min(16, d.NB - b0), xs_attn, u == 0);  // (ends in a barrier)
+        const f4* src = reinterpret_cast<const f4*>(xs_attn + (b - b0) * 64 + lg * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f4 v = src[i];
+            xv[4 * i] = v.x;
+            xv[4 * i + 1] = v.y;
+            xv[4 * i + 2] = v.z;
+            xv[4 * i + 3] = v.w;
+        }
+    } else if (p.x_f16) {
         const u4* src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(d.x) + f0);
         const u4 h0 = src[0], h1 = src[1];
 #pragma unroll
@@ -692,8 +708,8 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
         for (int i = 0; i < 16; ++i)
             xv[i] = (xv[i] * (1.0f / (1.0f + expf(-xv[i])))) * x2[i];
     }
-    if (XOP != CSDR_XOP_NONE && u == 0 && d.xe) {
-        // the transformed edge-strip inputs
+    if (XOP != CSDR_XOP_NONE && XOP != CSDR_XOP_ATTN && u == 0 && d.xe) {
+        // the transformed edge-strip inputs (the attention combine writes its own)
         for (int t = tid; t < d.Ce; t += NT) {
             const int f = d.C_full + t;
             float x = xload(d.x, p.x_f16, (size_t)f);
@@ -1993,9 +2009,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     // 2 <= M <= 16 with 64-long blocks everywhere: the thread-per-atom dx kernel
     bool dxm = M >= 2 && M <= kMaxXopM;
     for (int i = 0; i < n; ++i) dxm = dxm && segs[i] && segs[i]->tile_cols == 64;
-    // M == 1 with 64-long blocks, 16-byte aligned inputs and no attention x op: the
-    // matrix-core dx kernel
-    bool dx1 = M == 1 && xa.xop != CSDR_XOP_ATTN;
+    // M == 1 with 64-long blocks and 16-byte aligned inputs: the matrix-core dx kernel
+    bool dx1 = M == 1;
     for (int i = 0; i < n && dx1; ++i) {
         const uintptr_t al = reinterpret_cast<uintptr_t>(xs[i]) |
                              (xa.xop == CSDR_XOP_SILU_MUL ? reinterpret_cast<uintptr_t>(xa.x2[i]) : 0);
@@ -2119,6 +2134,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         switch (p.xop) {
             case CSDR_XOP_RMSNORM: dx1_mfma_kernel<CSDR_XOP_RMSNORM><<<ndx, kThreads, 0, st>>>(p); break;
             case CSDR_XOP_SILU_MUL: dx1_mfma_kernel<CSDR_XOP_SILU_MUL><<<ndx, kThreads, 0, st>>>(p); break;
+            case CSDR_XOP_ATTN: dx1_mfma_kernel<CSDR_XOP_ATTN><<<ndx, kThreads, 0, st>>>(p); break;
             default: dx1_mfma_kernel<CSDR_XOP_NONE><<<ndx, kThreads, 0, st>>>(p); break;
         }
         CSDR_LAUNCH_CHECK("hsdb dx");
