@@ -727,7 +727,9 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
     if (bo < d.NB) {
         float* out = d.P + (size_t)bo * d.K + ao;
         if (ao + 3 < d.K && (d.K & 3) == 0) {
-            *reinterpret_cast<f4*>(out) = acc;
+            // streamed past this XCD's L2: the gather reads P from every XCD (headline step
+            // 15.64 -> 15.42 us)
+            __builtin_nontemporal_store(acc, reinterpret_cast<f4*>(out));
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
