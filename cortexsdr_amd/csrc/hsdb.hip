@@ -879,8 +879,8 @@ __global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
         float* out = d.P + (size_t)bj * d.K * M + mj;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int a = a0 + 4 * lg + v;
-            if (a < d.K) out[(size_t)a * M] = acc[v];
+            const int a = a0 + 4 * lg + v;  // (streamed past this XCD's L2, as in dx1_body)
+            if (a < d.K) __builtin_nontemporal_store(acc[v], out + (size_t)a * M);
         }
     }
 }
