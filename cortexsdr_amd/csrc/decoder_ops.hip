@@ -174,7 +174,7 @@ struct Row8<_Float16> {
     h8 v;
     __device__ static Row8 load(const _Float16* p) {
         Row8 r;
-        r.v = *reinterpret_cast<const h8*>(p);
+        r.v = __builtin_nontemporal_load(reinterpret_cast<const h8*>(p));  // read once per step
         return r;
     }
     __device__ void store(_Float16* p) const { *reinterpret_cast<h8*>(p) = v; }
@@ -187,8 +187,8 @@ struct Row8<float> {
     f4 a, b;
     __device__ static Row8 load(const float* p) {
         Row8 r;
-        r.a = reinterpret_cast<const f4*>(p)[0];
-        r.b = reinterpret_cast<const f4*>(p)[1];
+        r.a = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));  // read once per step
+        r.b = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p) + 1);
         return r;
     }
     __device__ void store(float* p) const {
