@@ -843,8 +843,8 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* 
     const bool has_row = r < R;
     const int np = has_row ? npiece : 0;
     auto load = [&](int p) {  // piece p of the row, or zeros past its end
-        return __builtin_amdgcn_raw_buffer_load_b128(
-            rs, p < np ? (uint32_t)p * 16 : 0x80000000u, 0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(  // streaming (nontemporal) policy
+            rs, p < np ? (uint32_t)p * 16 : 0x80000000u, 0, 2);
     };
     // the row in batches of kRowLoads pieces per lane
 #pragma unroll
