@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     constexpr int ND = Step<F>::kDwords;
     constexpr int ROWS = 16 * RT;
     constexpr int NW = kThreads / 64;
-    __shared__ uint32_t stage[NW][ROWS * ND];
+    __shared__ uint32_t stage[NW][ROWS * ND + 1];  // + 1: Dec8W's dword pairs end inside
     __shared__ floatx4 red[NW - 1][RT][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, j = lane >> 4;
