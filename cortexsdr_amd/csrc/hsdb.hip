@@ -1309,7 +1309,11 @@ void gatherv_kernel(Params p) {
         for (int i0 = 0; i0 < n4; i0 += kGThreads * 8) {
             f4 v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = Pg[min(i0 + j * kGThreads + tid, n4 - 1)];
+            for (int j = 0; j < 8; ++j) {  // nontemporal, as the M == 1 gather's P slice
+                typedef float f4v __attribute__((ext_vector_type(4)));
+                v[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(Pg) +
+                                                  min(i0 + j * kGThreads + tid, n4 - 1));
+            }
             if (i0 == 0) {
 #pragma unroll
                 for (int k = 0; k < TD; ++k) tile(k, buf[k]);
