@@ -20,7 +20,8 @@ The JSON line carries:
   roofline      the dominant kernel (the gather launch over both matrices): median over 100
                 replays of a graph of K back-to-back gather launches, HIP events on the
                 launch stream; `traffic` = HBM bytes per launch from the committed rocprofv3
-                --pmc measurement of the current kernel (profiles/hsdb_gather_cfg2_traffic.json)
+                --pmc measurement (profiles/hsdb_gather_cfg2_traffic.json), null unless it
+                was made from the kernel sources in this tree
   cpu_baseline  the CPU restatement of the reference algorithm (oracle/, OpenMP) on a
                 bounded sample of the same workload, on this host's cores, with the CPU
                 model, its physical cores and a single-thread time (the reference's fused
@@ -53,20 +54,22 @@ MALL_BYTES = 256 * 1024 * 1024
 
 # HBM bytes per gather launch (cfg2, M = 1, both matrices): two rocprofv3 --pmc runs of this
 # script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same counter
-# reads for a plain 256 MiB device copy in the same run (--calibrate-copy); the measured
-# values, the scale factors and the commands are in this JSON file, written from those runs.
+# reads for a plain 256 MiB device copy in the same run (--calibrate-copy), written by
+# cortexsdr_amd/traffic.py with the digest of the kernel's sources; reported only when that
+# digest is the current tree's (a measurement of an older kernel is not this kernel's).
 TRAFFIC_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "hsdb_gather_cfg2_traffic.json")
 
 
 def gather_traffic():
-    """(bytes per launch, kernel name) from the committed PMC measurement, or (None, None)."""
-    try:
-        with open(TRAFFIC_JSON) as f:
-            t = json.load(f)
-        return int(t["traffic_bytes"]), t.get("kernel")
-    except (OSError, ValueError, KeyError):
-        return None, None
+    """(bytes per launch, the measurement's record) from the committed PMC measurement of the
+    current sources, or (None, reason)."""
+    from cortexsdr_amd import traffic
+
+    t, why = traffic.load_current(TRAFFIC_JSON)
+    if t is None:
+        return None, why
+    return int(t["traffic_bytes"]), t
 
 
 def cpu_info():
@@ -449,7 +452,7 @@ def main():
     g_bytes = sum(alg_bytes(w)["gather"] for w in wl)
     achieved = g_bytes / (kern_ms * 1e-3) / 1e9
 
-    traffic, traffic_kernel = gather_traffic() if args.config == "cfg2" else (None, None)
+    traffic, trec = gather_traffic() if args.config == "cfg2" else (None, "not measured")
     out = {
         "metric": "fused decode-GEMV HBM GB/s",
         "value": round(value, 2),
@@ -492,7 +495,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "traffic_source": "profiles/hsdb_gather_cfg2_traffic.json" if traffic else None,
+            "traffic_source": ("profiles/hsdb_gather_cfg2_traffic.json (sources "
+                               f"{trec['source_digest']}, commit {trec.get('git_head')})"
+                               if traffic else trec),
             "algorithmic_bytes_per_launch": g_bytes,
         },
         "cpu_baseline": None,
