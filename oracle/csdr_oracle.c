@@ -626,64 +626,81 @@ static void softmax_row(float* s, size_t n) {
 
 void orc_mha_causal(const float* q, const float* k, const float* v, float* out, size_t B,
                     size_t T, size_t hidden, size_t heads) {
-    /* attention_kernels.cpp:26-113 */
+    /* attention_kernels.cpp:26-113. Each output element sums over positions j in ascending
+     * order with fmaf (the V loop runs j-outer over a row of accumulators: the same order per
+     * element); queries are independent, so they run in parallel. */
     const size_t d = hidden / heads;
     const float scale = 1.0f / sqrtf((float)d);
-    float* sc = (float*)malloc(T * 4 + 4);
-    for (size_t b = 0; b < B; ++b)
-        for (size_t h = 0; h < heads; ++h)
-            for (size_t i = 0; i < T; ++i) {
-                const float* qi = q + (b * T + i) * hidden + h * d;
-                for (size_t j = 0; j < T; ++j) {
-                    const float* kj = k + (b * T + j) * hidden + h * d;
-                    float acc = 0.0f;
-                    for (size_t t = 0; t < d; ++t) acc = fmaf(qi[t], kj[t], acc);
-                    sc[j] = (j > i) ? -INFINITY : acc * scale; /* apply_causal_mask */
-                }
-                softmax_row(sc, T);
-                float* o = out + (b * T + i) * hidden + h * d;
-                for (size_t t = 0; t < d; ++t) {
-                    float acc = 0.0f;
-                    for (size_t j = 0; j < T; ++j)
-                        acc = fmaf(sc[j], v[(b * T + j) * hidden + h * d + t], acc);
-                    o[t] = acc;
-                }
+    const long long n = (long long)(B * heads * T);
+#pragma omp parallel
+    {
+        float* sc = (float*)malloc(T * 4 + 4);
+        float* acc = (float*)malloc(d * 4 + 4);
+#pragma omp for schedule(static)
+        for (long long it = 0; it < n; ++it) {
+            const size_t i = (size_t)it % T, h = ((size_t)it / T) % heads,
+                         b = (size_t)it / (T * heads);
+            const float* qi = q + (b * T + i) * hidden + h * d;
+            for (size_t j = 0; j < T; ++j) {
+                const float* kj = k + (b * T + j) * hidden + h * d;
+                float a = 0.0f;
+                for (size_t t = 0; t < d; ++t) a = fmaf(qi[t], kj[t], a);
+                sc[j] = (j > i) ? -INFINITY : a * scale; /* apply_causal_mask */
             }
-    free(sc);
+            softmax_row(sc, T);
+            for (size_t t = 0; t < d; ++t) acc[t] = 0.0f;
+            for (size_t j = 0; j < T; ++j) {
+                const float* vj = v + (b * T + j) * hidden + h * d;
+                for (size_t t = 0; t < d; ++t) acc[t] = fmaf(sc[j], vj[t], acc[t]);
+            }
+            float* o = out + (b * T + i) * hidden + h * d;
+            for (size_t t = 0; t < d; ++t) o[t] = acc[t];
+        }
+        free(acc);
+        free(sc);
+    }
 }
 
 void orc_attn_decode(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                      const int32_t* lens, size_t B, size_t T, size_t Hq, size_t Hkv, size_t d,
                      float scale, float* out) {
+    /* per (sequence, query head): scores over the cached positions, softmax, then the V sum
+     * per element in ascending position order with fmaf (j-outer over a row of accumulators);
+     * the (sequence, head) pairs are independent and run in parallel */
     const size_t rep = Hq / Hkv;
-    float* sc = (float*)malloc(T * 4 + 4);
-    for (size_t b = 0; b < B; ++b) {
-        const size_t L = lens ? (size_t)lens[b] : T;
-        for (size_t h = 0; h < Hq; ++h) {
+    const long long n = (long long)(B * Hq);
+#pragma omp parallel
+    {
+        float* sc = (float*)malloc(T * 4 + 4);
+        float* acc = (float*)malloc(d * 4 + 4);
+#pragma omp for schedule(static)
+        for (long long it = 0; it < n; ++it) {
+            const size_t b = (size_t)it / Hq, h = (size_t)it % Hq;
+            const size_t L = lens ? (size_t)lens[b] : T;
             const size_t kvh = h / rep;
             const float* qh = q + (b * Hq + h) * d;
-            for (size_t j = 0; j < L; ++j) {
-                const uint16_t* kj = kcache + ((b * T + j) * Hkv + kvh) * d;
-                float acc = 0.0f;
-                for (size_t t = 0; t < d; ++t) acc = fmaf(qh[t], orc_f16_to_f32(kj[t]), acc);
-                sc[j] = acc * scale;
-            }
             float* o = out + (b * Hq + h) * d;
             if (L == 0) {
                 for (size_t t = 0; t < d; ++t) o[t] = 0.0f;
                 continue;
             }
-            softmax_row(sc, L);
-            for (size_t t = 0; t < d; ++t) {
-                float acc = 0.0f;
-                for (size_t j = 0; j < L; ++j)
-                    acc = fmaf(sc[j], orc_f16_to_f32(vcache[((b * T + j) * Hkv + kvh) * d + t]),
-                               acc);
-                o[t] = acc;
+            for (size_t j = 0; j < L; ++j) {
+                const uint16_t* kj = kcache + ((b * T + j) * Hkv + kvh) * d;
+                float a = 0.0f;
+                for (size_t t = 0; t < d; ++t) a = fmaf(qh[t], orc_f16_to_f32(kj[t]), a);
+                sc[j] = a * scale;
             }
+            softmax_row(sc, L);
+            for (size_t t = 0; t < d; ++t) acc[t] = 0.0f;
+            for (size_t j = 0; j < L; ++j) {
+                const uint16_t* vj = vcache + ((b * T + j) * Hkv + kvh) * d;
+                for (size_t t = 0; t < d; ++t) acc[t] = fmaf(sc[j], orc_f16_to_f32(vj[t]), acc[t]);
+            }
+            for (size_t t = 0; t < d; ++t) o[t] = acc[t];
         }
+        free(acc);
+        free(sc);
     }
-    free(sc);
 }
 
 /* ---------------------------------------------------------- decoder ops */

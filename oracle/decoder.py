@@ -19,6 +19,12 @@ step_cached continues B sequences from a given fp16 K/V context (a cached prompt
 decode step of configs[4]): the same block with the new K/V row appended to the cache at fp16
 (as the device cache stores it) and cached decode attention (orc_attn_decode).
 
+DenseWeights decodes every linear once to dense fp32 (hsdr_decompress, bit-exact with the
+reference's decompress) so that long contexts run as dense products: the fused product equals
+decode-then-dense (pinned in tests/test_oracle.py), so this changes only the summation order.
+step_cached also continues fp32 K/V caches (the device decoder's default precision, the
+reference recompute's) with textbook attention in float64.
+
 Parity status: every op above is pinned on its own (tests/test_oracle.py); the composition
 follows the reference's call sequence, which cannot be compiled here (the SDK needs protobuf
 headers), and is checked against an independent float64 dense restatement on tiny models
@@ -32,9 +38,29 @@ from . import (attn_decode, f32_to_f16, hsdb_matmul, hsdr_decompress, mha_causal
                rope, select_best, silu_mul)
 
 
-def _linear(stream, x_tc: np.ndarray, bias=None) -> np.ndarray:
-    """(T, C) -> (T, R): the reference's run_cached_linear per token on feature-major x."""
-    y = hsdb_matmul(stream, np.ascontiguousarray(x_tc.T, np.float32)).T
+class DenseWeights:
+    """Each coded linear decoded once to dense fp32 R x C (hsdr_decompress), keyed by stream."""
+
+    def __init__(self):
+        self._w = {}
+
+    def get(self, stream) -> np.ndarray:
+        key = id(stream)
+        hit = self._w.get(key)
+        if hit is None or hit[0] is not stream:
+            hit = (stream, hsdr_decompress(stream))
+            self._w[key] = hit
+        return hit[1]
+
+
+def _linear(stream, x_tc: np.ndarray, bias=None, dense: DenseWeights | None = None) -> np.ndarray:
+    """(T, C) -> (T, R): the reference's run_cached_linear per token on feature-major x (with
+    `dense`: x times the decoded W^T, in float64)."""
+    if dense is not None:
+        W = dense.get(stream)
+        y = np.asarray(x_tc, np.float64) @ W.T.astype(np.float64)
+    else:
+        y = hsdb_matmul(stream, np.ascontiguousarray(x_tc.T, np.float32)).T
     if bias is not None:
         y = y + bias[None, :]
     return np.ascontiguousarray(y, np.float32)
@@ -51,35 +77,51 @@ def hidden_last(w, tokens, dense_embed: np.ndarray | None = None) -> np.ndarray:
     return _forward(w, tokens, dense_embed)[0]
 
 
-def context_kv(w, tokens, dense_embed: np.ndarray | None = None):
+def context_kv(w, tokens, dense_embed: np.ndarray | None = None, dense=None):
     """Per layer the rotated K and the V of every position of the full-context forward,
     (T, Hkv, hd) fp32 each: the context a cached decoder holds after these tokens."""
-    return _forward(w, tokens, dense_embed)[1]
+    return _forward(w, tokens, dense_embed, dense)[1]
 
 
-def _forward(w, tokens, dense_embed=None):
+def prompt_state(w, tokens, dense=None):
+    """The full-context forward over a prompt: (lm_head scores of the position after it,
+    per layer (K, V) of every prompt position, (T, Hkv, hd) fp32 each)."""
+    h, kvs = _forward(w, tokens, None, dense)
+    return _scores(w, sanitize(h)[None, :], dense)[0], kvs
+
+
+def _scores(w, hs: np.ndarray, dense=None) -> np.ndarray:
+    """(B, hidden) sanitized hidden states -> (B, vocab) lm_head scores."""
+    if dense is not None:
+        return _linear(w.lm_head, hs, None, dense)
+    return np.ascontiguousarray(hsdb_matmul(w.lm_head, np.ascontiguousarray(hs.T)).T, np.float32)
+
+
+def _forward(w, tokens, dense_embed=None, dense=None):
     s = w.spec
     T = len(tokens)
     hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
     rep = Hq // Hkv
+    if dense_embed is None and dense is not None:
+        dense_embed = dense.get(w.embedding if w.embedding is not None else w.lm_head)
     x = (dense_embed[np.asarray(tokens, np.int64)] if dense_embed is not None
          else embed_rows(w, tokens)).astype(np.float32)
     kvs = []
     for L in w.layers:
         h = rms_norm(x, L["attn_norm"], s.rms_eps)
-        q = _linear(L["q"], h, L.get("bq"))
-        k = _linear(L["k"], h, L.get("bk"))
-        v = _linear(L["v"], h, L.get("bv"))
+        q = _linear(L["q"], h, L.get("bq"), dense)
+        k = _linear(L["k"], h, L.get("bk"), dense)
+        v = _linear(L["v"], h, L.get("bv"), dense)
         q = rope(q, Hq, hd, s.rope_theta, 0)
         k = rope(k, Hkv, hd, s.rope_theta, 0)
         kvs.append((k.reshape(T, Hkv, hd).copy(), v.reshape(T, Hkv, hd).copy()))
         ke = np.repeat(k.reshape(T, Hkv, hd), rep, axis=1).reshape(T, Hq * hd)
         ve = np.repeat(v.reshape(T, Hkv, hd), rep, axis=1).reshape(T, Hq * hd)
         a = mha_causal(q[None], ke[None], ve[None], Hq)[0]
-        x = (x + _linear(L["o"], a)).astype(np.float32)
+        x = (x + _linear(L["o"], a, None, dense)).astype(np.float32)
         h = rms_norm(x, L["ffn_norm"], s.rms_eps)
-        f = silu_mul(_linear(L["gate"], h), _linear(L["up"], h))
-        x = (x + _linear(L["down"], f)).astype(np.float32)
+        f = silu_mul(_linear(L["gate"], h, None, dense), _linear(L["up"], h, None, dense))
+        x = (x + _linear(L["down"], f, None, dense)).astype(np.float32)
     if w.final_norm is not None:
         x = rms_norm(x, w.final_norm, s.rms_eps)
     return x[-1].copy(), kvs
@@ -119,40 +161,78 @@ def generate(w, prompt, max_new_tokens, temperature=0.8, penalty=1.5, forced=Non
     return np.asarray(gen, np.int32), scores
 
 
-def step_cached(w, tokens, kv, n: int):
+def attn_cached_f32(q, kc, vc, n: int, Hq: int, Hkv: int, hd: int) -> np.ndarray:
+    """Textbook attention of B queries over positions [0, n] of fp32 caches, in float64:
+    q (B, Hq, hd); kc, vc (B, >= n + 1, Hkv, hd); query head h reads KV head h / (Hq / Hkv),
+    scale 1 / sqrt(hd) (attention_kernels.cpp:26-113 at the last position)."""
+    B = q.shape[0]
+    rep = Hq // Hkv
+    out = np.empty((B, Hq, hd), np.float32)
+    for b in range(B):
+        K = np.asarray(kc[b, :n + 1], np.float64)
+        V = np.asarray(vc[b, :n + 1], np.float64)
+        for h in range(Hq):
+            sc = K[:, h // rep, :] @ np.asarray(q[b, h], np.float64) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            out[b, h] = p @ V[:, h // rep, :]
+    return out
+
+
+def step_cached(w, tokens, kv, n: int, dense: DenseWeights | None = None):
     """One decode step of B sequences at position n over a cached context.
 
     tokens: (B,) the token at position n of each sequence; kv: per layer (K, V), each
-    (B, n, Hkv, hd) fp16 bits (uint16) for positions [0, n). Returns (scores (B, vocab),
-    new rows: per layer (K, V) of position n, (B, Hkv, hd) fp16 bits) -- the rows the next
-    step's context appends."""
+    (B, T, Hkv, hd) with T >= n, holding positions [0, n): fp16 bits (uint16; the new row is
+    rounded to fp16 as the device's fp16 cache stores it) or float32 (fp32 cache). When
+    T > n the new row is also written into position n of the given arrays, so a caller can
+    keep one preallocated cache per layer. Returns (scores (B, vocab), new rows: per layer
+    (K, V) of position n, (B, Hkv, hd), in the cache's element type)."""
     s = w.spec
     hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
     tokens = np.asarray(tokens, np.int64)
     B = tokens.size
     table = w.embedding if w.embedding is not None else w.lm_head
-    x = hsdr_decompress(table)[tokens].astype(np.float32)
+    if dense is not None:
+        x = dense.get(table)[tokens].astype(np.float32)
+    else:
+        x = hsdr_decompress(table)[tokens].astype(np.float32)
     rows = []
     for L, (kc, vc) in zip(w.layers, kv):
+        f32 = np.asarray(kc).dtype == np.float32
         h = rms_norm(x, L["attn_norm"], s.rms_eps)
-        q = _linear(L["q"], h, L.get("bq"))
-        k = _linear(L["k"], h, L.get("bk"))
-        v = _linear(L["v"], h, L.get("bv"))
+        q = _linear(L["q"], h, L.get("bq"), dense)
+        k = _linear(L["k"], h, L.get("bk"), dense)
+        v = _linear(L["v"], h, L.get("bv"), dense)
         for b in range(B):  # every sequence at position n
             q[b] = rope(q[b], Hq, hd, s.rope_theta, n)
             k[b] = rope(k[b], Hkv, hd, s.rope_theta, n)
-        k16 = f32_to_f16(k).reshape(B, 1, Hkv, hd)
-        v16 = f32_to_f16(v).reshape(B, 1, Hkv, hd)
-        rows.append((k16[:, 0], v16[:, 0]))
-        kfull = np.concatenate([np.asarray(kc, np.uint16).reshape(B, n, Hkv, hd), k16], axis=1)
-        vfull = np.concatenate([np.asarray(vc, np.uint16).reshape(B, n, Hkv, hd), v16], axis=1)
-        a = attn_decode(q.reshape(B, Hq, hd), kfull, vfull, None, Hq, Hkv, hd)
-        x = (x + _linear(L["o"], a.reshape(B, Hq * hd))).astype(np.float32)
+        if f32:
+            kr = k.reshape(B, 1, Hkv, hd).astype(np.float32)
+            vr = v.reshape(B, 1, Hkv, hd).astype(np.float32)
+        else:
+            kr = f32_to_f16(k).reshape(B, 1, Hkv, hd)
+            vr = f32_to_f16(v).reshape(B, 1, Hkv, hd)
+        rows.append((kr[:, 0].copy(), vr[:, 0].copy()))
+        kc4 = np.asarray(kc).reshape(B, -1, Hkv, hd)
+        vc4 = np.asarray(vc).reshape(B, -1, Hkv, hd)
+        if kc4.shape[1] > n:  # room for position n: write it in place
+            kc4[:, n] = kr[:, 0]
+            vc4[:, n] = vr[:, 0]
+            kfull, vfull = kc4, vc4
+        else:
+            kfull = np.concatenate([kc4[:, :n], kr], axis=1)
+            vfull = np.concatenate([vc4[:, :n], vr], axis=1)
+        if f32:
+            a = attn_cached_f32(q.reshape(B, Hq, hd), kfull, vfull, n, Hq, Hkv, hd)
+        else:
+            lens = np.full(B, n + 1, np.int32)
+            a = attn_decode(q.reshape(B, Hq, hd), kfull, vfull, lens, Hq, Hkv, hd)
+        x = (x + _linear(L["o"], a.reshape(B, Hq * hd), None, dense)).astype(np.float32)
         h = rms_norm(x, L["ffn_norm"], s.rms_eps)
-        f = silu_mul(_linear(L["gate"], h), _linear(L["up"], h))
-        x = (x + _linear(L["down"], f)).astype(np.float32)
+        f = silu_mul(_linear(L["gate"], h, None, dense), _linear(L["up"], h, None, dense))
+        x = (x + _linear(L["down"], f, None, dense)).astype(np.float32)
     if w.final_norm is not None:
         x = rms_norm(x, w.final_norm, s.rms_eps)
     hs = np.stack([sanitize(x[b]) for b in range(B)])
-    scores = hsdb_matmul(w.lm_head, np.ascontiguousarray(hs.T)).T
-    return np.ascontiguousarray(scores, np.float32), rows
+    return _scores(w, hs, dense), rows

@@ -133,3 +133,64 @@ def test_cached_step_equals_whole_context_recompute(spec):
     # the batch rows are independent: one sequence alone gives its row
     s1, _ = odec.step_cached(w, seqs[1:2, n], [(k[1:2], v[1:2]) for k, v in kv], n)
     assert np.array_equal(s1[0], scores[1])
+
+
+@pytest.mark.parametrize("spec", [DecoderSpec(2, 256, 4, 2, 64, 96, 150, 32),
+                                  DecoderSpec(1, 256, 2, 2, 128, 128, 90, 32)])
+def test_cached_fp32_dense_steps_equal_whole_context_recompute(spec):
+    """The forms the long-run GPU checks use: the prompt forward with dense (decoded-once)
+    weights, then fp32-cache steps written in place into preallocated caches, against the
+    whole-context recompute through the fused product at every step (same scores to float
+    summation order: dense and fused products differ only there), and the fp16 path of
+    step_cached on the same preallocated layout against its concatenating form."""
+    w = synthetic_weights(spec, n_atoms=64, nnz=4, seed=29, sigma=0.1, norm_jitter=0.1,
+                          bias_sigma=0.05)
+    rng = np.random.default_rng(8)
+    n0, steps = 7, 4
+    seq = rng.integers(0, spec.vocab, size=n0 + steps).astype(np.int32)
+    dense = odec.DenseWeights()
+    sc0, kvs = odec.prompt_state(w, seq[:n0], dense)
+    assert rel_l2(sc0, odec.step_scores(w, seq[:n0])) < 1e-5
+    cap = n0 + steps
+    kv = []
+    for k, v in kvs:
+        kb = np.zeros((1, cap, spec.n_kv_heads, spec.head_dim), np.float32)
+        vb = np.zeros_like(kb)
+        kb[0, :n0], vb[0, :n0] = k, v
+        kv.append((kb, vb))
+    for i in range(steps - 1):
+        n = n0 + i
+        sc, rows = odec.step_cached(w, seq[n:n + 1], kv, n, dense)
+        assert rel_l2(sc[0], odec.step_scores(w, seq[:n + 1])) < 1e-5, i
+        # the row was written into the preallocated caches at position n
+        assert np.array_equal(kv[0][0][0, n], rows[0][0][0])
+    # fp16 caches: in place over a preallocated cache == the concatenating form
+    n = n0
+    kv16 = [(oracle.f32_to_f16(k).reshape(1, n, *k.shape[1:]),
+             oracle.f32_to_f16(v).reshape(1, n, *v.shape[1:])) for k, v in kvs]
+    a, _ = odec.step_cached(w, seq[n:n + 1], kv16, n)
+    pre = []
+    for k, v in kv16:
+        kb = np.zeros((1, n + 3) + k.shape[2:], np.uint16)
+        vb = np.zeros_like(kb)
+        kb[:, :n], vb[:, :n] = k, v
+        pre.append((kb, vb))
+    b, _ = odec.step_cached(w, seq[n:n + 1], pre, n)
+    assert np.array_equal(a, b)
+
+
+def test_attn_cached_f32_matches_orc_attn_decode():
+    """The float64 textbook attention of the fp32-cache step against orc_attn_decode on
+    fp16-representable caches (the same values in both element types)."""
+    rng = np.random.default_rng(3)
+    B, n, Hq, Hkv, hd = 2, 40, 6, 2, 64
+    q = rng.standard_normal((B, Hq, hd)).astype(np.float32)
+    k16 = oracle.f32_to_f16(rng.standard_normal((B, n + 1, Hkv, hd)).astype(np.float32))
+    v16 = oracle.f32_to_f16(rng.standard_normal((B, n + 1, Hkv, hd)).astype(np.float32))
+    k16 = k16.reshape(B, n + 1, Hkv, hd)
+    v16 = v16.reshape(B, n + 1, Hkv, hd)
+    kf = oracle.f16_to_f32(k16).reshape(k16.shape)
+    vf = oracle.f16_to_f32(v16).reshape(v16.shape)
+    got = odec.attn_cached_f32(q, kf, vf, n, Hq, Hkv, hd)
+    want = oracle.attn_decode(q, k16, v16, None, Hq, Hkv, hd)
+    assert rel_l2(got, want) < 1e-6
