@@ -213,23 +213,15 @@ def cpu_decode_step(w, ctx: int, seconds: float):
 
 def decode_leg(args):
     """tokens/s of graph-replayed decode steps after a 512-token prefill."""
-    from cortexsdr_amd import synth
-    from cortexsdr_amd.decoder import QWEN2_0_5B, Decoder, synthetic_weights
+    from cortexsdr_amd import bench_cli
+    from cortexsdr_amd.decoder import Decoder
 
-    spec, n_prompt, n_new = QWEN2_0_5B, 512, 128
-    w = synthetic_weights(spec, seed=0)
-    prompt = (synth.uniform(77, n_prompt, stream=61) * spec.vocab).astype(np.int32)
+    n_prompt, n_new = 512, 128
+    # the workload and call sequence tests/test_full_depth_gpu.py checks against the oracle
+    w, prompt = bench_cli.cfg4_workload(n_prompt, seed=0)
     dec = Decoder(w)
     try:
-        dec.prefill(prompt[:8], 0.0, 0.0)   # captures the step graphs; untimed
-        dec.decode(8, 0.0, 0.0)
-        t0 = time.perf_counter()
-        dec.prefill(prompt, 0.0, 0.0)       # greedy: temperature 0 (scale 1), no penalty
-        t_pre = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        dec.decode(n_new - 1, 0.0, 0.0)     # token 1 came from the prefill's last step
-        t_dec = time.perf_counter() - t0
-        toks = dec.tokens(n_prompt, n_new)
+        t_pre, t_dec, toks = bench_cli.cfg4_run(dec, prompt, n_new)
     finally:
         dec.close()
     per_tok = t_dec / (n_new - 1)

@@ -181,26 +181,45 @@ def bench_gguf(torch, fmt_name, R, Cc, M, steps):
             "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
 
 
+def cfg4_workload(n_prompt=512, seed=0):
+    """Config 4's model and prompt: the Qwen2-0.5B-shaped decoder with every linear
+    HSDB-coded against one shared 1024 x 64 dictionary (8 nnz per block) and a prompt of
+    n_prompt uniform random token ids. bench.py, this CLI and the GPU parity test of the
+    benchmarked run share it."""
+    from .decoder import QWEN2_0_5B, synthetic_weights
+
+    w = synthetic_weights(QWEN2_0_5B, seed=seed)
+    prompt = (synth.uniform(seed + 77, n_prompt, stream=61) * QWEN2_0_5B.vocab).astype(np.int32)
+    return w, prompt
+
+
+def cfg4_run(dec, prompt, n_new):
+    """The benchmarked greedy run on a decoder: a warm-up over the first 8 prompt tokens
+    (captures both step graphs), then the prompt (multi-token prefill, its last token through
+    the step graph, which picks new token 1) and n_new - 1 decode steps in one call.
+    Returns (prefill seconds, decode seconds, the n_new new tokens)."""
+    dec.prefill(prompt[:8], 0.0, 0.0)
+    dec.decode(8, 0.0, 0.0)
+    t0 = time.perf_counter()
+    dec.prefill(prompt, 0.0, 0.0)       # greedy: temperature 0 (scale 1), no penalty
+    t_prefill = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    dec.decode(n_new - 1, 0.0, 0.0)
+    t_decode = time.perf_counter() - t0
+    return t_prefill, t_decode, dec.tokens(len(prompt), n_new)
+
+
 def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
     """Config 4: Qwen2-0.5B-shaped decoder, all linears HSDB-coded (1024 x 64 shared
     dictionary, 8 nnz per block), prompt of uniform random ids, greedy (plain argmax)."""
-    from .decoder import QWEN2_0_5B, Decoder, synthetic_weights
+    from .decoder import QWEN2_0_5B, Decoder
 
     t0 = time.time()
-    w = synthetic_weights(QWEN2_0_5B, seed=seed)
+    w, prompt = cfg4_workload(n_prompt, seed)
     t_build = time.time() - t0
-    prompt = (synth.uniform(seed + 77, n_prompt, stream=61) * QWEN2_0_5B.vocab).astype(np.int32)
     dec = Decoder(w)
     try:
-        dec.prefill(prompt[:8], 0.0, 0.0)          # capture both graphs, warm up
-        dec.decode(8, 0.0, 0.0)
-        t0 = time.perf_counter()
-        dec.prefill(prompt, 0.0, 0.0)
-        t_prefill = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        dec.decode(n_new - 1, 0.0, 0.0)
-        t_decode = time.perf_counter() - t0
-        toks = dec.tokens(n_prompt, n_new)
+        t_prefill, t_decode, toks = cfg4_run(dec, prompt, n_new)
         per_tok = t_decode / (n_new - 1)
         code = w.code_bytes()
         kv = 2 * QWEN2_0_5B.n_layers * QWEN2_0_5B.n_kv_heads * QWEN2_0_5B.head_dim * 4  # fp32 cache
@@ -218,6 +237,21 @@ def bench_decoder(torch, n_prompt=512, n_new=128, seed=0):
         dec.close()
 
 
+def cfg5_weights(max_ctx: int, seed: int = 5):
+    """Config 5's model: Llama-7B shape (32 layers, hidden 4096, 32 heads of 128, SwiGLU
+    11008, vocab 32000, fp16 K/V cache), every linear HSDB-coded (1024 x 64 dictionary, 8 nnz
+    per block). Two distinct coded layers are generated and used 16 times each (the decoder
+    loads a device copy per layer, so a step still streams 32 layers' codes)."""
+    import dataclasses
+
+    from .decoder import DecoderSpec, DecoderWeights, synthetic_weights
+
+    spec = DecoderSpec(32, 4096, 32, 32, 128, 11008, 32000, max_ctx, kv_dtype="f16")
+    w2 = synthetic_weights(dataclasses.replace(spec, n_layers=2), seed=seed)
+    return DecoderWeights(spec, [w2.layers[l % 2] for l in range(32)], w2.lm_head,
+                          w2.final_norm)
+
+
 def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
     """Config 5: Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads of 128, SwiGLU
     11008, vocab 32000, all linears HSDB-coded: 1024 x 64 dictionary, 8 nnz per block) at
@@ -225,14 +259,11 @@ def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
     sequences, weights resident.
     Two distinct coded layers are generated and loaded 16 times each: every layer has its own
     device copy, so HBM traffic per step is that of 32 distinct layers."""
-    import dataclasses
+    from .decoder import Decoder
 
-    from .decoder import Decoder, DecoderSpec, DecoderWeights, synthetic_weights
-
-    spec = DecoderSpec(32, 4096, 32, 32, 128, 11008, 32000, ctx + steps + 8, kv_dtype="f16")
     t0 = time.time()
-    w2 = synthetic_weights(dataclasses.replace(spec, n_layers=2), seed=seed)
-    w = DecoderWeights(spec, [w2.layers[l % 2] for l in range(32)], w2.lm_head, w2.final_norm)
+    w = cfg5_weights(ctx + steps + 8, seed)
+    spec = w.spec
     t_build = time.time() - t0
     dec = Decoder(w, batch=batch)
     try:

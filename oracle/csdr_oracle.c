@@ -197,27 +197,35 @@ int orc_hsdr_decompress(const uint8_t* buf, size_t n, float* out, size_t out_flo
     float* D = copy_dict(buf, &v);
     float* coef = (float*)malloc(v.n_codes * 4 + 4);
     uint16_t* idx = (uint16_t*)malloc(v.n_codes * 2 + 2);
-    float* tile = (float*)malloc(tile_dim * 4);
-    if (!D || !coef || !idx || !tile) {
-        free(D), free(coef), free(idx), free(tile);
+    if (!D || !coef || !idx) {
+        free(D), free(coef), free(idx);
         return ORC_E_ARG;
     }
     orc_hsdr_unpack(buf, n, idx, NULL, coef);
-    for (size_t t = 0; t < v.n_tiles; ++t) {
-        /* decodeAllTiles, :612-634: zero tile, then stage-major slot accumulation */
-        for (size_t c = 0; c < tile_dim; ++c) tile[c] = 0.0f;
-        for (size_t s = 0; s < v.slots_per_tile; ++s) {
-            size_t slot = t * v.slots_per_tile + s;
-            const float scale = coef[slot];
-            /* the reference's sign-0 skip (:626) never fires: unpacked signs are +-1 */
-            if (idx[slot] >= v.n_atoms) continue; /* out of range: reference reads past D */
-            const float* atom = D + (size_t)idx[slot] * tile_dim;
-            for (size_t c = 0; c < tile_dim; ++c) tile[c] = fmaf(scale, atom[c], tile[c]);
+    /* tiles are decoded independently (each element's slot order is the reference's), so
+     * they run in parallel */
+#pragma omp parallel
+    {
+        float* tile = (float*)malloc(tile_dim * 4);
+#pragma omp for schedule(static)
+        for (long long tt = 0; tt < (long long)v.n_tiles; ++tt) {
+            const size_t t = (size_t)tt;
+            /* decodeAllTiles, :612-634: zero tile, then stage-major slot accumulation */
+            for (size_t c = 0; c < tile_dim; ++c) tile[c] = 0.0f;
+            for (size_t s = 0; s < v.slots_per_tile; ++s) {
+                size_t slot = t * v.slots_per_tile + s;
+                const float scale = coef[slot];
+                /* the reference's sign-0 skip (:626) never fires: unpacked signs are +-1 */
+                if (idx[slot] >= v.n_atoms) continue; /* out of range: reference reads past D */
+                const float* atom = D + (size_t)idx[slot] * tile_dim;
+                for (size_t c = 0; c < tile_dim; ++c) tile[c] = fmaf(scale, atom[c], tile[c]);
+            }
+            /* reassembleTiles, :119-135: tile (br, bc) -> rows br*tr.., cols bc*tc.. */
+            size_t br = t / n_col_tiles, bc = t % n_col_tiles;
+            for (size_t r = 0; r < tr; ++r)
+                memcpy(out + (br * tr + r) * C + bc * tc, tile + r * tc, tc * 4);
         }
-        /* reassembleTiles, :119-135: tile (br, bc) -> rows br*tr.., cols bc*tc.. */
-        size_t br = t / n_col_tiles, bc = t % n_col_tiles;
-        for (size_t r = 0; r < tr; ++r)
-            memcpy(out + (br * tr + r) * C + bc * tc, tile + r * tc, tc * 4);
+        free(tile);
     }
     /* edge splice: top-right strip then bottom strip, :1401-1438 */
     size_t e = 0;
@@ -226,7 +234,7 @@ int orc_hsdr_decompress(const uint8_t* buf, size_t n, float* out, size_t out_flo
         for (size_t c = C_full; c < C; ++c, ++e) memcpy(out + r * C + c, eb + 4 * e, 4);
     for (size_t r = R_full; r < R; ++r)
         for (size_t c = 0; c < C; ++c, ++e) memcpy(out + r * C + c, eb + 4 * e, 4);
-    free(D), free(coef), free(idx), free(tile);
+    free(D), free(coef), free(idx);
     return ORC_OK;
 }
 

@@ -55,10 +55,10 @@ class DenseWeights:
 
 def _linear(stream, x_tc: np.ndarray, bias=None, dense: DenseWeights | None = None) -> np.ndarray:
     """(T, C) -> (T, R): the reference's run_cached_linear per token on feature-major x (with
-    `dense`: x times the decoded W^T, in float64)."""
+    `dense`: x times the decoded W^T, an fp32 dense product)."""
     if dense is not None:
         W = dense.get(stream)
-        y = np.asarray(x_tc, np.float64) @ W.T.astype(np.float64)
+        y = np.asarray(x_tc, np.float32) @ W.T
     else:
         y = hsdb_matmul(stream, np.ascontiguousarray(x_tc.T, np.float32)).T
     if bias is not None:
