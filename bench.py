@@ -34,6 +34,9 @@ The JSON line carries:
   decode_7b     configs[4]: the Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads
                 of 128, SwiGLU 11008, vocab 32000, HSDB-coded linears) over an fp16 KV
                 context of 4096 positions, batch 1 and 8, weights and KV resident
+  decode_7b_streaming  the same step with on-demand layer streaming: blocks in pinned host
+                memory, copied to the device per step (prefetch on at batch 1 and 8, off at
+                batch 1), ms per step and the host-to-device GB/s of the streamed codes
   encode        the compress side: GPU matching pursuit (rows/s, TFLOP/s against the fp32
                 vector peak) and compress wall time on Qwen2-0.5B-shaped attention / MLP
                 matrices, next to the reference's own compress (oracle/_ref)
@@ -258,6 +261,22 @@ def decode_7b_leg(torch):
         out.append({k: r[k] for k in ("batch", "context", "ms_per_step", "tokens_per_s",
                                       "code_GB_per_step", "kv_GB_per_step", "alg_GBps",
                                       "hbm_frac")})
+        torch.cuda.empty_cache()
+    return out
+
+
+def decode_7b_streaming_leg(torch):
+    """configs[4] "with on-demand layer streaming": the same step with every block's codes in
+    pinned host memory, copied to the device when the block runs (the next block's copy under
+    the current block's kernels with prefetch); ms per step and the host-to-device rate of the
+    streamed code bytes (PCIe-bound, reported apart from the resident headline)."""
+    from cortexsdr_amd import bench_cli
+
+    out = []
+    for B, pf in ((1, True), (8, True), (1, False)):
+        r = bench_cli.bench_decoder_7b(torch, batch=B, stream_layers=True, prefetch=pf)
+        out.append({k: r[k] for k in ("batch", "prefetch", "context", "ms_per_step",
+                                      "tokens_per_s", "streamed_GB_per_step", "pcie_GBps")})
         torch.cuda.empty_cache()
     return out
 
@@ -516,6 +535,7 @@ def main():
         out["decode"] = decode_leg(args)
     if not args.no_7b:
         out["decode_7b"] = decode_7b_leg(torch)
+        out["decode_7b_streaming"] = decode_7b_streaming_leg(torch)
     if not args.no_encode:
         out["encode"] = encode_leg(args)
     if args.calibrate_copy:

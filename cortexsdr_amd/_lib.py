@@ -239,6 +239,9 @@ SIGNATURES["csdr_attn_prefill"] = (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.
                                            C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp,
                                            _vp])
 SIGNATURES["csdr_decoder_set_prefill_chunk"] = (C.c_int, [_vp, C.c_int])
+SIGNATURES["csdr_hsdb_load_host"] = (C.c_int, [_vp, _sz, _vp, C.POINTER(_vp)])
+SIGNATURES["csdr_decoder_set_layer_prefetch"] = (C.c_int, [_vp, C.c_int])
+SIGNATURES["csdr_decoder_streamed_bytes"] = (C.c_int64, [_vp])
 SIGNATURES["csdr_hsdr_source_format"] = (C.c_int, [C.c_char_p, C.c_int])
 SIGNATURES["csdr_hsdr_source_elements"] = (_sz, [C.c_int, _sz])
 SIGNATURES["csdr_hsdr_source_decode"] = (C.c_int, [_vp, _sz, C.c_int, C.c_float, C.c_float, _vp,

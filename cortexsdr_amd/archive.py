@@ -194,7 +194,13 @@ class InferenceEngine:
         _ce(self._lib.cortex_inference_engine_init_memory_pool(self._h, mb))
 
     def set_aggressive_memory(self, enable: bool):
+        """Also the decoder's residency: on, generate_text's blocks stay in pinned host memory
+        and are streamed to the device when they run."""
         _ce(self._lib.cortex_inference_engine_enable_aggressive_memory(self._h, int(enable)))
+
+    def set_layer_prefetch(self, enable: bool):
+        """Streamed blocks: copy the next block while the current one runs (default on)."""
+        _ce(self._lib.cortex_inference_engine_enable_layer_prefetch(self._h, int(enable)))
 
     def matmul_device(self, name: str, x, y, stream=None):
         """Device x (C, M) fp32/fp16 torch tensor -> device y (R, M) fp32."""

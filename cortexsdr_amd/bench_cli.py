@@ -252,7 +252,8 @@ def cfg5_weights(max_ctx: int, seed: int = 5):
                           w2.final_norm)
 
 
-def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
+def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1, stream_layers=False,
+                     prefetch=True):
     """Config 5: Llama-7B-shaped decode step (32 layers, hidden 4096, 32 heads of 128, SwiGLU
     11008, vocab 32000, all linears HSDB-coded: 1024 x 64 dictionary, 8 nnz per block) at
     context `ctx` with the fp16 KV cache (as configs[4] states) filled with N(0,1), `batch`
@@ -265,7 +266,7 @@ def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
     w = cfg5_weights(ctx + steps + 8, seed)
     spec = w.spec
     t_build = time.time() - t0
-    dec = Decoder(w, batch=batch)
+    dec = Decoder(w, batch=batch, stream_layers=stream_layers, prefetch=prefetch)
     try:
         for l in range(spec.n_layers):
             k = torch.randn((batch, ctx, spec.n_kv_heads, spec.head_dim), device="cuda").half()
@@ -288,7 +289,11 @@ def bench_decoder_7b(torch, ctx=4096, steps=16, seed=5, batch=1):
                 "alg_GBps": round((code + kv) / dt / 1e9, 1),
                 "hbm_frac": round((code + kv) / dt / HBM_PEAK, 4),
                 "device_GB": round(dec.device_bytes() / 1e9, 2),
-                "host_build_s": round(t_build, 1)}
+                "host_build_s": round(t_build, 1),
+                **({"streamed": True, "prefetch": bool(prefetch),
+                    "streamed_GB_per_step": round(dec.streamed_bytes() / 1e9, 3),
+                    "pcie_GBps": round(dec.streamed_bytes() / dt / 1e9, 2)}
+                   if stream_layers else {})}
     finally:
         dec.close()
 
@@ -369,6 +374,8 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default=None)
     ap.add_argument("--cfg2-batches", default="1,16,64,256")
     ap.add_argument("--cfg5-batches", default="1,8")
+    ap.add_argument("--cfg5-stream", action="store_true",
+                    help="cfg5 also with on-demand layer streaming (host-resident blocks)")
     ap.add_argument("--suite", default=None, help="run a bench suite JSON through the text CLI")
     args = ap.parse_args(argv)
     if args.suite:
@@ -421,6 +428,11 @@ def main(argv=None) -> int:
             out.append(bench_decoder_7b(torch, batch=B))
             print(json.dumps(out[-1]), flush=True)
             torch.cuda.empty_cache()
+            if args.cfg5_stream:
+                for pf in (True, False):
+                    out.append(bench_decoder_7b(torch, batch=B, stream_layers=True, prefetch=pf))
+                    print(json.dumps(out[-1]), flush=True)
+                    torch.cuda.empty_cache()
         res["results"]["cfg5"] = out
     if "cfg4" in cfgs:
         res["results"]["cfg4"] = bench_decoder(torch)

@@ -36,6 +36,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "hsdb_impl.hpp"
 
 namespace {
 
@@ -110,12 +111,22 @@ __global__ __launch_bounds__(kSanThreads) void sanitize_kernel(float* __restrict
     }
 }
 
+constexpr int kBlockMats = 7;  // q, k, v, o, gate, up, down
+
 struct Layer {
     const csdr_hsdb *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
     const csdr_hsdb *gate = nullptr, *up = nullptr, *down = nullptr;
     float *attn_norm = nullptr, *ffn_norm = nullptr;
     float *bq = nullptr, *bk = nullptr, *bv = nullptr;
     void *kc = nullptr, *vc = nullptr;  // cfg.kv_dtype elements
+    // streamed block: the caller's host-resident segments, and device views of them whose
+    // code words are the block's copy in staging buffer `slot` (at off[i])
+    bool streamed = false;
+    const csdr_hsdb* src[kBlockMats] = {};
+    csdr_hsdb view[kBlockMats];
+    size_t off[kBlockMats] = {};
+    size_t bytes = 0;
+    int slot = 0, rank = 0;  // staging buffer; position among the streamed blocks
 };
 
 }  // namespace
@@ -158,6 +169,15 @@ struct csdr_decoder {
     float *pf_x = nullptr, *pf_h = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     float *pf_a = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_w = nullptr;
     int* pf_tok = nullptr;
+    // on-demand layer streaming (blocks of host-resident segments)
+    bool prefetch = true;           // copy block j + 2 while block j + 1 runs (else j + 1 after j)
+    bool stage_ready = false;       // staging buffers, views, copy stream and events built
+    std::vector<int> streamed;      // the streamed blocks in order
+    void* stage[2] = {nullptr, nullptr};
+    size_t stage_bytes = 0;
+    hipStream_t cstream = nullptr;  // the staging copies' stream (default priority)
+    std::vector<hipEvent_t> ev_copied, ev_done;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -231,6 +251,151 @@ int mm_xop(csdr_decoder* d, int n, const csdr_hsdb* const* segs, const float* x,
                                       st);
 }
 
+// ---- on-demand layer streaming
+// A streamed block's code words are copied (on d->cstream) into staging buffer slot
+// rank % 2 before the block runs; the copy of the block `depth` places later (2 with
+// prefetch, else 1) waits for this block's kernels to finish, the last reader of that
+// buffer. Events order the two streams, so the same sequence works issued directly or
+// captured into the step graph (the copies become graph nodes).
+
+void free_streaming(csdr_decoder* d) {
+    if (d->cstream) {
+        (void)hipStreamSynchronize(d->cstream);
+        (void)hipStreamDestroy(d->cstream);
+    }
+    for (hipEvent_t e : d->ev_copied) if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : d->ev_done) if (e) (void)hipEventDestroy(e);
+    if (d->ev_fork) (void)hipEventDestroy(d->ev_fork);
+    if (d->ev_join) (void)hipEventDestroy(d->ev_join);
+    for (void*& p : d->stage) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+    }
+    d->cstream = nullptr;
+    d->ev_copied.clear();
+    d->ev_done.clear();
+    d->ev_fork = d->ev_join = nullptr;
+    d->stage_bytes = 0;
+    d->stage_ready = false;
+}
+
+// Staging buffers sized for the largest streamed block, the blocks' device views, the copy
+// stream and the events.
+int setup_streaming(csdr_decoder* d) {
+    free_streaming(d);
+    d->streamed.clear();
+    size_t most = 0;
+    for (int l = 0; l < (int)d->layers.size(); ++l) {
+        Layer& L = d->layers[l];
+        if (!L.streamed) continue;
+        L.rank = (int)d->streamed.size();
+        L.slot = L.rank % 2;
+        d->streamed.push_back(l);
+        size_t off = 0;
+        for (int i = 0; i < kBlockMats; ++i) {
+            L.off[i] = off;
+            off += csdr::align_up(csdr::code_bytes(L.src[i]), 256);
+        }
+        L.bytes = off;
+        most = std::max(most, off);
+    }
+    if (d->streamed.empty()) {
+        d->stage_ready = true;
+        return CSDR_OK;
+    }
+    for (void*& p : d->stage)
+        if (hipMalloc(&p, std::max<size_t>(most, 256)) != hipSuccess) {
+            free_streaming(d);
+            return set_error(CSDR_E_HIP, "decoder: out of device memory for the layer staging "
+                                         "buffers (2 x " + std::to_string(most) + " bytes)");
+        }
+    d->stage_bytes = most;
+    for (int l : d->streamed) {
+        Layer& L = d->layers[l];
+        for (int i = 0; i < kBlockMats; ++i) {
+            L.view[i] = *L.src[i];
+            L.view[i].h_codes = nullptr;
+            L.view[i].dict_ref = nullptr;  // a view: never released
+            L.view[i].d_codes =
+                reinterpret_cast<uint32_t*>(static_cast<char*>(d->stage[L.slot]) + L.off[i]);
+        }
+    }
+    if (hipStreamCreateWithFlags(&d->cstream, hipStreamNonBlocking) != hipSuccess) {
+        free_streaming(d);
+        return set_error(CSDR_E_HIP, "decoder: copy stream creation failed");
+    }
+    const size_t nl = d->layers.size();
+    d->ev_copied.assign(nl, nullptr);
+    d->ev_done.assign(nl, nullptr);
+    bool okv = hipEventCreateWithFlags(&d->ev_fork, hipEventDisableTiming) == hipSuccess &&
+               hipEventCreateWithFlags(&d->ev_join, hipEventDisableTiming) == hipSuccess;
+    for (int l : d->streamed)
+        okv = okv &&
+              hipEventCreateWithFlags(&d->ev_copied[l], hipEventDisableTiming) == hipSuccess &&
+              hipEventCreateWithFlags(&d->ev_done[l], hipEventDisableTiming) == hipSuccess;
+    if (!okv) {
+        free_streaming(d);
+        return set_error(CSDR_E_HIP, "decoder: event creation failed");
+    }
+    d->stage_ready = true;
+    return CSDR_OK;
+}
+
+// Block l's code words into its staging buffer, on the copy stream.
+int stage_copy(csdr_decoder* d, int l) {
+    const Layer& L = d->layers[l];
+    char* dst = static_cast<char*>(d->stage[L.slot]);
+    for (int i = 0; i < kBlockMats; ++i) {
+        const size_t n = csdr::code_bytes(L.src[i]);
+        if (n)
+            CSDR_HIP_CHECK(hipMemcpyAsync(dst + L.off[i], L.src[i]->h_codes, n,
+                                          hipMemcpyHostToDevice, d->cstream));
+    }
+    CSDR_HIP_CHECK(hipEventRecord(d->ev_copied[l], d->cstream));
+    return CSDR_OK;
+}
+
+int stream_depth(const csdr_decoder* d) { return d->prefetch ? 2 : 1; }
+
+// Before the first block of a step or pass: the copy stream joins st's work, and the first
+// blocks' copies start.
+int stream_begin(csdr_decoder* d, hipStream_t st) {
+    if (d->streamed.empty()) return CSDR_OK;
+    CSDR_HIP_CHECK(hipEventRecord(d->ev_fork, st));
+    CSDR_HIP_CHECK(hipStreamWaitEvent(d->cstream, d->ev_fork, 0));
+    const int n = std::min<int>(stream_depth(d), (int)d->streamed.size());
+    for (int j = 0; j < n; ++j) RC(stage_copy(d, d->streamed[j]));
+    return CSDR_OK;
+}
+
+// Block l runs after its copy.
+int layer_begin(csdr_decoder* d, int l, hipStream_t st) {
+    if (!d->layers[l].streamed) return CSDR_OK;
+    CSDR_HIP_CHECK(hipStreamWaitEvent(st, d->ev_copied[l], 0));
+    return CSDR_OK;
+}
+
+// After block l: the copy into its buffer of the block `depth` streamed places later.
+int layer_end(csdr_decoder* d, int l, hipStream_t st) {
+    const Layer& L = d->layers[l];
+    if (!L.streamed) return CSDR_OK;
+    CSDR_HIP_CHECK(hipEventRecord(d->ev_done[l], st));
+    const int j = L.rank + stream_depth(d);
+    if (j < (int)d->streamed.size()) {
+        CSDR_HIP_CHECK(hipStreamWaitEvent(d->cstream, d->ev_done[l], 0));
+        RC(stage_copy(d, d->streamed[j]));
+    }
+    return CSDR_OK;
+}
+
+// After the last block: st waits for the copy stream's work (joins a captured fork).
+int stream_end(csdr_decoder* d, hipStream_t st) {
+    if (d->streamed.empty()) return CSDR_OK;
+    CSDR_HIP_CHECK(hipEventRecord(d->ev_join, d->cstream));
+    CSDR_HIP_CHECK(hipStreamWaitEvent(st, d->ev_join, 0));
+    return CSDR_OK;
+}
+
 // Prefill pass rows: row b * T + t takes sequence b's token at position p0 + t.
 __global__ void pass_tokens_kernel(const int* __restrict__ ring, int cap, int B, int T, int p0,
                                    int* __restrict__ tok) {
@@ -300,8 +465,10 @@ int prefill_pass(csdr_decoder* d, int p0, int T, hipStream_t st) {
     pass_tokens_kernel<<<(M + 255) / 256, 256, 0, st>>>(d->ring, cap, B, T, p0, d->pf_tok);
     CSDR_LAUNCH_CHECK("decoder pass tokens");
     RC(csdr_hsdb_decode_rows(d->emb, d->pf_tok, M, d->pf_x, st));
+    RC(stream_begin(d, st));
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer& L = d->layers[l];
+        RC(layer_begin(d, l, st));
         RC(csdr_rms_norm(d->pf_x, L.attn_norm, M, H, c.rms_eps, d->pf_h, st));
         RC(pass_linear(d, L.q, d->pf_h, M, d->pf_q, L.bq, 0, st));
         RC(pass_linear(d, L.k, d->pf_h, M, d->pf_k, L.bk, 0, st));
@@ -316,8 +483,9 @@ int prefill_pass(csdr_decoder* d, int p0, int T, hipStream_t st) {
         RC(pass_linear(d, L.up, d->pf_h, M, d->pf_u, nullptr, 0, st));
         RC(csdr_silu_mul(d->pf_g, d->pf_u, (size_t)M * F, d->pf_a, st));
         RC(pass_linear(d, L.down, d->pf_a, M, d->pf_x, nullptr, CSDR_HSDB_ACCUMULATE, st));
+        RC(layer_end(d, l, st));
     }
-    return CSDR_OK;
+    return stream_end(d, st);
 }
 
 // One step at device position *pos for the token ring[*pos]; with_head adds the output norm,
@@ -329,10 +497,15 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
     step_begin_kernel<<<1, 64, 0, st>>>(d->pos, d->ring, cap, B, d->tok, d->len);
     CSDR_LAUNCH_CHECK("decoder step_begin");
     RC(csdr_hsdb_decode_rows(d->emb, d->tok, B, d->x, st));
+    if (!d->fused && (B > 1 || c.kv_dtype != CSDR_F16))
+        return set_error(CSDR_E_UNSUPPORTED,
+                         "decoder: the unfused step runs batch 1 over an fp16 K/V cache only");
+    RC(stream_begin(d, st));
     for (int l = 0; l < c.n_layers && d->fused; ++l) {
         // fused form: 5 calls (9 launches) per block; the normed inputs, the rotated q/k, the
         // attention output and silu(gate)*up are never written out
         const Layer& L = d->layers[l];
+        RC(layer_begin(d, l, st));
         {
             const csdr_hsdb* segs[3] = {L.q, L.k, L.v};
             float* ys[3] = {d->q, d->k, d->v};
@@ -364,12 +537,11 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
             RC(mm_xop(d, 1, segs, d->g, d->u, ys, nullptr, CSDR_HSDB_ACCUMULATE,
                       CSDR_XOP_SILU_MUL, nullptr, st));
         }
+        RC(layer_end(d, l, st));
     }
-    if (!d->fused && (B > 1 || c.kv_dtype != CSDR_F16))
-        return set_error(CSDR_E_UNSUPPORTED,
-                         "decoder: the unfused step runs batch 1 over an fp16 K/V cache only");
     for (int l = 0; l < c.n_layers && !d->fused; ++l) {
         const Layer& L = d->layers[l];
+        RC(layer_begin(d, l, st));
         RC(csdr_rms_norm(d->x, L.attn_norm, 1, H, c.rms_eps, d->h, st));
         {
             const csdr_hsdb* segs[3] = {L.q, L.k, L.v};
@@ -401,7 +573,9 @@ int step(csdr_decoder* d, hipStream_t st, bool with_head, float temperature, flo
             float* ys[1] = {d->x};
             RC(mm(d, 1, segs, d->a, ys, nullptr, CSDR_HSDB_ACCUMULATE, st));  // x += down(a)
         }
+        RC(layer_end(d, l, st));
     }
+    RC(stream_end(d, st));
     if (!with_head) {
         advance_kernel<<<1, 64, 0, st>>>(d->pos);
         CSDR_LAUNCH_CHECK("decoder advance");
@@ -447,6 +621,10 @@ int ready(csdr_decoder* d) {
         if (!d->layers[l].q)
             return set_error(CSDR_E_INVALID, "decoder: layer " + std::to_string(l) + " not set");
     if (!d->lm || !d->emb) return set_error(CSDR_E_INVALID, "decoder: output head not set");
+    if (!d->stage_ready) {
+        destroy_graphs(d);
+        RC(setup_streaming(d));
+    }
     if (d->ws_hsdb_alloc < d->ws_hsdb_bytes) {
         unsigned char* p = nullptr;
         RC(dalloc(d, &p, d->ws_hsdb_bytes));
@@ -576,6 +754,7 @@ CSDR_API int csdr_decoder_free(csdr_decoder* d) {
     if (!d) return CSDR_OK;
     if (d->stream) (void)hipStreamSynchronize(d->stream);
     destroy_graphs(d);
+    free_streaming(d);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     free_prefill(d);
     for (void* p : d->allocs) (void)hipFree(p);
@@ -600,10 +779,25 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* d, int layer, const csdr_hsdb*
     RC(check_shape(wgate, F, H, "gate"));
     RC(check_shape(wup, F, H, "up"));
     RC(check_shape(wdown, H, F, "down"));
+    const csdr_hsdb* w7[kBlockMats] = {wq, wk, wv, wo, wgate, wup, wdown};
+    int on_host = 0;
+    for (const csdr_hsdb* w : w7) on_host += csdr::codes_on_device(w) ? 0 : 1;
+    if (on_host != 0 && on_host != kBlockMats)
+        return set_error(CSDR_E_INVALID, "decoder_set_layer: a block's segments must be all "
+                                         "device-resident or all host-resident");
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
     destroy_graphs(d);
+    if (d->cstream) CSDR_HIP_CHECK(hipStreamSynchronize(d->cstream));
+    d->stage_ready = false;  // the staging layout is rebuilt before the next run
     Layer& L = d->layers[layer];
-    L.q = wq, L.k = wk, L.v = wv, L.o = wo, L.gate = wgate, L.up = wup, L.down = wdown;
+    L.streamed = on_host == kBlockMats;
+    if (L.streamed) {
+        for (int i = 0; i < kBlockMats; ++i) L.src[i] = w7[i];
+        L.q = &L.view[0], L.k = &L.view[1], L.v = &L.view[2], L.o = &L.view[3];
+        L.gate = &L.view[4], L.up = &L.view[5], L.down = &L.view[6];
+    } else {
+        L.q = wq, L.k = wk, L.v = wv, L.o = wo, L.gate = wgate, L.up = wup, L.down = wdown;
+    }
     RC(upload_vec(d, &L.attn_norm, attn_norm, H));
     RC(upload_vec(d, &L.ffn_norm, ffn_norm, H));
     RC(upload_vec(d, &L.bq, bq, H));
@@ -619,12 +813,33 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* d, int layer, const csdr_hsdb*
     return CSDR_OK;
 }
 
+CSDR_API int csdr_decoder_set_layer_prefetch(csdr_decoder* d, int enable) {
+    if (!d) return set_error(CSDR_E_INVALID, "decoder_set_layer_prefetch: null handle");
+    if (d->prefetch == (enable != 0)) return CSDR_OK;
+    CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
+    destroy_graphs(d);  // the captured copy dependencies change
+    d->prefetch = enable != 0;
+    return CSDR_OK;
+}
+
+CSDR_API int64_t csdr_decoder_streamed_bytes(const csdr_decoder* d) {
+    if (!d) return -1;
+    int64_t n = 0;
+    for (const Layer& L : d->layers)
+        if (L.streamed)
+            for (const csdr_hsdb* w : L.src) n += (int64_t)csdr::code_bytes(w);
+    return n;
+}
+
 CSDR_API int csdr_decoder_set_output(csdr_decoder* d, const csdr_hsdb* lm_head,
                                      const float* final_norm, const csdr_hsdb* embedding) {
     if (!d) return set_error(CSDR_E_INVALID, "decoder_set_output: null handle");
     const csdr_decoder_config& c = d->cfg;
     RC(check_shape(lm_head, c.vocab, c.hidden, "lm_head"));
     if (embedding) RC(check_shape(embedding, c.vocab, c.hidden, "embedding"));
+    if (!csdr::codes_on_device(lm_head) || (embedding && !csdr::codes_on_device(embedding)))
+        return set_error(CSDR_E_INVALID, "decoder_set_output: the output head and embedding "
+                                         "must be device-resident segments");
     CSDR_HIP_CHECK(hipStreamSynchronize(d->stream));
     destroy_graphs(d);
     d->lm = lm_head;

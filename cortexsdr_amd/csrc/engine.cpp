@@ -23,6 +23,8 @@
 #include <map>
 #include <mutex>
 #include <regex>
+#include <exception>
+#include <new>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -40,6 +42,22 @@ CortexError fail(int code, const std::string& m) {
     t_msg = m;
     return {t_msg.c_str(), code};
 }
+
+// No C++ exception crosses the C ABI: every CortexError entry point runs its body inside
+// CORTEX_GUARD_BEGIN ... CORTEX_GUARD_END(name), which turns std::bad_alloc into
+// CORTEX_ERROR_MEMORY and any other exception into CORTEX_ERROR_UNKNOWN with its message.
+#define CORTEX_GUARD_BEGIN try {
+#define CORTEX_GUARD_END(fn_)                                                            \
+    }                                                                                    \
+    catch (const std::bad_alloc&) {                                                      \
+        return fail(CORTEX_ERROR_MEMORY, std::string(fn_) + ": out of host memory");    \
+    }                                                                                    \
+    catch (const std::exception& ex_) {                                                  \
+        return fail(CORTEX_ERROR_UNKNOWN, std::string(fn_) + ": " + ex_.what());        \
+    }                                                                                    \
+    catch (...) {                                                                        \
+        return fail(CORTEX_ERROR_UNKNOWN, std::string(fn_) + ": unknown exception");    \
+    }
 // A csdr_* status as an SDK error.
 CortexError from_csdr(int rc, const std::string& what) {
     int code = CORTEX_ERROR_UNKNOWN;
@@ -98,6 +116,10 @@ struct CortexInferenceEngine {
     int lazy_mode = 0;              // token choice by the CLI's lazy HSDR scoring (0 = off)
     csdr_lazy_hsdr* lazy = nullptr;
     int lazy_loaded_mode = 0;
+    // aggressive memory: the decoder's blocks are host-resident segments streamed to the
+    // device when they run (owned here, released with the decoder)
+    std::vector<csdr_hsdb*> host_segs;
+    bool dec_streamed = false;
 };
 
 namespace {
@@ -269,6 +291,34 @@ struct Block {
     }
 };
 
+void free_decoder(CortexInferenceEngine* e) {
+    if (e->dec) csdr_decoder_free(e->dec);
+    e->dec = nullptr;
+    e->dec_ctx = 0;
+    for (csdr_hsdb* s : e->host_segs) csdr_hsdb_free(s);
+    e->host_segs.clear();
+}
+
+// A strategy-5 segment loaded with its codes in pinned host memory (not cached on the
+// device): the unit of the on-demand layer loading (loadLayerByNameAsync,
+// SparseInferenceEngine.cpp:1101-1224).
+CortexError load_host(CortexInferenceEngine* e, const std::string& name, csdr_hsdb** out) {
+    size_t idx;
+    if (!resolve(e, name, &idx)) return fail(CORTEX_ERROR_INFERENCE, "Segment not found: " + name);
+    csdr_segment_info info;
+    csdr_archive_info(e->ar, idx, &info);
+    if (info.strategy_id != 5)
+        return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
+                    "decoder: '" + name + "' must be an HSDR/HSDB (strategy 5) segment");
+    std::vector<uint8_t> bytes((size_t)info.compressed_size);
+    int rc = csdr_archive_read(e->ar, idx, bytes.data(), bytes.size(), nullptr);
+    if (rc) return from_csdr(rc, "load '" + name + "'");
+    rc = csdr_hsdb_load_host(bytes.data(), bytes.size(), e->st, out);
+    if (rc) return from_csdr(rc, "decoder: segment '" + name + "'");
+    e->host_segs.push_back(*out);
+    return ok();
+}
+
 CortexError build_decoder(CortexInferenceEngine* e, int ctx) {
     std::string emb, out_norm, out_proj;
     std::map<size_t, Block> blocks;
@@ -365,24 +415,38 @@ CortexError build_decoder(CortexInferenceEngine* e, int ctx) {
     cfg.rms_eps = 1e-5f;          // rms_norm default (cortex_sdk.cpp:1212)
     if (q0->R != H)
         return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT, "decoder: attn_q must be hidden x hidden");
-    if (e->dec) csdr_decoder_free(e->dec);
-    e->dec = nullptr;
+    free_decoder(e);
     int rc = csdr_decoder_create(&cfg, &e->dec);
     if (rc) return from_csdr(rc, "decoder");
+    // aggressive memory management: blocks are not kept on the device; each is streamed
+    // from pinned host memory when it runs (runLayersOnDemand, SparseInferenceEngine.cpp:
+    // 2911-3027), the next block's copy overlapping the current one when prefetch is on
+    const bool streamed = e->aggressive;
     for (size_t l = 0; l < layers.size(); ++l) {
         const Block& b = layers[l];
-        Cached* w[7];
+        csdr_hsdb* w[7];
         const std::string* names[7] = {&b.q, &b.k, &b.v, &b.o, &b.gate, &b.up, &b.down};
-        for (int i = 0; i < 7; ++i)
-            if ((r = seg_of(*names[i], &w[i])).code) return r;
+        for (int i = 0; i < 7; ++i) {
+            if (streamed) {
+                if ((r = load_host(e, *names[i], &w[i])).code) return r;
+            } else {
+                Cached* c = nullptr;
+                if ((r = seg_of(*names[i], &c)).code) return r;
+                w[i] = c->seg;
+            }
+        }
         std::vector<float> an, fn;
         if ((r = read_vector(e, b.attn_norm, H, an)).code || (r = read_vector(e, b.ffn_norm, H, fn)).code)
             return r;
-        rc = csdr_decoder_set_layer(e->dec, (int)l, w[0]->seg, w[1]->seg, w[2]->seg, w[3]->seg,
-                                    w[4]->seg, w[5]->seg, w[6]->seg, an.data(), fn.data(),
-                                    nullptr, nullptr, nullptr);
+        rc = csdr_decoder_set_layer(e->dec, (int)l, w[0], w[1], w[2], w[3], w[4], w[5], w[6],
+                                    an.data(), fn.data(), nullptr, nullptr, nullptr);
         if (rc) return from_csdr(rc, "decoder block " + std::to_string(l));
     }
+    rc = csdr_decoder_set_layer_prefetch(e->dec, e->prefetch ? 1 : 0);
+    if (rc) return from_csdr(rc, "decoder prefetch");
+    e->dec_streamed = streamed;
+    if (streamed)  // block 0's device copies only served the shape discovery above
+        for (Cached* c : {q0, k0, v0, g0}) c->pinned = false;
     std::vector<float> onw;
     if (!out_norm.empty() && (r = read_vector(e, out_norm, H, onw)).code) return r;
     rc = csdr_decoder_set_output(e->dec, lmc->seg, onw.empty() ? nullptr : onw.data(),
@@ -431,6 +495,7 @@ extern "C" {
 
 CSDR_API CortexError cortex_inference_engine_create(const char* path,
                                                     CortexInferenceEngineHandle* handle) {
+    CORTEX_GUARD_BEGIN
     if (!path || !handle)
         return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid arguments (null pointers)");
     *handle = nullptr;
@@ -453,15 +518,17 @@ CSDR_API CortexError cortex_inference_engine_create(const char* path,
     }
     *handle = e;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_create")
 }
 
 CSDR_API CortexError cortex_inference_engine_free(CortexInferenceEngineHandle e) {
+    CORTEX_GUARD_BEGIN
     {
         std::lock_guard<std::mutex> g(g_mu);
         if (!e || !g_live.erase(e)) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid handle");
     }
     (void)hipStreamSynchronize(e->st);
-    if (e->dec) csdr_decoder_free(e->dec);
+    free_decoder(e);
     if (e->lazy) csdr_lazy_hsdr_free(e->lazy);
     for (auto& kv : e->cache) release(kv.second);
     if (e->ws) (void)hipFree(e->ws);
@@ -471,6 +538,7 @@ CSDR_API CortexError cortex_inference_engine_free(CortexInferenceEngineHandle e)
     csdr_archive_close(e->ar);
     delete e;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_free")
 }
 
 #define CHECK_HANDLE(e) \
@@ -478,62 +546,84 @@ CSDR_API CortexError cortex_inference_engine_free(CortexInferenceEngineHandle e)
 
 CSDR_API CortexError cortex_inference_engine_set_batch_size(CortexInferenceEngineHandle e,
                                                             size_t batch_size) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (batch_size == 0) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "batch size must be > 0");
     e->batch = batch_size;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_set_batch_size")
 }
 
 CSDR_API CortexError cortex_inference_engine_enable_dropout(CortexInferenceEngineHandle e,
                                                             int enable) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     e->dropout = enable != 0;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_enable_dropout")
 }
 
 CSDR_API CortexError cortex_inference_engine_set_mode(CortexInferenceEngineHandle e,
                                                       int training_mode) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     e->training = training_mode != 0;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_set_mode")
 }
 
 CSDR_API CortexError cortex_inference_engine_init_memory_pool(CortexInferenceEngineHandle e,
                                                               size_t max_memory_mb) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     e->budget = max_memory_mb * 1024 * 1024;
     make_room(e, 0);
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_init_memory_pool")
 }
 
 CSDR_API CortexError cortex_inference_engine_enable_aggressive_memory(
     CortexInferenceEngineHandle e, int enable) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     e->aggressive = enable != 0;
+    // the decoder's blocks change residency: rebuilt at the next generate_text
+    if (e->dec && e->dec_streamed != e->aggressive) free_decoder(e);
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_enable_aggressive_memory")
 }
 
 CSDR_API CortexError cortex_inference_engine_get_memory_usage(CortexInferenceEngineHandle e,
                                                               size_t* bytes) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (!bytes) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "null output");
     *bytes = e->cache_bytes;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_get_memory_usage")
 }
 
 CSDR_API CortexError cortex_inference_engine_enable_layer_prefetch(CortexInferenceEngineHandle e,
                                                                    int enable) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     e->prefetch = enable != 0;
+    if (e->dec) {
+        const int rc = csdr_decoder_set_layer_prefetch(e->dec, e->prefetch ? 1 : 0);
+        if (rc) return from_csdr(rc, "layer prefetch");
+    }
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_enable_layer_prefetch")
 }
 
 CSDR_API CortexError cortex_inference_engine_get_last_run_stats_json(CortexInferenceEngineHandle e,
                                                                      char** out_json) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (!out_json) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "null output");
     *out_json = dup_c(e->stats);
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_get_last_run_stats_json")
 }
 
 CSDR_API void cortex_free_string(char* s) { std::free(s); }
@@ -546,11 +636,13 @@ CSDR_API const char* cortex_sdk_version(void) { return "1.0.0-mi355x"; }
 
 CSDR_API CortexError cortex_inference_engine_run(CortexInferenceEngineHandle e, const float*, size_t,
                                                  float*, size_t, size_t* actual_output_size) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (actual_output_size) *actual_output_size = 0;
     return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
                 "run: whole-graph execution is outside the coded-weight device path; use "
                 "cortex_inference_engine_run_layer or cortex_inference_engine_generate_text");
+    CORTEX_GUARD_END("cortex_inference_engine_run")
 }
 
 CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHandle e,
@@ -558,6 +650,7 @@ CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHand
                                                        const float* input, size_t input_size,
                                                        float* output, size_t output_size,
                                                        size_t* actual_output_size) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (!layer_name || !input || !output || !actual_output_size)
         return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid arguments (null pointers)");
@@ -657,12 +750,14 @@ CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHand
     e->stats = buf;
     if (e->aggressive) evict(e, idx);
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_run_layer")
 }
 
 CSDR_API CortexError cortex_inference_engine_matmul_device(CortexInferenceEngineHandle e,
                                                            const char* layer_name, const void* x,
                                                            int x_dtype, int M, float* y,
                                                            void* hip_stream) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (!layer_name || !x || !y || M <= 0)
         return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid arguments");
@@ -686,20 +781,24 @@ CSDR_API CortexError cortex_inference_engine_matmul_device(CortexInferenceEngine
     rc = csdr_hsdb_matmul(c->seg, x, x_dtype, M, y, e->ws, e->ws_bytes, hip_stream);
     if (rc) return from_csdr(rc, std::string("matmulHSDR '") + layer_name + "'");
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_matmul_device")
 }
 
 CSDR_API CortexError cortex_inference_engine_set_lazy_hsdr_selection(CortexInferenceEngineHandle e,
                                                                      int mode) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (mode < 0 || mode > 2)
         return fail(CORTEX_ERROR_INVALID_ARGUMENT, "lazy HSDR selection mode must be 0, 1 or 2");
     e->lazy_mode = mode;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_set_lazy_hsdr_selection")
 }
 
 CSDR_API CortexError cortex_inference_engine_generate_text(CortexInferenceEngineHandle e,
                                                            const char* prompt, int max_new_tokens,
                                                            char** out_text) {
+    CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
     if (!prompt || !out_text) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid argument(s)");
     *out_text = nullptr;
@@ -762,6 +861,7 @@ CSDR_API CortexError cortex_inference_engine_generate_text(CortexInferenceEngine
                   steps > 1 ? (steps - 1) / (dec_ms * 1e-3) : 0.0, e->cache_bytes);
     e->stats = buf;
     return ok();
+    CORTEX_GUARD_END("cortex_inference_engine_generate_text")
 }
 
 }  // extern "C"

@@ -1644,9 +1644,14 @@ void release_dict(csdr_hsdb* s) {
     s->d_dict16p = nullptr;
 }
 
+const char* const kHostCodesMsg =
+    "hsdb: the segment's codes are host-resident (csdr_hsdb_load_host); a decoder streams "
+    "them per layer, or load the segment with csdr_hsdb_load";
+
 // Stream parse with the reference's checks (HierarchicalSDRStrategy.cpp:1265-1290 and
 // readBuffer's truncation check) plus index < n_atoms.
-int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s) {
+int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s,
+                     bool host_codes = false) {
     if (!buf) return set_error(CSDR_E_INVALID, "hsdb_load: null stream");
     if (n < 36) return set_error(CSDR_E_TRUNCATED, "hsdb_load: stream shorter than header");
     if (std::memcmp(buf, "HSDR", 4) == 0) {
@@ -1743,11 +1748,19 @@ int parse_and_upload(const uint8_t* buf, size_t n, hipStream_t st, csdr_hsdb* s)
         const int rc = acquire_dict(s, buf + off_dict, b_dict, st);
         if (rc) return rc;
     }
-    CSDR_HIP_CHECK(hipMalloc(&s->d_codes, std::max<size_t>(b_codes, 4)));
+    if (host_codes) {
+        // pinned, so a decoder's staging copies run as DMA (and can be graph nodes)
+        CSDR_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&s->h_codes),
+                                     std::max<size_t>(b_codes, 4), hipHostMallocDefault));
+        if (b_codes) std::memcpy(s->h_codes, words.data(), b_codes);
+    } else {
+        CSDR_HIP_CHECK(hipMalloc(&s->d_codes, std::max<size_t>(b_codes, 4)));
+        s->device_bytes += b_codes;
+    }
     CSDR_HIP_CHECK(hipMalloc(&s->d_slot_gamma, b_gamma));
     CSDR_HIP_CHECK(hipMalloc(&s->d_edge, std::max<size_t>(b_edge, 4)));
-    s->device_bytes += b_codes + b_gamma + b_edge;
-    if (b_codes)
+    s->device_bytes += b_gamma + b_edge;
+    if (b_codes && s->d_codes)
         CSDR_HIP_CHECK(
             hipMemcpyAsync(s->d_codes, words.data(), b_codes, hipMemcpyHostToDevice, st));
     CSDR_HIP_CHECK(
@@ -1763,6 +1776,7 @@ void release(csdr_hsdb* s) {
     if (!s) return;
     release_dict(s);
     if (s->d_codes) (void)hipFree(s->d_codes);
+    if (s->h_codes) (void)hipHostFree(s->h_codes);
     if (s->d_slot_gamma) (void)hipFree(s->d_slot_gamma);
     if (s->d_edge) (void)hipFree(s->d_edge);
     delete s;
@@ -1955,9 +1969,12 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
                                              std::to_string(kMaxGroup) + ")");
     if (x_dtype != CSDR_F32 && x_dtype != CSDR_F16)
         return set_error(CSDR_E_INVALID, "hsdb_matmul: x_dtype must be CSDR_F32 or CSDR_F16");
-    for (int i = 0; i < n; ++i)
+    for (int i = 0; i < n; ++i) {
         if (!segs[i] || !xs[i] || !ys[i])
             return set_error(CSDR_E_INVALID, "hsdb_matmul: null entry");
+        if (!csdr::codes_on_device(segs[i]))
+            return set_error(CSDR_E_UNSUPPORTED, kHostCodesMsg);
+    }
     if (xa.xop != CSDR_XOP_NONE) {
         if (x_dtype != CSDR_F32 || M > kMaxXopM)
             return set_error(CSDR_E_INVALID, "hsdb_matmul: x ops take fp32 x and M <= " +
@@ -2270,6 +2287,31 @@ CSDR_API int csdr_hsdb_load(const void* stream, size_t nbytes, void* hip_stream,
     return CSDR_OK;
 }
 
+CSDR_API int csdr_hsdb_load_host(const void* stream, size_t nbytes, void* hip_stream,
+                                 csdr_hsdb** out) {
+    if (!out) return set_error(CSDR_E_INVALID, "hsdb_load_host: null out");
+    *out = nullptr;
+    csdr_hsdb* s = new (std::nothrow) csdr_hsdb();
+    if (!s) return set_error(CSDR_E_INVALID, "hsdb_load_host: out of host memory");
+    if (hipGetDevice(&s->device) != hipSuccess) {
+        delete s;
+        return set_error(CSDR_E_HIP, "hsdb_load_host: no HIP device");
+    }
+    int rc;
+    try {
+        rc = parse_and_upload(static_cast<const uint8_t*>(stream), nbytes,
+                              static_cast<hipStream_t>(hip_stream), s, true);
+    } catch (const std::bad_alloc&) {
+        rc = set_error(CSDR_E_INVALID, "hsdb_load_host: out of host memory");
+    }
+    if (rc != CSDR_OK) {
+        release(s);
+        return rc;
+    }
+    *out = s;
+    return CSDR_OK;
+}
+
 CSDR_API int csdr_hsdb_free(csdr_hsdb* seg) {
     release(seg);
     return CSDR_OK;
@@ -2376,6 +2418,7 @@ CSDR_API int csdr_hsdb_matmul_group_xop(int n, const csdr_hsdb* const* segs,
 CSDR_API int csdr_hsdb_decode_row(const csdr_hsdb* s, const int* row_dev, int row_host, float* out,
                                   void* hip_stream) {
     if (!s || !out) return set_error(CSDR_E_INVALID, "hsdb_decode_row: bad argument");
+    if (!csdr::codes_on_device(s)) return set_error(CSDR_E_UNSUPPORTED, kHostCodesMsg);
     if (s->tile_rows != 1)
         return set_error(CSDR_E_FORMAT, "hsdb_decode_row: needs 1-row tiles");
     if (!row_dev && (row_host < 0 || (uint32_t)row_host >= s->R))
@@ -2390,6 +2433,7 @@ CSDR_API int csdr_hsdb_decode_rows(const csdr_hsdb* s, const int* rows_dev, int 
                                    void* hip_stream) {
     if (!s || !rows_dev || !out || n <= 0 || n > 65535)
         return set_error(CSDR_E_INVALID, "hsdb_decode_rows: bad argument");
+    if (!csdr::codes_on_device(s)) return set_error(CSDR_E_UNSUPPORTED, kHostCodesMsg);
     if (s->tile_rows != 1)
         return set_error(CSDR_E_FORMAT, "hsdb_decode_rows: needs 1-row tiles");
     decode_row_kernel<<<dim3(grid_for(s->C), n), kThreads, 0,
@@ -2414,6 +2458,7 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
 
 CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* s, float* w, void* hip_stream) {
     if (!s || !w) return set_error(CSDR_E_INVALID, "hsdb_decompress: bad argument");
+    if (!csdr::codes_on_device(s)) return set_error(CSDR_E_UNSUPPORTED, kHostCodesMsg);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     const size_t work = (size_t)s->n_tiles * s->tile_rows * s->tile_cols;
     if (work) {
@@ -2430,6 +2475,7 @@ CSDR_API int csdr_hsdb_decompress(const csdr_hsdb* s, float* w, void* hip_stream
 CSDR_API int csdr_hsdb_export_codes(const csdr_hsdb* s, uint16_t* packed, uint16_t* coef_abs,
                                     void* hip_stream) {
     if (!s || !packed) return set_error(CSDR_E_INVALID, "hsdb_export_codes: bad argument");
+    if (!csdr::codes_on_device(s)) return set_error(CSDR_E_UNSUPPORTED, kHostCodesMsg);
     const size_t work = (size_t)s->n_tiles * s->slots;
     if (work) {
         export_codes_kernel<<<grid_for(work), kThreads, 0, static_cast<hipStream_t>(hip_stream)>>>(

@@ -17,7 +17,9 @@ struct csdr_hsdb {
     int device = 0;
     float* d_dict = nullptr;        // K x tile_dim fp32 (shared, see dict_ref)
     _Float16* d_dict16p = nullptr;  // 64-wide blocks: K x 64 fp16, rows in kperm64 order
-    uint32_t* d_codes = nullptr;    // n_tiles * slots words
+    uint32_t* d_codes = nullptr;    // n_tiles * slots words (null for host-resident codes)
+    uint32_t* h_codes = nullptr;    // host-resident segments: the same words in pinned host
+                                    // memory (a decoder streams them to the device per layer)
     float* d_slot_gamma = nullptr;  // slots floats: gamma[j / k]
     float* d_edge = nullptr;        // top-right strip (R_full x Ce) then bottom strip
     float h_slot_gamma[32] = {};    // host copy of the first 32 slot gammas (kernel args)
@@ -29,6 +31,13 @@ struct csdr_hsdb {
 };
 
 namespace csdr {
+
+// Bytes of the segment's device code words (4 per slot).
+inline size_t code_bytes(const csdr_hsdb* s) { return (size_t)s->n_tiles * s->slots * 4; }
+
+// The kernels read code words from device memory: false for a host-resident segment (whose
+// words are in pinned host memory until a caller stages them).
+inline bool codes_on_device(const csdr_hsdb* s) { return s->d_codes || code_bytes(s) == 0; }
 
 // ---- chunk-major code layout of 1-row tiles
 // Block columns are grouped in chunks: full chunks of NBc (a power of two) columns, then the

@@ -42,6 +42,22 @@ CortexError fail(int code, const std::string& m) {
     t_msg = m;
     return {t_msg.c_str(), code};
 }
+
+// No C++ exception crosses the C ABI: every CortexError entry point runs its body inside
+// CORTEX_GUARD_BEGIN ... CORTEX_GUARD_END(name), which turns std::bad_alloc into
+// CORTEX_ERROR_MEMORY and any other exception into CORTEX_ERROR_UNKNOWN with its message.
+#define CORTEX_GUARD_BEGIN try {
+#define CORTEX_GUARD_END(fn_)                                                            \
+    }                                                                                    \
+    catch (const std::bad_alloc&) {                                                      \
+        return fail(CORTEX_ERROR_MEMORY, std::string(fn_) + ": out of host memory");    \
+    }                                                                                    \
+    catch (const std::exception& ex_) {                                                  \
+        return fail(CORTEX_ERROR_UNKNOWN, std::string(fn_) + ": " + ex_.what());        \
+    }                                                                                    \
+    catch (...) {                                                                        \
+        return fail(CORTEX_ERROR_UNKNOWN, std::string(fn_) + ": unknown exception");    \
+    }
 CortexError unsupported(const char* what) {
     return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
                 std::string(what) +
@@ -93,6 +109,7 @@ std::vector<std::string> model_parts(const std::string& model_path) {
 extern "C" {
 
 CSDR_API CortexError cortex_compression_options_init(CortexCompressionOptions* options) {
+    CORTEX_GUARD_BEGIN
     if (!options) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid options pointer");
     options->num_threads = 1;
     options->verbose = 0;
@@ -105,6 +122,7 @@ CSDR_API CortexError cortex_compression_options_init(CortexCompressionOptions* o
     options->use_hsdr = 0;
     options->sparsity = 0.02f;
     return ok();
+    CORTEX_GUARD_END("cortex_compression_options_init")
 }
 
 CSDR_API const char* cortex_error_string(int code) {
@@ -137,6 +155,7 @@ CSDR_API int cortex_model_get_parts(const char* model_path, char*** parts_out, i
 CSDR_API CortexError cortex_archive_get_tokenizer_info(const char* archive_path,
                                                        int* out_has_tokenizer,
                                                        char** out_tokenizer_type) {
+    CORTEX_GUARD_BEGIN
     if (!archive_path || !out_has_tokenizer)
         return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid argument(s)");
     *out_has_tokenizer = 0;
@@ -182,86 +201,107 @@ CSDR_API CortexError cortex_archive_get_tokenizer_info(const char* archive_path,
         if (out_tokenizer_type) *out_tokenizer_type = dup_c(spm ? "sentencepiece" : "gpt2-bpe");
     }
     return ok();
+    CORTEX_GUARD_END("cortex_archive_get_tokenizer_info")
 }
 
 CSDR_API CortexError cortex_compressor_create(const char* model_path, const char* format,
                                               const CortexCompressionOptions* options,
                                               CortexCompressorHandle* handle) {
+    CORTEX_GUARD_BEGIN
     (void)model_path;
     (void)format;
     (void)options;
     if (handle) *handle = nullptr;
     return unsupported("cortex_compressor_create");
+    CORTEX_GUARD_END("cortex_compressor_create")
 }
 
 CSDR_API CortexError cortex_compressor_add_file(CortexCompressorHandle handle,
                                                 const char* model_path) {
+    CORTEX_GUARD_BEGIN
     (void)handle;
     (void)model_path;
     return unsupported("cortex_compressor_add_file");
+    CORTEX_GUARD_END("cortex_compressor_add_file")
 }
 
 CSDR_API CortexError cortex_compressor_compress(CortexCompressorHandle handle,
                                                 const char* output_path) {
+    CORTEX_GUARD_BEGIN
     (void)handle;
     (void)output_path;
     return unsupported("cortex_compressor_compress");
+    CORTEX_GUARD_END("cortex_compressor_compress")
 }
 
 CSDR_API CortexError cortex_compressor_get_stats(CortexCompressorHandle handle,
                                                  size_t* original_size, size_t* compressed_size,
                                                  double* compression_ratio,
                                                  double* compression_time_ms) {
+    CORTEX_GUARD_BEGIN
     (void)handle;
     (void)original_size;
     (void)compressed_size;
     (void)compression_ratio;
     (void)compression_time_ms;
     return unsupported("cortex_compressor_get_stats");
+    CORTEX_GUARD_END("cortex_compressor_get_stats")
 }
 
 CSDR_API CortexError cortex_compressor_free(CortexCompressorHandle handle) {
+    CORTEX_GUARD_BEGIN
     if (handle) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid compressor handle");
     return ok();
+    CORTEX_GUARD_END("cortex_compressor_free")
 }
 
 CSDR_API CortexError cortex_decompressor_create(const char* compressed_path,
                                                 CortexDecompressorHandle* handle, float sparsity) {
+    CORTEX_GUARD_BEGIN
     (void)compressed_path;
     (void)sparsity;
     if (handle) *handle = nullptr;
     return unsupported("cortex_decompressor_create");
+    CORTEX_GUARD_END("cortex_decompressor_create")
 }
 
 CSDR_API CortexError cortex_decompressor_decompress(CortexDecompressorHandle handle,
                                                     const char* compressed_path,
                                                     const char* output_path) {
+    CORTEX_GUARD_BEGIN
     (void)handle;
     (void)compressed_path;
     (void)output_path;
     return unsupported("cortex_decompressor_decompress");
+    CORTEX_GUARD_END("cortex_decompressor_decompress")
 }
 
 CSDR_API CortexError cortex_decompressor_free(CortexDecompressorHandle handle) {
+    CORTEX_GUARD_BEGIN
     if (handle) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid decompressor handle");
     return ok();
+    CORTEX_GUARD_END("cortex_decompressor_free")
 }
 
 CSDR_API CortexError cortex_archive_extract(const char* compressed_path, const char* output_dir,
                                             float sparsity) {
+    CORTEX_GUARD_BEGIN
     (void)compressed_path;
     (void)output_dir;
     (void)sparsity;
     return unsupported("cortex_archive_extract");
+    CORTEX_GUARD_END("cortex_archive_extract")
 }
 
 CSDR_API CortexError cortex_compress_from_url(const char* url_or_path, const char* format,
                                               const char* output_path, float sparsity) {
+    CORTEX_GUARD_BEGIN
     (void)url_or_path;
     (void)format;
     (void)output_path;
     (void)sparsity;
     return unsupported("cortex_compress_from_url");
+    CORTEX_GUARD_END("cortex_compress_from_url")
 }
 
 }  // extern "C"

@@ -115,7 +115,11 @@ class Decoder:
     """A device decoder over resident HSDB segments (greedy / penalised argmax) decoding
     `batch` sequences in lockstep; per-sequence arrays are sequence-major (batch, ...)."""
 
-    def __init__(self, weights: DecoderWeights, batch: int = 1, prefill_chunk: int | None = None):
+    def __init__(self, weights: DecoderWeights, batch: int = 1, prefill_chunk: int | None = None,
+                 stream_layers: bool = False, prefetch: bool = True):
+        """stream_layers: the blocks' code words stay in pinned host memory and each block is
+        copied to the device when it runs (csdr_decoder_set_layer_prefetch: with prefetch,
+        the next block's copy overlaps the current block's kernels)."""
         import torch
 
         if not torch.cuda.is_available():
@@ -135,7 +139,7 @@ class Decoder:
         self._keep = []
         try:
             for l, L in enumerate(weights.layers):
-                segs = [HsdbSegment(L[name]) for name in LINEARS]
+                segs = [HsdbSegment(L[name], host_codes=stream_layers) for name in LINEARS]
                 self._segs += segs
                 vecs = [np.ascontiguousarray(L[nm], np.float32) if L.get(nm) is not None
                         else None for nm in ("attn_norm", "ffn_norm", "bq", "bk", "bv")]
@@ -151,6 +155,8 @@ class Decoder:
                 self._h, self._lm._h, _fptr(fn), self._emb._h if self._emb else None))
             if prefill_chunk is not None:
                 self.set_prefill_chunk(prefill_chunk)
+            if not prefetch:
+                self.set_layer_prefetch(False)
         except Exception:
             self.close()
             raise
@@ -179,6 +185,13 @@ class Decoder:
         self._lazy = emb
         _lib.check(self._lib.csdr_decoder_set_lazy_selection(self._h, emb._h if emb else None,
                                                              penalty))
+
+    def set_layer_prefetch(self, enable: bool) -> None:
+        _lib.check(self._lib.csdr_decoder_set_layer_prefetch(self._h, int(bool(enable))))
+
+    def streamed_bytes(self) -> int:
+        """Code bytes the streamed blocks copy to the device per step."""
+        return int(self._lib.csdr_decoder_streamed_bytes(self._h))
 
     def set_prefill_chunk(self, tokens: int) -> None:
         """Prompt tokens per sequence in one multi-token prefill pass (0: one decode step

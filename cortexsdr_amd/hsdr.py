@@ -50,15 +50,19 @@ def _stream_ptr(stream=None) -> int:
 
 
 class HsdbSegment:
-    """A device-resident HSDR (binary) or HSDB (block-coded) weight segment."""
+    """A device-resident HSDR (binary) or HSDB (block-coded) weight segment; with
+    host_codes=True the code words stay in pinned host memory (csdr_hsdb_load_host: a
+    decoder block of such segments is streamed to the device when it runs)."""
 
-    def __init__(self, stream: bytes, hip_stream=None):
+    def __init__(self, stream: bytes, hip_stream=None, host_codes: bool = False):
         lib = _lib.load()
         _torch()
         self._buf = C.create_string_buffer(bytes(stream), len(stream))
         h = C.c_void_p()
-        _check(lib.csdr_hsdb_load(C.cast(self._buf, C.c_void_p), len(stream),
-                                  _stream_ptr(hip_stream), C.byref(h)))
+        loader = lib.csdr_hsdb_load_host if host_codes else lib.csdr_hsdb_load
+        self.host_codes = bool(host_codes)
+        _check(loader(C.cast(self._buf, C.c_void_p), len(stream), _stream_ptr(hip_stream),
+                      C.byref(h)))
         self._h = h
         self._buf = None
         info = _lib.HsdbInfo()

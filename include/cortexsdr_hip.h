@@ -102,6 +102,15 @@ typedef struct csdr_hsdb_info {
  * < n_atoms (the reference would read outside D). */
 CSDR_API int csdr_hsdb_load(const void* stream, size_t nbytes, void* hip_stream,
                             csdr_hsdb** out);
+/* csdr_hsdb_load with the code words kept in pinned host memory instead of device memory
+ * (the dictionary, stage gammas and edge strips are uploaded): the unit of the on-demand
+ * layer loading of SDRInferenceEngine::runLayersOnDemand / loadLayerByNameAsync
+ * (SparseInferenceEngine.cpp:2911-3027, 1101-1224), whose layers are read when they run.
+ * A decoder streams such a layer's codes to the device when the layer runs
+ * (csdr_decoder_set_layer_prefetch); products, decodes and exports on the segment itself
+ * return CSDR_E_UNSUPPORTED. device_bytes in csdr_hsdb_get_info excludes the host codes. */
+CSDR_API int csdr_hsdb_load_host(const void* stream, size_t nbytes, void* hip_stream,
+                                 csdr_hsdb** out);
 CSDR_API int csdr_hsdb_free(csdr_hsdb* seg);
 CSDR_API int csdr_hsdb_get_info(const csdr_hsdb* seg, csdr_hsdb_info* info);
 
@@ -639,6 +648,19 @@ CSDR_API int csdr_decoder_set_layer(csdr_decoder* dec, int layer, const csdr_hsd
                                     const csdr_hsdb* wdown, const float* attn_norm,
                                     const float* ffn_norm, const float* bq, const float* bk,
                                     const float* bv);
+/* On-demand layer streaming. A block whose seven segments are host-resident
+ * (csdr_hsdb_load_host) is streamed: when it runs, its code words are copied to one of two
+ * device staging buffers on a second stream and its products read them there (the other
+ * blocks stay resident; a block mixing both kinds is refused). With prefetch on (the
+ * default, as the SDK engine enables it, cortex_sdk.cpp:1770) the copy of the block after
+ * next is issued as soon as a block finishes, so the next block's copy runs under the
+ * current block's kernels (double buffering, prefetchNextLayer SparseInferenceEngine.cpp:
+ * 3461-3467); off, each copy waits for the previous block (no overlap). The copies are part
+ * of the captured step graph. The kernels and code words are the resident decoder's, so
+ * results equal its results to the products' float-atomic summation order. */
+CSDR_API int csdr_decoder_set_layer_prefetch(csdr_decoder* dec, int enable);
+/* Code bytes the streamed blocks copy per step (0 when every block is resident). */
+CSDR_API int64_t csdr_decoder_streamed_bytes(const csdr_decoder* dec);
 /* Output projection (vocab x H) and output norm (NULL = none, as when output_norm_layer_name
  * is empty, cortex_sdk.cpp:1682-1688); embedding NULL = tied (rows of lm_head). */
 CSDR_API int csdr_decoder_set_output(csdr_decoder* dec, const csdr_hsdb* lm_head,
