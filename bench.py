@@ -37,6 +37,11 @@ The JSON line carries:
   decode_7b_streaming  the same step with on-demand layer streaming: blocks in pinned host
                 memory, copied to the device per step (prefetch on at batch 1 and 8, off at
                 batch 1), ms per step and the host-to-device GB/s of the streamed codes
+  cfg1          configs[0] (the reference CPU path's configuration): W 4096x4096, K=512, 4
+                nnz, x fp32, M=1, one matrix and 8 layers per call, next to the CPU
+                restatement (OpenMP and one thread)
+  cfg3          configs[2]: Q4_K 4096x4096 / 4096x14336 at M = 1 and 32, next to the
+                reference engine's dequantize + fp32 linear restated on the CPU
   encode        the compress side: GPU matching pursuit (rows/s, TFLOP/s against the fp32
                 vector peak) and compress wall time on Qwen2-0.5B-shaped attention / MLP
                 matrices, next to the reference's own compress (oracle/_ref)
@@ -119,6 +124,8 @@ def parse():
     ap.add_argument("--decode-cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-encode", action="store_true", help="skip the HSDR encoder leg")
     ap.add_argument("--no-7b", action="store_true", help="skip the config-5 decode-step leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config-1 and config-3 legs")
     ap.add_argument("--replays", type=int, default=100,
                     help="graph replays for the median / min / max statistics")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -214,6 +221,101 @@ def cpu_decode_step(w, ctx: int, seconds: float):
     return (time.perf_counter() - t0) / n, n
 
 
+def _threads():
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+
+
+def _cpu_time(fn, seconds, min_runs=2):
+    """Seconds per call of fn after one warm-up call: at least min_runs calls and `seconds`."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= seconds and n >= min_runs:
+            break
+    return (time.perf_counter() - t0) / n, n
+
+
+def cfg1_leg(torch, args):
+    """configs[0], the configuration the reference CPU path runs: W 4096x4096 (64-blocks,
+    K=512 unit-norm fp32 atoms, 4 nnz, fp16 coefficients), x fp32, M=1. GPU: one matrix per
+    call, and 8 independent layers per grouped call (bench_cli); CPU: the restated fused
+    product (oracle orc_hsdb_matmul) on the same matrix and x, OpenMP and one thread."""
+    from cortexsdr_amd import bench_cli, synth
+
+    one = bench_cli.bench_hsdb(torch, 4096, 4096, 512, 4, 1, np.float32, 50)
+    eight = bench_cli.bench_hsdb_layers(torch, 4096, 4096, 512, 4, 8, np.float32, 50)
+    alg = 4096 * 64 * 4 * 4 + 512 * 64 * 4 + 4096 * 4 + 4096 * 4
+    out = {"workload": "cfg1: W 4096x4096, K=512, 4 nnz/block, x fp32, M=1",
+           "algorithmic_bytes": alg,
+           "us_per_call": one["us"], "GBps": one["GBps"], "hbm_frac": one["hbm_frac"],
+           "eight_layers_per_call": {"us_per_layer": eight["us_per_layer"],
+                                     "GBps": eight["GBps"], "hbm_frac": eight["hbm_frac"]},
+           "cpu_baseline": None}
+    if not args.no_cpu:
+        import oracle
+
+        stream = synth.hsdb_layer(4096, 4096, 512, 4, seed_dict=1, seed_codes=2)
+        x = synth.activations(4096, 1, seed=3)
+        th = _threads()
+        prev = oracle.set_threads(th)
+        try:
+            dt, n = _cpu_time(lambda: oracle.hsdb_matmul(stream, x), args.cpu_seconds / 2)
+            oracle.set_threads(1)
+            dt1, n1 = _cpu_time(lambda: oracle.hsdb_matmul(stream, x), args.cpu_seconds / 4)
+        finally:
+            oracle.set_threads(prev)
+        out["cpu_baseline"] = {
+            "value": round(alg / dt / 1e9, 3), "unit": "GB/s", "cores": th, "kind": "port",
+            "sample": f"{n} products of the same matrix and x through oracle/csdr_oracle.c "
+                      f"orc_hsdb_matmul, {th} OpenMP threads, {dt * 1e3:.2f} ms each",
+            "single_thread": {"value": round(alg / dt1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                              "sample": f"{n1} products on one thread, {dt1 * 1e3:.2f} ms each"}}
+    return out
+
+
+def cfg3_leg(torch, args):
+    """Q4_K dequant-matmul, W 4096x4096 and 4096x14336, x fp16, M = 1 and 32
+    (bench_cli.bench_q4k: ggml element order, HIP graph replays); CPU: the reference engine's
+    path restated (oracle orc_q4k_linear: dequantize each row to fp32 as
+    decodeSupportedGGUFQuantized does, then the fp32 row dot products of linear_forward),
+    OpenMP, on the same matrix and x."""
+    from cortexsdr_amd import bench_cli, synth
+
+    rows = []
+    for (R, Cc) in ((4096, 4096), (4096, 14336)):
+        for M in (1, 32):
+            r = bench_cli.bench_q4k(torch, R, Cc, M, 50)
+            rows.append({k: r[k] for k in ("R", "C", "M", "us", "GBps", "hbm_frac",
+                                           "dense_equiv_TFLOPs")})
+    out = {"workload": "cfg3: Q4_K 4096x4096 / 4096x14336, x fp16, M=1/32", "gpu": rows,
+           "cpu_baseline": None}
+    if not args.no_cpu:
+        import oracle
+
+        th = _threads()
+        prev = oracle.set_threads(th)
+        cpu = []
+        try:
+            R, Cc = 4096, 14336
+            blob = synth.q4k_matrix(R, Cc, seed=7)
+            for M in (1, 32):
+                x = synth.activations(Cc, M, seed=11).T.copy().astype(np.float16).astype(np.float32)
+                dt, n = _cpu_time(lambda: oracle.q4k_linear(blob, R, Cc, x), args.cpu_seconds / 4)
+                alg = len(blob) + Cc * M * 2 + R * M * 4
+                cpu.append({"R": R, "C": Cc, "M": M, "us": round(dt * 1e6, 1),
+                            "GBps": round(alg / dt / 1e9, 3), "calls": n})
+        finally:
+            oracle.set_threads(prev)
+        out["cpu_baseline"] = {
+            "value": cpu[0]["GBps"], "unit": "GB/s", "cores": th, "kind": "port",
+            "sample": "W 4096x14336 at M=1 (and M=32 below) through oracle/csdr_oracle.c "
+                      "orc_q4k_linear (per-row dequantize + fp32 dot), "
+                      f"{th} OpenMP threads", "rows": cpu}
+    return out
+
+
 def decode_leg(args):
     """tokens/s of graph-replayed decode steps after a 512-token prefill."""
     from cortexsdr_amd import bench_cli
@@ -241,15 +343,46 @@ def decode_leg(args):
     }
     if not args.no_cpu:
         dt, n = cpu_decode_step(w, n_prompt + n_new // 2, args.decode_cpu_seconds)
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+        threads = _threads()
         out["cpu_baseline"] = {
             "value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": (f"{n} KV-cached decode steps at context {n_prompt + n_new // 2} through "
                        f"oracle/ (orc_hsdb_matmul OpenMP linears), {dt * 1e3:.0f} ms/token")}
+        out["cpu_full_recompute"] = cpu_recompute_steps(w, prompt, toks, args)
     return out
 
 
-def decode_7b_leg(torch):
+def cpu_recompute_steps(w, prompt, toks, args, steps=2):
+    """The reference's own decode loop, labelled: run_transformer_decode recomputes the whole
+    context for every generated token (api/cortex_sdk.cpp:1995-2006, 1543-1696) over weights
+    decompressed to dense fp32 at load. Restated with the oracle (every weight decoded once,
+    fp32 BLAS products, whole-context causal attention); `steps` tokens after the 512-token
+    prompt, seconds per token (not extrapolated to the 128-token run)."""
+    from oracle import decoder as odec
+
+    th = _threads()
+    t0 = time.perf_counter()
+    dense = odec.DenseWeights()
+    for L in w.layers:
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
+            dense.get(L[name])
+    dense.get(w.lm_head)
+    t_load = time.perf_counter() - t0
+    per = []
+    for i in range(steps):
+        ctx = np.concatenate([prompt, toks[:i]]).astype(np.int32)
+        t0 = time.perf_counter()
+        odec.prompt_state(w, ctx, dense)
+        per.append(time.perf_counter() - t0)
+    dt = float(np.median(per))
+    return {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": th, "kind": "port",
+            "sample": (f"{steps} tokens at context {len(prompt)}..{len(prompt) + steps - 1}, each "
+                       f"recomputing the whole context (dense fp32 weights decoded once in "
+                       f"{t_load:.1f} s, numpy BLAS products, OpenMP attention), "
+                       f"{dt:.2f} s/token")}
+
+
+def decode_7b_leg(torch, args):
     """ms per decode step of the Llama-7B-shaped model at context 4096, batch 1 and
     8 (bench_cli.bench_decoder_7b: HIP-graph steps, weights and the N(0,1) fp16 KV context
     resident); HBM fraction from codes + KV bytes per step."""
@@ -262,7 +395,34 @@ def decode_7b_leg(torch):
                                       "code_GB_per_step", "kv_GB_per_step", "alg_GBps",
                                       "hbm_frac")})
         torch.cuda.empty_cache()
+    if not args.no_cpu:
+        out[0]["cpu_baseline"] = cpu_7b_step()
     return out
+
+
+def cpu_7b_step(ctx=4096):
+    """One configs[4] decode step at batch 1 on the CPU restatement (oracle.decoder
+    .step_cached: orc_hsdb_matmul OpenMP linears over the same 32 coded layers, RoPE, cached
+    attention over a 4096-position fp16 context of N(0,1) values, SwiGLU, lm_head)."""
+    from cortexsdr_amd import bench_cli
+    from oracle import decoder as odec
+
+    w = bench_cli.cfg5_weights(ctx + 8)
+    s = w.spec
+    rng = np.random.default_rng(5)
+    kv = []
+    for _ in range(s.n_layers):
+        k = rng.standard_normal((1, ctx + 1, s.n_kv_heads, s.head_dim), np.float32)
+        v = rng.standard_normal((1, ctx + 1, s.n_kv_heads, s.head_dim), np.float32)
+        kv.append((k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)))
+    t0 = time.perf_counter()
+    odec.step_cached(w, [1], kv, ctx)
+    dt = time.perf_counter() - t0
+    th = _threads()
+    return {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": th, "kind": "port",
+            "ms_per_step": round(dt * 1e3, 1),
+            "sample": (f"one batch-1 step at context {ctx} through "
+                       f"oracle.decoder.step_cached, {th} OpenMP threads")}
 
 
 def decode_7b_streaming_leg(torch):
@@ -531,10 +691,13 @@ def main():
                 "sample": f"{n1} steps on one thread, {dt1 * 1e3:.1f} ms/step (the reference's "
                           "fused HSDR path is single-threaded)"},
         }
+    if not args.no_configs:
+        out["cfg1"] = cfg1_leg(torch, args)
+        out["cfg3"] = cfg3_leg(torch, args)
     if not args.no_decode:
         out["decode"] = decode_leg(args)
     if not args.no_7b:
-        out["decode_7b"] = decode_7b_leg(torch)
+        out["decode_7b"] = decode_7b_leg(torch, args)
         out["decode_7b_streaming"] = decode_7b_streaming_leg(torch)
     if not args.no_encode:
         out["encode"] = encode_leg(args)

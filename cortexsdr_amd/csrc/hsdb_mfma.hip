@@ -6,12 +6,14 @@
 // strip is decoded into registers straight in the MFMA A-operand layout and multiplied
 // against the matching 64 x M slice of X.
 //
-// Decode: W[r][k] = sum_j c_j * D[idx_j][k] in fp32 over the row's slots, with the dictionary
-// held in LDS as fp16 (K <= 1024 atoms: 128 KiB), then rounded to fp16 for the MFMA
-// (v_mfma_f32_16x16x32_f16, fp32 accumulation; gfx950 runs it at full rate, the 16-deep
-// form at half). X is fp16 as given, or split into fp16 hi + lo parts for fp32 input (two
-// MFMAs). The two fp16 roundings (D, decoded W) keep the product within ~2e-4 relative L2
-// of the fp32 decode.
+// Decode: W[r][k] = g0 * sum_j (c_j * g_j / g0) * D[idx_j][k] over the row's slots (g0 the
+// largest stage gain), with the
+// dictionary held in LDS as fp16 (K <= 1024 atoms: 128 KiB): packed fp16 fused multiply-adds
+// (v_pk_fma_f16, two weights per lane instruction) accumulate each lane's 16 weights of a
+// row straight in the A-operand registers of the matrix-core step (v_mfma_f32_16x16x32_f16,
+// fp32 accumulation; gfx950 runs it at full rate), and g0 scales the fp32 result. X is fp16 as given, or split into fp16 hi + lo parts for fp32 input (two
+// MFMAs). The fp16 dictionary and the fp16 accumulation over the slots keep the product
+// within ~5e-4 relative L2 of the fp32 decode (the path's bar is 1e-3).
 //
 // Layout. Every 64-long k range (one block column) is stored permuted (kperm64), in both the
 // LDS dictionary and the transposed X, so that lane l (q = l/16) reads 16 consecutive
@@ -28,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <string>
 
@@ -58,7 +61,8 @@ struct MDesc {
     _Float16* xt;  // Mpad x C_full fp16 (hi), then Mpad x C_full (lo) for fp32 X
     int R, K, NB, NBc, slots, Ce, C_full;
     int u_base, u_count;  // units (row strip x block column) [u_base, u_base + u_count)
-    float sgam[16];
+    float g0;             // the largest stage gain: scales the accumulated products
+    uint32_t grel[16];    // slot j's gain relative to g0 as an fp16 pair (g_j / g0, same)
 };
 
 struct MParams {
@@ -130,8 +134,10 @@ __device__ __forceinline__ int find_matrix(const MParams& p, int u, int g) {
 // 32 rows (strip = 32 W rows). The codes and X slice of unit u + 1 are loaded into registers
 // while unit u is decoded and multiplied. One workgroup per CU (the dictionary fills most of
 // the LDS), so latency is hidden by the W waves of that workgroup.
-template <int NT, bool XS, int W, int RT>
+template <int NT, bool XS, int W, int RT, int SLOTS>
 __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr int CW = SLOTS / 4;  // 16-byte code pieces per tile
     constexpr int kThreads = W * 64;
     constexpr int kStripRows = W * 16 * RT;
     extern __shared__ __attribute__((aligned(16))) _Float16 smem16[];
@@ -153,7 +159,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
 
     floatx4 acc[RT][NT];
     u32x4 xr[GPT];   // prefetched X granules of the next unit
-    u32x4 cr[RT][4];  // prefetched code words of the next unit (RT row tiles, <= 16 slots)
+    u32x4 cr[RT][CW];  // prefetched code words of the next unit (RT row tiles)
     int ng = -1, nstrip = 0, nb = 0;  // the prefetched unit
 
     auto prefetch = [&](int u) {
@@ -178,8 +184,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
             const uint32_t* cw =
                 d.codes + csdr::tile_word_offset(r, nb, d.R, d.NB, d.NBc, d.slots);
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4)
-                cr[rt][j4] = *reinterpret_cast<const u32x4*>(cw + min(j4 * 4, d.slots - 4));
+            for (int j4 = 0; j4 < CW; ++j4) cr[rt][j4] = *reinterpret_cast<const u32x4*>(cw + j4 * 4);
         }
     };
 
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
                     const int r = rbase + i;
                     if (r < d.R && m < M)
                         __hip_atomic_fetch_add(d.y + (p.tm ? (size_t)m * d.R + r : (size_t)r * M + m),
-                                               acc[rt][nt][i],
+                                               acc[rt][nt][i] * d.g0,
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
@@ -249,52 +254,52 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
             *reinterpret_cast<u32x4*>(Xs + (size_t)part * MT * 64 + mrow * 64 +
                                       ((gr ^ (mrow & 7)) * 8)) = xr[i];
         }
-        u32x4 cc[RT][4];
+        u32x4 cc[RT][CW];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4) cc[rt][j4] = cr[rt][j4];
-        const int slots = d.slots;
-        float sg[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) sg[j] = d.sgam[j];
+            for (int j4 = 0; j4 < CW; ++j4) cc[rt][j4] = cr[rt][j4];
         __syncthreads();
         if (u + 1 < u1) prefetch(u + 1);
-        // decode this lane's 16 k values of its two rows (fp32 sums of fp16 atoms)
+        // decode this lane's 16 k values of each of its rows: per slot the coefficient as an
+        // fp16 pair (times the slot's gain relative to slot 0) and 8 packed fp16 FMAs over the
+        // atom's two 16-byte granules, accumulated in place as the two 8-value A operands
         half8 a[RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            float w[16];
+            h2 w[8];
 #pragma unroll
-            for (int t = 0; t < 16; ++t) w[t] = 0.0f;
+            for (int t = 0; t < 8; ++t) w[t] = h2{(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4) {
-                if (j4 * 4 < slots) {
+            for (int j = 0; j < SLOTS; ++j) {
+                const uint32_t word = cc[rt][j >> 2][j & 3];
+                // (c, c): the word's high half in both halves
+                const h2 c2 =
+                    __builtin_bit_cast(h2, __builtin_amdgcn_perm(word, word, 0x07060706u)) *
+                    __builtin_bit_cast(h2, d.grel[j]);
+                const uint32_t at = word & 0x7FFFu;
+                const uint32_t sw = (at >> 1) & 7;
+                const _Float16* drow = Ds + at * 64;
+                const u32x4 lo = *reinterpret_cast<const u32x4*>(drow + (((2 * q) ^ sw) * 8));
+                const u32x4 hi =
+                    *reinterpret_cast<const u32x4*>(drow + (((2 * q + 1) ^ sw) * 8));
+                // (vector elements go through a scalar: bit-casting a subscripted vector element
+                // directly reads element 0 whatever the subscript)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const uint32_t word = cc[rt][j4][jj];
-                        const float cf = sg[j4 * 4 + jj] * csdr::h2f(word >> 16);
-                        const uint32_t a = word & 0x7FFFu;
-                        const uint32_t sw = (a >> 1) & 7;
-                        const _Float16* drow = Ds + a * 64;
-                        const u32x4 lo =
-                            *reinterpret_cast<const u32x4*>(drow + (((2 * q) ^ sw) * 8));
-                        const u32x4 hi =
-                            *reinterpret_cast<const u32x4*>(drow + (((2 * q + 1) ^ sw) * 8));
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            w[2 * t] = fmaf(cf, csdr::h2f(lo[t] & 0xFFFFu), w[2 * t]);
-                            w[2 * t + 1] = fmaf(cf, csdr::h2f(lo[t] >> 16), w[2 * t + 1]);
-                            w[8 + 2 * t] = fmaf(cf, csdr::h2f(hi[t] & 0xFFFFu), w[8 + 2 * t]);
-                            w[9 + 2 * t] = fmaf(cf, csdr::h2f(hi[t] >> 16), w[9 + 2 * t]);
-                        }
-                    }
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t el = lo[t], eh = hi[t];
+                    w[t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, el), w[t]);
+                    w[4 + t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, eh), w[4 + t]);
                 }
             }
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a[rt][c][i] = (_Float16)w[8 * c + i];
+            for (int c = 0; c < 2; ++c) {
+                const u32x4 v = {__builtin_bit_cast(uint32_t, w[4 * c]),
+                                 __builtin_bit_cast(uint32_t, w[4 * c + 1]),
+                                 __builtin_bit_cast(uint32_t, w[4 * c + 2]),
+                                 __builtin_bit_cast(uint32_t, w[4 * c + 3])};
+                a[rt][c] = __builtin_bit_cast(half8, v);
+            }
         }
         // two 32-deep steps over the block column: lane group q holds positions 16 q + 8 c ..
         // + 7 of the permuted k order in step c, in both operands
@@ -341,21 +346,33 @@ size_t xt_bytes(const csdr_hsdb* s, int M) {
 // 64 columns and 8 beyond: M = 32 / 64 / 128 / 256 at 4096 x 11008: 47.1 -> 44.0, 58.6 ->
 // 52.2, 78.2 -> 68.7, 105.5 -> 98.6 us (M = 16 unchanged).
 constexpr int waves_for(int nt) { return nt <= 4 ? 16 : 8; }
+// (two 16-row tiles per wave from 64 columns up, so that each X operand read from LDS feeds
+// two matrix-core steps, measured slower: cfg2 M = 64 44.3 -> 56.6 us, M = 256 88.0 -> 104.8)
 constexpr int rows_for(int) { return 1; }
 
-template <int NT, bool XS>
+template <int NT, bool XS, int SLOTS>
 int launch_one(const MParams& p, int grid, size_t lds, hipStream_t st) {
     constexpr int W = waves_for(NT), RT = rows_for(NT);
-    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W, RT>);
+    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W, RT, SLOTS>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    mfma_kernel<NT, XS, W, RT><<<grid, W * 64, lds, st>>>(p);
+    mfma_kernel<NT, XS, W, RT, SLOTS><<<grid, W * 64, lds, st>>>(p);
     CSDR_LAUNCH_CHECK("hsdb mfma");
     return CSDR_OK;
 }
 
+template <int NT, bool XS>
+int launch_slots(const MParams& p, int slots, int grid, size_t lds, hipStream_t st) {
+    switch (slots) {
+        case 4: return launch_one<NT, XS, 4>(p, grid, lds, st);
+        case 8: return launch_one<NT, XS, 8>(p, grid, lds, st);
+        default: return launch_one<NT, XS, 16>(p, grid, lds, st);
+    }
+}
+
 template <int NT>
-int launch_main(const MParams& p, bool xs, int grid, size_t lds, hipStream_t st) {
-    return xs ? launch_one<NT, true>(p, grid, lds, st) : launch_one<NT, false>(p, grid, lds, st);
+int launch_main(const MParams& p, bool xs, int slots, int grid, size_t lds, hipStream_t st) {
+    return xs ? launch_slots<NT, true>(p, slots, grid, lds, st)
+              : launch_slots<NT, false>(p, slots, grid, lds, st);
 }
 
 }  // namespace
@@ -370,7 +387,8 @@ bool mfma_eligible(int n, const csdr_hsdb* const* segs, int M) {
         const csdr_hsdb* s = segs[i];
         if (!s || s->tile_rows != 1 || s->tile_cols != 64 || s->K > (uint32_t)kMaxAtoms ||
             !s->d_dict16p ||
-            s->NB == 0 || !(s->slots == 4 || s->slots == 8 || s->slots == 16))
+            s->NB == 0 || !(s->slots == 4 || s->slots == 8 || s->slots == 16) ||
+            s->slots != segs[0]->slots)
             return false;
     }
     return true;
@@ -417,7 +435,17 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
         d.slots = (int)s->slots;
         d.Ce = (int)s->Ce;
         d.C_full = (int)s->C_full;
-        for (uint32_t j = 0; j < s->slots && j < 16; ++j) d.sgam[j] = s->h_slot_gamma[j];
+        // the slots' gains relative to the largest: 1 for the usual single stage and powers of
+        // two for gamma_l = 0.5^l (exact in fp16), never above 1 (no fp16 overflow)
+        float gmax = 0.0f;
+        for (uint32_t j = 0; j < s->slots && j < 16; ++j)
+            gmax = std::max(gmax, std::fabs(s->h_slot_gamma[j]));
+        d.g0 = gmax > 0.0f ? gmax : 1.0f;
+        for (uint32_t j = 0; j < 16; ++j) {
+            const float rel = j < s->slots ? s->h_slot_gamma[j] / d.g0 : 0.0f;
+            const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)rel);
+            d.grel[j] = h << 16 | h;
+        }
         max_elems = std::max(max_elems, (size_t)d.R * M + (size_t)p.Mpad * d.NB * 8);
     }
     int dev = 0, ncu = 256, lds_max = 65536;
@@ -467,12 +495,13 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
         MParams q = p;
         q.m0 = m0;
         int rc;
+        const int slots = (int)segs[0]->slots;
         switch (nt) {
-            case 16: rc = launch_main<16>(q, xsplit, grid, lds, st); break;
-            case 8: rc = launch_main<8>(q, xsplit, grid, lds, st); break;
-            case 4: rc = launch_main<4>(q, xsplit, grid, lds, st); break;
-            case 2: rc = launch_main<2>(q, xsplit, grid, lds, st); break;
-            default: rc = launch_main<1>(q, xsplit, grid, lds, st); break;
+            case 16: rc = launch_main<16>(q, xsplit, slots, grid, lds, st); break;
+            case 8: rc = launch_main<8>(q, xsplit, slots, grid, lds, st); break;
+            case 4: rc = launch_main<4>(q, xsplit, slots, grid, lds, st); break;
+            case 2: rc = launch_main<2>(q, xsplit, slots, grid, lds, st); break;
+            default: rc = launch_main<1>(q, xsplit, slots, grid, lds, st); break;
         }
         if (rc != CSDR_OK) return rc;
     }
