@@ -169,6 +169,17 @@ class InferenceEngine:
             _ce(err)
             return out[:n.value].copy()
 
+    def run(self, x: np.ndarray, out_size: int | None = None) -> np.ndarray:
+        """cortex_inference_engine_run: the archive's layer chain on x (M x C floats)."""
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        cap = out_size if out_size is not None else max(1 << 16, 64 * x.size)
+        y = np.empty(cap, np.float32)
+        n = C.c_size_t()
+        _ce(self._lib.cortex_inference_engine_run(self._h, x.ctypes.data_as(C.c_void_p), x.size,
+                                                  y.ctypes.data_as(C.c_void_p), cap,
+                                                  C.byref(n)))
+        return y[:n.value].copy()
+
     def generate(self, prompt_ids, max_new_tokens: int) -> list:
         txt = C.c_void_p()
         p = " ".join(str(int(t)) for t in prompt_ids).encode()

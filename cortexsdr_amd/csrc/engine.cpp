@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cctype>
+#include <cmath>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -275,6 +276,14 @@ CortexError read_vector(CortexInferenceEngine* e, const std::string& name, size_
     return ok();
 }
 
+// Every input finite and within fp16's range, so x = fp16(x) + fp16(x - fp16(x)) holds to
+// about 2^-22 of each element.
+bool split_ok(const float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (!(std::fabs(x[i]) <= 32768.0f)) return false;
+    return true;
+}
+
 char* dup_c(const std::string& s) {
     char* p = static_cast<char*>(std::malloc(s.size() + 1));
     if (p) std::memcpy(p, s.c_str(), s.size() + 1);
@@ -489,6 +498,181 @@ CortexError apply_lazy(CortexInferenceEngine* e) {
     return rc ? from_csdr(rc, "lazy selection") : ok();
 }
 
+// getExecutionOrder without a graph (SparseInferenceEngine.cpp:2852-2893): the weight-like
+// segments (isWeightLikeSegmentType :91-100) and executable op layers (:102-130), those with
+// a layer name first by (layer index, layer name), then by name; each under its execution
+// name (deriveExecutionName :529-547: the layer name, else the name without a weight/bias
+// suffix), token embeddings skipped, each name once.
+std::vector<std::string> execution_order(const CortexInferenceEngine* e) {
+    struct Cand {
+        std::string name, layer_name;
+        uint32_t layer_index;
+    };
+    static const char* const kOps[] = {"add", "sub", "mul", "div", "relu", "sigmoid", "tanh",
+                                       "softmax", "gelu", "leakyrelu", "elu", "silu", "swish",
+                                       "reshape", "transpose", "flatten", "concat", "slice"};
+    std::vector<Cand> cands;
+    const size_t n = csdr_archive_count(e->ar);
+    for (size_t i = 0; i < n; ++i) {
+        csdr_segment_info info;
+        csdr_archive_info(e->ar, i, &info);
+        const uint32_t t = info.original_type;
+        bool take = t == 1 || t == 2 || t == 3 || t == 4 || (t >= 11 && t <= 14);
+        const std::string lt = lower(info.layer_type ? info.layer_type : "");
+        for (const char* op : kOps) take = take || lt == op;
+        if (take)
+            cands.push_back({info.name, info.layer_name ? info.layer_name : "", info.layer_index});
+    }
+    std::stable_sort(cands.begin(), cands.end(), [](const Cand& a, const Cand& b) {
+        const bool ha = !a.layer_name.empty(), hb = !b.layer_name.empty();
+        if (ha != hb) return ha > hb;
+        if (ha && hb) {
+            if (a.layer_index != b.layer_index) return a.layer_index < b.layer_index;
+            if (a.layer_name != b.layer_name) return a.layer_name < b.layer_name;
+        }
+        return a.name < b.name;
+    });
+    static const char* const kSuffixes[] = {".weight", ".weights", ".bias", "/weight",
+                                            "/weights", "/bias", "_weight", "_bias"};
+    std::vector<std::string> order;
+    std::unordered_set<std::string> seen;
+    for (const Cand& c : cands) {
+        std::string x = c.layer_name;
+        if (x.empty()) {
+            x = c.name;
+            for (const char* suf : kSuffixes) {
+                const size_t k = std::strlen(suf);
+                if (x.size() > k && x.compare(x.size() - k, k, suf) == 0) {
+                    x.erase(x.size() - k);
+                    break;
+                }
+            }
+        }
+        const std::string lx = lower(x);
+        if (lx.find("token_embd") != std::string::npos ||
+            lx.find("tok_embeddings") != std::string::npos ||
+            lx.find("embed_tokens") != std::string::npos)
+            continue;
+        if (!x.empty() && seen.insert(x).second) order.push_back(x);
+    }
+    return order;
+}
+
+const char* path_name(const Cached* c) {
+    return c->kind == kHsdb   ? "hsdb"
+           : c->kind == kQ4k  ? "q4_k"
+           : c->kind == kGguf ? "gguf"
+                              : "dense_f32";
+}
+
+// y (M x R, host) = x (M x C, host) . W^T through the loaded segment's device path (the
+// body of run_layer and of each layer of run); *dev_ms gets the device time.
+CortexError run_linear(CortexInferenceEngine* e, Cached* c, const std::string& layer_name,
+                       const float* input, size_t M, std::vector<float>& output, float* dev_ms) {
+    const size_t R = c->R, C = c->C, input_size = M * C;
+    int rc = grow((void**)&e->xd, &e->xcap, input_size * 4);
+    if (!rc) rc = grow((void**)&e->yd, &e->ycap, M * R * 4);
+    if (rc) return from_csdr(rc, "staging");
+    std::vector<float> host;
+    bool split = false;  // Q4_K / GGUF batch through the matrix cores (fp16 hi + lo inputs)
+    hipEvent_t ev0, ev1;
+    (void)hipEventCreate(&ev0);
+    (void)hipEventCreate(&ev1);
+    struct Events {
+        hipEvent_t a, b;
+        ~Events() {
+            (void)hipEventDestroy(a);
+            (void)hipEventDestroy(b);
+        }
+    } evs{ev0, ev1};
+    if (c->kind == kHsdb) {
+        // M x C token-major in, the coded product takes C x M feature-major
+        const float* xin = input;
+        if (M > 1) {
+            host.resize(input_size);
+            for (size_t m = 0; m < M; ++m)
+                for (size_t k = 0; k < C; ++k) host[k * M + m] = input[m * C + k];
+            xin = host.data();
+        }
+        if (hipMemcpyAsync(e->xd, xin, input_size * 4, hipMemcpyHostToDevice, e->st) != hipSuccess)
+            return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
+        const size_t need = csdr_hsdb_workspace_bytes(c->seg, (int)M);
+        if ((rc = grow(&e->ws, &e->ws_bytes, need))) return from_csdr(rc, "workspace");
+        (void)hipEventRecord(ev0, e->st);
+        rc = csdr_hsdb_matmul(c->seg, e->xd, CSDR_F32, (int)M, e->yd, e->ws, e->ws_bytes, e->st);
+    } else {
+        const bool tc = (c->kind == kQ4k || c->kind == kGguf) && M > 1 &&
+                        split_ok(input, input_size) && (c->kind == kQ4k || C % 16 == 0);
+        if (!tc) {
+            if (hipMemcpyAsync(e->xd, input, input_size * 4, hipMemcpyHostToDevice, e->st) !=
+                hipSuccess)
+                return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
+            (void)hipEventRecord(ev0, e->st);
+        }
+        if (tc) {
+            // the matrix-core form for the whole batch: it reads fp16 activations, so the fp32
+            // input goes in as two exact fp16 parts, hi = fp16(x) and lo = fp16(x - hi), whose
+            // products are added in fp32 on the way out (x to about 2^-22, the weights read
+            // twice instead of M times)
+            split = true;
+            std::vector<_Float16> parts(2 * input_size);
+            for (size_t i = 0; i < input_size; ++i) {
+                const _Float16 h = (_Float16)input[i];
+                parts[i] = h;
+                parts[input_size + i] = (_Float16)(input[i] - (float)h);
+            }
+            // the fp32 staging holds both fp16 parts; the second product's output follows y
+            if ((rc = grow((void**)&e->yd, &e->ycap, 2 * M * R * 4)))
+                return from_csdr(rc, "staging");
+            (void)hipEventRecord(ev0, e->st);
+            if (hipMemcpyAsync(e->xd, parts.data(), 2 * input_size * 2, hipMemcpyHostToDevice,
+                               e->st) != hipSuccess)
+                return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
+            const _Float16* xh = reinterpret_cast<const _Float16*>(e->xd);
+            for (int part = 0; part < 2 && rc == CSDR_OK; ++part) {
+                const _Float16* xp = xh + part * input_size;
+                float* yp = e->yd + part * M * R;
+                rc = c->kind == kQ4k
+                         ? csdr_q4k_linear(c->dev, (int)R, (int)C, CSDR_Q4K_GGML, xp, CSDR_F16,
+                                           (int)M, yp, e->st)
+                         : csdr_gguf_linear(c->dev, c->gguf, (int)R, (int)C, xp, CSDR_F16,
+                                            (int)M, yp, e->st);
+            }
+        } else if (c->kind == kQ4k || c->kind == kGguf) {
+            // M == 1 (or inputs beyond fp16's range): the GEMV form on fp32 x, row by row
+            rc = CSDR_OK;
+            for (size_t m = 0; m < M && rc == CSDR_OK; ++m)
+                rc = c->kind == kQ4k
+                         ? csdr_q4k_linear(c->dev, (int)R, (int)C, CSDR_Q4K_GGML, e->xd + m * C,
+                                           CSDR_F32, 1, e->yd + m * R, e->st)
+                         : csdr_gguf_linear(c->dev, c->gguf, (int)R, (int)C, e->xd + m * C,
+                                            CSDR_F32, 1, e->yd + m * R, e->st);
+        } else {
+            rc = csdr_dense_linear(static_cast<const float*>(c->dev), (int)R, (int)C, e->xd,
+                                   (int)M, e->yd, e->st);
+        }
+    }
+    (void)hipEventRecord(ev1, e->st);
+    if (rc) return from_csdr(rc, "run_layer '" + layer_name + "'");
+    host.resize((split ? 2 : 1) * M * R);
+    if (hipMemcpyAsync(host.data(), e->yd, host.size() * 4, hipMemcpyDeviceToHost, e->st) !=
+            hipSuccess ||
+        hipStreamSynchronize(e->st) != hipSuccess)
+        return fail(CORTEX_ERROR_INFERENCE, "output download failed");
+    *dev_ms = 0.f;
+    (void)hipEventElapsedTime(dev_ms, ev0, ev1);
+    output.resize(M * R);
+    if (c->kind == kHsdb && M > 1) {
+        for (size_t r2 = 0; r2 < R; ++r2)
+            for (size_t m = 0; m < M; ++m) output[m * R + r2] = host[r2 * M + m];
+    } else if (split) {
+        for (size_t i = 0; i < M * R; ++i) output[i] = host[i] + host[M * R + i];
+    } else {
+        std::memcpy(output.data(), host.data(), M * R * 4);
+    }
+    return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -634,14 +818,77 @@ CSDR_API void cortex_error_free(CortexError* error) {
 
 CSDR_API const char* cortex_sdk_version(void) { return "1.0.0-mi355x"; }
 
-CSDR_API CortexError cortex_inference_engine_run(CortexInferenceEngineHandle e, const float*, size_t,
-                                                 float*, size_t, size_t* actual_output_size) {
+CSDR_API CortexError cortex_inference_engine_run(CortexInferenceEngineHandle e,
+                                                 const float* input, size_t input_size,
+                                                 float* output, size_t output_size,
+                                                 size_t* actual_output_size) {
     CORTEX_GUARD_BEGIN
     CHECK_HANDLE(e);
-    if (actual_output_size) *actual_output_size = 0;
-    return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
-                "run: whole-graph execution is outside the coded-weight device path; use "
-                "cortex_inference_engine_run_layer or cortex_inference_engine_generate_text");
+    if (!input || !output || !actual_output_size)
+        return fail(CORTEX_ERROR_INVALID_ARGUMENT, "Invalid arguments (null pointers)");
+    *actual_output_size = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    // SDRInferenceEngine::run (SparseInferenceEngine.cpp:2220-2262) -> runLayersOnDemand
+    // (:2911-3027): the archive's layers in execution order, each output the next input
+    std::vector<float> cur(input, input + input_size), next;
+    std::string layers_json;
+    for (const std::string& name : execution_order(e)) {
+        size_t idx;
+        if (!resolve(e, name, &idx))
+            return fail(CORTEX_ERROR_INFERENCE, "Segment info not found for layer: " + name);
+        csdr_segment_info info;
+        csdr_archive_info(e->ar, idx, &info);
+        const auto l0 = std::chrono::steady_clock::now();
+        Cached* c = nullptr;
+        CortexError r = load(e, idx, &c);
+        if (r.code == CORTEX_ERROR_UNSUPPORTED_FORMAT || r.code == CORTEX_ERROR_INFERENCE)
+            return fail(CORTEX_ERROR_UNSUPPORTED_FORMAT,
+                        "run: layer '" + name + "' is not a linear layer of the device path " +
+                            "(strategy-5 HSDR/HSDB, fp32, q4_k or GGUF 2-D weights): " +
+                            std::string(r.message ? r.message : ""));
+        if (r.code) return r;
+        const auto l1 = std::chrono::steady_clock::now();
+        if (cur.empty() || cur.size() % c->C)
+            return fail(CORTEX_ERROR_INFERENCE,
+                        "run: layer '" + name + "' takes " + std::to_string(c->C) +
+                            " input features; its input has " + std::to_string(cur.size()) +
+                            " values");
+        const size_t M = cur.size() / c->C;
+        float ms = 0.f;
+        r = run_linear(e, c, name, cur.data(), M, next, &ms);
+        if (r.code) return r;
+        if (c->kind != kHsdb) {
+            // a loaded layer carries its bias segment (name.bias, loadLayerByName :1128-1137);
+            // the HSDR stub of runLayersOnDemand (:2931-2955) carries only the shapes
+            size_t bidx;
+            if (csdr_archive_find(e->ar, (name + ".bias").c_str(), &bidx) == CSDR_OK) {
+                std::vector<float> bias;
+                r = read_vector(e, name + ".bias", c->R, bias);
+                if (r.code) return r;
+                for (size_t m = 0; m < M; ++m)
+                    for (size_t j = 0; j < c->R; ++j) next[m * c->R + j] += bias[j];
+            }
+        }
+        cur.swap(next);
+        char buf[384];
+        std::snprintf(buf, sizeof buf,
+                      "%s{\"name\":\"%s\",\"path\":\"%s\",\"load_ms\":%.4f,"
+                      "\"device_ms\":%.4f,\"output_size\":%zu}",
+                      layers_json.empty() ? "" : ",", name.c_str(), path_name(c),
+                      std::chrono::duration<double, std::milli>(l1 - l0).count(), ms,
+                      cur.size());
+        layers_json += buf;
+        if (e->aggressive) evict(e, idx);
+    }
+    *actual_output_size = cur.size();
+    if (cur.size() > output_size) return fail(CORTEX_ERROR_MEMORY, "Output buffer too small");
+    std::copy(cur.begin(), cur.end(), output);
+    char head[128];
+    std::snprintf(head, sizeof head, "{\"total_ms\":%.4f,\"layers\":[",
+                  std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+                      .count());
+    e->stats = std::string(head) + layers_json + "]}";
+    return ok();
     CORTEX_GUARD_END("cortex_inference_engine_run")
 }
 
@@ -671,80 +918,17 @@ CSDR_API CortexError cortex_inference_engine_run_layer(CortexInferenceEngineHand
     if (M > (size_t)1 << 20) return fail(CORTEX_ERROR_INVALID_ARGUMENT, "batch too large");
     *actual_output_size = M * R;
     if (output_size < M * R) return fail(CORTEX_ERROR_MEMORY, "Output buffer too small");
-    int rc = grow((void**)&e->xd, &e->xcap, input_size * 4);
-    if (!rc) rc = grow((void**)&e->yd, &e->ycap, M * R * 4);
-    if (rc) return from_csdr(rc, "staging");
-    std::vector<float> host;
-    hipEvent_t ev0, ev1;
-    (void)hipEventCreate(&ev0);
-    (void)hipEventCreate(&ev1);
-    if (c->kind == kHsdb) {
-        // M x C token-major in, the coded product takes C x M feature-major
-        const float* xin = input;
-        if (M > 1) {
-            host.resize(input_size);
-            for (size_t m = 0; m < M; ++m)
-                for (size_t k = 0; k < C; ++k) host[k * M + m] = input[m * C + k];
-            xin = host.data();
-        }
-        if (hipMemcpyAsync(e->xd, xin, input_size * 4, hipMemcpyHostToDevice, e->st) != hipSuccess)
-            return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
-        const size_t need = csdr_hsdb_workspace_bytes(c->seg, (int)M);
-        if ((rc = grow(&e->ws, &e->ws_bytes, need))) return from_csdr(rc, "workspace");
-        (void)hipEventRecord(ev0, e->st);
-        rc = csdr_hsdb_matmul(c->seg, e->xd, CSDR_F32, (int)M, e->yd, e->ws, e->ws_bytes, e->st);
-    } else {
-        if (hipMemcpyAsync(e->xd, input, input_size * 4, hipMemcpyHostToDevice, e->st) != hipSuccess)
-            return fail(CORTEX_ERROR_INFERENCE, "input upload failed");
-        (void)hipEventRecord(ev0, e->st);
-        if (c->kind == kQ4k || c->kind == kGguf) {
-            // fp32 activations take the GEMV form row by row (the matrix-core form reads
-            // fp16 activations)
-            rc = CSDR_OK;
-            for (size_t m = 0; m < M && rc == CSDR_OK; ++m)
-                rc = c->kind == kQ4k
-                         ? csdr_q4k_linear(c->dev, (int)R, (int)C, CSDR_Q4K_GGML, e->xd + m * C,
-                                           CSDR_F32, 1, e->yd + m * R, e->st)
-                         : csdr_gguf_linear(c->dev, c->gguf, (int)R, (int)C, e->xd + m * C,
-                                            CSDR_F32, 1, e->yd + m * R, e->st);
-        } else {
-            rc = csdr_dense_linear(static_cast<const float*>(c->dev), (int)R, (int)C, e->xd,
-                                   (int)M, e->yd, e->st);
-        }
-    }
-    (void)hipEventRecord(ev1, e->st);
-    if (rc) {
-        (void)hipEventDestroy(ev0);
-        (void)hipEventDestroy(ev1);
-        return from_csdr(rc, std::string("run_layer '") + layer_name + "'");
-    }
-    host.resize(M * R);
-    if (hipMemcpyAsync(host.data(), e->yd, M * R * 4, hipMemcpyDeviceToHost, e->st) != hipSuccess ||
-        hipStreamSynchronize(e->st) != hipSuccess) {
-        (void)hipEventDestroy(ev0);
-        (void)hipEventDestroy(ev1);
-        return fail(CORTEX_ERROR_INFERENCE, "output download failed");
-    }
+    std::vector<float> y;
     float dev_ms = 0.f;
-    (void)hipEventElapsedTime(&dev_ms, ev0, ev1);
-    (void)hipEventDestroy(ev0);
-    (void)hipEventDestroy(ev1);
-    if (c->kind == kHsdb && M > 1) {
-        for (size_t r2 = 0; r2 < R; ++r2)
-            for (size_t m = 0; m < M; ++m) output[m * R + r2] = host[r2 * M + m];
-    } else {
-        std::memcpy(output, host.data(), M * R * 4);
-    }
+    r = run_linear(e, c, layer_name, input, M, y, &dev_ms);
+    if (r.code) return r;
+    std::memcpy(output, y.data(), M * R * 4);
     const auto t2 = std::chrono::steady_clock::now();
-    const char* path = c->kind == kHsdb   ? "hsdb"
-                       : c->kind == kQ4k  ? "q4_k"
-                       : c->kind == kGguf ? "gguf"
-                                          : "dense_f32";
     char buf[512];
     std::snprintf(buf, sizeof buf,
                   "{\"layer\":\"%s\",\"path\":\"%s\",\"rows\":%zu,\"cols\":%zu,\"batch\":%zu,"
                   "\"load_ms\":%.4f,\"device_ms\":%.4f,\"total_ms\":%.4f,\"cached_bytes\":%zu}",
-                  layer_name, path, R, C, M,
+                  layer_name, path_name(c), R, C, M,
                   std::chrono::duration<double, std::milli>(t1 - t0).count(), dev_ms,
                   std::chrono::duration<double, std::milli>(t2 - t0).count(), e->cache_bytes);
     e->stats = buf;

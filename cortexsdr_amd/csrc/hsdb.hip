@@ -1960,6 +1960,33 @@ struct XopArgs {
     int nsplit = 0, hd = 0;
 };
 
+// 2 <= M <= 8: the streaming multi-column gather reads every code once for all columns
+// (fp32 throughout), where the matrix-core path decodes each weight through the LDS
+// dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count in the group) and a P
+// slice within the gather's budget.
+bool vec_path(int n, const csdr_hsdb* const* segs, int M) {
+    bool vec = M >= 2 && M <= kMaxVecM;
+    for (int i = 0; i < n && vec; ++i) {
+        const csdr_hsdb* s = segs[i];
+        const int mc = gatherv_mc(M);
+        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMinRows) * 4 * mc;
+        vec = s->tile_rows == 1 && s->NB > 0 && (s->slots == 4 || s->slots == 8 || s->slots == 16) &&
+              s->slots == segs[0]->slots && lds <= (size_t)160 * 1024 / gatherv_wgs_per_cu(mc);
+    }
+    return vec;
+}
+
+// A plain product (both phases, no x op) at batch M takes the matrix-core path.
+bool plain_takes_mfma(int n, const csdr_hsdb* const* segs, int M) {
+    return !vec_path(n, segs, M) && csdr::mfma_eligible(n, segs, M);
+}
+
+// Workspace a plain product at batch M needs on the path it takes.
+size_t plain_ws_bytes(int n, const csdr_hsdb* const* segs, int M) {
+    return plain_takes_mfma(n, segs, M) ? csdr::mfma_workspace_bytes(n, segs, M)
+                                        : p_path_ws_bytes(n, segs, M);
+}
+
 int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int x_dtype, int M,
                  float* const* ys, void* workspace, size_t workspace_bytes, hipStream_t st,
                  int phases = kPhaseDx | kPhaseGather, const float* const* bias = nullptr,
@@ -1995,16 +2022,9 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     // (fp32 throughout), where the matrix-core path decodes each weight through the LDS
     // dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count in the group) and
     // a P slice within the gather's budget
-    bool vec = M >= 2 && M <= kMaxVecM;
-    for (int i = 0; i < n && vec; ++i) {
-        const csdr_hsdb* s = segs[i];
-        const int mc = gatherv_mc(M);
-        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMinRows) * 4 * mc;
-        vec = s->tile_rows == 1 && s->NB > 0 && (s->slots == 4 || s->slots == 8 || s->slots == 16) &&
-              s->slots == segs[0]->slots && lds <= (size_t)160 * 1024 / gatherv_wgs_per_cu(mc);
-    }
-    if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE && !vec &&
-        csdr::mfma_eligible(n, segs, M))
+    const bool vec = vec_path(n, segs, M);
+    if (phases == (kPhaseDx | kPhaseGather) && xa.xop == CSDR_XOP_NONE &&
+        plain_takes_mfma(n, segs, M))
         return csdr::mfma_matmul(n, segs, xs, x_dtype, M, ys, bias,
                                  (flags & CSDR_HSDB_ACCUMULATE) ? 1 : 0, tm ? 1 : 0, workspace,
                                  workspace_bytes, st);
@@ -2366,7 +2386,9 @@ CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* s, const void* x, int x_d
                          "hsdb_matmul_noalloc: the segment lives on device " +
                              std::to_string(s->device) + ", the current device is " +
                              std::to_string(dev));
-    const size_t need = group_ws_bytes(1, &s, M);
+    // sized for the path this plain product takes (a matrix-core product needs only its
+    // transposed X, far less than the P path would at the same M)
+    const size_t need = plain_ws_bytes(1, &s, M);
     if (need > kScratchBytes)
         return set_error(CSDR_E_WORKSPACE,
                          "hsdb_matmul_noalloc: this product needs " + std::to_string(need) +

@@ -9,9 +9,9 @@
 // v & 1, :545-546, :716-717), chosen at load; indices >= K are skipped.
 //
 // Selection, per sequence row:
-//   lazy_ah_kernel     ah[a] = float(sum_c double(atom[a][c]) * hidden[c]): one wave per atom,
-//                      fp64 partial sums over strided features and a fp64 butterfly (the CLI
-//                      sums c in order; both round the fp64 sum to float once);
+//   lazy_ah_kernel     ah[a] = float(sum_c double(atom[a][c]) * hidden[c]): one thread per atom
+//                      adding the (exact) fp64 products in feature order, as the CLI does, so
+//                      ah is the CLI's value bit for bit;
 //   lazy_score_kernel  one thread per token: the float sum over its slots in order of
 //                      (gamma_l * sign) * ah[idx] (separately rounded multiply and add, as the
 //                      CLI's source evaluates it), optionally stored, times 1 / temperature
@@ -84,20 +84,40 @@ __global__ __launch_bounds__(kThreads) void lazy_row_kernel(csdr_lazy_hsdr h, co
     }
 }
 
+// ah[row][a] = (float) sum_c atom_a[c] * hidden[c] in fp64, one thread per atom adding the
+// products in feature order, as the CLI's loop does (cortexsdr_cli.cpp:700-704): each product
+// of two floats is exact in fp64, so the sum's rounding sequence, and the float it rounds to,
+// is the reference's. The workgroup's atoms are staged kAhTile features at a time through LDS
+// (coalesced row reads; rows padded by one float so a column read meets distinct banks).
+constexpr int kAhTile = 32;
+
 __global__ __launch_bounds__(kThreads) void lazy_ah_kernel(csdr_lazy_hsdr h,
                                                            const float* __restrict__ hidden,
                                                            float* __restrict__ ah) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t a = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    __shared__ float tile[kThreads * (kAhTile + 1)];
+    __shared__ float xs[kAhTile];
+    const int tid = threadIdx.x;
+    const uint32_t a0 = blockIdx.x * kThreads;
     const int row = blockIdx.y;
-    if (a >= h.K) return;
-    const float* atom = h.atoms + (size_t)a * h.C;
     const float* x = hidden + (size_t)row * h.C;
     double s = 0.0;
-    for (uint32_t c = lane; c < h.C; c += 64) s += (double)atom[c] * (double)x[c];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (lane == 0) ah[(size_t)row * h.K + a] = (float)s;
+    for (uint32_t c0 = 0; c0 < h.C; c0 += kAhTile) {
+        const uint32_t nc = min((uint32_t)kAhTile, h.C - c0);
+        __syncthreads();
+        // atoms a0 .. a0 + kThreads - 1, features c0 .. c0 + nc - 1: consecutive threads read
+        // consecutive features of one atom
+        for (uint32_t i = tid; i < (uint32_t)kThreads * kAhTile; i += kThreads) {
+            const uint32_t r = i / kAhTile, c = i - r * kAhTile;
+            const uint32_t a = a0 + r;
+            tile[r * (kAhTile + 1) + c] =
+                (a < h.K && c < nc) ? h.atoms[(size_t)a * h.C + c0 + c] : 0.0f;
+        }
+        if (tid < kAhTile) xs[tid] = tid < (int)nc ? x[c0 + tid] : 0.0f;
+        __syncthreads();
+        const float* t = tile + tid * (kAhTile + 1);
+        for (uint32_t c = 0; c < nc; ++c) s += (double)t[c] * (double)xs[c];
+    }
+    if (a0 + tid < h.K) ah[(size_t)row * h.K + a0 + tid] = (float)s;
 }
 
 __device__ __forceinline__ bool better(float s, int i, float bs, int bi) {
@@ -314,8 +334,8 @@ CSDR_API int csdr_lazy_hsdr_select(const csdr_lazy_hsdr* h, const float* hidden,
     int* ws_i = reinterpret_cast<int*>(ws_s + (size_t)rows * nb);
     const float ts = temperature > 0.0f ? 1.0f / temperature : 1.0f;
     if (h->K) {
-        lazy_ah_kernel<<<dim3((h->K + kThreads / 64 - 1) / (kThreads / 64), rows), kThreads, 0,
-                         st>>>(*h, hidden, ah);
+        lazy_ah_kernel<<<dim3((h->K + kThreads - 1) / kThreads, rows), kThreads, 0, st>>>(
+            *h, hidden, ah);
         CSDR_LAUNCH_CHECK("lazy_hsdr ah");
     }
     lazy_score_kernel<<<dim3(nb, rows), kThreads, 0, st>>>(*h, ah, repeated, ts, penalty, scores,

@@ -17,8 +17,9 @@
  *     cortex_sdk.cpp:114); one handle must still not be used by two threads at once.
  *   - generate_text takes the prompt as whitespace-separated token ids and returns the
  *     generated ids the same way: the tokenizer (LLMTokenizer) is outside this path.
- *   - cortex_inference_engine_run (whole-graph execution of non-decoder models) returns
- *     CORTEX_ERROR_UNSUPPORTED_FORMAT: the graph executor is outside the coded-weight path.
+ *   - cortex_inference_engine_run runs the archive's layers in the reference's execution
+ *     order as a chain of linear layers (see below); layers that are not 2-D weights of the
+ *     device path (conv, pooling, graph ops) return CORTEX_ERROR_UNSUPPORTED_FORMAT.
  */
 #ifndef CORTEX_SDK_GPU_H
 #define CORTEX_SDK_GPU_H
@@ -80,6 +81,14 @@ CSDR_API CortexError cortex_inference_engine_get_last_run_stats_json(
 CSDR_API void cortex_free_string(char* s);
 CSDR_API void cortex_error_free(CortexError* error);
 
+/* SDRInferenceEngine::run (SparseInferenceEngine.cpp:2220-2262) without an ONNX graph: the
+ * archive's weight-like segments in getExecutionOrder's order (:2852-2893: layer_index and
+ * layer_name first, then names; token embeddings skipped), run on demand as
+ * runLayersOnDemand does (:2911-3027), each layer's output the next one's input: strategy-5
+ * layers through the coded product (no bias, as the reference's HSDR stub), fp32 / q4_k / GGUF
+ * layers through their device products plus a `name.bias` segment when present. The input
+ * is M x C of the first layer (M = input_size / C). get_last_run_stats_json then lists the
+ * layers with their load and device times. */
 CSDR_API CortexError cortex_inference_engine_run(CortexInferenceEngineHandle handle,
                                                  const float* input_data, size_t input_size,
                                                  float* output_data, size_t output_size,

@@ -275,7 +275,10 @@ CSDR_API int csdr_hsdr_compress(const float* w, uint32_t rows, uint32_t cols, ui
  * tiles widen to each matrix's width; one dictionary per bucket, buckets in the order of the
  * reference's std::unordered_map over the same key and hash); a matrix whose shape is not a
  * whole number of tiles, or with more than 1e-3 non-finite values, is skipped (others are
- * zeroed); each bucket's tiles are pooled, reservoir-sampled to max_tiles_for_fit when that
+ * zeroed: with 2-D tiles the reference re-encodes such a matrix from its raw values,
+ * :2472-2476, so NaN/Inf reach its matching pursuit there; this build encodes the zeroed
+ * values in both modes, a deliberate difference that no reference fixture covers); each
+ * bucket's tiles are pooled, reservoir-sampled to max_tiles_for_fit when that
  * is non-zero and smaller (mt19937(0xC0DECAFE ^ cap), :2277-2395), the dictionary fitted on
  * the pool as csdr_hsdr_compress fits one matrix (ksvd_iters passes), and every matrix of
  * the bucket encoded against it as an HSDC codes stream (compressFP32WithExternalDictionary,

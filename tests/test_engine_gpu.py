@@ -81,10 +81,17 @@ def test_run_layer_routes(gpu, model, golden):
         xd = np.random.default_rng(1).normal(size=(2, 7)).astype(np.float32)
         Y = eng.run_layer("dense.weight", xd).reshape(2, 5)
         assert rel_l2(Y, xd @ model["dense"].T) < 1e-6
-        xq = synth.activations(512, 2, seed=7)
-        Y = eng.run_layer("blk.0.ffn_down.weight", xq.T).reshape(2, 8)
-        ref = oracle.q4k_linear(model["q4"], 8, 512, xq.T.copy())
-        assert rel_l2(Y, ref) < 1e-5
+        # Q4_K batches take the matrix-core form (x as exact fp16 hi + lo parts, weights
+        # unrounded): fp32-level agreement at every batch
+        for M in (1, 2, 32):
+            xq = synth.activations(512, M, seed=7)
+            Y = eng.run_layer("blk.0.ffn_down.weight", xq.T).reshape(M, 8)
+            ref = oracle.q4k_linear(model["q4"], 8, 512, xq.T.copy())
+            assert rel_l2(Y, ref) < 1e-5, M
+        # inputs beyond fp16's range keep the fp32 GEMV form
+        xb = (synth.activations(512, 2, seed=8) * 1e5).astype(np.float32)
+        Y = eng.run_layer("blk.0.ffn_down.weight", xb.T).reshape(2, 8)
+        assert rel_l2(Y, oracle.q4k_linear(model["q4"], 8, 512, xb.T.copy())) < 1e-5
         assert eng.memory_usage() > 0
     finally:
         eng.close()
@@ -96,12 +103,15 @@ def test_run_layer_gguf_formats(gpu, model):
     eng = InferenceEngine(model["path"])
     try:
         for name, fmt, R, Cc in GGUF_ENTRIES:
-            x = np.random.default_rng(R).normal(size=(2, Cc)).astype(np.float32)
-            Y = eng.run_layer(name, x).reshape(2, R)
-            ref = oracle.gguf_linear(model["gguf"][name], oracle.GGUF_FORMATS[fmt.lower()], R,
-                                     Cc, x)
-            assert rel_l2(Y, ref) < 1e-5, fmt
-            assert eng.stats()["path"] == "gguf"
+            # M = 1: the GEMV on fp32 x (1e-5); M > 1: the matrix-core form for the whole batch
+            # (fp16 hi + lo parts of x, decoded values rounded to fp16 once: the path's 1e-3)
+            for M, tol in ((1, 1e-5), (3, 1e-3)):
+                x = np.random.default_rng(R + M).normal(size=(M, Cc)).astype(np.float32)
+                Y = eng.run_layer(name, x).reshape(M, R)
+                ref = oracle.gguf_linear(model["gguf"][name], oracle.GGUF_FORMATS[fmt.lower()],
+                                         R, Cc, x)
+                assert rel_l2(Y, ref) < tol, (fmt, M)
+                assert eng.stats()["path"] == "gguf"
     finally:
         eng.close()
 
@@ -241,5 +251,59 @@ def test_generate_text_matches_oracle(gpu, tmp_path):
         assert eng.generate(prompt, 8) == toks                # deterministic, state reset
         with pytest.raises(EngineError):
             eng.generate([1, 2, 300], 2)                      # id beyond the vocabulary
+    finally:
+        eng.close()
+
+
+def test_run_chains_linear_layers(gpu, tmp_path):
+    """cortex_inference_engine_run (SDRInferenceEngine::run -> runLayersOnDemand): the
+    archive's weight segments in getExecutionOrder's order (layer_index first, then names),
+    each output the next input: a strategy-5 layer (no bias, the reference's HSDR stub), an
+    fp32 layer plus its .bias segment, a Q4_K layer; a token embedding is skipped. Checked
+    against the oracle layer by layer; a chain with a mismatched width and one with a non-linear
+    segment are refused."""
+    hs = synth.hsdb_layer(128, 256, 64, 4, seed_dict=5, seed_codes=6)
+    rng = np.random.default_rng(3)
+    dense = (rng.standard_normal((256, 128)) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(256).astype(np.float32)
+    q4e, q4 = q4k_entry("head.weight", 48, 256, 12)
+    q4e.layer_name, q4e.layer_index = "head", 2
+    ents = [
+        q4e,
+        formats.SdrEntry(name="mid.weight", payload=dense.tobytes(), dims=(256, 128),
+                         layer_name="mid", layer_index=1),
+        formats.SdrEntry(name="mid.bias", payload=bias.tobytes(), dims=(256,),
+                         layer_name="mid", layer_index=1),
+        formats.hsdb_entry("first.weight", hs, layer_name="first", layer_index=0),
+        formats.hsdb_entry("token_embd.weight", hs, original_type=13),
+    ]
+    path = str(tmp_path / "chain.sdr")
+    formats.write_sdr(path, ents)
+    eng = InferenceEngine(path)
+    try:
+        for M in (1, 3):
+            x = rng.standard_normal((M, 256)).astype(np.float32)
+            y = eng.run(x).reshape(M, 48)
+            h1 = oracle.hsdb_matmul(hs, x.T.copy()).T
+            h2 = h1 @ dense.T + bias[None, :]
+            ref = oracle.q4k_linear(q4, 48, 256, h2.astype(np.float32))
+            # batches through the matrix-core HSDB product (fp16 weights): the path's 1e-3
+            assert rel_l2(y, ref) < (1e-5 if M == 1 else 1e-3), M
+            st = eng.stats()
+            assert [l["name"] for l in st["layers"]] == ["first", "mid", "head"]
+            assert [l["path"] for l in st["layers"]] == ["hsdb", "dense_f32", "q4_k"]
+        with pytest.raises(EngineError):
+            eng.run(np.ones(100, np.float32))        # not a multiple of the first layer's width
+    finally:
+        eng.close()
+    # a layer-norm vector in the chain is not a linear layer of the device path
+    path2 = str(tmp_path / "chain2.sdr")
+    formats.write_sdr(path2, [formats.hsdb_entry("first.weight", hs, layer_name="first"),
+                              formats.vector_entry("norm.weight", np.ones(128, np.float32))])
+    eng = InferenceEngine(path2)
+    try:
+        with pytest.raises(EngineError) as ei:
+            eng.run(np.ones(256, np.float32))
+        assert ei.value.code == -4
     finally:
         eng.close()

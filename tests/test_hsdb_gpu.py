@@ -203,3 +203,30 @@ def test_shared_dictionary_lifetime(gpu, monkeypatch, share):
     check("c", segs["c"])
     segs["d"].free()
     segs["c"].free()
+
+
+@pytest.mark.parametrize("dtype,shift", [(np.float16, 1), (np.float16, 3), (np.float32, 1),
+                                         (np.float32, 2)])
+def test_gemv_misaligned_x(gpu, dtype, shift):
+    """M = 1 with 64-long blocks and an x that is not 16-byte aligned: the product takes the
+    general dx kernel (the matrix-core one loads x as 16-byte pieces), with the same result."""
+    torch = gpu
+    R, Cc, K, s = 1024, 4096, 1024, 8
+    stream = layer(R, Cc, K, s)
+    x = synth.activations(Cc, 1, seed=9, dtype=dtype)
+    buf = torch.zeros(Cc + 8, dtype=torch.float16 if dtype == np.float16 else torch.float32,
+                      device="cuda")
+    xd = buf[shift:shift + Cc].view(Cc, 1)
+    xd.copy_(torch.from_numpy(np.ascontiguousarray(x)))
+    assert xd.data_ptr() % 16 != 0
+    seg = seg_of(stream)
+    try:
+        y = seg.matmul(xd).cpu().numpy()
+        ref = oracle.hsdb_matmul(stream, x.astype(np.float32))
+        assert rel_l2(y, ref) <= 1e-5
+        # the aligned product agrees
+        xa = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        ya = seg.matmul(xa).cpu().numpy()
+        assert rel_l2(y, ya) <= 1e-6
+    finally:
+        seg.free()

@@ -57,6 +57,26 @@ def test_noalloc_matches_workspace_entry_point(gpu, first, second):
         seg.free()
 
 
+def test_noalloc_sizes_scratch_for_the_path_taken(gpu):
+    """cfg2's 4096 x 11008 at M = 16 takes the matrix-core path (under 1 MB of transposed X);
+    the P path's 11 MB at that M, over the 8 MiB scratch, is not what it needs. Then a smaller
+    product at M = 12 on the same scratch."""
+    torch = gpu
+    for i, (R, C_, K, s, M) in enumerate(((4096, 11008, 1024, 8, 16), (1024, 4096, 512, 8, 12))):
+        seg, x = _case(torch, R, C_, K, s, M, True, seed=61 + 10 * i)
+        if i == 0:
+            # the caller-workspace size covers every path at this M (the P path's 11 MB)
+            assert seg.workspace_bytes(M) > SCRATCH_BYTES
+        want = seg.matmul(x).cpu().numpy()
+        rc, y = _noalloc(torch, seg, x, CSDR_F16, M)
+        torch.cuda.synchronize()
+        assert rc == 0
+        got = y.cpu().numpy()
+        assert np.isfinite(got).all()
+        assert rel_l2(got, want) <= 1e-5, (i, rel_l2(got, want))
+        seg.free()
+
+
 def test_noalloc_rejects_products_beyond_its_scratch(gpu):
     from cortexsdr_amd import _lib
 
