@@ -135,7 +135,11 @@ def test_run_layer_errors(gpu, model):
         from cortexsdr_amd import _lib
         n = C.c_size_t()
         err = _lib.load().cortex_inference_engine_run(eng._h, None, 0, None, 0, C.byref(n))
-        assert err.code == -4
+        assert err.code == -1                                # null pointers (cortex_sdk.cpp:1860)
+        # this archive's segments do not chain (widths differ from layer to layer)
+        with pytest.raises(EngineError) as e:
+            eng.run(np.zeros(256, np.float32))
+        assert e.value.code in (-4, -7)
     finally:
         eng.close()
     with pytest.raises(EngineError):
