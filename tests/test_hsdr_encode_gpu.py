@@ -133,7 +133,9 @@ def test_compress_refined_matches_reference(gpu, enc):
     sums (the tile-norm mean under OpenMP, a vectorised re-seed norm) and, on another CPU
     model, the initial dictionary end in different last bits; the bars are: codes equal in
     >= 99% of slots, the dictionary within 1e-4 of its magnitude, the reconstruction error
-    within 0.1% of the reference's."""
+    within 0.1% of the reference's. The codes the reference writes are matching pursuit over
+    its own refined dictionary, so on any CPU the GPU's matching pursuit over that dictionary
+    must give them bit for bit."""
     from cortexsdr_amd import encode
 
     n = len([k for k in enc.files if k.startswith("fit_") and k.endswith("_stream")])
@@ -151,6 +153,8 @@ def test_compress_refined_matches_reference(gpu, enc):
         em = np.linalg.norm(oracle.hsdr_decompress(s) - w)
         er = np.linalg.norm(oracle.hsdr_decompress(ref) - w)
         assert abs(em - er) <= 1e-3 * er, f"case {i}"
+        t = tiles_of(w, rv.tile_rows, rv.tile_cols)
+        assert np.array_equal(gpu_codes(gpu, t, rD, rg, S, k), rcodes), f"case {i}"
 
 
 def test_compress_rejects(gpu):
