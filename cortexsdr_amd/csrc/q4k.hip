@@ -18,12 +18,14 @@
 //     16 blocks, and a wave keeps up to 2 steps in flight. x is staged once per workgroup in a
 //     lane-major LDS layout with the sub-block sums of x. Per group:
 //     y += d*sc*(sum q*x) - dmin*m*(sum x), the products exact and summed in fp32.
-//   q4k_mm_kernel (M > 1): 8 waves own 128 rows and a range of super-blocks (split K). Per
-//     super-block a lane forms q * sc for 8 values of each sub-block of its row as exact fp16
-//     subnormals, and v_mfma_f32_16x16x32_f16 multiplies them with fp16 X (staged in LDS in
-//     the matching k order) into an fp32 tile scaled by d per super-block; the dmin * m term
-//     is a second small product with the sub-block sums of X. No rounding of W: the product
-//     is within about 1e-6 (relative L2) of fp32. Workgroups of one row range add into Y.
+//   q4k_mm_kernel (M > 1): 8 waves own 32 rows, up to 64 columns and a range of
+//     super-blocks (split K in at most 8 parts, each on its own XCDs). Wave w takes quant
+//     group w % 4 of every other super-block; per super-block a lane forms q * sc for 8 values
+//     of each of its two sub-blocks as exact fp16 subnormals, and v_mfma_f32_16x16x32_f16
+//     multiplies them with fp16 X (loaded straight into the A operands in the matching k
+//     order) into an fp32 tile scaled by d; the dmin * m term is a second small product with
+//     the sub-block sums of X. No rounding of W: the product is within about 1e-6 (relative
+//     L2) of fp32. The waves' tiles meet in LDS and each output is written once per split.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -397,222 +399,245 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__
 
 // ---------------------------------------------------------------- M > 1, exact quants
 //
-// A workgroup of 8 waves owns 128 rows (a 16-row tile per wave), the range of super-blocks
-// blockIdx.y covers (split K) and 16 NT columns. Per super-block every wave multiplies its
-// tile on v_mfma_f32_16x16x32_f16 with W as the B operand (k x rows) and X as A (columns x k),
-// so each output element a lane holds belongs to the lane's own W row:
-//   * a lane (row rl = l % 16, k-slice j = l / 16) takes the 8 values 8j .. 8j + 7 of each
-//     32-element sub-block s of its row; q * sc (at most 15 * 63 = 945) is formed as a pair of
-//     16-bit integers with one v_pk_mul_lo_u16 and read as two fp16 subnormals q * sc * 2^-24,
-//     exact, so the 8 sub-blocks of a super-block accumulate in one fp32 D tile;
-//   * the min term sum_s m_s * (sum of x over s) is one more product, of the sub-block sums
-//     of X (split into fp16 hi + lo parts, two steps) with m_s (6-bit, exact in fp16);
-//   * per super-block: acc += (d * 2^24) * D - dmin * Dm in fp32.
-// The k order inside a lane's 8 values follows how a quant dword splits into value pairs; X
-// is staged in LDS in the same order, one super-block ahead (two buffers), with the
-// sub-block sums. Workgroups of one row range add their partial sums into Y (zeroed first).
+// A workgroup of 8 waves owns 64 rows (four 16-row tiles), 16 NT columns and a range of
+// super-blocks (split K in S parts, S in {1, 2, 4, 8}). Wave w takes row tile w / 2 and half
+// w % 2 of every super-block (sub-blocks 4h .. 4h + 3) and multiplies on
+// v_mfma_f32_16x16x32_f16 with W as the B operand (k x rows) and X as A (columns x k), so each
+// output element a lane holds belongs to the lane's own W row:
+//   * a lane (row rl = l % 16, k-slice j = l / 16) takes the 8 values 8j .. 8j + 7 of each of
+//     its sub-blocks in element order: the nibbles are split with two masks and paired with
+//     v_perm_b32, and q * sc (at most 15 * 63 = 945) is formed as a pair of 16-bit integers
+//     with one v_pk_mul_lo_u16 and read as two fp16 subnormals q * sc * 2^-24, exact;
+//   * the min term sum_s m_s * (sum of x over s) is a second product with m_s (6-bit) in every
+//     k position, also as subnormals m_s * 2^-24, so no sums of X are formed;
+//   * per super-block: acc += (d * 2^24) * D - (dmin * 2^24) * Dm in fp32.
+// X moves through LDS in memory order (plain 16-byte copies into tiles laid out as the A
+// operands are read), in a ring of two buffers fed from kMmXR register sets, so each copy has
+// kMmXR super-blocks' time to land; W runs kMmWD super-blocks ahead in registers. One barrier
+// per super-block. The halves' tiles meet in LDS at the end and each output is written once per
+// split: stored when S = 1, else added into Y (zeroed first).
+//
+// Placement: workgroup i runs on XCD i % 8. Split h of every row tile goes to the XCDs with
+// xcd % S == h, so an XCD fetches 1/S of X into its L2.
 constexpr int kMmWaves = 8;
 constexpr int kMmThreads = 64 * kMmWaves;
-constexpr int kMmRows = 16 * kMmWaves;
+constexpr int kMmRows = 64;
+// W super-blocks in flight per wave and X super-blocks per thread (register sets). Measured at
+// 4096 x 14336, M = 32 (us): 24.4 here, 25.8 with 4 X sets, 26.5 with 6, 27.0 with 4 W; the
+// split count the same way: 39.3 with S = 2, 30.4 with S = 8 against S = 4 here.
+constexpr int kMmWD = 2;
+constexpr int kMmXR = 2;
+constexpr int kMmUnroll = 2;  // a multiple of 2 (buffers), kMmWD and kMmXR
+
+// q4k_mm_kernel's placement: nrt row tiles (padded to nrt_p, a multiple of 8 / S), S splits of
+// KB super-blocks, column groups of 16 NT outer
+struct MmGrid {
+    int nrt, nrt_p, S, KB;
+};
+
+// LDS bytes of one X buffer: NT column tiles x 8 sub-blocks x 64 lanes x 16 bytes
+template <int NT>
+constexpr int mm_xbuf_bytes() {
+    return NT * 8 * 64 * 16;
+}
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// 16-byte LDS chunks of one super-block buffer: per column tile 8 X tiles and 2 sum tiles
-template <int NT>
-constexpr int mm_buf_chunks() {
-    return NT * 10 * 64;
+// four (value, value) nibble pairs p0..p3 (values at bits 0-3 and 16-19) times the sub-block
+// scale: 8 fp16 subnormals q * sc * 2^-24
+__device__ __forceinline__ half8 mm_scale(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3,
+                                          uint32_t sc2) {
+    const u16x2 s = __builtin_bit_cast(u16x2, sc2);
+    const u32x4 v = {__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p0) * s),
+                     __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p1) * s),
+                     __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p2) * s),
+                     __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p3) * s)};
+    return __builtin_bit_cast(half8, v);
 }
 
-// x values e0..e7 (dwords d = (e0,e1) (e2,e3) (e4,e5) (e6,e7)) in the order the quant pairs
-// take them: ggml (e0,e2) (e1,e3) (e4,e6) (e5,e7), interleaved (e0,e4) (e1,e5) (e2,e6) (e3,e7)
-template <int ORDER>
-__device__ __forceinline__ u32x4 mm_x_order(const u32x4& d) {
-    u32x4 o;
-    if (ORDER == 0) {
-        o.x = __builtin_amdgcn_perm(d.y, d.x, 0x05040100u);
-        o.y = __builtin_amdgcn_perm(d.y, d.x, 0x07060302u);
-        o.z = __builtin_amdgcn_perm(d.w, d.z, 0x05040100u);
-        o.w = __builtin_amdgcn_perm(d.w, d.z, 0x07060302u);
+// the 4 scales and 4 mins of sub-blocks 4h .. 4h + 3 (h uniform across the wave), one per
+// byte, from the 12 scale bytes (header words y, z, w), as scale_min unpacks them one at a time
+__device__ __forceinline__ void scale_min_quad(const u32x4& hdr, int h, uint32_t& sc4,
+                                               uint32_t& mn4) {
+    if (h == 0) {
+        sc4 = hdr.y & 0x3F3F3F3Fu;
+        mn4 = hdr.z & 0x3F3F3F3Fu;
     } else {
-        o.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
-        o.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
-        o.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
-        o.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+        sc4 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+        mn4 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
     }
-    return o;
-}
-
-// one nibble pair (bits 0-3 and 16-19 of v) times the sub-block scale, as two fp16 subnormals
-__device__ __forceinline__ uint32_t mm_qs(uint32_t v, uint32_t sc2) {
-    const u16x2 q = __builtin_bit_cast(u16x2, v & 0x000F000Fu);
-    return __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(u16x2, sc2));
 }
 
 template <int ORDER, int NT>
 __global__ __launch_bounds__(kMmThreads) void q4k_mm_kernel(const uint8_t* __restrict__ W, int R,
                                                             int nblk, const _Float16* __restrict__ X,
-                                                            int M, float* __restrict__ Y, int KB) {
+                                                            int M, float* __restrict__ Y, MmGrid g) {
     extern __shared__ __attribute__((aligned(16))) unsigned char mm_smem[];
-    u32x4* xl = reinterpret_cast<u32x4*>(mm_smem);  // [2][mm_buf_chunks<NT>()]
-    constexpr int kBuf = mm_buf_chunks<NT>();
+    u32x4* xl = reinterpret_cast<u32x4*>(mm_smem);  // [2 buffers][NT * 8 tiles][64 lanes]
+    constexpr int kBuf = NT * 8 * 64;               // u32x4 per buffer
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int rt = wave >> 1, half = wave & 1;
     const int rl = lane & 15, j = lane >> 4;
-    const int r0 = blockIdx.x * kMmRows + wave * 16;
-    const int b0 = blockIdx.y * KB, b1 = min(nblk, b0 + KB);
-    const int n0 = blockIdx.z * 16 * NT;
+    // the workgroup's tile from its number (number % 8 is the XCD it runs on)
+    const int per_z = g.nrt_p * g.S;
+    const int z = (int)blockIdx.x / per_z, rest = (int)blockIdx.x - z * per_z;
+    const int xcd = rest & 7;
+    const int sp = xcd % g.S;
+    const int t = (rest >> 3) * (8 / g.S) + xcd / g.S;
+    const int b0 = sp * g.KB, b1 = min(nblk, b0 + g.KB);
+    if (t >= g.nrt || b0 >= b1) return;  // padding or an empty split (the whole workgroup)
+    const int nb = b1 - b0;
+    const int r0 = t * kMmRows, n0 = z * 16 * NT;
     const int C = nblk * 256;
-    // the sum tiles hold values at k < 8 only (lanes 0-15): zero the rest once
-    for (int i = threadIdx.x; i < 2 * NT * 2 * 48; i += kMmThreads) {
-        const int l = 16 + i % 48, t = i / 48;  // t: buffer * 2 NT + nt * 2 + hi/lo
-        const int buf = t / (2 * NT), nt = (t / 2) % NT, hl = t & 1;
-        xl[buf * kBuf + (nt * 10 + 8 + hl) * 64 + l] = u32x4{0u, 0u, 0u, 0u};
+    const uint8_t* wrow = W + (size_t)min(r0 + 16 * rt + rl, R - 1) * nblk * kBlockBytes;
+    // X staging: pieces q = i * kMmThreads + tid, i < NT: tile q / 64 = (column tile, sub-block),
+    // lane q % 64 = (column c, k-slice j); 16 bytes each
+    const _Float16* xsrc[NT];
+    bool xlive[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int q = i * kMmThreads + (int)threadIdx.x;
+        const int tile = q >> 6, ln = q & 63;
+        const int n = n0 + 16 * (tile >> 3) + (ln & 15);
+        xlive[i] = n < M;
+        xsrc[i] = X + (size_t)min(n, M - 1) * C + 32 * (tile & 7) + 8 * (ln >> 4);
     }
-    // X staging: piece p = (column, sub-block, k-slice), 16 NT * 32 per super-block, NT per
-    // thread
-    auto stage_load = [&](int b, u32x4 (&xr)[NT]) {
+    auto xload = [&](int k, u32x4 (&xr)[NT]) {
+        const int b = b0 + min(k, nb - 1);
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const int p = i * kMmThreads + threadIdx.x;
-            const int col = n0 + (p >> 5), s = (p >> 2) & 7, jj = p & 3;
-            const u32x4 v = *reinterpret_cast<const u32x4*>(X + (size_t)min(col, M - 1) * C +
-                                                            (size_t)b * 256 + 32 * s + 8 * jj);
-            xr[i] = col < M ? v : u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int i = 0; i < NT; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + (size_t)b * 256);
     };
-    auto stage_store = [&](int buf, const u32x4 (&xr)[NT]) {
+    auto xstore = [&](int buf, const u32x4 (&xr)[NT]) {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const int p = i * kMmThreads + threadIdx.x;
-            const int c = p >> 5, s = (p >> 2) & 7, jj = p & 3;
-            const int nt = c >> 4, l = (c & 15) + 16 * jj;
-            xl[buf * kBuf + (nt * 10 + s) * 64 + l] = mm_x_order<ORDER>(xr[i]);
-            // the sub-block sum of this column: 4 neighbouring threads hold its 4 slices
-            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-            const h8 v = __builtin_bit_cast(h8, xr[i]);
-            float sm = (((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3])) +
-                       (((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]));
-            sm += __shfl_xor(sm, 1);
-            sm += __shfl_xor(sm, 2);
-            if (jj == 0) {
-                const _Float16 hi = (_Float16)sm;
-                const _Float16 lo = (_Float16)(sm - (float)hi);
-                _Float16* th = reinterpret_cast<_Float16*>(xl + buf * kBuf + (nt * 10 + 8) * 64);
-                _Float16* tl = reinterpret_cast<_Float16*>(xl + buf * kBuf + (nt * 10 + 9) * 64);
-                th[(c & 15) * 8 + s] = hi;
-                tl[(c & 15) * 8 + s] = lo;
-            }
-        }
+        for (int i = 0; i < NT; ++i) xl[buf * kBuf + i * kMmThreads + threadIdx.x] = xlive[i] ? xr[i] : zero;
     };
-    // this lane's bytes of a super-block of its row: header, and per sub-block pair (ggml) or
-    // sub-block (interleaved) the 8 or 4 bytes of its k-slice
-    struct Blk {
+    // a super-block's W for this lane: the header and the quant bytes of its 4 sub-blocks
+    struct Wq {
         u32x4 hdr;
-        uint32_t q[8];
+        uint32_t q[4];
     };
-    const uint8_t* wrow = W + (size_t)min(r0 + rl, R - 1) * nblk * kBlockBytes;
-    auto load_blk = [&](int b, Blk& o) {
-        const uint8_t* bp = wrow + (size_t)b * kBlockBytes;
+    auto wload = [&](int k, Wq& o) {
+        const uint8_t* bp = wrow + (size_t)(b0 + min(k, nb - 1)) * kBlockBytes;
         o.hdr = *reinterpret_cast<const u32x4*>(bp);
         if (ORDER == 0) {
+            // groups 2h, 2h + 1: bytes 8j .. 8j + 7 of each (low nibbles: sub-block 2g, high: 2g+1)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const uint2 v = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * j);
-                o.q[2 * g] = v.x;
-                o.q[2 * g + 1] = v.y;
+            for (int gi = 0; gi < 2; ++gi) {
+                const uint2 v = *reinterpret_cast<const uint2*>(bp + 16 + 32 * (2 * half + gi) + 8 * j);
+                o.q[2 * gi] = v.x;
+                o.q[2 * gi + 1] = v.y;
             }
         } else {
+            // sub-blocks 4h .. 4h + 3: bytes 4j .. 4j + 3 of each (two values per byte)
 #pragma unroll
-            for (int s = 0; s < 8; ++s)
-                o.q[s] = *reinterpret_cast<const uint32_t*>(bp + 16 + 16 * s + 4 * j);
+            for (int u = 0; u < 4; ++u)
+                o.q[u] = *reinterpret_cast<const uint32_t*>(bp + 16 + 16 * (4 * half + u) + 4 * j);
         }
     };
     floatx4 acc[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](int buf, const Blk& cb) {
-        // B operands: q * sc per sub-block, and m at k = s for the min product
-        half8 bq[8];
-        float scf[8], mnf[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) scale_min(cb.hdr, s, scf[s], mnf[s]);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const uint32_t sc = (uint32_t)scf[s], sc2 = sc | (sc << 16);
-            uint32_t w0, w1;  // this lane's 8 (ggml) or 4 (interleaved) bytes of sub-block s
-            if (ORDER == 0) {
-                const int sh = (s & 1) * 4;  // odd sub-blocks: high nibbles
-                w0 = cb.q[2 * (s >> 1)] >> sh;
-                w1 = cb.q[2 * (s >> 1) + 1] >> sh;
-                bq[s] = __builtin_bit_cast(
-                    half8, u32x4{mm_qs(w0, sc2), mm_qs(w0 >> 8, sc2), mm_qs(w1, sc2),
-                                 mm_qs(w1 >> 8, sc2)});
-            } else {
-                w0 = cb.q[s];
-                bq[s] = __builtin_bit_cast(
-                    half8, u32x4{mm_qs(w0, sc2), mm_qs(w0 >> 4, sc2), mm_qs(w0 >> 8, sc2),
-                                 mm_qs(w0 >> 12, sc2)});
-            }
-        }
-        half8 bm;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) bm[s] = j == 0 ? (_Float16)mnf[s] : (_Float16)0.0f;
-        const float d24 = hdr_d(cb.hdr) * 16777216.0f, dm = hdr_dmin(cb.hdr);
-        const u32x4* xb = xl + buf * kBuf + lane;
+    auto compute = [&](int buf, const Wq& w) {
+        uint32_t sc4, mn4;
+        scale_min_quad(w.hdr, half, sc4, mn4);
+        floatx4 D[NT], Dm[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            floatx4 D = {0.f, 0.f, 0.f, 0.f}, Dm = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const half8 a = __builtin_bit_cast(half8, xb[(nt * 10 + s) * 64]);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[s], D, 0, 0, 0);
-            }
-            const half8 ah = __builtin_bit_cast(half8, xb[(nt * 10 + 8) * 64]);
-            const half8 al = __builtin_bit_cast(half8, xb[(nt * 10 + 9) * 64]);
-            Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bm, Dm, 0, 0, 0);
-            Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bm, Dm, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[nt][i] += d24 * D[i] - dm * Dm[i];
+            D[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            Dm[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // sub-block 4h + u: the scale and min of byte u in both 16-bit lanes
+            const uint32_t sel = 0x0c000c00u + 0x00010001u * (uint32_t)u;
+            const uint32_t sc2 = __builtin_amdgcn_perm(sc4, sc4, sel);
+            const uint32_t m2 = __builtin_amdgcn_perm(mn4, mn4, sel);
+            half8 bq;
+            if (ORDER == 0) {
+                // group 2h + u / 2, nibble u % 2 of its 8 bytes
+                const int sh = 4 * (u & 1);
+                const uint32_t ta = (w.q[2 * (u >> 1)] >> sh) & 0x0F0F0F0Fu;
+                const uint32_t tb = (w.q[2 * (u >> 1) + 1] >> sh) & 0x0F0F0F0Fu;
+                bq = mm_scale(__builtin_amdgcn_perm(ta, ta, 0x0c010c00u),
+                              __builtin_amdgcn_perm(ta, ta, 0x0c030c02u),
+                              __builtin_amdgcn_perm(tb, tb, 0x0c010c00u),
+                              __builtin_amdgcn_perm(tb, tb, 0x0c030c02u), sc2);
+            } else {
+                // value 2i: low nibble of byte i; 2i + 1: its high nibble
+                const uint32_t lo = w.q[u] & 0x0F0F0F0Fu, hi = (w.q[u] >> 4) & 0x0F0F0F0Fu;
+                bq = mm_scale(__builtin_amdgcn_perm(hi, lo, 0x0c040c00u),
+                              __builtin_amdgcn_perm(hi, lo, 0x0c050c01u),
+                              __builtin_amdgcn_perm(hi, lo, 0x0c060c02u),
+                              __builtin_amdgcn_perm(hi, lo, 0x0c070c03u), sc2);
+            }
+            const half8 bm = __builtin_bit_cast(half8, u32x4{m2, m2, m2, m2});
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const half8 a = __builtin_bit_cast(half8, xl[buf * kBuf + (nt * 8 + 4 * half + u) * 64 + lane]);
+                D[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, D[nt], 0, 0, 0);
+                Dm[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bm, Dm[nt], 0, 0, 0);
+            }
+        }
+        const float d24 = hdr_d(w.hdr) * 16777216.0f, dm24 = hdr_dmin(w.hdr) * 16777216.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nt][i] += d24 * D[nt][i] - dm24 * Dm[nt][i];
     };
-    // the range's super-blocks, two at a time (named buffers keep both in registers); X and
-    // W of the next super-block are loaded while this one is multiplied
-    Blk ba, bb;
-    u32x4 xa[NT], xb2[NT];
-    if (b0 < b1) {
-        stage_load(b0, xa);
-        load_blk(b0, ba);
-        stage_store(0, xa);
+    // prologue: X of super-blocks 0 .. kMmXR - 1 in the register sets, 0 stored into buffer 0
+    // and kMmXR loaded in its place; W 0 .. kMmWD - 1 (every load is issued, past the end as a
+    // repeat of the last super-block, so that the compiler's wait counts stay exact)
+    u32x4 xr[kMmXR][NT];
+    Wq wr[kMmWD];
+#pragma unroll
+    for (int s = 0; s < kMmXR; ++s) xload(s, xr[s]);
+#pragma unroll
+    for (int k = 0; k < kMmWD; ++k) wload(k, wr[k]);
+    xstore(0, xr[0]);
+    xload(kMmXR, xr[0]);
+    __syncthreads();
+    // iteration k: multiply super-block k from buffer k % 2; store X(k + 1) from its register
+    // set into the other buffer (last read in iteration k - 1, before its barrier) and load
+    // X(k + 1 + kMmXR) into that set, so every X load has kMmXR iterations to land
+    static_assert(kMmUnroll % 2 == 0 && kMmUnroll % kMmWD == 0 && kMmUnroll % kMmXR == 0, "");
+    for (int k0 = 0; k0 < nb; k0 += kMmUnroll) {
+#pragma unroll
+        for (int u = 0; u < kMmUnroll; ++u) {
+            const int k = k0 + u;
+            if (k >= nb) break;
+            compute(u & 1, wr[u % kMmWD]);
+            wload(k + kMmWD, wr[u % kMmWD]);
+            xstore((u + 1) & 1, xr[(u + 1) % kMmXR]);
+            xload(k + 1 + kMmXR, xr[(u + 1) % kMmXR]);
+            __syncthreads();
+        }
+    }
+    // the halves' tiles: half 1 parks its tile in LDS (after the last barrier no wave reads X),
+    // half 0 adds it and writes the outputs; lane (rl, j) holds row rl, columns 4j .. 4j + 3
+    floatx4* red = reinterpret_cast<floatx4*>(mm_smem);  // [4 row tiles][NT][64 lanes]
+    if (half == 1) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) red[(rt * NT + nt) * 64 + lane] = acc[nt];
     }
     __syncthreads();
-    for (int b = b0; b < b1; b += 2) {
-        if (b + 1 < b1) {
-            stage_load(b + 1, xb2);
-            load_blk(b + 1, bb);
-        }
-        compute(0, ba);
-        if (b + 1 < b1) stage_store(1, xb2);
-        __syncthreads();
-        if (b + 1 >= b1) break;
-        if (b + 2 < b1) {
-            stage_load(b + 2, xa);
-            load_blk(b + 2, ba);
-        }
-        compute(1, bb);
-        if (b + 2 < b1) stage_store(0, xa);
-        __syncthreads();
-    }
-    // D tile: this lane holds columns 4 j + i of its row rl
+    if (half == 0) {
+        const int row = r0 + 16 * rt + rl;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int r = r0 + rl;
-        if (r >= R) continue;
+        for (int nt = 0; nt < NT; ++nt) {
+            const floatx4 v = acc[nt] + red[(rt * NT + nt) * 64 + lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int n = n0 + nt * 16 + 4 * j + i;
-            if (n < M)
-                __hip_atomic_fetch_add(Y + (size_t)n * R + r, acc[nt][i], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 4; ++i) {
+                const int col = n0 + 16 * nt + 4 * j + i;
+                if (row < R && col < M) {
+                    float* yp = Y + (size_t)col * R + row;
+                    if (g.S == 1)
+                        *yp = v[i];
+                    else
+                        __hip_atomic_fetch_add(yp, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
         }
     }
 }
@@ -711,31 +736,40 @@ CSDR_API int csdr_q4k_linear(const void* w, int R, int C, int order, const void*
             return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: M > 1 takes fp16 x");
         if (reinterpret_cast<uintptr_t>(x) % 16 || C % 8)
             return set_error(CSDR_E_INVALID, "q4k_linear: x must be 16-byte aligned");
-        // Y = 0, then the split-K tiles add into it
-        const size_t ny = (size_t)M * R;
-        fill_zero_kernel<<<(unsigned)std::min<size_t>((ny + kThreads - 1) / kThreads, 4096),
-                           kThreads, 0, st>>>(y, ny);
-        // 128-row workgroups, 16 NT columns each, and the super-blocks split so that the grid
-        // holds about 256 workgroups
+        // 64-row tiles of up to 64 columns; the super-blocks split in S parts (S a power of
+        // two up to 8) so that the grid holds at least 256 workgroups where the row tiles
+        // alone do not
         const int NT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-        const int gx = (R + kMmRows - 1) / kMmRows, gz = (M + 16 * NT - 1) / (16 * NT);
-        const int pk = std::max(1, std::min(nblk, (256 + gx * gz - 1) / (gx * gz)));
-        const int KB = (nblk + pk - 1) / pk;
-        dim3 grid(gx, (nblk + KB - 1) / KB, gz);
-        const size_t lds = (size_t)2 * 10 * 64 * 16 * NT;
+        const int gz = (M + 16 * NT - 1) / (16 * NT);
+        MmGrid g;
+        g.nrt = (R + kMmRows - 1) / kMmRows;
+        g.S = 1;
+        while (g.S < 8 && g.S < nblk && (long long)g.nrt * g.S * gz < 256) g.S *= 2;
+        g.KB = (nblk + g.S - 1) / g.S;
+        const int pad = 8 / g.S;
+        g.nrt_p = (g.nrt + pad - 1) / pad * pad;
+        const long long nwg = (long long)g.nrt_p * g.S * gz;
+        if (nwg > 0x7fffffffLL)
+            return set_error(CSDR_E_UNSUPPORTED, "q4k_linear: too many output tiles");
+        if (g.S > 1) {
+            // Y = 0, then the splits add into it
+            const size_t ny = (size_t)M * R;
+            fill_zero_kernel<<<(unsigned)std::min<size_t>((ny + kThreads - 1) / kThreads, 4096),
+                               kThreads, 0, st>>>(y, ny);
+        }
         const auto* wp = static_cast<const uint8_t*>(w);
         const auto* xp = static_cast<const _Float16*>(x);
-        auto go = [&](auto kern) {
+        auto go = [&](auto kern, size_t lds) {
             if (lds > 64 * 1024)
                 (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            kern<<<grid, kMmThreads, lds, st>>>(wp, R, nblk, xp, M, y, KB);
+            kern<<<(unsigned)nwg, kMmThreads, lds, st>>>(wp, R, nblk, xp, M, y, g);
         };
         auto pick = [&](auto ord) {
             constexpr int O = decltype(ord)::value;
-            if (NT == 1) go(q4k_mm_kernel<O, 1>);
-            else if (NT == 2) go(q4k_mm_kernel<O, 2>);
-            else go(q4k_mm_kernel<O, 4>);
+            if (NT == 1) go(q4k_mm_kernel<O, 1>, 2 * mm_xbuf_bytes<1>());
+            else if (NT == 2) go(q4k_mm_kernel<O, 2>, 2 * mm_xbuf_bytes<2>());
+            else go(q4k_mm_kernel<O, 4>, 2 * mm_xbuf_bytes<4>());
         };
         if (order == CSDR_Q4K_GGML) pick(std::integral_constant<int, 0>{});
         else pick(std::integral_constant<int, 1>{});

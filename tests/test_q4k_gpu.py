@@ -50,6 +50,9 @@ def test_dequant_bitexact(gpu, order):
     (64, 18432, 1, "ggml", np.float16),       # two x staging batches, partial last wave step
     (96, 18432, 1, "interleaved", np.float32),  # fp32 x: more than 64 KiB of LDS
     (40, 4352, 1, "ggml", np.float32),        # 17 super-blocks: one block in the last step
+    (8200, 512, 32, "interleaved", np.float16),  # 257 row tiles: one split, plain stores
+    (37, 1280, 3, "ggml", np.float16),        # 5 super-blocks in 8 splits (three empty)
+    (1000, 2816, 17, "ggml", np.float16),     # 11 super-blocks in 8 splits of 2; one live column
 ])
 def test_linear(gpu, R, C, M, order, xdt):
     from cortexsdr_amd import q4k
