@@ -29,7 +29,9 @@
 //     then per 32-wide k step each lane decodes 8 consecutive values of its row (Dec8), rounds
 //     them to fp16 once and issues one v_mfma_f32_16x16x32_f16 per 16 output columns (fp32
 //     accumulate; the single rounding of W puts the product ~3e-4 relative L2 from fp32). The
-//     waves' tiles meet in LDS; workgroups of one row tile add into Y (zeroed first).
+//     waves' tiles meet in LDS and each split adds every output into Y (zeroed first) once,
+//     16 neighbouring rows per 16 neighbouring threads; the splits of a row tile run on
+//     different XCDs, each XCD fetching its share of X.
 //   gguf_dequant_kernel: one thread per element.
 #include <hip/hip_runtime.h>
 
@@ -355,24 +357,40 @@ struct Dec8W<Packed<BB_, BE_, BITS>> {  // (q - 2^(BITS-1)) * d = fma(q, d, -2^(
     }
 };
 
+// gguf_mm_kernel's placement: nrt row tiles (padded to nrt_p, a multiple of 8 / S), S splits of
+// KB 256-element steps, column groups outer. Workgroup i runs on XCD i % 8, and split h of
+// every row tile goes to the XCDs with xcd % S == h, so an XCD fetches 1/S of X into its L2.
+struct MmGrid {
+    int nrt, nrt_p, S, KB;
+};
+
 // Two waves per SIMD: the decode and the step prefetch want registers more than occupancy
 // (measured at M = 32 against the default budget: q6_k 4096 x 14336 52.8 -> 42.5 us).
 template <class F, int NT, int RT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gguf_mm_kernel(const uint8_t* __restrict__ W, int R,
                                                            int C, const _Float16* __restrict__ X,
-                                                           int M, float* __restrict__ Y, int KS) {
+                                                           int M, float* __restrict__ Y, MmGrid gr) {
     typedef _Float16 half8 __attribute__((ext_vector_type(8)));
     constexpr int ND = Step<F>::kDwords;
     constexpr int ROWS = 16 * RT;
     constexpr int NW = kThreads / 64;
-    __shared__ uint32_t stage[NW][ROWS * ND + 1];  // + 1: Dec8W's dword pairs end inside
-    __shared__ floatx4 red[NW - 1][RT][NT][64];
+    // the waves' stages (+ 1: Dec8W's dword pairs end inside); after the steps, the waves'
+    // tiles for the reduction
+    constexpr int kStage = ROWS * ND + 1;
+    constexpr int kRed = NW * RT * NT * 64 * 4;
+    __shared__ __attribute__((aligned(16))) uint32_t smem[NW * kStage > kRed ? NW * kStage : kRed];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, j = lane >> 4;
-    const int r0 = blockIdx.x * ROWS;
+    // the workgroup's tile from its number (number % 8 is the XCD it runs on)
+    const int per_z = gr.nrt_p * gr.S;
+    const int z = (int)blockIdx.x / per_z, rest = (int)blockIdx.x - z * per_z;
+    const int xcd = rest & 7;
+    const int t = (rest >> 3) * (8 / gr.S) + xcd / gr.S;
     const int nsteps = (C + 255) / 256;
-    const int s0 = blockIdx.y * KS, s1 = min(nsteps, s0 + KS);
-    const int n0 = blockIdx.z * 16 * NT;
+    const int s0 = (xcd % gr.S) * gr.KB, s1 = min(nsteps, s0 + gr.KB);
+    if (t >= gr.nrt || s0 >= s1) return;  // padding or an empty split (the whole workgroup)
+    const int r0 = t * ROWS;
+    const int n0 = z * 16 * NT;
     const size_t rowbytes = (size_t)(C / F::BE) * F::BB;
     const size_t total = (size_t)R * rowbytes;
     floatx4 acc[RT][NT];
@@ -388,7 +406,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         xl[nt] = n < M;
         xr[nt] = X + (size_t)min(n, M - 1) * C + 8 * j;
     }
-    uint32_t* sw = stage[wave];
+    uint32_t* sw = smem + wave * kStage;
     // A step's staging: the wave's rows' bytes of the step, ROWS x ND dwords (row rr's bytes
     // start at byte (its start & 3) of its slot), PF per lane, loaded into registers one step
     // ahead of its use; the loads stay inside W (the last dword byte by byte).
@@ -472,33 +490,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
-    // the 4 waves' tiles: waves 1..3 park theirs in LDS, wave 0 sums and adds into Y
-    if (wave > 0) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) red[wave - 1][rt][nt][lane] = acc[rt][nt];
-    }
+    // the 4 waves' tiles meet in LDS (once every wave is past its steps) and the workgroup
+    // adds each output into Y once: output (row r, column c) of a tile is element r % 4 of lane
+    // c + 16 (r / 4), and 16 neighbouring threads take 16 neighbouring rows (one 64-byte run of
+    // Y per 16 atomics, where a lane's own 16 columns were 16 lines)
     __syncthreads();
-    if (wave == 0) {
+    floatx4* red = reinterpret_cast<floatx4*>(smem);  // [wave][RT][NT][64]
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                floatx4 v = acc[rt][nt];
+        for (int nt = 0; nt < NT; ++nt) red[((wave * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
+    __syncthreads();
+    const float* redf = reinterpret_cast<const float*>(smem);
+    for (int o = threadIdx.x; o < RT * NT * 256; o += kThreads) {
+        const int r = o & 15, c = (o >> 4) & 15, tile = o >> 8;  // tile = rt * NT + nt
+        const int at = (tile * 64 + c + 16 * (r >> 2)) * 4 + (r & 3);
+        float v = 0.f;
 #pragma unroll
-                for (int w = 0; w < NW - 1; ++w) v += red[w][rt][nt][lane];
-                // D tile: this lane holds rows 4 j + i, column rl
-                const int n = n0 + nt * 16 + rl;
-                if (n >= M) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = r0 + rt * 16 + 4 * j + i;
-                    if (r < R)
-                        __hip_atomic_fetch_add(Y + (size_t)n * R + r, v[i], __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
+        for (int w = 0; w < NW; ++w) v += redf[w * RT * NT * 256 + at];
+        const int row = r0 + 16 * (tile / NT) + r, col = n0 + 16 * (tile % NT) + c;
+        if (row < R && col < M)
+            __hip_atomic_fetch_add(Y + (size_t)col * R + row, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -933,17 +946,28 @@ int linear_of(const uint8_t* w, int R, int C, const void* x, int x_dtype, int M,
                            kThreads, 0, st>>>(y, ny);
         // two row tiles per wave; 256-element steps per workgroup: four per wave on long rows
         // (the prefetch covers three of them; 4096 x 14336 at M = 32: q8_0 41.3 us against 8
-        // steps' 48.6 at the default register budget), one on short ones
+        // steps' 48.6 at the default register budget), one on short ones; the split count
+        // rounded up to a power of two (at most 8) for the XCD placement
         constexpr int RT = 2;
         const int NT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
         const int nsteps = (C + 255) / 256;
-        const int KS = nsteps >= 32 ? 16 : 4;
-        dim3 grid((R + 16 * RT - 1) / (16 * RT), (nsteps + KS - 1) / KS,
-                  (M + 16 * NT - 1) / (16 * NT));
+        const int ks0 = nsteps >= 32 ? 16 : 4;
+        MmGrid g;
+        g.nrt = (R + 16 * RT - 1) / (16 * RT);
+        g.S = 1;
+        while (g.S < 8 && g.S * ks0 < nsteps) g.S *= 2;
+        g.KB = (nsteps + g.S - 1) / g.S;
+        const int pad = 8 / g.S;
+        g.nrt_p = (g.nrt + pad - 1) / pad * pad;
+        const int gz = (M + 16 * NT - 1) / (16 * NT);
+        const long long nwg = (long long)g.nrt_p * g.S * gz;
+        if (nwg > 0x7fffffffLL)
+            return set_error(CSDR_E_UNSUPPORTED, "gguf_linear: too many output tiles");
         const auto* xp = static_cast<const _Float16*>(x);
-        if (NT == 1) gguf_mm_kernel<F, 1, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, KS);
-        else if (NT == 2) gguf_mm_kernel<F, 2, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, KS);
-        else gguf_mm_kernel<F, 4, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, KS);
+        const unsigned grid = (unsigned)nwg;
+        if (NT == 1) gguf_mm_kernel<F, 1, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, g);
+        else if (NT == 2) gguf_mm_kernel<F, 2, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, g);
+        else gguf_mm_kernel<F, 4, RT><<<grid, kThreads, 0, st>>>(w, R, C, xp, M, y, g);
     }
     CSDR_LAUNCH_CHECK("gguf_linear");
     return CSDR_OK;

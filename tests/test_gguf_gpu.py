@@ -157,6 +157,27 @@ def test_linear_batched(gpu, fmt, M):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("fmt,R,nsteps,M", [
+    ("q4_0", 300, 40, 32),    # 40 steps in 4 splits of 10 (one per pair of XCDs)
+    ("q6_k", 96, 72, 70),     # 8 splits of 9, two column groups, padded row tiles
+    ("q8_0", 1000, 12, 5),    # short rows: 4 splits of 3
+    ("q4_k", 130, 33, 17),    # 33 steps in 4 splits of 9 (the last holds 6)
+])
+def test_linear_batched_split_k(gpu, fmt, R, nsteps, M):
+    from cortexsdr_amd import gguf
+
+    rng = np.random.default_rng(300 + F[fmt] + M)
+    _, be = oracle.gguf_block(F[fmt])
+    Cc = 256 * nsteps
+    w = blocks(fmt, R * Cc // be, rng)
+    x = rng.normal(size=(M, Cc)).astype(np.float16)
+    ref = oracle.gguf_linear(w.ravel(), F[fmt], R, Cc, x.astype(np.float32))
+    y = gguf.linear(_dev(gpu, w.ravel()), F[fmt], R, Cc, _dev(gpu, x)).cpu().numpy()
+    err = rel_l2(y, ref)
+    print(f"{fmt} R={R} C={Cc} M={M}: rel_l2={err:.2e}", flush=True)
+    assert err <= TOL
+
+
 def test_rejects_bad_use(gpu):
     from cortexsdr_amd import _lib, gguf
 
