@@ -514,8 +514,19 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     Row8<KT> knew{}, vnew{};
     if constexpr (ROPE) {
         // rotate this lane's 8 query dims of every head, and the new key, at position L - 1;
-        // each pair's (cos, sin) evaluated once per workgroup (the lanes of a position group
-        // share dims), while the K/V loads above are in flight
+        // the new K/V row is loaded with the cached rows above and each pair's (cos, sin)
+        // evaluated once per workgroup (the lanes of a position group share dims) while all of
+        // those loads are in flight
+        float kn[8], vn[8];
+        {
+            const float* knp = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+            const float* vnp = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kn[i] = knp[i];
+                vn[i] = vnp[i];
+            }
+        }
         __shared__ float2 cs[HD / 2];
         for (int i = tid; i < HD / 2; i += kThreads) {
             const float freq = powf(ra.theta, -((float)(2 * i) / (float)HD));
@@ -523,8 +534,6 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
             cs[i] = make_float2(cosf(ang), sinf(ang));
         }
         __syncthreads();
-        const float* kn = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
-        const float* vn = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
             const float2 csv = cs[(li * 8 + i) / 2];

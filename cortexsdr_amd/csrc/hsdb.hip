@@ -686,7 +686,11 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
     const int C = d.C_full + d.Ce;
     float inv = 1.0f;
     if constexpr (XOP == CSDR_XOP_RMSNORM) {
-        // 1 / rms over all C features (x ops take fp32 x)
+        // 1 / rms over all C features (x ops take fp32 x); this lane's norm weights are
+        // loaded first, so that their round trip overlaps the statistic's
+        float nwv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) nwv[i] = p.nw[f0 + i];
         __shared__ float red[NT / 64];
         const float* xf = static_cast<const float*>(d.x);
         float ss = 0.f;
@@ -701,7 +705,7 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
         ss = wg_sum<NT>(ss, red);
         inv = 1.0f / sqrtf(ss / (float)C + p.eps);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xv[i] = xv[i] * inv * p.nw[f0 + i];
+        for (int i = 0; i < 16; ++i) xv[i] = xv[i] * inv * nwv[i];
     } else if constexpr (XOP == CSDR_XOP_SILU_MUL) {
         const float* x2 = static_cast<const float*>(d.x2) + f0;
 #pragma unroll
