@@ -488,45 +488,54 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
         }
         return;
     }
+    // Loads, in the order they are used: the query rows and the new K/V row, then every K row
+    // of this lane's positions, then every V row (one memory round trip for the split). All are
+    // issued unconditionally (heads past the group and positions past the split repeat the last
+    // one), so the compiler's waits count exactly: the RoPE waits for the first loads only, the
+    // scores for each K row as it arrives, and the softmax runs while the V rows stream in.
     float qv[GW][8];
 #pragma unroll
     for (int g = 0; g < GW; ++g)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            qv[g][i] = (g < nh) ? q[((size_t)b * Hq + h0 + g) * HD + li * 8 + i] : 0.f;
+            qv[g][i] = q[((size_t)b * Hq + h0 + min(g, nh - 1)) * HD + li * 8 + i];
+    float kn[8], vn[8];
+    if constexpr (ROPE) {
+        const float* knp = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+        const float* vnp = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            kn[i] = knp[i];
+            vn[i] = vnp[i];
+        }
+    }
+    // (the scheduling barriers keep the three groups of loads in this order)
+    __builtin_amdgcn_sched_barrier(0);
     const size_t rstride = (size_t)Hkv * HD;
     const KT* kb = kc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
     const KT* vb = vc + ((size_t)b * T * Hkv + kvh) * HD + li * 8;
-    // every K and V row of this lane's positions is loaded before the first use (one memory
-    // round trip for the split, instead of one per pass and operand)
     constexpr int kMaxPass = (sizeof(KT) == 4 ? kAttnMaxS32 : kAttnMaxS) / NG;
     const int npass = (p1 - p0 + NG - 1) / NG;
     Row8<KT> kr[kMaxPass], vr[kMaxPass];
 #pragma unroll
-    for (int j = 0; j < kMaxPass; ++j) {
-        if (j < npass) {
-            const int p = min(p0 + lg + j * NG, p1 - 1);
-            kr[j] = Row8<KT>::load(kb + (size_t)p * rstride);
-            vr[j] = Row8<KT>::load(vb + (size_t)p * rstride);
-        }
-    }
+    for (int j = 0; j < kMaxPass; ++j)
+        kr[j] = Row8<KT>::load(kb + (size_t)min(p0 + lg + j * NG, p1 - 1) * rstride);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kMaxPass; ++j)
+        vr[j] = Row8<KT>::load(vb + (size_t)min(p0 + lg + j * NG, p1 - 1) * rstride);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < GW; ++g)
+        if (g >= nh)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qv[g][i] = 0.f;
     const int plast = L - 1;
     Row8<KT> knew{}, vnew{};
     if constexpr (ROPE) {
         // rotate this lane's 8 query dims of every head, and the new key, at position L - 1;
-        // the new K/V row is loaded with the cached rows above and each pair's (cos, sin)
-        // evaluated once per workgroup (the lanes of a position group share dims) while all of
-        // those loads are in flight
-        float kn[8], vn[8];
-        {
-            const float* knp = ra.knew + ((size_t)b * Hkv + kvh) * HD + li * 8;
-            const float* vnp = ra.vnew + ((size_t)b * Hkv + kvh) * HD + li * 8;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                kn[i] = knp[i];
-                vn[i] = vnp[i];
-            }
-        }
+        // each pair's (cos, sin) evaluated once per workgroup (the lanes of a position group
+        // share dims) while the K/V loads are in flight
         __shared__ float2 cs[HD / 2];
         for (int i = tid; i < HD / 2; i += kThreads) {
             const float freq = powf(ra.theta, -((float)(2 * i) / (float)HD));
