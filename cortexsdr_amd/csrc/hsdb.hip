@@ -366,7 +366,7 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
         const float* pst = attn_stats(part, h, ns);
         const float4* pv = reinterpret_cast<const float4*>(attn_vecs(part, nh, h, ns, hd) + (f - h * hd));
         const int vs = hd / 4;  // float4 stride between splits
-        constexpr int kSB = 8;  // splits per round trip
+        constexpr int kSB = 12;  // splits per round trip
         float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
         if (ns == 1) {
             // one split: its sum over its normaliser
@@ -383,15 +383,22 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
             int GS = 1;
             while (GS < ns) GS <<= 1;
             const int ngs = nh * GS;  // < 2 nst
+            // (every load is issued, at clamped indices: a conditional load here made the
+            // compiler wait for all earlier loads before each one)
             float2 ml[kStatPT];
 #pragma unroll
             for (int k = 0; k < kStatPT; ++k) {
-                const int e = tid + k * NT, hh = min(e / GS, nh - 1), j = min(e % GS, ns - 1);
-                if (k * NT < ngs) ml[k] = reinterpret_cast<const float2*>(part)[hh * ns + j];
+                const int e = min(tid + k * NT, ngs - 1), hh = min(e / GS, nh - 1),
+                          j = min(e % GS, ns - 1);
+                ml[k] = reinterpret_cast<const float2*>(part)[hh * ns + j];
             }
-            float4 os[kSB];
+            // the values of the first two rounds of kSB splits (2 kSB covers the splits of
+            // every shape measured here), in flight during the weights
+            float4 oa[kSB], ob[kSB];
 #pragma unroll
-            for (int j = 0; j < kSB; ++j) os[j] = pv[min(j, ns - 1) * vs];
+            for (int j = 0; j < kSB; ++j) oa[j] = pv[min(j, ns - 1) * vs];
+#pragma unroll
+            for (int j = 0; j < kSB; ++j) ob[j] = pv[min(kSB + j, ns - 1) * vs];
 #pragma unroll
             for (int k = 0; k < kStatPT; ++k) {
                 if (k * NT >= ngs) break;
@@ -407,20 +414,28 @@ __device__ void stage_x_m1(const Params& p, const MatDesc& d, int b0, int nb, fl
             }
             __syncthreads();
             const float* wr = wst + h * ns;
-            for (int s0 = 0; s0 < ns; s0 += kSB) {
-                if (s0 > 0) {
-#pragma unroll
-                    for (int j = 0; j < kSB; ++j) os[j] = pv[min(s0 + j, ns - 1) * vs];
-                }
+            // the first two rounds are summed from the loads issued above. Every load is issued,
+            // at clamped indices, and every value used (with weight 0 past the last split), so
+            // that no load is left to wait on its own: loads placed under a per-split branch
+            // ran one round trip at a time.
+            auto add_round = [&](const float4 (&o)[kSB], int s0) {
 #pragma unroll
                 for (int j = 0; j < kSB; ++j) {
-                    if (s0 + j >= ns) break;
-                    const float w = wr[s0 + j];
-                    r.x = fmaf(w, os[j].x, r.x);
-                    r.y = fmaf(w, os[j].y, r.y);
-                    r.z = fmaf(w, os[j].z, r.z);
-                    r.w = fmaf(w, os[j].w, r.w);
+                    const int sj = s0 + j;
+                    const float w = sj < ns ? wr[min(sj, ns - 1)] : 0.f;
+                    r.x = fmaf(w, o[j].x, r.x);
+                    r.y = fmaf(w, o[j].y, r.y);
+                    r.z = fmaf(w, o[j].z, r.z);
+                    r.w = fmaf(w, o[j].w, r.w);
                 }
+            };
+            add_round(oa, 0);
+            add_round(ob, kSB);
+            // more than 2 kSB splits: the rest a round at a time
+            for (int s0 = 2 * kSB; s0 < ns; s0 += kSB) {
+#pragma unroll
+                for (int j = 0; j < kSB; ++j) oa[j] = pv[min(s0 + j, ns - 1) * vs];
+                add_round(oa, s0);
             }
         } else {
             // more partials than the LDS table holds: one pass over the splits, four at a
@@ -509,9 +524,12 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
         const size_t ytot = (size_t)d.R * M;
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
         const size_t ye = min(ytot, (size_t)(u + 1) * yper);
-        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
-            const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
-            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        // (kept with no bias: nothing to do, and no read of y to wait for)
+        if (!p.accumulate || d.bias) {
+            for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
+                const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
+                d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+            }
         }
     }
     if (d.blen == 64) {
@@ -630,9 +648,12 @@ __device__ __forceinline__ void dx1_body(const Params& p, int wg) {
         const size_t ytot = (size_t)d.R;
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
         const size_t ye = min(ytot, (size_t)(u + 1) * yper);
-        for (size_t i = (size_t)u * yper + tid; i < ye; i += NT) {
-            const float bv = d.bias ? d.bias[i] : 0.0f;
-            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        // (kept with no bias: nothing to do, and no read of y to wait for)
+        if (!p.accumulate || d.bias) {
+            for (size_t i = (size_t)u * yper + tid; i < ye; i += NT) {
+                const float bv = d.bias ? d.bias[i] : 0.0f;
+                d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+            }
         }
     }
     const int na = (d.K + kAtoms - 1) / kAtoms;
@@ -852,9 +873,12 @@ __global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
         const size_t ytot = (size_t)d.R * M;
         const size_t yper = (ytot + d.dx_count - 1) / d.dx_count;
         const size_t ye = min(ytot, (size_t)(u + 1) * yper);
-        for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
-            const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
-            d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+        // (kept with no bias: nothing to do, and no read of y to wait for)
+        if (!p.accumulate || d.bias) {
+            for (size_t i = (size_t)u * yper + tid; i < ye; i += kThreads) {
+                const float bv = d.bias ? d.bias[p.tm ? i % d.R : i / M] : 0.0f;
+                d.y[i] = p.accumulate ? d.y[i] + bv : bv;
+            }
         }
     }
     if (u == 0 && XOP != CSDR_XOP_NONE && d.xe) {
