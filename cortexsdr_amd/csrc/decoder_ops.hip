@@ -930,15 +930,35 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
     const size_t npart = (size_t)gridDim.x * nsplit;
     const float* pst = part + (size_t)2 * bh * nsplit;             // (max, sum) per split
     const float* pv = part + attn_vec_offset(npart) + (size_t)bh * nsplit * HD;  // per split
+    // rounds of kR splits, every load of a round issued at once (indices clamped, entries past
+    // the last split or of empty splits weighted 0): loads under a per-split branch ran one
+    // round trip at a time
+    constexpr int kR = 16;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pst[2 * s]);
+    for (int s0 = 0; s0 < nsplit; s0 += kR) {
+        float mv[kR];
+#pragma unroll
+        for (int j = 0; j < kR; ++j) mv[j] = pst[2 * min(s0 + j, nsplit - 1)];
+#pragma unroll
+        for (int j = 0; j < kR; ++j) M = fmaxf(M, mv[j]);
+    }
     float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float ms = pst[2 * s];
-        if (ms == -INFINITY) continue;
-        const float w = expf(ms - M);
-        den = fmaf(w, pst[2 * s + 1], den);
-        num = fmaf(w, pv[(size_t)s * HD + threadIdx.x], num);
+    for (int s0 = 0; s0 < nsplit; s0 += kR) {
+        float ms[kR], ls[kR], vv[kR];
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+            const int sj = min(s0 + j, nsplit - 1);
+            ms[j] = pst[2 * sj];
+            ls[j] = pst[2 * sj + 1];
+            vv[j] = pv[(size_t)sj * HD + threadIdx.x];
+        }
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+            const bool live = s0 + j < nsplit && ms[j] != -INFINITY;
+            const float w = live ? expf(ms[j] - M) : 0.f;
+            den = fmaf(w, live ? ls[j] : 0.f, den);
+            num = fmaf(w, live ? vv[j] : 0.f, num);
+        }
     }
     out[(size_t)bh * HD + threadIdx.x] = den > 0.f ? num / den : 0.f;
 }

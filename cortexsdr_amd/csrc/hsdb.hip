@@ -830,10 +830,12 @@ __global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
         for (int i = 0; i < 4; ++i) dv[i] = src[i];
     }
     {
-        // 16 pairs x 64 features, 4 per thread
+        // 16 pairs x 64 features, 4 per thread (the element type's branch around all four
+        // loads: a branch per load left each to wait for the ones before it)
         float v[4], w2[4], iv[4];
         int dst[4];
         bool ok[4];
+        size_t xo[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // e -> (block column bl of the tile, column m, feature f) in memory order: features
@@ -852,14 +854,20 @@ __global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
             const int b = ng * BPT + bl;
             ok[i] = b < d.NB && m < M;
             const int fg = min(b, d.NB - 1) * 64 + f, mg = min(m, M - 1);
-            const size_t xo = xi(p, d, fg, mg);
-            v[i] = xload(d.x, p.x_f16, xo);
+            xo[i] = xi(p, d, fg, mg);
             if constexpr (XOP == CSDR_XOP_RMSNORM) {
                 iv[i] = p.inv[g * 16 + mg];
                 w2[i] = p.nw[fg];
             }
-            if constexpr (XOP == CSDR_XOP_SILU_MUL) w2[i] = static_cast<const float*>(d.x2)[xo];
+            if constexpr (XOP == CSDR_XOP_SILU_MUL) w2[i] = static_cast<const float*>(d.x2)[xo[i]];
             dst[i] = n * kXsStride + f;
+        }
+        if (p.x_f16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = xval<_Float16>(d.x, xo[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = xval<float>(d.x, xo[i]);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
