@@ -1,6 +1,7 @@
 """Bench CLI for the compressed-weight path: every BASELINE.json configuration on one GPU.
 
-    python -m cortexsdr_amd.bench_cli [--configs cfg1,cfg2,cfg3] [--steps 50] [--out f.json]
+    python -m cortexsdr_amd.bench_cli [--configs cfg1,cfg2,cfg3,gguf,cfg4,cfg5,strategy5]
+        [--steps 50] [--out f.json]
     python -m cortexsdr_amd.bench_cli --suite suite.json [--out summary.json]
 
 The role of the reference's `cortexsdr_bench` suite runner (src/cortexsdr_bench.cpp:52-79,
@@ -84,6 +85,52 @@ def bench_hsdb(torch, R, Cc, K, s, M, xdtype, steps, seed=2):
     return {"R": R, "C": Cc, "K": K, "nnz": s, "M": M, "us": round(us, 3),
             "GBps": round(alg / us / 1e3, 1), "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4),
             "dense_equiv_TFLOPs": round(2.0 * R * Cc * M / us / 1e6, 2), "copies": ncp}
+
+
+STRATEGY5_SHAPES = (("attn 896x896", 896, 896, 256, 3, 5), ("mlp 4864x896", 4864, 896, 512, 3, 8))
+
+
+def strategy5_stream(R, Cc, K, S, k, seed=9):
+    """An HSDR v2 stream in the reference's own strategy-5 geometry (one tile per row,
+    tile_cols = C, a K x C dictionary; configFor's 1-row mode, HierarchicalSDRStrategy.cpp:
+    1024-1062) from this package's encoder with no refinement passes."""
+    from . import encode
+
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((R, Cc)) * 0.02).astype(np.float32)
+    return encode.compress(w, 1, Cc, K, S, k, ksvd_iters=0)
+
+
+def strategy5_alg_bytes(R, Cc, K, S, k, M):
+    """The stream's own bytes a product reads and writes: u16 codes, the fp32 dictionary, x
+    (fp32) and y."""
+    return R * S * k * 2 + K * Cc * 4 + Cc * M * 4 + R * M * 4
+
+
+def bench_strategy5(torch, steps, Ms=(1, 8)):
+    """matmulRowMajor on the reference's strategy-5 geometry (HK3): Qwen2-0.5B-shaped attention
+    (K = 256, 3 x 5 picks) and MLP (K = 512, 3 x 8) matrices, x fp32 feature-major."""
+    from .hsdr import HsdbSegment
+
+    out = []
+    for name, R, Cc, K, S, k in STRATEGY5_SHAPES:
+        stream = strategy5_stream(R, Cc, K, S, k)
+        for M in Ms:
+            seg = HsdbSegment(stream)
+            x = torch.from_numpy(synth.activations(Cc, M, seed=3)).cuda()
+            ws = seg.workspace(M)
+            y = seg.matmul(x, workspace=ws)
+
+            def fn(i, seg=seg, x=x, y=y, ws=ws):
+                seg.matmul(x, out=y, workspace=ws)
+
+            us = time_graph(torch, fn, 1, steps)
+            alg = strategy5_alg_bytes(R, Cc, K, S, k, M)
+            out.append({"matrix": name, "R": R, "C": Cc, "K": K, "slots": S * k, "M": M,
+                        "us": round(us, 3), "GBps": round(alg / us / 1e3, 1),
+                        "hbm_frac": round(alg / us / 1e-6 / HBM_PEAK, 4)})
+            seg.free()
+    return out
 
 
 def bench_hsdb_layers(torch, R, Cc, K, s, G, xdtype, steps, seed=2):
@@ -422,6 +469,10 @@ def main(argv=None) -> int:
                     out.append(bench_gguf(torch, fmt, R, Cc, M, args.steps))
                     print(json.dumps(out[-1]), flush=True)
         res["results"]["gguf"] = out
+    if "strategy5" in cfgs:  # the reference's own strategy-5 geometry (HK3)
+        res["results"]["strategy5"] = bench_strategy5(torch, args.steps)
+        for r in res["results"]["strategy5"]:
+            print(json.dumps(r), flush=True)
     if "cfg5" in cfgs:
         out = []
         for B in (int(v) for v in args.cfg5_batches.split(",")):

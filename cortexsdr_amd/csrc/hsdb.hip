@@ -593,7 +593,12 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
             }
         }
     } else {
-        // any block length: one wave per (b, a, group of 8 columns), lane-strided dot
+        // any block length (the reference's own 1-row geometry has blocks of C features): one
+        // wave per (b, a, group of 8 columns), lane-strided dot. Rounds of kR features per
+        // lane with every load of a round issued before its first use, at clamped indices and
+        // with the element type's branch around the round (a load per feature under that
+        // branch ran one round trip per feature); lanes past the block keep their sums.
+        constexpr int kR = 8;
         const int lane = tid & 63;
         const int mg = (M + 7) / 8;
         const long long item = (long long)u * (kThreads / 64) + (tid >> 6);
@@ -606,13 +611,50 @@ __global__ __launch_bounds__(kThreads) void dx_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
             const float* drow = d.dict + (size_t)a * d.blen;
-            for (int t = lane; t < d.blen; t += 64) {
-                const float dv = drow[t];
+            for (int t0 = 0; t0 < d.blen; t0 += 64 * kR) {
+                float dv[kR];
+                size_t xo[kR];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (j < nm)
-                        acc[j] = fmaf(dv, xload(d.x, p.x_f16, xi(p, d, b * d.blen + t, m0 + j)),
-                                      acc[j]);
+                for (int r = 0; r < kR; ++r) {
+                    const int t = min(t0 + r * 64 + lane, d.blen - 1);
+                    dv[r] = drow[t];
+                    xo[r] = xi(p, d, b * d.blen + t, m0);
+                }
+                if (nm == 1) {
+                    float xv[kR];
+                    if (p.x_f16) {
+#pragma unroll
+                        for (int r = 0; r < kR; ++r) xv[r] = xval<_Float16>(d.x, xo[r]);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < kR; ++r) xv[r] = xval<float>(d.x, xo[r]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < kR; ++r)
+                        if (t0 + r * 64 + lane < d.blen) acc[0] = fmaf(dv[r], xv[r], acc[0]);
+                } else {
+                    // the columns of feature t: xo + j (feature-major) or + j * C (token-major)
+                    const size_t cs = p.tm ? (size_t)(d.C_full + d.Ce) : 1;
+                    float xv[kR][8];
+                    if (p.x_f16) {
+#pragma unroll
+                        for (int r = 0; r < kR; ++r)
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                xv[r][j] = xval<_Float16>(d.x, xo[r] + (size_t)min(j, nm - 1) * cs);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < kR; ++r)
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                xv[r][j] = xval<float>(d.x, xo[r] + (size_t)min(j, nm - 1) * cs);
+                    }
+#pragma unroll
+                    for (int r = 0; r < kR; ++r)
+                        if (t0 + r * 64 + lane < d.blen)
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) acc[j] = fmaf(dv[r], xv[r][j], acc[j]);
+                }
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = csdr::wave_sum(acc[j]);
@@ -1440,10 +1482,22 @@ __global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
         const int m0 = z * MV;
         if (z > 0) __syncthreads();
         const float* Pg = d.P + (size_t)b0 * d.K * M;
-        for (int i = tid; i < nbc * d.K * MV; i += kThreads) {
-            const int e = i / MV, mm = i - e * MV;
-            const int m = m0 + mm;
-            Ps[i] = (m < M) ? Pg[(size_t)e * M + m] : 0.0f;
+        // (kStageBatch loads in flight per thread, at clamped indices: a load under the
+        // column test waited for the one before it)
+        const int np = nbc * d.K * MV;
+        for (int i0 = 0; i0 < np; i0 += kThreads * kStageBatch) {
+            float v[kStageBatch];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = min(i0 + j * kThreads + tid, np - 1);
+                const int e = i / MV, mm = i - e * MV;
+                v[j] = Pg[(size_t)e * M + min(m0 + mm, M - 1)];
+            }
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int i = i0 + j * kThreads + tid;
+                if (i < np) Ps[i] = (m0 + (i % MV) < M) ? v[j] : 0.0f;
+            }
         }
         __syncthreads();
         for (int pi = tid; pi < npairs; pi += kThreads) {
@@ -1453,12 +1507,26 @@ __global__ __launch_bounds__(kThreads) void gatherm_kernel(Params p) {
             float acc[MV];
 #pragma unroll
             for (int mm = 0; mm < MV; ++mm) acc[mm] = 0.0f;
-            for (int sl = 0; sl < d.slots; ++sl) {
-                const uint32_t w = src[sl];
-                const float cf = d.slot_gamma[sl] * csdr::h2f(w >> 16);
-                const float* pv = Pb + (size_t)(w & 0x7FFFu) * MV;
+            // the pair's code words and gains 8 at a time, all loaded before the first is used
+            // and all used (slots past the last repeat it with a zero coefficient): a load per
+            // slot under the loop's exit ran a round trip per slot
+            for (int s0 = 0; s0 < d.slots; s0 += 8) {
+                uint32_t wv[8];
+                float gv[8];
 #pragma unroll
-                for (int mm = 0; mm < MV; ++mm) acc[mm] = fmaf(cf, pv[mm], acc[mm]);
+                for (int j = 0; j < 8; ++j) {
+                    const int sj = min(s0 + j, d.slots - 1);
+                    wv[j] = src[sj];
+                    gv[j] = d.slot_gamma[sj];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t w = wv[j];
+                    const float cf = s0 + j < d.slots ? gv[j] * csdr::h2f(w >> 16) : 0.0f;
+                    const float* pv = Pb + (size_t)(w & 0x7FFFu) * MV;
+#pragma unroll
+                    for (int mm = 0; mm < MV; ++mm) acc[mm] = fmaf(cf, pv[mm], acc[mm]);
+                }
             }
 #pragma unroll
             for (int mm = 0; mm < MV; ++mm) part[pi * MV + mm] = acc[mm];
