@@ -275,6 +275,39 @@ def cfg1_leg(torch, args):
     return out
 
 
+def strategy5_leg(torch, args):
+    """The reference's own strategy-5 geometry (one tile per row, tile_cols = C, a K x C
+    dictionary: what its compressor writes in 1-row mode, HierarchicalSDRStrategy.cpp:
+    1024-1062): Qwen2-0.5B-shaped attention (896 x 896, K = 256, 3 x 5 picks) and MLP
+    (4864 x 896, K = 512, 3 x 8) streams from this package's encoder, matmulRowMajor at M = 1
+    and 8 (bench_cli.bench_strategy5). CPU: the restated matmulRowMajor (oracle
+    orc_hsdr_matmul_row_major, one thread, as the reference's loop) on the same streams at
+    M = 1."""
+    from cortexsdr_amd import bench_cli, synth
+
+    gpu = bench_cli.bench_strategy5(torch, 50, Ms=(1, 8))
+    out = {"workload": "strategy-5 geometry (1-row tiles of C features), x fp32",
+           "gpu": gpu, "cpu_baseline": None}
+    if not args.no_cpu:
+        import oracle
+
+        rows = []
+        for name, R, Cc, K, S, k in bench_cli.STRATEGY5_SHAPES:
+            stream = bench_cli.strategy5_stream(R, Cc, K, S, k)
+            x = synth.activations(Cc, 1, seed=3)
+            dt, n = _cpu_time(lambda: oracle.hsdr_matmul_row_major(stream, x),
+                              args.cpu_seconds / 4)
+            alg = bench_cli.strategy5_alg_bytes(R, Cc, K, S, k, 1)
+            rows.append({"matrix": name, "M": 1, "us": round(dt * 1e6, 1),
+                         "GBps": round(alg / dt / 1e9, 3), "calls": n})
+        out["cpu_baseline"] = {
+            "value": rows[-1]["GBps"], "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "the MLP stream at M=1 (and the attention stream, rows) through "
+                      "oracle/csdr_oracle.c orc_hsdr_matmul_row_major on one thread",
+            "rows": rows}
+    return out
+
+
 def cfg3_leg(torch, args):
     """Q4_K dequant-matmul, W 4096x4096 and 4096x14336, x fp16, M = 1 and 32
     (bench_cli.bench_q4k: ggml element order, HIP graph replays); CPU: the reference engine's
@@ -694,6 +727,7 @@ def main():
     if not args.no_configs:
         out["cfg1"] = cfg1_leg(torch, args)
         out["cfg3"] = cfg3_leg(torch, args)
+        out["strategy5"] = strategy5_leg(torch, args)
     if not args.no_decode:
         out["decode"] = decode_leg(args)
     if not args.no_7b:
