@@ -409,9 +409,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     uint32_t* sw = smem + wave * kStage;
     // A step's staging: the wave's rows' bytes of the step, ROWS x ND dwords (row rr's bytes
     // start at byte (its start & 3) of its slot), PF per lane, loaded into registers one step
-    // ahead of its use; the loads stay inside W (the last dword byte by byte).
+    // ahead of its use. Every load is issued unconditionally: a dword past W's last byte reads
+    // the dword that holds that byte instead (W is 4-byte aligned, so an aligned dword holding
+    // a byte of W lies in W's page), and such dwords are never decoded. (A branch per load, for
+    // those few dwords, made every load wait for the one before it.)
     constexpr int PF = (ROWS * ND + 63) / 64;
     uint32_t pf[PF];
+    const size_t last_dword = (total - 1) & ~(size_t)3;
     auto fetch = [&](int s) {
         const size_t soff = (size_t)s * Step<F>::kBytes;
 #pragma unroll
@@ -419,26 +423,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const int i = min(lane + 64 * k, ROWS * ND - 1);
             const int rr = i / ND, q = i - rr * ND;
             const size_t start = (size_t)min(r0 + rr, R - 1) * rowbytes + soff;
-            const size_t a = (start & ~(size_t)3) + 4 * (size_t)q;
-            uint32_t v = 0;
-            if (a + 4 <= total) {
-                v = *reinterpret_cast<const uint32_t*>(W + a);
-            } else {
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (a + b < total) v |= (uint32_t)W[a + b] << (8 * b);
-            }
-            pf[k] = v;
+            const size_t a = min((start & ~(size_t)3) + 4 * (size_t)q, last_dword);
+            pf[k] = *reinterpret_cast<const uint32_t*>(W + a);
         }
     };
-    // 32-wide k step t of step s from the staged bytes
-    auto kstep = [&](int e0, const uint8_t* const* rowsb, const int* rowso, int t) {
-        half8 bv[NT];
+    // X of 32-wide k step t (this lane's 8 values of each column tile)
+    auto xload = [&](int e0, int t, half8 (&bv)[NT]) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const half8 v = *reinterpret_cast<const half8*>(xr[nt] + e0 + 32 * t);
             bv[nt] = xl[nt] ? v : half8{};
         }
+    };
+    // 32-wide k step t of step s from the staged bytes, with X already in bv
+    auto kstep_x = [&](const uint8_t* const* rowsb, const int* rowso, int t,
+                       const half8 (&bv)[NT]) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int e = 32 * t + 8 * j, b = e / F::BE;
@@ -482,10 +481,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
         const int nsub = min(256, C - e0) / 32;  // 32-wide k steps (C is a multiple of BE >= 32)
         if (nsub == 8) {
+            // X one k step ahead: its loads in flight during the step before
+            half8 xb[2][NT];
+            xload(e0, 0, xb[0]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) kstep(e0, rowsb, rowso, t);
+            for (int t = 0; t < 8; ++t) {
+                if (t + 1 < 8) xload(e0, t + 1, xb[(t + 1) & 1]);
+                kstep_x(rowsb, rowso, t, xb[t & 1]);
+            }
         } else {
-            for (int t = 0; t < nsub; ++t) kstep(e0, rowsb, rowso, t);
+            for (int t = 0; t < nsub; ++t) {
+                half8 bv[NT];
+                xload(e0, t, bv);
+                kstep_x(rowsb, rowso, t, bv);
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
