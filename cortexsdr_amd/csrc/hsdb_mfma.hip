@@ -24,9 +24,11 @@
 //
 // Launches: an init kernel (Y = bias (+ Y when accumulating) + the fp32 edge strip times X,
 // and X transposed to fp16 [m][k] with the permutation, in the workspace), then one
-// persistent kernel: workgroup = 4 waves x 32 rows; the (row strip, block column) units of
-// all matrices are split in contiguous ranges over the workgroups, and each strip's
-// partial sums are added into Y with device-scope float atomics.
+// persistent kernel: workgroup = 8 or 16 waves x 16 rows; the (row strip, block column) units
+// of all matrices are split in contiguous ranges over the workgroups, and each strip's
+// partial sums are added into Y with device-scope float atomics. A unit's X slice is staged
+// in LDS by the workgroup (two barriers per unit), or, for a single 16-column tile, each wave
+// loads its X operands from the workspace one unit ahead and the waves run without barriers.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -134,7 +136,12 @@ __device__ __forceinline__ int find_matrix(const MParams& p, int u, int g) {
 // 32 rows (strip = 32 W rows). The codes and X slice of unit u + 1 are loaded into registers
 // while unit u is decoded and multiplied. One workgroup per CU (the dictionary fills most of
 // the LDS), so latency is hidden by the W waves of that workgroup.
-template <int NT, bool XS, int W, int RT, int SLOTS>
+// XR: each wave loads its X operands straight from the transposed X (global memory, L1/L2
+// hits: the workgroup's waves all take the same unit sequence) one unit ahead, so the units
+// need no X staging and no barriers; the waves run apart and one's LDS reads overlap
+// another's arithmetic. Else the unit's X slice is staged in LDS by the whole workgroup.
+// LB: slots whose dictionary reads are issued together before their multiply-adds.
+template <int NT, bool XS, int W, int RT, int SLOTS, bool XR>
 __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     constexpr int CW = SLOTS / 4;  // 16-byte code pieces per tile
@@ -143,7 +150,9 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     extern __shared__ __attribute__((aligned(16))) _Float16 smem16[];
     constexpr int MT = NT * 16;
     constexpr int NGR = MT * 8 * (XS ? 2 : 1);  // 16-byte X granules per unit
-    constexpr int GPT = (NGR + kThreads - 1) / kThreads;
+    constexpr int GPT = XR ? 1 : (NGR + kThreads - 1) / kThreads;
+    constexpr int NP = XS ? 2 : 1;           // X parts (fp32 X: hi, lo)
+    constexpr int LB = SLOTS < 4 ? SLOTS : 4;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int q = lane >> 4, rl = lane & 15;
@@ -158,7 +167,8 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     const int M = p.M;
 
     floatx4 acc[RT][NT];
-    u32x4 xr[GPT];   // prefetched X granules of the next unit
+    u32x4 xr[GPT];   // prefetched X granules of the next unit (staged X)
+    u32x4 xb[XR ? NT : 1][NP][2];  // prefetched X operands of the next unit (XR)
     u32x4 cr[RT][CW];  // prefetched code words of the next unit (RT row tiles)
     int ng = -1, nstrip = 0, nb = 0;  // the prefetched unit
 
@@ -169,8 +179,20 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
         nstrip = lu / d.NB;
         nb = lu - nstrip * d.NB;
         const size_t nxt = (size_t)p.Mpad * d.C_full;
+        if constexpr (XR) {
+            // lane (column n = 16 nt + rl, group q): granules 2q and 2q + 1 of the block
 #pragma unroll
-        for (int i = 0; i < GPT; ++i) {
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int part = 0; part < NP; ++part)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c)
+                        xb[nt][part][c] = *reinterpret_cast<const u32x4*>(
+                            d.xt + part * nxt + (size_t)(p.m0 + nt * 16 + rl) * d.C_full +
+                            (size_t)nb * 64 + (2 * q + c) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < (XR ? 0 : GPT); ++i) {
             const int gi = min(tid + i * kThreads, NGR - 1);
             const int part = XS ? gi / (MT * 8) : 0;
             const int gg = gi - part * MT * 8;
@@ -239,14 +261,24 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
                                                       ((gr ^ ((a >> 1) & 7)) * 8)) = v[j];
                     }
                 }
+                if constexpr (XR) __syncthreads();
             }
             cur_g = g;
             cur_strip = strip;
         }
-        // X slice -> LDS; granule index XOR (row & 7) against bank conflicts
-        __syncthreads();
+        u32x4 xc[XR ? NT : 1][NP][2];
+        if constexpr (XR) {
 #pragma unroll
-        for (int i = 0; i < GPT; ++i) {
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int part = 0; part < NP; ++part)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) xc[nt][part][c] = xb[nt][part][c];
+        }
+        // X slice -> LDS; granule index XOR (row & 7) against bank conflicts
+        if constexpr (!XR) __syncthreads();
+#pragma unroll
+        for (int i = 0; i < (XR ? 0 : GPT); ++i) {
             const int gi = min(tid + i * kThreads, NGR - 1);
             const int part = XS ? gi / (MT * 8) : 0;
             const int gg = gi - part * MT * 8;
@@ -259,7 +291,7 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int j4 = 0; j4 < CW; ++j4) cc[rt][j4] = cr[rt][j4];
-        __syncthreads();
+        if constexpr (!XR) __syncthreads();
         if (u + 1 < u1) prefetch(u + 1);
         // decode this lane's 16 k values of each of its rows: per slot the coefficient as an
         // fp16 pair (times the slot's gain relative to slot 0) and 8 packed fp16 FMAs over the
@@ -271,25 +303,34 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) w[t] = h2{(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-            for (int j = 0; j < SLOTS; ++j) {
-                const uint32_t word = cc[rt][j >> 2][j & 3];
-                // (c, c): the word's high half in both halves
-                const h2 c2 =
-                    __builtin_bit_cast(h2, __builtin_amdgcn_perm(word, word, 0x07060706u)) *
-                    __builtin_bit_cast(h2, d.grel[j]);
-                const uint32_t at = word & 0x7FFFu;
-                const uint32_t sw = (at >> 1) & 7;
-                const _Float16* drow = Ds + at * 64;
-                const u32x4 lo = *reinterpret_cast<const u32x4*>(drow + (((2 * q) ^ sw) * 8));
-                const u32x4 hi =
-                    *reinterpret_cast<const u32x4*>(drow + (((2 * q + 1) ^ sw) * 8));
-                // (vector elements go through a scalar: bit-casting a subscripted vector element
-                // directly reads element 0 whatever the subscript)
+            for (int j0 = 0; j0 < SLOTS; j0 += LB) {
+                // the batch's LB atoms: both 16-byte granules of each read before any is used
+                u32x4 lo[LB], hi[LB];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t el = lo[t], eh = hi[t];
-                    w[t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, el), w[t]);
-                    w[4 + t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, eh), w[4 + t]);
+                for (int jj = 0; jj < LB; ++jj) {
+                    const uint32_t word = cc[rt][(j0 + jj) >> 2][(j0 + jj) & 3];
+                    const uint32_t at = word & 0x7FFFu;
+                    const uint32_t sw = (at >> 1) & 7;
+                    const _Float16* drow = Ds + at * 64;
+                    lo[jj] = *reinterpret_cast<const u32x4*>(drow + (((2 * q) ^ sw) * 8));
+                    hi[jj] = *reinterpret_cast<const u32x4*>(drow + (((2 * q + 1) ^ sw) * 8));
+                }
+#pragma unroll
+                for (int jj = 0; jj < LB; ++jj) {
+                    const int j = j0 + jj;
+                    const uint32_t word = cc[rt][j >> 2][j & 3];
+                    // (c, c): the word's high half in both halves
+                    const h2 c2 =
+                        __builtin_bit_cast(h2, __builtin_amdgcn_perm(word, word, 0x07060706u)) *
+                        __builtin_bit_cast(h2, d.grel[j]);
+                    // (vector elements go through a scalar: bit-casting a subscripted vector
+                    // element directly reads element 0 whatever the subscript)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t el = lo[jj][t], eh = hi[jj][t];
+                        w[t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, el), w[t]);
+                        w[4 + t] = __builtin_elementwise_fma(c2, __builtin_bit_cast(h2, eh), w[4 + t]);
+                    }
                 }
             }
 #pragma unroll
@@ -309,10 +350,15 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
             const int g0 = (2 * q) ^ (n & 7), g1 = (2 * q + 1) ^ (n & 7);
 #pragma unroll
             for (int part = 0; part < (XS ? 2 : 1); ++part) {
-                const _Float16* xrow = Xs + (size_t)part * MT * 64 + n * 64;
                 half8 bs[2];
-                bs[0] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g0 * 8));
-                bs[1] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g1 * 8));
+                if constexpr (XR) {
+                    bs[0] = __builtin_bit_cast(half8, xc[nt][part][0]);
+                    bs[1] = __builtin_bit_cast(half8, xc[nt][part][1]);
+                } else {
+                    const _Float16* xrow = Xs + (size_t)part * MT * 64 + n * 64;
+                    bs[0] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g0 * 8));
+                    bs[1] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(xrow + g1 * 8));
+                }
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -349,13 +395,18 @@ constexpr int waves_for(int nt) { return nt <= 4 ? 16 : 8; }
 // (two 16-row tiles per wave from 64 columns up, so that each X operand read from LDS feeds
 // two matrix-core steps, measured slower: cfg2 M = 64 44.3 -> 56.6 us, M = 256 88.0 -> 104.8)
 constexpr int rows_for(int) { return 1; }
+// X operands from global memory (no X staging) for one 16-column tile: cfg2 4096 x 11008 at
+// M = 16 36.2 -> 33.3 us per call; at two tiles (M = 32) slower, 40.4 -> 44.0; at four the
+// prefetched operands spill
+constexpr bool x_in_regs(int nt, bool) { return nt == 1; }
 
 template <int NT, bool XS, int SLOTS>
 int launch_one(const MParams& p, int grid, size_t lds, hipStream_t st) {
     constexpr int W = waves_for(NT), RT = rows_for(NT);
-    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W, RT, SLOTS>);
+    constexpr bool XR = x_in_regs(NT, XS);
+    const void* fn = reinterpret_cast<const void*>(&mfma_kernel<NT, XS, W, RT, SLOTS, XR>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    mfma_kernel<NT, XS, W, RT, SLOTS><<<grid, W * 64, lds, st>>>(p);
+    mfma_kernel<NT, XS, W, RT, SLOTS, XR><<<grid, W * 64, lds, st>>>(p);
     CSDR_LAUNCH_CHECK("hsdb mfma");
     return CSDR_OK;
 }
