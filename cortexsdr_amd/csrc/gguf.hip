@@ -22,7 +22,10 @@
 //     subnormal pairs for v_dot2_f32_f16 (scaled into the widest exact range: at 2^-24 the
 //     dot's products lose precision). The others take values 8 g .. 8 g + 7 per lane (Dec8:
 //     the block's header read once for the 8) in fp32. gguf_gemv_kernel is the element-wise
-//     form from memory, for rows longer than the LDS budget.
+//     form from memory, for rows longer than the LDS budget. gguf_gemv_pipe_kernel (q8_0
+//     and q5_k rows of 8192 values and more): x staged once per workgroup in LDS, a wave's
+//     rows cut into 2 KiB items of whole blocks with two items' loads in flight while it
+//     decodes a third from LDS.
 //   gguf_mm_kernel (M > 1, fp16 X): split-K over 256-element steps of the row, 16 RT rows per
 //     workgroup, the 4 waves taking every 4th step. A wave stages its rows' bytes of a step in
 //     LDS with dword loads issued one step ahead (a row's step need not start 4-byte aligned),
@@ -37,8 +40,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -911,6 +916,169 @@ __global__ __launch_bounds__(kThreads) void gguf_gemv_lds_kernel(const uint8_t* 
     if (lane == 0) y[r] = acc;
 }
 
+
+// ---- M == 1, pipelined: x staged once per workgroup in LDS, so a wave's only global loads are
+// its weight bytes and it can keep two items of them in flight while it decodes a third. The
+// workgroup's rows are cut into items of whole blocks (at most kPipeChunk bytes from the
+// 16-byte boundary at or below the item's first byte), flattened row-major and split into
+// one contiguous run per wave. Per item: the loads of item i + 2 are issued, item i is
+// decoded from its LDS slot (x from LDS), and item i + 1 is copied from registers to the
+// other slot. A wave's partial row sums meet in LDS (a row's items can fall to two waves).
+constexpr int kPipeWaves = 8;
+constexpr int kPipeThreads = kPipeWaves * 64;
+constexpr int kPipeLpc = 2;                       // 16-byte pieces per lane per item
+constexpr int kPipeChunk = 64 * kPipeLpc * 16;    // bytes per item, at most
+constexpr int kPipeSlot = kPipeChunk + 16;        // + the dword a read at the end reaches
+constexpr int kPipeMaxRows = 64;                  // rows per workgroup (LDS row sums)
+
+template <class F>
+constexpr int pipe_blocks() { return (kPipeChunk - 15) / F::BB; }  // blocks per item
+
+// Formats the pipelined kernel serves, on rows of at least kPipeMinC values (measured, 4096
+// rows, per call against the one-wave-per-row kernel: q8_0 x 14336 21.0 -> 18.1 us, q5_k
+// 18.7 -> 17.0; q4_0 14.1 -> 14.0; q6_k 21.4 -> 24.2 and every 4096-value row 0.7-1.2 us
+// slower, where a wave's run is two or three items: those keep the other kernel)
+template <class F>
+struct PipeM1 {
+    static constexpr bool value = false;
+};
+template <>
+struct PipeM1<Q8_0> {
+    static constexpr bool value = true;
+};
+template <>
+struct PipeM1<Packed<176, 256, 5>> {  // q5_k
+    static constexpr bool value = true;
+};
+constexpr int kPipeMinC = 8192;
+
+template <class F, typename XT>
+__global__ __launch_bounds__(kPipeThreads) void gguf_gemv_pipe_kernel(
+    const uint8_t* __restrict__ W, int R, int C, const XT* __restrict__ x, float* __restrict__ y,
+    int rpg, int xvec) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int BPC = pipe_blocks<F>();
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // LDS: x (C values), the row sums, then two item slots per wave
+    XT* xs = reinterpret_cast<XT*>(gsm);
+    const int xbytes = (C * (int)sizeof(XT) + 15) & ~15;
+    float* rsum = reinterpret_cast<float*>(gsm + xbytes);
+    uint8_t* slots = gsm + xbytes + kPipeMaxRows * 4 + (size_t)wave * 2 * kPipeSlot;
+    const int nbr = C / F::BE, nch = (nbr + BPC - 1) / BPC;
+    const int rw0 = blockIdx.x * rpg, rw1 = min(R, rw0 + rpg);
+    const int nitems = max(0, rw1 - rw0) * nch;
+    const int per = (nitems + kPipeWaves - 1) / kPipeWaves;
+    const int i0 = min(nitems, wave * per), i1 = min(nitems, i0 + per);
+    // one buffer resource over W from the 16-byte boundary at or below it; a load at or past
+    // the end returns zeros without a memory access
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(W), wb = wa & ~(uintptr_t)15;
+    const size_t rowbytes = (size_t)nbr * F::BB;
+    const uint32_t wlen = (uint32_t)((wa - wb + (size_t)R * rowbytes + 15) & ~(size_t)15);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(wb), (short)0, (int)wlen, 0x00020000);
+    auto span = [&](int it, int& row, int& cb0, int& nb, uint32_t& a0, int& lead) {
+        row = rw0 + it / nch;
+        cb0 = (it - (it / nch) * nch) * BPC;
+        nb = min(BPC, nbr - cb0);
+        const uint32_t off = (uint32_t)(wa - wb + (size_t)row * rowbytes + (size_t)cb0 * F::BB);
+        a0 = off & ~15u;
+        lead = (int)(off - a0);
+    };
+    auto issue = [&](int it, u32x4 (&v)[kPipeLpc]) {
+        int row, cb0, nb, lead;
+        uint32_t a0;
+        span(min(it, max(i1 - 1, 0)), row, cb0, nb, a0, lead);
+        const int np = it < i1 ? (lead + nb * F::BB + 15) >> 4 : 0;
+#pragma unroll
+        for (int j = 0; j < kPipeLpc; ++j) {
+            const int pc = j * 64 + lane;
+            v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, pc < np ? a0 + 16u * pc : 0x80000000u, 0, 2);
+        }
+    };
+    auto put = [&](int slot, const u32x4 (&v)[kPipeLpc]) {
+        u32x4* d = reinterpret_cast<u32x4*>(slots + slot * kPipeSlot);
+#pragma unroll
+        for (int j = 0; j < kPipeLpc; ++j) d[j * 64 + lane] = v[j];
+        // the slot is this wave's own: a wave-level ordering suffices
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // x loads first (so that waiting for them does not wait for the weight loads), then the
+    // first two items' loads, then x to LDS
+    constexpr int kXv = 16 / sizeof(XT);  // values per 16-byte piece
+    const int nxv = C / kXv;
+    constexpr int kXPer = 4;
+    u32x4 xr[kXPer];
+    if (xvec) {
+#pragma unroll
+        for (int j = 0; j < kXPer; ++j)
+            xr[j] = *reinterpret_cast<const u32x4*>(x + (size_t)min(j * kPipeThreads + tid, nxv - 1) * kXv);
+    }
+    u32x4 ring[3][kPipeLpc];
+    issue(i0, ring[0]);
+    issue(i0 + 1, ring[1]);
+    if (xvec) {
+#pragma unroll
+        for (int j = 0; j < kXPer; ++j)
+            if (j * kPipeThreads + tid < nxv)
+                reinterpret_cast<u32x4*>(xs)[j * kPipeThreads + tid] = xr[j];
+        for (int i = kXPer * kPipeThreads + tid; i < nxv; i += kPipeThreads)
+            reinterpret_cast<u32x4*>(xs)[i] = *reinterpret_cast<const u32x4*>(x + (size_t)i * kXv);
+    } else {
+        for (int i = tid; i < C; i += kPipeThreads) xs[i] = x[i];
+    }
+    for (int i = tid; i < kPipeMaxRows; i += kPipeThreads) rsum[i] = 0.0f;
+    __syncthreads();
+    put(0, ring[0]);
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(gsm);
+    float acc = 0.0f;
+    auto step = [&](int it, auto rb) {  // rb: ring index of item it (compile-time)
+        constexpr int kR = decltype(rb)::value;
+        issue(it + 2, ring[(kR + 2) % 3]);
+        if (it < i1) {
+            int row, cb0, nb, lead;
+            uint32_t a0;
+            span(it, row, cb0, nb, a0, lead);
+            const int sl = (it - i0) & 1;
+            const XT* xp = xs + (size_t)cb0 * F::BE;
+            if constexpr (Units<F>::value) {
+                const int ro = (int)(slots - gsm) + sl * kPipeSlot + lead;
+                const int nu = nb * Units<F>::kPerBlock;
+                for (int u = lane; u < nu; u += 64) acc += Units<F>::dot(s32, ro, u, xp, true);
+            } else {
+                const uint8_t* rowp = slots + sl * kPipeSlot + lead;
+                const int ng = nb * (F::BE / 8);
+                for (int g = lane; g < ng; g += 64) {
+                    const int e0 = g << 3, b = e0 / F::BE;
+                    float w8[8], xv[8];
+                    Dec8<F>::run(rowp + (size_t)b * F::BB, e0 - b * F::BE, w8);
+                    x8(xp, e0, true, xv);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) acc = fmaf(w8[k], xv[k], acc);
+                }
+            }
+            // the row's last item in this wave's run: its sum into the row's LDS total
+            const int nrow = rw0 + (it + 1) / nch;
+            if (it + 1 == i1 || nrow != row) {
+                const float t = csdr::wave_sum(acc);
+                if (lane == 0) atomicAdd(&rsum[row - rw0], t);
+                acc = 0.0f;
+            }
+        }
+        if (it + 1 < i1) put((it + 1 - i0) & 1, ring[(kR + 1) % 3]);
+    };
+    for (int it = i0; it < i1; it += 3) {
+        step(it, std::integral_constant<int, 0>{});
+        step(it + 1, std::integral_constant<int, 1>{});
+        step(it + 2, std::integral_constant<int, 2>{});
+    }
+    __syncthreads();
+    for (int i = tid; i < rw1 - rw0; i += kPipeThreads) y[rw0 + i] = rsum[i];
+}
+
 // ---- format table: name, id, and the launchers of each format
 struct Launch {
     int (*linear)(const uint8_t*, int, int, const void*, int, int, float*, hipStream_t);
@@ -923,6 +1091,37 @@ int linear_of(const uint8_t* w, int R, int C, const void* x, int x_dtype, int M,
     if (M == 1) {
         const int grid = (R + kThreads / 64 - 1) / (kThreads / 64);
         const int xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+        // the pipelined kernel: x and the item slots in LDS, W within a 32-bit buffer range
+        const size_t xb = ((size_t)C * (x_dtype == CSDR_F16 ? 2 : 4) + 15) & ~(size_t)15;
+        const size_t lds_p = xb + kPipeMaxRows * 4 + (size_t)kPipeWaves * 2 * kPipeSlot;
+        const size_t wbytes = (size_t)R * (C / F::BE) * F::BB + 16;
+        const char* ev = std::getenv("CSDR_GGUF_PIPE");
+        const bool pipe_on = !(ev && *ev && std::atoi(ev) == 0);
+        if (PipeM1<F>::value && C >= kPipeMinC && pipe_on && pipe_blocks<F>() >= 1 &&
+            lds_p <= 160 * 1024 && wbytes < 0x7FFFFFF0u) {
+            int dev = 0, ncu = 256;
+            if (hipGetDevice(&dev) == hipSuccess) {
+                int v = 0;
+                if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                        hipSuccess && v > 0)
+                    ncu = v;
+            }
+            // about two workgroups per CU (each LDS holds x), rows split evenly
+            int rpg = (R + 2 * ncu - 1) / (2 * ncu);
+            rpg = std::max(1, std::min(rpg, kPipeMaxRows));
+            const int g = (R + rpg - 1) / rpg;
+            auto go = [&](auto kern, const auto* xp) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_p);
+                kern<<<g, kPipeThreads, lds_p, st>>>(w, R, C, xp, y, rpg, xvec);
+            };
+            if (x_dtype == CSDR_F16)
+                go(gguf_gemv_pipe_kernel<F, _Float16>, static_cast<const _Float16*>(x));
+            else
+                go(gguf_gemv_pipe_kernel<F, float>, static_cast<const float*>(x));
+            CSDR_LAUNCH_CHECK("gguf_linear");
+            return CSDR_OK;
+        }
         const size_t slot = gv_row_slot<F>(C);
         const size_t lds = (kThreads / 64) * slot;
         if (StageRow<F>::value && lds <= 160 * 1024) {

@@ -84,7 +84,8 @@ def test_linear_m1(gpu, fmt, R, nblk):
 
 
 @pytest.mark.parametrize("fmt,R,Cc", [("q6_k", 4100, 14336), ("q4_0", 9001, 4096),
-                                      ("q8_0", 8500, 4096)])
+                                      ("q8_0", 8500, 4096), ("q5_k", 8500, 8448),
+                                      ("q8_0", 1031, 14336)])
 def test_linear_m1_many_rows(gpu, fmt, R, Cc):
     """More rows than the chip holds at once (several rounds of workgroups), ragged counts."""
     from cortexsdr_amd import gguf
@@ -116,6 +117,27 @@ def test_linear_m1_unaligned_x(gpu, fmt):
         ref = oracle.gguf_linear(w.ravel(), F[fmt], R, Cc, buf[:, 1:].astype(np.float32))
         y = gguf.linear(wd, F[fmt], R, Cc, _dev(gpu, buf)[:, 1:]).cpu().numpy()
         assert rel_l2(y, ref) <= TOL_M1, np.dtype(dt).name
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q5_k"])
+def test_linear_m1_pipelined_unaligned_x(gpu, fmt):
+    """Rows of 8192 values and more in q8_0 / q5_k take the pipelined kernel (x staged in LDS):
+    x one element into its buffer (the element-wise staging), a row count that leaves the last
+    workgroup short, items that straddle 16-byte boundaries."""
+    from cortexsdr_amd import gguf
+
+    rng = np.random.default_rng(500 + F[fmt])
+    _, be = oracle.gguf_block(F[fmt])
+    R, Cc = 517, 8448
+    w = blocks(fmt, R * Cc // be, rng)
+    wd = _dev(gpu, w.ravel())
+    for dt in (np.float32, np.float16):
+        buf = rng.normal(size=(1, Cc + 1)).astype(dt)
+        ref = oracle.gguf_linear(w.ravel(), F[fmt], R, Cc, buf[:, 1:].astype(np.float32))
+        y = gguf.linear(wd, F[fmt], R, Cc, _dev(gpu, buf)[:, 1:]).cpu().numpy()
+        err = rel_l2(y, ref)
+        print(f"{fmt} R={R} C={Cc} {np.dtype(dt).name} unaligned: rel_l2={err:.2e}", flush=True)
+        assert err <= TOL_M1
 
 
 @pytest.mark.parametrize("fmt,R,Cc", [
