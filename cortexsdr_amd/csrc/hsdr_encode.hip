@@ -803,7 +803,10 @@ CSDR_API int csdr_hsda_build(int n, const char* const* names, const float* const
             std::vector<std::vector<float>> seg_tiles;
             for (size_t i : kv.second) {
                 // per-segment non-finite gate (:2324-2358): probe 1 in 256, then sanitise and
-                // skip the segment when more than 1e-3 of it is bad
+                // skip the segment when more than 1e-3 of it is bad. The sanitised values are
+                // also what the segment is encoded from, in every tile mode; the reference
+                // re-encodes 2-D segments from the raw values (:2373, :2474-2475), letting
+                // NaN / Inf into matching pursuit (a deliberate difference)
                 std::vector<float> m(w[i], w[i] + (size_t)rows[i] * cols[i]);
                 bool any_bad = false;
                 for (size_t j = 0; j < m.size(); j += 256)
