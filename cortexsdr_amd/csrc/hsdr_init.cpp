@@ -12,14 +12,20 @@
 //     lanes added onto the lower, then lanes 2, 3 onto 0, 1, then lane 1 onto lane 0; a
 //     4-element remainder as plain products summed (1 + 3) + (0 + 2) and added on; FMAs for
 //     the last elements;
-//   * x / sqrt(s) as x * r with r = (y0 * (y0 * s) - 3) * (y0 * -0.5), y0 the CPU's approximate
-//     reciprocal square root (rsqrtss) and the inner product-sum fused: one Newton step.
-//     rsqrtss differs between CPU models, and so does the reference's dictionary; this code
-//     reproduces the reference on the CPU it runs on;
-//   * the mean tile norm in double (FMA sums), divided by n, rounded to float.
+//   * x / sqrt(s) as x * r with r = (y0 * (y0 * s) - 3) * (y0 * -0.5), y0 the approximate
+//     reciprocal square root (x86 rsqrtss) and the inner product-sum fused: one Newton step.
+//     rsqrtss differs between CPU models, and so does the reference's dictionary. y0 here is
+//     that of the CPU the golden vectors were written on (an Intel Xeon: a function of the
+//     exponent's parity and the top 10 mantissa bits, scaling by 2^-k for 4^k s; the table
+//     comes from rsqrt_table_gen.c run there), so the dictionary is the same on every host;
+//   * each tile's squared norm in double as the -O3 -ffast-math AVX2 build sums
+//     `sq += (double)t[c] * t[c]` (gcc 11): four lanes taking 8 values per step, lane j adding
+//     fma(t[c + j], t[c + j], t[c + 4 + j]^2), then (lane 0 + lane 2) + (lane 1 + lane 3); a
+//     remaining group of 4 as fma(t0, t0, t2^2) + fma(t1, t1, t3^2); FMAs for the last values;
+//   * the mean tile norm: those norms summed in tile order, divided by n (rounded to float
+//     for the initialisation).
 // The atom re-seeding of atomUpdateStep (:411-425, :461-474) is here too: a tile picked by a
-// per-atom generator, scaled to the target norm in double.
-#include <immintrin.h>
+// per-atom generator, its squared norm summed as above, scaled to the target norm in double.
 
 #include <algorithm>
 #include <cmath>
@@ -33,8 +39,22 @@ namespace csdr {
 
 namespace {
 
+#include "hsdr_rsqrt_table.inc"
+
+// The golden vectors' CPU's rsqrtss of a normal positive s
+float rsqrt_approx(float s) {
+    uint32_t b;
+    std::memcpy(&b, &s, 4);
+    const int e = (int)(b >> 23) - 127;
+    const int p = e & 1;          // s = 4^k 2^p (1 + m / 2^23)
+    const int k = (e - p) / 2;
+    float y;
+    std::memcpy(&y, &kRsqrtTable[p * 1024 + ((b >> 13) & 1023u)], 4);
+    return std::ldexp(y, -k);
+}
+
 float rsqrt_newton(float s) {
-    const float y0 = _mm_cvtss_f32(_mm_rsqrt_ss(_mm_set_ss(s)));
+    const float y0 = rsqrt_approx(s);
     const float ys = y0 * s;
     const float t = std::fma(y0, ys, -3.0f);
     const float h = y0 * -0.5f;
@@ -62,19 +82,37 @@ float squared_norm(const float* d, uint32_t C) {
     return sq;
 }
 
+// sum_c (double)t[c]^2 in the order of the reference's vectorised loop (header)
+double squared_norm_d(const float* t, uint32_t C) {
+    double total = 0.0;
+    uint32_t c = 0;
+    if (C >= 8) {
+        double a[4] = {0.0, 0.0, 0.0, 0.0};
+        for (; c + 8 <= C; c += 8)
+            for (int j = 0; j < 4; ++j) {
+                const double lo = t[c + j], hi = t[c + 4 + j];
+                a[j] = a[j] + std::fma(lo, lo, hi * hi);
+            }
+        total = (a[0] + a[2]) + (a[1] + a[3]);
+    }
+    if (C - c >= 4) {
+        const double t0 = t[c], t1 = t[c + 1], t2 = t[c + 2], t3 = t[c + 3];
+        const double e0 = std::fma(t0, t0, t2 * t2), e1 = std::fma(t1, t1, t3 * t3);
+        total = total + (e0 + e1);
+        c += 4;
+    }
+    for (; c < C; ++c) total = std::fma((double)t[c], (double)t[c], total);
+    return total;
+}
+
 }  // namespace
 
 // Mean of the tiles' Euclidean norms, in double (fitHierarchicalKSVD :529-536, atomUpdateStep
-// :374-383, whose OpenMP reduction sums per-thread partials: its last bits follow the thread
-// count).
+// :374-383): the norms summed in tile order, as the reference's OpenMP reduction does with
+// one thread (with more, its per-thread partials change the last bits).
 double hsdr_mean_tile_norm(const float* tiles, uint32_t n, uint32_t C) {
     double norm_sum = 0.0;
-    for (uint32_t i = 0; i < n; ++i) {
-        const float* t = tiles + (size_t)i * C;
-        double sq = 0.0;
-        for (uint32_t c = 0; c < C; ++c) sq = std::fma((double)t[c], (double)t[c], sq);
-        norm_sum += std::sqrt(sq);
-    }
+    for (uint32_t i = 0; i < n; ++i) norm_sum += std::sqrt(squared_norm_d(tiles + (size_t)i * C, C));
     return norm_sum / (double)std::max<uint32_t>(1u, n);
 }
 
@@ -105,8 +143,7 @@ void hsdr_reseed_atom(const float* tiles, uint32_t n, uint32_t C, uint64_t base_
     std::mt19937 local(static_cast<uint32_t>(base_seed ^ (uint64_t)(j * mul)));
     std::uniform_int_distribution<uint32_t> pick(0, n - 1);
     const float* src = tiles + (size_t)pick(local) * C;
-    double sq = 0.0;
-    for (uint32_t c = 0; c < C; ++c) sq = std::fma((double)src[c], (double)src[c], sq);
+    const double sq = squared_norm_d(src, C);
     const double s = target_norm / std::sqrt(std::max(sq, 1e-30));
     for (uint32_t c = 0; c < C; ++c) atom[c] = (float)((double)src[c] * s);
 }

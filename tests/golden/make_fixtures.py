@@ -40,6 +40,7 @@ and tests/golden/hsdr_encode_fixtures.npz (`encode` argument):
              uses that CPU's approximate reciprocal square root).
   fit_<i>_w, fit_<i>_stream, fit_<i>_cfg  the same compress with ksvd_iters = 3..6 (atom
              updates and re-encodes); cfg = (tile_rows, tile_cols, K, stages, k, iters).
+             Written with OMP_NUM_THREADS=1 (the tile-norm mean's reduction in tile order).
 
 and tests/golden/sdr_fixtures.npz (`sdr` argument):
 
@@ -65,6 +66,12 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
+
+if sys.argv[1:] in (["encode"], ["hsda"], ["hsda_grouped"]):
+    # one OpenMP thread: atomUpdateStep's tile-norm reduction (HierarchicalSDRStrategy.cpp
+    # :376) then sums the tiles in order, which the library restates. Set before any library
+    # that starts the OpenMP runtime is loaded (the oracle's is, at import).
+    os.environ["OMP_NUM_THREADS"] = "1"
 
 import oracle  # noqa: E402
 

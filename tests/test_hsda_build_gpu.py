@@ -5,11 +5,9 @@ hsda_grouped_fixtures.npz, written by the reference compiled here): a 1-row-tile
 capped fit pool (reservoir sampling), several tile widths (one dictionary each, in the
 reference's bucket order) and 2-D tiles with a matrix that is skipped.
 
-Bars, as for the single-matrix compress with K-SVD passes (test_hsdr_encode_gpu.py): archive
-layout, dictionary configs (padding bytes aside), stage scales, segment names, dictionary
-indices, sizes and types, HSDC headers and the skipped set exactly; codes equal in >= 99% of
-slots; every dictionary within 1e-4 of its magnitude; each matrix's reconstruction error
-within 0.1% of the reference archive's.
+Bar, as for the single-matrix compress (test_hsdr_encode_gpu.py): the reference's archive
+byte for byte on any host CPU, except the two padding bytes of each dictionary's
+HierarchicalSDRConfig record, which the reference writes uninitialised; and the skipped set.
 """
 import os
 
@@ -27,26 +25,36 @@ def _recon(dicts, seg, shape):
     return oracle.hsdr_decompress(oracle.hsdc_to_hsdr(seg[4], d)).reshape(shape)
 
 
+def _config_padding(b):
+    """Offsets of the two compiler padding bytes of every dictionary's 20-byte config record
+    (after u16 x 3 and u8 x 4; the layout oracle.hsda_parse reads)."""
+    import struct
+
+    (nd,) = struct.unpack_from("<I", b, 8)
+    off, pad = 16, set()
+    for _ in range(nd):
+        pad |= {off + 10, off + 11}
+        off += 20
+        (nsc,) = struct.unpack_from("<I", b, off)
+        off += 4 + 4 * nsc
+        (na,) = struct.unpack_from("<I", b, off)
+        off += 4 + 4 * na
+    return pad
+
+
 def _compare(ours, ref, mats, skipped_ours, skipped_ref):
-    assert ours[:16] == ref[:16]   # magic, version, dictionary and segment counts
     assert skipped_ours == skipped_ref
+    assert len(ours) == len(ref)
+    a = np.frombuffer(ours, np.uint8)
+    b = np.frombuffer(ref, np.uint8)
+    differ = set(np.nonzero(a != b)[0].tolist())
+    assert differ <= _config_padding(ref), sorted(differ)[:8]
+    # and each matrix reconstructs from our archive as from the reference's
     od, osg = oracle.hsda_parse(ours)
     rd, rsg = oracle.hsda_parse(ref)
-    for a, b in zip(od, rd):
-        for key in ("tile_rows", "tile_cols", "n_atoms", "n_stages", "k", "stage_decay"):
-            assert a[key] == b[key], key
-        assert np.array_equal(a["stage_scales"], b["stage_scales"])
-        assert np.abs(a["atoms"] - b["atoms"]).max() <= 1e-4 * np.abs(b["atoms"]).max()
-    for a, b in zip(osg, rsg):
-        assert a[:4] == b[:4]              # name, dictionary index, original size, type
-        assert a[4][:32] == b[4][:32]      # HSDC header
-        ca = np.frombuffer(a[4][32:], "<u2")
-        cb = np.frombuffer(b[4][32:], "<u2")
-        assert (ca == cb).mean() >= 0.99, a[0]
-        w = mats[a[0]]
-        em = np.linalg.norm(_recon(od, a, w.shape) - w)
-        er = np.linalg.norm(_recon(rd, b, w.shape) - w)
-        assert abs(em - er) <= 1e-3 * er, a[0]
+    for sa, sb in zip(osg, rsg):
+        w = mats[sa[0]]
+        assert np.array_equal(_recon(od, sa, w.shape), _recon(rd, sb, w.shape)), sa[0]
 
 
 def test_group_matches_reference_archive(gpu):

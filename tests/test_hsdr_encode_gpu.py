@@ -5,11 +5,10 @@ Bars:
     stream's dictionary) and against the oracle (pinned in test_hsdr_encode_oracle.py) on
     larger random cases; K, tile sizes with and without an 8-element chunk, many tiles per
     workgroup and one;
-  * compress with K-SVD passes (ksvd_iters > 0): within the bars of
-    test_compress_refined_matches_reference;
-  * compress (ksvd_iters = 0): the reference's stream byte for byte (on a CPU whose
-    approximate reciprocal square root is the fixtures'; elsewhere header, stage scales, edge
-    strips and codes exact around a dictionary within 8 ulp).
+  * compress, with and without K-SVD passes: the reference's stream byte for byte, on any
+    host CPU (the initialisation takes the approximate reciprocal square root of the CPU the
+    fixtures were written on from a table, and sums the tile norms in the reference build's
+    order; the fixtures were written with one OpenMP thread).
 """
 import os
 
@@ -100,10 +99,8 @@ def test_encode_large_tile_falls_back_to_one_per_workgroup(gpu, monkeypatch):
 
 
 def test_compress_matches_reference(gpu, enc):
-    """The whole stream is the reference's byte for byte when this CPU's reciprocal square
-    root is the one the fixtures were written with (the dictionary is then identical, see
-    test_init_dictionary_matches_reference); on another CPU model the dictionary may differ
-    in the last bits (as the reference's own would), and the rest is checked around it."""
+    """The whole stream (header, dictionary, stage scales, codes, edge strips) is the
+    reference's byte for byte, whatever CPU this host has."""
     from cortexsdr_amd import encode
 
     for i in range(n_cases(enc)):
@@ -113,29 +110,20 @@ def test_compress_matches_reference(gpu, enc):
         assert len(s) == len(ref)
         v, D, g, codes = stream_parts(s)
         rv, rD, rg, rcodes = stream_parts(ref)
-        assert s[:36] == ref[:36] and np.array_equal(g, rg)
-        assert s[v.off_edge:] == ref[rv.off_edge:]
-        if np.array_equal(D.view(np.uint32), rD.view(np.uint32)):
-            assert s == ref, f"case {i}"
-        else:
-            ulp = np.abs(D.view(np.int32).astype(np.int64) - rD.view(np.int32).astype(np.int64))
-            # two Newton-refined reciprocal square roots (atom norm, global scale), each
-            # within ~3 ulp of the CPU-independent value
-            assert ulp.max() <= 8, f"case {i}: dictionary differs by {ulp.max()} ulp"
-            t = tiles_of(w, v.tile_rows, v.tile_cols)
-            assert np.array_equal(codes, gpu_codes(gpu, t, D, g, S, k))
+        ulp = np.abs(D.view(np.int32).astype(np.int64) - rD.view(np.int32).astype(np.int64))
+        assert ulp.max() == 0, f"case {i}: dictionary differs by {ulp.max()} ulp"
+        assert np.array_equal(codes, rcodes), f"case {i}"
+        assert s == ref, f"case {i}"
         assert oracle.hsdr_decompress(s).shape == w.shape
 
 
 def test_compress_refined_matches_reference(gpu, enc):
     """ksvd_iters > 0 (atomUpdateStep then matching pursuit again, per pass): the reference's
-    per-atom corrections are double sums in its user order, restated exactly, but two of its
-    sums (the tile-norm mean under OpenMP, a vectorised re-seed norm) and, on another CPU
-    model, the initial dictionary end in different last bits; the bars are: codes equal in
-    >= 99% of slots, the dictionary within 1e-4 of its magnitude, the reconstruction error
-    within 0.1% of the reference's. The codes the reference writes are matching pursuit over
-    its own refined dictionary, so on any CPU the GPU's matching pursuit over that dictionary
-    must give them bit for bit."""
+    stream byte for byte on any host CPU. Its per-atom corrections are double sums in its user
+    order; its tile-norm mean and re-seed norms are sums in the order its -O3 -ffast-math
+    AVX2 build executes (the mean with one OpenMP thread, as the fixtures were written); the
+    initial dictionary takes the fixtures' CPU's reciprocal square root. Also: the GPU's
+    matching pursuit over the reference's own refined dictionary gives its codes."""
     from cortexsdr_amd import encode
 
     n = len([k for k in enc.files if k.startswith("fit_") and k.endswith("_stream")])
@@ -146,13 +134,11 @@ def test_compress_refined_matches_reference(gpu, enc):
         s = encode.compress(w, tr, tc, K, S, k, ksvd_iters=it, stage_decay=0.5)
         v, D, g, codes = stream_parts(s)
         rv, rD, rg, rcodes = stream_parts(ref)
-        assert s[:36] == ref[:36] and np.array_equal(g, rg)
-        assert s[v.off_edge:] == ref[rv.off_edge:]
-        assert (codes == rcodes).mean() >= 0.99, f"case {i}"
-        assert np.abs(D - rD).max() <= 1e-4 * np.abs(rD).max(), f"case {i}"
-        em = np.linalg.norm(oracle.hsdr_decompress(s) - w)
-        er = np.linalg.norm(oracle.hsdr_decompress(ref) - w)
-        assert abs(em - er) <= 1e-3 * er, f"case {i}"
+        ulp = np.abs(D.view(np.int32).astype(np.int64) - rD.view(np.int32).astype(np.int64))
+        print(f"fit {i}: dictionary {ulp.max()} ulp, codes {np.mean(codes == rcodes):.5f}")
+        assert ulp.max() == 0, f"case {i}"
+        assert np.array_equal(codes, rcodes), f"case {i}"
+        assert s == ref, f"case {i}"
         t = tiles_of(w, rv.tile_rows, rv.tile_cols)
         assert np.array_equal(gpu_codes(gpu, t, rD, rg, S, k), rcodes), f"case {i}"
 
