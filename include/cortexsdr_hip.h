@@ -249,9 +249,10 @@ CSDR_API size_t csdr_hsdr_compress_bytes(uint32_t rows, uint32_t cols, uint16_t 
  * host code: atom j = the tile std::uniform_int_distribution picks over std::mt19937(0xC0DE),
  * unit length, all scaled by the mean tile norm / max(1, sqrt(n_stages * k_per_stage)); in
  * the reference build's arithmetic (its -ffast-math 1/sqrt is the CPU's approximate
- * reciprocal square root plus one Newton step, reproduced instruction for instruction), so
- * D (host, n_atoms x tile_dim) is the reference's bit for bit on the same CPU. tiles: host,
- * n_tiles x tile_dim. */
+ * reciprocal square root plus one Newton step; the approximation is taken from a table of the
+ * Intel Xeon the reference's golden outputs were written on, and the tile norms are summed in
+ * the order its vectorised loop uses), so D (host, n_atoms x tile_dim) is that reference run's
+ * bit for bit on any host CPU. tiles: host, n_tiles x tile_dim. */
 CSDR_API int csdr_hsdr_init_dictionary(const float* tiles, uint32_t n_tiles, uint32_t tile_dim,
                                        uint16_t n_atoms, uint8_t n_stages, uint8_t k_per_stage,
                                        float* D);
