@@ -29,12 +29,16 @@
 // partial sums are added into Y with device-scope float atomics. A unit's X slice is staged
 // in LDS by the workgroup (two barriers per unit), or, for a single 16-column tile, each wave
 // loads its X operands from the workspace one unit ahead and the waves run without barriers.
+// At M <= 16 with fp16 X and 4 or 8 slots the persistent kernel is the dictionary route
+// instead (qroute_kernel): no weight is decoded; each unit's Q_b = D . X_b is formed on the
+// matrix cores and every row gathers its slots' rows of Q_b from LDS.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 #include "hsdb_impl.hpp"
@@ -371,6 +375,312 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
     if (cur_strip >= 0) flush(cur_g, cur_strip);
 }
 
+// ---- main, one 16-column tile (M <= 16): the dictionary route. Per unit (256-row strip,
+// block column b) the workgroup forms Q_b = D . X_b (K atoms x 16 columns) on the matrix
+// cores and each row then gathers its slots' rows of Q_b from LDS:
+//   y[r][m] += g0 * sum_j (c_j * g_j / g0) * Q_b[idx_j][m],
+// 32 bytes of LDS per (row, slot) where decoding the weights reads the atom's 128.
+// - The dictionary lives in registers for the whole launch: 16 waves x 64 atoms, each wave's
+//   atoms as the B operands of v_mfma_f32_16x16x32_f16 (8 x 16 bytes per lane), so LDS holds
+//   only Q (two 32 KiB buffers: Q_{u+1} is formed while unit u is gathered, one barrier per
+//   unit).
+// - Q^T = X_b^T . D^T: lane (n = l % 16, q = l / 16) of a 16-atom tile ends with atom n's
+//   columns 4q .. 4q + 3, one 8-byte LDS store. Q rows are 32 bytes, their two 16-byte halves
+//   swapped on odd atoms so that the gather's 16-byte reads of random rows use all bank groups.
+//   Q is stored in fp16 (fp32 accumulation; |Q| <= ||x_b|| for unit-norm atoms).
+// - Gather: lane (row l % 16 of the wave's 16, slot group q) takes slots q S/4 .. of its row
+//   (S/4 code words, no lane loads another's) and all 16 columns (two 16-byte reads per slot,
+//   fp16 x fp16 -> fp32 multiply-adds); the four slot groups of a row are summed by shuffles
+//   when the strip ends, then one device-scope atomic per (row, column) into Y.
+// - Loads: each unit's code words and the X operands of the unit after it form one bundle,
+//   issued RD units ahead into a register ring (the wait for a bundle's X also covers every
+//   earlier load, so both streams share one depth).
+// A unit's position: strip, block column b, and the chunk holding b (first column b0,
+// width nbc), advanced one unit at a time within one matrix whose geometry the caller keeps
+// in registers (reading it from the kernel arguments inside the loop puts a scalar load and
+// its wait, which also drains every LDS operation in flight, into every unit).
+struct UnitCursor {
+    int strip, b, b0, nbc;
+};
+
+struct SegGeom {
+    int NB, NBc, R, nstrips, nfull;  // nfull: columns in full chunks
+};
+
+__device__ __forceinline__ void cursor_chunk(const SegGeom& s, UnitCursor& c) {
+    if (c.b < s.nfull) {
+        c.b0 = c.b & ~(s.NBc - 1);
+        c.nbc = s.NBc;
+        return;
+    }
+    uint32_t cc, b0, nbc;
+    csdr::chunk_of((uint32_t)c.b, (uint32_t)s.NB, (uint32_t)s.NBc, cc, b0, nbc);
+    c.b0 = (int)b0;
+    c.nbc = (int)nbc;
+}
+
+// Next unit of the same matrix (wrapping past its last unit, so a cursor always names valid
+// codes and X: the pipeline's loads past a range's end stay unconditional and in bounds).
+__device__ __forceinline__ void cursor_next(const SegGeom& s, UnitCursor& c) {
+    if (++c.b == s.NB) {
+        c.b = 0;
+        if (++c.strip == s.nstrips) c.strip = 0;
+    }
+    if (c.b == 0 || c.b >= c.b0 + c.nbc) cursor_chunk(s, c);
+}
+
+template <int SLOTS, bool XS>
+__global__ __launch_bounds__(1024) void qroute_kernel(MParams p) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr int SPL = SLOTS / 4;   // slots per lane
+    constexpr int NP = XS ? 2 : 1;   // X parts (fp32 X: hi, lo)
+    constexpr int QB = kMaxAtoms * 16;  // fp16 per Q buffer
+    typedef typename std::conditional<SPL == 4, u32x4,
+            typename std::conditional<SPL == 2, uint2, uint32_t>::type>::type cword_t;
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem16[];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int q = lane >> 4, rl = lane & 15;
+    const int U = p.total_units;
+    const int u0 = (int)((long long)U * blockIdx.x / gridDim.x);
+    const int u1 = (int)((long long)U * (blockIdx.x + 1) / gridDim.x);
+    if (u0 >= u1) return;
+    const int M = p.M;
+
+    // the units of one matrix at a time: its atoms in registers, then a pipeline over its units
+    // in which every load is unconditional (a load under a branch makes the compiler's wait
+    // counts assume the worst at the join, which drained the pipeline every unit)
+    for (int s0 = u0; s0 < u1;) {
+        const int g = find_matrix(p, s0, -1);
+        const MDesc& d = p.m[g];
+        const int s1 = min(u1, d.u_base + d.u_count);
+        half8 dreg[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int a = min(wave * 64 + t * 16 + rl, d.K - 1);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                dreg[t][c] = __builtin_bit_cast(
+                    half8, *reinterpret_cast<const u32x4*>(d.dict16p + (size_t)a * 64 + (2 * q + c) * 8));
+        }
+        // this lane's slots' gains relative to g0 (fp16), chosen from uniform loads
+        _Float16 gl[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const uint32_t a0 = d.grel[j], a1 = d.grel[SPL + j], a2 = d.grel[2 * SPL + j],
+                           a3 = d.grel[3 * SPL + j];
+            const uint32_t w = q == 0 ? a0 : (q == 1 ? a1 : (q == 2 ? a2 : a3));
+            gl[j] = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+        }
+        const _Float16* xt0 = d.xt + (size_t)rl * d.C_full + q * 16;
+        const size_t nxt = (size_t)p.Mpad * d.C_full;
+        const int K = d.K;
+        SegGeom sg;
+        sg.NB = d.NB;
+        sg.NBc = d.NBc;
+        sg.R = d.R;
+        sg.nstrips = (d.R + 255) >> 8;
+        sg.nfull = d.NB & ~(d.NBc - 1);
+        const uint32_t* codes = d.codes;
+        float* y = d.y;
+        const float g0 = d.g0;
+
+        u32x4 xr[2][NP][2];
+        cword_t cr[2];
+        float ya[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ya[e] = 0.0f;
+
+        auto load_x = [&](const UnitCursor& c, u32x4 (&dst)[NP][2]) {
+            const _Float16* src = xt0 + (size_t)c.b * 64;
+#pragma unroll
+            for (int part = 0; part < NP; ++part)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc)
+                    dst[part][cc] = *reinterpret_cast<const u32x4*>(src + part * nxt + cc * 8);
+        };
+        auto load_codes = [&](const UnitCursor& c, cword_t& dst) {
+            const int r = min(c.strip * 256 + wave * 16 + rl, sg.R - 1);
+            const size_t w =
+                ((size_t)c.b0 * sg.R + (size_t)r * c.nbc + (c.b - c.b0)) * SLOTS + q * SPL;
+            dst = *reinterpret_cast<const cword_t*>(codes + w);
+        };
+        // Q of a unit from its X operands xo, two atom tiles (t0, t0 + 1) at a time, each pair
+        // then stored into buffer buf
+        auto q_mfma = [&](const u32x4 (&xo)[NP][2], floatx4 (&acc)[2], int t0) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                for (int part = 0; part < NP; ++part)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, xo[part][cc]), dreg[t0 + t][cc], acc[t], 0, 0, 0);
+        };
+        auto q_store = [&](const floatx4 (&acc)[2], int buf, int t0) {
+            _Float16* Qb = smem16 + (size_t)buf * QB;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int a = wave * 64 + (t0 + t) * 16 + rl;
+                if (wave * 64 + (t0 + t) * 16 < K) {  // (uniform per wave)
+                    const h2 lo = h2{(_Float16)acc[t][0], (_Float16)acc[t][1]};
+                    const h2 hi = h2{(_Float16)acc[t][2], (_Float16)acc[t][3]};
+                    const uint2 v = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+                    // 8-byte piece q of the 32-byte row at q ^ 2 (a bit 2): the two halves read
+                    // by the gather stay 16-byte granules, spread over all bank groups
+                    *reinterpret_cast<uint2*>(Qb + (size_t)a * 16 + ((q ^ ((a >> 1) & 2)) * 4)) = v;
+                }
+            }
+        };
+        auto words_of = [&](const cword_t& cw, uint32_t (&words)[SPL]) {
+            if constexpr (SPL == 1) {
+                words[0] = cw;
+            } else if constexpr (SPL == 2) {
+                words[0] = cw.x;
+                words[1] = cw.y;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) words[j] = cw[j];
+            }
+        };
+        auto g_read = [&](const uint32_t (&words)[SPL], int buf, u32x4 (&h)[SPL][2]) {
+            const _Float16* Qb = smem16 + (size_t)buf * QB;
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) {
+                const uint32_t at = words[j] & 0x7FFFu;
+                const uint32_t sw = (at >> 2) & 1;
+                const _Float16* row = Qb + at * 16;
+                h[j][0] = *reinterpret_cast<const u32x4*>(row + sw * 8);
+                h[j][1] = *reinterpret_cast<const u32x4*>(row + (sw ^ 1) * 8);
+            }
+        };
+        // the gather's multiply-adds of slot j
+        auto g_acc = [&](const uint32_t (&words)[SPL], const u32x4 (&h)[SPL][2], int j) {
+            const _Float16 cf = __builtin_bit_cast(_Float16, (uint16_t)(words[j] >> 16)) * gl[j];
+            const float cfl = (float)cf;
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t dw = h[j][half][k];
+                    const h2 pr = __builtin_bit_cast(h2, dw);
+                    ya[half * 8 + 2 * k] = fmaf(cfl, (float)pr[0], ya[half * 8 + 2 * k]);
+                    ya[half * 8 + 2 * k + 1] = fmaf(cfl, (float)pr[1], ya[half * 8 + 2 * k + 1]);
+                }
+        };
+        // the strip's row sums: the four slot groups of a row summed by shuffles, then the
+        // wave's 16 x 16 tile through LDS so that each atomic instruction covers four whole rows
+        // of Y (token-major: four whole columns) instead of 16 scattered 16-byte pieces
+        auto flush = [&](int strip) {
+            float* T = reinterpret_cast<float*>(smem16 + 2 * (size_t)QB) + wave * 256;
+            // reduce-scatter over the four slot groups (lanes l, l ^ 16, l ^ 32, l ^ 48): lane q
+            // ends with columns 8 (q & 1) + 4 (q >> 1) .. + 3 of its row
+            const bool b = q & 1, c = q >> 1;
+            float t[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float keep = b ? ya[8 + k] : ya[k];
+                const float send = b ? ya[k] : ya[8 + k];
+                t[k] = keep + __shfl_xor(send, 16, 64);
+            }
+            float4 w;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float keep = c ? t[4 + k] : t[k];
+                const float send = c ? t[k] : t[4 + k];
+                w[k] = keep + __shfl_xor(send, 32, 64);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) ya[e] = 0.0f;
+            *reinterpret_cast<float4*>(T + rl * 16 + 8 * (q & 1) + 4 * (q >> 1)) = w;
+            const int r0 = strip * 256 + wave * 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // row-major: rows 4i + lane / 16, column lane % 16; token-major: rows lane % 16,
+                // column 4i + lane / 16
+                const int rr = p.tm ? rl : 4 * i + q;
+                const int m = p.tm ? 4 * i + q : rl;
+                const float v = T[rr * 16 + m];
+                const int r = r0 + rr;
+                if (r < sg.R && m < M)
+                    __hip_atomic_fetch_add(y + (p.tm ? (size_t)m * sg.R + r : (size_t)r * M + m),
+                                           v * g0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        };
+
+        // cursors: gathered unit v, its successor (Q formed), the next bundle's codes (v + 2)
+        // and X (v + 3); bundle w = (codes of w, X of w + 1), two in flight
+        UnitCursor cg;
+        {
+            const int lu = s0 - d.u_base;
+            cg.strip = lu / sg.NB;
+            cg.b = lu - cg.strip * sg.NB;
+            cursor_chunk(sg, cg);
+        }
+        UnitCursor cm = cg;
+        cursor_next(sg, cm);
+        UnitCursor cc = cg, cx = cm;
+        {
+            u32x4 x0[NP][2];
+            load_x(cg, x0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                load_x(cx, xr[i]);
+                load_codes(cc, cr[i]);
+                cursor_next(sg, cx);
+                cursor_next(sg, cc);
+            }
+#pragma unroll
+            for (int t0 = 0; t0 < 4; t0 += 2) {
+                floatx4 acc[2];
+                q_mfma(x0, acc, t0);
+                q_store(acc, 0, t0);
+            }
+        }
+        __syncthreads();
+        // per unit: the gather's LDS reads of Q_v, the matrix-core steps of Q_{v+1} while they
+        // are in flight, the gather's multiply-adds, then Q_{v+1} into the other buffer
+        auto step = [&](int v, auto S) {
+            constexpr int sl = decltype(S)::value;
+            const bool more = v + 1 < s1;
+            uint32_t words[SPL];
+            words_of(cr[sl], words);
+            u32x4 h[SPL][2];
+            g_read(words, (v - s0) & 1, h);
+            // tile pairs interleaved with the slots' multiply-adds
+            constexpr int JP = SPL >= 2 ? SPL / 2 : 1;  // slots per tile pair
+#pragma unroll
+            for (int t0 = 0; t0 < 4; t0 += 2) {
+                floatx4 acc[2];
+                if (more) q_mfma(xr[sl], acc, t0);
+#pragma unroll
+                for (int jj = 0; jj < JP; ++jj) {
+                    const int j = (t0 / 2) * JP + jj;
+                    if (j < SPL) g_acc(words, h, j);
+                }
+                if (more) q_store(acc, (v + 1 - s0) & 1, t0);
+            }
+            load_x(cx, xr[sl]);
+            load_codes(cc, cr[sl]);
+            if (!more || cm.strip != cg.strip) flush(cg.strip);
+            cg = cm;
+            cursor_next(sg, cm);
+            cursor_next(sg, cc);
+            cursor_next(sg, cx);
+            __syncthreads();
+        };
+        int v = s0;
+        for (; v + 1 < s1; v += 2) {
+            step(v, std::integral_constant<int, 0>{});
+            step(v + 1, std::integral_constant<int, 1>{});
+        }
+        if (v < s1) step(v, std::integral_constant<int, 0>{});
+        s0 = s1;
+    }
+}
+
 // Columns of X the kernels see: M rounded up to a power of two >= 16 (<= 256), beyond 256 to
 // a multiple of 256, so every launch covers a power-of-two tile of 16 NT columns.
 int padded_m(int M) {
@@ -399,6 +709,13 @@ constexpr int rows_for(int) { return 1; }
 // M = 16 36.2 -> 33.3 us per call; at two tiles (M = 32) slower, 40.4 -> 44.0; at four the
 // prefetched operands spill
 constexpr bool x_in_regs(int nt, bool) { return nt == 1; }
+
+// The dictionary route for one 16-column tile (M <= 16); CSDR_HSDB_QROUTE=0 keeps the
+// weight-decoding kernel there.
+bool qroute_enabled() {
+    const char* e = std::getenv("CSDR_HSDB_QROUTE");
+    return !(e && *e && std::atoi(e) == 0);
+}
 
 template <int NT, bool XS, int SLOTS>
 int launch_one(const MParams& p, int grid, size_t lds, hipStream_t st) {
@@ -542,6 +859,22 @@ int mfma_matmul(int n, const csdr_hsdb* const* segs, const void* const* xs, int 
     }
     p.total_units = units;
     const int grid = std::max(1, std::min(units, ncu));
+    const int slots0 = (int)segs[0]->slots;
+    if (nt == 1 && !xsplit && (slots0 == 4 || slots0 == 8) && qroute_enabled()) {
+        // one 16-column tile of fp16 X: Q_b formed per unit on the matrix cores, rows gathered
+        // from LDS (fp32 X and 16 slots keep the decoding kernel: their operand rings spill)
+        // two Q buffers, then a 16 x 16 fp32 tile per wave for the strip flushes
+        const size_t qlds = (size_t)2 * kMaxAtoms * 16 * sizeof(_Float16) + 16 * 256 * sizeof(float);
+        auto go = [&](auto kern) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)qlds);
+            kern<<<grid, 1024, qlds, st>>>(p);
+        };
+        if (slots0 == 4) go(qroute_kernel<4, false>);
+        else go(qroute_kernel<8, false>);
+        CSDR_LAUNCH_CHECK("hsdb qroute");
+        return CSDR_OK;
+    }
     for (int m0 = 0; m0 < p.Mpad; m0 += mt) {
         MParams q = p;
         q.m0 = m0;

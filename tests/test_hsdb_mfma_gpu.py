@@ -1,10 +1,13 @@
-"""GPU parity of the batched (M >= 2) HSDB product on matrix cores (HK2: decoded 64-column
-tiles x X with v_mfma_f32_16x16x16f16, fp32 accumulation) against the CPU oracle's fp32
-fused product, through the C-ABI.
+"""GPU parity of the batched (M >= 9) HSDB product on matrix cores against the CPU oracle's
+fp32 fused product, through the C-ABI. Two kernels serve it: decoded 64-column weight tiles
+times X (v_mfma_f32_16x16x32_f16, fp32 accumulation), and at M <= 16 with fp16 X and 4 or 8
+slots the dictionary route (Q_b = D . X_b per 256-row strip and block column on the matrix
+cores, stored in fp16, each row's slots gathered from it with fp32 multiply-adds).
 
-Bar: relative L2 <= 1e-3 (the path's tolerance at fp32 accumulation). The kernel rounds the
-dictionary and each decoded weight to fp16 once (fp32 X is split into fp16 hi + lo), which
-puts it near 2e-4; the printed errors show the margin."""
+Bar: relative L2 <= 1e-3 (the path's tolerance at fp32 accumulation). The kernels round the
+dictionary to fp16 once, and each decoded weight (decoding kernel) or each Q value
+(dictionary route) to fp16 (fp32 X is split into fp16 hi + lo), which puts them near 2e-4;
+the printed errors show the margin."""
 import ctypes as C
 import functools
 import os
@@ -67,11 +70,28 @@ def test_batched_shapes(gpu, R, Cc, K, s, M, dtype):
     assert err <= TOL
 
 
-def test_group_bias_accumulate(gpu):
+@pytest.mark.parametrize("R,Cc,K,s,M", [
+    (300, 896, 1024, 8, 9),      # ragged strip, a remainder chunk (14 block columns)
+    (1000, 896, 256, 4, 16),     # 4 slots, a quarter of the waves holding atoms
+    (513, 704, 1024, 8, 13),     # one row past two 256-row strips, 11 block columns
+    (4096, 1024, 1024, 16, 16),  # 16 slots (the weight-decoding kernel)
+])
+def test_dictionary_route_shapes(gpu, R, Cc, K, s, M):
+    # M <= 16 with fp16 X: Q_b = D . X_b per unit on the matrix cores, rows gathered from LDS
+    stream = synth.hsdb_layer(R, Cc, K, s, seed_dict=12, seed_codes=13)
+    x = synth.activations(Cc, M, seed=14, dtype=np.float16)
+    y = product(gpu, stream, x, np.float16)
+    ref = oracle.hsdb_matmul(stream, x.astype(np.float32))
+    err = rel_l2(y, ref)
+    print(f"R={R} C={Cc} K={K} s={s} M={M} rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("M", [16, 24])
+def test_group_bias_accumulate(gpu, M):
     from cortexsdr_amd import _lib
     from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
 
-    M = 24
     shapes = [(896, 896), (128, 896), (4864, 896)]
     streams = [synth.hsdb_layer(R, Cc, 1024, 8, seed_dict=1, seed_codes=20 + i)
                for i, (R, Cc) in enumerate(shapes)]
