@@ -594,6 +594,7 @@ __device__ __forceinline__ void x4(const XT* __restrict__ x, int e, bool vec, fl
 template <class F>
 struct Units {
     static constexpr bool value = false;
+    static constexpr bool kUnitSums = false;
 };
 // x[e .. e + 7] in fp16 as four dwords of value pairs (16-byte aligned x)
 template <typename XT>
@@ -615,11 +616,19 @@ constexpr uint32_t kOnesH2 = 0x3C003C00u;  // fp16 (1.0, 1.0)
 template <bool HAS_M>
 struct UnitsQ4 {
     static constexpr bool value = true;
+    static constexpr bool kUnitSums = true;  // x sum over values 16 u .. 16 u + 15 (dotx)
     static constexpr int kPerBlock = 2;
     static constexpr int BB = HAS_M ? 20 : 18, kQs = HAS_M ? 4 : 2;
     template <typename XT>
     __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
                                 bool xvec) {
+        return dotx<false>(s32, ro, u, x, xvec, nullptr);
+    }
+    // US: fp16 x in LDS with the unit's x sum given (us[u], formed once for all rows by
+    // unit_xsum in the same order as below)
+    template <bool US, typename XT>
+    __device__ static float dotx(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                 bool xvec, const float* us) {
         const int blk = u >> 1, hf = u & 1;
         const int bo = ro + blk * BB;
         const uint32_t hd = lds32(s32, bo);
@@ -638,9 +647,10 @@ struct UnitsQ4 {
                     const uint32_t pk = __builtin_amdgcn_perm(H, L, 0x0C040C00u + 0x00010001u * k)
                                         << 6;
                     a = fdot2u(pk, xw[k], a);
-                    sx = fdot2u(xw[k], kOnesH2, sx);
+                    if constexpr (!US) sx = fdot2u(xw[k], kOnesH2, sx);
                 }
             }
+            if constexpr (US) sx = us[u];
             a *= 0x1p18f;
         } else {
 #pragma unroll
@@ -673,10 +683,16 @@ struct Units<Q4_1> : UnitsQ4<true> {};
 template <int BB_, int BE_, int QOFF, bool SCALE_F32>
 struct UnitsQ8 {
     static constexpr bool value = true;
+    static constexpr bool kUnitSums = true;
     static constexpr int kPerBlock = BE_ / 16;
     template <typename XT>
     __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
                                 bool xvec) {
+        return dotx<false>(s32, ro, u, x, xvec, nullptr);
+    }
+    template <bool US, typename XT>
+    __device__ static float dotx(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                 bool xvec, const float* us) {
         const int blk = u / kPerBlock, j = u - blk * kPerBlock;
         const int bo = ro + blk * BB_;
         const uint32_t hd = lds32(s32, bo);
@@ -696,10 +712,13 @@ struct UnitsQ8 {
                     const uint32_t p23 = __builtin_amdgcn_perm(0u, w, 0x0C030C02u) << 2;
                     a = fdot2u(p01, xw[2 * h], a);
                     a = fdot2u(p23, xw[2 * h + 1], a);
-                    sx = fdot2u(xw[2 * h], kOnesH2, sx);
-                    sx = fdot2u(xw[2 * h + 1], kOnesH2, sx);
+                    if constexpr (!US) {
+                        sx = fdot2u(xw[2 * h], kOnesH2, sx);
+                        sx = fdot2u(xw[2 * h + 1], kOnesH2, sx);
+                    }
                 }
             }
+            if constexpr (US) sx = us[u];
             return d * fmaf(-128.0f, sx, a * 0x1p22f);
         }
 #pragma unroll
@@ -731,10 +750,16 @@ template <int BB_, int BE_, int BITS>
 struct Units<Packed<BB_, BE_, BITS>> {
     using F = Packed<BB_, BE_, BITS>;
     static constexpr bool value = true;
+    static constexpr bool kUnitSums = true;
     static constexpr int kPerBlock = BE_ / 16;
     template <typename XT>
     __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
                                 bool xvec) {
+        return dotx<false>(s32, ro, u, x, xvec, nullptr);
+    }
+    template <bool US, typename XT>
+    __device__ static float dotx(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
+                                 bool xvec, const float* us) {
         const int blk = u / kPerBlock, j = u - blk * kPerBlock;
         const int bo = ro + blk * BB_;
         float d = csdr::h2f(lds32(s32, bo) & 0xFFFFu);
@@ -761,7 +786,7 @@ struct Units<Packed<BB_, BE_, BITS>> {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     a = fdot2u((qv[2 * k] | (qv[2 * k + 1] << 16)) << kUp, xw[k], a);
-                    sx = fdot2u(xw[k], kOnesH2, sx);
+                    if constexpr (!US) sx = fdot2u(xw[k], kOnesH2, sx);
                 }
             } else {
                 float xv[8];
@@ -773,6 +798,7 @@ struct Units<Packed<BB_, BE_, BITS>> {
                 }
             }
         }
+        if constexpr (US) sx = us[u];
         if (h16x) a *= (float)(1u << (24 - kUp));
         return d * fmaf(-(float)(1 << (BITS - 1)), sx, a);
     }
@@ -786,6 +812,7 @@ struct Units<Packed<BB_, BE_, BITS>> {
 template <>
 struct Units<Q6_K> {
     static constexpr bool value = true;
+    static constexpr bool kUnitSums = false;  // (units of four 4-value groups 32 apart)
     static constexpr int kPerBlock = 16;
     template <typename XT>
     __device__ static float dot(const uint32_t* s32, int ro, int u, const XT* __restrict__ x,
@@ -952,6 +979,13 @@ struct PipeM1<Packed<176, 256, 5>> {  // q5_k
 };
 constexpr int kPipeMinC = 8192;
 
+// LDS bytes of the pipelined kernel before the item slots: x, the row totals, the unit sums
+// (16-byte multiples)
+template <typename XT>
+__host__ __device__ constexpr int pipe_fixed_bytes(int C) {
+    return ((C * (int)sizeof(XT) + 15) & ~15) + kPipeMaxRows * 4 + (((C / 16) * 4 + 15) & ~15);
+}
+
 template <class F, typename XT>
 __global__ __launch_bounds__(kPipeThreads) void gguf_gemv_pipe_kernel(
     const uint8_t* __restrict__ W, int R, int C, const XT* __restrict__ x, float* __restrict__ y,
@@ -961,11 +995,14 @@ __global__ __launch_bounds__(kPipeThreads) void gguf_gemv_pipe_kernel(
     constexpr int BPC = pipe_blocks<F>();
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // LDS: x (C values), the row sums, then two item slots per wave
+    // LDS: x (C values), the row sums, the x sum of every 16-value unit (C / 16 floats: the
+    // formats' offset terms, formed once here instead of per row), then two item slots per
+    // wave
     XT* xs = reinterpret_cast<XT*>(gsm);
     const int xbytes = (C * (int)sizeof(XT) + 15) & ~15;
     float* rsum = reinterpret_cast<float*>(gsm + xbytes);
-    uint8_t* slots = gsm + xbytes + kPipeMaxRows * 4 + (size_t)wave * 2 * kPipeSlot;
+    float* usum = rsum + kPipeMaxRows;
+    uint8_t* slots = gsm + pipe_fixed_bytes<XT>(C) + (size_t)wave * 2 * kPipeSlot;
     const int nbr = C / F::BE, nch = (nbr + BPC - 1) / BPC;
     const int rw0 = blockIdx.x * rpg, rw1 = min(R, rw0 + rpg);
     const int nitems = max(0, rw1 - rw0) * nch;
@@ -1032,6 +1069,17 @@ __global__ __launch_bounds__(kPipeThreads) void gguf_gemv_pipe_kernel(
     }
     for (int i = tid; i < kPipeMaxRows; i += kPipeThreads) rsum[i] = 0.0f;
     __syncthreads();
+    if constexpr (Units<F>::kUnitSums && sizeof(XT) == 2) {
+        // each unit's x sum in the order the decoders accumulate it (bit-identical results)
+        const uint32_t* xw = reinterpret_cast<const uint32_t*>(xs);
+        for (int v = tid; v < C / 16; v += kPipeThreads) {
+            float sx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sx = fdot2u(xw[v * 8 + k], kOnesH2, sx);
+            usum[v] = sx;
+        }
+        __syncthreads();
+    }
     put(0, ring[0]);
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(gsm);
     float acc = 0.0f;
@@ -1047,7 +1095,13 @@ __global__ __launch_bounds__(kPipeThreads) void gguf_gemv_pipe_kernel(
             if constexpr (Units<F>::value) {
                 const int ro = (int)(slots - gsm) + sl * kPipeSlot + lead;
                 const int nu = nb * Units<F>::kPerBlock;
-                for (int u = lane; u < nu; u += 64) acc += Units<F>::dot(s32, ro, u, xp, true);
+                if constexpr (Units<F>::kUnitSums && sizeof(XT) == 2) {
+                    const float* up = usum + cb0 * (F::BE / 16);
+                    for (int u = lane; u < nu; u += 64)
+                        acc += Units<F>::template dotx<true>(s32, ro, u, xp, true, up);
+                } else {
+                    for (int u = lane; u < nu; u += 64) acc += Units<F>::dot(s32, ro, u, xp, true);
+                }
             } else {
                 const uint8_t* rowp = slots + sl * kPipeSlot + lead;
                 const int ng = nb * (F::BE / 8);
@@ -1092,8 +1146,9 @@ int linear_of(const uint8_t* w, int R, int C, const void* x, int x_dtype, int M,
         const int grid = (R + kThreads / 64 - 1) / (kThreads / 64);
         const int xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
         // the pipelined kernel: x and the item slots in LDS, W within a 32-bit buffer range
-        const size_t xb = ((size_t)C * (x_dtype == CSDR_F16 ? 2 : 4) + 15) & ~(size_t)15;
-        const size_t lds_p = xb + kPipeMaxRows * 4 + (size_t)kPipeWaves * 2 * kPipeSlot;
+        const size_t lds_p = (size_t)(x_dtype == CSDR_F16 ? pipe_fixed_bytes<_Float16>(C)
+                                                          : pipe_fixed_bytes<float>(C)) +
+                             (size_t)kPipeWaves * 2 * kPipeSlot;
         const size_t wbytes = (size_t)R * (C / F::BE) * F::BB + 16;
         const char* ev = std::getenv("CSDR_GGUF_PIPE");
         const bool pipe_on = !(ev && *ev && std::atoi(ev) == 0);
