@@ -385,16 +385,18 @@ __global__ __launch_bounds__(W * 64) void mfma_kernel(MParams p) {
 //   only Q (two 32 KiB buffers: Q_{u+1} is formed while unit u is gathered, one barrier per
 //   unit).
 // - Q^T = X_b^T . D^T: lane (n = l % 16, q = l / 16) of a 16-atom tile ends with atom n's
-//   columns 4q .. 4q + 3, one 8-byte LDS store. Q rows are 32 bytes, their two 16-byte halves
-//   swapped on odd atoms so that the gather's 16-byte reads of random rows use all bank groups.
-//   Q is stored in fp16 (fp32 accumulation; |Q| <= ||x_b|| for unit-norm atoms).
+//   columns 4q .. 4q + 3, one 8-byte LDS store. Q rows are 32 bytes of four 8-byte pieces,
+//   piece q at q ^ 2 on atoms with bit 2 set, so that the gather's 16-byte halves stay whole
+//   and its reads of random rows spread over all bank groups. Q is stored in fp16 (fp32
+//   accumulation; |Q| <= ||x_b|| for unit-norm atoms).
 // - Gather: lane (row l % 16 of the wave's 16, slot group q) takes slots q S/4 .. of its row
 //   (S/4 code words, no lane loads another's) and all 16 columns (two 16-byte reads per slot,
-//   fp16 x fp16 -> fp32 multiply-adds); the four slot groups of a row are summed by shuffles
-//   when the strip ends, then one device-scope atomic per (row, column) into Y.
+//   fp16 x fp16 -> fp32 multiply-adds). When the strip ends the four slot groups of a row are
+//   reduce-scattered by shuffles and the wave's 16 x 16 tile goes through LDS, so that each
+//   device-scope atomic instruction into Y covers four whole rows.
 // - Loads: each unit's code words and the X operands of the unit after it form one bundle,
-//   issued RD units ahead into a register ring (the wait for a bundle's X also covers every
-//   earlier load, so both streams share one depth).
+//   issued two units ahead into a register ring (the wait for a bundle's X also covers every
+//   earlier load, so both streams share one depth). Every load is unconditional (see below).
 // A unit's position: strip, block column b, and the chunk holding b (first column b0,
 // width nbc), advanced one unit at a time within one matrix whose geometry the caller keeps
 // in registers (reading it from the kernel arguments inside the loop puts a scalar load and
