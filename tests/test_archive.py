@@ -91,6 +91,98 @@ def test_sdr_index_round_trip(tmp_path, version):
         a.find("missing")
 
 
+def _walk_reference_order(raw):
+    """Every index field of a version-2 .sdr archive, read in the order and widths of the
+    reference lister's loop (src/tool_sdr_inspect.cpp:39-83: u32-length strings, the POD
+    fields, then the metadata record and the two shapes), keeping the metadata values that
+    the lister reads and discards."""
+    pos = 0
+
+    def pod(fmt):
+        nonlocal pos
+        v = struct.unpack_from("<" + fmt, raw, pos)
+        pos += struct.calcsize("<" + fmt)
+        return v[0] if len(v) == 1 else v
+
+    def string():
+        nonlocal pos
+        n = pod("I")
+        s = raw[pos:pos + n].decode()
+        pos += n
+        return s
+
+    assert raw[:8] == b"CORTEXSR"
+    pos = 8
+    version, nseg, index_off = pod("I"), pod("Q"), pod("Q")
+    pos = index_off
+    out = []
+    for _ in range(nseg):
+        e = {"name": string(), "data_format": string(), "layer_type": string(),
+             "original_type": pod("B"), "strategy_id": pod("B"), "original_size": pod("Q"),
+             "compressed_size": pod("Q"), "data_offset": pod("Q"), "layer_name": string(),
+             "layer_index": pod("I")}
+        e["dims"] = e["sparsity"] = e["sorted"] = e["scale"] = e["zero_point"] = None
+        if pod("B"):
+            nd = pod("B")
+            e["dims"] = tuple(pod("I") for _ in range(nd))
+            e["sparsity"], e["sorted"] = pod("f"), pod("B")
+            e["scale"] = pod("f") if pod("B") else None
+            e["zero_point"] = pod("f") if pod("B") else None
+        shapes = []
+        for _ in range(2):
+            shapes.append(tuple(pod("I") for _ in range(pod("B"))) if pod("B") else ())
+        e["input_shape"], e["output_shape"] = shapes
+        out.append(e)
+    assert pos == len(raw)  # the index runs to the end of the file
+    return version, out
+
+
+def test_sdr_fields_in_reference_read_order(tmp_path):
+    """The writer puts every index field where the reference reads it, including the metadata
+    values the reference lister skips (sparsity, sorted, scale, zero point): the archive walked
+    in the lister's field order gives back the entries' values, and the C-ABI reader reports
+    the same for the fields it exposes."""
+    ents = _entries() + [
+        formats.SdrEntry(name="q.weight", payload=bytes(range(40)), dims=(5, 8), sparsity=0.25,
+                         sorted_indices=True, scale=0.125, zero_point=-3.5, layer_type="MatMul",
+                         layer_name="q", layer_index=7, input_shape=(2, 8), output_shape=(2, 5),
+                         strategy_id=5, original_size=160),
+        formats.SdrEntry(name="s.weight", payload=b"\x01\x02", dims=(2,), scale=2.0),
+    ]
+    path = str(tmp_path / "f.sdr")
+    formats.write_sdr(path, ents, version=2)
+    raw = open(path, "rb").read()
+    version, walked = _walk_reference_order(raw)
+    assert version == 2 and len(walked) == len(ents)
+    a = SdrArchive(path)
+    for i, (e, w) in enumerate(zip(ents, walked)):
+        assert w["name"] == e.name and w["data_format"] == e.data_format
+        assert w["layer_type"] == e.layer_type and w["layer_name"] == e.layer_name
+        assert (w["original_type"], w["strategy_id"], w["layer_index"]) == (
+            e.original_type, e.strategy_id, e.layer_index)
+        assert w["compressed_size"] == len(e.payload)
+        assert w["original_size"] == (e.original_size if e.original_size is not None
+                                      else len(e.payload))
+        assert raw[w["data_offset"]:w["data_offset"] + len(e.payload)] == bytes(e.payload)
+        if e.dims is None:
+            assert w["dims"] is None
+        else:
+            assert w["dims"] == tuple(e.dims)
+            assert w["sparsity"] == np.float32(e.sparsity)
+            assert w["sorted"] == (1 if e.sorted_indices else 0)
+            assert w["scale"] == (None if e.scale is None else np.float32(e.scale))
+            assert w["zero_point"] == (None if e.zero_point is None else np.float32(e.zero_point))
+        assert w["input_shape"] == tuple(e.input_shape)
+        assert w["output_shape"] == tuple(e.output_shape)
+        info = a.info(i)
+        for k in ("name", "data_format", "layer_type", "layer_name", "original_type",
+                  "strategy_id", "original_size", "compressed_size", "data_offset",
+                  "layer_index", "dims", "input_shape", "output_shape"):
+            assert info[k] == w[k], (i, k)
+        if w["dims"] is not None:
+            assert info["sparsity_ratio"] == w["sparsity"]
+
+
 def test_sdr_bad_archives_rejected(tmp_path):
     path = str(tmp_path / "m.sdr")
     formats.write_sdr(path, _entries())
