@@ -148,7 +148,11 @@ CSDR_API int csdr_hsdb_matmul_noalloc(const csdr_hsdb* seg, const void* x, int x
  * 64-column blocks, K <= 1024 atoms and 4/8/16 slots: an init launch and a matrix-core launch that
  * decodes 64-column tiles (dictionary and decoded weights rounded to fp16, fp32 X split into
  * fp16 hi + lo, fp32 accumulation: about 3e-4 relative L2 from the fp32 product); setting the
- * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. The workspace
+ * environment variable CSDR_HSDB_MFMA=0 keeps such calls on the fp32 P path. At M <= 16 with
+ * fp16 X and 4 or 8 slots the matrix-core launch forms Q = D . X per block column instead
+ * and gathers each row's slots from it. Q is stored in fp16, so each 64-value block of an X
+ * column needs a norm below 65504, the fp16 maximum (|Q| <= ||x_block|| for unit-norm atoms).
+ * CSDR_HSDB_QROUTE=0 keeps those calls on the decoding launch. The workspace
  * is csdr_hsdb_group_workspace_bytes(n, segs, M) bytes, enough for every path and phase at
  * that M (x-op calls and the separate dx / gather phases take the P path). csdr_hsdb_matmul
  * is the n = 1 case. Y rows are accumulated over block-column ranges with device-scope float
