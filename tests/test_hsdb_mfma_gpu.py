@@ -87,6 +87,38 @@ def test_dictionary_route_shapes(gpu, R, Cc, K, s, M):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("M", [12, 16])
+def test_group_mixed_dictionaries(gpu, M):
+    # matrices of different K, R and C in one call: workgroup unit ranges cross matrix
+    # segments, and the dictionary route reloads its atoms per segment
+    from cortexsdr_amd import _lib
+    from cortexsdr_amd.hsdr import HsdbSegment, group_workspace
+
+    shapes = [(300, 896, 256), (1000, 1024, 1024), (513, 640, 512)]
+    streams = [synth.hsdb_layer(R, Cc, K, 8, seed_dict=30 + i, seed_codes=40 + i)
+               for i, (R, Cc, K) in enumerate(shapes)]
+    segs = [HsdbSegment(st) for st in streams]
+    xs = [synth.activations(Cc, M, seed=50 + i, dtype=np.float16)
+          for i, (_, Cc, _) in enumerate(shapes)]
+    xd = [gpu.from_numpy(x).cuda() for x in xs]
+    ys = [gpu.zeros((R, M), dtype=gpu.float32, device="cuda") for R, _, _ in shapes]
+    ws = group_workspace(segs, M)
+    n = len(segs)
+    hs = (C.c_void_p * n)(*[sg._h.value for sg in segs])
+    xp = (C.c_void_p * n)(*[x.data_ptr() for x in xd])
+    yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+    lib = _lib.load()
+    sp = int(gpu.cuda.current_stream().cuda_stream)
+    _lib.check(lib.csdr_hsdb_matmul_group_ex(n, hs, xp, 1, M, yp, None, 0, ws.data_ptr(),
+                                             ws.numel(), sp))
+    for st, x, y in zip(streams, xs, ys):
+        err = rel_l2(y.cpu().numpy(), oracle.hsdb_matmul(st, x.astype(np.float32)))
+        print(f"M={M} rel_l2={err:.3e}")
+        assert err <= TOL
+    for sg in segs:
+        sg.free()
+
+
 @pytest.mark.parametrize("M", [16, 24])
 def test_group_bias_accumulate(gpu, M):
     from cortexsdr_amd import _lib
