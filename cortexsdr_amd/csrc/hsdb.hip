@@ -106,6 +106,7 @@ struct Params {
     float eps;
     int nsplit, hd;   // attention combine: splits and head size of the partials in x
     int gtotal;       // 2 <= M <= 8: gather units of all matrices (the launch is padded to 8s)
+    int p16;          // 5 <= M <= 8 on the multi-column gather: P is fp16 [block][atom][8]
 };
 
 template <int CTRL>
@@ -953,6 +954,22 @@ __global__ __launch_bounds__(kThreads) void dxmm_kernel(Params p) {
     for (int s = 0; s < 16; ++s)
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(dv[s >> 2][s & 3], xb[s >> 2][s & 3], acc, 0, 0, 0);
     const int bj = ng * BPT + li / MC, mj = li % MC;
+    if constexpr (MC == 8) {
+        if (p.p16) {
+            // fp16 P, [block][atom][8] with the columns past M zero (their X' was staged as
+            // zeros): 16 bytes per (block, atom), a pair of columns per even lane
+            uint32_t* out = reinterpret_cast<uint32_t*>(d.P) + (size_t)bj * d.K * 4 + (mj >> 1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float o = dpp_move<0xB1>(acc[v]);  // the odd column's value
+                const int a = a0 + 4 * lg + v;
+                const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)acc[v]) |
+                                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)o) << 16);
+                if (bj < d.NB && !(mj & 1) && a < d.K) __builtin_nontemporal_store(w, out + (size_t)a * 4);
+            }
+            return;
+        }
+    }
     if (bj < d.NB && mj < M) {
         float* out = d.P + (size_t)bj * d.K * M + mj;
 #pragma unroll
@@ -1224,7 +1241,7 @@ constexpr int kGvMinRows = 256;  // rows per workgroup the LDS share must hold, 
 // of the row), `buf` holding the first TD tiles already issued. Lanes past the wave's valid
 // tiles read zeros (coefficient 0), and a row's lanes are all valid or all past the end, so no
 // selects are needed before the row reductions.
-template <int SLOTS, int MC, int TD, int LPR, typename TileFn>
+template <int SLOTS, int MC, int TD, int LPR, bool P16, typename TileFn>
 __device__ __forceinline__ void gatherv_stream(const MatDesc& d, const float* Ps, float* rowt,
                                                u32x4 (*buf)[SLOTS / 4], TileFn tile, int nk,
                                                int wfirst, int ntiles) {
@@ -1253,7 +1270,20 @@ __device__ __forceinline__ void gatherv_stream(const MatDesc& d, const float* Ps
             const uint32_t word = w[j >> 2][j & 3];
             const float cf = gm[j] * csdr::h2f(word >> 16);
             const int e = ebase + (int)(uint16_t)word;
-            if constexpr (MC == 2) {
+            if constexpr (P16) {
+                // 8 fp16 columns in one 16-byte read (multiply-adds with an fp16 operand)
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const u32x4 v = *reinterpret_cast<const u32x4*>(Ps + (size_t)e * 4);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    // (the element through a scalar: a bit cast of the vector element
+                    // expression v[k] itself compiles to a read of element 0 only)
+                    const uint32_t dw = v[k];
+                    const h2 pr = __builtin_bit_cast(h2, dw);
+                    acc[2 * k] = fmaf(cf, (float)pr[0], acc[2 * k]);
+                    acc[2 * k + 1] = fmaf(cf, (float)pr[1], acc[2 * k + 1]);
+                }
+            } else if constexpr (MC == 2) {
                 const f2 v = *reinterpret_cast<const f2*>(Ps + (size_t)e * 2);
                 acc[0] = fmaf(cf, v.x, acc[0]);
                 acc[1] = fmaf(cf, v.y, acc[1]);
@@ -1308,9 +1338,10 @@ __device__ __forceinline__ void gatherv_stream(const MatDesc& d, const float* Ps
         if (k0 + jj < nk) consume(buf[jj], k0 + jj);
 }
 
-template <int SLOTS, int MC, int DEPTH, int WPE>
+template <int SLOTS, int MC, int DEPTH, int WPE, bool P16>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gatherv_kernel(Params p) {
+    static_assert(!P16 || MC == 8, "fp16 P has 8 columns");
     extern __shared__ float smem[];
     // Workgroups go to the eight XCDs round-robin (workgroup b on XCD b % 8). XCD x takes the
     // x-th eighth of the units in chunk-major order, so the row ranges of one chunk share the
@@ -1367,8 +1398,8 @@ void gatherv_kernel(Params p) {
             out[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + i * 16, 0, kCachePolicyNT);
     };
 
-    float* Ps = smem;                          // NBc * K * MC floats
-    float* xe = Ps + (size_t)d.NBc * d.K * MC;  // Ce (< 64) x MC floats
+    float* Ps = smem;  // NBc * K * MC floats (fp16 P: NBc * K * 8 halves)
+    float* xe = Ps + (size_t)d.NBc * d.K * (P16 ? 4 : MC);  // Ce (< 64) x MC floats
     float* rowt = xe + 64 * MC;                 // (rend - rbeg) x MC row totals
     const bool edge = (c == d.nchunks - 1) && d.Ce > 0;
 
@@ -1378,12 +1409,13 @@ void gatherv_kernel(Params p) {
     constexpr int NBUF = TD + 1;
     u32x4 buf[NBUF][PPB];
     typedef float f4 __attribute__((ext_vector_type(4)));
-    if (M == MC && (d.K * MC) % 4 == 0) {
-        // P slice: global [block][atom][M] -> LDS, a straight copy of 16-byte pieces (at most 8
-        // per thread: one round trip)
-        const f4* Pg = reinterpret_cast<const f4*>(d.P + (size_t)b0 * d.K * M);
+    if (P16 || (M == MC && (d.K * MC) % 4 == 0)) {
+        // P slice: global [block][atom][M] (fp16 P: [block][atom][8] halves) -> LDS, a
+        // straight copy of 16-byte pieces (at most 8 per thread: one round trip)
+        const f4* Pg = P16 ? reinterpret_cast<const f4*>(d.P) + (size_t)b0 * d.K
+                           : reinterpret_cast<const f4*>(d.P + (size_t)b0 * d.K * M);
         f4* Pl = reinterpret_cast<f4*>(Ps);
-        const int n4 = nbc * d.K * MC / 4;
+        const int n4 = nbc * d.K * (P16 ? 4 : MC) / 4;
         for (int i0 = 0; i0 < n4; i0 += kGThreads * 8) {
             f4 v[8];
 #pragma unroll
@@ -1423,13 +1455,13 @@ void gatherv_kernel(Params p) {
     // the stream, specialised on the lanes per row (the chunk's block columns, a power of two),
     // so each column's row reduction is a straight DPP / shuffle sequence
     switch (nbc) {
-        case 1: gatherv_stream<SLOTS, MC, TD, 1>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        case 2: gatherv_stream<SLOTS, MC, TD, 2>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        case 4: gatherv_stream<SLOTS, MC, TD, 4>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        case 8: gatherv_stream<SLOTS, MC, TD, 8>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        case 16: gatherv_stream<SLOTS, MC, TD, 16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        case 32: gatherv_stream<SLOTS, MC, TD, 32>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
-        default: gatherv_stream<SLOTS, MC, TD, 64>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 1: gatherv_stream<SLOTS, MC, TD, 1, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 2: gatherv_stream<SLOTS, MC, TD, 2, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 4: gatherv_stream<SLOTS, MC, TD, 4, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 8: gatherv_stream<SLOTS, MC, TD, 8, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 16: gatherv_stream<SLOTS, MC, TD, 16, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        case 32: gatherv_stream<SLOTS, MC, TD, 32, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
+        default: gatherv_stream<SLOTS, MC, TD, 64, P16>(d, Ps, rowt, buf, tile, nk, wfirst, ntiles); break;
     }
     // the top-right strip's inputs of the last chunk: [cc][m] (x-op transformed when given)
     if (edge) {
@@ -1941,33 +1973,44 @@ void launch_gatherw(const Params& p, int slots, int grid, size_t lds, hipStream_
         launch_gatherw_p<false>(p, slots, grid, lds, st);
 }
 
-// The 2 <= M <= 8 gather: MC = M rounded up to 2, 4 or 8; the 128 KiB P slice of MC = 8 allows
-// one workgroup per CU (4 waves per SIMD for the register budget), the smaller ones two.
-template <int MC, int WPE>
+inline int gatherv_mc(int M) { return M <= 2 ? 2 : (M <= 4 ? 4 : 8); }
+// 5 <= M <= 8 with CSDR_HSDB_P16=1 (off by default): P in fp16, 8 columns in 16 bytes per
+// (block, atom); the slice is half as large, two workgroups per CU and one LDS read per slot.
+// One rounding per P value (about 2e-4 relative) which a decoder's layers compound.
+inline bool gatherv_p16(int M) { return gatherv_mc(M) == 8 && env_flag("CSDR_HSDB_P16", false); }
+inline int gatherv_wgs_per_cu(int mc, bool p16) { return mc == 8 && !p16 ? 1 : 2; }
+inline size_t gatherv_p_atom_bytes(int mc, bool p16) { return p16 ? 16 : (size_t)mc * 4; }
+
+// The 2 <= M <= 8 gather: MC = M rounded up to 2, 4 or 8; the 128 KiB fp32 P slice of MC = 8
+// allows one workgroup per CU (4 waves per SIMD for the register budget), the smaller ones and
+// the fp16 slice two.
+template <int MC, int WPE, bool P16>
 void launch_gatherv_mc(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
-    constexpr int kDepth = MC == 8 ? 6 : 4;
+    constexpr int kDepth = MC == 8 && !P16 ? 6 : 4;
     const void* fn = nullptr;
     switch (slots) {
-        case 4: fn = reinterpret_cast<const void*>(&gatherv_kernel<4, MC, kDepth, WPE>); break;
-        case 8: fn = reinterpret_cast<const void*>(&gatherv_kernel<8, MC, kDepth, WPE>); break;
-        default: fn = reinterpret_cast<const void*>(&gatherv_kernel<16, MC, kDepth, WPE>); break;
+        case 4: fn = reinterpret_cast<const void*>(&gatherv_kernel<4, MC, kDepth, WPE, P16>); break;
+        case 8: fn = reinterpret_cast<const void*>(&gatherv_kernel<8, MC, kDepth, WPE, P16>); break;
+        default: fn = reinterpret_cast<const void*>(&gatherv_kernel<16, MC, kDepth, WPE, P16>); break;
     }
     if (lds > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     switch (slots) {
-        case 4: gatherv_kernel<4, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
-        case 8: gatherv_kernel<8, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
-        default: gatherv_kernel<16, MC, kDepth, WPE><<<grid, kGThreads, lds, st>>>(p); break;
+        case 4: gatherv_kernel<4, MC, kDepth, WPE, P16><<<grid, kGThreads, lds, st>>>(p); break;
+        case 8: gatherv_kernel<8, MC, kDepth, WPE, P16><<<grid, kGThreads, lds, st>>>(p); break;
+        default: gatherv_kernel<16, MC, kDepth, WPE, P16><<<grid, kGThreads, lds, st>>>(p); break;
     }
 }
 
-inline int gatherv_mc(int M) { return M <= 2 ? 2 : (M <= 4 ? 4 : 8); }
-inline int gatherv_wgs_per_cu(int mc) { return mc == 8 ? 1 : 2; }
-
 void launch_gatherv(const Params& p, int slots, int grid, size_t lds, hipStream_t st) {
     switch (gatherv_mc(p.M)) {
-        case 2: launch_gatherv_mc<2, 8>(p, slots, grid, lds, st); break;
-        case 4: launch_gatherv_mc<4, 8>(p, slots, grid, lds, st); break;
-        default: launch_gatherv_mc<8, 4>(p, slots, grid, lds, st); break;
+        case 2: launch_gatherv_mc<2, 8, false>(p, slots, grid, lds, st); break;
+        case 4: launch_gatherv_mc<4, 8, false>(p, slots, grid, lds, st); break;
+        default:
+            if (p.p16)
+                launch_gatherv_mc<8, 8, true>(p, slots, grid, lds, st);
+            else
+                launch_gatherv_mc<8, 4, false>(p, slots, grid, lds, st);
+            break;
     }
 }
 
@@ -2064,18 +2107,28 @@ struct XopArgs {
     int nsplit = 0, hd = 0;
 };
 
-// 2 <= M <= 8: the streaming multi-column gather reads every code once for all columns
-// (fp32 throughout), where the matrix-core path decodes each weight through the LDS
-// dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count in the group) and a P
-// slice within the gather's budget.
+// fp16 P on the multi-column gather: at 5 <= M <= 8 where the thread-per-atom dx kernel (64-long
+// blocks) writes P
+bool group_p16(int n, const csdr_hsdb* const* segs, int M) {
+    bool on = M >= 2 && M <= kMaxVecM && gatherv_p16(M);
+    for (int i = 0; i < n && on; ++i) on = segs[i] && segs[i]->tile_cols == 64;
+    return on;
+}
+
+// 2 <= M <= 8: the streaming multi-column gather reads every code once for all columns (fp32
+// accumulation; P in fp32, or optionally fp16 at 5 <= M <= 8), where the matrix-core path decodes each
+// weight through the LDS dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count
+// in the group) and a P slice within the gather's budget.
 bool vec_path(int n, const csdr_hsdb* const* segs, int M) {
     bool vec = M >= 2 && M <= kMaxVecM;
     for (int i = 0; i < n && vec; ++i) {
         const csdr_hsdb* s = segs[i];
         const int mc = gatherv_mc(M);
-        const size_t lds = ((size_t)s->NBc * s->K + 64 + kGvMinRows) * 4 * mc;
+        const bool p16 = group_p16(n, segs, M);
+        const size_t lds = (size_t)s->NBc * s->K * gatherv_p_atom_bytes(mc, p16) +
+                           (size_t)(64 + kGvMinRows) * 4 * mc;
         vec = s->tile_rows == 1 && s->NB > 0 && (s->slots == 4 || s->slots == 8 || s->slots == 16) &&
-              s->slots == segs[0]->slots && lds <= (size_t)160 * 1024 / gatherv_wgs_per_cu(mc);
+              s->slots == segs[0]->slots && lds <= (size_t)160 * 1024 / gatherv_wgs_per_cu(mc, p16);
     }
     return vec;
 }
@@ -2123,7 +2176,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     }
     const bool tm = (flags & CSDR_HSDB_TOKEN_MAJOR) && M > 1;
     // 2 <= M <= 8: the streaming multi-column gather reads every code once for all columns
-    // (fp32 throughout), where the matrix-core path decodes each weight through the LDS
+    // (fp32 unless CSDR_HSDB_P16=1), where the matrix-core path decodes each weight through the LDS
     // dictionary; it needs 1-row tiles of 4, 8 or 16 slots (the same count in the group) and
     // a P slice within the gather's budget
     const bool vec = vec_path(n, segs, M);
@@ -2139,6 +2192,7 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
     Params p{};
     p.G = n;
     p.M = M;
+    p.p16 = vec && group_p16(n, segs, M) ? 1 : 0;
     // generic gather: P staged 4 columns at a time when that fits in LDS, else 1
     size_t max_pk = 0;
     for (int i = 0; i < n; ++i) max_pk = std::max(max_pk, (size_t)segs[i]->NBc * segs[i]->K);
@@ -2247,7 +2301,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
         // columns allows; fewer for small groups: at least kGMinWgBytes of codes per workgroup
         // (each one stages a P slice first)
         const int mc = fast ? 1 : gatherv_mc(M);
-        const int wpc = fast ? kGWgsPerCu : gatherv_wgs_per_cu(mc);
+        const bool p16 = !fast && p.p16;
+        const int wpc = fast ? kGWgsPerCu : gatherv_wgs_per_cu(mc, p16);
         long long target = (long long)ncu * wpc;
         // rows per workgroup: M == 1 kGMaxRows; else what the LDS share left by the widest P
         // slice holds (row totals of mc floats)
@@ -2256,7 +2311,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             size_t pk = 0;
             for (int i = 0; i < n; ++i) pk = std::max(pk, (size_t)segs[i]->NBc * segs[i]->K);
             const size_t share = (size_t)160 * 1024 / wpc;
-            max_rows = (int)std::min<size_t>(kGMaxRows, (share - (pk + 64) * mc * 4) / (mc * 4));
+            max_rows = (int)std::min<size_t>(
+                kGMaxRows, (share - pk * gatherv_p_atom_bytes(mc, p16) - 64 * mc * 4) / (mc * 4));
         }
         long long code_bytes = 0;
         for (int i = 0; i < n; ++i) code_bytes += (long long)p.m[i].R * p.m[i].NB * slots * 4;
@@ -2268,7 +2324,8 @@ int matmul_group(int n, const csdr_hsdb* const* segs, const void* const* xs, int
             int rows = d.splits ? d.rows_per_wg : 0;  // rows per workgroup
             for (int j = 0; j < 4; ++j)
                 if (d.rsplit[j]) rows = std::max(rows, d.rrpw[j]);
-            lds_g = std::max(lds_g, ((size_t)d.NBc * d.K + 64 + rows) * 4 * mc);
+            lds_g = std::max(lds_g, (size_t)d.NBc * d.K * (fast ? 4 : gatherv_p_atom_bytes(mc, p16)) +
+                                        (size_t)(64 + rows) * 4 * mc);
             base += d.g_count;
         }
     } else {

@@ -177,7 +177,10 @@ CSDR_API int csdr_hsdb_gather_group(int n, const csdr_hsdb* const* segs, const v
  * CSDR_HSDB_TOKEN_MAJOR takes X as M x C and writes Y as M x R (token-major, the layout of
  * Kernels::linear_forward, blas_kernels.cpp:264-293, and of the SDK's run_layer) instead of
  * C x M and R x M (identical at M == 1). 2 <= M <= 8 (1-row tiles of 4, 8 or 16 slots) runs
- * the streaming gather with M columns per code read (fp32 throughout). */
+ * the streaming gather with M columns per code read (fp32 throughout; with the environment
+ * variable CSDR_HSDB_P16=1, 5 <= M <= 8 keeps the per-block products D.x_b in fp16 instead:
+ * faster, about 2e-4 relative per value, and the transformed x's block norms must stay below
+ * 65504). */
 #define CSDR_HSDB_ACCUMULATE 1
 #define CSDR_HSDB_TOKEN_MAJOR 2
 CSDR_API int csdr_hsdb_matmul_group_ex(int n, const csdr_hsdb* const* segs, const void* const* x,
